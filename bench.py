@@ -1,0 +1,214 @@
+"""Benchmark of the MI355X quantized decode path (one GPU).
+
+Headline (``value``): W4A16 int4 GEMV throughput in GB/s on BASELINE config 2's
+M=1, N=12288, K=4096 point (group 128, bf16 scales, asymmetric int8 zero points).
+A step is one int4 linear call over one batch; the K timed steps are captured
+into a HIP graph that cycles through enough distinct weight copies (> 512 MB) that
+the 256 MB Infinity Cache cannot serve them, and are timed with HIP events on the
+stream the kernels run on.  The rest of the sweep (and the other path sections)
+are reported under ``sections``.
+
+Usage: python bench.py [--gpus 1] [--steps 60] [--warmup 10] [--sections int4,...]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+import torch  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+ROTATE_BYTES = 600 * 2**20  # distinct buffers per timed region (> 2 x 256 MB Infinity Cache)
+METRIC = "int4 GEMV/GEMM GB/s & TFLOPs (% roofline); TQ-KV decode attn tokens/s"
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def time_graph(fns, steps: int, warmup: int) -> float:
+    """Capture `steps` calls (fns[i % len(fns)]) into one HIP graph; return ms per step."""
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        for f in fns[: min(len(fns), 3)]:  # eager warm-up (loads code objects)
+            f()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(steps):
+            fns[i % len(fns)]()
+    for _ in range(max(1, warmup // max(1, steps) + 1)):
+        graph.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        graph.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+# ---------------------------------------------------------------- int4 linear
+
+
+def int4_bytes(m, n, k, group, scale_bytes=2):
+    g = k // group
+    return n * k // 2 + g * n * scale_bytes + g * n + m * k * 2 + m * n * 2
+
+
+def make_int4_copies(n, k, group, copies, device, gen):
+    g = k // group
+    out = []
+    for _ in range(copies):
+        qw = torch.randint(-(2**31), 2**31 - 1, (n, k // 8), dtype=torch.int32, device=device, generator=gen)
+        qs = (torch.randn((g, n), device=device, generator=gen) * 0.02).abs_().add_(1e-3).to(torch.bfloat16)
+        qz = torch.randint(0, 16, (g, n), dtype=torch.int8, device=device, generator=gen)
+        out.append((qw, qs, qz))
+    return out
+
+
+def bench_int4_point(m, n, k, steps, warmup, device, group=128):
+    from anna_amd import fused_ops
+
+    gen = torch.Generator(device=device)
+    gen.manual_seed(1234 + m + n + k)
+    per_copy = int4_bytes(m, n, k, group)
+    copies = max(2, math.ceil(ROTATE_BYTES / per_copy))
+    ws = make_int4_copies(n, k, group, copies, device, gen)
+    x = torch.randn((m, k), device=device, generator=gen).to(torch.bfloat16)
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=device)
+
+    def mk(w):
+        return lambda: fused_ops.int4_linear_out(x, w[0], w[1], w[2], group, k, y)
+
+    ms = time_graph([mk(w) for w in ws], steps, warmup)
+    sec = ms / 1e3
+    gbs = per_copy / sec / 1e9
+    tflops = 2.0 * m * n * k / sec / 1e12
+    bound = "hbm" if m <= 64 else "mfma"
+    frac = gbs / HBM_PEAK_GBS if bound == "hbm" else tflops / BF16_PEAK_TFLOPS
+    del ws
+    torch.cuda.empty_cache()
+    return {"M": m, "N": n, "K": k, "ms": ms, "us": ms * 1e3, "GB/s": gbs, "TFLOP/s": tflops, "bound": bound,
+            "roofline_frac": frac, "bytes": per_copy, "distinct_weight_copies": copies}
+
+
+def cpu_baseline_int4(m, n, k, group, budget_s):
+    from oracle.cpu_paths import int4_forward_dequant
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    g = torch.Generator().manual_seed(7)
+    qw = torch.randint(-(2**31), 2**31 - 1, (n, k // 8), dtype=torch.int32, generator=g)
+    qs = (torch.randn((k // group, n), generator=g) * 0.02).abs_().add_(1e-3).to(torch.bfloat16).float()
+    qz = torch.randint(0, 16, (k // group, n), dtype=torch.int8, generator=g)
+    x = torch.randn((m, k), generator=g).to(torch.bfloat16)
+    int4_forward_dequant(x, qw, qs, qz, group, k)  # warm-up
+    t0 = time.perf_counter()
+    int4_forward_dequant(x, qw, qs, qz, group, k)
+    one = time.perf_counter() - t0
+    iters = max(3, min(200, int(budget_s / max(one, 1e-6))))
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        int4_forward_dequant(x, qw, qs, qz, group, k)
+    sec = (time.perf_counter() - t0) / iters
+    return {
+        "value": int4_bytes(m, n, k, group) / sec / 1e9,
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"{iters} calls of the reference CPU dequant path (XPUInt4Linear._forward_dequant restated in "
+                   f"torch) at M={m} N={n} K={k}; {sec * 1e3:.1f} ms/call; CPU: {cpu_model()}, "
+                   f"os.cpu_count()={os.cpu_count()}"),
+    }
+
+
+def section_int4(args, device):
+    sweep = []
+    for (m, n, k) in [(1, 6144, 2048)] + [(m, n, 4096) for n in (12288, 6144) for m in (1, 8, 64, 256, 2048)]:
+        steps = args.steps if m <= 64 else max(10, args.steps // 4)
+        r = bench_int4_point(m, n, k, steps, args.warmup, device)
+        log(f"int4 M={m:5d} N={n:6d} K={k}: {r['us']:8.2f} us  {r['GB/s']:8.1f} GB/s  "
+            f"{r['TFLOP/s']:7.1f} TFLOP/s  {100 * r['roofline_frac']:5.1f}% of {r['bound']} peak")
+        sweep.append(r)
+    return sweep
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=60)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--sections", default="int4")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the sharding plan is described in DESIGN.md); run with --gpus 1.", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs an MI355X (no ROCm device visible)", file=sys.stderr)
+        return 1
+    device = torch.device("cuda", 0)
+    from anna_amd import fused_ops
+
+    fused_ops.register_ops()
+    sections = {}
+    wanted = set(args.sections.split(","))
+    if "int4" in wanted:
+        sections["int4_sweep"] = section_int4(args, device)
+    head = next(r for r in sections["int4_sweep"] if (r["M"], r["N"], r["K"]) == (1, 12288, 4096))
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline_int4(1, 12288, 4096, 128, args.cpu_seconds)
+        log(f"cpu baseline: {cpu['value']:.2f} GB/s on {cpu['cores']} threads")
+    line = {
+        "metric": METRIC,
+        "value": round(head["GB/s"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded codes U{0..15}, bf16 scales |N(0,0.02)|+1e-3, zero points U{0..15}, x ~N(0,1))",
+        "config": {"workload": "W4A16 int4 GEMV, M=1 N=12288 K=4096 group=128 (BASELINE config 2, fused gate_up)",
+                   "M": 1, "N": 12288, "K": 4096, "group_size": 128, "scale_dtype": "bf16"},
+        "roofline": {"bound": "hbm", "achieved": round(head["GB/s"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(head["GB/s"] / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "sections": sections,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,416 @@
+/*
+ * anna_oracle.c -- CPU restatement of funkpopo/Anna's quantized decode path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product (anna_amd/, the HIP
+ * library) may call, link or load this file; only tests/, the smoke check in
+ * __graft_entry__.py and bench.py's cpu_baseline leg use it, as the checker.
+ *
+ * Every function cites the reference lines it restates (paths relative to the
+ * reference repository root).  Arithmetic is written so that each float
+ * operation rounds exactly where the reference's torch expression rounds:
+ * the file is compiled with -ffp-contract=off, and fused multiply-adds appear
+ * only where they are spelled out with fmaf() (the TurboQuant-MSE quantizer,
+ * whose summation order is part of this build's own format definition).
+ *
+ * Parity status per function (what pins it, see tests/test_oracle_*.py):
+ *   orc_int4_quantize        closed form + reference test bounds
+ *                            (tests/test_quantization_replace.py:179-199)
+ *   orc_autoround_to_int4    reference known-answer test
+ *                            (tests/test_quantization_replace.py:145-176)
+ *   orc_int4_dequant/linear  brute-force textbook dequant+matmul in fp64
+ *   orc_tq_values_*          closed form, round-trip bound, bit layout
+ *   orc_tq_codebook          published Lloyd-Max levels (Max 1960)
+ *   orc_tq_mse_*             PARITY UNPINNED against the reference: the
+ *                            reference delegates to the absent third-party
+ *                            `turboquant>=0.2,<0.3` package; pinned here only by
+ *                            invariants (orthogonality, round trip, distortion).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+#include <stdlib.h>
+
+/* ------------------------------------------------------------------ */
+/* scalar conversions (round-to-nearest-even, like torch's .to())      */
+/* ------------------------------------------------------------------ */
+
+static uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+uint16_t orc_f32_to_bf16(float f) {
+    uint32_t u = f2u(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u); /* quiet NaN */
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+float orc_bf16_to_f32(uint16_t h) { return u2f(((uint32_t)h) << 16); }
+
+uint16_t orc_f32_to_f16(float f) {
+    uint32_t u = f2u(f);
+    uint32_t sign = (u >> 16) & 0x8000u;
+    uint32_t a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u);
+    if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* rounds to inf */
+    if (a < 0x38800000u) {                                   /* subnormal half */
+        /* value = a * 2^-24 units; round-to-nearest-even on the shifted mantissa */
+        if (a < 0x33000000u) return (uint16_t)sign;          /* < 2^-25 -> 0 */
+        uint32_t e = a >> 23;
+        uint32_t m = (a & 0x7fffffu) | 0x800000u;
+        /* |f| = m * 2^(e-150); the half subnormal unit is 2^-24 */
+        uint32_t shift = 126u - e;
+        uint32_t q = m >> shift;
+        uint32_t rem = m & ((1u << shift) - 1u);
+        uint32_t halfway = 1u << (shift - 1u);
+        if (rem > halfway || (rem == halfway && (q & 1u))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t r = a - 0x38000000u;                             /* rebias 127 -> 15 */
+    uint32_t q = r >> 13;
+    uint32_t rem = r & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) q++;
+    return (uint16_t)(sign | q);
+}
+
+float orc_f16_to_f32(uint16_t h) {
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1fu;
+    uint32_t m = h & 0x3ffu;
+    if (e == 0) {
+        if (m == 0) return u2f(sign);
+        float v = (float)m * (1.0f / 16777216.0f);
+        return sign ? -v : v;
+    }
+    if (e == 31) return u2f(sign | 0x7f800000u | (m << 13));
+    return u2f(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+/* dtype codes shared with the HIP library: 0 = bf16, 1 = fp16, 2 = fp32 */
+static float load_any(const void* p, int dtype, int64_t i) {
+    if (dtype == 0) return orc_bf16_to_f32(((const uint16_t*)p)[i]);
+    if (dtype == 1) return orc_f16_to_f32(((const uint16_t*)p)[i]);
+    return ((const float*)p)[i];
+}
+
+/* round a float to the storage dtype and back (torch `.to(dtype)`) */
+static float round_to(float v, int dtype) {
+    if (dtype == 0) return orc_bf16_to_f32(orc_f32_to_bf16(v));
+    if (dtype == 1) return orc_f16_to_f32(orc_f32_to_f16(v));
+    return v;
+}
+
+static void store_any(void* p, int dtype, int64_t i, float v) {
+    if (dtype == 0) ((uint16_t*)p)[i] = orc_f32_to_bf16(v);
+    else if (dtype == 1) ((uint16_t*)p)[i] = orc_f32_to_f16(v);
+    else ((float*)p)[i] = v;
+}
+
+/* ------------------------------------------------------------------ */
+/* a1: symmetric runtime int4 quantizer + packer                      */
+/* ------------------------------------------------------------------ */
+
+/*
+ * Restates XPUInt4Linear._quantize_weight (src/anna/model/quantization.py:597-624)
+ * for rounding == 0 (torch.round: half to even), and the Rust load-time packer
+ * quantize_linear_raw (crates/anna-rust/src/lib.rs:341-401) for rounding == 1
+ * (f32::round: half away from zero).
+ *   scale = amax/7 (1 when amax == 0), q = clamp(round(w/scale + 8), 0, 15),
+ *   qzeros = 8, nibble k%8 of word k/8 at bits 4*(k%8).
+ * w is [N, K] fp32; padded columns K..Kp-1 quantize as zeros.
+ * Outputs: qweight int32 [N, Kp/8], qscale fp32 [Kp/group, N], qzeros int8 [Kp/group, N].
+ */
+void orc_int4_quantize(const float* w, int64_t N, int64_t K, int64_t group, int64_t Kp,
+                       int rounding, int32_t* qweight, float* qscale, int8_t* qzeros) {
+    int64_t G = Kp / group;
+    for (int64_t n = 0; n < N; ++n) {
+        for (int64_t g = 0; g < G; ++g) {
+            float amax = 0.0f;
+            for (int64_t j = 0; j < group; ++j) {
+                int64_t k = g * group + j;
+                float v = k < K ? w[n * K + k] : 0.0f;
+                float a = fabsf(v);
+                if (a > amax) amax = a;
+            }
+            float scale = amax > 0.0f ? amax / 7.0f : 1.0f;
+            qscale[g * N + n] = scale;
+            qzeros[g * N + n] = 8;
+        }
+        for (int64_t kw = 0; kw < Kp / 8; ++kw) {
+            uint32_t word = 0;
+            for (int j = 0; j < 8; ++j) {
+                int64_t k = kw * 8 + j;
+                float v = k < K ? w[n * K + k] : 0.0f;
+                float scale = qscale[(k / group) * N + n];
+                float t = v / scale;
+                t = t + 8.0f;
+                float r = rounding == 0 ? nearbyintf(t) : roundf(t);
+                if (r < 0.0f) r = 0.0f;
+                if (r > 15.0f) r = 15.0f;
+                word |= ((uint32_t)(int32_t)r & 0xfu) << (4 * j);
+            }
+            qweight[n * (Kp / 8) + kw] = (int32_t)word;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* a2: AutoRound / GPTQ layout -> XPU int4 layout                      */
+/* ------------------------------------------------------------------ */
+
+/*
+ * Restates AutoRoundGPTQLinear._to_xpu_int4_tensors with _unpack_int4_first_dim /
+ * _unpack_qzeros (src/anna/model/quantization.py:239-252, 329-375).
+ *   gptq_qweight int32 [ceil(K/8), N]: k = 8*row + nibble, nibble i at bits 4i.
+ *   gptq_qzeros  int32 [G, ceil(N/8)]: stored zero = zero - 1.
+ *   scales fp16 [G, N] -> fp32.
+ * Padded K rows take the zero point of group min(G-1, K/group), so they dequantize to 0.
+ * Outputs as orc_int4_quantize; qzeros are the true zero points (stored + 1) as int8.
+ */
+void orc_autoround_to_int4(const int32_t* gptq_qweight, const int32_t* gptq_qzeros,
+                           const uint16_t* scales_f16, int64_t K, int64_t N, int64_t group,
+                           int64_t G, int64_t Kp, int32_t* qweight, float* qscale, int8_t* qzeros) {
+    int64_t n8 = (N + 7) / 8;
+    for (int64_t g = 0; g < G; ++g)
+        for (int64_t n = 0; n < N; ++n) {
+            uint32_t zw = (uint32_t)gptq_qzeros[g * n8 + n / 8];
+            int32_t z = (int32_t)((zw >> (4 * (n % 8))) & 0xfu) + 1;
+            qzeros[g * N + n] = (int8_t)z;
+            qscale[g * N + n] = orc_f16_to_f32(scales_f16[g * N + n]);
+        }
+    int64_t tail_g = K / group;
+    if (tail_g > G - 1) tail_g = G - 1;
+    for (int64_t n = 0; n < N; ++n)
+        for (int64_t kw = 0; kw < Kp / 8; ++kw) {
+            uint32_t word = 0;
+            for (int j = 0; j < 8; ++j) {
+                int64_t k = kw * 8 + j;
+                int32_t q;
+                if (k < K) {
+                    uint32_t src = (uint32_t)gptq_qweight[(k / 8) * N + n];
+                    q = (int32_t)((src >> (4 * (k % 8))) & 0xfu);
+                } else {
+                    q = qzeros[tail_g * N + n];
+                }
+                word |= ((uint32_t)q & 0xfu) << (4 * j);
+            }
+            qweight[n * (Kp / 8) + kw] = (int32_t)word;
+        }
+}
+
+/* ------------------------------------------------------------------ */
+/* a3: dequant and the reference CPU linear                            */
+/* ------------------------------------------------------------------ */
+
+/*
+ * Restates XPUInt4Linear._dequantize_weight (src/anna/model/quantization.py:626-635):
+ * w[n,k] = (q - z[g,n]) * s[g,n] in fp32, truncated to the first K columns.
+ * scale_dtype: 0 bf16, 1 fp16, 2 fp32 (the reference's buffer is fp32; the tiled
+ * op of gated_delta_fused_op.sycl:3272-3343 also accepts bf16/fp16 scales).
+ */
+void orc_int4_dequant(const int32_t* qweight, const void* qscale, int scale_dtype,
+                      const int8_t* qzeros, int64_t N, int64_t K, int64_t Kp, int64_t group,
+                      float* w) {
+    for (int64_t n = 0; n < N; ++n)
+        for (int64_t k = 0; k < K; ++k) {
+            uint32_t word = (uint32_t)qweight[n * (Kp / 8) + k / 8];
+            int32_t q = (int32_t)((word >> (4 * (k % 8))) & 0xfu);
+            int64_t gi = (k / group) * N + n;
+            float s = load_any(qscale, scale_dtype, gi);
+            float z = (float)qzeros[gi];
+            w[n * K + k] = ((float)q - z) * s;
+        }
+}
+
+/*
+ * Restates XPUInt4Linear._forward_dequant (src/anna/model/quantization.py:645-648):
+ * y = F.linear(x_bf16, dequant(W).to(bf16)).  x is bf16 [M, K]; the dot products are
+ * accumulated in fp64 (the textbook value the bf16 GEMM approximates); y is fp32
+ * [M, N], not yet rounded to bf16.
+ */
+void orc_int4_linear(const uint16_t* x_bf16, const int32_t* qweight, const void* qscale,
+                     int scale_dtype, const int8_t* qzeros, int64_t M, int64_t N, int64_t K,
+                     int64_t Kp, int64_t group, float* y) {
+    float* wrow = (float*)malloc(sizeof(float) * (size_t)K);
+    for (int64_t n = 0; n < N; ++n) {
+        for (int64_t k = 0; k < K; ++k) {
+            uint32_t word = (uint32_t)qweight[n * (Kp / 8) + k / 8];
+            int32_t q = (int32_t)((word >> (4 * (k % 8))) & 0xfu);
+            int64_t gi = (k / group) * N + n;
+            float s = load_any(qscale, scale_dtype, gi);
+            wrow[k] = round_to(((float)q - (float)qzeros[gi]) * s, 0);
+        }
+        for (int64_t m = 0; m < M; ++m) {
+            double acc = 0.0;
+            for (int64_t k = 0; k < K; ++k)
+                acc += (double)orc_bf16_to_f32(x_bf16[m * K + k]) * (double)wrow[k];
+            y[m * N + n] = (float)acc;
+        }
+    }
+    free(wrow);
+}
+
+/* ------------------------------------------------------------------ */
+/* a9: TurboQuant value min/max group quantizer                        */
+/* ------------------------------------------------------------------ */
+
+static int storage_bits_of(int bits) { return bits == 2 ? 2 : 4; }
+
+/*
+ * Restates quantize_turboquant_values and _pack_value_data
+ * (src/anna/model/turboquant.py:164-175, 199-230).  Per (head, token, group):
+ *   scale = clamp((max - min) / (2^b - 1), min=1e-8) cast to the value dtype,
+ *   zero  = min cast to the value dtype,
+ *   q = clamp(round((v - zero) / scale), 0, 2^b - 1)       (fp32, half to even),
+ * packed 4 per byte (2-bit, element i at bits 2i) or 2 per byte (3/4-bit, element i at
+ * bits 4i).  values [H, T, D] of dtype `dtype`; data uint8 [H, T, D*sb/8];
+ * scales/zeros [H, T, D/group] of dtype `dtype`.
+ */
+void orc_tq_values_quantize(const void* values, int dtype, int64_t H, int64_t T, int64_t D,
+                            int bits, int64_t group, uint8_t* data, void* scales, void* zeros) {
+    int sb = storage_bits_of(bits);
+    int per_byte = 8 / sb;
+    float levels = (float)((1 << bits) - 1);
+    int64_t ng = D / group;
+    int64_t packed = D / per_byte;
+    for (int64_t r = 0; r < H * T; ++r) {
+        const int64_t base = r * D;
+        memset(data + r * packed, 0, (size_t)packed);
+        for (int64_t g = 0; g < ng; ++g) {
+            float vmin = INFINITY, vmax = -INFINITY;
+            for (int64_t j = 0; j < group; ++j) {
+                float v = load_any(values, dtype, base + g * group + j);
+                if (v < vmin) vmin = v;
+                if (v > vmax) vmax = v;
+            }
+            float sc = (vmax - vmin) / levels;
+            if (sc < 1e-8f) sc = 1e-8f;
+            sc = round_to(sc, dtype);
+            float zr = round_to(vmin, dtype);
+            store_any(scales, dtype, r * ng + g, sc);
+            store_any(zeros, dtype, r * ng + g, zr);
+            for (int64_t j = 0; j < group; ++j) {
+                int64_t d = g * group + j;
+                float v = load_any(values, dtype, base + d);
+                float t = (v - zr) / sc;
+                t = nearbyintf(t);
+                if (t < 0.0f) t = 0.0f;
+                if (t > levels) t = levels;
+                uint32_t q = (uint32_t)t;
+                data[r * packed + d / per_byte] |= (uint8_t)(q << (sb * (d % per_byte)));
+            }
+        }
+    }
+}
+
+/* Restates dequantize_turboquant_values (src/anna/model/turboquant.py:233-252): q*scale + zero in fp32. */
+void orc_tq_values_dequant(const uint8_t* data, const void* scales, const void* zeros, int dtype,
+                           int64_t H, int64_t T, int64_t D, int bits, int64_t group, float* out) {
+    int sb = storage_bits_of(bits);
+    int per_byte = 8 / sb;
+    uint32_t mask = (1u << sb) - 1u;
+    int64_t ng = D / group;
+    int64_t packed = D / per_byte;
+    for (int64_t r = 0; r < H * T; ++r)
+        for (int64_t d = 0; d < D; ++d) {
+            uint32_t q = (data[r * packed + d / per_byte] >> (sb * (d % per_byte))) & mask;
+            float sc = load_any(scales, dtype, r * ng + d / group);
+            float zr = load_any(zeros, dtype, r * ng + d / group);
+            out[r * D + d] = (float)q * sc + zr;
+        }
+}
+
+/* ------------------------------------------------------------------ */
+/* a10/a11: TurboQuant-MSE (rotation + Lloyd-Max codebook + norm)      */
+/* ------------------------------------------------------------------ */
+
+static double std_normal_pdf(double x) { return exp(-0.5 * x * x) * 0.39894228040143267794; }
+static double std_normal_cdf(double x) { return 0.5 * erfc(-x * 0.70710678118654752440); }
+
+/*
+ * Lloyd-Max quantizer of N(0,1) with 2^bits levels, solved by Lloyd iteration in fp64
+ * (conditional means between midpoint thresholds).  The third-party package the
+ * reference imports (`turboquant`, turboquant.py:45,57) is absent, so this build
+ * defines its codebook as the Gaussian Lloyd-Max levels scaled by 1/sqrt(D) -- the
+ * large-D limit of the Beta-distributed rotated coordinate used by TurboQuant
+ * (Zandieh et al. 2025).  Output: 2^bits ascending levels of N(0,1).
+ */
+void orc_lloyd_max_gaussian(int bits, double* levels) {
+    int n = 1 << bits;
+    double* c = levels;
+    for (int i = 0; i < n; ++i) c[i] = -3.0 + 6.0 * (i + 0.5) / n;
+    for (int it = 0; it < 20000; ++it) {
+        double maxdelta = 0.0;
+        for (int i = 0; i < n; ++i) {
+            double lo = i == 0 ? -INFINITY : 0.5 * (c[i - 1] + c[i]);
+            double hi = i == n - 1 ? INFINITY : 0.5 * (c[i] + c[i + 1]);
+            double plo = isinf(lo) ? 0.0 : std_normal_pdf(lo);
+            double phi = isinf(hi) ? 0.0 : std_normal_pdf(hi);
+            double mass = std_normal_cdf(hi) - std_normal_cdf(lo);
+            double nc = (plo - phi) / mass;
+            double dlt = fabs(nc - c[i]);
+            if (dlt > maxdelta) maxdelta = dlt;
+            c[i] = nc;
+        }
+        if (maxdelta < 1e-15) break;
+    }
+}
+
+/*
+ * TurboQuant-MSE quantizer (this build's definition; reference call sites
+ * src/anna/model/turboquant.py:75-82, 335-477 -- PARITY UNPINNED, see header).
+ * For each vector x (D values of dtype `dtype`):
+ *   nrm = sqrt(fma-chain sum of x_k^2, k ascending)              (fp32)
+ *   y_i = fma-chain sum_k P[i*D + k] * x_k, k ascending          (fp32)
+ *   code_i = #{ j : y_i >= thr[j] * nrm }                         (thr ascending)
+ *   norm stored as fp16 (round to nearest even).
+ * Codes pack like the values: 2-bit 4 per byte at bits 2i, 3/4-bit 2 per byte.
+ */
+void orc_tq_mse_quantize(const void* x, int dtype, int64_t nvec, int64_t D, const float* P,
+                         const float* thr, int bits, uint8_t* codes, uint16_t* norms) {
+    int sb = storage_bits_of(bits);
+    int per_byte = 8 / sb;
+    int nthr = (1 << bits) - 1;
+    int64_t packed = D / per_byte;
+    float* xv = (float*)malloc(sizeof(float) * (size_t)D);
+    for (int64_t v = 0; v < nvec; ++v) {
+        float ss = 0.0f;
+        for (int64_t k = 0; k < D; ++k) {
+            xv[k] = load_any(x, dtype, v * D + k);
+            ss = fmaf(xv[k], xv[k], ss);
+        }
+        float nrm = sqrtf(ss);
+        norms[v] = orc_f32_to_f16(nrm);
+        memset(codes + v * packed, 0, (size_t)packed);
+        for (int64_t i = 0; i < D; ++i) {
+            float y = 0.0f;
+            for (int64_t k = 0; k < D; ++k) y = fmaf(P[i * D + k], xv[k], y);
+            uint32_t c = 0;
+            for (int j = 0; j < nthr; ++j) c += (y >= thr[j] * nrm) ? 1u : 0u;
+            codes[v * packed + i / per_byte] |= (uint8_t)(c << (sb * (i % per_byte)));
+        }
+    }
+    free(xv);
+}
+
+/* x_hat = norm_fp16 * P^T c[code]   (fp64 accumulation, fp32 out) */
+void orc_tq_mse_dequant(const uint8_t* codes, const uint16_t* norms, int64_t nvec, int64_t D,
+                        const float* P, const float* centroids, int bits, float* out) {
+    int sb = storage_bits_of(bits);
+    int per_byte = 8 / sb;
+    uint32_t mask = (1u << sb) - 1u;
+    int64_t packed = D / per_byte;
+    double* yr = (double*)malloc(sizeof(double) * (size_t)D);
+    for (int64_t v = 0; v < nvec; ++v) {
+        double nrm = (double)orc_f16_to_f32(norms[v]);
+        for (int64_t i = 0; i < D; ++i) {
+            uint32_t c = (codes[v * packed + i / per_byte] >> (sb * (i % per_byte))) & mask;
+            yr[i] = (double)centroids[c];
+        }
+        for (int64_t k = 0; k < D; ++k) {
+            double acc = 0.0;
+            for (int64_t i = 0; i < D; ++i) acc += (double)P[i * D + k] * yr[i];
+            out[v * D + k] = (float)(nrm * acc);
+        }
+    }
+    free(yr);
+}

@@ -1,0 +1,150 @@
+"""Parity of the HIP int4 path against the CPU oracle (through the C ABI / anna:: ops).
+
+Packing, repacking and dequant are integer/exact work: bit-exact.  Linear outputs:
+normwise max relative error <= 1e-2 against the oracle's x_bf16 @ bf16(dequant(W))^T
+(the reference CPU path, quantization.py:645-648).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from anna_amd import fused_ops
+from anna_amd.quantization import XPUInt4Linear
+from oracle import oracle as orc
+from tests._util import BF16_TOL, int4_payload, rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a, device):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+
+def _x_tensor(bits_u16, dtype, device):
+    t = torch.from_numpy(bits_u16.view(np.int16)).view(torch.bfloat16).to(device)
+    return t.to(dtype)
+
+
+LINEAR_CASES = [
+    # (M, K, N, group, scale dtype)
+    (1, 2048, 6144, 128, "bf16"),   # benchmark config 1
+    (1, 4096, 512, 128, "fp32"),
+    (2, 256, 100, 128, "fp32"),     # N tail
+    (8, 4096, 384, 128, "bf16"),
+    (16, 1024, 64, 128, "fp32"),
+    (3, 384, 48, 128, "fp32"),      # K = 3 blocks, odd block count per wave
+    (17, 512, 130, 128, "fp32"),    # GEMM path, M and N tails
+    (64, 1024, 256, 128, "bf16"),
+    (130, 256, 200, 128, "fp32"),
+    (5, 96, 40, 32, "fp32"),        # group 32: generic kernel
+]
+
+
+@pytest.mark.parametrize("m,k,n,group,sdt", LINEAR_CASES)
+def test_int4_linear_matches_oracle(gpu, m, k, n, group, sdt):
+    print(f"[case] int4_linear M={m} K={k} N={n} g={group} scale={sdt}", flush=True)
+    rng = np.random.default_rng(m * 1000 + k + n)
+    qw, qs, qz = int4_payload(rng, n, k, group, scale_dtype=sdt)
+    xb = orc.bf16_bits(rng.normal(size=(m, k)).astype(np.float32))
+    ref = orc.int4_linear(xb, qw, qs, qz, group)
+    qs_t = _dev(qs, gpu).to(torch.bfloat16 if sdt == "bf16" else torch.float32)
+    x = _x_tensor(xb, torch.bfloat16, gpu)
+    y = torch.ops.anna.xpu_int4_gemv(x, _dev(qw, gpu), qs_t, _dev(qz, gpu), group, k)
+    assert y.dtype == torch.bfloat16 and y.shape == (m, n)
+    assert rel_err(y.float().cpu().numpy(), ref) <= BF16_TOL
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.float32])
+def test_int4_linear_other_activation_dtypes(gpu, xdt):
+    rng = np.random.default_rng(7)
+    m, k, n, group = 4, 1024, 192, 128
+    qw, qs, qz = int4_payload(rng, n, k, group, scale_dtype="fp32")
+    xb = orc.bf16_bits(rng.normal(size=(m, k)).astype(np.float32))
+    ref = orc.int4_linear(xb, qw, qs, qz, group)
+    x = _x_tensor(xb, xdt, gpu)
+    y = torch.ops.anna.xpu_int4_gemv(x, _dev(qw, gpu), _dev(qs, gpu), _dev(qz, gpu), group, k)
+    assert y.dtype == xdt
+    assert rel_err(y.float().cpu().numpy(), ref) <= BF16_TOL
+
+
+def test_int4_linear_strided_rows(gpu):
+    rng = np.random.default_rng(8)
+    m, k, n, group = 3, 512, 64, 128
+    qw, qs, qz = int4_payload(rng, n, k, group, scale_dtype="fp32")
+    xb = orc.bf16_bits(rng.normal(size=(m, 2 * k)).astype(np.float32))
+    ref = orc.int4_linear(np.ascontiguousarray(xb[:, :k]), qw, qs, qz, group)
+    x = _x_tensor(xb, torch.bfloat16, gpu)[:, :k]
+    assert not x.is_contiguous()
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=gpu)
+    fused_ops.int4_linear_out(x, _dev(qw, gpu), _dev(qs, gpu), _dev(qz, gpu), group, k, out)
+    assert rel_err(out.float().cpu().numpy(), ref) <= BF16_TOL
+
+
+@pytest.mark.parametrize("rounding", ["half_even", "half_away"])
+def test_int4_quantize_bit_exact(gpu, rounding):
+    rng = np.random.default_rng(9)
+    n, k, group = 40, 300, 32
+    kp = XPUInt4Linear._padded_in_features(k, group)
+    w = rng.normal(size=(n, k)).astype(np.float32)
+    w[0, :8] = [7.0, 0.5, 1.5, -0.5, -7.0, 2.5, -2.5, 0.0]  # exact ties at scale 1
+    w[1] = 0.0
+    ref = orc.int4_quantize(w, group, kp, rounding=0 if rounding == "half_even" else 1)
+    got = fused_ops.int4_quantize(_dev(w, gpu), group_size=group, padded_in_features=kp, rounding=rounding)
+    for a, b in zip(got, ref):
+        np.testing.assert_array_equal(a.cpu().numpy(), b)
+
+
+def test_int4_quantize_bf16_weight_bit_exact(gpu):
+    rng = np.random.default_rng(10)
+    n, k, group = 16, 256, 128
+    wb = orc.bf16_bits(rng.normal(size=(n, k)).astype(np.float32))
+    ref = orc.int4_quantize(orc.bf16_to_f32(wb), group, k)
+    got = fused_ops.int4_quantize(_x_tensor(wb, torch.bfloat16, gpu), group_size=group, padded_in_features=k)
+    for a, b in zip(got, ref):
+        np.testing.assert_array_equal(a.cpu().numpy(), b)
+
+
+def test_autoround_repack_bit_exact(gpu):
+    rng = np.random.default_rng(11)
+    k, n, group, kp = 200, 24, 64, 256
+    g = -(-k // group)
+    codes = rng.integers(0, 16, size=(-(-k // 8) * 8, n))
+    v = codes.reshape(-1, 8, n).astype(np.int64)
+    words = (v << (4 * np.arange(8))[None, :, None]).sum(1)
+    gq = np.where(words >= 2**31, words - 2**32, words).astype(np.int32)
+    zeros = rng.integers(0, 15, size=(g, n))
+    zw = (zeros.reshape(g, n // 8, 8).astype(np.int64) << (4 * np.arange(8))).sum(-1)
+    gz = np.where(zw >= 2**31, zw - 2**32, zw).astype(np.int32)
+    sc = orc.f16_bits(rng.uniform(0.01, 0.1, size=(g, n)).astype(np.float32))
+    ref = orc.autoround_to_int4(gq, gz, sc, k, n, group, kp)
+    got = fused_ops.autoround_to_int4(_dev(gq, gpu), _dev(gz, gpu), _dev(sc.view(np.int16), gpu).view(torch.float16),
+                                      in_features=k, out_features=n, group_size=group, padded_in_features=kp)
+    for a, b in zip(got, ref):
+        np.testing.assert_array_equal(a.cpu().numpy(), b)
+
+
+def test_int4_dequant_exact(gpu):
+    rng = np.random.default_rng(12)
+    n, k, group = 33, 384, 128
+    qw, qs, qz = int4_payload(rng, n, k, group, scale_dtype="fp32")
+    ref = orc.int4_dequant(qw, qs, qz, k, group)
+    got = fused_ops.int4_dequant(_dev(qw, gpu), _dev(qs, gpu), _dev(qz, gpu), group, k, out_dtype=torch.float32)
+    np.testing.assert_array_equal(got.cpu().numpy(), ref)
+
+
+def test_module_from_linear_and_forward(gpu):
+    torch.manual_seed(13)
+    dense = torch.nn.Linear(1000, 96, bias=True)
+    mod = XPUInt4Linear.from_linear(dense, group_size=128, compute_dtype=torch.bfloat16, device=gpu)
+    assert mod.padded_in_features == 1024 and mod.qweight.shape == (96, 128)
+    w = dense.weight.detach().numpy()
+    qw, qs, qz = orc.int4_quantize(w, 128, 1024)
+    np.testing.assert_array_equal(mod.qweight.cpu().numpy(), qw)
+    np.testing.assert_array_equal(mod.qscale.cpu().numpy(), qs)
+    x = torch.randn(2, 3, 1000)
+    xb = orc.bf16_bits(x.reshape(6, 1000).numpy())
+    ref = orc.int4_linear(xb, qw, qs, qz, 128) + orc.bf16_to_f32(orc.bf16_bits(dense.bias.detach().numpy()))
+    y = mod(x.to(gpu).to(torch.bfloat16))
+    assert y.shape == (2, 3, 96)
+    assert rel_err(y.float().cpu().reshape(6, 96).numpy(), ref) <= BF16_TOL
