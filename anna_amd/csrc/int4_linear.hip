@@ -19,6 +19,10 @@
 //                    dequant numerics) next to a 128x128 tile of x, and 4 waves run
 //                    v_mfma_f32_32x32x16_bf16 on it.
 //   int4_linear_generic  any dtype / group / alignment; VALU, one wave per output row.
+#include <stdlib.h>
+
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace anna {
@@ -63,25 +67,31 @@ __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
 
 // ------------------------------------------------------------------ GEMV (M <= 16)
 
-constexpr int GEMV_UNROLL = 2;  // K blocks whose loads are issued together
+// K blocks (128 k each) one wave keeps in flight per pass: all of them are loaded
+// before any is consumed, so a wave has 8 x 16 B x NT per lane outstanding.
+constexpr int GEMV_BPW = 8;
+// x is staged in LDS when M * K * 2 bytes fit this budget (else read through L1/L2).
+constexpr int64_t GEMV_LDS_X_LIMIT = 32768;  // = 2048 chunks of 16 B
 
-template <int XDT, int SDT, int NT, int KW>
+template <int XDT, int SDT, int NT, int KW, bool XLDS>
 __global__ __launch_bounds__(64 * KW) void int4_gemv_mfma(
     const uint16_t* __restrict__ x, int64_t M, int64_t K, int64_t xs,
     const uint32_t* __restrict__ qw, int64_t N, int64_t pc,
     const typename Elem<SDT>::T* __restrict__ qs, const int8_t* __restrict__ qz,
-    int64_t blocks_per_group, uint16_t* __restrict__ y) {
+    int64_t blocks_per_group, uint16_t* __restrict__ y, int contiguous, int nontemporal) {
   constexpr float OFF = XDT == ANNA_MI_BF16 ? 128.0f : 1024.0f;
   constexpr uint32_t ONES = XDT == ANNA_MI_BF16 ? 0x3F803F80u : 0x3C003C00u;
+  extern __shared__ __attribute__((aligned(16))) uint16_t xsm[];  // [M][K + 8] when XLDS
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int r = lane & 15;
   const int kq = lane >> 4;
   const int64_t n_base = (int64_t)blockIdx.x * (16 * NT);
   const bool m_ok = r < M;
-  const uint16_t* xrow = x + (int64_t)r * xs;
   const int64_t nblk = (K + 127) >> 7;
+  const int64_t xp = K + 8;  // LDS row pitch (elements): rows land 4 banks apart
   const u32x4 ones = {ONES, ONES, ONES, ONES};
+  const u32x4 zero4 = {0u, 0u, 0u, 0u};
 
   const uint32_t* wrow[NT];
   bool n_ok[NT];
@@ -96,55 +106,111 @@ __global__ __launch_bounds__(64 * KW) void int4_gemv_mfma(
 #pragma unroll
   for (int t = 0; t < NT; ++t) out[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int64_t b0 = wave; b0 < nblk; b0 += (int64_t)KW * GEMV_UNROLL) {
-    u32x4 wv[GEMV_UNROLL][NT];
-    u32x4 xa[GEMV_UNROLL][4];
+  // Block j of a pass: interleaved (b = p0 + wave + KW*j) or contiguous per wave
+  // (b = p0 + wave*BPW + j, so one wave reads whole 128 B lines back to back).
+  const int64_t bw0 = contiguous ? (int64_t)wave * GEMV_BPW : wave;
+  const int64_t bstep = contiguous ? 1 : KW;
+  // x staging (first pass only): its loads are issued before the weight loads so that
+  // waiting for x leaves every weight load in flight.
+  constexpr int XCH = XLDS ? (2048 / (64 * KW)) : 1;  // 16 B chunks of x per thread
+  const int64_t xchunks = M * (K >> 3);
+  u32x4 xst[XCH];
+  if constexpr (XLDS) {
 #pragma unroll
-    for (int u = 0; u < GEMV_UNROLL; ++u) {
-      const int64_t b = b0 + (int64_t)u * KW;
-      const bool b_ok = b < nblk;
+    for (int i = 0; i < XCH; ++i) {
+      int64_t c = threadIdx.x + (int64_t)i * 64 * KW;
+      c = c < xchunks ? c : 0;
+      const int64_t row = c / (K >> 3), col = (c % (K >> 3)) * 8;
+      xst[i] = *(const u32x4*)(x + row * xs + col);
+    }
+  }
+  // One pass = GEMV_BPW blocks per wave.  The first pass is peeled out of the loop so
+  // that no loop-header wait holds the weight loads behind the x staging loads.
+  auto pass = [&](int64_t p0, auto first_tag) {
+    constexpr bool FIRST = decltype(first_tag)::value;
+    // Issue every global load of the pass up front: weights, scales, zero points.
+    u32x4 wv[GEMV_BPW][NT];
+    float scv[GEMV_BPW][NT];
+    float cv[GEMV_BPW][NT];
+    // Loads are unconditional (addresses clamped into range, results selected after):
+    // predicated loads would split the pass into branches with a full vmcnt wait each.
+#pragma unroll
+    for (int j = 0; j < GEMV_BPW; ++j) {
+      const int64_t b = p0 + bw0 + bstep * j;
+      const int64_t bc = b < nblk ? b : nblk - 1;
+      const int64_t g = bc / blocks_per_group;
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        wv[u][t] = (b_ok && n_ok[t]) ? __builtin_nontemporal_load((const u32x4*)(wrow[t] + b * 16))
-                                     : u32x4{0u, 0u, 0u, 0u};
-      }
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int64_t k = b * 128 + kq * 32 + s * 8;
-        xa[u][s] = (b_ok && m_ok && k < K) ? *(const u32x4*)(xrow + k) : u32x4{0u, 0u, 0u, 0u};
+        const int64_t gi = g * N + (n_ok[t] ? n_base + t * 16 + r : 0);
+        const u32x4* src = (const u32x4*)(wrow[t] + bc * 16);
+        wv[j][t] = nontemporal ? __builtin_nontemporal_load(src) : *src;
+        scv[j][t] = Elem<SDT>::load(qs, gi);
+        cv[j][t] = (float)qz[gi];
       }
     }
 #pragma unroll
-    for (int u = 0; u < GEMV_UNROLL; ++u) {
-      const int64_t b = b0 + (int64_t)u * KW;
+    for (int j = 0; j < GEMV_BPW; ++j)
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        if (!n_ok[t]) wv[j][t] = zero4;
+    if constexpr (XLDS && FIRST) {
+      {
+#pragma unroll
+        for (int i = 0; i < XCH; ++i) {
+          const int64_t c = threadIdx.x + (int64_t)i * 64 * KW;
+          if (c < xchunks) {
+            const int64_t row = c / (K >> 3), col = (c % (K >> 3)) * 8;
+            *(u32x4*)(xsm + row * xp + col) = xst[i];
+          }
+        }
+        __syncthreads();
+      }
+    }
+    // x fragments of the next block are fetched while the current block computes.
+    auto load_x = [&](int64_t b, int s) -> u32x4 {
+      const int64_t k = b * 128 + kq * 32 + s * 8;
+      const bool ok = b < nblk && m_ok && k < K;
+      const int64_t kc = ok ? k : 0;
+      const int64_t rc = m_ok ? r : 0;
+      u32x4 v;
+      if constexpr (XLDS) v = *(const u32x4*)(xsm + rc * xp + kc);
+      else v = *(const u32x4*)(x + rc * xs + kc);
+      return ok ? v : zero4;
+    };
+    u32x4 xa[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) xa[s] = load_x(p0 + bw0, s);
+#pragma unroll
+    for (int j = 0; j < GEMV_BPW; ++j) {
+      const int64_t b = p0 + bw0 + bstep * j;
       if (b >= nblk) break;
+      u32x4 xn[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) xn[s] = j + 1 < GEMV_BPW ? load_x(b + bstep, s) : zero4;
       f32x4 acc[NT];
       f32x4 sx = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const u32x4 a = interleave_x(xa[u][s]);
+        const u32x4 a = interleave_x(xa[s]);
         sx = mfma16<XDT>(a, ones, sx);
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-          const uint32_t w = wv[u][t][s];
-          acc[t] = mfma16<XDT>(a, nibbles_to_frag<XDT>(w), acc[t]);
-        }
+        for (int t = 0; t < NT; ++t) acc[t] = mfma16<XDT>(a, nibbles_to_frag<XDT>(wv[j][t][s]), acc[t]);
       }
       // C layout: lane holds rows m = 4*kq + i of column n = n_base + 16t + r.
-      const int64_t g = b / blocks_per_group;
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        const int64_t n = n_base + t * 16 + r;
-        const int64_t gi = g * N + (n_ok[t] ? n : 0);
-        const float sc = Elem<SDT>::load(qs, gi);
-        const float c = OFF + (float)qz[gi];
+        const float c = OFF + cv[j][t];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) out[t][i] = fmaf(sc, acc[t][i] - c * sx[i], out[t][i]);
+        for (int i = 0; i < 4; ++i) out[t][i] = fmaf(scv[j][t], acc[t][i] - c * sx[i], out[t][i]);
       }
+#pragma unroll
+      for (int s = 0; s < 4; ++s) xa[s] = xn[s];
     }
-  }
+  };
+  pass(0, std::true_type{});
+  for (int64_t p0 = (int64_t)KW * GEMV_BPW; p0 < nblk; p0 += (int64_t)KW * GEMV_BPW) pass(p0, std::false_type{});
 
   if constexpr (KW > 1) {
     __shared__ float red[KW - 1][NT * 4][64];
@@ -172,6 +238,204 @@ __global__ __launch_bounds__(64 * KW) void int4_gemv_mfma(
       const int64_t m = 4 * kq + i;
       if (m < M) y[m * N + n] = Elem<XDT>::cvt(out[t][i]);
     }
+  }
+}
+
+// ------------------------------------------------------------------ GEMV, VALU dot2 (M <= 2)
+//
+// Streaming kernel for the bandwidth-critical M = 1..2 case.  A load instruction covers
+// 64/LPR rows x (LPR x 16 B) contiguous bytes of each (whole 128 B lines).  Wave w of a
+// workgroup owns the k-slice [w*LPR*32, (w+1)*LPR*32) of RW rows; a lane keeps its 32 x
+// values in registers (loaded first, so they never wait behind weights) and walks RG row
+// groups whose loads are all issued up front.  Per 8 nibbles: 7 ALU ops build the bf16
+// pairs (128+q_i, 128+q_{i+4}) and 4 v_dot2c_f32_bf16 accumulate; per 32 k the zero point
+// and scale are applied as s * (acc - (128 + z) * sum(x)).  Lanes of a row and the waves of
+// the workgroup are reduced at the end.
+
+template <int XDT>
+__device__ __forceinline__ float dot2_acc(uint32_t a, uint32_t b, float c) {
+  if constexpr (XDT == ANNA_MI_BF16) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+  } else {
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);
+  }
+}
+
+template <int XDT>
+__device__ __forceinline__ float sum8_16bit(u32x4 v) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t w = v[i];
+    if constexpr (XDT == ANNA_MI_BF16) {
+      s += __uint_as_float(w << 16) + __uint_as_float(w & 0xFFFF0000u);
+    } else {
+      s += f16_bits_to_f32((uint16_t)(w & 0xFFFFu)) + f16_bits_to_f32((uint16_t)(w >> 16));
+    }
+  }
+  return s;
+}
+
+constexpr int DOT2_MAX_WAVES = 16;
+constexpr uint32_t OOB = 0x80000000u;  // buffer offset past any num_records: the load returns 0
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+
+// Butterfly step within 32-lane groups: value of lane (lane ^ MASK).
+template <int MASK>
+__device__ __forceinline__ float swz_xor(float v) {
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), (MASK << 10) | 0x1F));
+}
+
+template <int XDT, int SDT, int MR, int RG>
+__global__ __launch_bounds__(64 * DOT2_MAX_WAVES) void int4_gemv_dot2(
+    const uint16_t* __restrict__ x, int64_t M, int64_t K, int64_t xs,
+    const uint32_t* __restrict__ qw, int64_t N, int64_t pc,
+    const typename Elem<SDT>::T* __restrict__ qs, const int8_t* __restrict__ qz,
+    int64_t gsz, uint16_t* __restrict__ y) {
+  constexpr int RPI = 4;        // rows per load instruction: 16 lanes x 16 B per row
+  constexpr int RW = RPI * RG;  // rows per workgroup
+  constexpr int KSL = 512;      // k per wave slice
+  constexpr float OFF = XDT == ANNA_MI_BF16 ? 128.0f : 1024.0f;
+  constexpr uint32_t ONES = XDT == ANNA_MI_BF16 ? 0x3F803F80u : 0x3C003C00u;
+  static_assert(RG == 4 || RG == 8 || RG == 16, "row groups");
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int kw = blockDim.x >> 6;
+  const int sub = lane >> 4, c = lane & 15;
+  const int64_t n0 = (int64_t)blockIdx.x * RW;
+  const int64_t G = (K + gsz - 1) / gsz;
+  // Weight rows of this workgroup; rows >= N fall outside num_records and read 0.
+  const int64_t rows_here = N - n0 < RW ? N - n0 : RW;
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(qw + n0 * pc, (uint32_t)(rows_here * pc * 4));
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(qs, (uint32_t)(G * N * sizeof(typename Elem<SDT>::T)));
+  const __amdgpu_buffer_rsrc_t rz = make_rsrc(qz, (uint32_t)(G * N));
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)(((M - 1) * xs + K) * 2));
+
+  float yacc[MR][RG];
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int g = 0; g < RG; ++g) yacc[m][g] = 0.f;
+
+  for (int64_t k0 = (int64_t)wave * KSL; k0 < K; k0 += (int64_t)kw * KSL) {
+    const int64_t kl = k0 + c * 32;
+    const bool k_ok = kl < K;
+    // x first (in-order returns: it never waits behind the weights).
+    u32x4 xv[MR][4];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      const uint32_t xo = (k_ok && m < M) ? (uint32_t)((m * xs + kl) * 2) : OOB;
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4)
+        xv[m][s4] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, xo, s4 * 16, 0));
+    }
+    u32x4 wv[RG];
+    float sc[RG], cz[RG];
+    const uint32_t wo = k_ok ? (uint32_t)((sub * pc + (kl >> 3)) * 4) : OOB;
+    const int64_t grp = k_ok ? kl / gsz : 0;
+    const uint32_t so = k_ok ? (uint32_t)(grp * N + n0 + sub) : OOB / 4;
+#pragma unroll
+    for (int g = 0; g < RG; ++g) {
+      wv[g] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            rw, wo, (int)(g * RPI * pc * 4), 2 /* slc: streamed once */));
+      if constexpr (SDT == ANNA_MI_F32) {
+        sc[g] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, so * 4, g * RPI * 4, 0));
+      } else {
+        const uint32_t h = __builtin_amdgcn_raw_buffer_load_b16(rs, so * 2, g * RPI * 2, 0);
+        sc[g] = SDT == ANNA_MI_BF16 ? __uint_as_float(h << 16) : f16_bits_to_f32((uint16_t)h);
+      }
+      cz[g] = OFF + (float)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(rz, so, g * RPI, 0);
+    }
+    // x to nibble-pair order; its sum by dot2 against ones (the zero-point term)
+    uint32_t xp[MR][16];
+    float sx[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      float t = 0.f;
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const u32x4 iv = interleave_x(xv[m][s4]);
+        xp[m][s4 * 4 + 0] = iv.x;
+        xp[m][s4 * 4 + 1] = iv.y;
+        xp[m][s4 * 4 + 2] = iv.z;
+        xp[m][s4 * 4 + 3] = iv.w;
+        t = dot2_acc<XDT>(iv.x, ONES, t);
+        t = dot2_acc<XDT>(iv.y, ONES, t);
+        t = dot2_acc<XDT>(iv.z, ONES, t);
+        t = dot2_acc<XDT>(iv.w, ONES, t);
+      }
+      sx[m] = t;
+    }
+#pragma unroll
+    for (int g = 0; g < RG; ++g) {
+      float acc[MR];
+#pragma unroll
+      for (int m = 0; m < MR; ++m) acc[m] = 0.f;
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const u32x4 f = nibbles_to_frag<XDT>(wv[g][s4]);
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+          acc[m] = dot2_acc<XDT>(xp[m][s4 * 4 + 0], f.x, acc[m]);
+          acc[m] = dot2_acc<XDT>(xp[m][s4 * 4 + 1], f.y, acc[m]);
+          acc[m] = dot2_acc<XDT>(xp[m][s4 * 4 + 2], f.z, acc[m]);
+          acc[m] = dot2_acc<XDT>(xp[m][s4 * 4 + 3], f.w, acc[m]);
+        }
+      }
+#pragma unroll
+      for (int m = 0; m < MR; ++m) yacc[m][g] = fmaf(sc[g], fmaf(-cz[g], sx[m], acc[m]), yacc[m][g]);
+    }
+  }
+  // Reduce-scatter across the 16 lanes of a row: after the butterfly, lane c holds the
+  // full sum of row group (c >> (4 - log2 RG)) ... see index below.
+  float red_v[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    float v[RG];
+#pragma unroll
+    for (int g = 0; g < RG; ++g) v[g] = yacc[m][g];
+    // stage on lane bit 3: keep the half selected by that bit
+    auto stage = [&](auto mask_tag, int half, float* vals) {
+      constexpr int MASK = decltype(mask_tag)::value;
+      const bool upper = (c & MASK) != 0;
+      for (int i = 0; i < half; ++i) {
+        const float mine = upper ? vals[i + half] : vals[i];
+        const float give = upper ? vals[i] : vals[i + half];
+        vals[i] = mine + swz_xor<MASK>(give);
+      }
+    };
+    using M8 = std::integral_constant<int, 8>;
+    using M4 = std::integral_constant<int, 4>;
+    using M2 = std::integral_constant<int, 2>;
+    using M1 = std::integral_constant<int, 1>;
+    if constexpr (RG == 16) { stage(M8{}, 8, v); stage(M4{}, 4, v); stage(M2{}, 2, v); stage(M1{}, 1, v); }
+    if constexpr (RG == 8) { stage(M8{}, 4, v); stage(M4{}, 2, v); stage(M2{}, 1, v); v[0] += swz_xor<1>(v[0]); }
+    if constexpr (RG == 4) { stage(M8{}, 2, v); stage(M4{}, 1, v); v[0] += swz_xor<2>(v[0]); v[0] += swz_xor<1>(v[0]); }
+    red_v[m] = v[0];
+  }
+  // Row group held by lane c: bits 3,2,1,0 of c select halves in order (MSB first).
+  int gsel;
+  if constexpr (RG == 16) gsel = ((c >> 3) & 1) * 8 + ((c >> 2) & 1) * 4 + ((c >> 1) & 1) * 2 + (c & 1);
+  else if constexpr (RG == 8) gsel = ((c >> 3) & 1) * 4 + ((c >> 2) & 1) * 2 + ((c >> 1) & 1);
+  else gsel = ((c >> 3) & 1) * 2 + ((c >> 2) & 1);
+  const bool writer = RG == 16 ? true : RG == 8 ? (c & 1) == 0 : (c & 3) == 0;
+  __shared__ float red[DOT2_MAX_WAVES][MR][RW];
+  if (writer) {
+#pragma unroll
+    for (int m = 0; m < MR; ++m) red[wave][m][gsel * RPI + sub] = red_v[m];
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < MR * RW; i += blockDim.x) {
+    const int m = i / RW, row = i % RW;
+    float v = 0.f;
+    for (int w = 0; w < kw; ++w) v += red[w][m][row];
+    const int64_t n = n0 + row;
+    if (m < M && n < N) y[m * N + n] = Elem<XDT>::cvt(v);
   }
 }
 
@@ -399,13 +663,45 @@ __global__ __launch_bounds__(256) void int4_dequant_kernel(
   }
 }
 
+int env_int(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return (v && *v) ? atoi(v) : dflt;
+}
+// ANNA_MI_INT4_GEMV_CONTIG / ANNA_MI_INT4_GEMV_NT: block order and nontemporal weight loads.
+static const int g_contig = env_int("ANNA_MI_INT4_GEMV_CONTIG", 0);
+static const int g_nt = env_int("ANNA_MI_INT4_GEMV_NT", 1);
+
 template <int XDT, int SDT, int NT, int KW>
 void launch_gemv(const void* x, int64_t M, int64_t K, int64_t xs, const int32_t* qw, int64_t N,
                  int64_t pc, const void* qs, const int8_t* qz, int64_t gsz, void* y, hipStream_t st) {
   dim3 grid((unsigned)((N + 16 * NT - 1) / (16 * NT)), 1, 1);
-  hipLaunchKernelGGL((int4_gemv_mfma<XDT, SDT, NT, KW>), grid, dim3(64 * KW), 0, st,
-                     (const uint16_t*)x, M, K, xs, (const uint32_t*)qw, N, pc,
-                     (const typename Elem<SDT>::T*)qs, qz, gsz / 128, (uint16_t*)y);
+  const int64_t xbytes = M * (K + 8) * 2;
+  if (M * K * 2 <= GEMV_LDS_X_LIMIT) {
+    hipLaunchKernelGGL((int4_gemv_mfma<XDT, SDT, NT, KW, true>), grid, dim3(64 * KW), (size_t)xbytes, st,
+                       (const uint16_t*)x, M, K, xs, (const uint32_t*)qw, N, pc,
+                       (const typename Elem<SDT>::T*)qs, qz, gsz / 128, (uint16_t*)y, g_contig, g_nt);
+  } else {
+    hipLaunchKernelGGL((int4_gemv_mfma<XDT, SDT, NT, KW, false>), grid, dim3(64 * KW), 0, st,
+                       (const uint16_t*)x, M, K, xs, (const uint32_t*)qw, N, pc,
+                       (const typename Elem<SDT>::T*)qs, qz, gsz / 128, (uint16_t*)y, g_contig, g_nt);
+  }
+}
+
+// Tuning knobs (read once): ANNA_MI_INT4_GEMV_WAVES in {4, 8} splits K across that many
+// waves per workgroup; ANNA_MI_INT4_GEMV_TILES in {1, 2} sets 16-row tiles per wave.
+
+template <int XDT, int SDT>
+void dispatch_gemv(const void* x, int64_t M, int64_t K, int64_t xs, const int32_t* qw, int64_t N, int64_t pc,
+                   const void* qs, const int8_t* qz, int64_t gsz, void* y, hipStream_t st) {
+  static const int env_waves = env_int("ANNA_MI_INT4_GEMV_WAVES", 0);
+  static const int env_tiles = env_int("ANNA_MI_INT4_GEMV_TILES", 0);
+  const int64_t nblk = (K + 127) / 128;
+  const int waves = env_waves ? env_waves : (nblk >= 32 ? 8 : 4);
+  const int tiles = env_tiles ? env_tiles : 1;
+  if (waves == 8 && tiles == 2) launch_gemv<XDT, SDT, 2, 8>(x, M, K, xs, qw, N, pc, qs, qz, gsz, y, st);
+  else if (waves == 8) launch_gemv<XDT, SDT, 1, 8>(x, M, K, xs, qw, N, pc, qs, qz, gsz, y, st);
+  else if (tiles == 2) launch_gemv<XDT, SDT, 2, 4>(x, M, K, xs, qw, N, pc, qs, qz, gsz, y, st);
+  else launch_gemv<XDT, SDT, 1, 4>(x, M, K, xs, qw, N, pc, qs, qz, gsz, y, st);
 }
 
 }  // namespace
@@ -430,12 +726,47 @@ extern "C" int anna_mi_int4_linear(const void* x, int x_dtype, int64_t M, int64_
   const bool x16 = x_dtype != ANNA_MI_F32;
   const bool aligned = ((uintptr_t)x % 16 == 0) && (xs % 8 == 0) && (K % 8 == 0) &&
                        ((uintptr_t)qweight % 16 == 0) && (pc % 4 == 0) && (gsz % 128 == 0);
+  if (x16 && aligned && M <= 2 && K % 32 == 0 && gsz % 32 == 0) {
+    static const int env_dot2_rg = env_int("ANNA_MI_INT4_DOT2_RG", 8);
+    const int64_t ksl = 16 * 32;
+    int64_t waves = (K + ksl - 1) / ksl;
+    waves = waves > DOT2_MAX_WAVES ? DOT2_MAX_WAVES : waves;
+    ANNA_DISPATCH_DTYPE(scale_dtype, SDT, {
+      auto go = [&](auto xdt_tag, auto mr_tag, auto rg_tag) {
+        constexpr int XDT = decltype(xdt_tag)::value, MR = decltype(mr_tag)::value, RG = decltype(rg_tag)::value;
+        dim3 grid((unsigned)((N + 4 * RG - 1) / (4 * RG)));
+        hipLaunchKernelGGL((int4_gemv_dot2<XDT, SDT, MR, RG>), grid, dim3((unsigned)(64 * waves)), 0, st,
+                           (const uint16_t*)x, M, K, xs, (const uint32_t*)qweight, N, pc,
+                           (const typename Elem<SDT>::T*)qscale, qzeros, gsz, (uint16_t*)y);
+      };
+      using I1 = std::integral_constant<int, 1>;
+      using I2 = std::integral_constant<int, 2>;
+      using I4 = std::integral_constant<int, 4>;
+      using I8 = std::integral_constant<int, 8>;
+      using I16 = std::integral_constant<int, 16>;
+      using XB = std::integral_constant<int, ANNA_MI_BF16>;
+      using XH = std::integral_constant<int, ANNA_MI_F16>;
+      const bool bf = x_dtype == ANNA_MI_BF16;
+      if (env_dot2_rg == 4) {
+        if (bf) { if (M == 1) go(XB{}, I1{}, I4{}); else go(XB{}, I2{}, I4{}); }
+        else { if (M == 1) go(XH{}, I1{}, I4{}); else go(XH{}, I2{}, I4{}); }
+      } else if (env_dot2_rg == 16) {
+        if (bf) { if (M == 1) go(XB{}, I1{}, I16{}); else go(XB{}, I2{}, I16{}); }
+        else { if (M == 1) go(XH{}, I1{}, I16{}); else go(XH{}, I2{}, I16{}); }
+      } else {
+        if (bf) { if (M == 1) go(XB{}, I1{}, I8{}); else go(XB{}, I2{}, I8{}); }
+        else { if (M == 1) go(XH{}, I1{}, I8{}); else go(XH{}, I2{}, I8{}); }
+      }
+    });
+    ANNA_LAUNCH_CHECK("int4_gemv_dot2");
+    return ANNA_MI_OK;
+  }
   if (x16 && aligned && M <= 16) {
     ANNA_DISPATCH_DTYPE(scale_dtype, SDT, {
       if (x_dtype == ANNA_MI_BF16)
-        launch_gemv<ANNA_MI_BF16, SDT, 1, 4>(x, M, K, xs, qweight, N, pc, qscale, qzeros, gsz, y, st);
+        dispatch_gemv<ANNA_MI_BF16, SDT>(x, M, K, xs, qweight, N, pc, qscale, qzeros, gsz, y, st);
       else
-        launch_gemv<ANNA_MI_F16, SDT, 1, 4>(x, M, K, xs, qweight, N, pc, qscale, qzeros, gsz, y, st);
+        dispatch_gemv<ANNA_MI_F16, SDT>(x, M, K, xs, qweight, N, pc, qscale, qzeros, gsz, y, st);
     });
     ANNA_LAUNCH_CHECK("int4_gemv_mfma");
     return ANNA_MI_OK;

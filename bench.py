@@ -148,7 +148,10 @@ def cpu_baseline_int4(m, n, k, group, budget_s):
 
 def section_int4(args, device):
     sweep = []
-    for (m, n, k) in [(1, 6144, 2048)] + [(m, n, 4096) for n in (12288, 6144) for m in (1, 8, 64, 256, 2048)]:
+    points = [(1, 6144, 2048)] + [(m, n, 4096) for n in (12288, 6144) for m in (1, 8, 64, 256, 2048)]
+    if args.int4_points:
+        points = [tuple(int(v) for v in p.split("x")) for p in args.int4_points.split(",")]
+    for (m, n, k) in points:
         steps = args.steps if m <= 64 else max(10, args.steps // 4)
         r = bench_int4_point(m, n, k, steps, args.warmup, device)
         log(f"int4 M={m:5d} N={n:6d} K={k}: {r['us']:8.2f} us  {r['GB/s']:8.1f} GB/s  "
@@ -165,6 +168,7 @@ def main() -> int:
     ap.add_argument("--sections", default="int4")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--int4-points", default="", help="comma list of MxNxK (default: the BASELINE sweep)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -181,7 +185,8 @@ def main() -> int:
     wanted = set(args.sections.split(","))
     if "int4" in wanted:
         sections["int4_sweep"] = section_int4(args, device)
-    head = next(r for r in sections["int4_sweep"] if (r["M"], r["N"], r["K"]) == (1, 12288, 4096))
+    head = next((r for r in sections["int4_sweep"] if (r["M"], r["N"], r["K"]) == (1, 12288, 4096)),
+                sections["int4_sweep"][0])
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline_int4(1, 12288, 4096, 128, args.cpu_seconds)

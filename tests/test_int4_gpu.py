@@ -38,6 +38,9 @@ LINEAR_CASES = [
     (64, 1024, 256, 128, "bf16"),
     (130, 256, 200, 128, "fp32"),
     (5, 96, 40, 32, "fp32"),        # group 32: generic kernel
+    (1, 96, 40, 32, "fp32"),        # group 32 on the dot2 GEMV, partial k-slice
+    (2, 9216, 72, 128, "bf16"),     # dot2 GEMV with more k-slices than waves
+    (1, 4096, 12288, 128, "bf16"),  # benchmark config 2, M = 1
 ]
 
 
@@ -56,9 +59,10 @@ def test_int4_linear_matches_oracle(gpu, m, k, n, group, sdt):
 
 
 @pytest.mark.parametrize("xdt", [torch.float16, torch.float32])
-def test_int4_linear_other_activation_dtypes(gpu, xdt):
+@pytest.mark.parametrize("m", [1, 4])
+def test_int4_linear_other_activation_dtypes(gpu, xdt, m):
     rng = np.random.default_rng(7)
-    m, k, n, group = 4, 1024, 192, 128
+    k, n, group = 1024, 192, 128
     qw, qs, qz = int4_payload(rng, n, k, group, scale_dtype="fp32")
     xb = orc.bf16_bits(rng.normal(size=(m, k)).astype(np.float32))
     ref = orc.int4_linear(xb, qw, qs, qz, group)
