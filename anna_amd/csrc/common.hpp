@@ -105,6 +105,15 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup p runs on XCD p % 8).
+// Remapping p to a tile index this way hands each XCD a contiguous range of tiles, so
+// tiles that share cache lines (neighbouring rows of scales / zero points) meet in one L2.
+constexpr int NUM_XCD = 8;
+__device__ __forceinline__ int64_t xcd_tile(int64_t p, int64_t tiles) {
+  if (tiles % NUM_XCD != 0) return p;
+  return (p % NUM_XCD) * (tiles / NUM_XCD) + p / NUM_XCD;
+}
+
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 }  // namespace anna

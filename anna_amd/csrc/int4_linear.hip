@@ -34,12 +34,17 @@ namespace {
 // the MFMA: element 2p is nibble p, element 2p+1 is nibble p+4.
 template <int XDT>
 __device__ __forceinline__ u32x4 nibbles_to_frag(uint32_t w) {
+  // The magic constant is materialized in a VGPR (one VOP1 move, hoisted by the
+  // compiler) so that each pair is a single v_and_or_b32 (mask in an SGPR): VOP3 on
+  // gfx9 takes no literal operands.
   constexpr uint32_t MAGIC = XDT == ANNA_MI_BF16 ? 0x43004300u : 0x64006400u;
+  uint32_t magic;
+  asm("v_mov_b32 %0, %1" : "=v"(magic) : "i"(MAGIC));
   u32x4 r;
-  r.x = (w & 0x000F000Fu) | MAGIC;
-  r.y = ((w >> 4) & 0x000F000Fu) | MAGIC;
-  r.z = ((w >> 8) & 0x000F000Fu) | MAGIC;
-  r.w = ((w >> 12) & 0x000F000Fu) | MAGIC;
+  r.x = (w & 0x000F000Fu) | magic;
+  r.y = ((w >> 4) & 0x000F000Fu) | magic;
+  r.z = ((w >> 8) & 0x000F000Fu) | magic;
+  r.w = ((w >> 12) & 0x000F000Fu) | magic;
   return r;
 }
 
@@ -86,7 +91,7 @@ __global__ __launch_bounds__(64 * KW) void int4_gemv_mfma(
   const int wave = threadIdx.x >> 6;
   const int r = lane & 15;
   const int kq = lane >> 4;
-  const int64_t n_base = (int64_t)blockIdx.x * (16 * NT);
+  const int64_t n_base = xcd_tile(blockIdx.x, gridDim.x) * (16 * NT);
   const bool m_ok = r < M;
   const int64_t nblk = (K + 127) >> 7;
   const int64_t xp = K + 8;  // LDS row pitch (elements): rows land 4 banks apart
@@ -296,7 +301,7 @@ __global__ __launch_bounds__(64 * DOT2_MAX_WAVES) void int4_gemv_dot2(
     const uint16_t* __restrict__ x, int64_t M, int64_t K, int64_t xs,
     const uint32_t* __restrict__ qw, int64_t N, int64_t pc,
     const typename Elem<SDT>::T* __restrict__ qs, const int8_t* __restrict__ qz,
-    int64_t gsz, uint16_t* __restrict__ y) {
+    int gshift, uint16_t* __restrict__ y) {
   constexpr int RPI = 4;        // rows per load instruction: 16 lanes x 16 B per row
   constexpr int RW = RPI * RG;  // rows per workgroup
   constexpr int KSL = 512;      // k per wave slice
@@ -307,8 +312,8 @@ __global__ __launch_bounds__(64 * DOT2_MAX_WAVES) void int4_gemv_dot2(
   const int wave = threadIdx.x >> 6;
   const int kw = blockDim.x >> 6;
   const int sub = lane >> 4, c = lane & 15;
-  const int64_t n0 = (int64_t)blockIdx.x * RW;
-  const int64_t G = (K + gsz - 1) / gsz;
+  const int64_t n0 = xcd_tile(blockIdx.x, gridDim.x) * RW;
+  const int64_t G = (K + (1 << gshift) - 1) >> gshift;
   // Weight rows of this workgroup; rows >= N fall outside num_records and read 0.
   const int64_t rows_here = N - n0 < RW ? N - n0 : RW;
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(qw + n0 * pc, (uint32_t)(rows_here * pc * 4));
@@ -337,7 +342,7 @@ __global__ __launch_bounds__(64 * DOT2_MAX_WAVES) void int4_gemv_dot2(
     u32x4 wv[RG];
     float sc[RG], cz[RG];
     const uint32_t wo = k_ok ? (uint32_t)((sub * pc + (kl >> 3)) * 4) : OOB;
-    const int64_t grp = k_ok ? kl / gsz : 0;
+    const int64_t grp = k_ok ? kl >> gshift : 0;
     const uint32_t so = k_ok ? (uint32_t)(grp * N + n0 + sub) : OOB / 4;
 #pragma unroll
     for (int g = 0; g < RG; ++g) {
@@ -726,8 +731,10 @@ extern "C" int anna_mi_int4_linear(const void* x, int x_dtype, int64_t M, int64_
   const bool x16 = x_dtype != ANNA_MI_F32;
   const bool aligned = ((uintptr_t)x % 16 == 0) && (xs % 8 == 0) && (K % 8 == 0) &&
                        ((uintptr_t)qweight % 16 == 0) && (pc % 4 == 0) && (gsz % 128 == 0);
-  if (x16 && aligned && M <= 2 && K % 32 == 0 && gsz % 32 == 0) {
-    static const int env_dot2_rg = env_int("ANNA_MI_INT4_DOT2_RG", 8);
+  const bool gsz_pow2 = gsz >= 32 && (gsz & (gsz - 1)) == 0;
+  if (x16 && aligned && M <= 2 && K % 32 == 0 && gsz_pow2) {
+    const int gshift = __builtin_ctzll((unsigned long long)gsz);
+    static const int env_dot2_rg = env_int("ANNA_MI_INT4_DOT2_RG", 4);
     const int64_t ksl = 16 * 32;
     int64_t waves = (K + ksl - 1) / ksl;
     waves = waves > DOT2_MAX_WAVES ? DOT2_MAX_WAVES : waves;
@@ -737,7 +744,7 @@ extern "C" int anna_mi_int4_linear(const void* x, int x_dtype, int64_t M, int64_
         dim3 grid((unsigned)((N + 4 * RG - 1) / (4 * RG)));
         hipLaunchKernelGGL((int4_gemv_dot2<XDT, SDT, MR, RG>), grid, dim3((unsigned)(64 * waves)), 0, st,
                            (const uint16_t*)x, M, K, xs, (const uint32_t*)qweight, N, pc,
-                           (const typename Elem<SDT>::T*)qscale, qzeros, gsz, (uint16_t*)y);
+                           (const typename Elem<SDT>::T*)qscale, qzeros, gshift, (uint16_t*)y);
       };
       using I1 = std::integral_constant<int, 1>;
       using I2 = std::integral_constant<int, 2>;
