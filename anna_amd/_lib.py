@@ -32,6 +32,42 @@ PROTOTYPES: dict[str, list] = {
     "anna_mi_autoround_to_int4": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P],
 }
 
+
+class View(ctypes.Structure):
+    """anna_mi_view: pointer + 4 element strides."""
+
+    _fields_ = [("ptr", ctypes.c_void_p), ("s0", _I64), ("s1", _I64), ("s2", _I64), ("s3", _I64)]
+
+
+class DecodeArgs(ctypes.Structure):
+    """anna_mi_decode_args (field order and types as in include/anna_mi.h)."""
+
+    _fields_ = [
+        ("dtype", _I), ("batch", _I64), ("q_heads", _I64), ("kv_heads", _I64), ("head_dim", _I64),
+        ("query", View), ("len1", _I64), ("key_format", _I), ("key", View), ("key_norms", View), ("key_bits", _I),
+        ("value_format", _I), ("value", View), ("value_scales", View), ("value_zeros", View), ("value_bits", _I),
+        ("value_group_size", _I64), ("rotation", _P), ("rotation_t", _P), ("key_centroids", _P),
+        ("value_centroids", _P), ("query_rot", _P), ("len2", _I64), ("residual_key", View), ("residual_value", View),
+        ("scaling", _F), ("block_size", _I64), ("gate_layout", _I), ("gate", View), ("out", View),
+        ("partial_stats", View), ("partial_values", View), ("partial_capacity", _I64),
+    ]
+
+
+PROTOTYPES.update({
+    "anna_mi_tq_rotation": [_I64, ctypes.c_uint64, _P],
+    "anna_mi_tq_codebook": [_I, _I64, _P, _P],
+    "anna_mi_tq_mse_quantize": [_P, _I, _I64, _I64, _I64, _P, _P, _I, _P, _P, _P],
+    "anna_mi_tq_mse_dequant": [_P, _P, _I64, _I64, _P, _P, _I, _P, _I, _I64, _P],
+    "anna_mi_tq_values_quantize": [_P, _I, _I64, _I64, _I64, _I64, _I64, _I, _I64, _P, _P, _P, _P],
+    "anna_mi_tq_values_dequant": [_P, _P, _P, _I, _I64, _I64, _I, _I64, _P, _I, _P],
+    "anna_mi_gqa_decode_splitkv": [ctypes.POINTER(DecodeArgs), _P],
+})
+# entry points that do not return a status code
+RAW_PROTOTYPES: dict[str, tuple] = {
+    "anna_mi_decode_num_blocks": (_I64, [ctypes.POINTER(DecodeArgs)]),
+    "anna_mi_sizeof_decode_args": (_I64, []),
+}
+
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
 
@@ -55,6 +91,10 @@ def load() -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.restype = ctypes.c_int
             fn.argtypes = argtypes
+        for name, (restype, argtypes) in RAW_PROTOTYPES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
         _lib = lib
         return lib
 
@@ -72,6 +112,14 @@ def dtype_code(dtype: torch.dtype) -> int:
         return _DTYPE_CODES[dtype]
     except KeyError:
         raise RuntimeError(f"unsupported dtype {dtype}; expected bfloat16, float16 or float32") from None
+
+
+def view(t: torch.Tensor | None, dims: tuple[int, ...] = (0, 1, 2, 3)) -> View:
+    """View over tensor dims `dims` (index -1 = absent, stride 0)."""
+    if t is None:
+        return View(None, 0, 0, 0, 0)
+    st = [t.stride(d) if d >= 0 else 0 for d in dims] + [0] * (4 - len(dims))
+    return View(t.data_ptr(), *st[:4])
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

@@ -1,0 +1,390 @@
+// Split-KV (flash-decoding) GQA decode attention for one query token per sequence.
+//
+// Kernel 1 (decode_split_kernel): one workgroup per (block of tokens, KV head, batch).
+//   All G = Hq/Hkv query heads of the KV head are processed together, so each K/V
+//   element is read (and dequantized) once for the whole group instead of once per
+//   q-head.  4 waves share the block's tokens; a lane owns D/64 consecutive dims; each
+//   wave keeps an online softmax per head, and the waves are merged through LDS.
+//   Output: per (b, q-head, block) the running max, the denominator and the
+//   unnormalized accumulator, in the reference's partial_stats / partial_values layout.
+// Kernel 2 (decode_merge_kernel): log-sum-exp merge of the blocks per (b, q-head),
+//   optional un-rotation of TQ-MSE value accumulators, optional sigmoid gate.
+//
+// Reference: launch_gqa_decode_splitkv_fused_xpu (gated_delta_fused_op.sycl:4494-4706)
+// and launch_gqa_decode_splitkv_turboquant_fused_xpu (sycl:4771-5094).
+#include "common.hpp"
+
+namespace anna {
+namespace {
+
+constexpr int DEC_WAVES = 4;
+
+__device__ __forceinline__ float ldv(const void* p, int64_t i, int dt) {
+  if (dt == ANNA_MI_BF16) return bf16_bits_to_f32(((const uint16_t*)p)[i]);
+  if (dt == ANNA_MI_F16) return f16_bits_to_f32(((const uint16_t*)p)[i]);
+  return ((const float*)p)[i];
+}
+
+__device__ __forceinline__ void stv(const void* p, int64_t i, int dt, float v) {
+  if (dt == ANNA_MI_BF16) ((uint16_t*)p)[i] = f32_to_bf16_bits(v);
+  else if (dt == ANNA_MI_F16) ((uint16_t*)p)[i] = f32_to_f16_bits(v);
+  else ((float*)p)[i] = v;
+}
+
+__device__ __forceinline__ int sbits(int bits) { return bits == 2 ? 2 : 4; }
+
+struct Split {
+  int64_t eb, nb1, eb2;  // block size (segment 1 or whole range), blocks of segment 1, residual block size
+  int aligned;           // 1: blocks never straddle the two segments
+};
+
+// q' = R q for every (b, q-head); grid (Hq, B), D threads.
+__global__ __launch_bounds__(1024) void decode_rotate_query_kernel(const anna_mi_decode_args a) {
+  const int64_t h = blockIdx.x, b = blockIdx.y, D = a.head_dim;
+  const int i = threadIdx.x;
+  const int64_t qb = b * a.query.s0 + h * a.query.s1;
+  float acc = 0.f;
+  for (int64_t k = 0; k < D; ++k) acc = fmaf(a.rotation_t[k * D + i], ldv(a.query.ptr, qb + k * a.query.s3, a.dtype), acc);
+  a.query_rot[(b * a.q_heads + h) * D + i] = acc;
+}
+
+template <int KF, int VF, int DPL, int GM>  // GM: max q-heads per KV group held in registers
+__global__ __launch_bounds__(64 * DEC_WAVES) void decode_split_kernel(const anna_mi_decode_args a, const Split sp) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t blk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int G = (int)(a.q_heads / a.kv_heads);
+  const int64_t D = a.head_dim, L1 = a.len1, L = a.len1 + a.len2;
+  const int dt = a.dtype;
+
+  int64_t t0, t1;
+  if (sp.aligned && blk >= sp.nb1) {
+    t0 = L1 + (blk - sp.nb1) * sp.eb2;
+    t1 = t0 + sp.eb2 < L ? t0 + sp.eb2 : L;
+  } else {
+    t0 = blk * sp.eb;
+    const int64_t lim = sp.aligned ? L1 : L;
+    t1 = t0 + sp.eb < lim ? t0 + sp.eb : lim;
+  }
+
+  __shared__ float s_m[DEC_WAVES][16], s_l[DEC_WAVES][16];
+  extern __shared__ float s_acc[];  // [G][D]
+  for (int64_t i = threadIdx.x; i < (int64_t)G * D; i += blockDim.x) s_acc[i] = 0.f;
+
+  // With TQ-MSE keys blocks never straddle the segments: the whole block scores either
+  // rotated codes (against q' = R q) or dense residual keys (against q).
+  const bool rot_block = KF == ANNA_MI_KEYS_TQ_MSE && t0 < L1;
+  float qv[GM][DPL];
+#pragma unroll
+  for (int h = 0; h < GM; ++h)
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+      const int64_t d = lane * DPL + j;
+      const int64_t hq = kvh * G + h;
+      float v = 0.f;
+      if (h < G) {
+        v = rot_block ? a.query_rot[(b * a.q_heads + hq) * D + d]
+                      : ldv(a.query.ptr, b * a.query.s0 + hq * a.query.s1 + d * a.query.s3, dt);
+      }
+      qv[h][j] = v;
+    }
+  float m[GM], l[GM], acc[GM][DPL];
+#pragma unroll
+  for (int h = 0; h < GM; ++h) {
+    m[h] = -INFINITY;
+    l[h] = 0.f;
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) acc[h][j] = 0.f;
+  }
+
+  const int ksb = sbits(a.key_bits), kper = 8 / ksb;
+  const int vsb = sbits(a.value_bits), vper = 8 / vsb;
+  for (int64_t t = t0 + wave; t < t1; t += DEC_WAVES) {
+    const bool res = t >= L1;
+    const int64_t tr = t - L1;
+    float kv[DPL], vv[DPL];
+    if (!res) {
+      if constexpr (KF == ANNA_MI_KEYS_TQ_MSE) {
+        const int64_t cb = b * a.key.s0 + kvh * a.key.s1 + t * a.key.s2;
+        const float nk = f16_bits_to_f32(((const uint16_t*)a.key_norms.ptr)[b * a.key_norms.s0 + kvh * a.key_norms.s1 +
+                                                                            t * a.key_norms.s2]);
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) {
+          const int64_t d = lane * DPL + j;
+          const uint32_t byte = ((const uint8_t*)a.key.ptr)[cb + (d / kper) * a.key.s3];
+          kv[j] = a.key_centroids[(byte >> (ksb * (d % kper))) & ((1u << ksb) - 1u)] * nk;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < DPL; ++j)
+          kv[j] = ldv(a.key.ptr, b * a.key.s0 + kvh * a.key.s1 + t * a.key.s2 + (lane * DPL + j) * a.key.s3, dt);
+      }
+      if constexpr (VF == ANNA_MI_VALUES_DENSE) {
+#pragma unroll
+        for (int j = 0; j < DPL; ++j)
+          vv[j] = ldv(a.value.ptr, b * a.value.s0 + kvh * a.value.s1 + t * a.value.s2 + (lane * DPL + j) * a.value.s3, dt);
+      } else if constexpr (VF == ANNA_MI_VALUES_MINMAX) {
+        const int64_t cb = b * a.value.s0 + kvh * a.value.s1 + t * a.value.s2;
+        const int64_t sb0 = b * a.value_scales.s0 + kvh * a.value_scales.s1 + t * a.value_scales.s2;
+        const int64_t zb0 = b * a.value_zeros.s0 + kvh * a.value_zeros.s1 + t * a.value_zeros.s2;
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) {
+          const int64_t d = lane * DPL + j;
+          const uint32_t byte = ((const uint8_t*)a.value.ptr)[cb + (d / vper) * a.value.s3];
+          const uint32_t q = (byte >> (vsb * (d % vper))) & ((1u << vsb) - 1u);
+          const int64_t g = d / a.value_group_size;
+          vv[j] = (float)q * ldv(a.value_scales.ptr, sb0 + g * a.value_scales.s3, dt) +
+                  ldv(a.value_zeros.ptr, zb0 + g * a.value_zeros.s3, dt);
+        }
+      } else {
+        const int64_t cb = b * a.value.s0 + kvh * a.value.s1 + t * a.value.s2;
+        const float nv = f16_bits_to_f32(((const uint16_t*)a.value_scales.ptr)[b * a.value_scales.s0 +
+                                                                               kvh * a.value_scales.s1 +
+                                                                               t * a.value_scales.s2]);
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) {
+          const int64_t d = lane * DPL + j;
+          const uint32_t byte = ((const uint8_t*)a.value.ptr)[cb + (d / vper) * a.value.s3];
+          vv[j] = a.value_centroids[(byte >> (vsb * (d % vper))) & ((1u << vsb) - 1u)] * nv;
+        }
+      }
+    } else {
+      const anna_mi_view& rk = a.residual_key;
+      const anna_mi_view& rv = a.residual_value;
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) {
+        const int64_t d = lane * DPL + j;
+        kv[j] = ldv(rk.ptr, b * rk.s0 + kvh * rk.s1 + tr * rk.s2 + d * rk.s3, dt);
+        vv[j] = ldv(rv.ptr, b * rv.s0 + kvh * rv.s1 + tr * rv.s2 + d * rv.s3, dt);
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < GM; ++h) {
+      if (h >= G) continue;
+      float p = 0.f;
+#pragma unroll
+      for (int j = 0; j < DPL; ++j)
+        p = fmaf(qv[h][j], kv[j], p);
+      const float s = wave_sum(p) * a.scaling;
+      const float nm = fmaxf(m[h], s);
+      const float alpha = l[h] == 0.f ? 0.f : expf(m[h] - nm);
+      const float e = expf(s - nm);
+      l[h] = l[h] * alpha + e;
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) acc[h][j] = acc[h][j] * alpha + e * vv[j];
+      m[h] = nm;
+    }
+  }
+  // merge the 4 waves: common max, rescale, LDS float atomics
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < GM; ++h)
+      if (h < G) {
+        s_m[wave][h] = m[h];
+        s_l[wave][h] = l[h];
+      }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < GM; ++h) {
+    if (h >= G) continue;
+    float M = -INFINITY;
+    for (int w = 0; w < DEC_WAVES; ++w) M = fmaxf(M, s_m[w][h]);
+    const float f = l[h] == 0.f ? 0.f : expf(m[h] - M);
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) atomicAdd(&s_acc[h * D + lane * DPL + j], acc[h][j] * f);
+  }
+  __syncthreads();
+  for (int64_t i = threadIdx.x; i < (int64_t)G * D; i += blockDim.x) {
+    const int h = (int)(i / D);
+    const int64_t d = i % D, hq = kvh * G + h;
+    const anna_mi_view& pv = a.partial_values;
+    ((float*)pv.ptr)[b * pv.s0 + hq * pv.s1 + blk * pv.s2 + d * pv.s3] = s_acc[i];
+  }
+  if (threadIdx.x < G) {
+    const int h = threadIdx.x;
+    float M = -INFINITY, S = 0.f;
+    for (int w = 0; w < DEC_WAVES; ++w) M = fmaxf(M, s_m[w][h]);
+    for (int w = 0; w < DEC_WAVES; ++w)
+      if (s_l[w][h] != 0.f) S += s_l[w][h] * expf(s_m[w][h] - M);
+    const anna_mi_view& ps = a.partial_stats;
+    const int64_t base = b * ps.s0 + (kvh * G + h) * ps.s1 + blk * ps.s2;
+    ((float*)ps.ptr)[base] = M;
+    ((float*)ps.ptr)[base + ps.s3] = S;
+  }
+}
+
+// grid (Hq, B), 256 threads.  Blocks [0, nrot) hold rotated (TQ-MSE) value accumulators.
+__global__ __launch_bounds__(256) void decode_merge_kernel(const anna_mi_decode_args a, int64_t nblk, int64_t nrot) {
+  extern __shared__ float s_rot[];  // [D] rotated accumulator
+  __shared__ float s_red[256];
+  const int64_t h = blockIdx.x, b = blockIdx.y, D = a.head_dim;
+  const anna_mi_view& ps = a.partial_stats;
+  const anna_mi_view& pv = a.partial_values;
+  const float* st = (const float*)ps.ptr + b * ps.s0 + h * ps.s1;
+  const float* va = (const float*)pv.ptr + b * pv.s0 + h * pv.s1;
+  float mx = -INFINITY;
+  for (int64_t k = threadIdx.x; k < nblk; k += blockDim.x) mx = fmaxf(mx, st[k * ps.s2]);
+  s_red[threadIdx.x] = mx;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if ((int)threadIdx.x < s) s_red[threadIdx.x] = fmaxf(s_red[threadIdx.x], s_red[threadIdx.x + s]);
+    __syncthreads();
+  }
+  const float M = s_red[0];
+  __syncthreads();
+  float den = 0.f;
+  for (int64_t k = threadIdx.x; k < nblk; k += blockDim.x) {
+    const float dk = st[k * ps.s2 + ps.s3];
+    if (dk != 0.f) den += dk * expf(st[k * ps.s2] - M);
+  }
+  s_red[threadIdx.x] = den;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if ((int)threadIdx.x < s) s_red[threadIdx.x] += s_red[threadIdx.x + s];
+    __syncthreads();
+  }
+  const float denom = s_red[0];
+  float accr[4] = {0.f, 0.f, 0.f, 0.f};  // D <= 1024 -> at most 4 dims per thread
+  for (int j = 0; j < 4; ++j) {
+    const int64_t d = threadIdx.x + (int64_t)j * blockDim.x;
+    if (d >= D) break;
+    float ar = 0.f, aq = 0.f;
+    for (int64_t k = 0; k < nblk; ++k) {
+      const float dk = st[k * ps.s2 + ps.s3];
+      if (dk == 0.f) continue;
+      const float c = expf(st[k * ps.s2] - M) * va[k * pv.s2 + d * pv.s3];
+      if (k < nrot) ar += c; else aq += c;
+    }
+    if (nrot > 0) s_rot[d] = ar;
+    accr[j] = aq;
+  }
+  if (nrot > 0) __syncthreads();
+  for (int j = 0; j < 4; ++j) {
+    const int64_t d = threadIdx.x + (int64_t)j * blockDim.x;
+    if (d >= D) break;
+    float o = accr[j];
+    if (nrot > 0) {
+      float u = 0.f;
+      for (int64_t i = 0; i < D; ++i) u = fmaf(a.rotation[i * D + d], s_rot[i], u);
+      o += u;
+    }
+    o = denom > 0.f ? o / denom : 0.f;
+    if (a.gate_layout == ANNA_MI_GATE_FLAT) {
+      o *= 1.f / (1.f + expf(-ldv(a.gate.ptr, b * a.gate.s0 + (h * D + d) * a.gate.s2, a.dtype)));
+    } else if (a.gate_layout == ANNA_MI_GATE_HEADS) {
+      o *= 1.f / (1.f + expf(-ldv(a.gate.ptr, b * a.gate.s0 + h * a.gate.s1 + d * a.gate.s3, a.dtype)));
+    }
+    stv(a.out.ptr, b * a.out.s0 + h * a.out.s1 + d * a.out.s3, a.dtype, o);
+  }
+}
+
+Split make_split(const anna_mi_decode_args& a) {
+  Split sp{};
+  const int64_t bs = a.block_size < 16 ? 16 : a.block_size;
+  const int64_t L = a.len1 + a.len2;
+  sp.aligned = a.value_format == ANNA_MI_VALUES_TQ_MSE || a.key_format == ANNA_MI_KEYS_TQ_MSE;
+  if (sp.aligned) {
+    sp.eb = a.len1 > 0 ? (bs < a.len1 ? bs : a.len1) : 1;
+    sp.nb1 = a.len1 > 0 ? (a.len1 + sp.eb - 1) / sp.eb : 0;
+    sp.eb2 = a.len2 > 0 ? (bs < a.len2 ? bs : a.len2) : 1;
+  } else {
+    sp.eb = bs < L ? bs : L;
+    sp.nb1 = 0;
+    sp.eb2 = 1;
+  }
+  return sp;
+}
+
+int64_t total_blocks(const anna_mi_decode_args& a, const Split& sp) {
+  if (sp.aligned) return sp.nb1 + (a.len2 > 0 ? (a.len2 + sp.eb2 - 1) / sp.eb2 : 0);
+  const int64_t L = a.len1 + a.len2;
+  return (L + sp.eb - 1) / sp.eb;
+}
+
+template <int KF, int VF>
+void launch_split(const anna_mi_decode_args& a, const Split& sp, int64_t nblk, hipStream_t st) {
+  dim3 grid((unsigned)nblk, (unsigned)a.kv_heads, (unsigned)a.batch);
+  const int64_t G = a.q_heads / a.kv_heads;
+  const size_t lds = (size_t)G * a.head_dim * 4;
+  const dim3 blk(64 * DEC_WAVES);
+#define ANNA_SPLIT(DPL, GM) hipLaunchKernelGGL((decode_split_kernel<KF, VF, DPL, GM>), grid, blk, lds, st, a, sp)
+  const bool small = G <= 8;
+  switch (a.head_dim) {
+    case 64: if (small) ANNA_SPLIT(1, 8); else ANNA_SPLIT(1, 16); break;
+    case 128: if (small) ANNA_SPLIT(2, 8); else ANNA_SPLIT(2, 16); break;
+    case 256: if (small) ANNA_SPLIT(4, 8); else ANNA_SPLIT(4, 16); break;
+    default: ANNA_SPLIT(8, 8); break;
+  }
+#undef ANNA_SPLIT
+}
+
+}  // namespace
+}  // namespace anna
+
+using namespace anna;
+
+extern "C" int64_t anna_mi_sizeof_decode_args(void) { return (int64_t)sizeof(anna_mi_decode_args); }
+
+extern "C" int64_t anna_mi_decode_num_blocks(const anna_mi_decode_args* a) {
+  if (!a || a->len1 + a->len2 <= 0) return 0;
+  return total_blocks(*a, make_split(*a));
+}
+
+extern "C" int anna_mi_gqa_decode_splitkv(const anna_mi_decode_args* ap, void* stream) {
+  ANNA_CHECK(ap != nullptr, "anna_mi_gqa_decode_splitkv: null args");
+  const anna_mi_decode_args& a = *ap;
+  ANNA_CHECK(valid_dtype(a.dtype), "anna_mi_gqa_decode_splitkv: bad dtype code");
+  ANNA_CHECK(a.batch > 0 && a.q_heads > 0 && a.kv_heads > 0, "anna_mi_gqa_decode_splitkv: empty batch or heads");
+  ANNA_CHECK(a.q_heads % a.kv_heads == 0, "query heads must be divisible by kv_heads");
+  ANNA_CHECK(a.head_dim == 64 || a.head_dim == 128 || a.head_dim == 256 || a.head_dim == 512,
+             "anna_mi_gqa_decode_splitkv: head_dim must be 64, 128, 256 or 512 (got %lld)", (long long)a.head_dim);
+  const int64_t G = a.q_heads / a.kv_heads;
+  const int64_t gmax = a.head_dim == 512 ? 8 : 16;
+  ANNA_CHECK(G <= gmax, "anna_mi_gqa_decode_splitkv: %lld query heads per KV head exceed %lld", (long long)G, (long long)gmax);
+  ANNA_CHECK(a.len1 >= 0 && a.len2 >= 0 && a.len1 + a.len2 >= 1, "key_len must be positive");
+  ANNA_CHECK(a.block_size >= 16, "block_size must be at least 16");
+  ANNA_CHECK(a.key_format == ANNA_MI_KEYS_DENSE || a.key_format == ANNA_MI_KEYS_TQ_MSE, "bad key_format");
+  ANNA_CHECK(a.value_format >= ANNA_MI_VALUES_DENSE && a.value_format <= ANNA_MI_VALUES_TQ_MSE, "bad value_format");
+  ANNA_CHECK(a.query.ptr && a.out.ptr && a.partial_stats.ptr && a.partial_values.ptr, "null query/out/workspace");
+  if (a.len1 > 0) ANNA_CHECK(a.key.ptr && a.value.ptr, "null key/value");
+  if (a.len2 > 0) ANNA_CHECK(a.residual_key.ptr && a.residual_value.ptr, "null residual key/value");
+  if (a.value_format == ANNA_MI_VALUES_MINMAX && a.len1 > 0) {
+    ANNA_CHECK(a.value_bits == 2 || a.value_bits == 3 || a.value_bits == 4, "TurboQuant value_bits must be 2, 3, or 4");
+    ANNA_CHECK(a.value_group_size > 0 && a.head_dim % a.value_group_size == 0,
+               "TurboQuant value_group_size must evenly divide head_dim");
+    ANNA_CHECK(a.value_scales.ptr && a.value_zeros.ptr, "null value scales/zeros");
+  }
+  if (a.key_format == ANNA_MI_KEYS_TQ_MSE && a.len1 > 0)
+    ANNA_CHECK(a.key_norms.ptr && a.rotation_t && a.key_centroids && a.query_rot, "TQ-MSE keys need norms, rotation_t, centroids and query_rot");
+  if (a.value_format == ANNA_MI_VALUES_TQ_MSE && a.len1 > 0)
+    ANNA_CHECK(a.value_scales.ptr && a.rotation && a.value_centroids, "TQ-MSE values need norms, rotation and centroids");
+  if (a.gate_layout != ANNA_MI_GATE_NONE) ANNA_CHECK(a.gate.ptr != nullptr, "null gate");
+  const Split sp = make_split(a);
+  const int64_t nblk = total_blocks(a, sp);
+  ANNA_CHECK(nblk <= a.partial_capacity, "partial_stats/partial_values capacity %lld is smaller than %lld blocks",
+             (long long)a.partial_capacity, (long long)nblk);
+  hipStream_t st = as_stream(stream);
+  if (a.key_format == ANNA_MI_KEYS_TQ_MSE && a.len1 > 0) {
+    hipLaunchKernelGGL(decode_rotate_query_kernel, dim3((unsigned)a.q_heads, (unsigned)a.batch), dim3((unsigned)a.head_dim),
+                       0, st, a);
+    ANNA_LAUNCH_CHECK("decode_rotate_query_kernel");
+  }
+  const bool kq = a.key_format == ANNA_MI_KEYS_TQ_MSE;
+  switch (a.value_format) {
+    case ANNA_MI_VALUES_DENSE:
+      kq ? launch_split<1, 0>(a, sp, nblk, st) : launch_split<0, 0>(a, sp, nblk, st);
+      break;
+    case ANNA_MI_VALUES_MINMAX:
+      kq ? launch_split<1, 1>(a, sp, nblk, st) : launch_split<0, 1>(a, sp, nblk, st);
+      break;
+    default:
+      kq ? launch_split<1, 2>(a, sp, nblk, st) : launch_split<0, 2>(a, sp, nblk, st);
+      break;
+  }
+  ANNA_LAUNCH_CHECK("decode_split_kernel");
+  const int64_t nrot = a.value_format == ANNA_MI_VALUES_TQ_MSE ? sp.nb1 : 0;
+  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)a.q_heads, (unsigned)a.batch), dim3(256),
+                     (size_t)a.head_dim * 4, st, a, nblk, nrot);
+  ANNA_LAUNCH_CHECK("decode_merge_kernel");
+  return ANNA_MI_OK;
+}

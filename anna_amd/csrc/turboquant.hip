@@ -1,0 +1,335 @@
+// TurboQuant KV-cache packing and split-KV GQA decode attention on gfx950.
+//
+// Formats
+//   values (reference format, src/anna/model/turboquant.py:157-252): per (head, token,
+//     group of G dims) min/max quantization, scale = clamp((max-min)/(2^b-1), 1e-8) and
+//     zero = min stored in the value dtype, codes packed 4 per byte (2-bit) or 2 per byte
+//     (3/4-bit), element i at bits sb*(i % per_byte).
+//   TQ-MSE (this build's definition of the absent `turboquant` package's MSE quantizer,
+//     turboquant.py:75-82): y = R x with a seeded Haar rotation R, code_i = number of
+//     codebook thresholds t_j with y_i >= t_j * |x|, norm |x| stored as fp16; the
+//     reconstruction is |x|_fp16 * R^T c[code].  Codes pack like the values.
+//
+// Numerics of the MSE quantizer are fixed so that the GPU reproduces the CPU oracle bit
+// for bit: |x|^2 and every y_i are fma chains in ascending k, sqrt is correctly rounded.
+#include <math.h>
+#include <stdlib.h>
+
+#include <vector>
+
+#include "common.hpp"
+
+namespace anna {
+namespace {
+
+__host__ __device__ inline int storage_bits(int bits) { return bits == 2 ? 2 : 4; }
+
+// ------------------------------------------------------------------ host: rotation, codebook
+
+uint64_t splitmix64(uint64_t& s) {
+  uint64_t z = (s += 0x9E3779B97F4A7C15ull);
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+// Haar-distributed orthogonal D x D matrix: a seeded standard-normal matrix (splitmix64
+// stream, Box-Muller) whose rows are orthonormalized by modified Gram-Schmidt applied
+// twice, in fp64, then rounded to fp32.  Row i of the result is R[i][:], y = R x.
+void make_rotation(int64_t D, uint64_t seed, float* out) {
+  std::vector<double> g((size_t)(D * D));
+  uint64_t s = seed;
+  for (int64_t i = 0; i < D * D; i += 2) {
+    double u1 = ((double)(splitmix64(s) >> 11) + 0.5) * (1.0 / 9007199254740992.0);
+    double u2 = ((double)(splitmix64(s) >> 11) + 0.5) * (1.0 / 9007199254740992.0);
+    double r = sqrt(-2.0 * log(u1));
+    g[(size_t)i] = r * cos(6.283185307179586 * u2);
+    if (i + 1 < D * D) g[(size_t)i + 1] = r * sin(6.283185307179586 * u2);
+  }
+  for (int64_t i = 0; i < D; ++i) {
+    double* gi = &g[(size_t)(i * D)];
+    for (int pass = 0; pass < 2; ++pass)
+      for (int64_t j = 0; j < i; ++j) {
+        const double* gj = &g[(size_t)(j * D)];
+        double dot = 0.0;
+        for (int64_t k = 0; k < D; ++k) dot += gi[k] * gj[k];
+        for (int64_t k = 0; k < D; ++k) gi[k] -= dot * gj[k];
+      }
+    double nrm = 0.0;
+    for (int64_t k = 0; k < D; ++k) nrm += gi[k] * gi[k];
+    nrm = sqrt(nrm);
+    for (int64_t k = 0; k < D; ++k) gi[k] /= nrm;
+  }
+  for (int64_t i = 0; i < D * D; ++i) out[i] = (float)g[(size_t)i];
+}
+
+// Lloyd-Max quantizer of N(0, 1): positive half of the levels (Max 1960), to 17 digits.
+const double kLloydMax1[] = {0.79788456080286629};
+const double kLloydMax2[] = {0.45278003463649735, 1.5104176084991006};
+const double kLloydMax3[] = {0.2450941789442308, 0.75600528120588584, 1.3439092785050075, 2.151945704536995};
+const double kLloydMax4[] = {0.12839502985114548, 0.38804829949029002, 0.65675911853246316, 0.94234045648696207,
+                             1.2562311973471787,  1.6180463860218879,  2.0690172265313875,  2.732589570995156};
+
+}  // namespace
+
+// 2-bit levels are stored as fp16 magnitudes whose encodings share their low byte
+// (0x3C7E = 1.123046875, 0x437E = 3.74609375; ratio 3.335652 vs the Lloyd-Max 3.335686),
+// so a 2-bit code becomes an fp16 MFMA operand with one byte permute.
+constexpr float TQ2_A16 = 1.123046875f, TQ2_B16 = 3.74609375f;
+
+int tq_codebook(int bits, int64_t D, float* centroids, float* thresholds) {
+  const int n = 1 << bits;
+  const double* half = bits == 1 ? kLloydMax1 : bits == 2 ? kLloydMax2 : bits == 3 ? kLloydMax3 : kLloydMax4;
+  std::vector<double> lv((size_t)n);
+  const double inv = 1.0 / sqrt((double)D);
+  for (int i = 0; i < n / 2; ++i) {
+    double v = half[i];
+    if (bits == 2) v = i == 0 ? kLloydMax2[0] : kLloydMax2[0] * ((double)TQ2_B16 / (double)TQ2_A16);
+    lv[(size_t)(n / 2 + i)] = v * inv;
+    lv[(size_t)(n / 2 - 1 - i)] = -v * inv;
+  }
+  for (int i = 0; i < n; ++i) centroids[i] = (float)lv[(size_t)i];
+  for (int i = 0; i + 1 < n; ++i) thresholds[i] = (float)(0.5 * (lv[(size_t)i] + lv[(size_t)i + 1]));
+  return 0;
+}
+
+namespace {
+
+// ------------------------------------------------------------------ TQ-MSE quantize / dequant
+
+constexpr int TQ_VB = 16;  // vectors per workgroup
+
+// grid: ceil(nvec / VB); block: D threads (D multiple of 64, <= 1024)
+template <int XDT>
+__global__ __launch_bounds__(1024) void tq_mse_quantize_kernel(
+    const typename Elem<XDT>::T* __restrict__ x, int64_t nvec, int64_t D, int64_t xs,
+    const float* __restrict__ rot_t, const float* __restrict__ thr, int bits,
+    uint8_t* __restrict__ codes, uint16_t* __restrict__ norms) {
+  extern __shared__ float smem[];  // xs_[VB][D] then codes as bytes [VB][D]
+  float* xsm = smem;
+  uint8_t* csm = (uint8_t*)(smem + TQ_VB * D);
+  __shared__ float nrm[TQ_VB];
+  const int i = threadIdx.x;
+  const int64_t v0 = (int64_t)blockIdx.x * TQ_VB;
+  const int nv = (int)(nvec - v0 < TQ_VB ? nvec - v0 : TQ_VB);
+  for (int v = 0; v < TQ_VB; ++v) xsm[v * D + i] = v < nv ? Elem<XDT>::load(x, (v0 + v) * xs + i) : 0.f;
+  __syncthreads();
+  if (i < TQ_VB) {
+    float ss = 0.f;
+    for (int64_t k = 0; k < D; ++k) ss = __builtin_fmaf(xsm[i * D + k], xsm[i * D + k], ss);
+    nrm[i] = __builtin_sqrtf(ss);
+    if (i < nv) norms[v0 + i] = f32_to_f16_bits(nrm[i]);
+  }
+  float acc[TQ_VB];
+#pragma unroll
+  for (int v = 0; v < TQ_VB; ++v) acc[v] = 0.f;
+  for (int64_t k = 0; k < D; ++k) {
+    const float p = rot_t[k * D + i];
+#pragma unroll
+    for (int v = 0; v < TQ_VB; ++v) acc[v] = __builtin_fmaf(p, xsm[v * D + k], acc[v]);
+  }
+  __syncthreads();
+  const int nthr = (1 << bits) - 1;
+#pragma unroll
+  for (int v = 0; v < TQ_VB; ++v) {
+    uint32_t c = 0;
+    for (int j = 0; j < nthr; ++j) c += acc[v] >= __fmul_rn(thr[j], nrm[v]) ? 1u : 0u;
+    csm[v * D + i] = (uint8_t)c;
+  }
+  __syncthreads();
+  const int sb = storage_bits(bits), per = 8 / sb;
+  const int64_t pb = D / per;  // packed bytes per vector
+  for (int64_t idx = i; idx < (int64_t)nv * pb; idx += blockDim.x) {
+    const int64_t v = idx / pb, b = idx % pb;
+    uint32_t byte = 0;
+    for (int e = 0; e < per; ++e) byte |= (uint32_t)csm[v * D + b * per + e] << (sb * e);
+    codes[(v0 + v) * pb + b] = (uint8_t)byte;
+  }
+}
+
+// out[v][k] = norm_v * sum_i R[i][k] c[code_i]  (fp32 accumulation)
+template <int ODT>
+__global__ __launch_bounds__(1024) void tq_mse_dequant_kernel(
+    const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms, int64_t nvec, int64_t D,
+    const float* __restrict__ rot, const float* __restrict__ cent, int bits,
+    typename Elem<ODT>::T* __restrict__ out, int64_t os) {
+  extern __shared__ float yv[];  // [VB][D] centroid values
+  const int k = threadIdx.x;
+  const int64_t v0 = (int64_t)blockIdx.x * TQ_VB;
+  const int nv = (int)(nvec - v0 < TQ_VB ? nvec - v0 : TQ_VB);
+  const int sb = storage_bits(bits), per = 8 / sb;
+  const uint32_t mask = (1u << sb) - 1u;
+  const int64_t pb = D / per;
+  for (int v = 0; v < TQ_VB; ++v) {
+    float c = 0.f;
+    if (v < nv) c = cent[(codes[(v0 + v) * pb + k / per] >> (sb * (k % per))) & mask];
+    yv[v * D + k] = c;
+  }
+  __syncthreads();
+  float acc[TQ_VB];
+#pragma unroll
+  for (int v = 0; v < TQ_VB; ++v) acc[v] = 0.f;
+  for (int64_t i = 0; i < D; ++i) {
+    const float p = rot[i * D + k];
+#pragma unroll
+    for (int v = 0; v < TQ_VB; ++v) acc[v] = fmaf(p, yv[v * D + i], acc[v]);
+  }
+  for (int v = 0; v < nv; ++v) out[(v0 + v) * os + k] = Elem<ODT>::cvt(f16_bits_to_f32(norms[v0 + v]) * acc[v]);
+}
+
+// ------------------------------------------------------------------ values: min/max groups
+
+// One thread per (row, run of `gpt` groups); rows = H*T with row strides (sh, st).  A run
+// always ends on a packed-byte boundary (gpt = 1 when group_size is a multiple of the
+// pack width, else the whole row), so no two threads write the same byte.
+template <int DT>
+__global__ __launch_bounds__(256) void tq_values_quantize_kernel(
+    const typename Elem<DT>::T* __restrict__ v, int64_t H, int64_t T, int64_t D, int64_t sh, int64_t st,
+    int bits, int64_t gsz, int64_t gpt, uint8_t* __restrict__ data, typename Elem<DT>::T* __restrict__ scales,
+    typename Elem<DT>::T* __restrict__ zeros) {
+  const int64_t ng = D / gsz;
+  const int64_t runs = ng / gpt;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= H * T * runs) return;
+  const int64_t row = idx / runs, g0 = (idx % runs) * gpt;
+  const int64_t h = row / T, t = row % T;
+  const typename Elem<DT>::T* src = v + h * sh + t * st;
+  const float levels = (float)((1 << bits) - 1);
+  const int sb = storage_bits(bits), per = 8 / sb;
+  const int64_t pb = D / per;
+  uint32_t byte = 0;
+  for (int64_t g = g0; g < g0 + gpt; ++g) {
+    float vmin = INFINITY, vmax = -INFINITY;
+    for (int64_t j = 0; j < gsz; ++j) {
+      const float f = Elem<DT>::to_f32(src[g * gsz + j]);
+      vmin = fminf(vmin, f);
+      vmax = fmaxf(vmax, f);
+    }
+    float sc = __fdiv_rn(__fsub_rn(vmax, vmin), levels);
+    sc = sc < 1e-8f ? 1e-8f : sc;
+    const typename Elem<DT>::T sc_s = Elem<DT>::cvt(sc), z_s = Elem<DT>::cvt(vmin);
+    scales[row * ng + g] = sc_s;
+    zeros[row * ng + g] = z_s;
+    const float scf = Elem<DT>::to_f32(sc_s), zf = Elem<DT>::to_f32(z_s);
+    for (int64_t j = 0; j < gsz; ++j) {
+      const int64_t d = g * gsz + j;
+      float q = rintf(__fdiv_rn(__fsub_rn(Elem<DT>::to_f32(src[d]), zf), scf));
+      q = fminf(fmaxf(q, 0.f), levels);
+      byte |= (uint32_t)q << (sb * (d % per));
+      if (d % per == per - 1) {
+        data[row * pb + d / per] = (uint8_t)byte;
+        byte = 0;
+      }
+    }
+  }
+}
+
+template <int DT, int ODT>
+__global__ __launch_bounds__(256) void tq_values_dequant_kernel(
+    const uint8_t* __restrict__ data, const typename Elem<DT>::T* __restrict__ scales,
+    const typename Elem<DT>::T* __restrict__ zeros, int64_t rows, int64_t D, int bits, int64_t gsz,
+    typename Elem<ODT>::T* __restrict__ out) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= rows * D) return;
+  const int64_t row = idx / D, d = idx % D;
+  const int sb = storage_bits(bits), per = 8 / sb;
+  const uint32_t q = (data[row * (D / per) + d / per] >> (sb * (d % per))) & ((1u << sb) - 1u);
+  const int64_t gi = row * (D / gsz) + d / gsz;
+  out[idx] = Elem<ODT>::cvt((float)q * Elem<DT>::to_f32(scales[gi]) + Elem<DT>::to_f32(zeros[gi]));
+}
+
+}  // namespace
+}  // namespace anna
+
+using namespace anna;
+
+extern "C" int anna_mi_tq_rotation(int64_t D, uint64_t seed, float* out) {
+  ANNA_CHECK(out != nullptr && D > 0 && D <= 4096, "anna_mi_tq_rotation: bad arguments");
+  make_rotation(D, seed, out);
+  return ANNA_MI_OK;
+}
+
+extern "C" int anna_mi_tq_codebook(int bits, int64_t D, float* centroids, float* thresholds) {
+  ANNA_CHECK(bits >= 1 && bits <= 4, "anna_mi_tq_codebook: bits must be 1..4");
+  ANNA_CHECK(centroids && thresholds && D > 0, "anna_mi_tq_codebook: bad arguments");
+  return tq_codebook(bits, D, centroids, thresholds);
+}
+
+extern "C" int anna_mi_tq_mse_quantize(const void* x, int x_dtype, int64_t nvec, int64_t D, int64_t x_row_stride,
+                                       const float* rot_t, const float* thresholds, int bits, uint8_t* codes,
+                                       uint16_t* norms, void* stream) {
+  ANNA_CHECK(x && rot_t && thresholds && codes && norms, "anna_mi_tq_mse_quantize: null pointer");
+  ANNA_CHECK(valid_dtype(x_dtype), "anna_mi_tq_mse_quantize: bad dtype code");
+  ANNA_CHECK(bits >= 1 && bits <= 4, "anna_mi_tq_mse_quantize: bits must be 1..4");
+  ANNA_CHECK(D >= 64 && D <= 1024 && D % 64 == 0, "anna_mi_tq_mse_quantize: head_dim must be a multiple of 64 in [64, 1024]");
+  ANNA_CHECK(x_row_stride >= D, "anna_mi_tq_mse_quantize: row stride smaller than head_dim");
+  if (nvec <= 0) return ANNA_MI_OK;
+  const size_t lds = (size_t)TQ_VB * D * 4 + (size_t)TQ_VB * D;
+  ANNA_DISPATCH_DTYPE(x_dtype, XDT, {
+    hipLaunchKernelGGL((tq_mse_quantize_kernel<XDT>), dim3((unsigned)((nvec + TQ_VB - 1) / TQ_VB)), dim3((unsigned)D),
+                       lds, as_stream(stream), (const typename Elem<XDT>::T*)x, nvec, D, x_row_stride, rot_t,
+                       thresholds, bits, codes, norms);
+  });
+  ANNA_LAUNCH_CHECK("tq_mse_quantize_kernel");
+  return ANNA_MI_OK;
+}
+
+extern "C" int anna_mi_tq_mse_dequant(const uint8_t* codes, const uint16_t* norms, int64_t nvec, int64_t D,
+                                      const float* rot, const float* centroids, int bits, void* out, int out_dtype,
+                                      int64_t out_row_stride, void* stream) {
+  ANNA_CHECK(codes && norms && rot && centroids && out, "anna_mi_tq_mse_dequant: null pointer");
+  ANNA_CHECK(valid_dtype(out_dtype), "anna_mi_tq_mse_dequant: bad dtype code");
+  ANNA_CHECK(bits >= 1 && bits <= 4, "anna_mi_tq_mse_dequant: bits must be 1..4");
+  ANNA_CHECK(D >= 64 && D <= 1024 && D % 64 == 0, "anna_mi_tq_mse_dequant: head_dim must be a multiple of 64 in [64, 1024]");
+  if (nvec <= 0) return ANNA_MI_OK;
+  ANNA_DISPATCH_DTYPE(out_dtype, ODT, {
+    hipLaunchKernelGGL((tq_mse_dequant_kernel<ODT>), dim3((unsigned)((nvec + TQ_VB - 1) / TQ_VB)), dim3((unsigned)D),
+                       (size_t)TQ_VB * D * 4, as_stream(stream), codes, norms, nvec, D, rot, centroids, bits,
+                       (typename Elem<ODT>::T*)out, out_row_stride);
+  });
+  ANNA_LAUNCH_CHECK("tq_mse_dequant_kernel");
+  return ANNA_MI_OK;
+}
+
+extern "C" int anna_mi_tq_values_quantize(const void* values, int dtype, int64_t H, int64_t T, int64_t D,
+                                          int64_t stride_h, int64_t stride_t, int bits, int64_t group_size,
+                                          uint8_t* data, void* scales, void* zeros, void* stream) {
+  ANNA_CHECK(values && data && scales && zeros, "anna_mi_tq_values_quantize: null pointer");
+  ANNA_CHECK(valid_dtype(dtype), "anna_mi_tq_values_quantize: bad dtype code");
+  ANNA_CHECK(bits == 2 || bits == 3 || bits == 4, "Unsupported TurboQuant value bit-width: %d. Expected 2, 3, or 4.", bits);
+  ANNA_CHECK(group_size > 0 && D % group_size == 0,
+             "TurboQuant value group_size=%lld must evenly divide head_dim=%lld.", (long long)group_size, (long long)D);
+  ANNA_CHECK(D % (8 / storage_bits(bits)) == 0, "packed TurboQuant values need head_dim divisible by the pack width");
+  const int per = 8 / storage_bits(bits);
+  const int64_t gpt = group_size % per == 0 ? 1 : D / group_size;
+  const int64_t n = H * T * (D / group_size / gpt);
+  if (n <= 0) return ANNA_MI_OK;
+  ANNA_DISPATCH_DTYPE(dtype, DT, {
+    hipLaunchKernelGGL((tq_values_quantize_kernel<DT>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       as_stream(stream), (const typename Elem<DT>::T*)values, H, T, D, stride_h, stride_t, bits,
+                       group_size, gpt, data, (typename Elem<DT>::T*)scales, (typename Elem<DT>::T*)zeros);
+  });
+  ANNA_LAUNCH_CHECK("tq_values_quantize_kernel");
+  return ANNA_MI_OK;
+}
+
+extern "C" int anna_mi_tq_values_dequant(const uint8_t* data, const void* scales, const void* zeros, int dtype,
+                                         int64_t rows, int64_t D, int bits, int64_t group_size, void* out,
+                                         int out_dtype, void* stream) {
+  ANNA_CHECK(data && scales && zeros && out, "anna_mi_tq_values_dequant: null pointer");
+  ANNA_CHECK(valid_dtype(dtype) && valid_dtype(out_dtype), "anna_mi_tq_values_dequant: bad dtype code");
+  ANNA_CHECK(bits == 2 || bits == 3 || bits == 4, "anna_mi_tq_values_dequant: bits must be 2, 3 or 4");
+  ANNA_CHECK(group_size > 0 && D % group_size == 0, "anna_mi_tq_values_dequant: group_size must divide head_dim");
+  const int64_t n = rows * D;
+  if (n <= 0) return ANNA_MI_OK;
+  ANNA_DISPATCH_DTYPE(dtype, DT, {
+    ANNA_DISPATCH_DTYPE(out_dtype, ODT, {
+      hipLaunchKernelGGL((tq_values_dequant_kernel<DT, ODT>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                         as_stream(stream), data, (const typename Elem<DT>::T*)scales,
+                         (const typename Elem<DT>::T*)zeros, rows, D, bits, group_size,
+                         (typename Elem<ODT>::T*)out);
+    });
+  });
+  ANNA_LAUNCH_CHECK("tq_values_dequant_kernel");
+  return ANNA_MI_OK;
+}

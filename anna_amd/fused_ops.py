@@ -25,6 +25,21 @@ SCHEMAS = {
         "xpu_int4_gemv(Tensor hidden_states, Tensor qweight, Tensor qscale, Tensor qzeros, "
         "int group_size, int in_features) -> Tensor"
     ),
+    "gqa_decode_splitkv_fused": (
+        "gqa_decode_splitkv_fused(Tensor query, Tensor key, Tensor value, float scaling, int block_size, "
+        "Tensor? gate=None) -> Tensor"
+    ),
+    "gqa_decode_splitkv_fused_out": (
+        "gqa_decode_splitkv_fused_out(Tensor query, Tensor key, Tensor value, Tensor(a!) output, "
+        "Tensor(b!) partial_stats, Tensor(c!) partial_values, float scaling, int block_size, "
+        "Tensor? gate=None) -> Tensor(a!)"
+    ),
+    "gqa_decode_splitkv_turboquant_fused_out": (
+        "gqa_decode_splitkv_turboquant_fused_out(Tensor query, Tensor quantized_key, Tensor value_data, "
+        "Tensor value_scales, Tensor value_zeros, Tensor residual_key, Tensor residual_value, Tensor(a!) output, "
+        "Tensor(b!) partial_stats, Tensor(c!) partial_values, float scaling, int value_bits, int value_group_size, "
+        "int block_size, Tensor? gate=None) -> Tensor(a!)"
+    ),
 }
 
 
@@ -154,10 +169,280 @@ def autoround_to_int4(gptq_qweight, gptq_qzeros, scales, *, in_features, out_fea
     return qweight, qscale, qzeros
 
 
+# ---------------------------------------------------------------- split-KV decode
+
+KEYS_DENSE, KEYS_TQ_MSE = 0, 1
+VALUES_DENSE, VALUES_MINMAX, VALUES_TQ_MSE = 0, 1, 2
+GATE_NONE, GATE_FLAT, GATE_HEADS = 0, 1, 2
+
+
+def _gate_view(gate, num_heads, head_dim):
+    """Accepts the reference's two gate layouts (prepare_gqa_decode_gate, sycl:1631-1669):
+    flat [B, 1, Hq*D] or query-aligned [B, Hq, 1, D]."""
+    if gate is None:
+        return GATE_NONE, _lib.view(None)
+    if gate.dim() == 3 and gate.size(1) == 1 and gate.size(2) == num_heads * head_dim:
+        return GATE_FLAT, _lib.view(gate, (0, 1, 2, -1))
+    if gate.dim() == 4 and gate.size(1) == num_heads and gate.size(2) == 1 and gate.size(3) == head_dim:
+        return GATE_HEADS, _lib.view(gate)
+    raise RuntimeError("gate must be [batch, 1, heads * head_dim] or [batch, heads, 1, head_dim]")
+
+
+def _splitkv_num_blocks(key_len: int, block_size: int) -> int:
+    eb = min(max(int(block_size), 16), int(key_len))
+    return (int(key_len) + eb - 1) // eb
+
+
+def decode_args(*, query, len1, key=None, key_format=KEYS_DENSE, key_norms=None, key_bits=0,
+                value=None, value_format=VALUES_DENSE, value_scales=None, value_zeros=None, value_bits=0,
+                value_group_size=1, rotation=None, rotation_t=None, key_centroids=None, value_centroids=None,
+                query_rot=None, residual_key=None, residual_value=None, scaling, block_size, gate=None, output,
+                partial_stats, partial_values):
+    """Fills anna_mi_decode_args from tensors (query/out [B, Hq, 1, D], K/V [B, Hkv, L, ...])."""
+    b, hq, _, d = query.shape
+    hkv = (key if key is not None else residual_key).size(1)
+    len2 = 0 if residual_key is None else residual_key.size(2)
+    gl, gv = _gate_view(gate, hq, d)
+    a = _lib.DecodeArgs()
+    a.dtype = _lib.dtype_code(query.dtype)
+    a.batch, a.q_heads, a.kv_heads, a.head_dim = b, hq, hkv, d
+    a.query = _lib.view(query)
+    a.len1 = int(len1)
+    a.key_format = key_format
+    a.key = _lib.view(key)
+    a.key_norms = _lib.view(key_norms, (0, 1, 2)) if key_norms is not None else _lib.view(None)
+    a.key_bits = key_bits
+    a.value_format = value_format
+    a.value = _lib.view(value)
+    if value_format == VALUES_TQ_MSE:
+        a.value_scales = _lib.view(value_scales, (0, 1, 2))
+    else:
+        a.value_scales = _lib.view(value_scales)
+    a.value_zeros = _lib.view(value_zeros)
+    a.value_bits = value_bits
+    a.value_group_size = int(value_group_size)
+    a.rotation = _lib.ptr(rotation)
+    a.rotation_t = _lib.ptr(rotation_t)
+    a.key_centroids = _lib.ptr(key_centroids)
+    a.value_centroids = _lib.ptr(value_centroids)
+    a.query_rot = _lib.ptr(query_rot)
+    a.len2 = len2
+    a.residual_key = _lib.view(residual_key)
+    a.residual_value = _lib.view(residual_value)
+    a.scaling = float(scaling)
+    a.block_size = int(block_size)
+    a.gate_layout = gl
+    a.gate = gv
+    a.out = _lib.view(output)
+    a.partial_stats = _lib.view(partial_stats)
+    a.partial_values = _lib.view(partial_values)
+    a.partial_capacity = min(partial_stats.size(2), partial_values.size(2))
+    return a
+
+
+def decode_num_blocks(args) -> int:
+    return int(_lib.load().anna_mi_decode_num_blocks(args))
+
+
+def run_decode(args, stream_tensor) -> None:
+    import ctypes
+
+    _lib.call("anna_mi_gqa_decode_splitkv", ctypes.byref(args), _lib.stream_of(stream_tensor))
+
+
+def _check_decode_common(query, key, value, block_size, name):
+    if query.dim() != 4 or key.dim() != 4 or value.dim() != 4:
+        raise RuntimeError("query must be [batch, heads, 1, head_dim]; key/value must be [batch, kv_heads, key_len, head_dim]")
+    if query.size(2) != 1:
+        raise RuntimeError(f"{name} only supports single-token query")
+    if query.size(0) != key.size(0):
+        raise RuntimeError("query/key batch size mismatch")
+    if key.shape != value.shape:
+        raise RuntimeError("key and value must share the same shape")
+    if query.size(3) != key.size(3):
+        raise RuntimeError("query/key head_dim mismatch")
+    if query.size(1) % key.size(1) != 0:
+        raise RuntimeError("query heads must be divisible by kv_heads")
+    if key.size(2) < 1:
+        raise RuntimeError("key_len must be positive")
+    if block_size < 16:
+        raise RuntimeError(f"{name} block_size must be at least 16")
+    if not (query.dtype == key.dtype == value.dtype):
+        raise RuntimeError("query, key, and value must share the same dtype")
+
+
+def _check_workspace(query, key_len, block_size, output, partial_stats, partial_values, name):
+    nblk = _splitkv_num_blocks(key_len, block_size)
+    b, h, _, d = query.shape
+    if output.shape != query.shape or output.dtype != query.dtype:
+        raise RuntimeError(f"{name} output must match query shape and dtype")
+    if partial_stats.dtype != torch.float32 or partial_values.dtype != torch.float32:
+        raise RuntimeError(f"{name} partial_stats/partial_values must be float32")
+    if (partial_stats.dim() != 4 or partial_stats.size(0) != b or partial_stats.size(1) != h
+            or partial_stats.size(2) < nblk or partial_stats.size(3) != 2):
+        raise RuntimeError(f"{name} partial_stats shape/capacity mismatch")
+    if (partial_values.dim() != 4 or partial_values.size(0) != b or partial_values.size(1) != h
+            or partial_values.size(2) < nblk or partial_values.size(3) != d):
+        raise RuntimeError(f"{name} partial_values shape/capacity mismatch")
+
+
+def _gqa_decode_splitkv_fused_out_impl(query, key, value, output, partial_stats, partial_values, scaling,
+                                       block_size, gate=None):
+    name = "gqa_decode_splitkv_fused_out"
+    _check_decode_common(query, key, value, block_size, name)
+    _check_workspace(query, key.size(2), block_size, output, partial_stats, partial_values, name)
+    _lib.require_device(query, key, value, output, partial_stats, partial_values, gate)
+    a = decode_args(query=query, len1=key.size(2), key=key, value=value, scaling=scaling, block_size=block_size,
+                    gate=gate, output=output, partial_stats=partial_stats, partial_values=partial_values)
+    run_decode(a, query)
+    return output
+
+
+def _gqa_decode_splitkv_fused_impl(query, key, value, scaling, block_size, gate=None):
+    nblk = _splitkv_num_blocks(key.size(2), block_size)
+    b, h, _, d = query.shape
+    out = torch.empty_like(query)
+    ps = torch.empty((b, h, nblk, 2), dtype=torch.float32, device=query.device)
+    pv = torch.empty((b, h, nblk, d), dtype=torch.float32, device=query.device)
+    return _gqa_decode_splitkv_fused_out_impl(query, key, value, out, ps, pv, scaling, block_size, gate)
+
+
+def _gqa_decode_splitkv_turboquant_fused_out_impl(query, quantized_key, value_data, value_scales, value_zeros,
+                                                  residual_key, residual_value, output, partial_stats,
+                                                  partial_values, scaling, value_bits, value_group_size,
+                                                  block_size, gate=None):
+    # checks of validate_gqa_decode_splitkv_turboquant_inputs (sycl:1412-1500)
+    name = "gqa_decode_splitkv_turboquant_fused_out"
+    for t, what in ((query, "query"), (quantized_key, "quantized_key"), (value_data, "value_data"),
+                    (value_scales, "value_scales"), (value_zeros, "value_zeros"), (residual_key, "residual_key"),
+                    (residual_value, "residual_value")):
+        if t.dim() != 4:
+            raise RuntimeError(f"{what} must be 4-D")
+    if query.size(2) != 1:
+        raise RuntimeError("gqa_decode_splitkv_turboquant_fused only supports single-token query")
+    if residual_key.shape != residual_value.shape:
+        raise RuntimeError("residual_key and residual_value must share the same shape")
+    if quantized_key.size(1) != residual_key.size(1):
+        raise RuntimeError("quantized and residual KV head count mismatch")
+    if query.size(1) % quantized_key.size(1) != 0:
+        raise RuntimeError("query heads must be divisible by kv_heads")
+    if quantized_key.size(2) < 1:
+        raise RuntimeError("gqa_decode_splitkv_turboquant_fused requires a non-empty quantized prefix")
+    if value_bits not in (2, 3, 4):
+        raise RuntimeError("TurboQuant value_bits must be 2, 3, or 4")
+    d = query.size(3)
+    if value_group_size <= 0 or d % value_group_size != 0:
+        raise RuntimeError("TurboQuant value_group_size must evenly divide head_dim")
+    if value_scales.size(3) * value_group_size != d:
+        raise RuntimeError("TurboQuant value group count/head_dim mismatch")
+    per = 4 if value_bits == 2 else 2
+    if value_data.size(3) * per < d:
+        raise RuntimeError("TurboQuant packed value width is smaller than head_dim")
+    if value_data.dtype != torch.uint8:
+        raise RuntimeError("TurboQuant value_data must be uint8")
+    if block_size < 16:
+        raise RuntimeError("gqa_decode_splitkv_turboquant_fused block_size must be at least 16")
+    if not (query.dtype == quantized_key.dtype == residual_key.dtype == residual_value.dtype
+            == value_scales.dtype == value_zeros.dtype):
+        raise RuntimeError("query, keys, residual values, value_scales, and value_zeros must share the same dtype")
+    key_len = quantized_key.size(2) + residual_key.size(2)
+    _check_workspace(query, key_len, block_size, output, partial_stats, partial_values, name)
+    _lib.require_device(query, quantized_key, value_data, value_scales, value_zeros, residual_key, residual_value,
+                        output, partial_stats, partial_values, gate)
+    a = decode_args(query=query, len1=quantized_key.size(2), key=quantized_key, value=value_data,
+                    value_format=VALUES_MINMAX, value_scales=value_scales, value_zeros=value_zeros,
+                    value_bits=value_bits, value_group_size=value_group_size,
+                    residual_key=residual_key if residual_key.size(2) > 0 else None,
+                    residual_value=residual_value if residual_key.size(2) > 0 else None,
+                    scaling=scaling, block_size=block_size, gate=gate, output=output,
+                    partial_stats=partial_stats, partial_values=partial_values)
+    run_decode(a, query)
+    return output
+
+
+def _meta_out(query, *args, **kwargs):
+    return args[2] if len(args) > 2 else query.new_empty(query.shape)
+
+
+# ---------------------------------------------------------------- TurboQuant packing
+
+
+def tq_rotation(head_dim: int, seed: int = 42) -> torch.Tensor:
+    """Seeded Haar rotation R (fp32 [D, D], host), generated by the native library."""
+    out = torch.empty((head_dim, head_dim), dtype=torch.float32)
+    _lib.call("anna_mi_tq_rotation", head_dim, seed, out.data_ptr())
+    return out
+
+
+def tq_codebook(bits: int, head_dim: int) -> tuple[torch.Tensor, torch.Tensor]:
+    c = torch.empty(1 << bits, dtype=torch.float32)
+    t = torch.empty((1 << bits) - 1, dtype=torch.float32)
+    _lib.call("anna_mi_tq_codebook", bits, head_dim, c.data_ptr(), t.data_ptr())
+    return c, t
+
+
+def tq_mse_quantize(x2d, rotation_t, thresholds, bits):
+    """x [nvec, D] -> (codes uint8 [nvec, D*sb/8], norms fp16 [nvec])."""
+    _lib.require_device(x2d, rotation_t, thresholds)
+    nvec, d = x2d.shape
+    if x2d.stride(1) != 1:
+        x2d = x2d.contiguous()
+    sb = 2 if bits == 2 else 4
+    codes = torch.empty((nvec, d * sb // 8), dtype=torch.uint8, device=x2d.device)
+    norms = torch.empty((nvec,), dtype=torch.float16, device=x2d.device)
+    _lib.call("anna_mi_tq_mse_quantize", x2d.data_ptr(), _lib.dtype_code(x2d.dtype), nvec, d, x2d.stride(0),
+              rotation_t.data_ptr(), thresholds.data_ptr(), bits, codes.data_ptr(), norms.data_ptr(),
+              _lib.stream_of(x2d))
+    return codes, norms
+
+
+def tq_mse_dequant(codes, norms, rotation, centroids, bits, out_dtype=torch.bfloat16):
+    _lib.require_device(codes, norms, rotation, centroids)
+    nvec = codes.size(0)
+    d = rotation.size(0)
+    out = torch.empty((nvec, d), dtype=out_dtype, device=codes.device)
+    _lib.call("anna_mi_tq_mse_dequant", codes.data_ptr(), norms.data_ptr(), nvec, d, rotation.data_ptr(),
+              centroids.data_ptr(), bits, out.data_ptr(), _lib.dtype_code(out_dtype), d, _lib.stream_of(codes))
+    return out
+
+
+def tq_values_quantize(values, bits, group_size):
+    """values [H, T, D] (last dim contiguous) -> (data uint8 [H,T,P], scales, zeros [H,T,D/group])."""
+    _lib.require_device(values)
+    h, t, d = values.shape
+    if values.stride(2) != 1:
+        values = values.contiguous()
+    sb = 2 if bits == 2 else 4
+    data = torch.empty((h, t, d * sb // 8), dtype=torch.uint8, device=values.device)
+    scales = torch.empty((h, t, d // group_size), dtype=values.dtype, device=values.device)
+    zeros = torch.empty_like(scales)
+    _lib.call("anna_mi_tq_values_quantize", values.data_ptr(), _lib.dtype_code(values.dtype), h, t, d,
+              values.stride(0), values.stride(1), bits, group_size, data.data_ptr(), scales.data_ptr(),
+              zeros.data_ptr(), _lib.stream_of(values))
+    return data, scales, zeros
+
+
+def tq_values_dequant(data, scales, zeros, bits, group_size, out_dtype):
+    _lib.require_device(data, scales, zeros)
+    d = scales.size(-1) * group_size
+    rows = data.numel() // data.size(-1)
+    out = torch.empty((*data.shape[:-1], d), dtype=out_dtype, device=data.device)
+    _lib.call("anna_mi_tq_values_dequant", data.data_ptr(), scales.data_ptr(), zeros.data_ptr(),
+              _lib.dtype_code(scales.dtype), rows, d, bits, group_size, out.data_ptr(), _lib.dtype_code(out_dtype),
+              _lib.stream_of(data))
+    return out
+
+
 # ---------------------------------------------------------------- registration
 
 _IMPLS = {
     "xpu_int4_gemv": (_xpu_int4_gemv_impl, _xpu_int4_gemv_meta),
+    "gqa_decode_splitkv_fused": (_gqa_decode_splitkv_fused_impl, lambda q, *a, **k: q.new_empty(q.shape)),
+    "gqa_decode_splitkv_fused_out": (_gqa_decode_splitkv_fused_out_impl, lambda q, k, v, out, *a, **kw: out),
+    "gqa_decode_splitkv_turboquant_fused_out": (
+        _gqa_decode_splitkv_turboquant_fused_out_impl,
+        lambda q, qk, vd, vs, vz, rk, rv, out, *a, **kw: out,
+    ),
 }
 
 
@@ -193,3 +478,27 @@ def _op(name: str):
 
 def run_xpu_int4_gemv(*, hidden_states, qweight, qscale, qzeros, group_size, in_features):
     return _op("xpu_int4_gemv")(hidden_states, qweight, qscale, qzeros, int(group_size), int(in_features))
+
+
+def run_gqa_decode_splitkv_fused(*, query, key, value, scaling, block_size, gate=None):
+    op = _op("gqa_decode_splitkv_fused")
+    if gate is None:
+        return op(query, key, value, float(scaling), int(block_size))
+    return op(query, key, value, float(scaling), int(block_size), gate)
+
+
+def run_gqa_decode_splitkv_fused_out(*, query, key, value, output, partial_stats, partial_values, scaling,
+                                     block_size, gate=None):
+    op = _op("gqa_decode_splitkv_fused_out")
+    if gate is None:
+        return op(query, key, value, output, partial_stats, partial_values, float(scaling), int(block_size))
+    return op(query, key, value, output, partial_stats, partial_values, float(scaling), int(block_size), gate)
+
+
+def run_gqa_decode_splitkv_turboquant_fused_out(*, query, quantized_key, value_data, value_scales, value_zeros,
+                                                residual_key, residual_value, output, partial_stats, partial_values,
+                                                scaling, value_bits, value_group_size, block_size, gate=None):
+    op = _op("gqa_decode_splitkv_turboquant_fused_out")
+    args = (query, quantized_key, value_data, value_scales, value_zeros, residual_key, residual_value, output,
+            partial_stats, partial_values, float(scaling), int(value_bits), int(value_group_size), int(block_size))
+    return op(*args) if gate is None else op(*args, gate)

@@ -82,6 +82,116 @@ int anna_mi_autoround_to_int4(const int32_t* gptq_qweight, const int32_t* gptq_q
                               int64_t G, int64_t Kp, int32_t* qweight, float* qscale,
                               int8_t* qzeros, void* stream);
 
+
+/* ------------------------------------------------------------------ TurboQuant
+ * Value format (reference quantize_turboquant_values, src/anna/model/turboquant.py:157-252):
+ *   data uint8 [rows, D*sb/8] (sb = 2 for 2-bit, 4 for 3/4-bit; element i at bits
+ *   sb*(i % (8/sb)) of byte i/(8/sb)), scales/zeros [rows, D/group] in the value dtype.
+ * TQ-MSE format (this build's definition of the third-party TurboQuantMSE the reference
+ *   calls at turboquant.py:75-82; the package is absent): y = R x, code_i = #{j : y_i >=
+ *   thr_j * |x|}, norm |x| as fp16 bits, codes packed like the values; reconstruction
+ *   |x| * R^T c[code]. */
+
+/* Seeded Haar rotation R (fp32 [D, D] row-major, host memory, y = R x).  Replaces
+ * TurboQuantMSE(dim, bits, seed=42)'s rotation (turboquant.py:80). */
+int anna_mi_tq_rotation(int64_t D, uint64_t seed, float* out_host);
+
+/* Codebook of the MSE quantizer: 2^bits ascending centroids (Gaussian Lloyd-Max levels
+ * scaled by 1/sqrt(D); the 2-bit pair is fp16-structured, see turboquant.hip) and the
+ * 2^bits - 1 midpoint thresholds, host memory. */
+int anna_mi_tq_codebook(int bits, int64_t D, float* centroids_host, float* thresholds_host);
+
+/* MSE quantizer (the quantize step of TurboQuantTensorRow.append, turboquant.py:382-394):
+ * x [nvec, D] (row stride x_row_stride) -> codes uint8 [nvec, D*sb/8], norms fp16 bits
+ * [nvec].  rot_t = R^T (fp32 [D, D], device), thresholds fp32 (device). */
+int anna_mi_tq_mse_quantize(const void* x, int x_dtype, int64_t nvec, int64_t D, int64_t x_row_stride,
+                            const float* rot_t, const float* thresholds, int bits, uint8_t* codes,
+                            uint16_t* norms, void* stream);
+
+/* MSE reconstruction (TurboQuantTensorRow.materialize, turboquant.py:401-431):
+ * out [nvec, D] (row stride out_row_stride, out_dtype) = norm * R^T c[codes].  rot = R. */
+int anna_mi_tq_mse_dequant(const uint8_t* codes, const uint16_t* norms, int64_t nvec, int64_t D,
+                           const float* rot, const float* centroids, int bits, void* out, int out_dtype,
+                           int64_t out_row_stride, void* stream);
+
+/* quantize_turboquant_values + _pack_value_data (turboquant.py:164-175, 199-230):
+ * values [H, T, D] with strides (stride_h, stride_t, 1) -> data/scales/zeros (contiguous). */
+int anna_mi_tq_values_quantize(const void* values, int dtype, int64_t H, int64_t T, int64_t D,
+                               int64_t stride_h, int64_t stride_t, int bits, int64_t group_size,
+                               uint8_t* data, void* scales, void* zeros, void* stream);
+
+/* dequantize_turboquant_values (turboquant.py:233-252): out [rows, D] = q * scale + zero. */
+int anna_mi_tq_values_dequant(const uint8_t* data, const void* scales, const void* zeros, int dtype,
+                              int64_t rows, int64_t D, int bits, int64_t group_size, void* out,
+                              int out_dtype, void* stream);
+
+/* ------------------------------------------------------------------ split-KV GQA decode */
+
+/* A strided view; strides in elements. */
+typedef struct {
+  const void* ptr;
+  int64_t s0, s1, s2, s3;
+} anna_mi_view;
+
+#define ANNA_MI_KEYS_DENSE 0
+#define ANNA_MI_KEYS_TQ_MSE 1
+#define ANNA_MI_VALUES_DENSE 0
+#define ANNA_MI_VALUES_MINMAX 1
+#define ANNA_MI_VALUES_TQ_MSE 2
+#define ANNA_MI_GATE_NONE 0
+#define ANNA_MI_GATE_FLAT 1  /* [B, 1, Hq*D]: s0 batch, s2 inner */
+#define ANNA_MI_GATE_HEADS 2 /* [B, Hq, 1, D]: s0, s1, s3 */
+
+typedef struct {
+  int dtype; /* query, dense keys/values, value scales/zeros, residual, gate, output */
+  int64_t batch, q_heads, kv_heads, head_dim;
+  anna_mi_view query; /* [B, Hq, 1, D] */
+  /* main segment of `len1` tokens (the quantized prefix, or every token) */
+  int64_t len1;
+  int key_format;          /* ANNA_MI_KEYS_* */
+  anna_mi_view key;        /* dense [B, Hkv, len1, D] | MSE codes uint8 [B, Hkv, len1, bytes] */
+  anna_mi_view key_norms;  /* MSE: fp16 bits [B, Hkv, len1] (s0, s1, s2) */
+  int key_bits;
+  int value_format;        /* ANNA_MI_VALUES_* */
+  anna_mi_view value;      /* dense [B, Hkv, len1, D] | packed uint8 [B, Hkv, len1, bytes] */
+  anna_mi_view value_scales; /* MINMAX: [B, Hkv, len1, groups]; MSE: norms fp16 bits [B, Hkv, len1] */
+  anna_mi_view value_zeros;  /* MINMAX: [B, Hkv, len1, groups] */
+  int value_bits;
+  int64_t value_group_size;
+  const float* rotation;   /* MSE formats: R and R^T (fp32 [D, D]) and the centroids */
+  const float* rotation_t;
+  const float* key_centroids;
+  const float* value_centroids;
+  float* query_rot;        /* MSE keys: workspace fp32 [B, Hq, D] */
+  /* residual segment of `len2` dense tokens (may be 0) */
+  int64_t len2;
+  anna_mi_view residual_key, residual_value; /* [B, Hkv, len2, D] */
+  float scaling;
+  int64_t block_size;
+  int gate_layout;         /* ANNA_MI_GATE_* */
+  anna_mi_view gate;
+  anna_mi_view out;        /* [B, Hq, 1, D] */
+  anna_mi_view partial_stats;  /* fp32 [B, Hq, capacity, 2] */
+  anna_mi_view partial_values; /* fp32 [B, Hq, capacity, D] */
+  int64_t partial_capacity;
+} anna_mi_decode_args;
+
+/* sizeof(anna_mi_decode_args), so that bindings can check their struct layout. */
+int64_t anna_mi_sizeof_decode_args(void);
+
+/* Number of split blocks a call uses (the workspace must hold at least this many):
+ * ceil(L / eb) with eb = min(max(block_size, 16), L) as in the reference
+ * (sycl:1521-1556); with TQ-MSE keys or values the two segments are split separately. */
+int64_t anna_mi_decode_num_blocks(const anna_mi_decode_args* args);
+
+/* Single-token GQA decode over [main segment ++ residual], flash-decoding in two kernels
+ * (per-block online softmax partials, then log-sum-exp merge, optional sigmoid gate).
+ * With dense values and keys this is gqa_decode_splitkv_fused_out (schema sycl:7640-7651,
+ * launch sycl:4494-4706); with min/max-packed values it is
+ * gqa_decode_splitkv_turboquant_fused_out (schema sycl:7652-7668, launch sycl:4771-5094).
+ * All q-heads of a KV group share one workgroup and one read of each K/V token. */
+int anna_mi_gqa_decode_splitkv(const anna_mi_decode_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

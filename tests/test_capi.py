@@ -29,7 +29,13 @@ def test_every_declared_symbol_has_a_binding():
     for name in declared_symbols():
         if name in ("anna_mi_last_error", "anna_mi_abi_version"):
             continue
-        assert name in _lib.PROTOTYPES, f"{name} has no ctypes prototype"
+        assert name in _lib.PROTOTYPES or name in _lib.RAW_PROTOTYPES, f"{name} has no ctypes prototype"
+
+
+def test_decode_args_binding_matches_the_c_struct():
+    import ctypes
+
+    assert _lib.load().anna_mi_sizeof_decode_args() == ctypes.sizeof(_lib.DecodeArgs)
 
 
 def test_abi_version_matches_header():
