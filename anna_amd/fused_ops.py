@@ -398,6 +398,7 @@ def tq_mse_quantize(x2d, rotation_t, thresholds, bits):
 
 def tq_mse_dequant(codes, norms, rotation, centroids, bits, out_dtype=torch.bfloat16):
     _lib.require_device(codes, norms, rotation, centroids)
+    codes, norms = codes.contiguous(), norms.contiguous()
     nvec = codes.size(0)
     d = rotation.size(0)
     out = torch.empty((nvec, d), dtype=out_dtype, device=codes.device)
@@ -424,6 +425,7 @@ def tq_values_quantize(values, bits, group_size):
 
 def tq_values_dequant(data, scales, zeros, bits, group_size, out_dtype):
     _lib.require_device(data, scales, zeros)
+    data, scales, zeros = data.contiguous(), scales.contiguous(), zeros.contiguous()
     d = scales.size(-1) * group_size
     rows = data.numel() // data.size(-1)
     out = torch.empty((*data.shape[:-1], d), dtype=out_dtype, device=data.device)
