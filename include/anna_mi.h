@@ -192,6 +192,57 @@ int64_t anna_mi_decode_num_blocks(const anna_mi_decode_args* args);
  * All q-heads of a KV group share one workgroup and one read of each K/V token. */
 int anna_mi_gqa_decode_splitkv(const anna_mi_decode_args* args, void* stream);
 
+/* ------------------------------------------------------------------ batched TQ decode
+ * Batched, variable-length single-token GQA decode over a 2-bit TQ-MSE K/V cache
+ * (head_dim 256): the batched replacement of the per-row loop of
+ * Qwen3DynamicCache.turboquant_single_token_decode_attention (src/anna/model/ops.py:1024-1072)
+ * over TurboQuantKVRow.decode_attention (turboquant.py:1181-1346).  Layout of the cache:
+ * see tq_decode.hip.  Work items (b, kv_head, t0, t1) come from anna_mi_tq_decode_plan;
+ * a residual item has t0 = t1 = -1. */
+typedef struct {
+  int64_t batch, q_heads, kv_heads, head_dim;
+  int key_bits, value_bits;
+  const uint16_t* query;            /* bf16 [B][Hq][D] */
+  const uint8_t* key_codes;         /* [Hkv][pool][D/4] */
+  const uint16_t* key_norms;        /* fp16 [Hkv][pool] */
+  const uint8_t* value_codes;       /* [Hkv][pool/32][32*D/4] blocked */
+  const uint16_t* value_norms;      /* fp16 [Hkv][pool] */
+  int64_t pool_tokens;
+  const int64_t* seq_offsets;       /* [B] device, multiples of 32 */
+  const uint16_t* residual_key;     /* bf16 [B][Hkv][R][D] */
+  const uint16_t* residual_value_t; /* bf16 [B][Hkv][D][R] */
+  const int32_t* residual_lens;     /* [B] device */
+  int64_t residual_capacity;        /* R, multiple of 32 */
+  const uint16_t* rotation_f16;     /* R as fp16 [D][D] */
+  const uint16_t* rotation_t_f16;   /* R^T as fp16 [D][D] */
+  float key_scale, value_scale;     /* centroid c = key_scale * fp16 LUT value */
+  float scaling;
+  const int32_t* items;             /* [num_items][4] device */
+  int64_t num_items;
+  const int32_t* item_ranges;       /* [B*Hkv + 1] device */
+  uint16_t* query_rot;              /* workspace fp16 [B][Hq][D] */
+  float* partial_stats;             /* workspace [num_items][16][2] */
+  float* partial_values;            /* workspace [num_items][16][D] */
+  uint16_t* out;                    /* bf16 [B][Hq][D] */
+} anna_mi_tq_decode_args;
+
+/* Host: split each sequence's quantized prefix into items of tokens_per_item tokens (a
+ * multiple of 32), one residual item per (b, kv_head) with a residual, ordered by
+ * (b, kv_head); item_ranges[b*Hkv + h] .. [+1] delimit the items of (b, h). */
+int anna_mi_tq_decode_plan(int64_t batch, int64_t kv_heads, const int64_t* quantized_lens_host,
+                           const int64_t* residual_lens_host, int64_t tokens_per_item, int32_t* items_host,
+                           int64_t items_capacity, int32_t* item_ranges_host, int64_t* num_items);
+
+/* sizeof(anna_mi_tq_decode_args), for binding checks. */
+int64_t anna_mi_sizeof_tq_decode_args(void);
+
+/* Three launches: q' = R q, split (per item), merge (per b, kv_head). */
+int anna_mi_tq_decode(const anna_mi_tq_decode_args* args, void* stream);
+
+/* Reorders natural 2-bit codes [tokens][64] (D = 256) of one KV head into the blocked
+ * value layout [tokens/32][2048] read by anna_mi_tq_decode.  Pure permutation. */
+int anna_mi_tq_block_values(const uint8_t* codes, int64_t tokens, uint8_t* blocked, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

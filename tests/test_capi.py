@@ -36,6 +36,7 @@ def test_decode_args_binding_matches_the_c_struct():
     import ctypes
 
     assert _lib.load().anna_mi_sizeof_decode_args() == ctypes.sizeof(_lib.DecodeArgs)
+    assert _lib.load().anna_mi_sizeof_tq_decode_args() == ctypes.sizeof(_lib.TQDecodeArgs)
 
 
 def test_abi_version_matches_header():
