@@ -63,7 +63,7 @@ class TQDecodeArgs(ctypes.Structure):
         ("residual_value_t", _P), ("residual_lens", _P), ("residual_capacity", _I64), ("rotation_f16", _P),
         ("rotation_t_f16", _P), ("key_scale", _F), ("value_scale", _F), ("scaling", _F), ("items", _P),
         ("num_items", _I64), ("item_ranges", _P), ("query_rot", _P), ("partial_stats", _P),
-        ("partial_values", _P), ("out", _P),
+        ("partial_values", _P), ("out_residual", _P), ("out", _P),
     ]
 
 

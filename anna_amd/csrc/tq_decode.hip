@@ -10,18 +10,20 @@
 //   residual_key     bf16 [B][Hkv][R][256]  newest tokens, dense, token-major
 //   residual_value_t bf16 [B][Hkv][256][R]  dense, dim-major
 //
-// Kernels (one call = three launches):
+// Kernels (one call = four launches):
 //   tq_rotate_query  q' = R q (MFMA, fp16 in / fp32 accumulate) for every (b, q-head).
 //   tq_decode_split  one workgroup per work item (b, kv-head, <= tokens_per_item tokens or the
-//     residual window).  4 waves take 32-token blocks.  Scores are formed transposed,
+//     residual window).  8 waves take 32-token blocks (next block prefetched).  Scores are formed transposed,
 //     S^T = Khat Q'^T, by v_mfma_f32_16x16x32_f16 on codes turned into fp16 centroids with one
 //     v_perm per pair (the 2-bit centroids are fp16 values sharing their low byte); S^T's
 //     accumulator layout is exactly the B operand of O'^T = Vhat^T P^T, so probabilities
 //     never leave registers.  Online softmax in base 2 with lazy rescaling (the running max
 //     only moves when a block exceeds it by 2^4).  Output: per item and q-head
 //     (max, denominator) and the unnormalized accumulator (rotated space for packed items).
-//   tq_decode_merge  per (b, kv-head): log-sum-exp merge of the items, un-rotation of the
-//     packed part (Y = A R, MFMA), plus the residual part, bf16 output.
+//   tq_decode_combine  per (b, q-head): log-sum-exp weights of the items, weighted sums of the
+//     packed (rotated) and residual partial accumulators.
+//   tq_decode_unrotate  out = (rotated sum) R + (residual sum), a [B*Hq x 256] x [256 x 256]
+//     MFMA product, bf16 output.
 #include <vector>
 
 #include "common.hpp"
@@ -31,7 +33,6 @@ namespace {
 
 constexpr int TD = 256;              // head_dim
 constexpr int TBT = 32;              // tokens per block
-constexpr int TWAVES = 4;
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LAZY = 4.0f;         // rescale threshold (log2 units)
 constexpr float P_SCALE = 1.0f / 64.0f;  // keeps p * norm inside fp16 range; divided out at the end
@@ -71,46 +72,71 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 
 // ------------------------------------------------------------------ q' = R q
 
-// grid (B * Hkv), 256 threads.  Q [16 heads x 256] (bf16 -> fp16) times R^T -> fp16 q'.
-__global__ __launch_bounds__(256) void tq_rotate_query_kernel(const anna_mi_tq_decode_args a) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// grid (B * Hkv, 16 output tiles), one wave.  Q [16 heads x 256] (bf16 -> fp16) times R^T.
+__global__ __launch_bounds__(64) void tq_rotate_query_kernel(const anna_mi_tq_decode_args a) {
+  const int lane = threadIdx.x;
   const int r = lane & 15, kq = lane >> 4;
   const int64_t bh = blockIdx.x, b = bh / a.kv_heads, h = bh % a.kv_heads;
+  const int tile = blockIdx.y;  // output dims i in [16 tile, 16 tile + 16)
   const int G = (int)(a.q_heads / a.kv_heads);
   const uint16_t* q = (const uint16_t*)a.query + (b * a.q_heads + h * G) * TD;
   const uint16_t* R = (const uint16_t*)a.rotation_f16;
-  u32x4 af[8];
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s = 0; s < 8; ++s) {
     u32x4 v = {0u, 0u, 0u, 0u};
     if (r < G) v = *(const u32x4*)(q + r * TD + s * 32 + kq * 8);
-    u32x4 o;
+    u32x4 af;
 #pragma unroll
     for (int w = 0; w < 4; ++w)
-      o[w] = pack_f16x2(bf16_bits_to_f32((uint16_t)(v[w] & 0xFFFFu)), bf16_bits_to_f32((uint16_t)(v[w] >> 16)));
-    af[s] = o;
+      af[w] = pack_f16x2(bf16_bits_to_f32((uint16_t)(v[w] & 0xFFFFu)), bf16_bits_to_f32((uint16_t)(v[w] >> 16)));
+    const u32x4 bfr = *(const u32x4*)(R + (int64_t)(tile * 16 + r) * TD + s * 32 + kq * 8);
+    acc = mfma_f16(af, bfr, acc);
   }
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) {
-    const int tile = wave * 4 + tt;  // output dims i in [16 tile, 16 tile + 16)
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const u32x4 bfr = *(const u32x4*)(R + (int64_t)(tile * 16 + r) * TD + s * 32 + kq * 8);
-      acc = mfma_f16(af[s], bfr, acc);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int n = 4 * kq + i;
-      if (n < G) ((uint16_t*)a.query_rot)[(b * a.q_heads + h * G + n) * TD + tile * 16 + r] = f32_to_f16_bits(acc[i]);
-    }
+  for (int i = 0; i < 4; ++i) {
+    const int n = 4 * kq + i;
+    if (n < G) ((uint16_t*)a.query_rot)[(b * a.q_heads + h * G + n) * TD + tile * 16 + r] = f32_to_f16_bits(acc[i]);
   }
 }
 
 // ------------------------------------------------------------------ split
 
-__global__ __launch_bounds__(64 * TWAVES) void tq_decode_split_kernel(const anna_mi_tq_decode_args a) {
-  __shared__ float s_m[TWAVES][16], s_l[TWAVES][16];
+constexpr int SWAVES = 8;  // waves per work item
+
+struct BlockRaw {
+  u32x4 k0, k1, v0, v1;     // key codes (tokens r, 16 + r), value codes (dims 16 r .. 16 r + 15)
+  uint2 kn0, kn1, vn0, vn1;  // norms of tokens 4 kq .. 4 kq + 3 and 16 + 4 kq ..
+};
+
+__device__ __forceinline__ void load_block(const anna_mi_tq_decode_args& a, int64_t h, int64_t p0, int r, int kq,
+                                           BlockRaw& o) {
+  const int64_t T = a.pool_tokens;
+  const uint8_t* kc = a.key_codes + (h * T + p0) * 64;
+  o.k0 = __builtin_nontemporal_load((const u32x4*)(kc + r * 64 + kq * 16));
+  o.k1 = __builtin_nontemporal_load((const u32x4*)(kc + (16 + r) * 64 + kq * 16));
+  const uint8_t* vc = a.value_codes + (h * (T / TBT) + p0 / TBT) * 2048 + kq * 512 + r * 32;
+  o.v0 = __builtin_nontemporal_load((const u32x4*)(vc));
+  o.v1 = __builtin_nontemporal_load((const u32x4*)(vc + 16));
+  const uint16_t* kn = a.key_norms + h * T + p0;
+  const uint16_t* vn = a.value_norms + h * T + p0;
+  o.kn0 = *(const uint2*)(kn + 4 * kq);
+  o.kn1 = *(const uint2*)(kn + 16 + 4 * kq);
+  o.vn0 = *(const uint2*)(vn + 4 * kq);
+  o.vn1 = *(const uint2*)(vn + 16 + 4 * kq);
+}
+
+__device__ __forceinline__ float half_of(uint2 v, int i) {
+  const uint32_t w = (i >> 1) ? v.y : v.x;
+  return f16_bits_to_f32((uint16_t)(w >> (16 * (i & 1))));
+}
+
+__global__ __launch_bounds__(64 * SWAVES) __attribute__((amdgpu_waves_per_eu(2, 8)))
+void tq_decode_split_kernel(const anna_mi_tq_decode_args a) {
+  __shared__ u32x4 s_qf[8][64];  // B operand of S^T = Khat Q'^T per dim-step and lane
+  __shared__ float s_m[SWAVES][16], s_l[SWAVES][16];
+  // s_acc[(i * 16 + j) * 64 + lane] holds head r, dim (4 kq + i) * 16 + j: the 64 lanes of
+  // one atomic add hit 64 consecutive words (no bank conflict).
   __shared__ float s_acc[16 * TD];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, kq = lane >> 4;
@@ -120,43 +146,47 @@ __global__ __launch_bounds__(64 * TWAVES) void tq_decode_split_kernel(const anna
   const int64_t t0 = it[2], t1 = it[3];
   const bool resid = t0 < 0;
   const int G = (int)(a.q_heads / a.kv_heads);
-  const int64_t T = a.pool_tokens;
   const int64_t Rc = a.residual_capacity;
   const int64_t tb0 = resid ? 0 : t0;
   const int64_t tend = resid ? (int64_t)a.residual_lens[b] : t1;
   const int64_t nblk = (tend - tb0 + TBT - 1) / TBT;
 
   for (int i = threadIdx.x; i < 16 * TD; i += blockDim.x) s_acc[i] = 0.f;
-
-  const uint32_t lut_hi = vconst(0x433CBCC3u), lut_lo = vconst(0x7E7E7E7Eu), or_c = vconst(0x04000400u);
-
-  // B operand of S^T = Khat Q'^T for the 8 dim-steps (lane: head n = r, k-group kq).
-  u32x4 qf[8];
-  if (!resid) {
-    const uint16_t* qr = (const uint16_t*)a.query_rot + (b * a.q_heads + h * G + r) * TD;
+  const int64_t off = resid ? 0 : a.seq_offsets[b];
+  BlockRaw cur;
+  if (!resid && wave < nblk) load_block(a, h, off + tb0 + wave * TBT, r, kq, cur);  // in flight across the barrier
+  if (wave == 0) {
+    if (!resid) {
+      // q' rows in the pair order of codes_to_f16 (see the K conversion below)
+      const uint16_t* qr = (const uint16_t*)a.query_rot + (b * a.q_heads + h * G + r) * TD;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const int da = 64 * kq + 16 * (s >> 1) + 4 * (s & 1);
-      uint2 lo = {0u, 0u}, hi = {0u, 0u};
-      if (r < G) {
-        lo = *(const uint2*)(qr + da);
-        hi = *(const uint2*)(qr + da + 8);
+      for (int s = 0; s < 8; ++s) {
+        const int da = 64 * kq + 16 * (s >> 1) + 4 * (s & 1);
+        uint2 lo = {0u, 0u}, hi = {0u, 0u};
+        if (r < G) {
+          lo = *(const uint2*)(qr + da);
+          hi = *(const uint2*)(qr + da + 8);
+        }
+        u32x4 f;
+        f.x = __builtin_amdgcn_perm(hi.x, lo.x, 0x05040100u);
+        f.y = __builtin_amdgcn_perm(hi.x, lo.x, 0x07060302u);
+        f.z = __builtin_amdgcn_perm(hi.y, lo.y, 0x05040100u);
+        f.w = __builtin_amdgcn_perm(hi.y, lo.y, 0x07060302u);
+        s_qf[s][lane] = f;
       }
-      qf[s].x = __builtin_amdgcn_perm(hi.x, lo.x, 0x05040100u);
-      qf[s].y = __builtin_amdgcn_perm(hi.x, lo.x, 0x07060302u);
-      qf[s].z = __builtin_amdgcn_perm(hi.y, lo.y, 0x05040100u);
-      qf[s].w = __builtin_amdgcn_perm(hi.y, lo.y, 0x07060302u);
-    }
-  } else {
-    const uint16_t* q = (const uint16_t*)a.query + (b * a.q_heads + h * G + r) * TD;
+    } else {
+      const uint16_t* q = (const uint16_t*)a.query + (b * a.q_heads + h * G + r) * TD;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (r < G) v = *(const u32x4*)(q + s * 32 + kq * 8);
-      qf[s] = v;
+      for (int s = 0; s < 8; ++s) {
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (r < G) v = *(const u32x4*)(q + s * 32 + kq * 8);
+        s_qf[s][lane] = v;
+      }
     }
   }
+  __syncthreads();
 
+  const uint32_t lut_hi = vconst(0x433CBCC3u), lut_lo = vconst(0x7E7E7E7Eu), or_c = vconst(0x04000400u);
   const float kscale = a.key_scale * a.scaling * LOG2E;
   const float vscale = a.value_scale * P_SCALE;
   f32x4 acc[16];
@@ -164,52 +194,37 @@ __global__ __launch_bounds__(64 * TWAVES) void tq_decode_split_kernel(const anna
   for (int j = 0; j < 16; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
 
-  const int64_t off = resid ? 0 : a.seq_offsets[b];
-  for (int64_t blk = wave; blk < nblk; blk += TWAVES) {
-    const int64_t tb = tb0 + blk * TBT;  // first token of the block
-    float s[8];
-    float nv[8];
-    u32x4 vraw[2];
+  for (int64_t blk = wave; blk < nblk; blk += SWAVES) {
+    const int64_t tb = tb0 + blk * TBT;
+    if (!resid && blk != wave) load_block(a, h, off + tb, r, kq, cur);
+    float s[8], nv[8];
+    f32x4 st0 = {0.f, 0.f, 0.f, 0.f}, st1 = {0.f, 0.f, 0.f, 0.f};
     if (!resid) {
-      const int64_t p0 = off + tb;
-      const uint8_t* kc = a.key_codes + (h * T + p0) * 64;
-      const u32x4 k0 = *(const u32x4*)(kc + r * 64 + kq * 16);
-      const u32x4 k1 = *(const u32x4*)(kc + (16 + r) * 64 + kq * 16);
-      const uint16_t* kn = a.key_norms + h * T + p0;
-      const uint16_t* vn = a.value_norms + h * T + p0;
-      const uint2 kn0 = *(const uint2*)(kn + 4 * kq), kn1 = *(const uint2*)(kn + 16 + 4 * kq);
-      const uint2 vn0 = *(const uint2*)(vn + 4 * kq), vn1 = *(const uint2*)(vn + 16 + 4 * kq);
-      const uint8_t* vc = a.value_codes + (h * (T / TBT) + p0 / TBT) * 2048 + kq * 512 + r * 32;
-      vraw[0] = *(const u32x4*)(vc);
-      vraw[1] = *(const u32x4*)(vc + 16);
-      f32x4 st0 = {0.f, 0.f, 0.f, 0.f}, st1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int st = 0; st < 8; ++st) {
-        const uint32_t w0 = k0[st >> 1], w1 = k1[st >> 1];
+        const u32x4 qf = s_qf[st][lane];
+        const uint32_t w0 = cur.k0[st >> 1], w1 = cur.k1[st >> 1];
         const uint32_t x0 = (st & 1) ? w0 : (w0 << 8), x1 = (st & 1) ? w1 : (w1 << 8);
-        st0 = mfma_f16(codes_to_f16(x0, lut_hi, lut_lo, or_c), qf[st], st0);
-        st1 = mfma_f16(codes_to_f16(x1, lut_hi, lut_lo, or_c), qf[st], st1);
+        st0 = mfma_f16(codes_to_f16(x0, lut_hi, lut_lo, or_c), qf, st0);
+        st1 = mfma_f16(codes_to_f16(x1, lut_hi, lut_lo, or_c), qf, st1);
+        __builtin_amdgcn_sched_barrier(0);
       }
-      const uint32_t kw[4] = {kn0.x, kn0.y, kn1.x, kn1.y};
-      const uint32_t vw[4] = {vn0.x, vn0.y, vn1.x, vn1.y};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float nk0 = f16_bits_to_f32((uint16_t)(kw[i >> 1] >> (16 * (i & 1))));
-        const float nk1 = f16_bits_to_f32((uint16_t)(kw[2 + (i >> 1)] >> (16 * (i & 1))));
-        s[i] = st0[i] * nk0 * kscale;
-        s[4 + i] = st1[i] * nk1 * kscale;
-        nv[i] = f16_bits_to_f32((uint16_t)(vw[i >> 1] >> (16 * (i & 1)))) * vscale;
-        nv[4 + i] = f16_bits_to_f32((uint16_t)(vw[2 + (i >> 1)] >> (16 * (i & 1)))) * vscale;
+        s[i] = st0[i] * half_of(cur.kn0, i) * kscale;
+        s[4 + i] = st1[i] * half_of(cur.kn1, i) * kscale;
+        nv[i] = half_of(cur.vn0, i) * vscale;
+        nv[4 + i] = half_of(cur.vn1, i) * vscale;
       }
     } else {
       const uint16_t* rk = a.residual_key + ((b * a.kv_heads + h) * Rc + tb) * TD;
-      f32x4 st0 = {0.f, 0.f, 0.f, 0.f}, st1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int st = 0; st < 8; ++st) {
+        const u32x4 qf = s_qf[st][lane];
         const u32x4 a0 = *(const u32x4*)(rk + r * TD + st * 32 + kq * 8);
         const u32x4 a1 = *(const u32x4*)(rk + (16 + r) * TD + st * 32 + kq * 8);
-        st0 = mfma_bf16(a0, qf[st], st0);
-        st1 = mfma_bf16(a1, qf[st], st1);
+        st0 = mfma_bf16(a0, qf, st0);
+        st1 = mfma_bf16(a1, qf, st1);
       }
       const float sc = a.scaling * LOG2E;
 #pragma unroll
@@ -242,25 +257,22 @@ __global__ __launch_bounds__(64 * TWAVES) void tq_decode_split_kernel(const anna
       for (int j = 0; j < 16; ++j) acc[j] *= alpha;
       m_run = m_new;
     }
-    float p[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      p[i] = exp2f(s[i] - m_run);
-      l_run += p[i];
-    }
     u32x4 pf;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float p0 = exp2f(s[i] - m_run), p1 = exp2f(s[4 + i] - m_run);
+      l_run += p0 + p1;
+      pf[i] = resid ? pack_bf16x2(p0 * nv[i], p1 * nv[4 + i]) : pack_f16x2(p0 * nv[i], p1 * nv[4 + i]);
+    }
     if (!resid) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) pf[i] = pack_f16x2(p[i] * nv[i], p[4 + i] * nv[4 + i]);
-#pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const uint32_t w = vraw[j >> 3][(j >> 1) & 3];
+        const uint32_t w = (j >> 3) ? cur.v1[(j >> 1) & 3] : cur.v0[(j >> 1) & 3];
         const uint32_t xv = __builtin_amdgcn_perm(w, w, (j & 1) ? 0x030C020Cu : 0x010C000Cu);
         acc[j] = mfma_f16(codes_to_f16(xv, lut_hi, lut_lo, or_c), pf, acc[j]);
+        __builtin_amdgcn_sched_barrier(0);
       }
     } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) pf[i] = pack_bf16x2(p[i] * nv[i], p[4 + i] * nv[4 + i]);
       const uint16_t* rv = a.residual_value_t + (b * a.kv_heads + h) * TD * Rc + tb;
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
@@ -286,22 +298,26 @@ __global__ __launch_bounds__(64 * TWAVES) void tq_decode_split_kernel(const anna
   __syncthreads();
   float M = -INFINITY;
 #pragma unroll
-  for (int w = 0; w < TWAVES; ++w) M = fmaxf(M, s_m[w][r]);
+  for (int w = 0; w < SWAVES; ++w) M = fmaxf(M, s_m[w][r]);
   const float f = l_run > 0.f ? exp2f(m_run - M) : 0.f;
-  if (r < G) {
+  if (r < G && f != 0.f) {
 #pragma unroll
     for (int j = 0; j < 16; ++j)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) atomicAdd(&s_acc[r * TD + (4 * kq + i) * 16 + j], acc[j][i] * f);
+      for (int i = 0; i < 4; ++i) atomicAdd(&s_acc[(i * 16 + j) * 64 + lane], acc[j][i] * f);
   }
   __syncthreads();
   float* pv = a.partial_values + item * 16 * TD;
-  for (int i = threadIdx.x; i < G * TD; i += blockDim.x) pv[i] = s_acc[i] * (1.0f / P_SCALE);
+  for (int e = threadIdx.x; e < G * TD; e += blockDim.x) {
+    const int n = e / TD, d = e % TD;
+    const int ekq = d >> 6, ei = (d >> 4) & 3, ej = d & 15;
+    pv[e] = s_acc[(ei * 16 + ej) * 64 + ekq * 16 + n] * (1.0f / P_SCALE);
+  }
   if (threadIdx.x < (unsigned)G) {
     const int n = threadIdx.x;
     float Mx = -INFINITY, L = 0.f;
-    for (int w = 0; w < TWAVES; ++w) Mx = fmaxf(Mx, s_m[w][n]);
-    for (int w = 0; w < TWAVES; ++w)
+    for (int w = 0; w < SWAVES; ++w) Mx = fmaxf(Mx, s_m[w][n]);
+    for (int w = 0; w < SWAVES; ++w)
       if (s_l[w][n] > 0.f) L += s_l[w][n] * exp2f(s_m[w][n] - Mx);
     a.partial_stats[(item * 16 + n) * 2] = Mx;
     a.partial_stats[(item * 16 + n) * 2 + 1] = L;
@@ -310,76 +326,64 @@ __global__ __launch_bounds__(64 * TWAVES) void tq_decode_split_kernel(const anna
 
 // ------------------------------------------------------------------ merge
 
-// grid (B * Hkv), 256 threads.
-__global__ __launch_bounds__(256) void tq_decode_merge_kernel(const anna_mi_tq_decode_args a) {
-  __shared__ float s_w[64][16];          // per-item weight exp2(m - M) / L (<= 64 items per (b,h) cached)
-  __shared__ float s_M[16], s_L[16];
-  __shared__ __attribute__((aligned(16))) uint16_t s_rot[16 * TD];  // normalized rotated accumulators, fp16 [head][i]
-  __shared__ float s_res[16 * TD];       // normalized residual accumulators
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int r = lane & 15, kq = lane >> 4;
-  const int64_t bh = blockIdx.x, b = bh / a.kv_heads, h = bh % a.kv_heads;
+// Phase 1, grid (B * Hq), 256 threads (thread = dim): weighted sum of the items of one
+// (b, q-head); writes the normalized rotated part (fp16) and the residual part (fp32).
+__global__ __launch_bounds__(256) void tq_decode_combine_kernel(const anna_mi_tq_decode_args a) {
+  __shared__ float s_w[64];
+  const int64_t bq = blockIdx.x, b = bq / a.q_heads, hq = bq % a.q_heads;
   const int G = (int)(a.q_heads / a.kv_heads);
-  const int32_t i0 = a.item_ranges[bh], i1 = a.item_ranges[bh + 1];
-  const int nit = i1 - i0;
-  if (threadIdx.x < 16) {
-    const int n = threadIdx.x;
-    float M = -INFINITY, L = 0.f;
-    if (n < G) {
-      for (int it = i0; it < i1; ++it) M = fmaxf(M, a.partial_stats[((int64_t)it * 16 + n) * 2]);
-      for (int it = i0; it < i1; ++it) {
-        const float l = a.partial_stats[((int64_t)it * 16 + n) * 2 + 1];
-        if (l > 0.f) L += l * exp2f(a.partial_stats[((int64_t)it * 16 + n) * 2] - M);
-      }
-    }
-    s_M[n] = M;
-    s_L[n] = L;
+  const int64_t h = hq / G, n = hq % G;
+  const int32_t i0 = a.item_ranges[b * a.kv_heads + h], i1 = a.item_ranges[b * a.kv_heads + h + 1];
+  if (threadIdx.x < 64) {
+    const int it = i0 + (int)threadIdx.x;
+    const float m = it < i1 ? a.partial_stats[((int64_t)it * 16 + n) * 2] : -INFINITY;
+    const float l = it < i1 ? a.partial_stats[((int64_t)it * 16 + n) * 2 + 1] : 0.f;
+    const float M = wave_max(l > 0.f ? m : -INFINITY);
+    const float e = l > 0.f ? exp2f(m - M) : 0.f;
+    const float L = wave_sum(l * e);
+    s_w[threadIdx.x] = L > 0.f ? e / L : 0.f;
   }
   __syncthreads();
-  for (int k = threadIdx.x; k < nit * 16 && k < 64 * 16; k += blockDim.x) {
-    const int it = k / 16, n = k % 16;
-    float w = 0.f;
-    if (n < G && s_L[n] > 0.f) {
-      const float l = a.partial_stats[((int64_t)(i0 + it) * 16 + n) * 2 + 1];
-      if (l > 0.f) w = exp2f(a.partial_stats[((int64_t)(i0 + it) * 16 + n) * 2] - s_M[n]) / s_L[n];
-    }
-    s_w[it][n] = w;
-  }
-  __syncthreads();
-  // thread = dim; accumulate the weighted partials per head
   const int d = threadIdx.x;
-  for (int n = 0; n < 16; ++n) {
-    float ar = 0.f, aq = 0.f;
-    if (n < G) {
-      for (int it = i0; it < i1; ++it) {
-        const float w = (it - i0) < 64 ? s_w[it - i0][n] : 0.f;
-        if (w == 0.f) continue;
-        const float v = a.partial_values[((int64_t)it * 16 + n) * TD + d] * w;
-        if (a.items[(int64_t)it * 4 + 2] < 0) aq += v; else ar += v;
-      }
-    }
-    s_rot[n * TD + d] = f32_to_f16_bits(ar);
-    s_res[n * TD + d] = aq;
+  // the residual item, when present, is the last of the range (anna_mi_tq_decode_plan)
+  const bool has_res = i1 > i0 && a.items[(int64_t)(i1 - 1) * 4 + 2] < 0;
+  const int ip = has_res ? i1 - 1 : i1;
+  const float* pv = a.partial_values + n * TD + d;
+  float ar = 0.f, aq = 0.f;
+  int it = i0;
+  for (; it + 4 <= ip; it += 4) {
+    const float v0 = pv[(int64_t)it * 16 * TD], v1 = pv[(int64_t)(it + 1) * 16 * TD];
+    const float v2 = pv[(int64_t)(it + 2) * 16 * TD], v3 = pv[(int64_t)(it + 3) * 16 * TD];
+    ar += v0 * s_w[it - i0] + v1 * s_w[it + 1 - i0] + v2 * s_w[it + 2 - i0] + v3 * s_w[it + 3 - i0];
   }
-  __syncthreads();
-  // Y[n][d] = sum_i rot[n][i] * R[i][d]: A = rot (lane: head r, 8 consecutive i), B from R^T rows.
+  for (; it < ip; ++it) ar += pv[(int64_t)it * 16 * TD] * s_w[it - i0];
+  if (has_res) aq = pv[(int64_t)(i1 - 1) * 16 * TD] * s_w[i1 - 1 - i0];
+  ((uint16_t*)a.query_rot)[bq * TD + d] = f32_to_f16_bits(ar);  // q' is no longer needed: reuse
+  ((float*)a.out_residual)[bq * TD + d] = aq;
+}
+
+// Phase 2, grid (ceil(B*Hq / 16), 16 output tiles), one wave: out = rot R + residual.
+__global__ __launch_bounds__(64) void tq_decode_unrotate_kernel(const anna_mi_tq_decode_args a) {
+  const int lane = threadIdx.x;
+  const int r = lane & 15, kq = lane >> 4;
+  const int64_t row0 = (int64_t)blockIdx.x * 16;
+  const int tile = blockIdx.y;
+  const int64_t rows = a.batch * a.q_heads;
+  const uint16_t* rot = (const uint16_t*)a.query_rot;
   const uint16_t* RT = (const uint16_t*)a.rotation_t_f16;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) {
-    const int tile = wave * 4 + tt;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < 8; ++s) {
+    u32x4 af = {0u, 0u, 0u, 0u};
+    if (row0 + r < rows) af = *(const u32x4*)(rot + (row0 + r) * TD + s * 32 + kq * 8);
+    const u32x4 bfr = *(const u32x4*)(RT + (int64_t)(tile * 16 + r) * TD + s * 32 + kq * 8);
+    acc = mfma_f16(af, bfr, acc);
+  }
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const u32x4 af = *(const u32x4*)(s_rot + r * TD + s * 32 + kq * 8);
-      const u32x4 bfr = *(const u32x4*)(RT + (int64_t)(tile * 16 + r) * TD + s * 32 + kq * 8);
-      acc = mfma_f16(af, bfr, acc);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int n = 4 * kq + i;
-      const int dd = tile * 16 + r;
-      if (n < G) ((uint16_t*)a.out)[(b * a.q_heads + h * G + n) * TD + dd] = f32_to_bf16_bits(acc[i] + s_res[n * TD + dd]);
-    }
+  for (int i = 0; i < 4; ++i) {
+    const int64_t row = row0 + 4 * kq + i;
+    const int dd = tile * 16 + r;
+    if (row < rows) ((uint16_t*)a.out)[row * TD + dd] = f32_to_bf16_bits(acc[i] + ((const float*)a.out_residual)[row * TD + dd]);
   }
 }
 
@@ -447,18 +451,21 @@ extern "C" int anna_mi_tq_decode(const anna_mi_tq_decode_args* ap, void* stream)
   ANNA_CHECK(a.kv_heads > 0 && a.q_heads % a.kv_heads == 0 && a.q_heads / a.kv_heads <= 16,
              "anna_mi_tq_decode: need q_heads = G * kv_heads with G <= 16");
   ANNA_CHECK(a.pool_tokens % TBT == 0 && a.residual_capacity % TBT == 0, "pool and residual capacity must be multiples of 32");
-  ANNA_CHECK(a.query && a.out && a.query_rot && a.partial_stats && a.partial_values && a.items && a.item_ranges,
+  ANNA_CHECK(a.query && a.out && a.out_residual && a.query_rot && a.partial_stats && a.partial_values && a.items &&
+             a.item_ranges,
              "anna_mi_tq_decode: null pointer");
   ANNA_CHECK(a.rotation_f16 && a.rotation_t_f16 && a.key_codes && a.key_norms && a.value_codes && a.value_norms,
              "anna_mi_tq_decode: null cache pointer");
   if (a.num_items <= 0) return ANNA_MI_OK;
   hipStream_t st = as_stream(stream);
-  hipLaunchKernelGGL(tq_rotate_query_kernel, dim3((unsigned)(a.batch * a.kv_heads)), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(tq_rotate_query_kernel, dim3((unsigned)(a.batch * a.kv_heads), 16), dim3(64), 0, st, a);
   ANNA_LAUNCH_CHECK("tq_rotate_query_kernel");
-  hipLaunchKernelGGL(tq_decode_split_kernel, dim3((unsigned)a.num_items), dim3(64 * TWAVES), 0, st, a);
+  hipLaunchKernelGGL(tq_decode_split_kernel, dim3((unsigned)a.num_items), dim3(64 * SWAVES), 0, st, a);
   ANNA_LAUNCH_CHECK("tq_decode_split_kernel");
-  hipLaunchKernelGGL(tq_decode_merge_kernel, dim3((unsigned)(a.batch * a.kv_heads)), dim3(256), 0, st, a);
-  ANNA_LAUNCH_CHECK("tq_decode_merge_kernel");
+  hipLaunchKernelGGL(tq_decode_combine_kernel, dim3((unsigned)(a.batch * a.q_heads)), dim3(256), 0, st, a);
+  ANNA_LAUNCH_CHECK("tq_decode_combine_kernel");
+  hipLaunchKernelGGL(tq_decode_unrotate_kernel, dim3((unsigned)((a.batch * a.q_heads + 15) / 16), 16), dim3(64), 0, st, a);
+  ANNA_LAUNCH_CHECK("tq_decode_unrotate_kernel");
   return ANNA_MI_OK;
 }
 

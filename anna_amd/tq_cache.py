@@ -107,6 +107,7 @@ class TurboQuantBatchCache:
             ps=torch.empty((max(n, 1), 16, 2), dtype=torch.float32, device=dev),
             pv=torch.empty((max(n, 1), 16, self.head_dim), dtype=torch.float32, device=dev),
             qrot=torch.empty((self.batch, self.q_heads, self.head_dim), dtype=torch.float16, device=dev),
+            ores=torch.empty((self.batch, self.q_heads, self.head_dim), dtype=torch.float32, device=dev),
         )
         return self._plan
 
@@ -127,6 +128,7 @@ class TurboQuantBatchCache:
         a.key_scale, a.value_scale, a.scaling = self.key_scale, self.value_scale, float(scaling)
         a.items, a.num_items, a.item_ranges = p["items"].data_ptr(), p["n"], p["ranges"].data_ptr()
         a.query_rot, a.partial_stats, a.partial_values = p["qrot"].data_ptr(), p["ps"].data_ptr(), p["pv"].data_ptr()
+        a.out_residual = p["ores"].data_ptr()
         a.out = out.data_ptr()
         return a
 

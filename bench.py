@@ -160,12 +160,127 @@ def section_int4(args, device):
     return sweep
 
 
+# ---------------------------------------------------------------- TurboQuant
+
+
+def _clone_cache(c):
+    import copy
+
+    n = copy.copy(c)
+    for name in ("key_codes", "key_norms", "value_codes", "value_norms", "residual_key", "residual_value_t"):
+        setattr(n, name, getattr(c, name).clone())
+    return n
+
+
+def section_tq_decode(args, device):
+    """B=8, Hq=16, Hkv=2, D=256, L ~ U[1024, 16384] + 128 bf16 residual."""
+    import numpy as np
+
+    from anna_amd.tq_cache import TurboQuantBatchCache
+
+    rng = np.random.default_rng(4)
+    lens = [int(v) for v in rng.integers(1024, 16385, size=8)]
+    B, HQ, HKV, D, R = 8, 16, 2, 256, 128
+    gen = torch.Generator(device=device)
+    gen.manual_seed(44)
+    base = TurboQuantBatchCache(batch=B, kv_heads=HKV, q_heads=HQ, capacities=lens, residual_capacity=R,
+                                device=device, tokens_per_item=args.tq_tokens_per_item)
+    dense = []
+    for b in range(B):
+        k = torch.randn((HKV, lens[b] + R, D), device=device, generator=gen).to(torch.bfloat16)
+        v = torch.randn((HKV, lens[b] + R, D), device=device, generator=gen).to(torch.bfloat16)
+        base.load_sequence(b, k, v, R)
+        dense.append((k, v))
+    q = torch.randn((B, HQ, D), device=device, generator=gen).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    base.decode(q, scaling=1.0 / 16, out=out)  # builds the plan
+    per_call = base.bytes_per_decode()
+    copies = [base] + [_clone_cache(base) for _ in range(max(1, math.ceil(ROTATE_BYTES / per_call)) - 1)]
+    fns = [(lambda c=c: c.decode(q, scaling=1.0 / 16, out=out)) for c in copies]
+    ms = time_graph(fns, args.steps, args.warmup)
+    sec = ms / 1e3
+    r = {"B": B, "Hq": HQ, "Hkv": HKV, "D": D, "lens": lens, "residual": R, "bits": 2, "ms": ms, "us": ms * 1e3,
+         "tokens/s": B / sec, "GB/s": per_call / sec / 1e9, "bytes": per_call, "roofline_frac": per_call / sec / 1e9 / HBM_PEAK_GBS,
+         "distinct_cache_copies": len(copies), "tokens_per_item": args.tq_tokens_per_item}
+    log(f"tq decode B=8 mean L={sum(lens) / 8:.0f}: {r['us']:.2f} us/call  {r['tokens/s']:.0f} tokens/s  "
+        f"{r['GB/s']:.0f} GB/s  {100 * r['roofline_frac']:.1f}% of HBM peak")
+    cpu = None
+    if not args.no_cpu:
+        from oracle.cpu_paths import tq_decode_rows
+
+        torch.set_num_threads(os.cpu_count() or 1)
+        ks = [k.cpu() for k, _ in dense]
+        vs = [v.cpu() for _, v in dense]
+        qc = q.cpu()
+        tq_decode_rows(qc, ks, vs, 1.0 / 16)
+        iters = 3
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            tq_decode_rows(qc, ks, vs, 1.0 / 16)
+        csec = (time.perf_counter() - t0) / iters
+        cpu = {"value": B / csec, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"{iters} calls of the reference CPU decode branch (bf16 matmuls over the kept dequantized "
+                         f"cache, fp32 softmax; dequant not timed), same B/L/H/D; {csec * 1e3:.1f} ms/call"}
+        log(f"tq decode cpu baseline: {cpu['value']:.1f} tokens/s")
+    r["cpu_baseline"] = cpu
+    return r
+
+
+def section_tq_pack(args, device):
+    """K, V bf16 [8192, 2, 256] with 1% outlier channels x8 -> 2-bit TQ-MSE
+    codes + fp16 norms, last 128 tokens kept bf16."""
+    from anna_amd import fused_ops
+    from anna_amd.turboquant import get_turboquant_quantizer
+
+    T, H, D, R = 8192, 2, 256, 128
+    gen = torch.Generator(device=device)
+    gen.manual_seed(33)
+    qn = get_turboquant_quantizer(head_dim=D, bits=2, device=device)
+    outl = torch.zeros(D, dtype=torch.bool)
+    outl[torch.randperm(D, generator=torch.Generator().manual_seed(3))[: max(1, D // 100)]] = True
+    outl = outl.to(device)
+    kv = []
+    for _ in range(2):
+        x = torch.randn((H, T, D), device=device, generator=gen)
+        x[..., outl] *= 8.0
+        kv.append(x.to(torch.bfloat16))
+    n = (T - R) * H
+    codes = torch.empty((2, n, D // 4), dtype=torch.uint8, device=device)
+    norms = torch.empty((2, n), dtype=torch.float16, device=device)
+    blocked = torch.empty((2, H, (T - R) // 32, 2048), dtype=torch.uint8, device=device)
+
+    def pack():
+        for i, x in enumerate(kv):
+            xs = x[:, : T - R].reshape(-1, D)
+            _lib_call_mse(fused_ops, xs, qn, codes[i], norms[i])
+        for h in range(H):
+            fused_ops._lib.call("anna_mi_tq_block_values", codes[1, h * (T - R):].data_ptr(), T - R,
+                                blocked[1, h].data_ptr(), fused_ops._lib.stream_of(codes))
+
+    ms = time_graph([pack], max(4, args.steps // 10), 2)
+    sec = ms / 1e3
+    bytes_ = 2 * H * T * D * 2 + 2 * n * (D // 4 + 2)
+    r = {"T": T, "H": H, "D": D, "residual": R, "ms": ms, "us": ms * 1e3, "GB/s": bytes_ / sec, "bytes": bytes_,
+         "vectors/s": 2 * n / sec, "bound": "valu (D x D fp32 fma rotation, bit-exact order)",
+         "GFLOP/s": 2 * n * D * D * 2 / sec / 1e9}
+    log(f"tq pack K+V [8192,2,256]: {r['us']:.1f} us  {r['vectors/s'] / 1e6:.2f} M vectors/s  "
+        f"{r['GFLOP/s']:.0f} GFLOP/s (fp32 rotation)")
+    return r
+
+
+def _lib_call_mse(fused_ops, xs, qn, codes, norms):
+    fused_ops._lib.call("anna_mi_tq_mse_quantize", xs.data_ptr(), fused_ops._lib.dtype_code(xs.dtype), xs.size(0),
+                        xs.size(1), xs.stride(0), qn.rotation_t.data_ptr(), qn.thresholds.data_ptr(), 2,
+                        codes.data_ptr(), norms.data_ptr(), fused_ops._lib.stream_of(xs))
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=60)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--sections", default="int4")
+    ap.add_argument("--sections", default="int4,tq_decode,tq_pack")
+    ap.add_argument("--tq-tokens-per-item", type=int, default=512)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--int4-points", default="", help="comma list of MxNxK (default: the BASELINE sweep)")
@@ -185,6 +300,13 @@ def main() -> int:
     wanted = set(args.sections.split(","))
     if "int4" in wanted:
         sections["int4_sweep"] = section_int4(args, device)
+    if "tq_decode" in wanted:
+        sections["tq_decode"] = section_tq_decode(args, device)
+    if "tq_pack" in wanted:
+        sections["tq_pack"] = section_tq_pack(args, device)
+    if "int4_sweep" not in sections:
+        print(json.dumps({"sections": sections}))
+        return 0
     head = next((r for r in sections["int4_sweep"] if (r["M"], r["N"], r["K"]) == (1, 12288, 4096)),
                 sections["int4_sweep"][0])
     cpu = None

@@ -220,9 +220,10 @@ typedef struct {
   const int32_t* items;             /* [num_items][4] device */
   int64_t num_items;
   const int32_t* item_ranges;       /* [B*Hkv + 1] device */
-  uint16_t* query_rot;              /* workspace fp16 [B][Hq][D] */
+  uint16_t* query_rot;              /* workspace fp16 [B][Hq][D] (q', then the rotated sum) */
   float* partial_stats;             /* workspace [num_items][16][2] */
   float* partial_values;            /* workspace [num_items][16][D] */
+  float* out_residual;              /* workspace [B][Hq][D] */
   uint16_t* out;                    /* bf16 [B][Hq][D] */
 } anna_mi_tq_decode_args;
 
@@ -236,7 +237,7 @@ int anna_mi_tq_decode_plan(int64_t batch, int64_t kv_heads, const int64_t* quant
 /* sizeof(anna_mi_tq_decode_args), for binding checks. */
 int64_t anna_mi_sizeof_tq_decode_args(void);
 
-/* Three launches: q' = R q, split (per item), merge (per b, kv_head). */
+/* Four launches: q' = R q, split (per item), combine (per b, q-head), un-rotation. */
 int anna_mi_tq_decode(const anna_mi_tq_decode_args* args, void* stream);
 
 /* Reorders natural 2-bit codes [tokens][64] (D = 256) of one KV head into the blocked

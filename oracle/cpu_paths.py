@@ -24,3 +24,21 @@ def int4_forward_dequant(x_bf16: torch.Tensor, qweight: torch.Tensor, qscale: to
     groups = unpacked.reshape(n, kp // group_size, group_size)
     w = ((groups - z.unsqueeze(-1)) * s.unsqueeze(-1)).reshape(n, kp)[:, :in_features]
     return F.linear(x_bf16, w.to(torch.bfloat16))
+
+
+def tq_decode_rows(query: torch.Tensor, keys: list, values: list, scaling: float) -> torch.Tensor:
+    """CPU branch of TurboQuantKVRow.decode_attention per row (turboquant.py:1295-1346), as
+    called row by row by Qwen3DynamicCache.turboquant_single_token_decode_attention
+    (ops.py:1055-1071): bf16 matmul against the (kept, already dequantized) bf16 keys,
+    fp32 softmax, bf16 matmul against the values.  query [B, Hq, D]; keys/values per row
+    [Hkv, L, D] bf16."""
+    outs = []
+    for b in range(query.shape[0]):
+        k, v = keys[b], values[b]
+        hkv, _, d = k.shape
+        g = query.shape[1] // hkv
+        q = query[b].reshape(hkv, g, 1, d)
+        s = torch.matmul(q, k.unsqueeze(1).transpose(-1, -2)) * scaling
+        p = torch.softmax(s.to(torch.float32), dim=-1).to(torch.bfloat16)
+        outs.append(torch.matmul(p, v.unsqueeze(1)).reshape(hkv * g, d))
+    return torch.stack(outs)
