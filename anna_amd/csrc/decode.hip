@@ -174,7 +174,7 @@ __global__ __launch_bounds__(64 * DEC_WAVES) void decode_split_kernel(const anna
       m[h] = nm;
     }
   }
-  // merge the 4 waves: common max, rescale, LDS float atomics
+  // merge the 4 waves: common max, rescale, ordered sum in LDS
   if (lane == 0) {
 #pragma unroll
     for (int h = 0; h < GM; ++h)
@@ -184,16 +184,21 @@ __global__ __launch_bounds__(64 * DEC_WAVES) void decode_split_kernel(const anna
       }
   }
   __syncthreads();
+  // waves add in a fixed order (deterministic sums; each lane owns its entries)
+  for (int w = 0; w < DEC_WAVES; ++w) {
+    if (wave == w) {
 #pragma unroll
-  for (int h = 0; h < GM; ++h) {
-    if (h >= G) continue;
-    float M = -INFINITY;
-    for (int w = 0; w < DEC_WAVES; ++w) M = fmaxf(M, s_m[w][h]);
-    const float f = l[h] == 0.f ? 0.f : expf(m[h] - M);
+      for (int h = 0; h < GM; ++h) {
+        if (h >= G) continue;
+        float M = -INFINITY;
+        for (int w2 = 0; w2 < DEC_WAVES; ++w2) M = fmaxf(M, s_m[w2][h]);
+        const float f = l[h] == 0.f ? 0.f : expf(m[h] - M);
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) atomicAdd(&s_acc[h * D + lane * DPL + j], acc[h][j] * f);
+        for (int j = 0; j < DPL; ++j) s_acc[h * D + lane * DPL + j] += acc[h][j] * f;
+      }
+    }
+    __syncthreads();
   }
-  __syncthreads();
   for (int64_t i = threadIdx.x; i < (int64_t)G * D; i += blockDim.x) {
     const int h = (int)(i / D);
     const int64_t d = i % D, hq = kvh * G + h;

@@ -1,7 +1,7 @@
 // Batched varlen GQA decode over a 2-bit TurboQuant-MSE KV cache (head_dim 256), MFMA.
 //
-// Cache layout (per KV head, a pool of `pool_tokens` token slots; sequence b owns slots
-// [seq_offsets[b], seq_offsets[b] + capacity), offsets multiple of 32):
+// Cache layout (per KV head, a pool of `pool_tokens` token slots; a sequence owns a range
+// of slots starting at a multiple of 32):
 //   key_codes   uint8 [Hkv][pool][64]       token-major, dim i at bits 2(i%4) of byte i/4
 //   key_norms   fp16  [Hkv][pool]
 //   value_codes uint8 [Hkv][pool/32][2048]  32-token blocks, byte ((t%16)/4)*512 + dim*2 + t/16,
@@ -10,20 +10,21 @@
 //   residual_key     bf16 [B][Hkv][R][256]  newest tokens, dense, token-major
 //   residual_value_t bf16 [B][Hkv][256][R]  dense, dim-major
 //
-// Kernels (one call = four launches):
-//   tq_rotate_query  q' = R q (MFMA, fp16 in / fp32 accumulate) for every (b, q-head).
-//   tq_decode_split  one workgroup per work item (b, kv-head, <= tokens_per_item tokens or the
-//     residual window).  8 waves take 32-token blocks (next block prefetched).  Scores are formed transposed,
-//     S^T = Khat Q'^T, by v_mfma_f32_16x16x32_f16 on codes turned into fp16 centroids with one
-//     v_perm per pair (the 2-bit centroids are fp16 values sharing their low byte); S^T's
-//     accumulator layout is exactly the B operand of O'^T = Vhat^T P^T, so probabilities
-//     never leave registers.  Online softmax in base 2 with lazy rescaling (the running max
-//     only moves when a block exceeds it by 2^4).  Output: per item and q-head
-//     (max, denominator) and the unnormalized accumulator (rotated space for packed items).
-//   tq_decode_combine  per (b, q-head): log-sum-exp weights of the items, weighted sums of the
-//     packed (rotated) and residual partial accumulators.
-//   tq_decode_unrotate  out = (rotated sum) R + (residual sum), a [B*Hq x 256] x [256 x 256]
-//     MFMA product, bf16 output.
+// One launch, one 512-thread workgroup per work item (b, kv-head, pool range) or per residual
+// window (see anna_mi_tq_decode_plan):
+//   prologue  q' = R q for the item's G q-heads (MFMA, fp16; R is read from L2), kept in LDS as
+//     the B operand of the score product; the first block of each wave already in flight.
+//   loop      8 waves take 32-token blocks (the next block prefetched).  Scores are formed
+//     transposed, S^T = Khat Q'^T, by v_mfma_f32_16x16x32_f16 on codes turned into fp16
+//     centroids with one v_perm per pair (the 2-bit centroids are fp16 values sharing their
+//     low byte); S^T's accumulator layout is the B operand of O'^T = Vhat^T P^T, so the
+//     probabilities never leave registers.  Online softmax in base 2 with lazy rescaling
+//     (the running max only moves when a block exceeds it by 2^4).
+//   reduce    the 8 waves' accumulators are summed through LDS; per item and q-head the
+//     (max, denominator) and the unnormalized accumulator go to the workspace.
+//   tail      the last workgroup of a (b, kv-head) to finish (a counter that it resets)
+//     combines the items with log-sum-exp weights and applies R^T to the rotated sum
+//     (MFMA), adds the residual window's part and writes bf16.
 #include <vector>
 
 #include "common.hpp"
@@ -70,45 +71,16 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
 }
 
-// ------------------------------------------------------------------ q' = R q
+// ------------------------------------------------------------------ decode kernel
 
-// grid (B * Hkv, 16 output tiles), one wave.  Q [16 heads x 256] (bf16 -> fp16) times R^T.
-__global__ __launch_bounds__(64) void tq_rotate_query_kernel(const anna_mi_tq_decode_args a) {
-  const int lane = threadIdx.x;
-  const int r = lane & 15, kq = lane >> 4;
-  const int64_t bh = blockIdx.x, b = bh / a.kv_heads, h = bh % a.kv_heads;
-  const int tile = blockIdx.y;  // output dims i in [16 tile, 16 tile + 16)
-  const int G = (int)(a.q_heads / a.kv_heads);
-  const uint16_t* q = (const uint16_t*)a.query + (b * a.q_heads + h * G) * TD;
-  const uint16_t* R = (const uint16_t*)a.rotation_f16;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (r < G) v = *(const u32x4*)(q + r * TD + s * 32 + kq * 8);
-    u32x4 af;
-#pragma unroll
-    for (int w = 0; w < 4; ++w)
-      af[w] = pack_f16x2(bf16_bits_to_f32((uint16_t)(v[w] & 0xFFFFu)), bf16_bits_to_f32((uint16_t)(v[w] >> 16)));
-    const u32x4 bfr = *(const u32x4*)(R + (int64_t)(tile * 16 + r) * TD + s * 32 + kq * 8);
-    acc = mfma_f16(af, bfr, acc);
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int n = 4 * kq + i;
-    if (n < G) ((uint16_t*)a.query_rot)[(b * a.q_heads + h * G + n) * TD + tile * 16 + r] = f32_to_f16_bits(acc[i]);
-  }
-}
-
-// ------------------------------------------------------------------ split
-
-constexpr int SWAVES = 8;  // waves per work item
+constexpr int SWAVES = 8;      // waves per work item
 
 struct BlockRaw {
   u32x4 k0, k1, v0, v1;     // key codes (tokens r, 16 + r), value codes (dims 16 r .. 16 r + 15)
   uint2 kn0, kn1, vn0, vn1;  // norms of tokens 4 kq .. 4 kq + 3 and 16 + 4 kq ..
 };
 
+// p0: pool slot of the block's first token (multiple of 32)
 __device__ __forceinline__ void load_block(const anna_mi_tq_decode_args& a, int64_t h, int64_t p0, int r, int kq,
                                            BlockRaw& o) {
   const int64_t T = a.pool_tokens;
@@ -131,75 +103,73 @@ __device__ __forceinline__ float half_of(uint2 v, int i) {
   return f16_bits_to_f32((uint16_t)(w >> (16 * (i & 1))));
 }
 
-__global__ __launch_bounds__(64 * SWAVES) __attribute__((amdgpu_waves_per_eu(2, 8)))
-void tq_decode_split_kernel(const anna_mi_tq_decode_args a) {
-  __shared__ u32x4 s_qf[8][64];  // B operand of S^T = Khat Q'^T per dim-step and lane
-  __shared__ float s_m[SWAVES][16], s_l[SWAVES][16];
-  // s_acc[(i * 16 + j) * 64 + lane] holds head r, dim (4 kq + i) * 16 + j: the 64 lanes of
-  // one atomic add hit 64 consecutive words (no bank conflict).
-  __shared__ float s_acc[16 * TD];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+__device__ __forceinline__ uint32_t f16x2_of_bf16x2(uint32_t v) {
+  return pack_f16x2(bf16_bits_to_f32((uint16_t)(v & 0xFFFFu)), bf16_bits_to_f32((uint16_t)(v >> 16)));
+}
+
+__device__ __forceinline__ uint32_t pkrtz(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+}
+
+// q' = R q for one tile of 16 dims of the G heads of one (b, kv-head), written into the B
+// operand fragments of the score product: frag[step s][lane][e] (fp16) holds q'[head lane % 16][dim],
+// dim = 64 (lane / 16) + 16 (s >> 1) + 4 (s & 1) + w', e = 2 (w' & 3) + (w' >> 3), w' in
+// {0..3, 8..11} (the pair order of codes_to_f16).  One wave: A = R rows (16 dims x 32), B = q^T
+// (32 x 16 heads, bf16 -> fp16); C lane: head r, dims 16 tile + 4 kq + i.
+__device__ __forceinline__ void tq_rotate_fragment(const anna_mi_tq_decode_args& a, const uint16_t* qg, int G, int tile,
+                                                   int lane, uint16_t* frag) {
   const int r = lane & 15, kq = lane >> 4;
-  const int64_t item = blockIdx.x;
-  const int32_t* it = a.items + item * 4;
-  const int64_t b = it[0], h = it[1];
-  const int64_t t0 = it[2], t1 = it[3];
-  const bool resid = t0 < 0;
-  const int G = (int)(a.q_heads / a.kv_heads);
-  const int64_t Rc = a.residual_capacity;
-  const int64_t tb0 = resid ? 0 : t0;
-  const int64_t tend = resid ? (int64_t)a.residual_lens[b] : t1;
-  const int64_t nblk = (tend - tb0 + TBT - 1) / TBT;
-
-  for (int i = threadIdx.x; i < 16 * TD; i += blockDim.x) s_acc[i] = 0.f;
-  const int64_t off = resid ? 0 : a.seq_offsets[b];
-  BlockRaw cur;
-  if (!resid && wave < nblk) load_block(a, h, off + tb0 + wave * TBT, r, kq, cur);  // in flight across the barrier
-  if (wave == 0) {
-    if (!resid) {
-      // q' rows in the pair order of codes_to_f16 (see the K conversion below)
-      const uint16_t* qr = (const uint16_t*)a.query_rot + (b * a.q_heads + h * G + r) * TD;
+  // unconditional loads (row clamped, value zeroed) so that they issue back to back
+  const uint16_t* qrow = qg + (r < G ? r : 0) * TD + kq * 8;
+  const uint32_t keep = r < G ? 0xFFFFFFFFu : 0u;
+  u32x4 qv[8], rv[8];
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const int da = 64 * kq + 16 * (s >> 1) + 4 * (s & 1);
-        uint2 lo = {0u, 0u}, hi = {0u, 0u};
-        if (r < G) {
-          lo = *(const uint2*)(qr + da);
-          hi = *(const uint2*)(qr + da + 8);
-        }
-        u32x4 f;
-        f.x = __builtin_amdgcn_perm(hi.x, lo.x, 0x05040100u);
-        f.y = __builtin_amdgcn_perm(hi.x, lo.x, 0x07060302u);
-        f.z = __builtin_amdgcn_perm(hi.y, lo.y, 0x05040100u);
-        f.w = __builtin_amdgcn_perm(hi.y, lo.y, 0x07060302u);
-        s_qf[s][lane] = f;
-      }
-    } else {
-      const uint16_t* q = (const uint16_t*)a.query + (b * a.q_heads + h * G + r) * TD;
-#pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (r < G) v = *(const u32x4*)(q + s * 32 + kq * 8);
-        s_qf[s][lane] = v;
-      }
-    }
+  for (int st = 0; st < 8; ++st) {
+    qv[st] = *(const u32x4*)(qrow + st * 32);
+    rv[st] = *(const u32x4*)(a.rotation_f16 + (int64_t)(tile * 16 + r) * TD + st * 32 + kq * 8);
   }
-  __syncthreads();
+  f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int st = 0; st < 8; ++st) {
+    u32x4 qb;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) qb[w] = f16x2_of_bf16x2(qv[st][w] & keep);
+    c = mfma_f16(rv[st], qb, c);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int dim = tile * 16 + 4 * kq + i;
+    const int kq2 = dim >> 6, rem = dim & 63, w = rem & 15;
+    const int sx = 2 * (rem >> 4) + ((rem >> 2) & 1), e = 2 * (w & 3) + (w >> 3);
+    frag[((sx * 64) + kq2 * 16 + r) * 8 + e] = f32_to_f16_bits(c[i]);
+  }
+}
 
+// grid (B * Hkv, 16 dim tiles), one wave: q' fragments of every (b, kv-head) into
+// query_frag[b][h] (4096 fp16 each).
+__global__ __launch_bounds__(64) void tq_rotate_query_kernel(const anna_mi_tq_decode_args a) {
+  const int64_t bh = blockIdx.x, b = bh / a.kv_heads, h = bh % a.kv_heads;
+  const int G = (int)(a.q_heads / a.kv_heads);
+  tq_rotate_fragment(a, a.query + (b * a.q_heads + h * G) * TD, G, blockIdx.y, threadIdx.x, a.query_frag + bh * 4096);
+}
+
+// One 32-token block of one wave (slot / window position tb): scores, online softmax, and
+// the value product into acc.  RESID: the dense residual window (bf16 MFMAs, loads issued
+// here); otherwise the 2-bit codes already loaded into cur.
+template <bool RESID>
+__device__ __forceinline__ void block_step(const anna_mi_tq_decode_args& a, const u32x4 (*s_qf)[64], int64_t b,
+                                           int64_t h, int64_t tb, int64_t tend, int lane, const BlockRaw& cur,
+                                           f32x4 (&acc)[16], float& m_run, float& l_run) {
+  const int r = lane & 15, kq = lane >> 4;
+  const int64_t Rc = a.residual_capacity;
   const uint32_t lut_hi = vconst(0x433CBCC3u), lut_lo = vconst(0x7E7E7E7Eu), or_c = vconst(0x04000400u);
   const float kscale = a.key_scale * a.scaling * LOG2E;
   const float vscale = a.value_scale * P_SCALE;
-  f32x4 acc[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;
-
-  for (int64_t blk = wave; blk < nblk; blk += SWAVES) {
-    const int64_t tb = tb0 + blk * TBT;
-    if (!resid && blk != wave) load_block(a, h, off + tb, r, kq, cur);
+  {
     float s[8], nv[8];
     f32x4 st0 = {0.f, 0.f, 0.f, 0.f}, st1 = {0.f, 0.f, 0.f, 0.f};
-    if (!resid) {
+    uint2 rlo[RESID ? 16 : 1], rhi[RESID ? 16 : 1];
+    if constexpr (!RESID) {
 #pragma unroll
       for (int st = 0; st < 8; ++st) {
         const u32x4 qf = s_qf[st][lane];
@@ -211,20 +181,34 @@ void tq_decode_split_kernel(const anna_mi_tq_decode_args a) {
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        s[i] = st0[i] * half_of(cur.kn0, i) * kscale;
-        s[4 + i] = st1[i] * half_of(cur.kn1, i) * kscale;
+        s[i] = st0[i] * (half_of(cur.kn0, i) * kscale);
+        s[4 + i] = st1[i] * (half_of(cur.kn1, i) * kscale);
         nv[i] = half_of(cur.vn0, i) * vscale;
         nv[4 + i] = half_of(cur.vn1, i) * vscale;
       }
     } else {
+      // every load of the block first (K rows, V columns), then the MFMAs: left to itself the
+      // scheduler interleaves load, wait and MFMA one tile at a time
       const uint16_t* rk = a.residual_key + ((b * a.kv_heads + h) * Rc + tb) * TD;
+      const uint16_t* rv = a.residual_value_t + (b * a.kv_heads + h) * TD * Rc + tb;
+      u32x4 ka[8], kb[8];
+#pragma unroll
+      for (int st = 0; st < 8; ++st) {
+        ka[st] = *(const u32x4*)(rk + r * TD + st * 32 + kq * 8);
+        kb[st] = *(const u32x4*)(rk + (16 + r) * TD + st * 32 + kq * 8);
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int64_t dim = r * 16 + j;
+        rlo[j] = *(const uint2*)(rv + dim * Rc + 4 * kq);
+        rhi[j] = *(const uint2*)(rv + dim * Rc + 16 + 4 * kq);
+      }
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int st = 0; st < 8; ++st) {
         const u32x4 qf = s_qf[st][lane];
-        const u32x4 a0 = *(const u32x4*)(rk + r * TD + st * 32 + kq * 8);
-        const u32x4 a1 = *(const u32x4*)(rk + (16 + r) * TD + st * 32 + kq * 8);
-        st0 = mfma_bf16(a0, qf, st0);
-        st1 = mfma_bf16(a1, qf, st1);
+        st0 = mfma_bf16(ka[st], qf, st0);
+        st1 = mfma_bf16(kb[st], qf, st1);
       }
       const float sc = a.scaling * LOG2E;
 #pragma unroll
@@ -235,13 +219,15 @@ void tq_decode_split_kernel(const anna_mi_tq_decode_args a) {
         nv[4 + i] = P_SCALE;
       }
     }
-    // mask tokens past the end (their memory may hold anything: select, never multiply)
+    if (tb + TBT > tend) {
+      // tokens past the end: their memory may hold anything (select, never multiply)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int64_t t = tb + (i >> 2) * 16 + 4 * kq + (i & 3);
-      if (t >= tend) {
-        s[i] = -INFINITY;
-        nv[i] = 0.f;
+      for (int i = 0; i < 8; ++i) {
+        const int64_t t = tb + (i >> 2) * 16 + 4 * kq + (i & 3);
+        if (t >= tend) {
+          s[i] = -INFINITY;
+          nv[i] = 0.f;
+        }
       }
     }
     float mx = s[0];
@@ -251,7 +237,7 @@ void tq_decode_split_kernel(const anna_mi_tq_decode_args a) {
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     if (__any(mx > m_run + LAZY)) {
       const float m_new = fmaxf(m_run, mx);
-      const float alpha = exp2f(m_run - m_new);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       l_run *= alpha;
 #pragma unroll
       for (int j = 0; j < 16; ++j) acc[j] *= alpha;
@@ -260,11 +246,11 @@ void tq_decode_split_kernel(const anna_mi_tq_decode_args a) {
     u32x4 pf;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float p0 = exp2f(s[i] - m_run), p1 = exp2f(s[4 + i] - m_run);
+      const float p0 = __builtin_amdgcn_exp2f(s[i] - m_run), p1 = __builtin_amdgcn_exp2f(s[4 + i] - m_run);
       l_run += p0 + p1;
-      pf[i] = resid ? pack_bf16x2(p0 * nv[i], p1 * nv[4 + i]) : pack_f16x2(p0 * nv[i], p1 * nv[4 + i]);
+      pf[i] = RESID ? pack_bf16x2(p0 * nv[i], p1 * nv[4 + i]) : pkrtz(p0 * nv[i], p1 * nv[4 + i]);
     }
-    if (!resid) {
+    if constexpr (!RESID) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const uint32_t w = (j >> 3) ? cur.v1[(j >> 1) & 3] : cur.v0[(j >> 1) & 3];
@@ -273,12 +259,9 @@ void tq_decode_split_kernel(const anna_mi_tq_decode_args a) {
         __builtin_amdgcn_sched_barrier(0);
       }
     } else {
-      const uint16_t* rv = a.residual_value_t + (b * a.kv_heads + h) * TD * Rc + tb;
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const int64_t dim = r * 16 + j;
-        const uint2 lo = *(const uint2*)(rv + dim * Rc + 4 * kq);
-        const uint2 hi = *(const uint2*)(rv + dim * Rc + 16 + 4 * kq);
+        const uint2 lo = rlo[j], hi = rhi[j];
         u32x4 av;
         av.x = __builtin_amdgcn_perm(hi.x, lo.x, 0x05040100u);
         av.y = __builtin_amdgcn_perm(hi.x, lo.x, 0x07060302u);
@@ -288,7 +271,92 @@ void tq_decode_split_kernel(const anna_mi_tq_decode_args a) {
       }
     }
   }
-  // lanes of one head: sum partial denominators
+}
+
+// The blocks of one item taken by one wave.  Residual windows (a few blocks): blocks wave,
+// wave + 8, ...  Packed items: the first block is `wave` (already loaded into A), the next
+// ones are taken from the workgroup's LDS counter *next, so that the two waves sharing a SIMD
+// (the second one issues less often) finish together.  Blocks ping-pong between two register
+// buffers; the prefetch is unconditional (clamped to the last block) so that no wait for it is
+// forced before the current block is consumed.
+template <bool RESID>
+__device__ __forceinline__ void run_blocks(const anna_mi_tq_decode_args& a, const u32x4 (*s_qf)[64], int64_t b, int64_t h,
+                                           int64_t tb0, int64_t tend, int64_t nblk, int wave, int lane, BlockRaw& A,
+                                           uint32_t* next, f32x4 (&acc)[16], float& m_run, float& l_run) {
+  const int r = lane & 15, kq = lane >> 4;
+  if constexpr (RESID) {
+    for (int64_t blk = wave; blk < nblk; blk += SWAVES)
+      block_step<true>(a, s_qf, b, h, tb0 + blk * TBT, tend, lane, A, acc, m_run, l_run);
+  } else {
+    auto take = [&]() -> int64_t {
+      uint32_t v = 0;
+      if (lane == 0) v = atomicAdd(next, 1u);
+      return (int64_t)__builtin_amdgcn_readfirstlane(v);
+    };
+    const int64_t last = nblk - 1;
+    int64_t c = wave;
+    if (c >= nblk) return;
+    int64_t n = take();
+    BlockRaw B;
+    for (;;) {
+      load_block(a, h, tb0 + (n < last ? n : last) * TBT, r, kq, B);
+      block_step<false>(a, s_qf, b, h, tb0 + c * TBT, tend, lane, A, acc, m_run, l_run);
+      c = n;
+      if (c >= nblk) break;
+      n = take();
+      load_block(a, h, tb0 + (n < last ? n : last) * TBT, r, kq, A);
+      block_step<false>(a, s_qf, b, h, tb0 + c * TBT, tend, lane, B, acc, m_run, l_run);
+      c = n;
+      if (c >= nblk) break;
+      n = take();
+    }
+  }
+}
+
+__global__ __launch_bounds__(64 * SWAVES) __attribute__((amdgpu_waves_per_eu(2, 8)))
+void tq_decode_split_kernel(const anna_mi_tq_decode_args a) {
+  // B operand of S^T = Khat Q'^T per dim-step and lane (fp16 q' or bf16 q)
+  __shared__ u32x4 s_qf[8][64];
+  __shared__ float s_m[SWAVES][16], s_l[SWAVES][16];
+  // cross-wave sums: [wave][tile j][kq * 8 + head % 8]
+  __shared__ f32x4 s_red[SWAVES][16][32];
+  __shared__ uint32_t s_next;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, kq = lane >> 4;
+  const int64_t item = blockIdx.x;
+  const int32_t* it = a.items + item * 4;
+  const int64_t b = it[0], h = it[1];
+  const bool resid = it[2] < 0;
+  const int64_t tb0 = resid ? 0 : it[2];
+  const int64_t tend = it[3];  // end slot (packed) or window length (residual)
+  const int G = (int)(a.q_heads / a.kv_heads);
+  const int64_t Rc = a.residual_capacity;
+  const int64_t nblk = (tend - tb0 + TBT - 1) / TBT;
+  const uint16_t* qg = a.query + (b * a.q_heads + h * G) * TD;
+  const int64_t bh = b * a.kv_heads + h;
+
+  BlockRaw cur;
+  if (!resid)  // in flight during the prologue (clamped: a wave without blocks reloads the last)
+    load_block(a, h, tb0 + (wave < nblk ? wave : nblk - 1) * TBT, r, kq, cur);
+  if (threadIdx.x == 0) s_next = SWAVES;
+  if (!resid) {
+    s_qf[wave][lane] = *(const u32x4*)(a.query_frag + bh * 4096 + (wave * 64 + lane) * 8);
+  } else {
+    const u32x4 v = *(const u32x4*)(qg + (r < G ? r : 0) * TD + wave * 32 + kq * 8);
+    s_qf[wave][lane] = r < G ? v : u32x4{0u, 0u, 0u, 0u};
+  }
+  __syncthreads();
+
+  f32x4 acc[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+  if (resid)
+    run_blocks<true>(a, s_qf, b, h, tb0, tend, nblk, wave, lane, cur, &s_next, acc, m_run, l_run);
+  else
+    run_blocks<false>(a, s_qf, b, h, tb0, tend, nblk, wave, lane, cur, &s_next, acc, m_run, l_run);
+
+  // ---- reduce the waves
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);
   if (kq == 0) {
@@ -296,94 +364,137 @@ void tq_decode_split_kernel(const anna_mi_tq_decode_args a) {
     s_l[wave][r] = l_run;
   }
   __syncthreads();
-  float M = -INFINITY;
+  {
+    float M = -INFINITY;
 #pragma unroll
-  for (int w = 0; w < SWAVES; ++w) M = fmaxf(M, s_m[w][r]);
-  const float f = l_run > 0.f ? exp2f(m_run - M) : 0.f;
-  if (r < G && f != 0.f) {
+    for (int w = 0; w < SWAVES; ++w) M = fmaxf(M, s_m[w][r]);
+    const float f = l_run > 0.f ? __builtin_amdgcn_exp2f(m_run - M) * (1.0f / P_SCALE) : 0.f;
 #pragma unroll
-    for (int j = 0; j < 16; ++j)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) atomicAdd(&s_acc[(i * 16 + j) * 64 + lane], acc[j][i] * f);
+    for (int j = 0; j < 16; ++j) acc[j] *= f;
   }
-  __syncthreads();
-  float* pv = a.partial_values + item * 16 * TD;
-  for (int e = threadIdx.x; e < G * TD; e += blockDim.x) {
-    const int n = e / TD, d = e % TD;
-    const int ekq = d >> 6, ei = (d >> 4) & 3, ej = d & 15;
-    pv[e] = s_acc[(ei * 16 + ej) * 64 + ekq * 16 + n] * (1.0f / P_SCALE);
+  // partial_values[item] as f32x4 [head block hb/8][tile j][kq * 8 + head % 8]; element i of
+  // entry (j, kq) is dim (4 kq + i) * 16 + j (the accumulator layout of O'^T)
+  f32x4* pvi = (f32x4*)(a.partial_values + item * 16 * TD);
+  for (int hb = 0; hb < G; hb += 8) {
+    if (r >= hb && r < hb + 8) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) s_red[wave][j][kq * 8 + r - hb] = acc[j];
+    }
+    __syncthreads();
+    const int t = threadIdx.x, j = t >> 5, e = t & 31;
+    if (hb + (e & 7) < G) {
+      f32x4 sum = s_red[0][j][e];
+#pragma unroll
+      for (int w = 1; w < SWAVES; ++w) sum += s_red[w][j][e];
+      pvi[(hb / 8) * 512 + t] = sum;
+    }
+    __syncthreads();
   }
   if (threadIdx.x < (unsigned)G) {
     const int n = threadIdx.x;
     float Mx = -INFINITY, L = 0.f;
     for (int w = 0; w < SWAVES; ++w) Mx = fmaxf(Mx, s_m[w][n]);
     for (int w = 0; w < SWAVES; ++w)
-      if (s_l[w][n] > 0.f) L += s_l[w][n] * exp2f(s_m[w][n] - Mx);
+      if (s_l[w][n] > 0.f) L += s_l[w][n] * __builtin_amdgcn_exp2f(s_m[w][n] - Mx);
     a.partial_stats[(item * 16 + n) * 2] = Mx;
     a.partial_stats[(item * 16 + n) * 2 + 1] = L;
   }
 }
 
-// ------------------------------------------------------------------ merge
+// ------------------------------------------------------------------ combine
 
-// Phase 1, grid (B * Hq), 256 threads (thread = dim): weighted sum of the items of one
-// (b, q-head); writes the normalized rotated part (fp16) and the residual part (fp32).
-__global__ __launch_bounds__(256) void tq_decode_combine_kernel(const anna_mi_tq_decode_args a) {
-  __shared__ float s_w[64];
-  const int64_t bq = blockIdx.x, b = bq / a.q_heads, hq = bq % a.q_heads;
+// grid (B * Hkv), 512 threads: combines the items of one (b, kv-head) with log-sum-exp weights,
+// applies R^T to the rotated sum (MFMA), adds the residual window's part and writes bf16.
+__global__ __launch_bounds__(64 * SWAVES) void tq_decode_combine_kernel(const anna_mi_tq_decode_args a) {
+  __shared__ float s_res[16 * TD];
+  constexpr int RP = TD + 8;  // padded fp16 rows of the rotated sum
+  __shared__ uint16_t s_rot[16 * RP];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, kq = lane >> 4;
+  const int64_t bh = blockIdx.x, b = bh / a.kv_heads, h = bh % a.kv_heads;
   const int G = (int)(a.q_heads / a.kv_heads);
-  const int64_t h = hq / G, n = hq % G;
-  const int32_t i0 = a.item_ranges[b * a.kv_heads + h], i1 = a.item_ranges[b * a.kv_heads + h + 1];
-  if (threadIdx.x < 64) {
-    const int it = i0 + (int)threadIdx.x;
-    const float m = it < i1 ? a.partial_stats[((int64_t)it * 16 + n) * 2] : -INFINITY;
-    const float l = it < i1 ? a.partial_stats[((int64_t)it * 16 + n) * 2 + 1] : 0.f;
-    const float M = wave_max(l > 0.f ? m : -INFINITY);
-    const float e = l > 0.f ? exp2f(m - M) : 0.f;
-    const float L = wave_sum(l * e);
-    s_w[threadIdx.x] = L > 0.f ? e / L : 0.f;
+  const int4 info = *(const int4*)(a.bh_items + bh * 4);  // first item, packed items, residual item
+  const int i0 = info.x, npk = info.y, ires = info.z;
+  const bool has_res = ires >= 0;
+  // R^T rows of this wave's two output tiles, in flight during the combine
+  u32x4 bfr[2][8];
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+    for (int st = 0; st < 8; ++st)
+      bfr[tt][st] = *(const u32x4*)(a.rotation_t_f16 + (int64_t)((2 * wave + tt) * 16 + r) * TD + st * 32 + kq * 8);
+  constexpr int64_t IS = 16 * TD / 4;  // item stride of partial_values in f32x4
+  // Thread t owns entry (tile j, e) of head n = hb + e % 8 in every item: it combines the
+  // items itself with an online log-sum-exp over batches of 8 (values and stats loaded together).
+  for (int hb = 0; hb < G; hb += 8) {
+    const int t = threadIdx.x, j = t >> 5, e = t & 31;
+    const int n = hb + (e & 7), ekq = e >> 3;
+    if (n >= G) continue;
+    const f32x4* src = (const f32x4*)a.partial_values + (hb / 8) * 512 + t;
+    const float* stn = a.partial_stats + n * 2;
+    f32x4 vr = {0.f, 0.f, 0.f, 0.f};
+    float2 mlr = {-INFINITY, 0.f};
+    if (has_res) {
+      vr = src[(int64_t)ires * IS];
+      mlr = *(const float2*)(stn + (int64_t)ires * 32);
+    }
+    f32x4 sr = {0.f, 0.f, 0.f, 0.f};
+    float M = -INFINITY, L = 0.f;
+    for (int k0 = 0; k0 < npk; k0 += 16) {
+      f32x4 v[16];
+      float2 ml[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const int64_t idx = i0 + (k0 + k < npk ? k0 + k : 0);
+        v[k] = src[idx * IS];
+        ml[k] = *(const float2*)(stn + idx * 32);
+      }
+      float mb = M;
+#pragma unroll
+      for (int k = 0; k < 16; ++k)
+        if (k0 + k < npk && ml[k].y > 0.f) mb = fmaxf(mb, ml[k].x);
+      if (mb == -INFINITY) continue;
+      const float f = __builtin_amdgcn_exp2f(M - mb);  // 0 while M is -inf
+      sr *= f;
+      L *= f;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const float w = (k0 + k < npk && ml[k].y > 0.f) ? __builtin_amdgcn_exp2f(ml[k].x - mb) : 0.f;
+        sr += v[k] * w;
+        L += ml[k].y * w;
+      }
+      M = mb;
+    }
+    const float Mt = fmaxf(M, mlr.y > 0.f ? mlr.x : -INFINITY);
+    const float fp = L > 0.f ? __builtin_amdgcn_exp2f(M - Mt) : 0.f;
+    const float fr = mlr.y > 0.f ? __builtin_amdgcn_exp2f(mlr.x - Mt) : 0.f;
+    const float inv = 1.0f / (L * fp + mlr.y * fr);
+    sr *= fp * inv;
+    vr *= fr * inv;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int dim = (4 * ekq + i) * 16 + j;
+      s_rot[n * RP + dim] = f32_to_f16_bits(sr[i]);
+      s_res[n * TD + dim] = vr[i];
+    }
   }
   __syncthreads();
-  const int d = threadIdx.x;
-  // the residual item, when present, is the last of the range (anna_mi_tq_decode_plan)
-  const bool has_res = i1 > i0 && a.items[(int64_t)(i1 - 1) * 4 + 2] < 0;
-  const int ip = has_res ? i1 - 1 : i1;
-  const float* pv = a.partial_values + n * TD + d;
-  float ar = 0.f, aq = 0.f;
-  int it = i0;
-  for (; it + 4 <= ip; it += 4) {
-    const float v0 = pv[(int64_t)it * 16 * TD], v1 = pv[(int64_t)(it + 1) * 16 * TD];
-    const float v2 = pv[(int64_t)(it + 2) * 16 * TD], v3 = pv[(int64_t)(it + 3) * 16 * TD];
-    ar += v0 * s_w[it - i0] + v1 * s_w[it + 1 - i0] + v2 * s_w[it + 2 - i0] + v3 * s_w[it + 3 - i0];
-  }
-  for (; it < ip; ++it) ar += pv[(int64_t)it * 16 * TD] * s_w[it - i0];
-  if (has_res) aq = pv[(int64_t)(i1 - 1) * 16 * TD] * s_w[i1 - 1 - i0];
-  ((uint16_t*)a.query_rot)[bq * TD + d] = f32_to_f16_bits(ar);  // q' is no longer needed: reuse
-  ((float*)a.out_residual)[bq * TD + d] = aq;
-}
-
-// Phase 2, grid (ceil(B*Hq / 16), 16 output tiles), one wave: out = rot R + residual.
-__global__ __launch_bounds__(64) void tq_decode_unrotate_kernel(const anna_mi_tq_decode_args a) {
-  const int lane = threadIdx.x;
-  const int r = lane & 15, kq = lane >> 4;
-  const int64_t row0 = (int64_t)blockIdx.x * 16;
-  const int tile = blockIdx.y;
-  const int64_t rows = a.batch * a.q_heads;
-  const uint16_t* rot = (const uint16_t*)a.query_rot;
-  const uint16_t* RT = (const uint16_t*)a.rotation_t_f16;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  // out = rot R + res: wave takes output dims [32 wave, 32 wave + 32); A = rot (16 heads x 32),
+  // B[k][d] = R[k][d] = R^T[d][k]; C lane: dim col r, heads 4 kq + i
 #pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    u32x4 af = {0u, 0u, 0u, 0u};
-    if (row0 + r < rows) af = *(const u32x4*)(rot + (row0 + r) * TD + s * 32 + kq * 8);
-    const u32x4 bfr = *(const u32x4*)(RT + (int64_t)(tile * 16 + r) * TD + s * 32 + kq * 8);
-    acc = mfma_f16(af, bfr, acc);
-  }
+  for (int tt = 0; tt < 2; ++tt) {
+    const int tile = 2 * wave + tt;
+    f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t row = row0 + 4 * kq + i;
-    const int dd = tile * 16 + r;
-    if (row < rows) ((uint16_t*)a.out)[row * TD + dd] = f32_to_bf16_bits(acc[i] + ((const float*)a.out_residual)[row * TD + dd]);
+    for (int st = 0; st < 8; ++st) {
+      const u32x4 af = *(const u32x4*)(s_rot + r * RP + st * 32 + kq * 8);
+      c = mfma_f16(af, bfr[tt][st], c);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int n = 4 * kq + i, d = tile * 16 + r;
+      if (n < G) a.out[(b * a.q_heads + h * G + n) * TD + d] = f32_to_bf16_bits(c[i] + s_res[n * TD + d]);
+    }
   }
 }
 
@@ -414,31 +525,68 @@ using namespace anna;
 
 extern "C" int64_t anna_mi_sizeof_tq_decode_args(void) { return (int64_t)sizeof(anna_mi_tq_decode_args); }
 
+// Blocks of 32 tokens per item for `slots` concurrent workgroups: the smallest multiple of 8
+// blocks (one per wave and pass) for which the items of every (b, kv-head) fit.
+static int64_t auto_blocks_per_item(int64_t batch, int64_t kv_heads, const int64_t* qlens, const int64_t* rlens) {
+  constexpr int64_t SLOTS = 256;  // MI355X compute units: one 512-thread workgroup each
+  int64_t total = 0, resid = 0;
+  for (int64_t b = 0; b < batch; ++b) {
+    total += (qlens[b] + TBT - 1) / TBT;
+    resid += rlens[b] > 0;
+  }
+  total *= kv_heads;
+  resid *= kv_heads;
+  const int64_t slots = SLOTS - resid > kv_heads * batch ? SLOTS - resid : kv_heads * batch;
+  int64_t bpi = ((total + slots - 1) / slots + SWAVES - 1) / SWAVES * SWAVES;
+  if (bpi < SWAVES) bpi = SWAVES;
+  for (;; bpi += SWAVES) {
+    int64_t n = 0;
+    for (int64_t b = 0; b < batch; ++b) n += ((qlens[b] + TBT - 1) / TBT + bpi - 1) / bpi;
+    if (n * kv_heads <= slots) return bpi;
+  }
+}
+
 extern "C" int anna_mi_tq_decode_plan(int64_t batch, int64_t kv_heads, const int64_t* quantized_lens,
-                                      const int64_t* residual_lens, int64_t tokens_per_item, int32_t* items,
-                                      int64_t items_capacity, int32_t* item_ranges, int64_t* num_items) {
-  ANNA_CHECK(items && item_ranges && num_items && quantized_lens && residual_lens, "anna_mi_tq_decode_plan: null pointer");
-  ANNA_CHECK(tokens_per_item > 0 && tokens_per_item % TBT == 0, "tokens_per_item must be a positive multiple of 32");
+                                      const int64_t* residual_lens, const int64_t* seq_offsets,
+                                      int64_t tokens_per_item, int32_t* items, int64_t items_capacity,
+                                      int32_t* bh_items, int64_t* num_items) {
+  ANNA_CHECK(items && bh_items && num_items && quantized_lens && residual_lens && seq_offsets,
+             "anna_mi_tq_decode_plan: null pointer");
+  ANNA_CHECK(tokens_per_item >= 0 && tokens_per_item % TBT == 0,
+             "tokens_per_item must be 0 (automatic) or a positive multiple of 32");
+  for (int64_t b = 0; b < batch; ++b) {
+    ANNA_CHECK(quantized_lens[b] >= 0 && residual_lens[b] >= 0, "anna_mi_tq_decode_plan: negative length");
+    ANNA_CHECK(quantized_lens[b] + residual_lens[b] > 0, "anna_mi_tq_decode_plan: a sequence has no tokens");
+    ANNA_CHECK(seq_offsets[b] % TBT == 0, "anna_mi_tq_decode_plan: sequence offsets must be multiples of 32");
+    ANNA_CHECK(seq_offsets[b] + quantized_lens[b] < ((int64_t)1 << 31), "anna_mi_tq_decode_plan: pool slot exceeds int32");
+  }
+  const int64_t bpi = tokens_per_item > 0 ? tokens_per_item / TBT
+                                          : auto_blocks_per_item(batch, kv_heads, quantized_lens, residual_lens);
   int64_t n = 0;
   for (int64_t b = 0; b < batch; ++b)
     for (int64_t h = 0; h < kv_heads; ++h) {
-      item_ranges[b * kv_heads + h] = (int32_t)n;
-      for (int64_t t = 0; t < quantized_lens[b]; t += tokens_per_item) {
+      int32_t* info = bh_items + (b * kv_heads + h) * 4;
+      info[0] = (int32_t)n, info[2] = -1, info[3] = 0;
+      const int64_t q = quantized_lens[b], nb = (q + TBT - 1) / TBT;
+      const int64_t k = (nb + bpi - 1) / bpi;  // items, with the blocks spread evenly over them
+      for (int64_t i = 0; i < k; ++i) {
         ANNA_CHECK(n < items_capacity, "anna_mi_tq_decode_plan: items capacity too small");
-        const int64_t e = t + tokens_per_item < quantized_lens[b] ? t + tokens_per_item : quantized_lens[b];
+        const int64_t b0 = nb * i / k, b1 = nb * (i + 1) / k;
+        const int64_t t1 = b1 * TBT < q ? b1 * TBT : q;
         int32_t* it = items + n * 4;
-        it[0] = (int32_t)b, it[1] = (int32_t)h, it[2] = (int32_t)t, it[3] = (int32_t)e;
+        it[0] = (int32_t)b, it[1] = (int32_t)h;
+        it[2] = (int32_t)(seq_offsets[b] + b0 * TBT), it[3] = (int32_t)(seq_offsets[b] + t1);
         ++n;
       }
+      info[1] = (int32_t)k;
       if (residual_lens[b] > 0) {
         ANNA_CHECK(n < items_capacity, "anna_mi_tq_decode_plan: items capacity too small");
+        info[2] = (int32_t)n;
         int32_t* it = items + n * 4;
-        it[0] = (int32_t)b, it[1] = (int32_t)h, it[2] = -1, it[3] = -1;
+        it[0] = (int32_t)b, it[1] = (int32_t)h, it[2] = -1, it[3] = (int32_t)residual_lens[b];
         ++n;
       }
-      ANNA_CHECK(n - item_ranges[b * kv_heads + h] <= 64, "more than 64 work items for one sequence: raise tokens_per_item");
     }
-  item_ranges[batch * kv_heads] = (int32_t)n;
   *num_items = n;
   return ANNA_MI_OK;
 }
@@ -451,8 +599,7 @@ extern "C" int anna_mi_tq_decode(const anna_mi_tq_decode_args* ap, void* stream)
   ANNA_CHECK(a.kv_heads > 0 && a.q_heads % a.kv_heads == 0 && a.q_heads / a.kv_heads <= 16,
              "anna_mi_tq_decode: need q_heads = G * kv_heads with G <= 16");
   ANNA_CHECK(a.pool_tokens % TBT == 0 && a.residual_capacity % TBT == 0, "pool and residual capacity must be multiples of 32");
-  ANNA_CHECK(a.query && a.out && a.out_residual && a.query_rot && a.partial_stats && a.partial_values && a.items &&
-             a.item_ranges,
+  ANNA_CHECK(a.query && a.out && a.query_frag && a.partial_stats && a.partial_values && a.items && a.bh_items,
              "anna_mi_tq_decode: null pointer");
   ANNA_CHECK(a.rotation_f16 && a.rotation_t_f16 && a.key_codes && a.key_norms && a.value_codes && a.value_norms,
              "anna_mi_tq_decode: null cache pointer");
@@ -462,10 +609,8 @@ extern "C" int anna_mi_tq_decode(const anna_mi_tq_decode_args* ap, void* stream)
   ANNA_LAUNCH_CHECK("tq_rotate_query_kernel");
   hipLaunchKernelGGL(tq_decode_split_kernel, dim3((unsigned)a.num_items), dim3(64 * SWAVES), 0, st, a);
   ANNA_LAUNCH_CHECK("tq_decode_split_kernel");
-  hipLaunchKernelGGL(tq_decode_combine_kernel, dim3((unsigned)(a.batch * a.q_heads)), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(tq_decode_combine_kernel, dim3((unsigned)(a.batch * a.kv_heads)), dim3(64 * SWAVES), 0, st, a);
   ANNA_LAUNCH_CHECK("tq_decode_combine_kernel");
-  hipLaunchKernelGGL(tq_decode_unrotate_kernel, dim3((unsigned)((a.batch * a.q_heads + 15) / 16), 16), dim3(64), 0, st, a);
-  ANNA_LAUNCH_CHECK("tq_decode_unrotate_kernel");
   return ANNA_MI_OK;
 }
 

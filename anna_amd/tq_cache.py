@@ -28,7 +28,7 @@ def _round32(n: int) -> int:
 
 class TurboQuantBatchCache:
     def __init__(self, *, batch: int, kv_heads: int, q_heads: int, capacities, residual_capacity: int = 128,
-                 head_dim: int = 256, bits: int = 2, device="cuda", tokens_per_item: int = 512):
+                 head_dim: int = 256, bits: int = 2, device="cuda", tokens_per_item: int = 0):
         if head_dim != 256 or bits != 2:
             raise ValueError("TurboQuantBatchCache supports head_dim 256 with 2-bit codes")
         self.batch, self.kv_heads, self.q_heads, self.head_dim, self.bits = batch, kv_heads, q_heads, head_dim, bits
@@ -52,7 +52,6 @@ class TurboQuantBatchCache:
         self.residual_value_t = torch.zeros((batch, kv_heads, D, R), dtype=torch.bfloat16, device=dev)
         self.quantized_lens = [0] * batch
         self.residual_lens = [0] * batch
-        self.seq_offsets = torch.tensor(offs, dtype=torch.int64, device=dev)
         self.qn = get_turboquant_quantizer(head_dim=D, bits=bits, device=dev)
         self.rotation_f16 = self.qn.rotation.to(torch.float16)
         self.rotation_t_f16 = self.qn.rotation_t.to(torch.float16)
@@ -91,23 +90,25 @@ class TurboQuantBatchCache:
     # ---- decode
     def _make_plan(self):
         B, H = self.batch, self.kv_heads
-        cap = sum(-(-q // self.tokens_per_item) for q in self.quantized_lens) * H + B * H + 1
+        if self.tokens_per_item > 0:
+            cap = sum(-(-q // self.tokens_per_item) for q in self.quantized_lens) * H + B * H + 1
+        else:
+            cap = max(256, B * H) + B * H + 1
         items = torch.empty((cap, 4), dtype=torch.int32)
-        ranges = torch.empty((B * H + 1,), dtype=torch.int32)
+        ranges = torch.empty((B * H, 4), dtype=torch.int32)
         ql = torch.tensor(self.quantized_lens, dtype=torch.int64)
         rl = torch.tensor(self.residual_lens, dtype=torch.int64)
+        so = torch.tensor(self.offsets, dtype=torch.int64)
         n = ctypes.c_int64(0)
-        _lib.call("anna_mi_tq_decode_plan", B, H, ql.data_ptr(), rl.data_ptr(), self.tokens_per_item,
+        _lib.call("anna_mi_tq_decode_plan", B, H, ql.data_ptr(), rl.data_ptr(), so.data_ptr(), self.tokens_per_item,
                   items.data_ptr(), cap, ranges.data_ptr(), ctypes.addressof(n))
         n = n.value
         dev = self.device
         self._plan = dict(
             items=items[:n].to(dev), ranges=ranges.to(dev), n=n,
-            rlens=torch.tensor(self.residual_lens, dtype=torch.int32, device=dev),
             ps=torch.empty((max(n, 1), 16, 2), dtype=torch.float32, device=dev),
             pv=torch.empty((max(n, 1), 16, self.head_dim), dtype=torch.float32, device=dev),
-            qrot=torch.empty((self.batch, self.q_heads, self.head_dim), dtype=torch.float16, device=dev),
-            ores=torch.empty((self.batch, self.q_heads, self.head_dim), dtype=torch.float32, device=dev),
+            qf=torch.empty((B, H, 4096), dtype=torch.float16, device=dev),
         )
         return self._plan
 
@@ -120,15 +121,13 @@ class TurboQuantBatchCache:
         a.key_codes, a.key_norms = self.key_codes.data_ptr(), self.key_norms.data_ptr()
         a.value_codes, a.value_norms = self.value_codes.data_ptr(), self.value_norms.data_ptr()
         a.pool_tokens = self.pool_tokens
-        a.seq_offsets = self.seq_offsets.data_ptr()
         a.residual_key, a.residual_value_t = self.residual_key.data_ptr(), self.residual_value_t.data_ptr()
-        a.residual_lens = p["rlens"].data_ptr()
         a.residual_capacity = self.residual_capacity
         a.rotation_f16, a.rotation_t_f16 = self.rotation_f16.data_ptr(), self.rotation_t_f16.data_ptr()
         a.key_scale, a.value_scale, a.scaling = self.key_scale, self.value_scale, float(scaling)
-        a.items, a.num_items, a.item_ranges = p["items"].data_ptr(), p["n"], p["ranges"].data_ptr()
-        a.query_rot, a.partial_stats, a.partial_values = p["qrot"].data_ptr(), p["ps"].data_ptr(), p["pv"].data_ptr()
-        a.out_residual = p["ores"].data_ptr()
+        a.items, a.num_items, a.bh_items = p["items"].data_ptr(), p["n"], p["ranges"].data_ptr()
+        a.query_frag = p["qf"].data_ptr()
+        a.partial_stats, a.partial_values = p["ps"].data_ptr(), p["pv"].data_ptr()
         a.out = out.data_ptr()
         return a
 

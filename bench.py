@@ -280,7 +280,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=60)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--sections", default="int4,tq_decode,tq_pack")
-    ap.add_argument("--tq-tokens-per-item", type=int, default=512)
+    ap.add_argument("--tq-tokens-per-item", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--int4-points", default="", help="comma list of MxNxK (default: the BASELINE sweep)")

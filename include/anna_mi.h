@@ -197,8 +197,7 @@ int anna_mi_gqa_decode_splitkv(const anna_mi_decode_args* args, void* stream);
  * (head_dim 256): the batched replacement of the per-row loop of
  * Qwen3DynamicCache.turboquant_single_token_decode_attention (src/anna/model/ops.py:1024-1072)
  * over TurboQuantKVRow.decode_attention (turboquant.py:1181-1346).  Layout of the cache:
- * see tq_decode.hip.  Work items (b, kv_head, t0, t1) come from anna_mi_tq_decode_plan;
- * a residual item has t0 = t1 = -1. */
+ * see tq_decode.hip.  Work items come from anna_mi_tq_decode_plan. */
 typedef struct {
   int64_t batch, q_heads, kv_heads, head_dim;
   int key_bits, value_bits;
@@ -208,36 +207,38 @@ typedef struct {
   const uint8_t* value_codes;       /* [Hkv][pool/32][32*D/4] blocked */
   const uint16_t* value_norms;      /* fp16 [Hkv][pool] */
   int64_t pool_tokens;
-  const int64_t* seq_offsets;       /* [B] device, multiples of 32 */
   const uint16_t* residual_key;     /* bf16 [B][Hkv][R][D] */
   const uint16_t* residual_value_t; /* bf16 [B][Hkv][D][R] */
-  const int32_t* residual_lens;     /* [B] device */
   int64_t residual_capacity;        /* R, multiple of 32 */
   const uint16_t* rotation_f16;     /* R as fp16 [D][D] */
   const uint16_t* rotation_t_f16;   /* R^T as fp16 [D][D] */
   float key_scale, value_scale;     /* centroid c = key_scale * fp16 LUT value */
   float scaling;
-  const int32_t* items;             /* [num_items][4] device */
+  const int32_t* items;             /* [num_items][4] device, from anna_mi_tq_decode_plan */
   int64_t num_items;
-  const int32_t* item_ranges;       /* [B*Hkv + 1] device */
-  uint16_t* query_rot;              /* workspace fp16 [B][Hq][D] (q', then the rotated sum) */
+  const int32_t* bh_items;          /* [B*Hkv][4] device: first item, packed items, residual item or -1, 0 */
+  uint16_t* query_frag;             /* workspace fp16 [B][Hkv][4096]: q' = R q as MFMA fragments */
   float* partial_stats;             /* workspace [num_items][16][2] */
   float* partial_values;            /* workspace [num_items][16][D] */
-  float* out_residual;              /* workspace [B][Hq][D] */
   uint16_t* out;                    /* bf16 [B][Hq][D] */
 } anna_mi_tq_decode_args;
 
-/* Host: split each sequence's quantized prefix into items of tokens_per_item tokens (a
- * multiple of 32), one residual item per (b, kv_head) with a residual, ordered by
- * (b, kv_head); item_ranges[b*Hkv + h] .. [+1] delimit the items of (b, h). */
+/* Host: split each sequence's quantized prefix (pool slots seq_offsets[b] ..
+ * + quantized_lens[b]) into work items (b, kv_head, first slot, end slot) of about
+ * tokens_per_item tokens (a multiple of 32; 0 = sized so that all items run at once on the
+ * GPU), and add one item (b, kv_head, -1, residual length) per (b, kv_head) with a residual.
+ * The packed items of (b, h) are consecutive; bh_items[b*Hkv + h] = {first item, number of
+ * packed items, residual item or -1, 0}. */
 int anna_mi_tq_decode_plan(int64_t batch, int64_t kv_heads, const int64_t* quantized_lens_host,
-                           const int64_t* residual_lens_host, int64_t tokens_per_item, int32_t* items_host,
-                           int64_t items_capacity, int32_t* item_ranges_host, int64_t* num_items);
+                           const int64_t* residual_lens_host, const int64_t* seq_offsets_host,
+                           int64_t tokens_per_item, int32_t* items_host, int64_t items_capacity,
+                           int32_t* bh_items_host, int64_t* num_items);
 
 /* sizeof(anna_mi_tq_decode_args), for binding checks. */
 int64_t anna_mi_sizeof_tq_decode_args(void);
 
-/* Four launches: q' = R q, split (per item), combine (per b, q-head), un-rotation. */
+/* Three launches: q' = R q, the split over work items, the combine.  Calls that share
+ * workspaces must not overlap. */
 int anna_mi_tq_decode(const anna_mi_tq_decode_args* args, void* stream);
 
 /* Reorders natural 2-bit codes [tokens][64] (D = 256) of one KV head into the blocked

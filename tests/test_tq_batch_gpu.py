@@ -32,7 +32,7 @@ def unblock(blocked: np.ndarray, tokens: int) -> np.ndarray:
     return out
 
 
-@pytest.mark.parametrize("tokens_per_item", [64, 512])
+@pytest.mark.parametrize("tokens_per_item", [0, 64, 512])
 def test_batched_decode_matches_oracle(gpu, tokens_per_item):
     torch.manual_seed(60)
     hkv, g, d = 2, 8, 256
