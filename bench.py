@@ -30,6 +30,7 @@ import torch  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 ROTATE_BYTES = 600 * 2**20  # distinct buffers per timed region (> 2 x 256 MB Infinity Cache)
+COPY_BYTES = 256 * 2**20
 METRIC = "int4 GEMV/GEMM GB/s & TFLOPs (% roofline); TQ-KV decode attn tokens/s"
 
 
@@ -47,9 +48,26 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
+EAGER = False  # --eager: launch the steps directly (for counter collection runs)
+
+
 def time_graph(fns, steps: int, warmup: int) -> float:
-    """Capture `steps` calls (fns[i % len(fns)]) into one HIP graph; return ms per step."""
+    """Capture `steps` calls (fns[i % len(fns)]) into one HIP graph; return ms per step.
+    With --eager the steps are launched one by one on the same stream instead."""
     stream = torch.cuda.Stream()
+    if EAGER:
+        with torch.cuda.stream(stream):
+            for i in range(warmup):
+                fns[i % len(fns)]()
+            torch.cuda.synchronize()
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            for i in range(steps):
+                fns[i % len(fns)]()
+            end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / steps
     torch.cuda.synchronize()
     with torch.cuda.stream(stream):
         for f in fns[: min(len(fns), 3)]:  # eager warm-up (loads code objects)
@@ -274,6 +292,34 @@ def _lib_call_mse(fused_ops, xs, qn, codes, norms):
                         codes.data_ptr(), norms.data_ptr(), fused_ops._lib.stream_of(xs))
 
 
+def calibrate_copy(device, steps: int = 5) -> dict:
+    """A plain elementwise kernel of known traffic (reads and writes COPY_BYTES each), run so
+    that a counter collection run can scale FETCH_SIZE / WRITE_SIZE to bytes."""
+    n = COPY_BYTES // 4
+    src = torch.randn(n, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    log(f"calibration copy: {steps} x torch.neg over {COPY_BYTES} bytes (fp32)")
+    return {"kernel": "torch.neg fp32 elementwise", "read_bytes": COPY_BYTES, "write_bytes": COPY_BYTES, "calls": steps}
+
+
+TRAFFIC_FILE = ROOT / "profiles" / "int4_gemv_dot2_m1_n12288_k4096_traffic.txt"
+
+
+def measured_traffic():
+    """HBM bytes per launch of the headline kernel from the committed counter summary
+    (FETCH_SIZE + WRITE_SIZE, scaled by the calibration copy); None if absent."""
+    try:
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -284,7 +330,11 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--int4-points", default="", help="comma list of MxNxK (default: the BASELINE sweep)")
+    ap.add_argument("--eager", action="store_true", help="launch steps one by one (counter collection runs)")
+    ap.add_argument("--calibrate-copy", action="store_true", help="also run a known-size copy kernel")
     args = ap.parse_args()
+    global EAGER
+    EAGER = args.eager
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(the sharding plan is described in DESIGN.md); run with --gpus 1.", file=sys.stderr)
@@ -297,6 +347,8 @@ def main() -> int:
 
     fused_ops.register_ops()
     sections = {}
+    if args.calibrate_copy:
+        sections["calibration_copy"] = calibrate_copy(device)
     wanted = set(args.sections.split(","))
     if "int4" in wanted:
         sections["int4_sweep"] = section_int4(args, device)
@@ -324,12 +376,13 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "int4xbf16 (int4 weights, bf16 activations, fp32 accumulation)",
         "data": "synthetic (seeded codes U{0..15}, bf16 scales |N(0,0.02)|+1e-3, zero points U{0..15}, x ~N(0,1))",
         "config": {"workload": "W4A16 int4 GEMV, M=1 N=12288 K=4096 group=128 (BASELINE config 2, fused gate_up)",
                    "M": 1, "N": 12288, "K": 4096, "group_size": 128, "scale_dtype": "bf16"},
         "roofline": {"bound": "hbm", "achieved": round(head["GB/s"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(head["GB/s"] / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(head["GB/s"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "bytes_per_launch": head["bytes"], "kernel": "int4_gemv_dot2"},
         "cpu_baseline": cpu,
         "sections": sections,
     }
