@@ -78,8 +78,33 @@ PROTOTYPES.update({
     "anna_mi_tq_values_dequant": [_P, _P, _P, _I, _I64, _I64, _I, _I64, _P, _I, _P],
     "anna_mi_gqa_decode_splitkv": [ctypes.POINTER(DecodeArgs), _P],
 })
+
+
+class MoeMlpArgs(ctypes.Structure):
+    """anna_mi_moe_mlp_args."""
+
+    _fields_ = [
+        ("dtype", _I), ("scale_dtype", _I), ("routes", _I64), ("hidden_dim", _I64), ("intermediate_dim", _I64),
+        ("compact_hidden", _P), ("compact_weights", _P), ("compact_outputs", _P), ("expert_offsets", _P),
+        ("active_experts", _P), ("active_slots", _P), ("active_count", _I64),
+        ("gate_qweight", _P), ("gate_qscale", _P), ("gate_qzeros", _P),
+        ("up_qweight", _P), ("up_qscale", _P), ("up_qzeros", _P),
+        ("down_qweight", _P), ("down_qscale", _P), ("down_qzeros", _P),
+        ("hidden_packed_cols", _I64), ("hidden_groups", _I64), ("intermediate_packed_cols", _I64),
+        ("intermediate_groups", _I64), ("group_size", _I64), ("activation", _P),
+    ]
+
+
+PROTOTYPES.update({
+    "anna_mi_moe_router": [_P, _I, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _P],
+    "anna_mi_moe_dispatch": [_P, _I, _I64, _I64, _I64, _P, _P, _P, _I, _I64, _I64, _P, _P, _P, _P, _P, _P, _P],
+    "anna_mi_moe_scatter": [_P, _I, _I64, _I64, _P, _I64, _P, _P, _P],
+    "anna_mi_moe_combine": [_P, _I, _I64, _P, _I64, _I64, _P, _P],
+    "anna_mi_moe_grouped_int4_mlp": [ctypes.POINTER(MoeMlpArgs), _P],
+})
 # entry points that do not return a status code
 RAW_PROTOTYPES: dict[str, tuple] = {
+    "anna_mi_sizeof_moe_mlp_args": (_I64, []),
     "anna_mi_decode_num_blocks": (_I64, [ctypes.POINTER(DecodeArgs)]),
     "anna_mi_sizeof_decode_args": (_I64, []),
     "anna_mi_sizeof_tq_decode_args": (_I64, []),

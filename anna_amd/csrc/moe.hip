@@ -1,0 +1,488 @@
+// Mixture-of-experts routing and grouped int4 expert MLP on gfx950.
+//
+//   moe_router_kernel     one wave per token: fp32 softmax over the experts, top-k by repeated
+//                         wave arg-max (ties go to the lower expert index, the order of the
+//                         reference's insertion sort), optional renormalisation, usage counts.
+//   moe_order_kernel      one workgroup per expert: expert offsets (prefix sum of usage) and
+//                         the compact route order sorted by (expert, token, k) -- the order
+//                         of the reference's CPU path -- by a ballot prefix scan over the
+//                         routes in token-major order.  Deterministic (no atomics).
+//   moe_gather_kernel     compact_hidden[p] = hidden[sorted_token_idx[p]].
+//   moe_int4_mlp_kernel   grouped W4A16 expert MLP.  grid (64-row output tiles, active
+//                         experts); each workgroup takes the routes of its expert 16 at a
+//                         time (staged in LDS as the MFMA A operand) against 4 waves x 16 rows
+//                         of int4 weights turned into bf16/f16 "off + q" fragments in registers
+//                         (v_mfma_f32_16x16x32).  Pass 1 (gate, up): act = silu(x Wg^T) * (x Wu^T)
+//                         in fp32; pass 2 (down): out = (act Wd^T) * routing weight.  Experts
+//                         without routes exit at once, so every expert of the bank can be passed
+//                         as active without a host synchronisation.
+//   moe_scatter_*         out[t] = sum of the compact rows of token t (fp32 atomics, the
+//                         reference op); moe_combine_kernel does the same as a deterministic
+//                         gather through the route positions written by the dispatch.
+#include <algorithm>
+
+#include "common.hpp"
+#include "int4_frag.hpp"
+
+namespace anna {
+namespace {
+
+// ------------------------------------------------------------------ router
+
+// One wave per token; lane l holds experts l, l + 64, ...
+template <int LDT>
+__global__ __launch_bounds__(256) void moe_router_kernel(const typename Elem<LDT>::T* __restrict__ logits,
+                                                         int64_t T, int64_t E, int64_t ls, int64_t top_k, int normalize,
+                                                         float* __restrict__ weights, int64_t* __restrict__ selected,
+                                                         int32_t* __restrict__ usage) {
+  constexpr int MAXV = 16;  // experts per lane (E <= 1024)
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  float v[MAXV];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) {
+    const int64_t e = lane + 64 * i;
+    v[i] = e < E ? Elem<LDT>::load(logits, t * ls + e) : -INFINITY;
+    mx = fmaxf(mx, v[i]);
+  }
+  mx = wave_max(mx);
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) {
+    const int64_t e = lane + 64 * i;
+    v[i] = e < E ? expf(v[i] - mx) : 0.f;
+    s += v[i];
+  }
+  const float inv = 1.0f / wave_sum(s);
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) v[i] = lane + 64 * i < E ? v[i] * inv : -1.0f;  // -1: not a candidate
+  float top_sum = 0.f;
+  float mine = 0.f;  // lane j < top_k keeps route j's probability
+  int64_t mine_e = 0;
+  for (int64_t j = 0; j < top_k; ++j) {
+    float bv = -2.0f;
+    int be = 0x7FFFFFFF;
+#pragma unroll
+    for (int i = 0; i < MAXV; ++i)
+      if (v[i] > bv) bv = v[i], be = lane + 64 * i;  // strict: lowest index among equals in this lane
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, 64);
+      const int oe = __shfl_xor(be, off, 64);
+      if (ov > bv || (ov == bv && oe < be)) bv = ov, be = oe;
+    }
+    top_sum += bv;
+    if (lane == (int)j) mine = bv, mine_e = be;
+#pragma unroll
+    for (int i = 0; i < MAXV; ++i)
+      if (lane + 64 * i == be) v[i] = -1.0f;
+  }
+  const float scale = normalize && top_sum > 0.f ? 1.0f / top_sum : 1.0f;
+  if (lane < top_k) {
+    weights[t * top_k + lane] = mine * scale;
+    selected[t * top_k + lane] = mine_e;
+    atomicAdd(usage + mine_e, 1);
+  }
+}
+
+__global__ void fill_i32_kernel(int32_t* p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+// ------------------------------------------------------------------ dispatch
+
+template <typename U>
+__global__ __launch_bounds__(256) void moe_order_kernel(const int64_t* __restrict__ selected, int64_t routes,
+                                                        int64_t top_k, const U* __restrict__ usage, int64_t E,
+                                                        int64_t* __restrict__ offsets, int64_t* __restrict__ sorted_token,
+                                                        int64_t* __restrict__ sorted_route, int64_t* __restrict__ route_pos) {
+  __shared__ int64_t s_part[4];
+  __shared__ int s_cnt[4];
+  const int64_t e = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int64_t part = 0;
+  for (int64_t i = threadIdx.x; i < e; i += blockDim.x) part += (int64_t)usage[i];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off, 64);
+  if (lane == 0) s_part[wave] = part;
+  __syncthreads();
+  const int64_t base = s_part[0] + s_part[1] + s_part[2] + s_part[3];
+  const int64_t cnt = (int64_t)usage[e];
+  if (threadIdx.x == 0) {
+    offsets[e + 1] = base + cnt;
+    if (e == 0) offsets[0] = 0;
+  }
+  if (cnt == 0) return;
+  int64_t running = 0;
+  for (int64_t c = 0; c < routes; c += blockDim.x) {
+    const int64_t route = c + threadIdx.x;
+    const bool match = route < routes && selected[route] == e;
+    const uint64_t bal = __ballot(match);
+    const int below = __popcll(bal & ((1ull << lane) - 1ull));
+    __syncthreads();  // s_cnt of the previous chunk has been read
+    if (lane == 0) s_cnt[wave] = __popcll(bal);
+    __syncthreads();
+    int before = 0;
+    for (int w = 0; w < wave; ++w) before += s_cnt[w];
+    if (match) {
+      const int64_t pos = base + running + before + below;
+      sorted_token[pos] = route / top_k;
+      sorted_route[pos] = route;
+      if (route_pos) route_pos[route] = pos;
+    }
+    running += s_cnt[0] + s_cnt[1] + s_cnt[2] + s_cnt[3];
+  }
+}
+
+// grid (routes), 64 threads x 16 B: compact row p = hidden row of its token; the compact
+// routing weight = routing_weights[route].
+template <int HDT>
+__global__ __launch_bounds__(64) void moe_gather_kernel(const typename Elem<HDT>::T* __restrict__ hidden, int64_t H,
+                                                        int64_t hs, const typename Elem<HDT>::T* __restrict__ rw,
+                                                        const int64_t* __restrict__ sorted_route, int64_t top_k,
+                                                        typename Elem<HDT>::T* __restrict__ compact,
+                                                        typename Elem<HDT>::T* __restrict__ compact_w) {
+  using T = typename Elem<HDT>::T;
+  constexpr int VEC = 16 / sizeof(T);
+  const int64_t p = blockIdx.x;
+  const int64_t route = sorted_route[p];
+  const int64_t t = route / top_k;
+  const T* src = hidden + t * hs;
+  T* dst = compact + p * H;
+  if ((H % VEC) == 0 && (hs % VEC) == 0) {
+    for (int64_t c = threadIdx.x; c < H / VEC; c += blockDim.x) ((u32x4*)dst)[c] = ((const u32x4*)src)[c];
+  } else {
+    for (int64_t c = threadIdx.x; c < H; c += blockDim.x) dst[c] = src[c];
+  }
+  if (threadIdx.x == 0) compact_w[p] = rw[route];
+}
+
+// ------------------------------------------------------------------ scatter / combine
+
+template <int HDT>
+__global__ void moe_scatter_add_kernel(const typename Elem<HDT>::T* __restrict__ compact, int64_t H,
+                                       const int64_t* __restrict__ sorted_token, float* __restrict__ acc) {
+  const int64_t p = blockIdx.x;
+  const int64_t t = sorted_token[p];
+  for (int64_t c = (int64_t)blockIdx.y * blockDim.x + threadIdx.x; c < H; c += (int64_t)gridDim.y * blockDim.x)
+    atomicAdd(acc + t * H + c, Elem<HDT>::load(compact, p * H + c));
+}
+
+template <int HDT>
+__global__ void moe_cast_kernel(const float* __restrict__ acc, int64_t n, typename Elem<HDT>::T* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = Elem<HDT>::cvt(acc[i]);
+}
+
+__global__ void fill_f32_kernel(float* p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.f;
+}
+
+// out[t] = sum_j compact[route_pos[t * top_k + j]], j ascending, fp32.
+template <int HDT>
+__global__ void moe_combine_kernel(const typename Elem<HDT>::T* __restrict__ compact, int64_t H,
+                                   const int64_t* __restrict__ route_pos, int64_t top_k,
+                                   typename Elem<HDT>::T* __restrict__ out) {
+  const int64_t t = blockIdx.x;
+  for (int64_t c = (int64_t)blockIdx.y * blockDim.x + threadIdx.x; c < H; c += (int64_t)gridDim.y * blockDim.x) {
+    float s = 0.f;
+    for (int64_t j = 0; j < top_k; ++j) s += Elem<HDT>::load(compact, route_pos[t * top_k + j] * H + c);
+    out[t * H + c] = Elem<HDT>::cvt(s);
+  }
+}
+
+// ------------------------------------------------------------------ grouped int4 MLP
+
+constexpr int MOE_ROWS = 64;   // output rows per workgroup (4 waves x 16)
+constexpr int MOE_CHUNK = 16;  // routes per pass (the MFMA M dimension)
+constexpr int MOE_PB = 8;      // 128-k blocks whose weights one wave loads ahead
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+
+// GU: pass 1 (gate and up, K = hidden, N = intermediate, act fp32 out);
+// otherwise pass 2 (down, K = intermediate, N = hidden, compact outputs in HDT).
+// MDT is the 16-bit MFMA type: f16 for f16 hidden states in pass 1, bf16 otherwise.
+// GPB: int4 groups per 128-k block (group size 128 / GPB; larger groups count as 1).
+template <int HDT, int SDT, bool GU, int GPB>
+__global__ __launch_bounds__(256) void moe_int4_mlp_kernel(const anna_mi_moe_mlp_args a) {
+  constexpr int MDT = (GU && HDT == ANNA_MI_F16) ? ANNA_MI_F16 : ANNA_MI_BF16;
+  constexpr float OFF = MDT == ANNA_MI_BF16 ? 128.0f : 1024.0f;
+  constexpr uint32_t ONES = MDT == ANNA_MI_BF16 ? 0x3F803F80u : 0x3C003C00u;
+  constexpr int NM = GU ? 2 : 1;  // weight matrices
+  using ST = typename Elem<SDT>::T;
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [16][K + 8]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, kq = lane >> 4;
+  const int64_t ai = blockIdx.y;
+  const int64_t e = a.active_experts[ai], slot = a.active_slots[ai];
+  const int64_t start = a.expert_offsets[e], end = a.expert_offsets[e + 1];
+  if (end <= start) return;
+  const int64_t N = GU ? a.intermediate_dim : a.hidden_dim;
+  const int64_t K = GU ? a.hidden_dim : a.intermediate_dim;
+  const int64_t pc = GU ? a.hidden_packed_cols : a.intermediate_packed_cols;
+  const int64_t G = GU ? a.hidden_groups : a.intermediate_groups;
+  const int64_t xp = K + 8;
+  const int64_t n = (int64_t)blockIdx.x * MOE_ROWS + wave * 16 + r;
+  const bool n_ok = n < N;
+  const int64_t nc = n_ok ? n : 0;
+  const uint32_t* wrow[NM];
+  const ST* sc[NM];
+  const int8_t* zp[NM];
+  if constexpr (GU) {
+    wrow[0] = (const uint32_t*)a.gate_qweight + (slot * N + nc) * pc + kq * 4;
+    wrow[1] = (const uint32_t*)a.up_qweight + (slot * N + nc) * pc + kq * 4;
+    sc[0] = (const ST*)a.gate_qscale + slot * G * N + nc;
+    sc[1] = (const ST*)a.up_qscale + slot * G * N + nc;
+    zp[0] = a.gate_qzeros + slot * G * N + nc;
+    zp[1] = a.up_qzeros + slot * G * N + nc;
+  } else {
+    wrow[0] = (const uint32_t*)a.down_qweight + (slot * N + nc) * pc + kq * 4;
+    sc[0] = (const ST*)a.down_qscale + slot * G * N + nc;
+    zp[0] = a.down_qzeros + slot * G * N + nc;
+  }
+  const int64_t nblk = K / 128;
+  const u32x4 ones = {ONES, ONES, ONES, ONES};
+
+  for (int64_t c0 = start; c0 < end; c0 += MOE_CHUNK) {
+    const int64_t cnt = end - c0 < MOE_CHUNK ? end - c0 : MOE_CHUNK;
+    // stage the chunk's activations as 16-bit MFMA rows (rows >= cnt are zero)
+    const int64_t cpr = K / 8;  // 8-element chunks per row
+    for (int64_t i = threadIdx.x; i < MOE_CHUNK * cpr; i += blockDim.x) {
+      const int64_t row = i / cpr, col = (i % cpr) * 8;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (row < cnt) {
+        if constexpr (GU && HDT != ANNA_MI_F32) {
+          v = *(const u32x4*)((const uint16_t*)a.compact_hidden + (c0 + row) * K + col);
+        } else {
+          const float* src = GU ? (const float*)a.compact_hidden + (c0 + row) * K + col
+                                : a.activation + (c0 + row) * K + col;
+          const float4 lo = *(const float4*)src, hi = *(const float4*)(src + 4);
+          v.x = (uint32_t)f32_to_bf16_bits(lo.x) | ((uint32_t)f32_to_bf16_bits(lo.y) << 16);
+          v.y = (uint32_t)f32_to_bf16_bits(lo.z) | ((uint32_t)f32_to_bf16_bits(lo.w) << 16);
+          v.z = (uint32_t)f32_to_bf16_bits(hi.x) | ((uint32_t)f32_to_bf16_bits(hi.y) << 16);
+          v.w = (uint32_t)f32_to_bf16_bits(hi.z) | ((uint32_t)f32_to_bf16_bits(hi.w) << 16);
+        }
+      }
+      *(u32x4*)(xs + row * xp + col) = v;
+    }
+    __syncthreads();
+
+    f32x4 out[NM];
+#pragma unroll
+    for (int m = 0; m < NM; ++m) out[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int64_t b0 = 0; b0 < nblk; b0 += MOE_PB) {
+      // every weight load of the pass first (clamped addresses, no branches around loads)
+      u32x4 wv[MOE_PB][NM];
+#pragma unroll
+      for (int j = 0; j < MOE_PB; ++j) {
+        const int64_t b = b0 + j < nblk ? b0 + j : nblk - 1;
+#pragma unroll
+        for (int m = 0; m < NM; ++m) wv[j][m] = __builtin_nontemporal_load((const u32x4*)(wrow[m] + b * 16));
+      }
+#pragma unroll
+      for (int j = 0; j < MOE_PB; ++j) {
+        const int64_t b = b0 + j;
+        if (b >= nblk) continue;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          // lanes kq hold k = 128 b + 32 kq + 8 s + e: a step spans the whole block, so each of
+          // its GPB groups gets its own MFMA with the other groups' lanes zeroed
+          const int64_t k = b * 128 + kq * 32 + s * 8;
+          const u32x4 xa = interleave_x(*(const u32x4*)(xs + r * xp + k));
+#pragma unroll
+          for (int q = 0; q < GPB; ++q) {
+            const u32x4 xm = (GPB == 1 || kq / (4 / GPB) == q) ? xa : u32x4{0u, 0u, 0u, 0u};
+            const int64_t g = b * GPB + q;
+            const f32x4 sx = mfma16<MDT>(xm, ones, f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+              const f32x4 acc = mfma16<MDT>(xm, nibbles_to_frag<MDT>(wv[j][m][s]), f32x4{0.f, 0.f, 0.f, 0.f});
+              const float scl = Elem<SDT>::to_f32(sc[m][g * N]);
+              const float c = OFF + (float)zp[m][g * N];
+#pragma unroll
+              for (int i = 0; i < 4; ++i) out[m][i] = fmaf(scl, acc[i] - c * sx[i], out[m][i]);
+            }
+          }
+        }
+      }
+    }
+    // C layout: lane holds routes c0 + 4 kq + i of output row n
+    if (n_ok) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t m = 4 * kq + i;
+        if (m >= cnt) continue;
+        const int64_t route = c0 + m;
+        if constexpr (GU) {
+          a.activation[route * N + n] = silu(out[0][i]) * out[1][i];
+        } else {
+          const float w = Elem<HDT>::load((const typename Elem<HDT>::T*)a.compact_weights, route);
+          ((typename Elem<HDT>::T*)a.compact_outputs)[route * N + n] = Elem<HDT>::cvt(out[0][i] * w);
+        }
+      }
+    }
+    __syncthreads();  // the next chunk overwrites xs
+  }
+}
+
+template <int HDT, int SDT, int GPB>
+int launch_moe_mlp(const anna_mi_moe_mlp_args& a, hipStream_t st, dim3 g1, dim3 g2, size_t l1, size_t l2) {
+  if (l1 > 65536)
+    ANNA_CHECK(hipFuncSetAttribute((const void*)moe_int4_mlp_kernel<HDT, SDT, true, GPB>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)l1) == hipSuccess,
+               "anna_mi_moe_grouped_int4_mlp: cannot raise the LDS limit");
+  if (l2 > 65536)
+    ANNA_CHECK(hipFuncSetAttribute((const void*)moe_int4_mlp_kernel<HDT, SDT, false, GPB>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)l2) == hipSuccess,
+               "anna_mi_moe_grouped_int4_mlp: cannot raise the LDS limit");
+  hipLaunchKernelGGL((moe_int4_mlp_kernel<HDT, SDT, true, GPB>), g1, dim3(256), l1, st, a);
+  ANNA_LAUNCH_CHECK("moe_int4_mlp_kernel (gate, up)");
+  hipLaunchKernelGGL((moe_int4_mlp_kernel<HDT, SDT, false, GPB>), g2, dim3(256), l2, st, a);
+  ANNA_LAUNCH_CHECK("moe_int4_mlp_kernel (down)");
+  return ANNA_MI_OK;
+}
+
+}  // namespace
+}  // namespace anna
+
+using namespace anna;
+
+extern "C" int anna_mi_moe_router(const void* logits, int logits_dtype, int64_t tokens, int64_t num_experts,
+                                  int64_t logits_row_stride, int64_t top_k, int normalize, float* weights,
+                                  int64_t* selected, int32_t* usage, void* stream) {
+  ANNA_CHECK(weights && selected && usage && (logits || tokens == 0), "anna_mi_moe_router: null pointer");
+  ANNA_CHECK(num_experts > 0 && num_experts <= 1024, "anna_mi_moe_router: num_experts must be in [1, 1024]");
+  ANNA_CHECK(top_k > 0 && top_k <= num_experts && top_k <= 64, "anna_mi_moe_router: need 0 < top_k <= min(num_experts, 64)");
+  ANNA_CHECK(tokens >= 0 && logits_row_stride >= num_experts, "anna_mi_moe_router: bad shape");
+  hipStream_t st = as_stream(stream);
+  hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)((num_experts + 255) / 256)), dim3(256), 0, st, usage, num_experts);
+  ANNA_LAUNCH_CHECK("fill_i32_kernel");
+  if (tokens == 0) return ANNA_MI_OK;
+  ANNA_DISPATCH_DTYPE(logits_dtype, LDT, {
+    hipLaunchKernelGGL((moe_router_kernel<LDT>), dim3((unsigned)((tokens + 3) / 4)), dim3(256), 0, st,
+                       (const typename Elem<LDT>::T*)logits, tokens, num_experts, logits_row_stride, top_k, normalize,
+                       weights, selected, usage);
+  });
+  ANNA_LAUNCH_CHECK("moe_router_kernel");
+  return ANNA_MI_OK;
+}
+
+extern "C" int anna_mi_moe_dispatch(const void* hidden, int dtype, int64_t tokens, int64_t hidden_dim,
+                                    int64_t hidden_row_stride, const void* routing_weights, const int64_t* selected,
+                                    const void* usage, int usage_is_int64, int64_t num_experts, int64_t top_k,
+                                    int64_t* sorted_token_idx, int64_t* sorted_route_idx, int64_t* expert_offsets,
+                                    void* compact_hidden, void* compact_weights, int64_t* route_pos, void* stream) {
+  ANNA_CHECK(selected && usage && sorted_token_idx && sorted_route_idx && expert_offsets && compact_hidden &&
+                 compact_weights && (hidden || tokens == 0) && (routing_weights || tokens == 0),
+             "anna_mi_moe_dispatch: null pointer");
+  ANNA_CHECK(num_experts > 0 && top_k > 0 && hidden_dim > 0 && tokens >= 0 && hidden_row_stride >= hidden_dim,
+             "anna_mi_moe_dispatch: bad shape");
+  hipStream_t st = as_stream(stream);
+  const int64_t routes = tokens * top_k;
+  if (usage_is_int64) {
+    hipLaunchKernelGGL((moe_order_kernel<int64_t>), dim3((unsigned)num_experts), dim3(256), 0, st, selected, routes,
+                       top_k, (const int64_t*)usage, num_experts, expert_offsets, sorted_token_idx, sorted_route_idx,
+                       route_pos);
+  } else {
+    hipLaunchKernelGGL((moe_order_kernel<int32_t>), dim3((unsigned)num_experts), dim3(256), 0, st, selected, routes,
+                       top_k, (const int32_t*)usage, num_experts, expert_offsets, sorted_token_idx, sorted_route_idx,
+                       route_pos);
+  }
+  ANNA_LAUNCH_CHECK("moe_order_kernel");
+  if (routes == 0) return ANNA_MI_OK;
+  ANNA_DISPATCH_DTYPE(dtype, HDT, {
+    using T = typename Elem<HDT>::T;
+    hipLaunchKernelGGL((moe_gather_kernel<HDT>), dim3((unsigned)routes), dim3(64), 0, st, (const T*)hidden, hidden_dim,
+                       hidden_row_stride, (const T*)routing_weights, sorted_route_idx, top_k, (T*)compact_hidden,
+                       (T*)compact_weights);
+  });
+  ANNA_LAUNCH_CHECK("moe_gather_kernel");
+  return ANNA_MI_OK;
+}
+
+extern "C" int anna_mi_moe_scatter(const void* compact_outputs, int dtype, int64_t routes, int64_t hidden_dim,
+                                   const int64_t* sorted_token_idx, int64_t num_tokens, float* accum, void* out,
+                                   void* stream) {
+  ANNA_CHECK(accum && out && (routes == 0 || (compact_outputs && sorted_token_idx)), "anna_mi_moe_scatter: null pointer");
+  ANNA_CHECK(hidden_dim > 0 && num_tokens >= 0 && routes >= 0, "anna_mi_moe_scatter: bad shape");
+  hipStream_t st = as_stream(stream);
+  const int64_t n = num_tokens * hidden_dim;
+  if (n == 0) return ANNA_MI_OK;
+  const unsigned nb = (unsigned)((n + 255) / 256);
+  hipLaunchKernelGGL(fill_f32_kernel, dim3(nb), dim3(256), 0, st, accum, n);
+  ANNA_LAUNCH_CHECK("fill_f32_kernel");
+  ANNA_DISPATCH_DTYPE(dtype, HDT, {
+    using T = typename Elem<HDT>::T;
+    if (routes > 0) {
+      hipLaunchKernelGGL((moe_scatter_add_kernel<HDT>), dim3((unsigned)routes, (unsigned)((hidden_dim + 255) / 256)),
+                         dim3(256), 0, st, (const T*)compact_outputs, hidden_dim, sorted_token_idx, accum);
+    }
+    hipLaunchKernelGGL((moe_cast_kernel<HDT>), dim3(nb), dim3(256), 0, st, accum, n, (T*)out);
+  });
+  ANNA_LAUNCH_CHECK("moe_scatter");
+  return ANNA_MI_OK;
+}
+
+extern "C" int anna_mi_moe_combine(const void* compact_outputs, int dtype, int64_t hidden_dim, const int64_t* route_pos,
+                                   int64_t num_tokens, int64_t top_k, void* out, void* stream) {
+  ANNA_CHECK(out && (num_tokens == 0 || (compact_outputs && route_pos)), "anna_mi_moe_combine: null pointer");
+  ANNA_CHECK(hidden_dim > 0 && num_tokens >= 0 && top_k > 0, "anna_mi_moe_combine: bad shape");
+  if (num_tokens == 0) return ANNA_MI_OK;
+  ANNA_DISPATCH_DTYPE(dtype, HDT, {
+    using T = typename Elem<HDT>::T;
+    hipLaunchKernelGGL((moe_combine_kernel<HDT>), dim3((unsigned)num_tokens, (unsigned)((hidden_dim + 255) / 256)),
+                       dim3(256), 0, as_stream(stream), (const T*)compact_outputs, hidden_dim, route_pos, top_k, (T*)out);
+  });
+  ANNA_LAUNCH_CHECK("moe_combine_kernel");
+  return ANNA_MI_OK;
+}
+
+extern "C" int64_t anna_mi_sizeof_moe_mlp_args(void) { return (int64_t)sizeof(anna_mi_moe_mlp_args); }
+
+extern "C" int anna_mi_moe_grouped_int4_mlp(const anna_mi_moe_mlp_args* ap, void* stream) {
+  ANNA_CHECK(ap != nullptr, "anna_mi_moe_grouped_int4_mlp: null args");
+  const anna_mi_moe_mlp_args& a = *ap;
+  ANNA_CHECK(valid_dtype(a.dtype) && valid_dtype(a.scale_dtype), "anna_mi_moe_grouped_int4_mlp: bad dtype code");
+  ANNA_CHECK(a.routes >= 0 && a.hidden_dim > 0 && a.intermediate_dim > 0 && a.active_count > 0,
+             "anna_mi_moe_grouped_int4_mlp: bad shape");
+  ANNA_CHECK(a.group_size > 0 && a.group_size % 32 == 0, "group_size must be a positive multiple of 32");
+  ANNA_CHECK(a.hidden_dim % 128 == 0 && a.intermediate_dim % 128 == 0,
+             "anna_mi_moe_grouped_int4_mlp: hidden_dim and intermediate_dim must be multiples of 128");
+  ANNA_CHECK(a.hidden_dim <= 4096 && a.intermediate_dim <= 4096,
+             "anna_mi_moe_grouped_int4_mlp: hidden_dim and intermediate_dim must be <= 4096");
+  ANNA_CHECK(a.hidden_packed_cols * 8 >= a.hidden_dim && a.intermediate_packed_cols * 8 >= a.intermediate_dim,
+             "anna_mi_moe_grouped_int4_mlp: packed width smaller than the input dimension");
+  ANNA_CHECK(a.hidden_groups * a.group_size >= a.hidden_dim && a.intermediate_groups * a.group_size >= a.intermediate_dim,
+             "anna_mi_moe_grouped_int4_mlp: group count too small");
+  ANNA_CHECK(a.compact_hidden && a.compact_weights && a.compact_outputs && a.expert_offsets && a.active_experts &&
+                 a.active_slots && a.activation && a.gate_qweight && a.gate_qscale && a.gate_qzeros && a.up_qweight &&
+                 a.up_qscale && a.up_qzeros && a.down_qweight && a.down_qscale && a.down_qzeros,
+             "anna_mi_moe_grouped_int4_mlp: null pointer");
+  if (a.routes == 0) return ANNA_MI_OK;
+  hipStream_t st = as_stream(stream);
+  const dim3 g1((unsigned)((a.intermediate_dim + MOE_ROWS - 1) / MOE_ROWS), (unsigned)a.active_count);
+  const dim3 g2((unsigned)((a.hidden_dim + MOE_ROWS - 1) / MOE_ROWS), (unsigned)a.active_count);
+  const size_t l1 = (size_t)MOE_CHUNK * (a.hidden_dim + 8) * 2, l2 = (size_t)MOE_CHUNK * (a.intermediate_dim + 8) * 2;
+  const int gpb = a.group_size >= 128 ? 1 : (int)(128 / a.group_size);
+  ANNA_CHECK(a.group_size % 128 == 0 || gpb * a.group_size == 128,
+             "anna_mi_moe_grouped_int4_mlp: group_size must be 32, 64 or a multiple of 128");
+  ANNA_DISPATCH_DTYPE(a.dtype, HDT, {
+    ANNA_DISPATCH_DTYPE(a.scale_dtype, SDT, {
+      if (gpb == 1) {
+        const int rc = launch_moe_mlp<HDT, SDT, 1>(a, st, g1, g2, l1, l2);
+        if (rc != ANNA_MI_OK) return rc;
+      } else if (gpb == 2) {
+        const int rc = launch_moe_mlp<HDT, SDT, 2>(a, st, g1, g2, l1, l2);
+        if (rc != ANNA_MI_OK) return rc;
+      } else {
+        const int rc = launch_moe_mlp<HDT, SDT, 4>(a, st, g1, g2, l1, l2);
+        if (rc != ANNA_MI_OK) return rc;
+      }
+    });
+  });
+  return ANNA_MI_OK;
+}

@@ -10,6 +10,7 @@ reference).
 
 from __future__ import annotations
 
+import ctypes
 import threading
 
 import torch
@@ -39,6 +40,19 @@ SCHEMAS = {
         "Tensor value_scales, Tensor value_zeros, Tensor residual_key, Tensor residual_value, Tensor(a!) output, "
         "Tensor(b!) partial_stats, Tensor(c!) partial_values, float scaling, int value_bits, int value_group_size, "
         "int block_size, Tensor? gate=None) -> Tensor(a!)"
+    ),
+    "moe_router_fused": "moe_router_fused(Tensor router_logits, int top_k, bool normalize_topk_prob=True) -> (Tensor, Tensor, Tensor)",
+    "moe_dispatch_fused": (
+        "moe_dispatch_fused(Tensor hidden_states, Tensor routing_weights, Tensor selected_experts, "
+        "Tensor expert_usage) -> (Tensor, Tensor, Tensor, Tensor)"
+    ),
+    "moe_scatter_fused": "moe_scatter_fused(Tensor compact_outputs, Tensor sorted_token_idx, int num_tokens) -> Tensor",
+    "moe_grouped_int4_mlp_fused": (
+        "moe_grouped_int4_mlp_fused(Tensor compact_hidden_states, Tensor compact_routing_weights, "
+        "Tensor(a!) compact_outputs, Tensor expert_offsets, Tensor active_experts, Tensor active_slots, "
+        "Tensor gate_qweight, Tensor gate_qscale, Tensor gate_qzeros, Tensor up_qweight, Tensor up_qscale, "
+        "Tensor up_qzeros, Tensor down_qweight, Tensor down_qscale, Tensor down_qzeros, int group_size, "
+        "int max_routes_per_expert) -> Tensor(a!)"
     ),
 }
 
@@ -435,6 +449,167 @@ def tq_values_dequant(data, scales, zeros, bits, group_size, out_dtype):
     return out
 
 
+
+# ---------------------------------------------------------------- MoE (sycl:3716-4324, ops.py:3280-3457)
+
+
+def _check_same_device(name, *tensors):
+    dev = tensors[0].device
+    _lib.require_device(tensors[0])
+    for t in tensors[1:]:
+        if t.device != dev:
+            raise RuntimeError(f"{name}: all tensors must be on {dev}")
+
+
+def moe_router(router_logits, top_k, normalize_topk_prob=True):
+    """softmax(fp32) -> top-k -> optional renorm -> usage; returns (weights fp32 [T,k],
+    selected int64 [T,k], usage int32 [E]) (moe_router_fused, sycl:3731-3839)."""
+    if router_logits.dim() != 2:
+        raise RuntimeError("router_logits must be [tokens, num_experts]")
+    t, e = router_logits.shape
+    if not (0 < top_k <= e):
+        raise RuntimeError("top_k must be in [1, num_experts]")
+    _lib.require_device(router_logits)
+    logits = router_logits if router_logits.stride(1) == 1 else router_logits.contiguous()
+    w = torch.empty((t, top_k), dtype=torch.float32, device=logits.device)
+    sel = torch.empty((t, top_k), dtype=torch.int64, device=logits.device)
+    usage = torch.empty((e,), dtype=torch.int32, device=logits.device)
+    _lib.call("anna_mi_moe_router", logits.data_ptr(), _lib.dtype_code(logits.dtype), t, e, logits.stride(0),
+              int(top_k), int(bool(normalize_topk_prob)), w.data_ptr(), sel.data_ptr(), usage.data_ptr(),
+              _lib.stream_of(logits))
+    return w, sel, usage
+
+
+def moe_dispatch(hidden_states, routing_weights, selected_experts, expert_usage, *, route_pos=None):
+    """Returns (sorted_token_idx [R], expert_offsets [E+1], compact_hidden [R,H],
+    compact_routing_weights [R,1]) with routes ordered by (expert, token, k)
+    (moe_dispatch_fused, sycl:3867-3965; order of ops.py:3301-3332)."""
+    if hidden_states.dim() != 2 or routing_weights.dim() != 2 or selected_experts.shape != routing_weights.shape:
+        raise RuntimeError("moe_dispatch: expected hidden [T,H], routing_weights/selected_experts [T,k]")
+    if selected_experts.dtype != torch.int64 or expert_usage.dtype not in (torch.int32, torch.int64):
+        raise RuntimeError("moe_dispatch: selected_experts must be int64 and expert_usage int32/int64")
+    _check_same_device("moe_dispatch", hidden_states, routing_weights, selected_experts, expert_usage)
+    t, h = hidden_states.shape
+    k = routing_weights.shape[1]
+    e = expert_usage.shape[0]
+    hs = hidden_states if hidden_states.stride(1) == 1 else hidden_states.contiguous()
+    rw = routing_weights.to(hs.dtype).contiguous()
+    sel = selected_experts.contiguous()
+    usage = expert_usage.contiguous()
+    dev = hs.device
+    sti = torch.empty((t * k,), dtype=torch.int64, device=dev)
+    sri = torch.empty((t * k,), dtype=torch.int64, device=dev)
+    offsets = torch.empty((e + 1,), dtype=torch.int64, device=dev)
+    compact = torch.empty((t * k, h), dtype=hs.dtype, device=dev)
+    cw = torch.empty((t * k, 1), dtype=hs.dtype, device=dev)
+    _lib.call("anna_mi_moe_dispatch", hs.data_ptr(), _lib.dtype_code(hs.dtype), t, h, hs.stride(0), rw.data_ptr(),
+              sel.data_ptr(), usage.data_ptr(), int(usage.dtype == torch.int64), e, k, sti.data_ptr(), sri.data_ptr(),
+              offsets.data_ptr(), compact.data_ptr(), cw.data_ptr(),
+              None if route_pos is None else route_pos.data_ptr(), _lib.stream_of(hs))
+    return sti, offsets, compact, cw
+
+
+def moe_scatter(compact_outputs, sorted_token_idx, num_tokens):
+    """out[t] = sum of the compact rows of token t (fp32 accumulation, moe_scatter_fused)."""
+    if compact_outputs.dim() != 2 or sorted_token_idx.dim() != 1 or sorted_token_idx.numel() != compact_outputs.shape[0]:
+        raise RuntimeError("moe_scatter: expected compact_outputs [R,H] and sorted_token_idx [R]")
+    _check_same_device("moe_scatter", compact_outputs, sorted_token_idx)
+    co = compact_outputs.contiguous()
+    sti = sorted_token_idx.to(torch.int64).contiguous()
+    r, h = co.shape
+    acc = torch.empty((num_tokens, h), dtype=torch.float32, device=co.device)
+    out = torch.empty((num_tokens, h), dtype=co.dtype, device=co.device)
+    _lib.call("anna_mi_moe_scatter", co.data_ptr(), _lib.dtype_code(co.dtype), r, h, sti.data_ptr(), int(num_tokens),
+              acc.data_ptr(), out.data_ptr(), _lib.stream_of(co))
+    return out
+
+
+def moe_combine(compact_outputs, route_pos, num_tokens, top_k, out=None):
+    """Deterministic scatter through the route positions kept from moe_dispatch."""
+    co = compact_outputs.contiguous()
+    h = co.shape[1]
+    if out is None:
+        out = torch.empty((num_tokens, h), dtype=co.dtype, device=co.device)
+    _lib.call("anna_mi_moe_combine", co.data_ptr(), _lib.dtype_code(co.dtype), h, route_pos.data_ptr(),
+              int(num_tokens), int(top_k), out.data_ptr(), _lib.stream_of(co))
+    return out
+
+
+def moe_mlp_args(compact_hidden_states, compact_routing_weights, compact_outputs, expert_offsets, active_experts,
+                 active_slots, gate_qweight, gate_qscale, gate_qzeros, up_qweight, up_qscale, up_qzeros,
+                 down_qweight, down_qscale, down_qzeros, group_size, activation) -> _lib.MoeMlpArgs:
+    a = _lib.MoeMlpArgs()
+    a.dtype = _lib.dtype_code(compact_hidden_states.dtype)
+    a.scale_dtype = _lib.dtype_code(gate_qscale.dtype)
+    a.routes, a.hidden_dim = compact_hidden_states.shape
+    a.intermediate_dim = gate_qweight.shape[1]
+    a.compact_hidden, a.compact_weights = compact_hidden_states.data_ptr(), compact_routing_weights.data_ptr()
+    a.compact_outputs, a.expert_offsets = compact_outputs.data_ptr(), expert_offsets.data_ptr()
+    a.active_experts, a.active_slots, a.active_count = active_experts.data_ptr(), active_slots.data_ptr(), active_experts.numel()
+    a.gate_qweight, a.gate_qscale, a.gate_qzeros = gate_qweight.data_ptr(), gate_qscale.data_ptr(), gate_qzeros.data_ptr()
+    a.up_qweight, a.up_qscale, a.up_qzeros = up_qweight.data_ptr(), up_qscale.data_ptr(), up_qzeros.data_ptr()
+    a.down_qweight, a.down_qscale, a.down_qzeros = down_qweight.data_ptr(), down_qscale.data_ptr(), down_qzeros.data_ptr()
+    a.hidden_packed_cols, a.hidden_groups = gate_qweight.shape[2], gate_qscale.shape[1]
+    a.intermediate_packed_cols, a.intermediate_groups = down_qweight.shape[2], down_qscale.shape[1]
+    a.group_size = int(group_size)
+    a.activation = activation.data_ptr()
+    return a
+
+
+def moe_grouped_int4_mlp_out(compact_hidden_states, compact_routing_weights, compact_outputs, expert_offsets,
+                             active_experts, active_slots, gate_qweight, gate_qscale, gate_qzeros, up_qweight,
+                             up_qscale, up_qzeros, down_qweight, down_qscale, down_qzeros, group_size,
+                             max_routes_per_expert, activation=None):
+    """moe_grouped_int4_mlp_fused (sycl:4078-4324): writes the routes of the active experts
+    into compact_outputs and returns it."""
+    bank = (gate_qweight, gate_qscale, gate_qzeros, up_qweight, up_qscale, up_qzeros, down_qweight, down_qscale,
+            down_qzeros)
+    _check_same_device("moe_grouped_int4_mlp_fused", compact_hidden_states, compact_routing_weights, compact_outputs,
+                       expert_offsets, active_experts, active_slots, *bank)
+    if compact_hidden_states.dim() != 2 or compact_outputs.shape != compact_hidden_states.shape:
+        raise RuntimeError("compact_outputs shape must match compact_hidden_states [routes, hidden_dim]")
+    if not compact_outputs.is_contiguous():
+        raise RuntimeError("compact_outputs must be contiguous")
+    if compact_routing_weights.dtype != compact_hidden_states.dtype or compact_outputs.dtype != compact_hidden_states.dtype:
+        raise RuntimeError("compact_routing_weights / compact_outputs dtype must match compact_hidden_states")
+    if expert_offsets.dtype != torch.int64 or active_experts.dtype != torch.int64 or active_slots.dtype != torch.int64:
+        raise RuntimeError("expert_offsets, active_experts and active_slots must be int64")
+    if active_experts.numel() != active_slots.numel() or active_experts.numel() == 0:
+        raise RuntimeError("active_experts/active_slots count mismatch or empty")
+    if int(max_routes_per_expert) <= 0:
+        raise RuntimeError("max_routes_per_expert must be positive")
+    for name, t, dt in (("gate_qweight", gate_qweight, torch.int32), ("up_qweight", up_qweight, torch.int32),
+                        ("down_qweight", down_qweight, torch.int32), ("gate_qzeros", gate_qzeros, torch.int8),
+                        ("up_qzeros", up_qzeros, torch.int8), ("down_qzeros", down_qzeros, torch.int8)):
+        if t.dtype != dt or t.dim() != 3:
+            raise RuntimeError(f"{name} must be a rank-3 {dt} tensor")
+    if not (gate_qscale.dtype == up_qscale.dtype == down_qscale.dtype):
+        raise RuntimeError("the bank's qscale tensors must share one dtype")
+    if gate_qweight.shape != up_qweight.shape or gate_qscale.shape != up_qscale.shape:
+        raise RuntimeError("gate/up bank shape mismatch")
+    x = compact_hidden_states.contiguous()
+    cw = compact_routing_weights.contiguous()
+    bank = tuple(t.contiguous() for t in bank)
+    if activation is None:
+        activation = torch.empty((x.shape[0], gate_qweight.shape[1]), dtype=torch.float32, device=x.device)
+    a = moe_mlp_args(x, cw, compact_outputs, expert_offsets.contiguous(), active_experts.contiguous(),
+                     active_slots.contiguous(), *bank, group_size, activation)
+    _lib.call("anna_mi_moe_grouped_int4_mlp", ctypes.byref(a), _lib.stream_of(x))
+    return compact_outputs
+
+
+def _moe_router_meta(router_logits, top_k, normalize_topk_prob=True):
+    t, e = router_logits.shape
+    return (router_logits.new_empty((t, top_k), dtype=torch.float32),
+            router_logits.new_empty((t, top_k), dtype=torch.int64), router_logits.new_empty((e,), dtype=torch.int32))
+
+
+def _moe_dispatch_meta(hidden_states, routing_weights, selected_experts, expert_usage):
+    r = routing_weights.numel()
+    return (selected_experts.new_empty((r,)), selected_experts.new_empty((expert_usage.shape[0] + 1,)),
+            hidden_states.new_empty((r, hidden_states.shape[1])), hidden_states.new_empty((r, 1)))
+
+
 # ---------------------------------------------------------------- registration
 
 _IMPLS = {
@@ -445,6 +620,10 @@ _IMPLS = {
         _gqa_decode_splitkv_turboquant_fused_out_impl,
         lambda q, qk, vd, vs, vz, rk, rv, out, *a, **kw: out,
     ),
+    "moe_router_fused": (moe_router, _moe_router_meta),
+    "moe_dispatch_fused": (moe_dispatch, _moe_dispatch_meta),
+    "moe_scatter_fused": (moe_scatter, lambda co, sti, n: co.new_empty((n, co.shape[1]))),
+    "moe_grouped_int4_mlp_fused": (moe_grouped_int4_mlp_out, lambda x, w, out, *a, **k: out),
 }
 
 
@@ -504,3 +683,25 @@ def run_gqa_decode_splitkv_turboquant_fused_out(*, query, quantized_key, value_d
     args = (query, quantized_key, value_data, value_scales, value_zeros, residual_key, residual_value, output,
             partial_stats, partial_values, float(scaling), int(value_bits), int(value_group_size), int(block_size))
     return op(*args) if gate is None else op(*args, gate)
+
+
+def run_moe_router_fused(*, router_logits, top_k, normalize_topk_prob=True):
+    return _op("moe_router_fused")(router_logits, int(top_k), bool(normalize_topk_prob))
+
+
+def run_moe_dispatch_fused(*, hidden_states, routing_weights, selected_experts, expert_usage):
+    return _op("moe_dispatch_fused")(hidden_states, routing_weights, selected_experts, expert_usage)
+
+
+def run_moe_scatter_fused(*, compact_outputs, sorted_token_idx, num_tokens):
+    return _op("moe_scatter_fused")(compact_outputs, sorted_token_idx, int(num_tokens))
+
+
+def run_moe_grouped_int4_mlp_fused(*, compact_hidden_states, compact_routing_weights, compact_outputs, expert_offsets,
+                                   active_experts, active_slots, gate_qweight, gate_qscale, gate_qzeros, up_qweight,
+                                   up_qscale, up_qzeros, down_qweight, down_qscale, down_qzeros, group_size,
+                                   max_routes_per_expert):
+    return _op("moe_grouped_int4_mlp_fused")(
+        compact_hidden_states, compact_routing_weights, compact_outputs, expert_offsets, active_experts, active_slots,
+        gate_qweight, gate_qscale, gate_qzeros, up_qweight, up_qscale, up_qzeros, down_qweight, down_qscale,
+        down_qzeros, int(group_size), int(max_routes_per_expert))

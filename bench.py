@@ -292,6 +292,123 @@ def _lib_call_mse(fused_ops, xs, qn, codes, norms):
                         codes.data_ptr(), norms.data_ptr(), fused_ops._lib.stream_of(xs))
 
 
+# ---------------------------------------------------------------- MoE (config 5)
+
+MOE_EXPERT_BYTES = 3 * 512 * 2048 // 2 + (2 * 16 * 512 + 4 * 2048) * 3  # int4 + bf16 scales + int8 zeros
+
+
+def _moe_bank(device, seed):
+    from anna_amd.moe import GroupedInt4ExpertBank
+
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    e, h, i, grp = 128, 2048, 512, 128
+
+    def lin(n, k):
+        qw = torch.randint(-(2**31), 2**31 - 1, (e, n, k // 8), dtype=torch.int32, device=device, generator=g)
+        qs = (torch.randn((e, k // grp, n), device=device, generator=g) * 0.02).abs_().add_(1e-3).to(torch.bfloat16)
+        qz = torch.randint(0, 16, (e, k // grp, n), dtype=torch.int8, device=device, generator=g)
+        return qw, qs, qz
+
+    return GroupedInt4ExpertBank(e, h, i, grp, *lin(i, h), *lin(i, h), *lin(h, i), list(range(e)),
+                                 {x: x for x in range(e)})
+
+
+def cpu_baseline_moe(tokens, budget_s):
+    """Reference CPU path of the quantized MoE block: _route_tokens, sorted dispatch, a
+    Qwen3MLP per hit expert whose projections run XPUInt4Linear._forward_dequant
+    (dequantize, bf16 F.linear), index_add_ scatter (ops.py:3280-3376, 3556-3568)."""
+    from oracle import cpu_paths as cp
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    g = torch.Generator().manual_seed(3)
+    e, k, h, i, grp = 128, 8, 2048, 512, 128
+
+    def lin(n, kk):
+        return (torch.randint(-(2**31), 2**31 - 1, (n, kk // 8), dtype=torch.int32, generator=g),
+                (torch.randn((kk // grp, n), generator=g) * 0.02).abs_().add_(1e-3),
+                torch.randint(0, 16, (kk // grp, n), dtype=torch.int8, generator=g))
+
+    experts = [(lin(i, h), lin(i, h), lin(h, i)) for _ in range(e)]
+    x = torch.randn(tokens, h, generator=g).to(torch.bfloat16)
+    logits = torch.randn(tokens, e, generator=g)
+
+    def step():
+        w, sel, usage = cp.moe_route(logits, k, True)
+        tok, rte, off = cp.moe_sorted_assignments(sel, usage, e)
+        compact = x.index_select(0, tok)
+        cw = w.to(torch.bfloat16)[tok, rte].unsqueeze(1)
+        outs = torch.empty_like(compact)
+        for ex in range(e):
+            s0, s1 = int(off[ex]), int(off[ex + 1])
+            if s1 <= s0:
+                continue
+            (gq, gs, gz), (uq, us, uz), (dq, ds, dz) = experts[ex]
+            xs = compact[s0:s1]
+            gate = cp.int4_forward_dequant(xs, gq, gs, gz, grp, h)
+            up = cp.int4_forward_dequant(xs, uq, us, uz, grp, h)
+            act = torch.nn.functional.silu(gate) * up
+            outs[s0:s1] = cp.int4_forward_dequant(act, dq, ds, dz, grp, i) * cw[s0:s1]
+        fin = torch.zeros((tokens, h), dtype=torch.bfloat16)
+        fin.index_add_(0, tok, outs)
+        return fin
+
+    step()
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        step()
+        n += 1
+        if time.perf_counter() - t0 > budget_s or n >= 20:
+            break
+    sec = (time.perf_counter() - t0) / n
+    return {"value": tokens / sec, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{n} MoE steps of {tokens} tokens through the reference CPU path; {sec * 1e3:.1f} ms/step"}
+
+
+def section_moe(args, device):
+    """128 experts, top-8 of softmax(N(0,1) logits), H=2048, I=512, group 128
+    int4 (bf16 scales, int8 zeros), T in {8, 64, 512} bf16 tokens."""
+    from anna_amd import fused_ops
+    from anna_amd.moe import SparseMoeInt4
+
+    banks = [_moe_bank(device, 100 + c) for c in range(3)]  # 3 x 211 MB: more than 2 x the Infinity Cache
+    out = []
+    for tokens in (8, 64, 512):
+        gen = torch.Generator(device=device)
+        gen.manual_seed(tokens)
+        x = torch.randn((tokens, 2048), device=device, generator=gen).to(torch.bfloat16)
+        logits = torch.randn((tokens, 128), device=device, generator=gen)
+        blocks = [SparseMoeInt4(b, num_experts=128, top_k=8) for b in banks]
+        w, sel, usage = fused_ops.moe_router(logits, 8, True)
+        active = int((usage > 0).sum())
+        sti, off, compact, cw = fused_ops.moe_dispatch(x, w.to(torch.bfloat16), sel, usage)
+        co = torch.empty_like(compact)
+        act = torch.empty((compact.shape[0], 512), dtype=torch.float32, device=device)
+        mlp = [(lambda b=b: fused_ops.moe_grouped_int4_mlp_out(compact, cw, co, off, blocks[0].active_experts,
+                                                               blocks[0].active_slots, *b.tensors(), 128, tokens * 8,
+                                                               activation=act)) for b in banks]
+        full = [(lambda blk=blk: blk(x, logits)) for blk in blocks]
+        ms_mlp = time_graph(mlp, args.steps, args.warmup)
+        ms_full = time_graph(full, args.steps, args.warmup)
+        wbytes = active * MOE_EXPERT_BYTES
+        io = tokens * 8 * 2048 * 2 * 2
+        r = {"tokens": tokens, "routes": tokens * 8, "active_experts": active, "weight_bytes": wbytes,
+             "mlp_us": ms_mlp * 1e3, "mlp_GB/s": (wbytes + io) / ms_mlp / 1e6,
+             "mlp_roofline_frac": (wbytes + io) / ms_mlp / 1e6 / HBM_PEAK_GBS,
+             "step_us": ms_full * 1e3, "step_tokens/s": tokens / ms_full * 1e3,
+             "TFLOP/s": tokens * 8 * 2 * (2048 * 1024 + 512 * 2048) / ms_mlp / 1e9}
+        log(f"moe T={tokens:4d} active={active:3d}: grouped MLP {r['mlp_us']:.1f} us {r['mlp_GB/s']:.0f} GB/s "
+            f"({100 * r['mlp_roofline_frac']:.1f}% HBM); full step {r['step_us']:.1f} us")
+        if not args.no_cpu and tokens in (8, 64):
+            r["cpu_baseline"] = cpu_baseline_moe(tokens, args.cpu_seconds / 2)
+            log(f"moe T={tokens} cpu baseline: {r['cpu_baseline']['value']:.1f} tokens/s")
+        out.append(r)
+    del banks
+    torch.cuda.empty_cache()
+    return out
+
+
 def calibrate_copy(device, steps: int = 5) -> dict:
     """A plain elementwise kernel of known traffic (reads and writes COPY_BYTES each), run so
     that a counter collection run can scale FETCH_SIZE / WRITE_SIZE to bytes."""
@@ -325,7 +442,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=60)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--sections", default="int4,tq_decode,tq_pack")
+    ap.add_argument("--sections", default="int4,tq_decode,tq_pack,moe")
     ap.add_argument("--tq-tokens-per-item", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -356,6 +473,8 @@ def main() -> int:
         sections["tq_decode"] = section_tq_decode(args, device)
     if "tq_pack" in wanted:
         sections["tq_pack"] = section_tq_pack(args, device)
+    if "moe" in wanted:
+        sections["moe"] = section_moe(args, device)
     if "int4_sweep" not in sections:
         print(json.dumps({"sections": sections}))
         return 0

@@ -245,6 +245,76 @@ int anna_mi_tq_decode(const anna_mi_tq_decode_args* args, void* stream);
  * value layout [tokens/32][2048] read by anna_mi_tq_decode.  Pure permutation. */
 int anna_mi_tq_block_values(const uint8_t* codes, int64_t tokens, uint8_t* blocked, void* stream);
 
+/* ------------------------------------------------------------------ MoE
+ * Routing around the grouped expert MLP (Qwen3SparseMoeBlock, src/anna/model/ops.py:3280-3376). */
+
+/* moe_router_fused (sycl:3731-3839; CPU path ops.py:3280-3299): per token, fp32 softmax over the
+ * experts, top-k (ties: lower expert index first), renormalised when `normalize`; usage[e]
+ * counts the routes of expert e (zeroed by the call).  logits [tokens][num_experts] (row
+ * stride given), weights fp32 [tokens][top_k], selected int64 [tokens][top_k], usage int32
+ * [num_experts].  num_experts <= 1024, top_k <= 64. */
+int anna_mi_moe_router(const void* logits, int logits_dtype, int64_t tokens, int64_t num_experts,
+                       int64_t logits_row_stride, int64_t top_k, int normalize, float* weights,
+                       int64_t* selected, int32_t* usage, void* stream);
+
+/* moe_dispatch_fused (sycl:3867-3965; CPU path ops.py:3301-3357): expert_offsets int64 [E+1]
+ * (prefix sum of usage, int32 or int64), routes sorted by (expert, token, k) -- the CPU
+ * path's order, deterministic: sorted_token_idx / sorted_route_idx int64 [tokens*top_k];
+ * compact_hidden [routes][hidden] and compact_weights [routes] in the hidden dtype
+ * (routing_weights [tokens][top_k] contiguous, hidden dtype).  route_pos (optional, may be
+ * NULL) receives the compact position of route t*top_k + j. */
+int anna_mi_moe_dispatch(const void* hidden, int dtype, int64_t tokens, int64_t hidden_dim,
+                         int64_t hidden_row_stride, const void* routing_weights, const int64_t* selected,
+                         const void* usage, int usage_is_int64, int64_t num_experts, int64_t top_k,
+                         int64_t* sorted_token_idx, int64_t* sorted_route_idx, int64_t* expert_offsets,
+                         void* compact_hidden, void* compact_weights, int64_t* route_pos, void* stream);
+
+/* moe_scatter_fused (sycl:3967-4037; CPU path ops.py:3359-3376): out[t] = sum of the compact
+ * rows p with sorted_token_idx[p] == t, accumulated in fp32 (workspace accum [tokens][hidden]
+ * fp32) and cast to the hidden dtype. */
+int anna_mi_moe_scatter(const void* compact_outputs, int dtype, int64_t routes, int64_t hidden_dim,
+                        const int64_t* sorted_token_idx, int64_t num_tokens, float* accum, void* out,
+                        void* stream);
+
+/* Deterministic form of the scatter for callers that kept route_pos from the dispatch:
+ * out[t] = sum_j compact_outputs[route_pos[t*top_k + j]] in fp32, j ascending. */
+int anna_mi_moe_combine(const void* compact_outputs, int dtype, int64_t hidden_dim, const int64_t* route_pos,
+                        int64_t num_tokens, int64_t top_k, void* out, void* stream);
+
+/* moe_grouped_int4_mlp_fused (sycl:4078-4324; caller ops.py:3405-3457; bank ops.py:73-89):
+ * for each active expert e (bank slot active_slots[i]) and its compact routes
+ * [expert_offsets[e], expert_offsets[e+1]):
+ *   act = silu(x Wg^T) * (x Wu^T) (fp32), out = (act Wd^T) * routing weight (hidden dtype).
+ * Bank layout (XPUInt4Linear buffers stacked over slots): gate/up qweight int32
+ * [S][I][Kh/8], qscale [S][Gh][I], qzeros int8 [S][Gh][I]; down qweight [S][H][Ki/8], qscale
+ * [S][Gi][H], qzeros [S][Gi][H].  hidden and intermediate dims: multiples of 128, <= 4096. */
+typedef struct {
+  int dtype;                      /* hidden dtype (bf16 / fp16 / fp32) */
+  int scale_dtype;                /* qscale dtype of the bank */
+  int64_t routes, hidden_dim, intermediate_dim;
+  const void* compact_hidden;     /* [routes][hidden] */
+  const void* compact_weights;    /* [routes], hidden dtype */
+  void* compact_outputs;          /* [routes][hidden], hidden dtype; rows of inactive experts untouched */
+  const int64_t* expert_offsets;  /* [E+1] */
+  const int64_t* active_experts;  /* [active_count] */
+  const int64_t* active_slots;    /* [active_count] */
+  int64_t active_count;
+  const int32_t* gate_qweight;
+  const void* gate_qscale;
+  const int8_t* gate_qzeros;
+  const int32_t* up_qweight;
+  const void* up_qscale;
+  const int8_t* up_qzeros;
+  const int32_t* down_qweight;
+  const void* down_qscale;
+  const int8_t* down_qzeros;
+  int64_t hidden_packed_cols, hidden_groups, intermediate_packed_cols, intermediate_groups, group_size;
+  float* activation;              /* workspace fp32 [routes][intermediate] */
+} anna_mi_moe_mlp_args;
+
+int64_t anna_mi_sizeof_moe_mlp_args(void);
+int anna_mi_moe_grouped_int4_mlp(const anna_mi_moe_mlp_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,142 @@
+"""MoE router / dispatch / grouped int4 MLP / scatter on the GPU against the CPU restatements.
+
+Router indices, usage, dispatch order and offsets are exact; routing weights within 1e-5;
+the grouped MLP within normwise relative error 1e-2 of the fp64 brute force over the
+dequantized bank (the north-star bf16 tolerance; the reference's own op tests use 2e-2).
+"""
+
+import pytest
+import torch
+
+from anna_amd import fused_ops
+from anna_amd.moe import GroupedInt4ExpertBank, SparseMoeInt4
+from oracle import cpu_paths as cp
+from tests._util import BF16_TOL, rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def make_bank(num_experts, hidden, inter, group, scale_dtype, device, seed):
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+
+    def lin(n, k):
+        qw = torch.randint(-(2**31), 2**31 - 1, (num_experts, n, k // 8), dtype=torch.int32, device=device, generator=g)
+        qs = (torch.randn((num_experts, k // group, n), device=device, generator=g) * 0.02).abs_().add_(1e-3)
+        qz = torch.randint(0, 16, (num_experts, k // group, n), dtype=torch.int8, device=device, generator=g)
+        return qw, qs.to(scale_dtype), qz
+
+    gq, gs, gz = lin(inter, hidden)
+    uq, us, uz = lin(inter, hidden)
+    dq, ds, dz = lin(hidden, inter)
+    return GroupedInt4ExpertBank(num_experts, hidden, inter, group, gq, gs, gz, uq, us, uz, dq, ds, dz,
+                                 list(range(num_experts)), {e: e for e in range(num_experts)})
+
+
+def dequant_experts(bank, experts):
+    out = {}
+    for e in experts:
+        s = bank.expert_to_slot[e]
+        f = [cp.int4_dequant_f32(q[s].cpu(), sc[s].cpu(), z[s].cpu(), bank.group_size, k)
+             for q, sc, z, k in ((bank.gate_qweight, bank.gate_qscale, bank.gate_qzeros, bank.hidden_dim),
+                                 (bank.up_qweight, bank.up_qscale, bank.up_qzeros, bank.hidden_dim),
+                                 (bank.down_qweight, bank.down_qscale, bank.down_qzeros, bank.intermediate_dim))]
+        out[e] = tuple(f)
+    return out
+
+
+@pytest.mark.parametrize("tokens,experts,top_k,dtype,norm", [
+    (11, 16, 4, torch.bfloat16, True),  # the reference test's shape (test_fused_op_xpu.py:948-966)
+    (11, 16, 4, torch.bfloat16, False),
+    (64, 128, 8, torch.float32, True),
+    (5, 300, 8, torch.float16, True),
+])
+def test_router_matches_reference(gpu, tokens, experts, top_k, dtype, norm):
+    torch.manual_seed(tokens + experts)
+    logits = torch.randn(tokens, experts, device=gpu, dtype=dtype)
+    w, sel, usage = torch.ops.anna.moe_router_fused(logits, top_k, norm)
+    rw, rsel, rusage = cp.moe_route(logits.cpu(), top_k, norm)
+    assert torch.equal(sel.cpu(), rsel)
+    assert torch.equal(usage.cpu().long(), rusage.long())
+    torch.testing.assert_close(w.cpu(), rw, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_dispatch_matches_cpu_order(gpu, dtype):
+    torch.manual_seed(3)
+    t, h, e, k = 37, 256, 16, 4
+    hidden = torch.randn(t, h, device=gpu, dtype=dtype)
+    w, sel, usage = fused_ops.moe_router(torch.randn(t, e, device=gpu), k, True)
+    rw = w.to(dtype)
+    pos = torch.empty(t * k, dtype=torch.int64, device=gpu)
+    sti, off, compact, cw = fused_ops.moe_dispatch(hidden, rw, sel, usage, route_pos=pos)
+    tok, rte, roff = cp.moe_sorted_assignments(sel.cpu(), usage.cpu(), e)
+    assert torch.equal(sti.cpu(), tok) and torch.equal(off.cpu(), roff)
+    assert torch.equal(compact.cpu(), hidden.cpu().index_select(0, tok))
+    assert torch.equal(cw.cpu()[:, 0], rw.cpu()[tok, rte])
+    # route_pos inverts the order
+    assert torch.equal(sti.cpu()[pos.cpu()], torch.arange(t).repeat_interleave(k))
+    # the op form returns the same
+    sti2, off2, compact2, cw2 = torch.ops.anna.moe_dispatch_fused(hidden, rw, sel, usage.long())
+    assert torch.equal(sti2, sti) and torch.equal(off2, off) and torch.equal(compact2, compact)
+
+
+@pytest.mark.parametrize("hdt,sdt,group,tokens", [
+    (torch.bfloat16, torch.float32, 128, 13),  # reference bank dtype (fp32 scales)
+    (torch.bfloat16, torch.bfloat16, 128, 40),  # > 16 routes per expert (chunking)
+    (torch.float16, torch.float32, 64, 9),
+    (torch.float32, torch.float32, 32, 6),
+])
+def test_grouped_int4_mlp_matches_oracle(gpu, hdt, sdt, group, tokens):
+    torch.manual_seed(7)
+    e, k, h, i = 8, 3, 256, 128
+    bank = make_bank(e, h, i, group, sdt, gpu, seed=11 + tokens)
+    hidden = torch.randn(tokens, h, device=gpu, dtype=hdt)
+    w, sel, usage = fused_ops.moe_router(torch.randn(tokens, e, device=gpu), k, True)
+    sti, off, compact, cw = fused_ops.moe_dispatch(hidden, w.to(hdt), sel, usage)
+    out = torch.full_like(compact, 7.0)
+    active = [0, 2, 3, 5, 6, 7]  # experts 1 and 4 inactive: their rows stay untouched
+    act_t = torch.tensor(active, dtype=torch.int64, device=gpu)
+    res = torch.ops.anna.moe_grouped_int4_mlp_fused(compact, cw, out, off, act_t, act_t, *bank.tensors(), group,
+                                                   int(usage.max()))
+    assert res.data_ptr() == out.data_ptr()
+    offc = off.cpu()
+    ref = cp.moe_grouped_mlp(compact.cpu(), cw.cpu(), offc, dequant_experts(bank, active), torch.float64)
+    rows = torch.cat([torch.arange(int(offc[x]), int(offc[x + 1])) for x in active])
+    got = out.cpu().double()
+    assert rel_err(got[rows].numpy(), ref[rows].numpy()) <= BF16_TOL
+    inactive = torch.cat([torch.arange(int(offc[x]), int(offc[x + 1])) for x in (1, 4)])
+    assert bool((out.cpu()[inactive] == 7.0).all())
+
+
+def test_scatter_and_combine(gpu):
+    torch.manual_seed(4)
+    t, h, e, k = 29, 384, 12, 3
+    w, sel, usage = fused_ops.moe_router(torch.randn(t, e, device=gpu), k, True)
+    pos = torch.empty(t * k, dtype=torch.int64, device=gpu)
+    sti, off, compact, cw = fused_ops.moe_dispatch(torch.randn(t, h, device=gpu, dtype=torch.bfloat16),
+                                                    w.to(torch.bfloat16), sel, usage, route_pos=pos)
+    co = torch.randn(t * k, h, device=gpu, dtype=torch.bfloat16)
+    ref = cp.moe_scatter(co.cpu(), sti.cpu(), t)
+    a = torch.ops.anna.moe_scatter_fused(co, sti, t)
+    b = fused_ops.moe_combine(co, pos, t, k)
+    torch.testing.assert_close(a.cpu().float(), ref.float(), rtol=8e-3, atol=1e-2)
+    torch.testing.assert_close(b.cpu().float(), ref.float(), rtol=8e-3, atol=1e-2)
+
+
+@pytest.mark.parametrize("tokens", [8, 64])
+def test_sparse_moe_block_matches_cpu_chain(gpu, tokens):
+    torch.manual_seed(tokens)
+    e, k, h, i, group = 16, 4, 256, 128, 128
+    bank = make_bank(e, h, i, group, torch.bfloat16, gpu, seed=5)
+    block = SparseMoeInt4(bank, num_experts=e, top_k=k)
+    hidden = torch.randn(tokens, h, device=gpu, dtype=torch.bfloat16)
+    logits = torch.randn(tokens, e, device=gpu, dtype=torch.float32)
+    out = block(hidden, logits)
+    w, sel, usage = cp.moe_route(logits.cpu(), k, True)
+    tok, rte, off = cp.moe_sorted_assignments(sel, usage, e)
+    compact = hidden.cpu().index_select(0, tok)
+    cw = w.to(torch.bfloat16)[tok, rte].unsqueeze(1)
+    co = cp.moe_grouped_mlp(compact, cw, off, dequant_experts(bank, range(e)), torch.float64)
+    ref = torch.zeros(tokens, h, dtype=torch.float64).index_add_(0, tok, co)
+    assert rel_err(out.cpu().double().numpy(), ref.numpy()) <= BF16_TOL
