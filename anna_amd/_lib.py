@@ -91,7 +91,7 @@ class MoeMlpArgs(ctypes.Structure):
         ("up_qweight", _P), ("up_qscale", _P), ("up_qzeros", _P),
         ("down_qweight", _P), ("down_qscale", _P), ("down_qzeros", _P),
         ("hidden_packed_cols", _I64), ("hidden_groups", _I64), ("intermediate_packed_cols", _I64),
-        ("intermediate_groups", _I64), ("group_size", _I64), ("activation", _P),
+        ("intermediate_groups", _I64), ("group_size", _I64), ("activation", _P), ("sweep_chunks", _I),
     ]
 
 

@@ -197,24 +197,163 @@ __global__ void moe_combine_kernel(const typename Elem<HDT>::T* __restrict__ com
 
 // ------------------------------------------------------------------ grouped int4 MLP
 
-constexpr int MOE_ROWS = 64;   // output rows per workgroup (4 waves x 16)
-constexpr int MOE_CHUNK = 16;  // routes per pass (the MFMA M dimension)
-constexpr int MOE_PB = 8;      // 128-k blocks whose weights one wave loads ahead
+constexpr int MOE_ROWS = 64;  // output rows per workgroup (4 waves x 16)
+constexpr int MOE_PB = 4;     // 128-k blocks per pass (x is staged 512 k at a time)
+constexpr int MOE_XP = MOE_PB * 128 + 8;  // LDS row pitch of the staged x slice (16-bit elements)
+constexpr int MOE_MAXC = 4;   // 16-route chunks per sweep over the weights (64 routes)
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
-// GU: pass 1 (gate and up, K = hidden, N = intermediate, act fp32 out);
-// otherwise pass 2 (down, K = intermediate, N = hidden, compact outputs in HDT).
-// MDT is the 16-bit MFMA type: f16 for f16 hidden states in pass 1, bf16 otherwise.
-// GPB: int4 groups per 128-k block (group size 128 / GPB; larger groups count as 1).
-template <int HDT, int SDT, bool GU, int GPB>
-__global__ __launch_bounds__(256) void moe_int4_mlp_kernel(const anna_mi_moe_mlp_args a) {
+// Convert 8 consecutive activations to the 16-bit MFMA type MDT.
+template <int SRC, int MDT>
+__device__ __forceinline__ u32x4 load8_as16(const void* base, int64_t idx) {
+  if constexpr (SRC == MDT) {
+    return *(const u32x4*)((const uint16_t*)base + idx);
+  } else {
+    // f32 sources (fp32 hidden states, the fp32 activation) -> bf16
+    const float* src = (const float*)base + idx;
+    const float4 lo = *(const float4*)src, hi = *(const float4*)(src + 4);
+    u32x4 v;
+    v.x = (uint32_t)f32_to_bf16_bits(lo.x) | ((uint32_t)f32_to_bf16_bits(lo.y) << 16);
+    v.y = (uint32_t)f32_to_bf16_bits(lo.z) | ((uint32_t)f32_to_bf16_bits(lo.w) << 16);
+    v.z = (uint32_t)f32_to_bf16_bits(hi.x) | ((uint32_t)f32_to_bf16_bits(hi.y) << 16);
+    v.w = (uint32_t)f32_to_bf16_bits(hi.z) | ((uint32_t)f32_to_bf16_bits(hi.w) << 16);
+    return v;
+  }
+}
+
+// One pass's worth of one wave's weights: PB blocks x NM matrices, with the scale and the
+// "off + zero" constant of each group.
+template <int NM, int GPB>
+struct MoePass {
+  u32x4 w[MOE_PB][NM];
+  float s[MOE_PB][GPB][NM];
+  float c[MOE_PB][GPB][NM];
+};
+
+// One sweep of a workgroup over its 64 output rows x all K for NC chunks of 16 routes.
+// Per pass: load this pass's x slice and store it to LDS, issue the next pass's weight loads
+// (after the x loads: vector loads complete in order, so waiting for x never waits for
+// them), then run the MFMAs of every chunk on the weights already in registers.
+template <int HDT, int SDT, bool GU, int GPB, int NC>
+__device__ __forceinline__ void moe_sweep(const anna_mi_moe_mlp_args& a, uint16_t* xs, int64_t c0, int64_t nrows,
+                                          int64_t slot, int64_t N, int64_t K, int64_t n, bool n_ok,
+                                          const uint32_t* const* wrow, const void* const* sc, const int8_t* const* zp) {
   constexpr int MDT = (GU && HDT == ANNA_MI_F16) ? ANNA_MI_F16 : ANNA_MI_BF16;
+  constexpr int SRC = GU ? HDT : ANNA_MI_F32;  // dtype of the activations read
   constexpr float OFF = MDT == ANNA_MI_BF16 ? 128.0f : 1024.0f;
   constexpr uint32_t ONES = MDT == ANNA_MI_BF16 ? 0x3F803F80u : 0x3C003C00u;
-  constexpr int NM = GU ? 2 : 1;  // weight matrices
+  constexpr int NM = GU ? 2 : 1;
+  constexpr int XPT = NC * 16 * (MOE_PB * 16) / 256;  // 16 B x chunks per thread per pass
   using ST = typename Elem<SDT>::T;
-  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [16][K + 8]
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15, kq = lane >> 4;
+  const int64_t nblk = K / 128;
+  const int64_t npass = (nblk + MOE_PB - 1) / MOE_PB;
+  const void* xsrc = GU ? a.compact_hidden : (const void*)a.activation;
+  const u32x4 ones = {ONES, ONES, ONES, ONES};
+
+  auto load_pass = [&](int64_t p, MoePass<NM, GPB>& P) {
+#pragma unroll
+    for (int j = 0; j < MOE_PB; ++j) {
+      int64_t b = p * MOE_PB + j;
+      b = b < nblk ? b : nblk - 1;
+#pragma unroll
+      for (int m = 0; m < NM; ++m) {
+        P.w[j][m] = __builtin_nontemporal_load((const u32x4*)(wrow[m] + b * 16));
+#pragma unroll
+        for (int q = 0; q < GPB; ++q) {
+          const int64_t gi = (b * GPB + q) * N;
+          P.s[j][q][m] = Elem<SDT>::to_f32(((const ST*)sc[m])[gi]);
+          P.c[j][q][m] = OFF + (float)zp[m][gi];
+        }
+      }
+    }
+  };
+
+  f32x4 out[NC][NM];
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int m = 0; m < NM; ++m) out[c][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  MoePass<NM, GPB> cur, nxt;
+  load_pass(0, cur);
+  for (int64_t p = 0; p < npass; ++p) {
+    // x slice [NC*16 rows][512 k] of this pass (rows past the expert's routes read as zero)
+    u32x4 xv[XPT];
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+      const int e = threadIdx.x + 256 * i;  // chunk index: row e / 64, 8-k column e % 64
+      const int row = e >> 6, col = (e & 63) * 8;
+      const int64_t k = p * MOE_PB * 128 + col;
+      const bool ok = row < nrows && k < K;
+      xv[i] = load8_as16<SRC, MDT>(xsrc, (c0 + (ok ? row : 0)) * K + (ok ? k : 0));
+      if (!ok) xv[i] = u32x4{0u, 0u, 0u, 0u};
+    }
+    __syncthreads();  // every wave is done with the previous slice
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+      const int e = threadIdx.x + 256 * i;
+      *(u32x4*)(xs + (e >> 6) * MOE_XP + (e & 63) * 8) = xv[i];
+    }
+    __syncthreads();
+    if (p + 1 < npass) load_pass(p + 1, nxt);  // in flight during this pass's MFMAs
+#pragma unroll
+    for (int j = 0; j < MOE_PB; ++j) {
+      if (p * MOE_PB + j >= nblk) continue;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        // lanes kq hold k = 128 b + 32 kq + 8 s + e: a step spans the whole block, so each of
+        // its GPB groups gets its own MFMA with the other groups' lanes zeroed
+        u32x4 wf[NM];
+#pragma unroll
+        for (int m = 0; m < NM; ++m) wf[m] = nibbles_to_frag<MDT>(cur.w[j][m][s]);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const u32x4 xa = interleave_x(*(const u32x4*)(xs + (c * 16 + r) * MOE_XP + j * 128 + kq * 32 + s * 8));
+#pragma unroll
+          for (int q = 0; q < GPB; ++q) {
+            const u32x4 xm = (GPB == 1 || kq / (4 / GPB) == q) ? xa : u32x4{0u, 0u, 0u, 0u};
+            const f32x4 sx = mfma16<MDT>(xm, ones, f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+              const f32x4 acc = mfma16<MDT>(xm, wf[m], f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+              for (int i = 0; i < 4; ++i) out[c][m][i] = fmaf(cur.s[j][q][m], acc[i] - cur.c[j][q][m] * sx[i], out[c][m][i]);
+            }
+          }
+        }
+      }
+    }
+    cur = nxt;
+  }
+  // C layout: lane holds routes c0 + 16 c + 4 kq + i of output row n
+  if (n_ok) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t m = c * 16 + 4 * kq + i;
+        if (m >= nrows) continue;
+        const int64_t route = c0 + m;
+        if constexpr (GU) {
+          a.activation[route * N + n] = silu(out[c][0][i]) * out[c][1][i];
+        } else {
+          const float w = Elem<HDT>::load((const typename Elem<HDT>::T*)a.compact_weights, route);
+          ((typename Elem<HDT>::T*)a.compact_outputs)[route * N + n] = Elem<HDT>::cvt(out[c][0][i] * w);
+        }
+      }
+  }
+}
+
+// GU: pass 1 (gate and up, K = hidden, N = intermediate, act fp32 out); otherwise pass 2
+// (down, K = intermediate, N = hidden, compact outputs in HDT).  GPB: int4 groups per 128-k
+// block (group size 128 / GPB; larger groups count as 1).  grid (N / 64, active experts).
+template <int HDT, int SDT, bool GU, int GPB, int NCMAX>
+__global__ __launch_bounds__(256) void moe_int4_mlp_kernel(const anna_mi_moe_mlp_args a) {
+  constexpr int NM = GU ? 2 : 1;
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [sweep_chunks * 16][MOE_XP]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, kq = lane >> 4;
   const int64_t ai = blockIdx.y;
@@ -225,13 +364,13 @@ __global__ __launch_bounds__(256) void moe_int4_mlp_kernel(const anna_mi_moe_mlp
   const int64_t K = GU ? a.hidden_dim : a.intermediate_dim;
   const int64_t pc = GU ? a.hidden_packed_cols : a.intermediate_packed_cols;
   const int64_t G = GU ? a.hidden_groups : a.intermediate_groups;
-  const int64_t xp = K + 8;
   const int64_t n = (int64_t)blockIdx.x * MOE_ROWS + wave * 16 + r;
   const bool n_ok = n < N;
   const int64_t nc = n_ok ? n : 0;
   const uint32_t* wrow[NM];
-  const ST* sc[NM];
+  const void* sc[NM];
   const int8_t* zp[NM];
+  using ST = typename Elem<SDT>::T;
   if constexpr (GU) {
     wrow[0] = (const uint32_t*)a.gate_qweight + (slot * N + nc) * pc + kq * 4;
     wrow[1] = (const uint32_t*)a.up_qweight + (slot * N + nc) * pc + kq * 4;
@@ -244,108 +383,44 @@ __global__ __launch_bounds__(256) void moe_int4_mlp_kernel(const anna_mi_moe_mlp
     sc[0] = (const ST*)a.down_qscale + slot * G * N + nc;
     zp[0] = a.down_qzeros + slot * G * N + nc;
   }
-  const int64_t nblk = K / 128;
-  const u32x4 ones = {ONES, ONES, ONES, ONES};
-
-  for (int64_t c0 = start; c0 < end; c0 += MOE_CHUNK) {
-    const int64_t cnt = end - c0 < MOE_CHUNK ? end - c0 : MOE_CHUNK;
-    // stage the chunk's activations as 16-bit MFMA rows (rows >= cnt are zero)
-    const int64_t cpr = K / 8;  // 8-element chunks per row
-    for (int64_t i = threadIdx.x; i < MOE_CHUNK * cpr; i += blockDim.x) {
-      const int64_t row = i / cpr, col = (i % cpr) * 8;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (row < cnt) {
-        if constexpr (GU && HDT != ANNA_MI_F32) {
-          v = *(const u32x4*)((const uint16_t*)a.compact_hidden + (c0 + row) * K + col);
-        } else {
-          const float* src = GU ? (const float*)a.compact_hidden + (c0 + row) * K + col
-                                : a.activation + (c0 + row) * K + col;
-          const float4 lo = *(const float4*)src, hi = *(const float4*)(src + 4);
-          v.x = (uint32_t)f32_to_bf16_bits(lo.x) | ((uint32_t)f32_to_bf16_bits(lo.y) << 16);
-          v.y = (uint32_t)f32_to_bf16_bits(lo.z) | ((uint32_t)f32_to_bf16_bits(lo.w) << 16);
-          v.z = (uint32_t)f32_to_bf16_bits(hi.x) | ((uint32_t)f32_to_bf16_bits(hi.y) << 16);
-          v.w = (uint32_t)f32_to_bf16_bits(hi.z) | ((uint32_t)f32_to_bf16_bits(hi.w) << 16);
-        }
-      }
-      *(u32x4*)(xs + row * xp + col) = v;
-    }
-    __syncthreads();
-
-    f32x4 out[NM];
-#pragma unroll
-    for (int m = 0; m < NM; ++m) out[m] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int64_t b0 = 0; b0 < nblk; b0 += MOE_PB) {
-      // every weight load of the pass first (clamped addresses, no branches around loads)
-      u32x4 wv[MOE_PB][NM];
-#pragma unroll
-      for (int j = 0; j < MOE_PB; ++j) {
-        const int64_t b = b0 + j < nblk ? b0 + j : nblk - 1;
-#pragma unroll
-        for (int m = 0; m < NM; ++m) wv[j][m] = __builtin_nontemporal_load((const u32x4*)(wrow[m] + b * 16));
-      }
-#pragma unroll
-      for (int j = 0; j < MOE_PB; ++j) {
-        const int64_t b = b0 + j;
-        if (b >= nblk) continue;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          // lanes kq hold k = 128 b + 32 kq + 8 s + e: a step spans the whole block, so each of
-          // its GPB groups gets its own MFMA with the other groups' lanes zeroed
-          const int64_t k = b * 128 + kq * 32 + s * 8;
-          const u32x4 xa = interleave_x(*(const u32x4*)(xs + r * xp + k));
-#pragma unroll
-          for (int q = 0; q < GPB; ++q) {
-            const u32x4 xm = (GPB == 1 || kq / (4 / GPB) == q) ? xa : u32x4{0u, 0u, 0u, 0u};
-            const int64_t g = b * GPB + q;
-            const f32x4 sx = mfma16<MDT>(xm, ones, f32x4{0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-            for (int m = 0; m < NM; ++m) {
-              const f32x4 acc = mfma16<MDT>(xm, nibbles_to_frag<MDT>(wv[j][m][s]), f32x4{0.f, 0.f, 0.f, 0.f});
-              const float scl = Elem<SDT>::to_f32(sc[m][g * N]);
-              const float c = OFF + (float)zp[m][g * N];
-#pragma unroll
-              for (int i = 0; i < 4; ++i) out[m][i] = fmaf(scl, acc[i] - c * sx[i], out[m][i]);
-            }
-          }
-        }
-      }
-    }
-    // C layout: lane holds routes c0 + 4 kq + i of output row n
-    if (n_ok) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t m = 4 * kq + i;
-        if (m >= cnt) continue;
-        const int64_t route = c0 + m;
-        if constexpr (GU) {
-          a.activation[route * N + n] = silu(out[0][i]) * out[1][i];
-        } else {
-          const float w = Elem<HDT>::load((const typename Elem<HDT>::T*)a.compact_weights, route);
-          ((typename Elem<HDT>::T*)a.compact_outputs)[route * N + n] = Elem<HDT>::cvt(out[0][i] * w);
-        }
-      }
-    }
-    __syncthreads();  // the next chunk overwrites xs
+  const int64_t sweep = (int64_t)a.sweep_chunks * 16;  // routes per sweep (the LDS holds their x slice)
+  for (int64_t c0 = start; c0 < end; c0 += sweep) {
+    const int64_t nrows = end - c0 < sweep ? end - c0 : sweep;
+    if (NCMAX == 1 || nrows <= 16)
+      moe_sweep<HDT, SDT, GU, GPB, 1>(a, xs, c0, nrows, slot, N, K, n, n_ok, wrow, sc, zp);
+    else if (NCMAX == 2 || nrows <= 32)
+      moe_sweep<HDT, SDT, GU, GPB, (NCMAX >= 2 ? 2 : 1)>(a, xs, c0, nrows, slot, N, K, n, n_ok, wrow, sc, zp);
+    else
+      moe_sweep<HDT, SDT, GU, GPB, NCMAX>(a, xs, c0, nrows, slot, N, K, n, n_ok, wrow, sc, zp);
+    __syncthreads();  // the next sweep overwrites xs
   }
 }
 
-template <int HDT, int SDT, int GPB>
-int launch_moe_mlp(const anna_mi_moe_mlp_args& a, hipStream_t st, dim3 g1, dim3 g2, size_t l1, size_t l2) {
-  if (l1 > 65536)
-    ANNA_CHECK(hipFuncSetAttribute((const void*)moe_int4_mlp_kernel<HDT, SDT, true, GPB>,
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)l1) == hipSuccess,
-               "anna_mi_moe_grouped_int4_mlp: cannot raise the LDS limit");
-  if (l2 > 65536)
-    ANNA_CHECK(hipFuncSetAttribute((const void*)moe_int4_mlp_kernel<HDT, SDT, false, GPB>,
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)l2) == hipSuccess,
-               "anna_mi_moe_grouped_int4_mlp: cannot raise the LDS limit");
-  hipLaunchKernelGGL((moe_int4_mlp_kernel<HDT, SDT, true, GPB>), g1, dim3(256), l1, st, a);
+}  // namespace
+
+namespace {
+template <int HDT, int SDT, int GPB, int NCMAX>
+int launch_moe_mlp_nc(const anna_mi_moe_mlp_args& a, hipStream_t st, dim3 g1, dim3 g2) {
+  const size_t lds = (size_t)NCMAX * 16 * MOE_XP * 2;
+  hipLaunchKernelGGL((moe_int4_mlp_kernel<HDT, SDT, true, GPB, NCMAX>), g1, dim3(256), lds, st, a);
   ANNA_LAUNCH_CHECK("moe_int4_mlp_kernel (gate, up)");
-  hipLaunchKernelGGL((moe_int4_mlp_kernel<HDT, SDT, false, GPB>), g2, dim3(256), l2, st, a);
+  hipLaunchKernelGGL((moe_int4_mlp_kernel<HDT, SDT, false, GPB, NCMAX>), g2, dim3(256), lds, st, a);
   ANNA_LAUNCH_CHECK("moe_int4_mlp_kernel (down)");
   return ANNA_MI_OK;
 }
 
+// sweep_chunks selects the kernel: 1, 2 or 4 chunks of 16 routes per sweep (3 runs as 4)
+template <int HDT, int SDT, int GPB>
+int launch_moe_mlp(const anna_mi_moe_mlp_args& a, hipStream_t st, dim3 g1, dim3 g2) {
+  anna_mi_moe_mlp_args b = a;
+  if (a.sweep_chunks <= 1) {
+    b.sweep_chunks = 1;
+    return launch_moe_mlp_nc<HDT, SDT, GPB, 1>(b, st, g1, g2);
+  }
+  if (a.sweep_chunks == 2) return launch_moe_mlp_nc<HDT, SDT, GPB, 2>(b, st, g1, g2);
+  b.sweep_chunks = 4;
+  return launch_moe_mlp_nc<HDT, SDT, GPB, 4>(b, st, g1, g2);
+}
 }  // namespace
 }  // namespace anna
 
@@ -452,8 +527,6 @@ extern "C" int anna_mi_moe_grouped_int4_mlp(const anna_mi_moe_mlp_args* ap, void
   ANNA_CHECK(a.group_size > 0 && a.group_size % 32 == 0, "group_size must be a positive multiple of 32");
   ANNA_CHECK(a.hidden_dim % 128 == 0 && a.intermediate_dim % 128 == 0,
              "anna_mi_moe_grouped_int4_mlp: hidden_dim and intermediate_dim must be multiples of 128");
-  ANNA_CHECK(a.hidden_dim <= 4096 && a.intermediate_dim <= 4096,
-             "anna_mi_moe_grouped_int4_mlp: hidden_dim and intermediate_dim must be <= 4096");
   ANNA_CHECK(a.hidden_packed_cols * 8 >= a.hidden_dim && a.intermediate_packed_cols * 8 >= a.intermediate_dim,
              "anna_mi_moe_grouped_int4_mlp: packed width smaller than the input dimension");
   ANNA_CHECK(a.hidden_groups * a.group_size >= a.hidden_dim && a.intermediate_groups * a.group_size >= a.intermediate_dim,
@@ -462,24 +535,24 @@ extern "C" int anna_mi_moe_grouped_int4_mlp(const anna_mi_moe_mlp_args* ap, void
                  a.active_slots && a.activation && a.gate_qweight && a.gate_qscale && a.gate_qzeros && a.up_qweight &&
                  a.up_qscale && a.up_qzeros && a.down_qweight && a.down_qscale && a.down_qzeros,
              "anna_mi_moe_grouped_int4_mlp: null pointer");
+  ANNA_CHECK(a.sweep_chunks >= 1 && a.sweep_chunks <= MOE_MAXC, "anna_mi_moe_grouped_int4_mlp: sweep_chunks must be 1..4");
   if (a.routes == 0) return ANNA_MI_OK;
   hipStream_t st = as_stream(stream);
   const dim3 g1((unsigned)((a.intermediate_dim + MOE_ROWS - 1) / MOE_ROWS), (unsigned)a.active_count);
   const dim3 g2((unsigned)((a.hidden_dim + MOE_ROWS - 1) / MOE_ROWS), (unsigned)a.active_count);
-  const size_t l1 = (size_t)MOE_CHUNK * (a.hidden_dim + 8) * 2, l2 = (size_t)MOE_CHUNK * (a.intermediate_dim + 8) * 2;
   const int gpb = a.group_size >= 128 ? 1 : (int)(128 / a.group_size);
   ANNA_CHECK(a.group_size % 128 == 0 || gpb * a.group_size == 128,
              "anna_mi_moe_grouped_int4_mlp: group_size must be 32, 64 or a multiple of 128");
   ANNA_DISPATCH_DTYPE(a.dtype, HDT, {
     ANNA_DISPATCH_DTYPE(a.scale_dtype, SDT, {
       if (gpb == 1) {
-        const int rc = launch_moe_mlp<HDT, SDT, 1>(a, st, g1, g2, l1, l2);
+        const int rc = launch_moe_mlp<HDT, SDT, 1>(a, st, g1, g2);
         if (rc != ANNA_MI_OK) return rc;
       } else if (gpb == 2) {
-        const int rc = launch_moe_mlp<HDT, SDT, 2>(a, st, g1, g2, l1, l2);
+        const int rc = launch_moe_mlp<HDT, SDT, 2>(a, st, g1, g2);
         if (rc != ANNA_MI_OK) return rc;
       } else {
-        const int rc = launch_moe_mlp<HDT, SDT, 4>(a, st, g1, g2, l1, l2);
+        const int rc = launch_moe_mlp<HDT, SDT, 4>(a, st, g1, g2);
         if (rc != ANNA_MI_OK) return rc;
       }
     });

@@ -537,7 +537,8 @@ def moe_combine(compact_outputs, route_pos, num_tokens, top_k, out=None):
 
 def moe_mlp_args(compact_hidden_states, compact_routing_weights, compact_outputs, expert_offsets, active_experts,
                  active_slots, gate_qweight, gate_qscale, gate_qzeros, up_qweight, up_qscale, up_qzeros,
-                 down_qweight, down_qscale, down_qzeros, group_size, activation) -> _lib.MoeMlpArgs:
+                 down_qweight, down_qscale, down_qzeros, group_size, activation,
+                 max_routes_per_expert) -> _lib.MoeMlpArgs:
     a = _lib.MoeMlpArgs()
     a.dtype = _lib.dtype_code(compact_hidden_states.dtype)
     a.scale_dtype = _lib.dtype_code(gate_qscale.dtype)
@@ -553,6 +554,7 @@ def moe_mlp_args(compact_hidden_states, compact_routing_weights, compact_outputs
     a.intermediate_packed_cols, a.intermediate_groups = down_qweight.shape[2], down_qscale.shape[1]
     a.group_size = int(group_size)
     a.activation = activation.data_ptr()
+    a.sweep_chunks = min(4, max(1, -(-int(max_routes_per_expert) // 16)))
     return a
 
 
@@ -593,7 +595,7 @@ def moe_grouped_int4_mlp_out(compact_hidden_states, compact_routing_weights, com
     if activation is None:
         activation = torch.empty((x.shape[0], gate_qweight.shape[1]), dtype=torch.float32, device=x.device)
     a = moe_mlp_args(x, cw, compact_outputs, expert_offsets.contiguous(), active_experts.contiguous(),
-                     active_slots.contiguous(), *bank, group_size, activation)
+                     active_slots.contiguous(), *bank, group_size, activation, max_routes_per_expert)
     _lib.call("anna_mi_moe_grouped_int4_mlp", ctypes.byref(a), _lib.stream_of(x))
     return compact_outputs
 

@@ -88,8 +88,11 @@ class SparseMoeInt4:
         _, offsets, compact, cw = fused_ops.moe_dispatch(hidden_states, w.to(hidden_states.dtype), sel, usage,
                                                           route_pos=route_pos)
         compact_out = torch.empty_like(compact)
+        # Routes per expert are only known on the device; the kernels sweep an expert's routes in
+        # as many passes as it needs, so this hint (twice the mean load) only sizes the sweep.
+        hint = min(t * self.top_k, 2 * -(-t * self.top_k // self.num_experts) + 8)
         fused_ops.moe_grouped_int4_mlp_out(compact, cw, compact_out, offsets, self.active_experts, self.active_slots,
-                                           *self.bank.tensors(), self.bank.group_size, max(1, t * self.top_k))
+                                           *self.bank.tensors(), self.bank.group_size, max(1, hint))
         return fused_ops.moe_combine(compact_out, route_pos, t, self.top_k)
 
     __call__ = forward

@@ -385,8 +385,9 @@ def section_moe(args, device):
         sti, off, compact, cw = fused_ops.moe_dispatch(x, w.to(torch.bfloat16), sel, usage)
         co = torch.empty_like(compact)
         act = torch.empty((compact.shape[0], 512), dtype=torch.float32, device=device)
+        max_routes = int(usage.max())  # host-known, as the reference caller passes it (ops.py:3430-3440)
         mlp = [(lambda b=b: fused_ops.moe_grouped_int4_mlp_out(compact, cw, co, off, blocks[0].active_experts,
-                                                               blocks[0].active_slots, *b.tensors(), 128, tokens * 8,
+                                                               blocks[0].active_slots, *b.tensors(), 128, max_routes,
                                                                activation=act)) for b in banks]
         full = [(lambda blk=blk: blk(x, logits)) for blk in blocks]
         ms_mlp = time_graph(mlp, args.steps, args.warmup)

@@ -310,6 +310,8 @@ typedef struct {
   const int8_t* down_qzeros;
   int64_t hidden_packed_cols, hidden_groups, intermediate_packed_cols, intermediate_groups, group_size;
   float* activation;              /* workspace fp32 [routes][intermediate] */
+  int sweep_chunks;               /* 1..4: routes an expert takes per sweep over its weights, in
+                                     chunks of 16; size it from the largest route count per expert */
 } anna_mi_moe_mlp_args;
 
 int64_t anna_mi_sizeof_moe_mlp_args(void);
