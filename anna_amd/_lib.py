@@ -101,6 +101,11 @@ PROTOTYPES.update({
     "anna_mi_moe_scatter": [_P, _I, _I64, _I64, _P, _I64, _P, _P, _P],
     "anna_mi_moe_combine": [_P, _I, _I64, _P, _I64, _I64, _P, _P],
     "anna_mi_moe_grouped_int4_mlp": [ctypes.POINTER(MoeMlpArgs), _P],
+    "anna_mi_int4_gemv_tiled": [_P, _I, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I, _P, _I64, _I64, _I64, _I64,
+                                _I64, _P, _I, _I64, _P],
+    "anna_mi_topk_rows": [_P, _I64, _I64, _I64, _I64, _P, _I, _P, _P],
+    "anna_mi_lm_head_int4_topk": [_P, _I, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I, _P, _I64, _I64, _I64, _I64,
+                                  _I64, _I64, _P, _P, _P, _P],
 })
 # entry points that do not return a status code
 RAW_PROTOTYPES: dict[str, tuple] = {

@@ -1,0 +1,268 @@
+// Tiled int4 GEMV (the LM-head weight layout) and the fused LM-head top-k on gfx950.
+//
+// Layout (reference quantization.py:491-538, sycl:3272-3343): qweight int32 [N/T][Kp/8][T]
+// (T = 1, 2, 4, 8; T = 1 is the plain [N][Kp/8] layout), row n = T * tile + t, word w of row n
+// at [tile][w][t]; scale / zero point of (group g, row n) at g * ss_g + n * ss_n, which covers
+// [G][N] (ss_g = N, ss_n = 1; also the tiled [G][N/T][T]) and the LM-head top-k layout [N][G]
+// (ss_g = 1, ss_n = G).  w = (q - z) * s.
+//
+//   int4_gemv_tiled_kernel  one wave per tile: lane l walks words l, l + 64, ... of the tile;
+//                           each word is one T x 4-byte coalesced load (8 k of T rows) used
+//                           against 8 activations of up to MR rows; fp32 accumulation
+//                           (s * (sum x q - z sum x) per word), wave reduction at the end.
+//   topk_rows_kernel        per row: 128 threads keep sorted top-k lists of their strided share
+//                           of the logits, merged pairwise in LDS (descending, ties to the
+//                           lower index).
+#include "common.hpp"
+
+namespace anna {
+namespace {
+
+constexpr int TG_MR = 4;  // activation rows per weight pass
+
+template <int T>
+struct TileWords {
+  uint32_t v[T];
+};
+
+template <int T>
+__device__ __forceinline__ TileWords<T> load_tile_words(const uint32_t* p) {
+  TileWords<T> r;
+  if constexpr (T == 8) {
+    const u32x4 a = *(const u32x4*)p, b = *(const u32x4*)(p + 4);
+    r.v[0] = a.x, r.v[1] = a.y, r.v[2] = a.z, r.v[3] = a.w, r.v[4] = b.x, r.v[5] = b.y, r.v[6] = b.z, r.v[7] = b.w;
+  } else if constexpr (T == 4) {
+    const u32x4 a = *(const u32x4*)p;
+    r.v[0] = a.x, r.v[1] = a.y, r.v[2] = a.z, r.v[3] = a.w;
+  } else if constexpr (T == 2) {
+    const uint2 a = *(const uint2*)p;
+    r.v[0] = a.x, r.v[1] = a.y;
+  } else {
+    r.v[0] = *p;
+  }
+  return r;
+}
+
+// OUT_F32: y is fp32 (logits); otherwise y is in the activation dtype.
+template <int XDT, int SDT, int T, bool OUT_F32>
+__global__ __launch_bounds__(256) void int4_gemv_tiled_kernel(
+    const typename Elem<XDT>::T* __restrict__ x, int64_t M, int64_t K, int64_t xs, const uint32_t* __restrict__ qw,
+    int64_t tiles, int64_t pc, const typename Elem<SDT>::T* __restrict__ qs, const int8_t* __restrict__ qz,
+    int64_t ss_g, int64_t ss_n, int64_t gsz, int64_t N, void* __restrict__ y, int64_t ys) {
+  const int lane = threadIdx.x & 63;
+  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tile >= tiles) return;
+  const int64_t words = (K + 7) / 8;
+  const bool vec_x = (K % 8) == 0 && (xs % 8) == 0;
+  const uint32_t* tw = qw + tile * pc * T;
+  for (int64_t m0 = 0; m0 < M; m0 += TG_MR) {
+    float acc[TG_MR][T];
+#pragma unroll
+    for (int m = 0; m < TG_MR; ++m)
+#pragma unroll
+      for (int t = 0; t < T; ++t) acc[m][t] = 0.f;
+    for (int64_t w = lane; w < words; w += 64) {
+      const TileWords<T> q = load_tile_words<T>(tw + w * T);
+      const int64_t k0 = w * 8;
+      const int64_t g = k0 / gsz;
+      float s[T], z[T];
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const int64_t n = tile * T + t;
+        const int64_t nc = n < N ? n : 0;
+        s[t] = Elem<SDT>::load(qs, g * ss_g + nc * ss_n);
+        z[t] = (float)qz[g * ss_g + nc * ss_n];
+      }
+#pragma unroll
+      for (int m = 0; m < TG_MR; ++m) {
+        if (m0 + m >= M) continue;
+        float xv[8];
+        const int64_t row = (m0 + m) * xs;
+        bool done = false;
+        if constexpr (XDT != ANNA_MI_F32) {
+          if (vec_x) {
+            const u32x4 v = *(const u32x4*)((const uint16_t*)x + row + k0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              xv[2 * e] = Elem<XDT>::to_f32((uint16_t)(v[e] & 0xFFFFu));
+              xv[2 * e + 1] = Elem<XDT>::to_f32((uint16_t)(v[e] >> 16));
+            }
+            done = true;
+          }
+        }
+        if (!done) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) xv[e] = k0 + e < K ? Elem<XDT>::load(x, row + k0 + e) : 0.f;
+        }
+        float sx = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sx += xv[e];
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          float d = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) d = fmaf(xv[e], (float)((q.v[t] >> (4 * e)) & 0xFu), d);
+          acc[m][t] = fmaf(s[t], d - z[t] * sx, acc[m][t]);
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < TG_MR; ++m) {
+      if (m0 + m >= M) continue;
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const float v = wave_sum(acc[m][t]);
+        const int64_t n = tile * T + t;
+        if (lane == 0 && n < N) {
+          if constexpr (OUT_F32) ((float*)y)[(m0 + m) * ys + n] = v;
+          else ((typename Elem<XDT>::T*)y)[(m0 + m) * ys + n] = Elem<XDT>::cvt(v);
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ top-k
+
+constexpr int TK_THREADS = 128;
+constexpr int TK_MAX = 32;  // top_k handled per call (larger k: error)
+
+__device__ __forceinline__ bool tk_better(float va, int32_t ia, float vb, int32_t ib) {
+  return va > vb || (va == vb && ia < ib);
+}
+
+// grid (rows), 128 threads.  The values are fp32 [rows][ld]; out values in ODT.
+template <int ODT>
+__global__ __launch_bounds__(TK_THREADS) void topk_rows_kernel(const float* __restrict__ logits, int64_t V, int64_t ld,
+                                                              int k, typename Elem<ODT>::T* __restrict__ out_v,
+                                                              int64_t* __restrict__ out_i) {
+  __shared__ float s_v[TK_THREADS][TK_MAX];
+  __shared__ int32_t s_i[TK_THREADS][TK_MAX];
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const float* lg = logits + row * ld;
+  // thread-local sorted list in LDS (descending; ties to the lower index)
+  float* lv = s_v[tid];
+  int32_t* li = s_i[tid];
+  for (int j = 0; j < k; ++j) lv[j] = -INFINITY, li[j] = INT32_MAX;
+  for (int32_t n = tid; n < V; n += TK_THREADS) {
+    const float v = lg[n];
+    if (!tk_better(v, n, lv[k - 1], li[k - 1])) continue;
+    int j = k - 1;
+    while (j > 0 && tk_better(v, n, lv[j - 1], li[j - 1])) {
+      lv[j] = lv[j - 1], li[j] = li[j - 1];
+      --j;
+    }
+    lv[j] = v, li[j] = n;
+  }
+  __syncthreads();
+  // pairwise merge: list tid += list tid + half
+  for (int half = TK_THREADS / 2; half >= 1; half >>= 1) {
+    if (tid < half) {
+      float mv[TK_MAX];
+      int32_t mi[TK_MAX];
+      const float* bv = s_v[tid + half];
+      const int32_t* bi = s_i[tid + half];
+      int a = 0, b = 0;
+      for (int j = 0; j < k; ++j) {
+        if (tk_better(lv[a], li[a], bv[b], bi[b])) mv[j] = lv[a], mi[j] = li[a], ++a;
+        else mv[j] = bv[b], mi[j] = bi[b], ++b;
+      }
+      for (int j = 0; j < k; ++j) lv[j] = mv[j], li[j] = mi[j];
+    }
+    __syncthreads();
+  }
+  if (tid < k) {
+    out_v[row * k + tid] = Elem<ODT>::cvt(s_v[0][tid]);
+    out_i[row * k + tid] = s_i[0][tid];
+  }
+}
+
+template <int XDT, int SDT, bool OUT_F32>
+int launch_tiled(const void* x, int64_t M, int64_t K, int64_t xs, const uint32_t* qw, int64_t tiles, int64_t pc,
+                 int64_t T, const void* qs, const int8_t* qz, int64_t ssg, int64_t ssn, int64_t gsz, int64_t N, void* y,
+                 int64_t ys, hipStream_t st) {
+  using XT = typename Elem<XDT>::T;
+  using ST = typename Elem<SDT>::T;
+  const dim3 grid((unsigned)((tiles + 3) / 4));
+#define ANNA_TILED_LAUNCH(TT)                                                                                  \
+  hipLaunchKernelGGL((int4_gemv_tiled_kernel<XDT, SDT, TT, OUT_F32>), grid, dim3(256), 0, st, (const XT*)x, M, K, \
+                     xs, qw, tiles, pc, (const ST*)qs, qz, ssg, ssn, gsz, N, y, ys)
+  switch (T) {
+    case 1: ANNA_TILED_LAUNCH(1); break;
+    case 2: ANNA_TILED_LAUNCH(2); break;
+    case 4: ANNA_TILED_LAUNCH(4); break;
+    case 8: ANNA_TILED_LAUNCH(8); break;
+    default: set_error("output tile must be 1, 2, 4 or 8 (got %lld)", (long long)T); return ANNA_MI_EINVAL;
+  }
+#undef ANNA_TILED_LAUNCH
+  ANNA_LAUNCH_CHECK("int4_gemv_tiled_kernel");
+  return ANNA_MI_OK;
+}
+
+int check_tiled(const void* x, int64_t M, int64_t K, int64_t xs, const uint32_t* qw, int64_t tiles, int64_t pc,
+                int64_t T, const void* qs, const int8_t* qz, int64_t G, int64_t gsz, int64_t N) {
+  ANNA_CHECK(x && qw && qs && qz, "int4 tiled GEMV: null pointer");
+  ANNA_CHECK(M >= 0 && K > 0 && xs >= K, "int4 tiled GEMV: bad activation shape");
+  ANNA_CHECK(tiles > 0 && pc * 8 >= K, "qweight packed columns are smaller than in_features");
+  ANNA_CHECK(tiles * T >= N && N > 0, "qweight output tiles are smaller than out_features");
+  ANNA_CHECK(gsz > 0 && gsz % 8 == 0 && G * gsz >= K, "qscale group count is smaller than in_features");
+  return ANNA_MI_OK;
+}
+
+}  // namespace
+}  // namespace anna
+
+using namespace anna;
+
+extern "C" int anna_mi_int4_gemv_tiled(const void* x, int x_dtype, int64_t M, int64_t K, int64_t x_row_stride,
+                                       const int32_t* qweight, int64_t tiles, int64_t packed_cols, int64_t tile,
+                                       const void* qscale, int scale_dtype, const int8_t* qzeros, int64_t group_count,
+                                       int64_t scale_stride_group, int64_t scale_stride_row, int64_t group_size,
+                                       int64_t N, void* y, int y_is_f32, int64_t y_row_stride, void* stream) {
+  const int rc = check_tiled(x, M, K, x_row_stride, (const uint32_t*)qweight, tiles, packed_cols, tile, qscale, qzeros,
+                             group_count, group_size, N);
+  if (rc != ANNA_MI_OK) return rc;
+  ANNA_CHECK(y != nullptr && y_row_stride >= N, "anna_mi_int4_gemv_tiled: bad output");
+  if (M == 0) return ANNA_MI_OK;
+  ANNA_DISPATCH_DTYPE(x_dtype, XDT, {
+    ANNA_DISPATCH_DTYPE(scale_dtype, SDT, {
+      return y_is_f32 ? launch_tiled<XDT, SDT, true>(x, M, K, x_row_stride, (const uint32_t*)qweight, tiles,
+                                                     packed_cols, tile, qscale, qzeros, scale_stride_group,
+                                                     scale_stride_row, group_size, N, y, y_row_stride, as_stream(stream))
+                      : launch_tiled<XDT, SDT, false>(x, M, K, x_row_stride, (const uint32_t*)qweight, tiles,
+                                                      packed_cols, tile, qscale, qzeros, scale_stride_group,
+                                                      scale_stride_row, group_size, N, y, y_row_stride,
+                                                      as_stream(stream));
+    });
+  });
+  return ANNA_MI_OK;
+}
+
+extern "C" int anna_mi_topk_rows(const float* values, int64_t rows, int64_t V, int64_t ld, int64_t top_k,
+                                 void* out_values, int out_dtype, int64_t* out_indices, void* stream) {
+  ANNA_CHECK(values && out_values && out_indices, "anna_mi_topk_rows: null pointer");
+  ANNA_CHECK(top_k >= 1 && top_k <= TK_MAX && top_k <= V, "top_k must be in [1, min(vocab_size, 32)]");
+  ANNA_CHECK(rows >= 0 && ld >= V && V < INT32_MAX, "anna_mi_topk_rows: bad shape");
+  if (rows == 0) return ANNA_MI_OK;
+  ANNA_DISPATCH_DTYPE(out_dtype, ODT, {
+    hipLaunchKernelGGL((topk_rows_kernel<ODT>), dim3((unsigned)rows), dim3(TK_THREADS), 0, as_stream(stream), values, V,
+                       ld, (int)top_k, (typename Elem<ODT>::T*)out_values, out_indices);
+  });
+  ANNA_LAUNCH_CHECK("topk_rows_kernel");
+  return ANNA_MI_OK;
+}
+
+extern "C" int anna_mi_lm_head_int4_topk(const void* x, int x_dtype, int64_t rows, int64_t K, int64_t x_row_stride,
+                                         const int32_t* qweight, int64_t tiles, int64_t packed_cols, int64_t tile,
+                                         const void* qscale, int scale_dtype, const int8_t* qzeros, int64_t group_count,
+                                         int64_t scale_stride_group, int64_t scale_stride_row, int64_t group_size,
+                                         int64_t vocab, int64_t top_k, float* logits, void* values, int64_t* indices,
+                                         void* stream) {
+  ANNA_CHECK(logits && values && indices, "anna_mi_lm_head_int4_topk: null pointer");
+  int rc = anna_mi_int4_gemv_tiled(x, x_dtype, rows, K, x_row_stride, qweight, tiles, packed_cols, tile, qscale,
+                                   scale_dtype, qzeros, group_count, scale_stride_group, scale_stride_row, group_size,
+                                   vocab, logits, 1, vocab, stream);
+  if (rc != ANNA_MI_OK) return rc;
+  return anna_mi_topk_rows(logits, rows, vocab, vocab, top_k, values, x_dtype, indices, stream);
+}

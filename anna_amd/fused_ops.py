@@ -41,6 +41,14 @@ SCHEMAS = {
         "Tensor(b!) partial_stats, Tensor(c!) partial_values, float scaling, int value_bits, int value_group_size, "
         "int block_size, Tensor? gate=None) -> Tensor(a!)"
     ),
+    "xpu_int4_gemv_tiled": (
+        "xpu_int4_gemv_tiled(Tensor hidden_states, Tensor qweight, Tensor qscale, Tensor qzeros, int group_size, "
+        "int in_features, int out_features) -> Tensor"
+    ),
+    "lm_head_int4_topk_fused": (
+        "lm_head_int4_topk_fused(Tensor hidden_states, Tensor qweight, Tensor qscale, Tensor qzeros, int group_size, "
+        "int in_features, int top_k) -> (Tensor, Tensor)"
+    ),
     "moe_router_fused": "moe_router_fused(Tensor router_logits, int top_k, bool normalize_topk_prob=True) -> (Tensor, Tensor, Tensor)",
     "moe_dispatch_fused": (
         "moe_dispatch_fused(Tensor hidden_states, Tensor routing_weights, Tensor selected_experts, "
@@ -450,6 +458,96 @@ def tq_values_dequant(data, scales, zeros, bits, group_size, out_dtype):
 
 
 
+
+# ---------------------------------------------------------------- tiled int4 GEMV, LM-head top-k
+# (sycl:3272-3343 xpu_int4_gemv_tiled, sycl:2137-2572 lm_head_int4_topk_fused)
+
+
+def _tiled_layout(qweight, qscale, qzeros, group_size, in_features, *, lm_head):
+    """-> (tiles, packed_cols, tile, rows N, group_count, scale stride per group, per row).
+    qweight [N/T, Kp/8, T] (or [N, Kp/8] for the LM head); qscale [G, N/T, T], [G, N] or, for the
+    LM head, [N, G] (validate_lm_head_int4_topk_inputs, sycl:1045-1086)."""
+    if qweight.dtype != torch.int32 or qzeros.dtype != torch.int8:
+        raise RuntimeError("qweight must be int32 and qzeros int8")
+    if qscale.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise RuntimeError("qscale must be float32, float16, or bfloat16")
+    if not (qweight.is_contiguous() and qscale.is_contiguous() and qzeros.is_contiguous()):
+        raise RuntimeError("qweight, qscale and qzeros must be contiguous")
+    if qzeros.shape != qscale.shape:
+        raise RuntimeError("qzeros shape must match qscale")
+    if group_size <= 0 or group_size % 8 != 0:
+        raise RuntimeError("group_size must be a positive multiple of 8")
+    if qweight.dim() == 3:
+        tiles, pc, tile = qweight.shape
+        if tile not in (1, 2, 4, 8):
+            raise RuntimeError("output_tile must be 1, 2, 4, or 8")
+    elif qweight.dim() == 2 and lm_head:
+        (tiles, pc), tile = qweight.shape, 1
+    else:
+        raise RuntimeError("qweight must be [output_tiles, packed_cols, output_tile]")
+    n = tiles * tile
+    if pc * 8 < in_features:
+        raise RuntimeError("qweight packed columns are smaller than in_features")
+    if qscale.dim() == 3 and not lm_head:
+        if qscale.shape[1] != tiles or qscale.shape[2] != tile:
+            raise RuntimeError("qscale must be [group_count, output_tiles, output_tile] matching qweight")
+        g, ssg, ssn = qscale.shape[0], n, 1
+    elif qscale.dim() == 2 and qscale.shape[1] == n and qscale.shape[0] * group_size >= in_features:
+        g, ssg, ssn = qscale.shape[0], n, 1
+    elif lm_head and qscale.dim() == 2 and qscale.shape[0] == n and qscale.shape[1] * group_size >= in_features:
+        g, ssg, ssn = qscale.shape[1], 1, qscale.shape[1]
+    else:
+        raise RuntimeError("qscale must be [group_count, vocab_size] or lm_head top-k layout [vocab_size, group_count]")
+    if g * group_size < in_features:
+        raise RuntimeError("qscale group count is smaller than in_features")
+    return tiles, pc, tile, n, g, ssg, ssn
+
+
+def int4_gemv_tiled(hidden_states, qweight, qscale, qzeros, group_size, in_features, out_features):
+    """y [M, out_features] = x . dequant(W)^T on the tiled layout, in x's dtype."""
+    if hidden_states.dim() != 2 or hidden_states.shape[1] != in_features:
+        raise RuntimeError("xpu_int4_gemv_tiled expects hidden_states shaped [rows, in_features]")
+    _check_same_device("xpu_int4_gemv_tiled", hidden_states, qweight, qscale, qzeros)
+    tiles, pc, tile, n, g, ssg, ssn = _tiled_layout(qweight, qscale, qzeros, group_size, in_features, lm_head=False)
+    if n < out_features or out_features <= 0:
+        raise RuntimeError("qweight output tiles are smaller than out_features")
+    x = hidden_states if hidden_states.stride(1) == 1 else hidden_states.contiguous()
+    y = torch.empty((x.shape[0], out_features), dtype=x.dtype, device=x.device)
+    _lib.call("anna_mi_int4_gemv_tiled", x.data_ptr(), _lib.dtype_code(x.dtype), x.shape[0], in_features, x.stride(0),
+              qweight.data_ptr(), tiles, pc, tile, qscale.data_ptr(), _lib.dtype_code(qscale.dtype), qzeros.data_ptr(), g,
+              ssg, ssn, int(group_size), int(out_features), y.data_ptr(), 0, out_features, _lib.stream_of(x))
+    return y
+
+
+def lm_head_int4_topk(hidden_states, qweight, qscale, qzeros, group_size, in_features, top_k):
+    """(values [..., k] in x's dtype, indices [..., k] int64) of the fp32 int4 logits, descending
+    (ties to the lower vocabulary index)."""
+    if hidden_states.dim() < 2 or hidden_states.shape[-1] != in_features:
+        raise RuntimeError("hidden_states hidden_dim must match in_features")
+    _check_same_device("lm_head_int4_topk_fused", hidden_states, qweight, qscale, qzeros)
+    tiles, pc, tile, vocab, g, ssg, ssn = _tiled_layout(qweight, qscale, qzeros, group_size, in_features, lm_head=True)
+    if not (1 <= top_k <= vocab):
+        raise RuntimeError("top_k must be in [1, vocab_size]")
+    lead = hidden_states.shape[:-1]
+    x = hidden_states.reshape(-1, in_features)
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    rows = x.shape[0]
+    logits = torch.empty((rows, vocab), dtype=torch.float32, device=x.device)
+    values = torch.empty((rows, top_k), dtype=x.dtype, device=x.device)
+    indices = torch.empty((rows, top_k), dtype=torch.int64, device=x.device)
+    _lib.call("anna_mi_lm_head_int4_topk", x.data_ptr(), _lib.dtype_code(x.dtype), rows, in_features, x.stride(0),
+              qweight.data_ptr(), tiles, pc, tile, qscale.data_ptr(), _lib.dtype_code(qscale.dtype), qzeros.data_ptr(),
+              g, ssg, ssn, int(group_size), vocab, int(top_k), logits.data_ptr(), values.data_ptr(), indices.data_ptr(),
+              _lib.stream_of(x))
+    return values.view(*lead, top_k), indices.view(*lead, top_k)
+
+
+def _lm_head_topk_meta(hidden_states, qweight, qscale, qzeros, group_size, in_features, top_k):
+    lead = hidden_states.shape[:-1]
+    return (hidden_states.new_empty((*lead, top_k)), hidden_states.new_empty((*lead, top_k), dtype=torch.int64))
+
+
 # ---------------------------------------------------------------- MoE (sycl:3716-4324, ops.py:3280-3457)
 
 
@@ -622,6 +720,8 @@ _IMPLS = {
         _gqa_decode_splitkv_turboquant_fused_out_impl,
         lambda q, qk, vd, vs, vz, rk, rv, out, *a, **kw: out,
     ),
+    "xpu_int4_gemv_tiled": (int4_gemv_tiled, lambda x, qw, qs, qz, g, k, n: x.new_empty((x.shape[0], n))),
+    "lm_head_int4_topk_fused": (lm_head_int4_topk, _lm_head_topk_meta),
     "moe_router_fused": (moe_router, _moe_router_meta),
     "moe_dispatch_fused": (moe_dispatch, _moe_dispatch_meta),
     "moe_scatter_fused": (moe_scatter, lambda co, sti, n: co.new_empty((n, co.shape[1]))),
@@ -707,3 +807,18 @@ def run_moe_grouped_int4_mlp_fused(*, compact_hidden_states, compact_routing_wei
         compact_hidden_states, compact_routing_weights, compact_outputs, expert_offsets, active_experts, active_slots,
         gate_qweight, gate_qscale, gate_qzeros, up_qweight, up_qscale, up_qzeros, down_qweight, down_qscale,
         down_qzeros, int(group_size), int(max_routes_per_expert))
+
+
+def run_xpu_int4_gemv_tiled(*, hidden_states, qweight, qscale, qzeros, group_size, in_features, out_features):
+    return _op("xpu_int4_gemv_tiled")(hidden_states, qweight, qscale, qzeros, int(group_size), int(in_features),
+                                      int(out_features))
+
+
+def lm_head_int4_topk_fused_is_available() -> bool:
+    register_ops()
+    return True
+
+
+def run_lm_head_int4_topk_fused(*, hidden_states, qweight, qscale, qzeros, group_size, in_features, top_k):
+    return _op("lm_head_int4_topk_fused")(hidden_states, qweight, qscale, qzeros, int(group_size), int(in_features),
+                                          int(top_k))

@@ -245,6 +245,34 @@ int anna_mi_tq_decode(const anna_mi_tq_decode_args* args, void* stream);
  * value layout [tokens/32][2048] read by anna_mi_tq_decode.  Pure permutation. */
 int anna_mi_tq_block_values(const uint8_t* codes, int64_t tokens, uint8_t* blocked, void* stream);
 
+/* ------------------------------------------------------------------ tiled int4 GEMV, LM-head top-k */
+
+/* xpu_int4_gemv_tiled (sycl:3272-3343; layout quantization.py:491-538): qweight int32
+ * [tiles][packed_cols][tile] (tile 1, 2, 4 or 8; row n = tile*t_idx + t, word w at
+ * [n / tile][w][n % tile]; tile 1 is the plain [N][Kp/8] layout); the scale / zero point of
+ * (group g, row n) sits at g * scale_stride_group + n * scale_stride_row ([G][N] or [G][N/T][T]:
+ * (N, 1); the LM-head top-k layout [N][G]: (1, G)).  y [M][N] (row stride given) is fp32 when
+ * y_is_f32, else in the activation dtype. */
+int anna_mi_int4_gemv_tiled(const void* x, int x_dtype, int64_t M, int64_t K, int64_t x_row_stride,
+                            const int32_t* qweight, int64_t tiles, int64_t packed_cols, int64_t tile,
+                            const void* qscale, int scale_dtype, const int8_t* qzeros, int64_t group_count,
+                            int64_t scale_stride_group, int64_t scale_stride_row, int64_t group_size, int64_t N,
+                            void* y, int y_is_f32, int64_t y_row_stride, void* stream);
+
+/* Top-k of each row of fp32 values [rows][ld] (first V columns): values (in out_dtype) and
+ * int64 indices [rows][top_k], descending, ties to the lower index.  top_k <= 32. */
+int anna_mi_topk_rows(const float* values, int64_t rows, int64_t V, int64_t ld, int64_t top_k, void* out_values,
+                      int out_dtype, int64_t* out_indices, void* stream);
+
+/* lm_head_int4_topk_fused (sycl:2137-2572; caller qwen3_5_text_model.py:65-110): fp32 logits of
+ * the int4 LM head into the workspace `logits` [rows][vocab], then their top-k (values in the
+ * activation dtype). */
+int anna_mi_lm_head_int4_topk(const void* x, int x_dtype, int64_t rows, int64_t K, int64_t x_row_stride,
+                              const int32_t* qweight, int64_t tiles, int64_t packed_cols, int64_t tile,
+                              const void* qscale, int scale_dtype, const int8_t* qzeros, int64_t group_count,
+                              int64_t scale_stride_group, int64_t scale_stride_row, int64_t group_size, int64_t vocab,
+                              int64_t top_k, float* logits, void* values, int64_t* indices, void* stream);
+
 /* ------------------------------------------------------------------ MoE
  * Routing around the grouped expert MLP (Qwen3SparseMoeBlock, src/anna/model/ops.py:3280-3376). */
 

@@ -1,0 +1,78 @@
+"""Tiled int4 GEMV (xpu_int4_gemv_tiled) and the fused int4 LM-head top-k against the CPU
+dequant path.  Shapes follow the reference's tests (test_fused_op_xpu.py:260-375): indices
+exact, values within the reference's 2e-2; the GEMV within normwise relative error 1e-2."""
+
+import pytest
+import torch
+
+from anna_amd import fused_ops
+from anna_amd.quantization import XPUInt4Linear
+from oracle import cpu_paths as cp
+from tests._util import BF16_TOL, rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def quantized_linear(k, n, seed, device, group=32, dtype=torch.float16):
+    torch.manual_seed(seed)
+    dense = torch.nn.Linear(k, n, bias=False, dtype=torch.float32)
+    return XPUInt4Linear.from_linear(dense, group_size=group, compute_dtype=dtype, device=device)
+
+
+def dense_logits(q, x):
+    w = cp.int4_dequant_f32(q.qweight.cpu(), q.qscale.cpu(), q.qzeros.cpu(), q.group_size, q.in_features)
+    return x.cpu().double() @ w.double().t()
+
+
+@pytest.mark.parametrize("k,n,seed,layout", [(16, 31, 0, "plain"), (64, 96, 8, "lm_head"), (96, 192, 5, "plain"),
+                                             (2048, 1000, 3, "lm_head")])
+def test_lm_head_int4_topk_matches_quantized_reference(gpu, k, n, seed, layout):
+    q = quantized_linear(k, n, seed, gpu)
+    x = torch.randn(2, 3, k, device=gpu, dtype=torch.float16)
+    if layout == "lm_head":
+        q.prepare_lm_head_topk_layout()
+        tensors = (q.lm_head_qweight, q.lm_head_qscale, q.lm_head_qzeros)
+    else:
+        tensors = (q.qweight, q.qscale, q.qzeros)
+    values, indices = torch.ops.anna.lm_head_int4_topk_fused(x, *tensors, q.group_size, q.in_features, 5)
+    assert values.shape == (2, 3, 5) and indices.dtype == torch.long
+    ref = dense_logits(q, x.reshape(-1, k)).view(2, 3, n)
+    rv, ri = torch.topk(ref, 5, dim=-1)
+    assert torch.equal(indices.cpu(), ri)
+    torch.testing.assert_close(values.cpu().double(), rv, atol=2e-2, rtol=2e-2)
+    # the module forward picks the same top-k
+    mv, mi = torch.topk(q(x), 5, dim=-1)
+    assert torch.equal(indices, mi)
+
+
+@pytest.mark.parametrize("tile,sdt,m", [(1, torch.float32, 1), (2, torch.bfloat16, 3), (4, torch.float16, 5),
+                                        (8, torch.float32, 2)])
+def test_xpu_int4_gemv_tiled_matches_dequant(gpu, tile, sdt, m):
+    q = quantized_linear(256, 200, 11 + tile, gpu, group=64, dtype=torch.bfloat16)
+    n, pc = q.qweight.shape
+    n_pad = -(-n // tile) * tile
+    qw = torch.zeros((n_pad, pc), dtype=torch.int32, device=gpu)
+    qw[:n] = q.qweight
+    qs = torch.ones((q.qscale.shape[0], n_pad), dtype=sdt, device=gpu)
+    qs[:, :n] = q.qscale.to(sdt)
+    qz = torch.full((q.qzeros.shape[0], n_pad), 8, dtype=torch.int8, device=gpu)
+    qz[:, :n] = q.qzeros
+    qw_t = qw.view(n_pad // tile, tile, pc).permute(0, 2, 1).contiguous()
+    x = torch.randn(m, 256, device=gpu, dtype=torch.bfloat16)
+    y = torch.ops.anna.xpu_int4_gemv_tiled(x, qw_t, qs.view(-1, n_pad // tile, tile), qz.view(-1, n_pad // tile, tile),
+                                           64, 256, n)
+    assert y.shape == (m, n) and y.dtype == torch.bfloat16
+    w = cp.int4_dequant_f32(q.qweight.cpu(), q.qscale.to(sdt).cpu(), q.qzeros.cpu(), 64, 256)
+    ref = x.cpu().double() @ w.double().t()
+    assert rel_err(y.cpu().double().numpy(), ref.numpy()) <= BF16_TOL
+
+
+def test_lm_head_topk_errors(gpu):
+    q = quantized_linear(16, 31, 0, gpu)
+    x = torch.randn(1, 16, device=gpu, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="top_k"):
+        fused_ops.run_lm_head_int4_topk_fused(hidden_states=x, qweight=q.qweight, qscale=q.qscale, qzeros=q.qzeros,
+                                              group_size=32, in_features=16, top_k=40)
+    with pytest.raises(RuntimeError, match="in_features"):
+        fused_ops.run_lm_head_int4_topk_fused(hidden_states=x, qweight=q.qweight, qscale=q.qscale, qzeros=q.qzeros,
+                                              group_size=32, in_features=8, top_k=3)
