@@ -14,7 +14,8 @@
 //                    128-k block with a row sum of x that a second MFMA against an
 //                    all-ones operand produces in the same C layout:
 //                       sum_k x (q - z) s = s * (sum_k x (off + q) - (off + z) sum_k x).
-//   int4_gemm_mfma   M > 16.  LDS-tiled: a 128x128 tile of W is dequantized once per
+//   (M >= 64 with 16-bit activations, K % 64 == 0: int4_gemm_tiled_kernel, int4_gemm.hip)
+//   int4_gemm_mfma   other M > 16.  LDS-tiled: a 128x128 tile of W is dequantized once per
 //                    workgroup to bf16 ((q - z) * s rounded to bf16, the reference's
 //                    dequant numerics) next to a 128x128 tile of x, and 4 waves run
 //                    v_mfma_f32_32x32x16_bf16 on it.
@@ -25,6 +26,7 @@
 
 #include "common.hpp"
 #include "int4_frag.hpp"
+#include "int4_gemm.hpp"
 
 namespace anna {
 namespace {
@@ -737,6 +739,8 @@ extern "C" int anna_mi_int4_linear(const void* x, int x_dtype, int64_t M, int64_
     ANNA_LAUNCH_CHECK("int4_gemv_mfma");
     return ANNA_MI_OK;
   }
+  if (int4_gemm_tiled_supported(x_dtype, M, K, xs, x, qweight, pc, gsz))
+    return int4_gemm_tiled_launch(x, x_dtype, M, K, xs, qweight, N, pc, qscale, scale_dtype, qzeros, gsz, y, st);
   if (x_dtype == ANNA_MI_BF16 && aligned && M > 16) {
     dim3 grid((unsigned)((N + GB_N - 1) / GB_N), (unsigned)((M + GB_M - 1) / GB_M), 1);
     ANNA_DISPATCH_DTYPE(scale_dtype, SDT, {

@@ -41,6 +41,9 @@ LINEAR_CASES = [
     (1, 96, 40, 32, "fp32"),        # group 32 on the dot2 GEMV, partial k-slice
     (2, 9216, 72, 128, "bf16"),     # dot2 GEMV with more k-slices than waves
     (1, 4096, 12288, 128, "bf16"),  # benchmark config 2, M = 1
+    (300, 512, 400, 64, "bf16"),    # tiled GEMM: group 64, M and N tails
+    (2048, 4096, 192, 128, "bf16"), # tiled GEMM at the config-2 M and K
+    (64, 4096, 6144, 128, "fp32"),  # tiled GEMM, config-2 N = 6144 at M = 64
 ]
 
 
@@ -59,7 +62,7 @@ def test_int4_linear_matches_oracle(gpu, m, k, n, group, sdt):
 
 
 @pytest.mark.parametrize("xdt", [torch.float16, torch.float32])
-@pytest.mark.parametrize("m", [1, 4])
+@pytest.mark.parametrize("m", [1, 4, 128])
 def test_int4_linear_other_activation_dtypes(gpu, xdt, m):
     rng = np.random.default_rng(7)
     k, n, group = 1024, 192, 128
