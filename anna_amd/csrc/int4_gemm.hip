@@ -9,8 +9,9 @@
 //                  and write both to the LDS buffer of the next step.
 // The two roles run between the same barriers (one per k-step, double-buffered LDS, 126 KB), so
 // each SIMD issues the loaders' VALU work while its MFMA waves keep the matrix core busy.  The
-// tile -> workgroup map is XCD-aware (the m-tiles of an n-tile share one XCD's L2); M = 2048
-// with N = 12288 gives 512 tiles (two rounds on 256 CUs), N = 6144 gives 256.
+// tile -> workgroup map is XCD-aware and m-major: the n-tiles of one m-tile share one XCD, so
+// that XCD's L2 holds the m-tile's slice of x (256 x K, 2 MB at K = 4096) and only the small
+// int4 W streams in; M = 2048 with N = 12288 gives 512 tiles (two rounds on 256 CUs).
 #include <type_traits>
 
 #include "common.hpp"
@@ -52,8 +53,12 @@ __global__ __launch_bounds__(GM_THREADS) void int4_gemm_tiled_kernel(
   using ST = typename Elem<SDT>::T;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int64_t t = xcd_tile(blockIdx.x, tiles_m * tiles_n);
-  const int64_t m0 = (t % tiles_m) * GM_BM, n0 = (t / tiles_m) * GM_BN;
+  // tile coordinates in 32-bit scalar registers: a value the compiler cannot prove uniform
+  // would turn every buffer load below into a loop over distinct descriptors
+  const int t = __builtin_amdgcn_readfirstlane((int)xcd_tile(blockIdx.x, tiles_m * tiles_n));
+  const int tn32 = (int)tiles_n;
+  const int64_t m0 = (int64_t)__builtin_amdgcn_readfirstlane((t / tn32) * GM_BM);
+  const int64_t n0 = (int64_t)__builtin_amdgcn_readfirstlane((t % tn32) * GM_BN);
   const int64_t nk = K / GM_BK;
 
   if (wave >= GM_MFMA_WAVES) {
@@ -83,17 +88,23 @@ __global__ __launch_bounds__(GM_THREADS) void int4_gemm_tiled_kernel(
       uint2 w[GM_WPT];
       uint32_t sc[GM_WPT], z[GM_WPT];
     };
-    auto load = [&](int64_t ks, Stage& S) {
-      ks = ks < nk ? ks : nk - 1;
+    // group of k-step ks = ks / (gsz / 64) as a multiply-high by ceil(2^32 / (gsz / 64)) (one
+    // group per step needs no map): exact while both are below 2^16 (checked by the launcher);
+    // a division here would branch and make the loads just issued wait
+    const uint32_t spg = (uint32_t)(gsz / GM_BK);
+    const uint32_t ginv = spg > 1 ? (uint32_t)(((1ull << 32) + spg - 1) / spg) : 0u;
+    const int nk32 = (int)nk;
+    auto load = [&](int ks, Stage& S) {
+      ks = ks < nk32 ? ks : nk32 - 1;
 #pragma unroll
       for (int i = 0; i < GM_XPT; ++i)
         S.x[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                               rx, xo, (int)(i * 32 * xs * 2 + ks * GM_BK * 2), 0));
-      const int64_t g = ks * GM_BK / gsz;
+                                               rx, xo, (int)(i * 32 * xs * 2) + ks * (GM_BK * 2), 0));
+      const int g = spg == 1 ? ks : (int)__umulhi((uint32_t)ks, ginv);
 #pragma unroll
       for (int i = 0; i < GM_WPT; ++i) {
         S.w[i] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
-                                               rw, wo, (int)(i * 64 * pc * 4 + ks * GM_BK / 2), 0));
+                                               rw, wo, (int)(i * 64 * pc * 4) + ks * (GM_BK / 2), 0));
         if constexpr (sizeof(ST) == 4)
           S.sc[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, so, (int)((g * N + 64 * i) * 4), 0);
         else
@@ -134,14 +145,14 @@ __global__ __launch_bounds__(GM_THREADS) void int4_gemm_tiled_kernel(
     load(1, S1);
     store(S0, 0);
     __syncthreads();
-    for (int64_t ks = 0; ks < nk; ks += 2) {
+    for (int ks = 0; ks < nk32; ks += 2) {
       // step ks: MFMA waves read buffer 0; store step ks + 1 into buffer 1
       load(ks + 2, S0);
-      if (ks + 1 < nk) store(S1, 1);
+      if (ks + 1 < nk32) store(S1, 1);
       __syncthreads();
-      if (ks + 1 >= nk) break;
+      if (ks + 1 >= nk32) break;
       load(ks + 3, S1);
-      if (ks + 2 < nk) store(S0, 0);
+      if (ks + 2 < nk32) store(S0, 0);
       __syncthreads();
     }
     return;
@@ -193,10 +204,13 @@ __global__ __launch_bounds__(GM_THREADS) void int4_gemm_tiled_kernel(
 
 }  // namespace
 
-bool int4_gemm_tiled_supported(int x_dtype, int64_t M, int64_t K, int64_t xs, const void* x, const void* qweight,
+bool int4_gemm_tiled_supported(int x_dtype, int64_t M, int64_t N, int64_t K, int64_t xs, const void* x, const void* qweight,
                                int64_t pc, int64_t gsz) {
-  // buffer loads address each workgroup's slice with 32-bit offsets
-  const bool fits = (int64_t)GM_BM * xs * 2 < (1ll << 31) && (int64_t)GM_BN * pc * 4 < (1ll << 31);
+  // buffer loads address each workgroup's slice with 32-bit offsets, and the k-step -> group map
+  // is a multiply-high that is exact below 2^16 steps
+  const int64_t G = gsz > 0 ? (K + gsz - 1) / gsz : 0;
+  const bool fits = (int64_t)GM_BM * xs * 2 < (1ll << 31) && (int64_t)GM_BN * pc * 4 < (1ll << 31) &&
+                    G * N * 4 < (1ll << 31) && K / GM_BK < (1 << 16) && gsz / GM_BK < (1 << 16);
   return (x_dtype == ANNA_MI_BF16 || x_dtype == ANNA_MI_F16) && M >= 64 && K % GM_BK == 0 && gsz % GM_BK == 0 &&
          xs % 8 == 0 && pc % 4 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)qweight % 16 == 0 && fits;
 }

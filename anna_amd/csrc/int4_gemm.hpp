@@ -5,7 +5,7 @@
 
 namespace anna {
 
-bool int4_gemm_tiled_supported(int x_dtype, int64_t M, int64_t K, int64_t xs, const void* x, const void* qweight,
+bool int4_gemm_tiled_supported(int x_dtype, int64_t M, int64_t N, int64_t K, int64_t xs, const void* x, const void* qweight,
                                int64_t pc, int64_t gsz);
 
 int int4_gemm_tiled_launch(const void* x, int x_dtype, int64_t M, int64_t K, int64_t xs, const int32_t* qweight,
