@@ -3,15 +3,20 @@
 // Tile 256 (m) x 192 (n) x 64 (k) per workgroup of 12 waves with two roles:
 //   8 MFMA waves   a 2 x 4 grid, each owning 128 x 48 of C as 8 x 3 v_mfma_f32_16x16x32
 //                  accumulators; they only read LDS;
-//   4 loader waves (one per SIMD) load x (256 x 64, 16-bit) and the int4 words of W (192 rows
-//                  x 64 k) two k-steps ahead, dequantize W to (q - z) * s in fp32 rounded to the
-//                  activation dtype (the reference's dequant numerics, quantization.py:626-648)
-//                  and write both to the LDS buffer of the next step.
-// The two roles run between the same barriers (one per k-step, double-buffered LDS, 126 KB), so
-// each SIMD issues the loaders' VALU work while its MFMA waves keep the matrix core busy.  The
-// tile -> workgroup map is XCD-aware and m-major: the n-tiles of one m-tile share one XCD, so
-// that XCD's L2 holds the m-tile's slice of x (256 x K, 2 MB at K = 4096) and only the small
-// int4 W streams in; M = 2048 with N = 12288 gives 512 tiles (two rounds on 256 CUs).
+//   4 loader waves (one per SIMD) copy the x tile (256 x 64, 16-bit) straight from memory into
+//                  LDS (buffer loads with the LDS destination, two k-steps ahead, three
+//                  buffers), and load the int4 words of W (192 rows x 64 k) two steps ahead into
+//                  registers, dequantize them to (q - z) * s in fp32 rounded to the activation
+//                  dtype (the reference's dequant numerics, quantization.py:626-648) and write
+//                  them to the LDS buffer of the next step (two buffers).
+// The two roles run between the same barriers (one per k-step), so each SIMD issues the
+// loaders' VALU work while its MFMA waves keep the matrix core busy.  LDS rows are 64 elements
+// (128 B) with the 16-byte chunk c of row r stored at slot c ^ (r & 7): the 16 lanes of an MFMA
+// operand read (16 consecutive rows, one chunk) then touch 8 distinct slots per 8 rows, and an
+// 8-row block is exactly the 1 KB one wave-wide LDS-destination load writes.  The tile ->
+// workgroup map is XCD-aware and m-major: the n-tiles of one m-tile share one XCD, so that XCD's
+// L2 holds the m-tile's slice of x (256 x K, 2 MB at K = 4096) and only the small int4 W streams
+// in; M = 2048 with N = 12288 gives 512 tiles (two rounds on 256 CUs).
 #include <type_traits>
 
 #include "common.hpp"
@@ -22,18 +27,31 @@ namespace anna {
 namespace {
 
 constexpr int GM_BM = 256, GM_BN = 192, GM_BK = 64;
-constexpr int GM_PITCH = GM_BK + 8;  // LDS row pitch (16-bit elements): rows land 4 banks apart
 constexpr int GM_MFMA_WAVES = 8, GM_LOAD_WAVES = 4;
 constexpr int GM_THREADS = 64 * (GM_MFMA_WAVES + GM_LOAD_WAVES);
-constexpr int GM_LT = 64 * GM_LOAD_WAVES;  // loader threads
-constexpr int GM_LDS_A = GM_BM * GM_PITCH, GM_LDS_B = GM_BN * GM_PITCH;  // elements per stage
-constexpr size_t GM_LDS_BYTES = (size_t)2 * (GM_LDS_A + GM_LDS_B) * 2;
-constexpr int GM_XPT = GM_BM * GM_BK / 8 / GM_LT;        // x chunks (16 B) per loader thread: 8
-constexpr int GM_WPT = GM_BN * (GM_BK / 16) / GM_LT;     // W chunks (8 B = 16 nibbles) per loader thread: 3
+constexpr int GM_LT = 64 * GM_LOAD_WAVES;                 // loader threads
+constexpr int GM_NA = 3, GM_NB = 2;                       // LDS buffers of x and of W
+constexpr int GM_LDS_A = GM_BM * GM_BK, GM_LDS_B = GM_BN * GM_BK;  // 16-bit elements per buffer
+constexpr size_t GM_LDS_BYTES = (size_t)(GM_NA * GM_LDS_A + GM_NB * GM_LDS_B) * 2;  // 144 KB
+constexpr int GM_XLD = GM_BM / 8 / GM_LOAD_WAVES;         // 8-row x blocks per loader wave: 8
+constexpr int GM_WPT = GM_BN * (GM_BK / 16) / GM_LT;      // W chunks (8 B = 16 nibbles) per loader thread: 3
+// vector-memory loads one loader thread issues per k-step: the x blocks plus word, scale and
+// zero point of each W chunk; the wait before each barrier keeps exactly these outstanding
+constexpr int GM_LOADS_PER_STEP = GM_XLD + 3 * GM_WPT;
+static_assert(GM_LOADS_PER_STEP == 17, "loader_barrier waits for vmcnt(17)");
+
+// The loader's end of a k-step: all but its 17 most recent loads have landed (so the previous
+// step's LDS-destination x loads are in LDS), its LDS writes are done, then the workgroup
+// barrier.  __syncthreads() would also wait for the loads just issued, since its release fence
+// covers LDS-destination loads.
+__device__ __forceinline__ void loader_barrier() {
+  asm volatile("s_waitcnt vmcnt(17) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
 typedef float f32x2v __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void* lds_ptr;
 
 template <int XDT>
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
@@ -44,6 +62,9 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
   }
 }
 
+// element offset of 16-byte chunk c of row r in a swizzled 64-element-row LDS tile
+__device__ __forceinline__ int swz(int r, int c) { return r * GM_BK + ((c ^ (r & 7)) << 3); }
+
 template <int XDT, int SDT>
 __global__ __launch_bounds__(GM_THREADS) void int4_gemm_tiled_kernel(
     const uint16_t* __restrict__ x, int64_t M, int64_t K, int64_t xs, const uint32_t* __restrict__ qw, int64_t N,
@@ -51,6 +72,8 @@ __global__ __launch_bounds__(GM_THREADS) void int4_gemm_tiled_kernel(
     uint16_t* __restrict__ y, int64_t tiles_m, int64_t tiles_n) {
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
   using ST = typename Elem<SDT>::T;
+  uint16_t* const sA0 = smem;                       // GM_NA x buffers
+  uint16_t* const sB0 = smem + GM_NA * GM_LDS_A;    // GM_NB W buffers
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   // tile coordinates in 32-bit scalar registers: a value the compiler cannot prove uniform
@@ -59,13 +82,13 @@ __global__ __launch_bounds__(GM_THREADS) void int4_gemm_tiled_kernel(
   const int tn32 = (int)tiles_n;
   const int64_t m0 = (int64_t)__builtin_amdgcn_readfirstlane((t / tn32) * GM_BM);
   const int64_t n0 = (int64_t)__builtin_amdgcn_readfirstlane((t % tn32) * GM_BN);
-  const int64_t nk = K / GM_BK;
+  const int nk = (int)(K / GM_BK);
 
   if (wave >= GM_MFMA_WAVES) {
-    // ---------------- loader waves: global -> registers (two steps ahead) -> dequant -> LDS
-    // Buffer loads: a per-lane 32-bit offset plus a uniform one, and rows past M or N read as
-    // zero (their products only reach rows / columns of C that are not stored).
-    const int lt = tid - 64 * GM_MFMA_WAVES;
+    // ---------------- loader waves
+    // Buffer loads: a per-lane 32-bit offset plus a uniform one; rows past M or N read as zero
+    // (their products only reach rows / columns of C that are not stored).
+    const int lw = __builtin_amdgcn_readfirstlane(wave - GM_MFMA_WAVES), lt = tid - 64 * GM_MFMA_WAVES;
     const int64_t rows_x = M - m0 < GM_BM ? M - m0 : GM_BM, rows_w = N - n0 < GM_BN ? N - n0 : GM_BN;
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(x + m0 * xs), 0, (int)(rows_x * xs * 2), 0x00020000);
@@ -76,30 +99,33 @@ __global__ __launch_bounds__(GM_THREADS) void int4_gemm_tiled_kernel(
         const_cast<ST*>(qs + n0), 0, (int)((G * N - n0) * (int64_t)sizeof(ST)), 0x00020000);
     const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<int8_t*>(qz + n0), 0, (int)(G * N - n0), 0x00020000);
-    // x chunk i of this thread: row lt / 8 + 32 i, 8 k at (lt % 8) * 8; W chunk i: row
-    // lt / 4 + 64 i, 16 k at (lt % 4) * 16
-    const uint32_t xo = (uint32_t)(((lt >> 3) * xs + (lt & 7) * 8) * 2);
+    // x: load j of this wave fills 8-row block b = 8 lw + j of the tile; lane l writes LDS slot
+    // l % 8 of row 8 b + l / 8, which holds chunk (l % 8) ^ (l / 8) of that row
+    const uint32_t xo = (uint32_t)((((lane >> 3) * xs) + (((lane & 7) ^ (lane >> 3)) << 3)) * 2);
+    // W chunk i of this thread: row lt / 4 + 64 i, 16 k at (lt % 4) * 16 (LDS chunks 2 (lt % 4) and
+    // 2 (lt % 4) + 1)
     const uint32_t wo = (uint32_t)(((lt >> 2) * pc + (lt & 3) * 2) * 4);
     const uint32_t so = (uint32_t)((lt >> 2) * sizeof(ST)), zo = (uint32_t)(lt >> 2);
-    // the scale and zero point stay raw until the store: converting them at the load would
-    // make the load wait for its data
-    struct Stage {
-      u32x4 x[GM_XPT];
-      uint2 w[GM_WPT];
-      uint32_t sc[GM_WPT], z[GM_WPT];
-    };
     // group of k-step ks = ks / (gsz / 64) as a multiply-high by ceil(2^32 / (gsz / 64)) (one
     // group per step needs no map): exact while both are below 2^16 (checked by the launcher);
     // a division here would branch and make the loads just issued wait
     const uint32_t spg = (uint32_t)(gsz / GM_BK);
     const uint32_t ginv = spg > 1 ? (uint32_t)(((1ull << 32) + spg - 1) / spg) : 0u;
-    const int nk32 = (int)nk;
-    auto load = [&](int ks, Stage& S) {
-      ks = ks < nk32 ? ks : nk32 - 1;
+    // the scale and zero point stay raw until the store: converting them at the load would
+    // make the load wait for its data
+    struct Stage {
+      uint2 w[GM_WPT];
+      uint32_t sc[GM_WPT], z[GM_WPT];
+    };
+    // every step issues the same GM_LOADS_PER_STEP loads (steps past the end reload the last
+    // one into a buffer nobody reads), so a fixed vmcnt names "all but this step's loads"
+    auto load = [&](int ks, int abuf, Stage& S) {
+      ks = ks < nk ? ks : nk - 1;
+      uint16_t* dst = sA0 + abuf * GM_LDS_A + lw * (GM_XLD * 8 * GM_BK);
 #pragma unroll
-      for (int i = 0; i < GM_XPT; ++i)
-        S.x[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                               rx, xo, (int)(i * 32 * xs * 2) + ks * (GM_BK * 2), 0));
+      for (int j = 0; j < GM_XLD; ++j)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(dst + j * 8 * GM_BK), 16, xo,
+                                                 (int)((8 * (GM_XLD * lw + j)) * xs * 2) + ks * (GM_BK * 2), 0, 0);
       const int g = spg == 1 ? ks : (int)__umulhi((uint32_t)ks, ginv);
 #pragma unroll
       for (int i = 0; i < GM_WPT; ++i) {
@@ -112,49 +138,57 @@ __global__ __launch_bounds__(GM_THREADS) void int4_gemm_tiled_kernel(
         S.z[i] = __builtin_amdgcn_raw_buffer_load_b8(rz, zo, (int)(g * N + 64 * i), 0);
       }
     };
-    auto store = [&](const Stage& S, int buf) {
-      uint16_t* sA = smem + buf * GM_LDS_A;
-      uint16_t* sB = smem + 2 * GM_LDS_A + buf * GM_LDS_B;
-#pragma unroll
-      for (int i = 0; i < GM_XPT; ++i)
-        *(u32x4*)(sA + ((lt >> 3) + 32 * i) * GM_PITCH + (lt & 7) * 8) = S.x[i];
+    // (q - z) * s as fma(q + o - z, s, -o * s): q + o - z is a byte in [0, 255] (o = 128, or 0
+    // for z < -112), so one v_add makes four of them; the fma rounds the exact (q - z) * s once,
+    // as the reference's fp32 product does
+    auto store = [&](const Stage& S, int bbuf) {
+      uint16_t* sB = sB0 + bbuf * GM_LDS_B;
 #pragma unroll
       for (int i = 0; i < GM_WPT; ++i) {
         float sc;
         if constexpr (sizeof(ST) == 4) sc = __uint_as_float(S.sc[i]);
         else sc = Elem<SDT>::to_f32((ST)S.sc[i]);
-        const float z = (float)(int8_t)S.z[i];
-        uint16_t* dst = sB + ((lt >> 2) + 64 * i) * GM_PITCH + (lt & 3) * 16;
+        const int z = (int)(int8_t)S.z[i];
+        const int off = z < -112 ? 0 : 128;
+        const uint32_t bias = (uint32_t)(off - z) * 0x01010101u;
+        const float c = -(float)off * sc;
+        const int row = (lt >> 2) + 64 * i;
 #pragma unroll
         for (int wi = 0; wi < 2; ++wi) {
           const uint32_t w = wi ? S.w[i].y : S.w[i].x;
-          const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+          const uint32_t lo = (w & 0x0F0F0F0Fu) + bias, hi = ((w >> 4) & 0x0F0F0F0Fu) + bias;
           u32x4 o;
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const float a = ((float)((lo >> (8 * j)) & 0xFFu) - z) * sc;  // nibble 2j
-            const float b = ((float)((hi >> (8 * j)) & 0xFFu) - z) * sc;  // nibble 2j + 1
+            const float a = __builtin_fmaf((float)((lo >> (8 * j)) & 0xFFu), sc, c);  // nibble 2j
+            const float b = __builtin_fmaf((float)((hi >> (8 * j)) & 0xFFu), sc, c);  // nibble 2j + 1
             o[j] = pack2<XDT>(a, b);
           }
-          *(u32x4*)(dst + wi * 8) = o;
+          *(u32x4*)(sB + swz(row, 2 * (lt & 3) + wi)) = o;
         }
       }
     };
     Stage S0, S1;
-    load(0, S0);
-    load(1, S1);
+    load(0, 0, S0);
+    load(1, 1, S1);
+    asm volatile("s_waitcnt vmcnt(17)" ::: "memory");
     store(S0, 0);
-    __syncthreads();
-    for (int ks = 0; ks < nk32; ks += 2) {
-      // step ks: MFMA waves read buffer 0; store step ks + 1 into buffer 1
-      load(ks + 2, S0);
-      if (ks + 1 < nk32) store(S1, 1);
-      __syncthreads();
-      if (ks + 1 >= nk32) break;
-      load(ks + 3, S1);
-      if (ks + 2 < nk32) store(S0, 0);
-      __syncthreads();
+    loader_barrier();
+    int a2 = 2;  // x buffer of step ks + 2
+    for (int ks = 0; ks < nk; ks += 2) {
+      // step ks: MFMA waves read x buffer ks % 3 and W buffer 0
+      load(ks + 2, a2, S0);
+      a2 = a2 == GM_NA - 1 ? 0 : a2 + 1;
+      if (ks + 1 < nk) store(S1, 1);
+      loader_barrier();
+      if (ks + 1 >= nk) break;
+      load(ks + 3, a2, S1);
+      a2 = a2 == GM_NA - 1 ? 0 : a2 + 1;
+      if (ks + 2 < nk) store(S0, 0);
+      loader_barrier();
     }
+    // the last steps' reloads land in buffers nobody reads; drain them before the wave ends
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     return;
   }
 
@@ -166,25 +200,32 @@ __global__ __launch_bounds__(GM_THREADS) void int4_gemm_tiled_kernel(
   for (int i = 0; i < 8; ++i)
 #pragma unroll
     for (int j = 0; j < 3; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  auto compute = [&](int buf) {
-    const uint16_t* sA = smem + buf * GM_LDS_A + (wm * 128 + r) * GM_PITCH + kq * 8;
-    const uint16_t* sB = smem + 2 * GM_LDS_A + buf * GM_LDS_B + (wn * 48 + r) * GM_PITCH + kq * 8;
+  // lane (r, kq) reads chunk kq + 4 s of rows r + 16 i: rows 16 i + r share r & 7, so the
+  // swizzled slot is the same for all i
+  const int a_off = (wm * 128 + r) * GM_BK, b_off = (wn * 48 + r) * GM_BK;
+  const int slot0 = ((kq ^ (r & 7)) << 3), slot1 = (((kq + 4) ^ (r & 7)) << 3);
+  auto compute = [&](int abuf, int bbuf) {
+    const uint16_t* sA = sA0 + abuf * GM_LDS_A + a_off;
+    const uint16_t* sB = sB0 + bbuf * GM_LDS_B + b_off;
 #pragma unroll
     for (int s = 0; s < GM_BK / 32; ++s) {
+      const int slot = s ? slot1 : slot0;
       u32x4 b[3];
 #pragma unroll
-      for (int j = 0; j < 3; ++j) b[j] = *(const u32x4*)(sB + j * 16 * GM_PITCH + s * 32);
+      for (int j = 0; j < 3; ++j) b[j] = *(const u32x4*)(sB + j * 16 * GM_BK + slot);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const u32x4 a = *(const u32x4*)(sA + i * 16 * GM_PITCH + s * 32);
+        const u32x4 a = *(const u32x4*)(sA + i * 16 * GM_BK + slot);
 #pragma unroll
         for (int j = 0; j < 3; ++j) acc[i][j] = mfma16<XDT>(a, b[j], acc[i][j]);
       }
     }
   };
-  __syncthreads();  // stage 0 is in LDS
-  for (int64_t ks = 0; ks < nk; ++ks) {
-    compute((int)(ks & 1));
+  __syncthreads();  // step 0 is in LDS
+  int ab = 0;
+  for (int ks = 0; ks < nk; ++ks) {
+    compute(ab, ks & 1);
+    ab = ab == GM_NA - 1 ? 0 : ab + 1;
     __syncthreads();
   }
   // C layout: lane holds rows 4 kq + e of column r of each 16 x 16 block
@@ -205,7 +246,9 @@ __global__ __launch_bounds__(GM_THREADS) void int4_gemm_tiled_kernel(
 }  // namespace
 
 bool int4_gemm_tiled_supported(int x_dtype, int64_t M, int64_t N, int64_t K, int64_t xs, const void* x, const void* qweight,
-                               int64_t pc, int64_t gsz) {
+                               int64_t pc, const void* qscale, const void* qzeros, int64_t gsz) {
+  (void)qscale;
+  (void)qzeros;
   // buffer loads address each workgroup's slice with 32-bit offsets, and the k-step -> group map
   // is a multiply-high that is exact below 2^16 steps
   const int64_t G = gsz > 0 ? (K + gsz - 1) / gsz : 0;
@@ -244,3 +287,4 @@ int int4_gemm_tiled_launch(const void* x, int x_dtype, int64_t M, int64_t K, int
 }
 
 }  // namespace anna
+

@@ -6,7 +6,7 @@
 namespace anna {
 
 bool int4_gemm_tiled_supported(int x_dtype, int64_t M, int64_t N, int64_t K, int64_t xs, const void* x, const void* qweight,
-                               int64_t pc, int64_t gsz);
+                               int64_t pc, const void* qscale, const void* qzeros, int64_t gsz);
 
 int int4_gemm_tiled_launch(const void* x, int x_dtype, int64_t M, int64_t K, int64_t xs, const int32_t* qweight,
                            int64_t N, int64_t pc, const void* qscale, int scale_dtype, const int8_t* qzeros, int64_t gsz,

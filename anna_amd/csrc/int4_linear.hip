@@ -739,7 +739,7 @@ extern "C" int anna_mi_int4_linear(const void* x, int x_dtype, int64_t M, int64_
     ANNA_LAUNCH_CHECK("int4_gemv_mfma");
     return ANNA_MI_OK;
   }
-  if (int4_gemm_tiled_supported(x_dtype, M, N, K, xs, x, qweight, pc, gsz))
+  if (int4_gemm_tiled_supported(x_dtype, M, N, K, xs, x, qweight, pc, qscale, qzeros, gsz))
     return int4_gemm_tiled_launch(x, x_dtype, M, K, xs, qweight, N, pc, qscale, scale_dtype, qzeros, gsz, y, st);
   if (x_dtype == ANNA_MI_BF16 && aligned && M > 16) {
     dim3 grid((unsigned)((N + GB_N - 1) / GB_N), (unsigned)((M + GB_M - 1) / GB_M), 1);
