@@ -156,9 +156,11 @@ __global__ __launch_bounds__(64) void tq_rotate_query_kernel(const anna_mi_tq_de
 // One 32-token block of one wave (slot / window position tb): scores, online softmax, and
 // the value product into acc.  RESID: the dense residual window (bf16 MFMAs, loads issued
 // here); otherwise the 2-bit codes already loaded into cur.
+// qf: the packed path's B fragments of the score product, held in registers for the whole item
+// (the residual path reads s_qf and passes nullptr)
 template <bool RESID>
-__device__ __forceinline__ void block_step(const anna_mi_tq_decode_args& a, const u32x4 (*s_qf)[64], int64_t b,
-                                           int64_t h, int64_t tb, int64_t tend, int lane, const BlockRaw& cur,
+__device__ __forceinline__ void block_step(const anna_mi_tq_decode_args& a, const u32x4 (*s_qf)[64], const u32x4* qf,
+                                           int64_t b, int64_t h, int64_t tb, int64_t tend, int lane, const BlockRaw& cur,
                                            f32x4 (&acc)[16], float& m_run, float& l_run) {
   const int r = lane & 15, kq = lane >> 4;
   const int64_t Rc = a.residual_capacity;
@@ -172,11 +174,10 @@ __device__ __forceinline__ void block_step(const anna_mi_tq_decode_args& a, cons
     if constexpr (!RESID) {
 #pragma unroll
       for (int st = 0; st < 8; ++st) {
-        const u32x4 qf = s_qf[st][lane];
         const uint32_t w0 = cur.k0[st >> 1], w1 = cur.k1[st >> 1];
         const uint32_t x0 = (st & 1) ? w0 : (w0 << 8), x1 = (st & 1) ? w1 : (w1 << 8);
-        st0 = mfma_f16(codes_to_f16(x0, lut_hi, lut_lo, or_c), qf, st0);
-        st1 = mfma_f16(codes_to_f16(x1, lut_hi, lut_lo, or_c), qf, st1);
+        st0 = mfma_f16(codes_to_f16(x0, lut_hi, lut_lo, or_c), qf[st], st0);
+        st1 = mfma_f16(codes_to_f16(x1, lut_hi, lut_lo, or_c), qf[st], st1);
         __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
@@ -273,43 +274,37 @@ __device__ __forceinline__ void block_step(const anna_mi_tq_decode_args& a, cons
   }
 }
 
-// The blocks of one item taken by one wave.  Residual windows (a few blocks): blocks wave,
-// wave + 8, ...  Packed items: the first block is `wave` (already loaded into A), the next
-// ones are taken from the workgroup's LDS counter *next, so that the two waves sharing a SIMD
-// (the second one issues less often) finish together.  Blocks ping-pong between two register
-// buffers; the prefetch is unconditional (clamped to the last block) so that no wait for it is
-// forced before the current block is consumed.
+// The blocks of one item taken by one wave: blocks wave, wave + 8, ... (the first one of a
+// packed item already loaded into A).  Packed blocks ping-pong between two register buffers in
+// a loop over pairs with no exit in between (an exit inside the pair would give the
+// accumulators two register homes and a copy per pair); the prefetch is unconditional (clamped
+// to the last block) so that no wait for it is forced before the current block is consumed.
 template <bool RESID>
 __device__ __forceinline__ void run_blocks(const anna_mi_tq_decode_args& a, const u32x4 (*s_qf)[64], int64_t b, int64_t h,
                                            int64_t tb0, int64_t tend, int64_t nblk, int wave, int lane, BlockRaw& A,
-                                           uint32_t* next, f32x4 (&acc)[16], float& m_run, float& l_run) {
+                                           f32x4 (&acc)[16], float& m_run, float& l_run) {
   const int r = lane & 15, kq = lane >> 4;
   if constexpr (RESID) {
     for (int64_t blk = wave; blk < nblk; blk += SWAVES)
-      block_step<true>(a, s_qf, b, h, tb0 + blk * TBT, tend, lane, A, acc, m_run, l_run);
+      block_step<true>(a, s_qf, nullptr, b, h, tb0 + blk * TBT, tend, lane, A, acc, m_run, l_run);
   } else {
-    auto take = [&]() -> int64_t {
-      uint32_t v = 0;
-      if (lane == 0) v = atomicAdd(next, 1u);
-      return (int64_t)__builtin_amdgcn_readfirstlane(v);
+    u32x4 qf[8];
+#pragma unroll
+    for (int st = 0; st < 8; ++st) qf[st] = s_qf[st][lane];
+    const int64_t cnt = wave < nblk ? (nblk - 1 - wave) / SWAVES + 1 : 0;
+    auto slot = [&](int64_t i) {
+      const int64_t c = wave + (int64_t)SWAVES * i;
+      return tb0 + (c < nblk ? c : nblk - 1) * TBT;
     };
-    const int64_t last = nblk - 1;
-    int64_t c = wave;
-    if (c >= nblk) return;
-    int64_t n = take();
     BlockRaw B;
-    for (;;) {
-      load_block(a, h, tb0 + (n < last ? n : last) * TBT, r, kq, B);
-      block_step<false>(a, s_qf, b, h, tb0 + c * TBT, tend, lane, A, acc, m_run, l_run);
-      c = n;
-      if (c >= nblk) break;
-      n = take();
-      load_block(a, h, tb0 + (n < last ? n : last) * TBT, r, kq, A);
-      block_step<false>(a, s_qf, b, h, tb0 + c * TBT, tend, lane, B, acc, m_run, l_run);
-      c = n;
-      if (c >= nblk) break;
-      n = take();
+    int64_t i = 0;
+    for (; i + 1 < cnt; i += 2) {
+      load_block(a, h, slot(i + 1), r, kq, B);
+      block_step<false>(a, s_qf, qf, b, h, slot(i), tend, lane, A, acc, m_run, l_run);
+      load_block(a, h, slot(i + 2), r, kq, A);
+      block_step<false>(a, s_qf, qf, b, h, slot(i + 1), tend, lane, B, acc, m_run, l_run);
     }
+    if (i < cnt) block_step<false>(a, s_qf, qf, b, h, slot(i), tend, lane, A, acc, m_run, l_run);
   }
 }
 
@@ -320,7 +315,6 @@ void tq_decode_split_kernel(const anna_mi_tq_decode_args a) {
   __shared__ float s_m[SWAVES][16], s_l[SWAVES][16];
   // cross-wave sums: [wave][tile j][kq * 8 + head % 8]
   __shared__ f32x4 s_red[SWAVES][16][32];
-  __shared__ uint32_t s_next;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, kq = lane >> 4;
   const int64_t item = blockIdx.x;
@@ -338,7 +332,6 @@ void tq_decode_split_kernel(const anna_mi_tq_decode_args a) {
   BlockRaw cur;
   if (!resid)  // in flight during the prologue (clamped: a wave without blocks reloads the last)
     load_block(a, h, tb0 + (wave < nblk ? wave : nblk - 1) * TBT, r, kq, cur);
-  if (threadIdx.x == 0) s_next = SWAVES;
   if (!resid) {
     s_qf[wave][lane] = *(const u32x4*)(a.query_frag + bh * 4096 + (wave * 64 + lane) * 8);
   } else {
@@ -352,9 +345,9 @@ void tq_decode_split_kernel(const anna_mi_tq_decode_args a) {
   for (int j = 0; j < 16; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
   if (resid)
-    run_blocks<true>(a, s_qf, b, h, tb0, tend, nblk, wave, lane, cur, &s_next, acc, m_run, l_run);
+    run_blocks<true>(a, s_qf, b, h, tb0, tend, nblk, wave, lane, cur, acc, m_run, l_run);
   else
-    run_blocks<false>(a, s_qf, b, h, tb0, tend, nblk, wave, lane, cur, &s_next, acc, m_run, l_run);
+    run_blocks<false>(a, s_qf, b, h, tb0, tend, nblk, wave, lane, cur, acc, m_run, l_run);
 
   // ---- reduce the waves
   l_run += __shfl_xor(l_run, 16, 64);
@@ -403,50 +396,59 @@ void tq_decode_split_kernel(const anna_mi_tq_decode_args a) {
 
 // ------------------------------------------------------------------ combine
 
-// grid (B * Hkv), 512 threads: combines the items of one (b, kv-head) with log-sum-exp weights,
-// applies R^T to the rotated sum (MFMA), adds the residual window's part and writes bf16.
-__global__ __launch_bounds__(64 * SWAVES) void tq_decode_combine_kernel(const anna_mi_tq_decode_args a) {
-  __shared__ float s_res[16 * TD];
+// grid (B * Hkv, 8 tiles of 32 output dims), 256 threads: combines the items of one
+// (b, kv-head) with log-sum-exp weights over all 256 rotated dims, applies R^T for the tile's
+// 32 output dims (MFMA), adds the residual window's part and writes bf16.  Each of the 8 tile
+// workgroups of a (b, kv-head) merges all dims itself: 8x the (L2-resident) partial reads, but
+// 8x the compute units pulling them, which is what bounds this kernel.
+constexpr int CMB_THREADS = 256, CMB_OT = 32;  // threads, output dims per workgroup
+__global__ __launch_bounds__(CMB_THREADS) void tq_decode_combine_kernel(const anna_mi_tq_decode_args a) {
   constexpr int RP = TD + 8;  // padded fp16 rows of the rotated sum
   __shared__ uint16_t s_rot[16 * RP];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __shared__ float s_res[16][CMB_OT];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, kq = lane >> 4;
   const int64_t bh = blockIdx.x, b = bh / a.kv_heads, h = bh % a.kv_heads;
+  const int d0 = blockIdx.y * CMB_OT;
   const int G = (int)(a.q_heads / a.kv_heads);
+  // R^T rows of the wave's output tile (waves 0 and 1): they depend on nothing, so they go first
+  u32x4 bfr[8];
+  if (wave < CMB_OT / 16) {
+#pragma unroll
+    for (int st = 0; st < 8; ++st)
+      bfr[st] = *(const u32x4*)(a.rotation_t_f16 + (int64_t)(d0 + wave * 16 + r) * TD + st * 32 + kq * 8);
+  }
   const int4 info = *(const int4*)(a.bh_items + bh * 4);  // first item, packed items, residual item
   const int i0 = info.x, npk = info.y, ires = info.z;
   const bool has_res = ires >= 0;
-  // R^T rows of this wave's two output tiles, in flight during the combine
-  u32x4 bfr[2][8];
-#pragma unroll
-  for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-    for (int st = 0; st < 8; ++st)
-      bfr[tt][st] = *(const u32x4*)(a.rotation_t_f16 + (int64_t)((2 * wave + tt) * 16 + r) * TD + st * 32 + kq * 8);
   constexpr int64_t IS = 16 * TD / 4;  // item stride of partial_values in f32x4
-  // Thread t owns entry (tile j, e) of head n = hb + e % 8 in every item: it combines the
-  // items itself with an online log-sum-exp over batches of 8 (values and stats loaded together).
+  // Entries (tile j, e) and (j + 8, e) of head n = hb + e % 8 in every item (512 entries per
+  // head block; both of this thread's entries share n and so the stats): the thread combines the
+  // items itself with an online log-sum-exp over batches of 16, every load of a batch issued
+  // together (one round trip per 16 items).
   for (int hb = 0; hb < G; hb += 8) {
-    const int t = threadIdx.x, j = t >> 5, e = t & 31;
+    const int t = tid, j = t >> 5, e = t & 31;
     const int n = hb + (e & 7), ekq = e >> 3;
     if (n >= G) continue;
     const f32x4* src = (const f32x4*)a.partial_values + (hb / 8) * 512 + t;
     const float* stn = a.partial_stats + n * 2;
-    f32x4 vr = {0.f, 0.f, 0.f, 0.f};
+    f32x4 vr0 = {0.f, 0.f, 0.f, 0.f}, vr1 = vr0;
     float2 mlr = {-INFINITY, 0.f};
     if (has_res) {
-      vr = src[(int64_t)ires * IS];
+      vr0 = src[(int64_t)ires * IS];
+      vr1 = src[(int64_t)ires * IS + CMB_THREADS];
       mlr = *(const float2*)(stn + (int64_t)ires * 32);
     }
-    f32x4 sr = {0.f, 0.f, 0.f, 0.f};
+    f32x4 sr0 = {0.f, 0.f, 0.f, 0.f}, sr1 = sr0;
     float M = -INFINITY, L = 0.f;
     for (int k0 = 0; k0 < npk; k0 += 16) {
-      f32x4 v[16];
+      f32x4 v0[16], v1[16];
       float2 ml[16];
 #pragma unroll
       for (int k = 0; k < 16; ++k) {
         const int64_t idx = i0 + (k0 + k < npk ? k0 + k : 0);
-        v[k] = src[idx * IS];
+        v0[k] = src[idx * IS];
+        v1[k] = src[idx * IS + CMB_THREADS];
         ml[k] = *(const float2*)(stn + idx * 32);
       }
       float mb = M;
@@ -455,12 +457,14 @@ __global__ __launch_bounds__(64 * SWAVES) void tq_decode_combine_kernel(const an
         if (k0 + k < npk && ml[k].y > 0.f) mb = fmaxf(mb, ml[k].x);
       if (mb == -INFINITY) continue;
       const float f = __builtin_amdgcn_exp2f(M - mb);  // 0 while M is -inf
-      sr *= f;
+      sr0 *= f;
+      sr1 *= f;
       L *= f;
 #pragma unroll
       for (int k = 0; k < 16; ++k) {
         const float w = (k0 + k < npk && ml[k].y > 0.f) ? __builtin_amdgcn_exp2f(ml[k].x - mb) : 0.f;
-        sr += v[k] * w;
+        sr0 += v0[k] * w;
+        sr1 += v1[k] * w;
         L += ml[k].y * w;
       }
       M = mb;
@@ -469,31 +473,34 @@ __global__ __launch_bounds__(64 * SWAVES) void tq_decode_combine_kernel(const an
     const float fp = L > 0.f ? __builtin_amdgcn_exp2f(M - Mt) : 0.f;
     const float fr = mlr.y > 0.f ? __builtin_amdgcn_exp2f(mlr.x - Mt) : 0.f;
     const float inv = 1.0f / (L * fp + mlr.y * fr);
-    sr *= fp * inv;
-    vr *= fr * inv;
+    sr0 *= fp * inv;
+    sr1 *= fp * inv;
+    vr0 *= fr * inv;
+    vr1 *= fr * inv;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int dim = (4 * ekq + i) * 16 + j;
-      s_rot[n * RP + dim] = f32_to_f16_bits(sr[i]);
-      s_res[n * TD + dim] = vr[i];
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const int dim = (4 * ekq + i) * 16 + j + 8 * hf;
+        s_rot[n * RP + dim] = f32_to_f16_bits(hf ? sr1[i] : sr0[i]);
+        if (dim >= d0 && dim < d0 + CMB_OT) s_res[n][dim - d0] = hf ? vr1[i] : vr0[i];
+      }
     }
   }
   __syncthreads();
-  // out = rot R + res: wave takes output dims [32 wave, 32 wave + 32); A = rot (16 heads x 32),
-  // B[k][d] = R[k][d] = R^T[d][k]; C lane: dim col r, heads 4 kq + i
-#pragma unroll
-  for (int tt = 0; tt < 2; ++tt) {
-    const int tile = 2 * wave + tt;
+  // out = rot R + res: wave w < 2 takes output dims [d0 + 16 w, d0 + 16 w + 16); A = rot (16 heads
+  // x 32), B[k][d] = R[k][d] = R^T[d][k]; C lane: dim col r, heads 4 kq + i
+  if (wave < CMB_OT / 16) {
     f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int st = 0; st < 8; ++st) {
       const u32x4 af = *(const u32x4*)(s_rot + r * RP + st * 32 + kq * 8);
-      c = mfma_f16(af, bfr[tt][st], c);
+      c = mfma_f16(af, bfr[st], c);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int n = 4 * kq + i, d = tile * 16 + r;
-      if (n < G) a.out[(b * a.q_heads + h * G + n) * TD + d] = f32_to_bf16_bits(c[i] + s_res[n * TD + d]);
+      const int n = 4 * kq + i, dl = wave * 16 + r;
+      if (n < G) a.out[(b * a.q_heads + h * G + n) * TD + d0 + dl] = f32_to_bf16_bits(c[i] + s_res[n][dl]);
     }
   }
 }
@@ -525,8 +532,9 @@ using namespace anna;
 
 extern "C" int64_t anna_mi_sizeof_tq_decode_args(void) { return (int64_t)sizeof(anna_mi_tq_decode_args); }
 
-// Blocks of 32 tokens per item for `slots` concurrent workgroups: the smallest multiple of 8
-// blocks (one per wave and pass) for which the items of every (b, kv-head) fit.
+// Blocks of 32 tokens per item for `slots` concurrent workgroups: the smallest count for which
+// the items of every (b, kv-head) fit (an item of nb blocks puts at most ceil(nb / 4) of them on
+// one SIMD, so no rounding to whole passes of the 8 waves).
 static int64_t auto_blocks_per_item(int64_t batch, int64_t kv_heads, const int64_t* qlens, const int64_t* rlens) {
   constexpr int64_t SLOTS = 256;  // MI355X compute units: one 512-thread workgroup each
   int64_t total = 0, resid = 0;
@@ -537,9 +545,9 @@ static int64_t auto_blocks_per_item(int64_t batch, int64_t kv_heads, const int64
   total *= kv_heads;
   resid *= kv_heads;
   const int64_t slots = SLOTS - resid > kv_heads * batch ? SLOTS - resid : kv_heads * batch;
-  int64_t bpi = ((total + slots - 1) / slots + SWAVES - 1) / SWAVES * SWAVES;
-  if (bpi < SWAVES) bpi = SWAVES;
-  for (;; bpi += SWAVES) {
+  int64_t bpi = (total + slots - 1) / slots;
+  if (bpi < 1) bpi = 1;
+  for (;; ++bpi) {
     int64_t n = 0;
     for (int64_t b = 0; b < batch; ++b) n += ((qlens[b] + TBT - 1) / TBT + bpi - 1) / bpi;
     if (n * kv_heads <= slots) return bpi;
@@ -609,7 +617,8 @@ extern "C" int anna_mi_tq_decode(const anna_mi_tq_decode_args* ap, void* stream)
   ANNA_LAUNCH_CHECK("tq_rotate_query_kernel");
   hipLaunchKernelGGL(tq_decode_split_kernel, dim3((unsigned)a.num_items), dim3(64 * SWAVES), 0, st, a);
   ANNA_LAUNCH_CHECK("tq_decode_split_kernel");
-  hipLaunchKernelGGL(tq_decode_combine_kernel, dim3((unsigned)(a.batch * a.kv_heads)), dim3(64 * SWAVES), 0, st, a);
+  hipLaunchKernelGGL(tq_decode_combine_kernel, dim3((unsigned)(a.batch * a.kv_heads), TD / CMB_OT), dim3(CMB_THREADS), 0,
+                     st, a);
   ANNA_LAUNCH_CHECK("tq_decode_combine_kernel");
   return ANNA_MI_OK;
 }
