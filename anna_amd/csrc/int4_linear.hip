@@ -33,13 +33,14 @@ namespace {
 
 // ------------------------------------------------------------------ GEMV (M <= 16)
 
-// K blocks (128 k each) one wave keeps in flight per pass: all of them are loaded
-// before any is consumed, so a wave has 8 x 16 B x NT per lane outstanding.
-constexpr int GEMV_BPW = 8;
-// x is staged in LDS when M * K * 2 bytes fit this budget (else read through L1/L2).
-constexpr int64_t GEMV_LDS_X_LIMIT = 32768;  // = 2048 chunks of 16 B
+// K blocks (128 k each) one wave keeps in flight per pass (BPW, a template parameter: 8, or 4
+// when the K split over the waves leaves at most 4 per wave): all of them are loaded before any
+// is consumed, so a wave has BPW x 16 B x NT per lane outstanding.  Loads past the wave's share
+// would be clamped duplicates that still cost registers, hence BPW = 4 when 4 suffice: it lets
+// two 8-wave workgroups share a CU.
 
-template <int XDT, int SDT, int NT, int KW, bool XLDS>
+// x is read through L1/L2 (staging it in LDS first was measured slower at every M).
+template <int XDT, int SDT, int NT, int KW, int GEMV_BPW>
 __global__ __launch_bounds__(64 * KW) void int4_gemv_mfma(
     const uint16_t* __restrict__ x, int64_t M, int64_t K, int64_t xs,
     const uint32_t* __restrict__ qw, int64_t N, int64_t pc,
@@ -47,7 +48,6 @@ __global__ __launch_bounds__(64 * KW) void int4_gemv_mfma(
     int64_t blocks_per_group, uint16_t* __restrict__ y, int contiguous, int nontemporal) {
   constexpr float OFF = XDT == ANNA_MI_BF16 ? 128.0f : 1024.0f;
   constexpr uint32_t ONES = XDT == ANNA_MI_BF16 ? 0x3F803F80u : 0x3C003C00u;
-  extern __shared__ __attribute__((aligned(16))) uint16_t xsm[];  // [M][K + 8] when XLDS
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int r = lane & 15;
@@ -55,7 +55,6 @@ __global__ __launch_bounds__(64 * KW) void int4_gemv_mfma(
   const int64_t n_base = xcd_tile(blockIdx.x, gridDim.x) * (16 * NT);
   const bool m_ok = r < M;
   const int64_t nblk = (K + 127) >> 7;
-  const int64_t xp = K + 8;  // LDS row pitch (elements): rows land 4 banks apart
   const u32x4 ones = {ONES, ONES, ONES, ONES};
   const u32x4 zero4 = {0u, 0u, 0u, 0u};
 
@@ -76,24 +75,8 @@ __global__ __launch_bounds__(64 * KW) void int4_gemv_mfma(
   // (b = p0 + wave*BPW + j, so one wave reads whole 128 B lines back to back).
   const int64_t bw0 = contiguous ? (int64_t)wave * GEMV_BPW : wave;
   const int64_t bstep = contiguous ? 1 : KW;
-  // x staging (first pass only): its loads are issued before the weight loads so that
-  // waiting for x leaves every weight load in flight.
-  constexpr int XCH = XLDS ? (2048 / (64 * KW)) : 1;  // 16 B chunks of x per thread
-  const int64_t xchunks = M * (K >> 3);
-  u32x4 xst[XCH];
-  if constexpr (XLDS) {
-#pragma unroll
-    for (int i = 0; i < XCH; ++i) {
-      int64_t c = threadIdx.x + (int64_t)i * 64 * KW;
-      c = c < xchunks ? c : 0;
-      const int64_t row = c / (K >> 3), col = (c % (K >> 3)) * 8;
-      xst[i] = *(const u32x4*)(x + row * xs + col);
-    }
-  }
-  // One pass = GEMV_BPW blocks per wave.  The first pass is peeled out of the loop so
-  // that no loop-header wait holds the weight loads behind the x staging loads.
-  auto pass = [&](int64_t p0, auto first_tag) {
-    constexpr bool FIRST = decltype(first_tag)::value;
+  // One pass = GEMV_BPW blocks per wave (one pass covers K = 4096 at 8 waves).
+  auto pass = [&](int64_t p0) {
     // Issue every global load of the pass up front: weights, scales, zero points.
     u32x4 wv[GEMV_BPW][NT];
     float scv[GEMV_BPW][NT];
@@ -119,28 +102,13 @@ __global__ __launch_bounds__(64 * KW) void int4_gemv_mfma(
 #pragma unroll
       for (int t = 0; t < NT; ++t)
         if (!n_ok[t]) wv[j][t] = zero4;
-    if constexpr (XLDS && FIRST) {
-      {
-#pragma unroll
-        for (int i = 0; i < XCH; ++i) {
-          const int64_t c = threadIdx.x + (int64_t)i * 64 * KW;
-          if (c < xchunks) {
-            const int64_t row = c / (K >> 3), col = (c % (K >> 3)) * 8;
-            *(u32x4*)(xsm + row * xp + col) = xst[i];
-          }
-        }
-        __syncthreads();
-      }
-    }
     // x fragments of the next block are fetched while the current block computes.
     auto load_x = [&](int64_t b, int s) -> u32x4 {
       const int64_t k = b * 128 + kq * 32 + s * 8;
       const bool ok = b < nblk && m_ok && k < K;
       const int64_t kc = ok ? k : 0;
       const int64_t rc = m_ok ? r : 0;
-      u32x4 v;
-      if constexpr (XLDS) v = *(const u32x4*)(xsm + rc * xp + kc);
-      else v = *(const u32x4*)(x + rc * xs + kc);
+      const u32x4 v = *(const u32x4*)(x + rc * xs + kc);
       return ok ? v : zero4;
     };
     u32x4 xa[4];
@@ -175,8 +143,7 @@ __global__ __launch_bounds__(64 * KW) void int4_gemv_mfma(
       for (int s = 0; s < 4; ++s) xa[s] = xn[s];
     }
   };
-  pass(0, std::true_type{});
-  for (int64_t p0 = (int64_t)KW * GEMV_BPW; p0 < nblk; p0 += (int64_t)KW * GEMV_BPW) pass(p0, std::false_type{});
+  for (int64_t p0 = 0; p0 < nblk; p0 += (int64_t)KW * GEMV_BPW) pass(p0);
 
   if constexpr (KW > 1) {
     __shared__ float red[KW - 1][NT * 4][64];
@@ -637,24 +604,17 @@ int env_int(const char* name, int dflt) {
 static const int g_contig = env_int("ANNA_MI_INT4_GEMV_CONTIG", 0);
 static const int g_nt = env_int("ANNA_MI_INT4_GEMV_NT", 1);
 
-template <int XDT, int SDT, int NT, int KW>
+template <int XDT, int SDT, int NT, int KW, int BPW>
 void launch_gemv(const void* x, int64_t M, int64_t K, int64_t xs, const int32_t* qw, int64_t N,
                  int64_t pc, const void* qs, const int8_t* qz, int64_t gsz, void* y, hipStream_t st) {
   dim3 grid((unsigned)((N + 16 * NT - 1) / (16 * NT)), 1, 1);
-  const int64_t xbytes = M * (K + 8) * 2;
-  if (M * K * 2 <= GEMV_LDS_X_LIMIT) {
-    hipLaunchKernelGGL((int4_gemv_mfma<XDT, SDT, NT, KW, true>), grid, dim3(64 * KW), (size_t)xbytes, st,
-                       (const uint16_t*)x, M, K, xs, (const uint32_t*)qw, N, pc,
-                       (const typename Elem<SDT>::T*)qs, qz, gsz / 128, (uint16_t*)y, g_contig, g_nt);
-  } else {
-    hipLaunchKernelGGL((int4_gemv_mfma<XDT, SDT, NT, KW, false>), grid, dim3(64 * KW), 0, st,
-                       (const uint16_t*)x, M, K, xs, (const uint32_t*)qw, N, pc,
-                       (const typename Elem<SDT>::T*)qs, qz, gsz / 128, (uint16_t*)y, g_contig, g_nt);
-  }
+  hipLaunchKernelGGL((int4_gemv_mfma<XDT, SDT, NT, KW, BPW>), grid, dim3(64 * KW), 0, st, (const uint16_t*)x, M, K, xs,
+                     (const uint32_t*)qw, N, pc, (const typename Elem<SDT>::T*)qs, qz, gsz / 128, (uint16_t*)y,
+                     g_contig, g_nt);
 }
 
 // Tuning knobs (read once): ANNA_MI_INT4_GEMV_WAVES in {4, 8} splits K across that many
-// waves per workgroup; ANNA_MI_INT4_GEMV_TILES in {1, 2} sets 16-row tiles per wave.
+// waves per workgroup; ANNA_MI_INT4_GEMV_TILES in {1, 2} sets 16-row tiles per wave (default 2).
 
 template <int XDT, int SDT>
 void dispatch_gemv(const void* x, int64_t M, int64_t K, int64_t xs, const int32_t* qw, int64_t N, int64_t pc,
@@ -663,11 +623,16 @@ void dispatch_gemv(const void* x, int64_t M, int64_t K, int64_t xs, const int32_
   static const int env_tiles = env_int("ANNA_MI_INT4_GEMV_TILES", 0);
   const int64_t nblk = (K + 127) / 128;
   const int waves = env_waves ? env_waves : (nblk >= 32 ? 8 : 4);
-  const int tiles = env_tiles ? env_tiles : 1;
-  if (waves == 8 && tiles == 2) launch_gemv<XDT, SDT, 2, 8>(x, M, K, xs, qw, N, pc, qs, qz, gsz, y, st);
-  else if (waves == 8) launch_gemv<XDT, SDT, 1, 8>(x, M, K, xs, qw, N, pc, qs, qz, gsz, y, st);
-  else if (tiles == 2) launch_gemv<XDT, SDT, 2, 4>(x, M, K, xs, qw, N, pc, qs, qz, gsz, y, st);
-  else launch_gemv<XDT, SDT, 1, 4>(x, M, K, xs, qw, N, pc, qs, qz, gsz, y, st);
+  const int tiles = env_tiles ? env_tiles : 2;
+  const bool b4 = nblk <= 4 * waves;  // one pass of 4 blocks per wave covers K
+#define ANNA_GEMV_GO(T, W)                                                                   \
+  (b4 ? launch_gemv<XDT, SDT, T, W, 4>(x, M, K, xs, qw, N, pc, qs, qz, gsz, y, st)           \
+      : launch_gemv<XDT, SDT, T, W, 8>(x, M, K, xs, qw, N, pc, qs, qz, gsz, y, st))
+  if (waves == 8 && tiles == 2) ANNA_GEMV_GO(2, 8);
+  else if (waves == 8) ANNA_GEMV_GO(1, 8);
+  else if (tiles == 2) ANNA_GEMV_GO(2, 4);
+  else ANNA_GEMV_GO(1, 4);
+#undef ANNA_GEMV_GO
 }
 
 }  // namespace
