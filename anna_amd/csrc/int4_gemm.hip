@@ -1,6 +1,8 @@
 // W4A16 GEMM for M >= 64 on gfx950: y[M, N] = x[M, K] . dequant(W)[N, K]^T.
 //
-// Tile 256 (m) x 192 (n) x 64 (k) per workgroup of 12 waves with two roles:
+// Tile 256 (m) x 192 (n) x 64 (k) per workgroup of 12 waves with two roles (for M >= 1024; the
+// same kernel runs 128 x 96 tiles with a 4 x 2 grid of MFMA waves for M >= 256 and 64 x 48 with
+// 4 x 1 below, so that every compute unit gets a workgroup):
 //   8 MFMA waves   a 2 x 4 grid, each owning 128 x 48 of C as 8 x 3 v_mfma_f32_16x16x32
 //                  accumulators; they only read LDS;
 //   4 loader waves (one per SIMD) copy the x tile (256 x 64, 16-bit) straight from memory into
@@ -17,6 +19,8 @@
 // workgroup map is XCD-aware and m-major: the n-tiles of one m-tile share one XCD, so that XCD's
 // L2 holds the m-tile's slice of x (256 x K, 2 MB at K = 4096) and only the small int4 W streams
 // in; M = 2048 with N = 12288 gives 512 tiles (two rounds on 256 CUs).
+#include <stdlib.h>
+
 #include <type_traits>
 
 #include "common.hpp"
@@ -26,26 +30,47 @@
 namespace anna {
 namespace {
 
-constexpr int GM_BM = 256, GM_BN = 192, GM_BK = 64;
-constexpr int GM_MFMA_WAVES = 8, GM_LOAD_WAVES = 4;
-constexpr int GM_THREADS = 64 * (GM_MFMA_WAVES + GM_LOAD_WAVES);
-constexpr int GM_LT = 64 * GM_LOAD_WAVES;                 // loader threads
-constexpr int GM_NA = 3, GM_NB = 2;                       // LDS buffers of x and of W
-constexpr int GM_LDS_A = GM_BM * GM_BK, GM_LDS_B = GM_BN * GM_BK;  // 16-bit elements per buffer
-constexpr size_t GM_LDS_BYTES = (size_t)(GM_NA * GM_LDS_A + GM_NB * GM_LDS_B) * 2;  // 144 KB
-constexpr int GM_XLD = GM_BM / 8 / GM_LOAD_WAVES;         // 8-row x blocks per loader wave: 8
-constexpr int GM_WPT = GM_BN * (GM_BK / 16) / GM_LT;      // W chunks (8 B = 16 nibbles) per loader thread: 3
-// vector-memory loads one loader thread issues per k-step: the x blocks plus word, scale and
-// zero point of each W chunk; the wait before each barrier keeps exactly these outstanding
-constexpr int GM_LOADS_PER_STEP = GM_XLD + 3 * GM_WPT;
-static_assert(GM_LOADS_PER_STEP == 17, "loader_barrier waits for vmcnt(17)");
+constexpr int GM_BK = 64, GM_LOAD_WAVES = 4;
+constexpr int GM_LT = 64 * GM_LOAD_WAVES;  // loader threads
+constexpr int GM_NA = 3, GM_NB = 2;        // LDS buffers of x and of W
+constexpr uint32_t GM_OOB = 0x80000000u;   // buffer offset past any num_records: the load returns 0
 
-// The loader's end of a k-step: all but its 17 most recent loads have landed (so the previous
+// Tile shape: BM x BN per workgroup, an MW x NW grid of MFMA waves (wave tile BM/MW x BN/NW).
+template <int BM_, int BN_, int MW_, int NW_>
+struct GemmTile {
+  static constexpr int BM = BM_, BN = BN_, MW = MW_, NW = NW_;
+  static constexpr int MFMA_WAVES = MW * NW, THREADS = 64 * (MFMA_WAVES + GM_LOAD_WAVES);
+  static constexpr int TM = BM / MW, TN = BN / NW, FM = TM / 16, FN = TN / 16;  // wave tile, fragments
+  static constexpr int LDS_A = BM * GM_BK, LDS_B = BN * GM_BK;                   // 16-bit elements per buffer
+  static constexpr size_t LDS_BYTES = (size_t)(GM_NA * LDS_A + GM_NB * LDS_B) * 2;
+  static constexpr int XLD = BM / 8 / GM_LOAD_WAVES;           // 8-row x blocks per loader wave
+  static constexpr int WPT = (BN * 4 + GM_LT - 1) / GM_LT;     // W chunks (8 B = 16 nibbles) per loader thread
+  // vector-memory loads one loader thread issues per k-step: the x blocks plus word, scale and
+  // zero point of each W chunk; the wait before each barrier keeps exactly these outstanding
+  static constexpr int LOADS_PER_STEP = XLD + 3 * WPT;
+  static_assert(TM % 16 == 0 && TN % 16 == 0 && BM % (8 * GM_LOAD_WAVES) == 0, "tile shape");
+  static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+};
+using TileL = GemmTile<256, 192, 2, 4>;  // M >= 1024: 128 x 48 wave tiles, 144 KB LDS
+using TileM = GemmTile<128, 96, 4, 2>;   // M >= 256:  32 x 48 wave tiles, 72 KB LDS
+using TileS = GemmTile<64, 48, 4, 1>;    // M < 256:   16 x 48 wave tiles, 36 KB LDS
+
+// The loader's end of a k-step: all but its N most recent loads have landed (so the previous
 // step's LDS-destination x loads are in LDS), its LDS writes are done, then the workgroup
 // barrier.  __syncthreads() would also wait for the loads just issued, since its release fence
 // covers LDS-destination loads.
+template <int N>
 __device__ __forceinline__ void loader_barrier() {
-  asm volatile("s_waitcnt vmcnt(17) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  static_assert(N == 17 || N == 10 || N == 5, "add the wait count of a new tile shape here");
+  if constexpr (N == 17) asm volatile("s_waitcnt vmcnt(17) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 10) asm volatile("s_waitcnt vmcnt(10) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+template <int N>
+__device__ __forceinline__ void loader_wait() {
+  if constexpr (N == 17) asm volatile("s_waitcnt vmcnt(17)" ::: "memory");
+  else if constexpr (N == 10) asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
 }
 
 typedef float f32x2v __attribute__((ext_vector_type(2)));
@@ -65,13 +90,15 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
 // element offset of 16-byte chunk c of row r in a swizzled 64-element-row LDS tile
 __device__ __forceinline__ int swz(int r, int c) { return r * GM_BK + ((c ^ (r & 7)) << 3); }
 
-template <int XDT, int SDT>
-__global__ __launch_bounds__(GM_THREADS) void int4_gemm_tiled_kernel(
+template <int XDT, int SDT, class T>
+__global__ __launch_bounds__(T::THREADS) void int4_gemm_tiled_kernel(
     const uint16_t* __restrict__ x, int64_t M, int64_t K, int64_t xs, const uint32_t* __restrict__ qw, int64_t N,
     int64_t pc, const typename Elem<SDT>::T* __restrict__ qs, const int8_t* __restrict__ qz, int64_t gsz,
     uint16_t* __restrict__ y, int64_t tiles_m, int64_t tiles_n) {
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
   using ST = typename Elem<SDT>::T;
+  constexpr int GM_BM = T::BM, GM_BN = T::BN, GM_LDS_A = T::LDS_A, GM_LDS_B = T::LDS_B;
+  constexpr int GM_MFMA_WAVES = T::MFMA_WAVES, GM_XLD = T::XLD, GM_WPT = T::WPT;
   uint16_t* const sA0 = smem;                       // GM_NA x buffers
   uint16_t* const sB0 = smem + GM_NA * GM_LDS_A;    // GM_NB W buffers
   const int tid = threadIdx.x;
@@ -103,9 +130,16 @@ __global__ __launch_bounds__(GM_THREADS) void int4_gemm_tiled_kernel(
     // l % 8 of row 8 b + l / 8, which holds chunk (l % 8) ^ (l / 8) of that row
     const uint32_t xo = (uint32_t)((((lane >> 3) * xs) + (((lane & 7) ^ (lane >> 3)) << 3)) * 2);
     // W chunk i of this thread: row lt / 4 + 64 i, 16 k at (lt % 4) * 16 (LDS chunks 2 (lt % 4) and
-    // 2 (lt % 4) + 1)
-    const uint32_t wo = (uint32_t)(((lt >> 2) * pc + (lt & 3) * 2) * 4);
-    const uint32_t so = (uint32_t)((lt >> 2) * sizeof(ST)), zo = (uint32_t)(lt >> 2);
+    // 2 (lt % 4) + 1).  Chunks of rows past the tile (a tile narrower than 64 WPT rows) load
+    // from an offset past the buffer (zero) and are not stored.
+    uint32_t wo[GM_WPT], so[GM_WPT], zo[GM_WPT];
+#pragma unroll
+    for (int i = 0; i < GM_WPT; ++i) {
+      const bool in_tile = (lt >> 2) + 64 * i < GM_BN;
+      wo[i] = in_tile ? (uint32_t)(((lt >> 2) * pc + (lt & 3) * 2) * 4) : GM_OOB;
+      so[i] = in_tile ? (uint32_t)((lt >> 2) * sizeof(ST)) : GM_OOB;
+      zo[i] = in_tile ? (uint32_t)(lt >> 2) : GM_OOB;
+    }
     // group of k-step ks = ks / (gsz / 64) as a multiply-high by ceil(2^32 / (gsz / 64)) (one
     // group per step needs no map): exact while both are below 2^16 (checked by the launcher);
     // a division here would branch and make the loads just issued wait
@@ -130,12 +164,12 @@ __global__ __launch_bounds__(GM_THREADS) void int4_gemm_tiled_kernel(
 #pragma unroll
       for (int i = 0; i < GM_WPT; ++i) {
         S.w[i] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
-                                               rw, wo, (int)(i * 64 * pc * 4) + ks * (GM_BK / 2), 0));
+                                               rw, wo[i], (int)(i * 64 * pc * 4) + ks * (GM_BK / 2), 0));
         if constexpr (sizeof(ST) == 4)
-          S.sc[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, so, (int)((g * N + 64 * i) * 4), 0);
+          S.sc[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, so[i], (int)((g * N + 64 * i) * 4), 0);
         else
-          S.sc[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, so, (int)((g * N + 64 * i) * 2), 0);
-        S.z[i] = __builtin_amdgcn_raw_buffer_load_b8(rz, zo, (int)(g * N + 64 * i), 0);
+          S.sc[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, so[i], (int)((g * N + 64 * i) * 2), 0);
+        S.z[i] = __builtin_amdgcn_raw_buffer_load_b8(rz, zo[i], (int)(g * N + 64 * i), 0);
       }
     };
     // (q - z) * s as fma(q + o - z, s, -o * s): q + o - z is a byte in [0, 255] (o = 128, or 0
@@ -153,6 +187,7 @@ __global__ __launch_bounds__(GM_THREADS) void int4_gemm_tiled_kernel(
         const uint32_t bias = (uint32_t)(off - z) * 0x01010101u;
         const float c = -(float)off * sc;
         const int row = (lt >> 2) + 64 * i;
+        if (GM_WPT * 64 > GM_BN && row >= GM_BN) continue;
 #pragma unroll
         for (int wi = 0; wi < 2; ++wi) {
           const uint32_t w = wi ? S.w[i].y : S.w[i].x;
@@ -171,38 +206,39 @@ __global__ __launch_bounds__(GM_THREADS) void int4_gemm_tiled_kernel(
     Stage S0, S1;
     load(0, 0, S0);
     load(1, 1, S1);
-    asm volatile("s_waitcnt vmcnt(17)" ::: "memory");
+    loader_wait<T::LOADS_PER_STEP>();
     store(S0, 0);
-    loader_barrier();
+    loader_barrier<T::LOADS_PER_STEP>();
     int a2 = 2;  // x buffer of step ks + 2
     for (int ks = 0; ks < nk; ks += 2) {
       // step ks: MFMA waves read x buffer ks % 3 and W buffer 0
       load(ks + 2, a2, S0);
       a2 = a2 == GM_NA - 1 ? 0 : a2 + 1;
       if (ks + 1 < nk) store(S1, 1);
-      loader_barrier();
+      loader_barrier<T::LOADS_PER_STEP>();
       if (ks + 1 >= nk) break;
       load(ks + 3, a2, S1);
       a2 = a2 == GM_NA - 1 ? 0 : a2 + 1;
       if (ks + 2 < nk) store(S0, 0);
-      loader_barrier();
+      loader_barrier<T::LOADS_PER_STEP>();
     }
     // the last steps' reloads land in buffers nobody reads; drain them before the wave ends
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     return;
   }
 
-  // ---------------- MFMA waves: 2 (m) x 4 (n) grid, wave (wm, wn) owns 128 x 48 of C
+  // ---------------- MFMA waves: MW (m) x NW (n) grid, wave (wm, wn) owns TM x TN of C
+  constexpr int FM = T::FM, FN = T::FN;
   const int r = lane & 15, kq = lane >> 4;
-  const int wm = wave >> 2, wn = wave & 3;
-  f32x4 acc[8][3];
+  const int wm = wave / T::NW, wn = wave % T::NW;
+  f32x4 acc[FM][FN];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 3; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   // lane (r, kq) reads chunk kq + 4 s of rows r + 16 i: rows 16 i + r share r & 7, so the
   // swizzled slot is the same for all i
-  const int a_off = (wm * 128 + r) * GM_BK, b_off = (wn * 48 + r) * GM_BK;
+  const int a_off = (wm * T::TM + r) * GM_BK, b_off = (wn * T::TN + r) * GM_BK;
   const int slot0 = ((kq ^ (r & 7)) << 3), slot1 = (((kq + 4) ^ (r & 7)) << 3);
   auto compute = [&](int abuf, int bbuf) {
     const uint16_t* sA = sA0 + abuf * GM_LDS_A + a_off;
@@ -210,14 +246,14 @@ __global__ __launch_bounds__(GM_THREADS) void int4_gemm_tiled_kernel(
 #pragma unroll
     for (int s = 0; s < GM_BK / 32; ++s) {
       const int slot = s ? slot1 : slot0;
-      u32x4 b[3];
+      u32x4 b[FN];
 #pragma unroll
-      for (int j = 0; j < 3; ++j) b[j] = *(const u32x4*)(sB + j * 16 * GM_BK + slot);
+      for (int j = 0; j < FN; ++j) b[j] = *(const u32x4*)(sB + j * 16 * GM_BK + slot);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < FM; ++i) {
         const u32x4 a = *(const u32x4*)(sA + i * 16 * GM_BK + slot);
 #pragma unroll
-        for (int j = 0; j < 3; ++j) acc[i][j] = mfma16<XDT>(a, b[j], acc[i][j]);
+        for (int j = 0; j < FN; ++j) acc[i][j] = mfma16<XDT>(a, b[j], acc[i][j]);
       }
     }
   };
@@ -230,14 +266,14 @@ __global__ __launch_bounds__(GM_THREADS) void int4_gemm_tiled_kernel(
   }
   // C layout: lane holds rows 4 kq + e of column r of each 16 x 16 block
 #pragma unroll
-  for (int j = 0; j < 3; ++j) {
-    const int64_t n = n0 + wn * 48 + j * 16 + r;
+  for (int j = 0; j < FN; ++j) {
+    const int64_t n = n0 + wn * T::TN + j * 16 + r;
     if (n >= N) continue;
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int64_t m = m0 + wm * 128 + i * 16 + 4 * kq + e;
+        const int64_t m = m0 + wm * T::TM + i * 16 + 4 * kq + e;
         if (m < M) y[m * N + n] = Elem<XDT>::cvt(acc[i][j][e]);
       }
   }
@@ -252,7 +288,7 @@ bool int4_gemm_tiled_supported(int x_dtype, int64_t M, int64_t N, int64_t K, int
   // buffer loads address each workgroup's slice with 32-bit offsets, and the k-step -> group map
   // is a multiply-high that is exact below 2^16 steps
   const int64_t G = gsz > 0 ? (K + gsz - 1) / gsz : 0;
-  const bool fits = (int64_t)GM_BM * xs * 2 < (1ll << 31) && (int64_t)GM_BN * pc * 4 < (1ll << 31) &&
+  const bool fits = (int64_t)TileL::BM * xs * 2 < (1ll << 31) && (int64_t)TileL::BN * pc * 4 < (1ll << 31) &&
                     G * N * 4 < (1ll << 31) && K / GM_BK < (1 << 16) && gsz / GM_BK < (1 << 16);
   return (x_dtype == ANNA_MI_BF16 || x_dtype == ANNA_MI_F16) && M >= 64 && K % GM_BK == 0 && gsz % GM_BK == 0 &&
          xs % 8 == 0 && pc % 4 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)qweight % 16 == 0 && fits;
@@ -261,25 +297,38 @@ bool int4_gemm_tiled_supported(int x_dtype, int64_t M, int64_t N, int64_t K, int
 int int4_gemm_tiled_launch(const void* x, int x_dtype, int64_t M, int64_t K, int64_t xs, const int32_t* qweight,
                            int64_t N, int64_t pc, const void* qscale, int scale_dtype, const int8_t* qzeros, int64_t gsz,
                            void* y, hipStream_t st) {
-  const int64_t tm = (M + GM_BM - 1) / GM_BM, tn = (N + GM_BN - 1) / GM_BN;
+  // the largest tile that still gives every compute unit a workgroup (256 of them)
+  auto tiles = [&](auto t) {
+    using TT = decltype(t);
+    return ((M + TT::BM - 1) / TT::BM) * ((N + TT::BN - 1) / TT::BN);
+  };
+  int shape = tiles(TileL{}) >= 256 ? 0 : tiles(TileM{}) >= 256 ? 1 : 2;
+  // ANNA_MI_INT4_GEMM_TILE = L / M / S forces a tile shape (read on every call; the tests run
+  // every shape on shapes small enough for the CPU oracle)
+  if (const char* f = getenv("ANNA_MI_INT4_GEMM_TILE"); f && *f) shape = f[0] == 'L' ? 0 : f[0] == 'M' ? 1 : 2;
   ANNA_DISPATCH_DTYPE(scale_dtype, SDT, {
-    auto go = [&](auto xdt_tag) {
+    auto go = [&](auto xdt_tag, auto tile_tag) {
       constexpr int XDT = decltype(xdt_tag)::value;
-      auto kern = int4_gemm_tiled_kernel<XDT, SDT>;
+      using TT = decltype(tile_tag);
+      const int64_t tm = (M + TT::BM - 1) / TT::BM, tn = (N + TT::BN - 1) / TT::BN;
+      auto kern = int4_gemm_tiled_kernel<XDT, SDT, TT>;
       static bool attr_set = false;
       if (!attr_set) {
         ANNA_CHECK(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)GM_LDS_BYTES) == hipSuccess,
+                                       (int)TT::LDS_BYTES) == hipSuccess,
                    "int4 GEMM: cannot raise the LDS limit");
         attr_set = true;
       }
-      hipLaunchKernelGGL(kern, dim3((unsigned)(tm * tn)), dim3(GM_THREADS), GM_LDS_BYTES, st, (const uint16_t*)x, M, K,
-                         xs, (const uint32_t*)qweight, N, pc, (const typename Elem<SDT>::T*)qscale, qzeros, gsz,
+      hipLaunchKernelGGL(kern, dim3((unsigned)(tm * tn)), dim3(TT::THREADS), TT::LDS_BYTES, st, (const uint16_t*)x, M,
+                         K, xs, (const uint32_t*)qweight, N, pc, (const typename Elem<SDT>::T*)qscale, qzeros, gsz,
                          (uint16_t*)y, tm, tn);
       return ANNA_MI_OK;
     };
-    const int rc = x_dtype == ANNA_MI_BF16 ? go(std::integral_constant<int, ANNA_MI_BF16>{})
-                                           : go(std::integral_constant<int, ANNA_MI_F16>{});
+    auto go_x = [&](auto tile_tag) {
+      return x_dtype == ANNA_MI_BF16 ? go(std::integral_constant<int, ANNA_MI_BF16>{}, tile_tag)
+                                     : go(std::integral_constant<int, ANNA_MI_F16>{}, tile_tag);
+    };
+    const int rc = shape == 0 ? go_x(TileL{}) : shape == 1 ? go_x(TileM{}) : go_x(TileS{});
     if (rc != ANNA_MI_OK) return rc;
   });
   ANNA_LAUNCH_CHECK("int4_gemm_tiled_kernel");

@@ -61,6 +61,23 @@ def test_int4_linear_matches_oracle(gpu, m, k, n, group, sdt):
     assert rel_err(y.float().cpu().numpy(), ref) <= BF16_TOL
 
 
+@pytest.mark.parametrize("tile", ["L", "M", "S"])
+@pytest.mark.parametrize("m,k,n,group,sdt", [(300, 512, 400, 64, "bf16"), (2048, 1024, 200, 128, "fp32"),
+                                             (64, 1024, 96, 128, "bf16"), (257, 256, 1000, 128, "bf16")])
+def test_int4_gemm_every_tile_shape(gpu, monkeypatch, tile, m, k, n, group, sdt):
+    """The tiled GEMM's three tile shapes (chosen by size in production), each forced."""
+    print(f"[case] int4 tiled GEMM tile={tile} M={m} K={k} N={n} g={group} scale={sdt}", flush=True)
+    monkeypatch.setenv("ANNA_MI_INT4_GEMM_TILE", tile)
+    rng = np.random.default_rng(m * 7 + k + n)
+    qw, qs, qz = int4_payload(rng, n, k, group, scale_dtype=sdt)
+    xb = orc.bf16_bits(rng.normal(size=(m, k)).astype(np.float32))
+    ref = orc.int4_linear(xb, qw, qs, qz, group)
+    qs_t = _dev(qs, gpu).to(torch.bfloat16 if sdt == "bf16" else torch.float32)
+    x = _x_tensor(xb, torch.bfloat16, gpu)
+    y = torch.ops.anna.xpu_int4_gemv(x, _dev(qw, gpu), qs_t, _dev(qz, gpu), group, k)
+    assert rel_err(y.float().cpu().numpy(), ref) <= BF16_TOL
+
+
 @pytest.mark.parametrize("xdt", [torch.float16, torch.float32])
 @pytest.mark.parametrize("m", [1, 4, 128])
 def test_int4_linear_other_activation_dtypes(gpu, xdt, m):
