@@ -302,25 +302,59 @@ __device__ __forceinline__ void moe_sweep(const anna_mi_moe_mlp_args& a, uint16_
 #pragma unroll
     for (int j = 0; j < MOE_PB; ++j) {
       if (p * MOE_PB + j >= nblk) continue;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        // lanes kq hold k = 128 b + 32 kq + 8 s + e: a step spans the whole block, so each of
-        // its GPB groups gets its own MFMA with the other groups' lanes zeroed
-        u32x4 wf[NM];
-#pragma unroll
-        for (int m = 0; m < NM; ++m) wf[m] = nibbles_to_frag<MDT>(cur.w[j][m][s]);
+      if constexpr (GPB == 1) {
+        // One group per block: its 4 steps accumulate in the MFMA (one accumulator per route
+        // chunk and matrix), and the group's scale and zero point apply once per block:
+        //   sum_k x (q - z) s = s * (sum_k x (off + q) - (off + z) sum_k x).
+        f32x4 acc[NC][NM], sx[NC];
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-          const u32x4 xa = interleave_x(*(const u32x4*)(xs + (c * 16 + r) * MOE_XP + j * 128 + kq * 32 + s * 8));
+          sx[c] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int q = 0; q < GPB; ++q) {
-            const u32x4 xm = (GPB == 1 || kq / (4 / GPB) == q) ? xa : u32x4{0u, 0u, 0u, 0u};
-            const f32x4 sx = mfma16<MDT>(xm, ones, f32x4{0.f, 0.f, 0.f, 0.f});
+          for (int m = 0; m < NM; ++m) acc[c][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
 #pragma unroll
-            for (int m = 0; m < NM; ++m) {
-              const f32x4 acc = mfma16<MDT>(xm, wf[m], f32x4{0.f, 0.f, 0.f, 0.f});
+        for (int s = 0; s < 4; ++s) {
+          u32x4 wf[NM];
 #pragma unroll
-              for (int i = 0; i < 4; ++i) out[c][m][i] = fmaf(cur.s[j][q][m], acc[i] - cur.c[j][q][m] * sx[i], out[c][m][i]);
+          for (int m = 0; m < NM; ++m) wf[m] = nibbles_to_frag<MDT>(cur.w[j][m][s]);
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            const u32x4 xa = interleave_x(*(const u32x4*)(xs + (c * 16 + r) * MOE_XP + j * 128 + kq * 32 + s * 8));
+            sx[c] = mfma16<MDT>(xa, ones, sx[c]);
+#pragma unroll
+            for (int m = 0; m < NM; ++m) acc[c][m] = mfma16<MDT>(xa, wf[m], acc[c][m]);
+          }
+        }
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              out[c][m][i] = fmaf(cur.s[j][0][m], acc[c][m][i] - cur.c[j][0][m] * sx[c][i], out[c][m][i]);
+      } else {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          // lanes kq hold k = 128 b + 32 kq + 8 s + e: a step spans the whole block, so each of
+          // its GPB groups gets its own MFMA with the other groups' lanes zeroed, scaled per step
+          u32x4 wf[NM];
+#pragma unroll
+          for (int m = 0; m < NM; ++m) wf[m] = nibbles_to_frag<MDT>(cur.w[j][m][s]);
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            const u32x4 xa = interleave_x(*(const u32x4*)(xs + (c * 16 + r) * MOE_XP + j * 128 + kq * 32 + s * 8));
+#pragma unroll
+            for (int q = 0; q < GPB; ++q) {
+              const u32x4 xm = kq / (4 / GPB) == q ? xa : u32x4{0u, 0u, 0u, 0u};
+              const f32x4 sxq = mfma16<MDT>(xm, ones, f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+              for (int m = 0; m < NM; ++m) {
+                const f32x4 accq = mfma16<MDT>(xm, wf[m], f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                  out[c][m][i] = fmaf(cur.s[j][q][m], accq[i] - cur.c[j][q][m] * sxq[i], out[c][m][i]);
+              }
             }
           }
         }
