@@ -59,19 +59,19 @@ using TileS = GemmTile<64, 48, 4, 1>;    // M < 256:   16 x 48 wave tiles, 36 KB
 // step's LDS-destination x loads are in LDS), its LDS writes are done, then the workgroup
 // barrier.  __syncthreads() would also wait for the loads just issued, since its release fence
 // covers LDS-destination loads.
+#define GM_WAIT_BARRIER(n) asm volatile("s_waitcnt vmcnt(" #n ") lgkmcnt(0)\n\ts_barrier" ::: "memory")
 template <int N>
 __device__ __forceinline__ void loader_barrier() {
-  static_assert(N == 17 || N == 10 || N == 5, "add the wait count of a new tile shape here");
-  if constexpr (N == 17) asm volatile("s_waitcnt vmcnt(17) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  else if constexpr (N == 10) asm volatile("s_waitcnt vmcnt(10) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  else asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  static_assert(N == 17 || N == 10 || N == 5 || N == 26 || N == 16 || N == 8,
+                "add the wait count of a new tile shape here");
+  if constexpr (N == 17) GM_WAIT_BARRIER(17);
+  else if constexpr (N == 10) GM_WAIT_BARRIER(10);
+  else if constexpr (N == 5) GM_WAIT_BARRIER(5);
+  else if constexpr (N == 26) GM_WAIT_BARRIER(26);
+  else if constexpr (N == 16) GM_WAIT_BARRIER(16);
+  else GM_WAIT_BARRIER(8);
 }
-template <int N>
-__device__ __forceinline__ void loader_wait() {
-  if constexpr (N == 17) asm volatile("s_waitcnt vmcnt(17)" ::: "memory");
-  else if constexpr (N == 10) asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
-  else asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
-}
+#undef GM_WAIT_BARRIER
 
 typedef float f32x2v __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
@@ -151,15 +151,20 @@ __global__ __launch_bounds__(T::THREADS) void int4_gemm_tiled_kernel(
       uint2 w[GM_WPT];
       uint32_t sc[GM_WPT], z[GM_WPT];
     };
-    // every step issues the same GM_LOADS_PER_STEP loads (steps past the end reload the last
-    // one into a buffer nobody reads), so a fixed vmcnt names "all but this step's loads"
-    auto load = [&](int ks, int abuf, Stage& S) {
+    // Every step issues the same loads: the x tile of step ks + 2 and the W words, scales and
+    // zero points of step ks + 3 (steps past the end reload the last one into a buffer nobody
+    // reads), so a fixed vmcnt names "all but this step's loads".  W is issued a step earlier
+    // than x because its dequant must finish within the step before the MFMAs use it.
+    auto load_x = [&](int ks, int abuf) {
       ks = ks < nk ? ks : nk - 1;
       uint16_t* dst = sA0 + abuf * GM_LDS_A + lw * (GM_XLD * 8 * GM_BK);
 #pragma unroll
       for (int j = 0; j < GM_XLD; ++j)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(dst + j * 8 * GM_BK), 16, xo,
                                                  (int)((8 * (GM_XLD * lw + j)) * xs * 2) + ks * (GM_BK * 2), 0, 0);
+    };
+    auto load_w = [&](int ks, Stage& S) {
+      ks = ks < nk ? ks : nk - 1;
       const int g = spg == 1 ? ks : (int)__umulhi((uint32_t)ks, ginv);
 #pragma unroll
       for (int i = 0; i < GM_WPT; ++i) {
@@ -203,24 +208,33 @@ __global__ __launch_bounds__(T::THREADS) void int4_gemm_tiled_kernel(
         }
       }
     };
-    Stage S0, S1;
-    load(0, 0, S0);
-    load(1, 1, S1);
-    loader_wait<T::LOADS_PER_STEP>();
+    // prologue: W of steps 0..2 and x of steps 0..1; W of step 0 to LDS; barrier once x of
+    // step 0 has landed (the loads after it: W 1, x 1, W 2)
+    Stage S0, S1, S2;
+    load_w(0, S0);
+    load_x(0, 0);
+    load_w(1, S1);
+    load_x(1, 1);
+    load_w(2, S2);
     store(S0, 0);
-    loader_barrier<T::LOADS_PER_STEP>();
-    int a2 = 2;  // x buffer of step ks + 2
-    for (int ks = 0; ks < nk; ks += 2) {
-      // step ks: MFMA waves read x buffer ks % 3 and W buffer 0
-      load(ks + 2, a2, S0);
+    loader_barrier<2 * T::LOADS_PER_STEP - T::XLD>();
+    // step ks: W of ks + 3 into the stage that held W of ks, x of ks + 2 into the x buffer read
+    // at step ks - 1, dequantize W of ks + 1, barrier once x of ks + 1 has landed
+    int a2 = 2, b1 = 1;  // x buffer of step ks + 2, W buffer of step ks + 1
+    auto step = [&](int ks, Stage& Sfree, Stage& Snext) {
+      load_w(ks + 3, Sfree);
+      load_x(ks + 2, a2);
       a2 = a2 == GM_NA - 1 ? 0 : a2 + 1;
-      if (ks + 1 < nk) store(S1, 1);
+      if (ks + 1 < nk) store(Snext, b1);
+      b1 ^= 1;
       loader_barrier<T::LOADS_PER_STEP>();
+    };
+    for (int ks = 0; ks < nk; ks += 3) {
+      step(ks, S0, S1);
       if (ks + 1 >= nk) break;
-      load(ks + 3, a2, S1);
-      a2 = a2 == GM_NA - 1 ? 0 : a2 + 1;
-      if (ks + 2 < nk) store(S0, 0);
-      loader_barrier<T::LOADS_PER_STEP>();
+      step(ks + 1, S1, S2);
+      if (ks + 2 >= nk) break;
+      step(ks + 2, S2, S0);
     }
     // the last steps' reloads land in buffers nobody reads; drain them before the wave ends
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
