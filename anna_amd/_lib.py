@@ -92,12 +92,15 @@ class MoeMlpArgs(ctypes.Structure):
         ("down_qweight", _P), ("down_qscale", _P), ("down_qzeros", _P),
         ("hidden_packed_cols", _I64), ("hidden_groups", _I64), ("intermediate_packed_cols", _I64),
         ("intermediate_groups", _I64), ("group_size", _I64), ("activation", _P), ("sweep_chunks", _I),
+        ("items", _P), ("items_prefilled", _I),
     ]
 
 
 PROTOTYPES.update({
     "anna_mi_moe_router": [_P, _I, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _P],
     "anna_mi_moe_dispatch": [_P, _I, _I64, _I64, _I64, _P, _P, _P, _I, _I64, _I64, _P, _P, _P, _P, _P, _P, _P],
+    "anna_mi_moe_route_small": [_P, _I, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P],
+    "anna_mi_moe_gather": [_P, _I, _I64, _I64, _P, _P, _I64, _I64, _P, _P, _P],
     "anna_mi_moe_scatter": [_P, _I, _I64, _I64, _P, _I64, _P, _P, _P],
     "anna_mi_moe_combine": [_P, _I, _I64, _P, _I64, _I64, _P, _P],
     "anna_mi_moe_grouped_int4_mlp": [ctypes.POINTER(MoeMlpArgs), _P],

@@ -29,16 +29,20 @@ namespace {
 
 // ------------------------------------------------------------------ router
 
-// One wave per token; lane l holds experts l, l + 64, ...
+// LDS scratch route_token needs per wave, in floats
+__host__ __device__ constexpr int route_scratch(int64_t E) { return (int)((E + 3) / 4 * 4) + 128; }
+
+// Softmax over the E logits of token t and its top_k (ties to the lower expert index), by one
+// wave; lane l holds experts l, l + 64, ...  Lane j < top_k returns route j's weight (normalized
+// over the top_k when asked) and expert.  The top_k is found by rank, not by k rounds of a
+// cross-lane argmax: the probabilities go to the wave's LDS scratch sp (route_scratch(E)
+// floats), every lane counts for each of its experts how many experts beat it (a larger
+// probability, or an equal one at a lower index), and an expert of rank j < top_k is route j.
 template <int LDT>
-__global__ __launch_bounds__(256) void moe_router_kernel(const typename Elem<LDT>::T* __restrict__ logits,
-                                                         int64_t T, int64_t E, int64_t ls, int64_t top_k, int normalize,
-                                                         float* __restrict__ weights, int64_t* __restrict__ selected,
-                                                         int32_t* __restrict__ usage) {
+__device__ __forceinline__ void route_token(const typename Elem<LDT>::T* __restrict__ logits, int64_t t, int64_t E,
+                                            int64_t ls, int64_t top_k, int normalize, int lane, float* sp,
+                                            float& w_out, int64_t& e_out) {
   constexpr int MAXV = 16;  // experts per lane (E <= 1024)
-  const int lane = threadIdx.x & 63;
-  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= T) return;
   float v[MAXV];
   float mx = -INFINITY;
 #pragma unroll
@@ -56,34 +60,144 @@ __global__ __launch_bounds__(256) void moe_router_kernel(const typename Elem<LDT
     s += v[i];
   }
   const float inv = 1.0f / wave_sum(s);
+  const int E4 = (int)((E + 3) / 4 * 4);
+  float* stp = sp + E4;                 // route j's probability
+  int* ste = (int*)(sp + E4 + 64);      // route j's expert
 #pragma unroll
-  for (int i = 0; i < MAXV; ++i) v[i] = lane + 64 * i < E ? v[i] * inv : -1.0f;  // -1: not a candidate
-  float top_sum = 0.f;
-  float mine = 0.f;  // lane j < top_k keeps route j's probability
-  int64_t mine_e = 0;
-  for (int64_t j = 0; j < top_k; ++j) {
-    float bv = -2.0f;
-    int be = 0x7FFFFFFF;
-#pragma unroll
-    for (int i = 0; i < MAXV; ++i)
-      if (v[i] > bv) bv = v[i], be = lane + 64 * i;  // strict: lowest index among equals in this lane
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      const float ov = __shfl_xor(bv, off, 64);
-      const int oe = __shfl_xor(be, off, 64);
-      if (ov > bv || (ov == bv && oe < be)) bv = ov, be = oe;
-    }
-    top_sum += bv;
-    if (lane == (int)j) mine = bv, mine_e = be;
-#pragma unroll
-    for (int i = 0; i < MAXV; ++i)
-      if (lane + 64 * i == be) v[i] = -1.0f;
+  for (int i = 0; i < MAXV; ++i) {
+    const int e = lane + 64 * i;
+    if (e < E) sp[e] = v[i] * inv;
+    else if (e < E4) sp[e] = -2.0f;     // padding: beats nothing, ties nothing
   }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  for (int e = lane; e < E; e += 64) {
+    const float p = sp[e];
+    int rank = 0;
+    for (int j = 0; j < E4; j += 4) {
+      const float4 q = *(const float4*)(sp + j);
+      rank += (q.x > p || (q.x == p && j < e)) + (q.y > p || (q.y == p && j + 1 < e)) +
+              (q.z > p || (q.z == p && j + 2 < e)) + (q.w > p || (q.w == p && j + 3 < e));
+    }
+    if (rank < top_k) {
+      stp[rank] = p;
+      ste[rank] = e;
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float top_sum = 0.f;  // in route order (descending), as the k rounds of argmax summed them
+  for (int64_t j = 0; j < top_k; ++j) top_sum += stp[j];
   const float scale = normalize && top_sum > 0.f ? 1.0f / top_sum : 1.0f;
+  w_out = lane < top_k ? stp[lane] * scale : 0.f;
+  e_out = lane < top_k ? ste[lane] : 0;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();  // sp is reused by the wave's next token
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// One wave per token.
+template <int LDT>
+__global__ __launch_bounds__(256) void moe_router_kernel(const typename Elem<LDT>::T* __restrict__ logits,
+                                                         int64_t T, int64_t E, int64_t ls, int64_t top_k, int normalize,
+                                                         float* __restrict__ weights, int64_t* __restrict__ selected,
+                                                         int32_t* __restrict__ usage) {
+  extern __shared__ float r_scratch[];  // 4 x route_scratch(E)
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  float w;
+  int64_t e;
+  route_token<LDT>(logits, t, E, ls, top_k, normalize, lane, r_scratch + (threadIdx.x >> 6) * route_scratch(E), w, e);
   if (lane < top_k) {
-    weights[t * top_k + lane] = mine * scale;
-    selected[t * top_k + lane] = mine_e;
-    atomicAdd(usage + mine_e, 1);
+    weights[t * top_k + lane] = w;
+    selected[t * top_k + lane] = e;
+    atomicAdd(usage + e, 1);
+  }
+}
+
+// Exclusive prefix sum of v over the 1024 threads of a workgroup (s: 16 ints of LDS); *total
+// receives the sum.
+__device__ __forceinline__ int block_exclusive_scan(int v, int* s, int* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int inc = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(inc, off, 64);
+    if (lane >= off) inc += o;
+  }
+  if (lane == 63) s[wave] = inc;
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < 16; ++w) {
+    before += w < wave ? s[w] : 0;
+    all += s[w];
+  }
+  __syncthreads();  // s may be reused by the caller
+  *total = all;
+  return before + inc - v;
+}
+
+// Router + dispatch order + the MLP's item list in one workgroup, for small batches (routes =
+// tokens x top_k <= 1024, E <= 1024): the outputs of moe_router_kernel (usage included, no
+// separate clearing) and of moe_order_kernel (offsets, sorted token / route, route_pos), in the
+// same deterministic (expert, token, k) order, plus items as moe_compact_items_kernel writes
+// them for the experts with routes (bank slot slots[e]).  Four launches become one; each of
+// them costs a few microseconds here whatever its work.
+template <int LDT>
+__global__ __launch_bounds__(1024) void moe_route_small_kernel(
+    const typename Elem<LDT>::T* __restrict__ logits, int64_t T, int64_t E, int64_t ls, int64_t top_k, int normalize,
+    float* __restrict__ weights, int64_t* __restrict__ selected, int32_t* __restrict__ usage,
+    int64_t* __restrict__ offsets, int64_t* __restrict__ sorted_token, int64_t* __restrict__ sorted_route,
+    int64_t* __restrict__ route_pos, const int64_t* __restrict__ slots, int32_t* __restrict__ items) {
+  __shared__ int s_cnt[1024], s_sel[1024], s_off[1024], s_scan[16];
+  extern __shared__ float r_scratch[];  // 16 x route_scratch(E)
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t R = T * top_k;
+  s_cnt[threadIdx.x] = 0;
+  __syncthreads();
+  for (int64_t t = wave; t < T; t += 16) {
+    float w;
+    int64_t e;
+    route_token<LDT>(logits, t, E, ls, top_k, normalize, lane, r_scratch + wave * route_scratch(E), w, e);
+    if (lane < top_k) {
+      weights[t * top_k + lane] = w;
+      selected[t * top_k + lane] = e;
+      s_sel[t * top_k + lane] = (int)e;
+      atomicAdd(&s_cnt[e], 1);
+    }
+  }
+  __syncthreads();
+  const int e = threadIdx.x;
+  const int cnt = e < E ? s_cnt[e] : 0;
+  int total;
+  const int start = block_exclusive_scan(cnt, s_scan, &total);
+  int nact;
+  const int j = block_exclusive_scan(cnt > 0 ? 1 : 0, s_scan, &nact);
+  if (e < E) {
+    usage[e] = cnt;
+    offsets[e] = start;
+    s_off[e] = start;
+    if (cnt > 0) *(int4*)(items + 4 + 4 * j) = make_int4((int)slots[e], start, start + cnt, 0);
+  }
+  if (e == 0) {
+    offsets[E] = total;
+    items[0] = nact;
+  }
+  __syncthreads();
+  // route r: position = first slot of its expert + the routes before it with the same expert
+  const int r = threadIdx.x;
+  if (r < R) {
+    const int er = s_sel[r];
+    int rank = 0;
+    for (int q = 0; q < r; ++q) rank += s_sel[q] == er;
+    const int64_t pos = s_off[er] + rank;
+    sorted_token[pos] = r / top_k;
+    sorted_route[pos] = r;
+    if (route_pos) route_pos[r] = pos;
   }
 }
 
@@ -201,6 +315,11 @@ constexpr int MOE_ROWS = 64;  // output rows per workgroup (4 waves x 16)
 constexpr int MOE_PB = 4;     // 128-k blocks per pass (x is staged 512 k at a time)
 constexpr int MOE_XP = MOE_PB * 128 + 8;  // LDS row pitch of the staged x slice (16-bit elements)
 constexpr int MOE_MAXC = 4;   // 16-route chunks per sweep over the weights (64 routes)
+// Whole-x staging (gate/up with one 16-route chunk): the x rows of all of K (<= MOE_XF_KMAX) go
+// to LDS once, by buffer loads with an LDS destination, in the same round trip as the first
+// pass's weights; the passes then wait only for their (prefetched) weights.
+constexpr int MOE_XF_KMAX = 2048;
+typedef __attribute__((address_space(3))) void* moe_lds_ptr;
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
@@ -235,7 +354,7 @@ struct MoePass {
 // Per pass: load this pass's x slice and store it to LDS, issue the next pass's weight loads
 // (after the x loads: vector loads complete in order, so waiting for x never waits for
 // them), then run the MFMAs of every chunk on the weights already in registers.
-template <int HDT, int SDT, bool GU, int GPB, int NC>
+template <int HDT, int SDT, bool GU, int GPB, int NC, bool XF = false>
 __device__ __forceinline__ void moe_sweep(const anna_mi_moe_mlp_args& a, uint16_t* xs, int64_t c0, int64_t nrows,
                                           int64_t slot, int64_t N, int64_t K, int64_t n, bool n_ok,
                                           const uint32_t* const* wrow, const void* const* sc, const int8_t* const* zp) {
@@ -279,8 +398,29 @@ __device__ __forceinline__ void moe_sweep(const anna_mi_moe_mlp_args& a, uint16_
 
   MoePass<NM, GPB> cur, nxt;
   load_pass(0, cur);
+  // x row pitch in LDS (16-bit elements): a 512-k slice per pass, or all of K (XF)
+  const int64_t xp = XF ? K + 8 : MOE_XP;
+  if constexpr (XF) {
+    static_assert(NC == 1 && GU, "whole-x staging is for the gate/up pass with one chunk");
+    // wave w copies rows 4w .. 4w + 3, 512 k (1 KB) per load; rows past the expert's routes
+    // fall outside the descriptor and read as zero
+    const int wave = threadIdx.x >> 6;
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void*>(xsrc), 0, (int)(((c0 + nrows) * K) * 2), 0x00020000);
+    const int64_t nq = K / 512;
+    for (int rr = 0; rr < 4; ++rr) {
+      const int row = 4 * wave + rr;
+      for (int64_t q = 0; q < nq; ++q)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (moe_lds_ptr)(xs + row * xp + q * 512), 16, (uint32_t)(lane * 16),
+                                                 (int)(((c0 + row) * K + q * 512) * 2), 0, 0);
+    }
+    // both the weights of pass 0 and x are needed now: wait for everything, then publish x
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
   for (int64_t p = 0; p < npass; ++p) {
     // x slice [NC*16 rows][512 k] of this pass (rows past the expert's routes read as zero)
+    if constexpr (!XF) {
     u32x4 xv[XPT];
 #pragma unroll
     for (int i = 0; i < XPT; ++i) {
@@ -298,6 +438,7 @@ __device__ __forceinline__ void moe_sweep(const anna_mi_moe_mlp_args& a, uint16_
       *(u32x4*)(xs + (e >> 6) * MOE_XP + (e & 63) * 8) = xv[i];
     }
     __syncthreads();
+    }
     if (p + 1 < npass) load_pass(p + 1, nxt);  // in flight during this pass's MFMAs
 #pragma unroll
     for (int j = 0; j < MOE_PB; ++j) {
@@ -320,7 +461,7 @@ __device__ __forceinline__ void moe_sweep(const anna_mi_moe_mlp_args& a, uint16_
           for (int m = 0; m < NM; ++m) wf[m] = nibbles_to_frag<MDT>(cur.w[j][m][s]);
 #pragma unroll
           for (int c = 0; c < NC; ++c) {
-            const u32x4 xa = interleave_x(*(const u32x4*)(xs + (c * 16 + r) * MOE_XP + j * 128 + kq * 32 + s * 8));
+            const u32x4 xa = interleave_x(*(const u32x4*)(xs + (c * 16 + r) * xp + (XF ? p * (MOE_PB * 128) : 0) + j * 128 + kq * 32 + s * 8));
             sx[c] = mfma16<MDT>(xa, ones, sx[c]);
 #pragma unroll
             for (int m = 0; m < NM; ++m) acc[c][m] = mfma16<MDT>(xa, wf[m], acc[c][m]);
@@ -343,7 +484,7 @@ __device__ __forceinline__ void moe_sweep(const anna_mi_moe_mlp_args& a, uint16_
           for (int m = 0; m < NM; ++m) wf[m] = nibbles_to_frag<MDT>(cur.w[j][m][s]);
 #pragma unroll
           for (int c = 0; c < NC; ++c) {
-            const u32x4 xa = interleave_x(*(const u32x4*)(xs + (c * 16 + r) * MOE_XP + j * 128 + kq * 32 + s * 8));
+            const u32x4 xa = interleave_x(*(const u32x4*)(xs + (c * 16 + r) * xp + (XF ? p * (MOE_PB * 128) : 0) + j * 128 + kq * 32 + s * 8));
 #pragma unroll
             for (int q = 0; q < GPB; ++q) {
               const u32x4 xm = kq / (4 / GPB) == q ? xa : u32x4{0u, 0u, 0u, 0u};
@@ -384,21 +525,19 @@ __device__ __forceinline__ void moe_sweep(const anna_mi_moe_mlp_args& a, uint16_
 // GU: pass 1 (gate and up, K = hidden, N = intermediate, act fp32 out); otherwise pass 2
 // (down, K = intermediate, N = hidden, compact outputs in HDT).  GPB: int4 groups per 128-k
 // block (group size 128 / GPB; larger groups count as 1).  grid (N / 64, active experts).
-template <int HDT, int SDT, bool GU, int GPB, int NCMAX>
-__global__ __launch_bounds__(256) void moe_int4_mlp_kernel(const anna_mi_moe_mlp_args a) {
+// One work item: output rows [64 tile, 64 tile + 64) of bank slot `slot` for the compact routes
+// [start, end) of one expert.
+template <int HDT, int SDT, bool GU, int GPB, int NCMAX, bool XF>
+__device__ __forceinline__ void moe_mlp_item(const anna_mi_moe_mlp_args& a, uint16_t* xs, int64_t tile, int64_t slot,
+                                             int64_t start, int64_t end) {
   constexpr int NM = GU ? 2 : 1;
-  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [sweep_chunks * 16][MOE_XP]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, kq = lane >> 4;
-  const int64_t ai = blockIdx.y;
-  const int64_t e = a.active_experts[ai], slot = a.active_slots[ai];
-  const int64_t start = a.expert_offsets[e], end = a.expert_offsets[e + 1];
-  if (end <= start) return;
   const int64_t N = GU ? a.intermediate_dim : a.hidden_dim;
   const int64_t K = GU ? a.hidden_dim : a.intermediate_dim;
   const int64_t pc = GU ? a.hidden_packed_cols : a.intermediate_packed_cols;
   const int64_t G = GU ? a.hidden_groups : a.intermediate_groups;
-  const int64_t n = (int64_t)blockIdx.x * MOE_ROWS + wave * 16 + r;
+  const int64_t n = tile * MOE_ROWS + wave * 16 + r;
   const bool n_ok = n < N;
   const int64_t nc = n_ok ? n : 0;
   const uint32_t* wrow[NM];
@@ -420,7 +559,9 @@ __global__ __launch_bounds__(256) void moe_int4_mlp_kernel(const anna_mi_moe_mlp
   const int64_t sweep = (int64_t)a.sweep_chunks * 16;  // routes per sweep (the LDS holds their x slice)
   for (int64_t c0 = start; c0 < end; c0 += sweep) {
     const int64_t nrows = end - c0 < sweep ? end - c0 : sweep;
-    if (NCMAX == 1 || nrows <= 16)
+    if constexpr (XF)
+      moe_sweep<HDT, SDT, GU, GPB, 1, true>(a, xs, c0, nrows, slot, N, K, n, n_ok, wrow, sc, zp);
+    else if (NCMAX == 1 || nrows <= 16)
       moe_sweep<HDT, SDT, GU, GPB, 1>(a, xs, c0, nrows, slot, N, K, n, n_ok, wrow, sc, zp);
     else if (NCMAX == 2 || nrows <= 32)
       moe_sweep<HDT, SDT, GU, GPB, (NCMAX >= 2 ? 2 : 1)>(a, xs, c0, nrows, slot, N, K, n, n_ok, wrow, sc, zp);
@@ -430,13 +571,108 @@ __global__ __launch_bounds__(256) void moe_int4_mlp_kernel(const anna_mi_moe_mlp
   }
 }
 
+// Two forms.  Without a.items: grid (tiles, active experts), one item per workgroup, empty
+// experts exit.  With a.items (the experts that have routes, compacted by
+// moe_compact_items_kernel): a persistent grid that walks the items (entry, tile) of the
+// compacted list, so no workgroup is dispatched for an empty expert (dispatching thousands of
+// workgroups that exit at once costs tens of microseconds here).
+template <int HDT, int SDT, bool GU, int GPB, int NCMAX, bool XF = false>
+__global__ __launch_bounds__(256) void moe_int4_mlp_kernel(const anna_mi_moe_mlp_args a) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [sweep_chunks * 16][MOE_XP]
+  if (a.items == nullptr) {
+    const int64_t ai = blockIdx.y;
+    const int64_t e = a.active_experts[ai], slot = a.active_slots[ai];
+    const int64_t start = a.expert_offsets[e], end = a.expert_offsets[e + 1];
+    if (end <= start) return;
+    moe_mlp_item<HDT, SDT, GU, GPB, NCMAX, XF>(a, xs, blockIdx.x, slot, start, end);
+    return;
+  }
+  const int64_t N = GU ? a.intermediate_dim : a.hidden_dim;
+  const int tiles = (int)((N + MOE_ROWS - 1) / MOE_ROWS);
+  const int64_t nitems = (int64_t)a.items[0] * tiles;
+  int64_t it = blockIdx.x;
+  if (it >= nitems) return;
+  int4 cur = *(const int4*)(a.items + 4 + 4 * (it / tiles));  // {slot, start, end, -}
+  for (;;) {
+    const int64_t nx = it + gridDim.x;
+    const int4 nxt = *(const int4*)(a.items + 4 + 4 * ((nx < nitems ? nx : it) / tiles));  // in flight meanwhile
+    moe_mlp_item<HDT, SDT, GU, GPB, NCMAX, XF>(a, xs, it % tiles, cur.x, cur.y, cur.z);
+    if (nx >= nitems) break;
+    it = nx;
+    cur = nxt;
+  }
+}
+
+// items[0] = number of active experts with routes; items[4 + 4 j ..] = {bank slot, first
+// compact route, end route, 0} of the j-th of them, in active-list order.  One workgroup.
+__global__ __launch_bounds__(1024) void moe_compact_items_kernel(const int64_t* __restrict__ active_experts,
+                                                                 const int64_t* __restrict__ active_slots,
+                                                                 int64_t active_count,
+                                                                 const int64_t* __restrict__ offsets,
+                                                                 int32_t* __restrict__ items) {
+  __shared__ int s_wave[16];
+  __shared__ int s_base;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (threadIdx.x == 0) s_base = 0;
+  __syncthreads();
+  for (int64_t i0 = 0; i0 < active_count; i0 += 1024) {
+    const int64_t ai = i0 + threadIdx.x;
+    int64_t e = 0, slot = 0, st = 0, en = 0;
+    if (ai < active_count) {
+      e = active_experts[ai];
+      slot = active_slots[ai];
+      st = offsets[e];
+      en = offsets[e + 1];
+    }
+    const bool has = ai < active_count && en > st;
+    const uint64_t bal = __ballot(has);
+    if (lane == 0) s_wave[wave] = __popcll(bal);
+    __syncthreads();
+    int before = s_base;
+    for (int w = 0; w < wave; ++w) before += s_wave[w];
+    if (has) {
+      int4* dst = (int4*)(items + 4 + 4 * (before + __popcll(bal & ((1ull << lane) - 1ull))));
+      *dst = make_int4((int)slot, (int)st, (int)en, 0);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int tot = 0;
+      for (int w = 0; w < 16; ++w) tot += s_wave[w];
+      s_base += tot;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) items[0] = s_base;
+}
+
 }  // namespace
 
 namespace {
 template <int HDT, int SDT, int GPB, int NCMAX>
 int launch_moe_mlp_nc(const anna_mi_moe_mlp_args& a, hipStream_t st, dim3 g1, dim3 g2) {
+  if (a.items) {
+    // persistent: at most the workgroups that fit at once (2 per CU for gate/up, 3 for down at
+    // these register counts), and no more than there can be items
+    const unsigned t1 = g1.x * g1.y, t2 = g2.x * g2.y;
+    g1 = dim3(t1 < 512u ? t1 : 512u);
+    g2 = dim3(t2 < 768u ? t2 : 768u);
+  }
   const size_t lds = (size_t)NCMAX * 16 * MOE_XP * 2;
-  hipLaunchKernelGGL((moe_int4_mlp_kernel<HDT, SDT, true, GPB, NCMAX>), g1, dim3(256), lds, st, a);
+  const int64_t K = a.hidden_dim;
+  if (NCMAX == 1 && HDT != ANNA_MI_F32 && K <= MOE_XF_KMAX && K % 512 == 0) {
+    auto kern = moe_int4_mlp_kernel<HDT, SDT, true, GPB, 1, true>;
+    const size_t lds_xf = (size_t)16 * (K + 8) * 2;
+    static bool attr_set = false;
+    if (!attr_set) {
+      ANNA_CHECK(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     (int)(16 * (MOE_XF_KMAX + 8) * 2)) == hipSuccess,
+                 "moe MLP: cannot raise the LDS limit");
+      attr_set = true;
+    }
+    hipLaunchKernelGGL(kern, g1, dim3(256), lds_xf, st, a);
+  } else {
+    hipLaunchKernelGGL((moe_int4_mlp_kernel<HDT, SDT, true, GPB, NCMAX>), g1, dim3(256), lds, st, a);
+  }
   ANNA_LAUNCH_CHECK("moe_int4_mlp_kernel (gate, up)");
   hipLaunchKernelGGL((moe_int4_mlp_kernel<HDT, SDT, false, GPB, NCMAX>), g2, dim3(256), lds, st, a);
   ANNA_LAUNCH_CHECK("moe_int4_mlp_kernel (down)");
@@ -472,7 +708,8 @@ extern "C" int anna_mi_moe_router(const void* logits, int logits_dtype, int64_t 
   ANNA_LAUNCH_CHECK("fill_i32_kernel");
   if (tokens == 0) return ANNA_MI_OK;
   ANNA_DISPATCH_DTYPE(logits_dtype, LDT, {
-    hipLaunchKernelGGL((moe_router_kernel<LDT>), dim3((unsigned)((tokens + 3) / 4)), dim3(256), 0, st,
+    hipLaunchKernelGGL((moe_router_kernel<LDT>), dim3((unsigned)((tokens + 3) / 4)), dim3(256),
+                       4 * route_scratch(num_experts) * sizeof(float), st,
                        (const typename Elem<LDT>::T*)logits, tokens, num_experts, logits_row_stride, top_k, normalize,
                        weights, selected, usage);
   });
@@ -508,6 +745,47 @@ extern "C" int anna_mi_moe_dispatch(const void* hidden, int dtype, int64_t token
     hipLaunchKernelGGL((moe_gather_kernel<HDT>), dim3((unsigned)routes), dim3(64), 0, st, (const T*)hidden, hidden_dim,
                        hidden_row_stride, (const T*)routing_weights, sorted_route_idx, top_k, (T*)compact_hidden,
                        (T*)compact_weights);
+  });
+  ANNA_LAUNCH_CHECK("moe_gather_kernel");
+  return ANNA_MI_OK;
+}
+
+extern "C" int anna_mi_moe_route_small(const void* logits, int logits_dtype, int64_t tokens, int64_t num_experts,
+                                       int64_t logits_row_stride, int64_t top_k, int normalize, float* weights,
+                                       int64_t* selected, int32_t* usage, int64_t* expert_offsets,
+                                       int64_t* sorted_token_idx, int64_t* sorted_route_idx, int64_t* route_pos,
+                                       const int64_t* slots, int32_t* items, void* stream) {
+  ANNA_CHECK(logits && weights && selected && usage && expert_offsets && sorted_token_idx && sorted_route_idx && slots &&
+                 items,
+             "anna_mi_moe_route_small: null pointer");
+  ANNA_CHECK(num_experts > 0 && num_experts <= 1024, "anna_mi_moe_route_small: num_experts must be in [1, 1024]");
+  ANNA_CHECK(top_k > 0 && top_k <= num_experts && top_k <= 64, "anna_mi_moe_route_small: need 0 < top_k <= min(num_experts, 64)");
+  ANNA_CHECK(tokens > 0 && tokens * top_k <= 1024 && logits_row_stride >= num_experts,
+             "anna_mi_moe_route_small: need 0 < tokens * top_k <= 1024 (use the router + dispatch entry points above)");
+  ANNA_CHECK(num_experts <= 512, "anna_mi_moe_route_small: num_experts must be <= 512 (LDS)");
+  ANNA_DISPATCH_DTYPE(logits_dtype, LDT, {
+    hipLaunchKernelGGL((moe_route_small_kernel<LDT>), dim3(1), dim3(1024), 16 * route_scratch(num_experts) * sizeof(float),
+                       as_stream(stream),
+                       (const typename Elem<LDT>::T*)logits, tokens, num_experts, logits_row_stride, top_k, normalize,
+                       weights, selected, usage, expert_offsets, sorted_token_idx, sorted_route_idx, route_pos, slots,
+                       items);
+  });
+  ANNA_LAUNCH_CHECK("moe_route_small_kernel");
+  return ANNA_MI_OK;
+}
+
+extern "C" int anna_mi_moe_gather(const void* hidden, int dtype, int64_t hidden_dim, int64_t hidden_row_stride,
+                                  const void* routing_weights, const int64_t* sorted_route_idx, int64_t routes,
+                                  int64_t top_k, void* compact_hidden, void* compact_weights, void* stream) {
+  ANNA_CHECK(hidden && routing_weights && sorted_route_idx && compact_hidden && compact_weights,
+             "anna_mi_moe_gather: null pointer");
+  ANNA_CHECK(routes >= 0 && top_k > 0 && hidden_dim > 0 && hidden_row_stride >= hidden_dim, "anna_mi_moe_gather: bad shape");
+  if (routes == 0) return ANNA_MI_OK;
+  ANNA_DISPATCH_DTYPE(dtype, HDT, {
+    using T = typename Elem<HDT>::T;
+    hipLaunchKernelGGL((moe_gather_kernel<HDT>), dim3((unsigned)routes), dim3(64), 0, as_stream(stream), (const T*)hidden,
+                       hidden_dim, hidden_row_stride, (const T*)routing_weights, sorted_route_idx, top_k,
+                       (T*)compact_hidden, (T*)compact_weights);
   });
   ANNA_LAUNCH_CHECK("moe_gather_kernel");
   return ANNA_MI_OK;
@@ -572,6 +850,12 @@ extern "C" int anna_mi_moe_grouped_int4_mlp(const anna_mi_moe_mlp_args* ap, void
   ANNA_CHECK(a.sweep_chunks >= 1 && a.sweep_chunks <= MOE_MAXC, "anna_mi_moe_grouped_int4_mlp: sweep_chunks must be 1..4");
   if (a.routes == 0) return ANNA_MI_OK;
   hipStream_t st = as_stream(stream);
+  ANNA_CHECK(a.active_count < (1ll << 30) && a.routes < (1ll << 31), "anna_mi_moe_grouped_int4_mlp: too many routes");
+  if (a.items && !a.items_prefilled) {
+    hipLaunchKernelGGL(moe_compact_items_kernel, dim3(1), dim3(1024), 0, st, a.active_experts, a.active_slots,
+                       a.active_count, a.expert_offsets, a.items);
+    ANNA_LAUNCH_CHECK("moe_compact_items_kernel");
+  }
   const dim3 g1((unsigned)((a.intermediate_dim + MOE_ROWS - 1) / MOE_ROWS), (unsigned)a.active_count);
   const dim3 g2((unsigned)((a.hidden_dim + MOE_ROWS - 1) / MOE_ROWS), (unsigned)a.active_count);
   const int gpb = a.group_size >= 128 ? 1 : (int)(128 / a.group_size);

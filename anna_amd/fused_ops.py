@@ -578,6 +578,54 @@ def moe_router(router_logits, top_k, normalize_topk_prob=True):
     return w, sel, usage
 
 
+def moe_route_small(router_logits, top_k, normalize_topk_prob, slots):
+    """moe_router followed by the ordering half of moe_dispatch in one launch, for
+    tokens * top_k <= 1024 and num_experts <= 512.  Returns (weights fp32 [T,k], selected int64
+    [T,k], usage int32 [E], expert_offsets [E+1], sorted_token_idx [R], sorted_route_idx [R],
+    route_pos [R], items int32 [4 + 4E]) -- the same values moe_router + moe_dispatch give, plus
+    the grouped MLP's list of experts with routes (bank slot slots[e])."""
+    if router_logits.dim() != 2:
+        raise RuntimeError("router_logits must be [tokens, num_experts]")
+    t, e = router_logits.shape
+    if not (0 < top_k <= min(e, 64)) or e > 512 or not (0 < t * top_k <= 1024):
+        raise RuntimeError("moe_route_small: need 0 < tokens * top_k <= 1024, num_experts <= 512, top_k <= 64")
+    if slots.dtype != torch.int64 or slots.numel() != e:
+        raise RuntimeError("moe_route_small: slots must be int64 [num_experts]")
+    _check_same_device("moe_route_small", router_logits, slots)
+    logits = router_logits if router_logits.stride(1) == 1 else router_logits.contiguous()
+    dev, r = logits.device, t * top_k
+    w = torch.empty((t, top_k), dtype=torch.float32, device=dev)
+    sel = torch.empty((t, top_k), dtype=torch.int64, device=dev)
+    usage = torch.empty((e,), dtype=torch.int32, device=dev)
+    offsets = torch.empty((e + 1,), dtype=torch.int64, device=dev)
+    sti = torch.empty((r,), dtype=torch.int64, device=dev)
+    sri = torch.empty((r,), dtype=torch.int64, device=dev)
+    route_pos = torch.empty((r,), dtype=torch.int64, device=dev)
+    items = torch.empty((4 + 4 * e,), dtype=torch.int32, device=dev)
+    _lib.call("anna_mi_moe_route_small", logits.data_ptr(), _lib.dtype_code(logits.dtype), t, e, logits.stride(0),
+              int(top_k), int(bool(normalize_topk_prob)), w.data_ptr(), sel.data_ptr(), usage.data_ptr(),
+              offsets.data_ptr(), sti.data_ptr(), sri.data_ptr(), route_pos.data_ptr(), slots.contiguous().data_ptr(),
+              items.data_ptr(), _lib.stream_of(logits))
+    return w, sel, usage, offsets, sti, sri, route_pos, items
+
+
+def moe_gather(hidden_states, routing_weights, sorted_route_idx, top_k):
+    """The gathering half of moe_dispatch: (compact_hidden [R,H], compact_routing_weights [R,1])
+    for routes already ordered by moe_route_small."""
+    if hidden_states.dim() != 2 or routing_weights.dim() != 2:
+        raise RuntimeError("moe_gather: expected hidden [T,H] and routing_weights [T,k]")
+    _check_same_device("moe_gather", hidden_states, routing_weights, sorted_route_idx)
+    hs = hidden_states if hidden_states.stride(1) == 1 else hidden_states.contiguous()
+    rw = routing_weights.to(hs.dtype).contiguous()
+    r, h = sorted_route_idx.numel(), hs.shape[1]
+    compact = torch.empty((r, h), dtype=hs.dtype, device=hs.device)
+    cw = torch.empty((r, 1), dtype=hs.dtype, device=hs.device)
+    _lib.call("anna_mi_moe_gather", hs.data_ptr(), _lib.dtype_code(hs.dtype), h, hs.stride(0), rw.data_ptr(),
+              sorted_route_idx.contiguous().data_ptr(), r, int(top_k), compact.data_ptr(), cw.data_ptr(),
+              _lib.stream_of(hs))
+    return compact, cw
+
+
 def moe_dispatch(hidden_states, routing_weights, selected_experts, expert_usage, *, route_pos=None):
     """Returns (sorted_token_idx [R], expert_offsets [E+1], compact_hidden [R,H],
     compact_routing_weights [R,1]) with routes ordered by (expert, token, k)
@@ -636,7 +684,7 @@ def moe_combine(compact_outputs, route_pos, num_tokens, top_k, out=None):
 def moe_mlp_args(compact_hidden_states, compact_routing_weights, compact_outputs, expert_offsets, active_experts,
                  active_slots, gate_qweight, gate_qscale, gate_qzeros, up_qweight, up_qscale, up_qzeros,
                  down_qweight, down_qscale, down_qzeros, group_size, activation,
-                 max_routes_per_expert) -> _lib.MoeMlpArgs:
+                 max_routes_per_expert, items=None, items_prefilled=False) -> _lib.MoeMlpArgs:
     a = _lib.MoeMlpArgs()
     a.dtype = _lib.dtype_code(compact_hidden_states.dtype)
     a.scale_dtype = _lib.dtype_code(gate_qscale.dtype)
@@ -653,15 +701,20 @@ def moe_mlp_args(compact_hidden_states, compact_routing_weights, compact_outputs
     a.group_size = int(group_size)
     a.activation = activation.data_ptr()
     a.sweep_chunks = min(4, max(1, -(-int(max_routes_per_expert) // 16)))
+    a.items = None if items is None else items.data_ptr()
+    a.items_prefilled = int(bool(items_prefilled) and items is not None)
     return a
 
 
 def moe_grouped_int4_mlp_out(compact_hidden_states, compact_routing_weights, compact_outputs, expert_offsets,
                              active_experts, active_slots, gate_qweight, gate_qscale, gate_qzeros, up_qweight,
                              up_qscale, up_qzeros, down_qweight, down_qscale, down_qzeros, group_size,
-                             max_routes_per_expert, activation=None):
+                             max_routes_per_expert, activation=None, items=None, items_prefilled=False):
     """moe_grouped_int4_mlp_fused (sycl:4078-4324): writes the routes of the active experts
-    into compact_outputs and returns it."""
+    into compact_outputs and returns it.  items: optional int32 workspace [4 + 4 * active
+    experts]; with it the experts that have routes are listed on the device and the launches
+    walk only those (callers that pass every expert as active, without a host sync);
+    items_prefilled: items already holds that list (from moe_route_small)."""
     bank = (gate_qweight, gate_qscale, gate_qzeros, up_qweight, up_qscale, up_qzeros, down_qweight, down_qscale,
             down_qzeros)
     _check_same_device("moe_grouped_int4_mlp_fused", compact_hidden_states, compact_routing_weights, compact_outputs,
@@ -692,8 +745,12 @@ def moe_grouped_int4_mlp_out(compact_hidden_states, compact_routing_weights, com
     bank = tuple(t.contiguous() for t in bank)
     if activation is None:
         activation = torch.empty((x.shape[0], gate_qweight.shape[1]), dtype=torch.float32, device=x.device)
+    if items is not None and (items.dtype != torch.int32 or not items.is_contiguous()
+                              or items.numel() < 4 + 4 * active_experts.numel() or items.device != x.device):
+        raise RuntimeError("items must be a contiguous int32 tensor of >= 4 + 4 * active experts on the device")
     a = moe_mlp_args(x, cw, compact_outputs, expert_offsets.contiguous(), active_experts.contiguous(),
-                     active_slots.contiguous(), *bank, group_size, activation, max_routes_per_expert)
+                     active_slots.contiguous(), *bank, group_size, activation, max_routes_per_expert, items,
+                     items_prefilled)
     _lib.call("anna_mi_moe_grouped_int4_mlp", ctypes.byref(a), _lib.stream_of(x))
     return compact_outputs
 

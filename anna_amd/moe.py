@@ -83,16 +83,28 @@ class SparseMoeInt4:
     def forward(self, hidden_states: torch.Tensor, router_logits: torch.Tensor) -> torch.Tensor:
         """hidden_states [T, H], router_logits [T, E] -> routed expert output [T, H] (hidden dtype)."""
         t = hidden_states.shape[0]
-        w, sel, usage = fused_ops.moe_router(router_logits, self.top_k, self.norm_topk_prob)
-        route_pos = torch.empty((t * self.top_k,), dtype=torch.int64, device=hidden_states.device)
-        _, offsets, compact, cw = fused_ops.moe_dispatch(hidden_states, w.to(hidden_states.dtype), sel, usage,
-                                                          route_pos=route_pos)
+        # decode-sized batches: router + dispatch order + the MLP's list of experts with routes in
+        # one launch (its single workgroup ranks each route against the earlier ones, which pays
+        # only while the routes are few)
+        small = t * self.top_k <= 128 and self.num_experts <= 512 and self.top_k <= 64
+        if small:
+            w, sel, usage, offsets, _, sri, route_pos, items = fused_ops.moe_route_small(
+                router_logits, self.top_k, self.norm_topk_prob, self.active_slots)
+            compact, cw = fused_ops.moe_gather(hidden_states, w, sri, self.top_k)
+        else:
+            w, sel, usage = fused_ops.moe_router(router_logits, self.top_k, self.norm_topk_prob)
+            route_pos = torch.empty((t * self.top_k,), dtype=torch.int64, device=hidden_states.device)
+            _, offsets, compact, cw = fused_ops.moe_dispatch(hidden_states, w.to(hidden_states.dtype), sel, usage,
+                                                              route_pos=route_pos)
+            # every expert is passed as active; the device lists the ones with routes (items)
+            items = torch.empty((4 + 4 * self.num_experts,), dtype=torch.int32, device=hidden_states.device)
         compact_out = torch.empty_like(compact)
         # Routes per expert are only known on the device; the kernels sweep an expert's routes in
         # as many passes as it needs, so this hint (twice the mean load) only sizes the sweep.
         hint = min(t * self.top_k, 2 * -(-t * self.top_k // self.num_experts) + 8)
         fused_ops.moe_grouped_int4_mlp_out(compact, cw, compact_out, offsets, self.active_experts, self.active_slots,
-                                           *self.bank.tensors(), self.bank.group_size, max(1, hint))
+                                           *self.bank.tensors(), self.bank.group_size, max(1, hint), items=items,
+                                           items_prefilled=small)
         return fused_ops.moe_combine(compact_out, route_pos, t, self.top_k)
 
     __call__ = forward

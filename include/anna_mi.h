@@ -297,6 +297,26 @@ int anna_mi_moe_dispatch(const void* hidden, int dtype, int64_t tokens, int64_t 
                          int64_t* sorted_token_idx, int64_t* sorted_route_idx, int64_t* expert_offsets,
                          void* compact_hidden, void* compact_weights, int64_t* route_pos, void* stream);
 
+/* No single counterpart in the reference: moe_router_fused (sycl:3731-3865) followed by the
+ * ordering half of moe_dispatch_fused (sycl:3867-3965), for small batches (tokens * top_k <=
+ * 1024, num_experts <= 512), in one launch.  Outputs are those of anna_mi_moe_router
+ * (weights, selected, usage as int32) and of the dispatch's ordering (expert_offsets [E+1],
+ * sorted_token_idx, sorted_route_idx, route_pos [tokens*top_k]), identical to them, plus
+ * items (int32 [4 + 4 E], the list the grouped MLP walks: see anna_mi_moe_mlp_args.items) with
+ * bank slot slots[e] for expert e.  For callers such as an MoE block that run the whole chain. */
+int anna_mi_moe_route_small(const void* logits, int logits_dtype, int64_t tokens, int64_t num_experts,
+                            int64_t logits_row_stride, int64_t top_k, int normalize, float* weights,
+                            int64_t* selected, int32_t* usage, int64_t* expert_offsets, int64_t* sorted_token_idx,
+                            int64_t* sorted_route_idx, int64_t* route_pos, const int64_t* slots, int32_t* items,
+                            void* stream);
+
+/* The gathering half of moe_dispatch_fused (sycl:3867-3965): compact_hidden[p] =
+ * hidden[sorted_route_idx[p] / top_k], compact_weights[p] = routing_weights[sorted_route_idx[p]]
+ * (hidden dtype), after anna_mi_moe_route_small. */
+int anna_mi_moe_gather(const void* hidden, int dtype, int64_t hidden_dim, int64_t hidden_row_stride,
+                       const void* routing_weights, const int64_t* sorted_route_idx, int64_t routes, int64_t top_k,
+                       void* compact_hidden, void* compact_weights, void* stream);
+
 /* moe_scatter_fused (sycl:3967-4037; CPU path ops.py:3359-3376): out[t] = sum of the compact
  * rows p with sorted_token_idx[p] == t, accumulated in fp32 (workspace accum [tokens][hidden]
  * fp32) and cast to the hidden dtype. */
@@ -340,6 +360,12 @@ typedef struct {
   float* activation;              /* workspace fp32 [routes][intermediate] */
   int sweep_chunks;               /* 1..4: routes an expert takes per sweep over its weights, in
                                      chunks of 16; size it from the largest route count per expert */
+  int32_t* items;                 /* optional workspace int32 [4 + 4 * active_count]: when set, the
+                                     active experts that have routes are listed on the device
+                                     first and the MLP launches walk that list (no workgroups
+                                     for empty experts); NULL: one workgroup per expert and tile */
+  int items_prefilled;            /* 1: items already holds the list (anna_mi_moe_route_small wrote
+                                     it), so it is not rebuilt */
 } anna_mi_moe_mlp_args;
 
 int64_t anna_mi_sizeof_moe_mlp_args(void);

@@ -109,6 +109,56 @@ def test_grouped_int4_mlp_matches_oracle(gpu, hdt, sdt, group, tokens):
     assert bool((out.cpu()[inactive] == 7.0).all())
 
 
+@pytest.mark.parametrize("tokens,sdt,group", [(6, torch.bfloat16, 128), (40, torch.float32, 128), (9, torch.float32, 64)])
+def test_grouped_int4_mlp_item_list_matches_grid(gpu, tokens, sdt, group):
+    """The device-listed (persistent) form walks only experts with routes and gives the same
+    bits as the one-workgroup-per-expert grid; experts without routes stay untouched."""
+    print(f"[case] moe grouped MLP item list tokens={tokens} scales={sdt} group={group}", flush=True)
+    torch.manual_seed(3)
+    e, k, h, i = 24, 2, 512, 256
+    bank = make_bank(e, h, i, group, sdt, gpu, seed=5 + tokens)
+    hidden = torch.randn(tokens, h, device=gpu, dtype=torch.bfloat16)
+    w, sel, usage = fused_ops.moe_router(torch.randn(tokens, e, device=gpu), k, True)
+    sti, off, compact, cw = fused_ops.moe_dispatch(hidden, w.to(torch.bfloat16), sel, usage)
+    every = torch.arange(e, dtype=torch.int64, device=gpu)  # empty experts included, as SparseMoeInt4 passes them
+    out_grid = torch.full_like(compact, 7.0)
+    out_list = torch.full_like(compact, 7.0)
+    mx = int(usage.max())
+    fused_ops.moe_grouped_int4_mlp_out(compact, cw, out_grid, off, every, every, *bank.tensors(), group, mx)
+    items = torch.full((4 + 4 * e,), -1, dtype=torch.int32, device=gpu)
+    fused_ops.moe_grouped_int4_mlp_out(compact, cw, out_list, off, every, every, *bank.tensors(), group, mx, items=items)
+    assert torch.equal(out_grid, out_list)
+    assert int(items[0]) == int((usage > 0).sum())
+
+
+@pytest.mark.parametrize("tokens,experts,top_k,ldt", [(8, 128, 8, torch.float32), (11, 16, 4, torch.bfloat16),
+                                                      (128, 128, 8, torch.float32), (3, 300, 2, torch.float16)])
+def test_route_small_matches_router_and_dispatch(gpu, tokens, experts, top_k, ldt):
+    """The one-launch router + dispatch order gives exactly the separate ops' outputs, and its
+    item list names the experts with routes, in order, with their bank slot and route range."""
+    print(f"[case] moe route_small tokens={tokens} experts={experts} k={top_k} logits={ldt}", flush=True)
+    torch.manual_seed(tokens + experts)
+    logits = torch.randn(tokens, experts, device=gpu).to(ldt)
+    if tokens >= 8:
+        logits[1] = logits[0]  # identical rows: ties between tokens
+    hidden = torch.randn(tokens, 64, device=gpu, dtype=torch.bfloat16)
+    slots = torch.randperm(experts, device=gpu).to(torch.int64)
+    w, sel, usage = fused_ops.moe_router(logits, top_k, True)
+    route_pos = torch.empty((tokens * top_k,), dtype=torch.int64, device=gpu)
+    sti, off, compact, cw = fused_ops.moe_dispatch(hidden, w.to(torch.bfloat16), sel, usage, route_pos=route_pos)
+    w2, sel2, usage2, off2, sti2, sri2, rp2, items = fused_ops.moe_route_small(logits, top_k, True, slots)
+    assert torch.equal(w, w2) and torch.equal(sel, sel2) and torch.equal(usage, usage2)
+    assert torch.equal(off, off2) and torch.equal(sti, sti2) and torch.equal(route_pos, rp2)
+    compact2, cw2 = fused_ops.moe_gather(hidden, w2, sri2, top_k)
+    assert torch.equal(compact, compact2) and torch.equal(cw, cw2)
+    offc, uc, sl = off.cpu(), usage.cpu(), slots.cpu()
+    have = [e for e in range(experts) if int(uc[e]) > 0]
+    it = items.cpu()
+    assert int(it[0]) == len(have)
+    for j, e in enumerate(have):
+        assert [int(v) for v in it[4 + 4 * j: 7 + 4 * j]] == [int(sl[e]), int(offc[e]), int(offc[e + 1])]
+
+
 def test_scatter_and_combine(gpu):
     torch.manual_seed(4)
     t, h, e, k = 29, 384, 12, 3
