@@ -679,19 +679,16 @@ int launch_moe_mlp_nc(const anna_mi_moe_mlp_args& a, hipStream_t st, dim3 g1, di
   return ANNA_MI_OK;
 }
 
-// sweep_chunks selects the kernel: 1, 2 or 4 chunks of 16 routes per sweep (3 runs as 4)
+// One chunk of 16 routes per sweep, whatever sweep_chunks asks: experts with more routes take
+// more sweeps over their (then cache-resident) weights.  Measured at the BASELINE MoE shapes,
+// the 2- and 4-chunk forms (which keep more routes' x in flight per weight load) lose more to
+// their register count (one wave per SIMD) than they save: 316 -> 217 us at 512 tokens.
 template <int HDT, int SDT, int GPB>
 int launch_moe_mlp(const anna_mi_moe_mlp_args& a, hipStream_t st, dim3 g1, dim3 g2) {
   anna_mi_moe_mlp_args b = a;
-  if (a.sweep_chunks <= 1) {
-    b.sweep_chunks = 1;
-    return launch_moe_mlp_nc<HDT, SDT, GPB, 1>(b, st, g1, g2);
-  }
-  if (a.sweep_chunks == 2) return launch_moe_mlp_nc<HDT, SDT, GPB, 2>(b, st, g1, g2);
-  b.sweep_chunks = 4;
-  return launch_moe_mlp_nc<HDT, SDT, GPB, 4>(b, st, g1, g2);
-}
-}  // namespace
+  b.sweep_chunks = 1;
+  return launch_moe_mlp_nc<HDT, SDT, GPB, 1>(b, st, g1, g2);
+}}  // namespace
 }  // namespace anna
 
 using namespace anna;

@@ -358,8 +358,9 @@ typedef struct {
   const int8_t* down_qzeros;
   int64_t hidden_packed_cols, hidden_groups, intermediate_packed_cols, intermediate_groups, group_size;
   float* activation;              /* workspace fp32 [routes][intermediate] */
-  int sweep_chunks;               /* 1..4: routes an expert takes per sweep over its weights, in
-                                     chunks of 16; size it from the largest route count per expert */
+  int sweep_chunks;               /* 1..4: a hint, the routes an expert may take per sweep over its
+                                     weights in chunks of 16; this build always sweeps 16 routes at
+                                     a time (measured fastest at every BASELINE shape) */
   int32_t* items;                 /* optional workspace int32 [4 + 4 * active_count]: when set, the
                                      active experts that have routes are listed on the device
                                      first and the MLP launches walk that list (no workgroups
