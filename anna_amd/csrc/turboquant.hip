@@ -97,10 +97,12 @@ namespace {
 
 // ------------------------------------------------------------------ TQ-MSE quantize / dequant
 
-constexpr int TQ_VB = 16;  // vectors per workgroup
+// Vectors per workgroup (VB): each workgroup re-reads the D x D rotation from L2, so more vectors
+// per workgroup mean less of that traffic; 32 up to D = 512, 16 above so the x stage fits in LDS.
+constexpr int tq_vectors_per_wg(int64_t D) { return D <= 512 ? 32 : 16; }
 
 // grid: ceil(nvec / VB); block: D threads (D multiple of 64, <= 1024)
-template <int XDT>
+template <int XDT, int TQ_VB>
 __global__ __launch_bounds__(1024) void tq_mse_quantize_kernel(
     const typename Elem<XDT>::T* __restrict__ x, int64_t nvec, int64_t D, int64_t xs,
     const float* __restrict__ rot_t, const float* __restrict__ thr, int bits,
@@ -120,13 +122,22 @@ __global__ __launch_bounds__(1024) void tq_mse_quantize_kernel(
     nrm[i] = __builtin_sqrtf(ss);
     if (i < nv) norms[v0 + i] = f32_to_f16_bits(nrm[i]);
   }
+  // y_i = sum_k R[i][k] x_k as one fma per k in ascending k (the oracle's order), four k per
+  // LDS read of x (D is a multiple of 64)
   float acc[TQ_VB];
 #pragma unroll
   for (int v = 0; v < TQ_VB; ++v) acc[v] = 0.f;
-  for (int64_t k = 0; k < D; ++k) {
-    const float p = rot_t[k * D + i];
+  for (int64_t k = 0; k < D; k += 4) {
+    const float p0 = rot_t[k * D + i], p1 = rot_t[(k + 1) * D + i];
+    const float p2 = rot_t[(k + 2) * D + i], p3 = rot_t[(k + 3) * D + i];
 #pragma unroll
-    for (int v = 0; v < TQ_VB; ++v) acc[v] = __builtin_fmaf(p, xsm[v * D + k], acc[v]);
+    for (int v = 0; v < TQ_VB; ++v) {
+      const float4 xv = *(const float4*)(xsm + v * D + k);
+      acc[v] = __builtin_fmaf(p0, xv.x, acc[v]);
+      acc[v] = __builtin_fmaf(p1, xv.y, acc[v]);
+      acc[v] = __builtin_fmaf(p2, xv.z, acc[v]);
+      acc[v] = __builtin_fmaf(p3, xv.w, acc[v]);
+    }
   }
   __syncthreads();
   const int nthr = (1 << bits) - 1;
@@ -148,7 +159,7 @@ __global__ __launch_bounds__(1024) void tq_mse_quantize_kernel(
 }
 
 // out[v][k] = norm_v * sum_i R[i][k] c[code_i]  (fp32 accumulation)
-template <int ODT>
+template <int ODT, int TQ_VB>
 __global__ __launch_bounds__(1024) void tq_mse_dequant_kernel(
     const uint8_t* __restrict__ codes, const uint16_t* __restrict__ norms, int64_t nvec, int64_t D,
     const float* __restrict__ rot, const float* __restrict__ cent, int bits,
@@ -169,10 +180,16 @@ __global__ __launch_bounds__(1024) void tq_mse_dequant_kernel(
   float acc[TQ_VB];
 #pragma unroll
   for (int v = 0; v < TQ_VB; ++v) acc[v] = 0.f;
-  for (int64_t i = 0; i < D; ++i) {
-    const float p = rot[i * D + k];
+  for (int64_t i = 0; i < D; i += 4) {
+    const float p0 = rot[i * D + k], p1 = rot[(i + 1) * D + k], p2 = rot[(i + 2) * D + k], p3 = rot[(i + 3) * D + k];
 #pragma unroll
-    for (int v = 0; v < TQ_VB; ++v) acc[v] = fmaf(p, yv[v * D + i], acc[v]);
+    for (int v = 0; v < TQ_VB; ++v) {
+      const float4 y4 = *(const float4*)(yv + v * D + i);
+      acc[v] = fmaf(p0, y4.x, acc[v]);
+      acc[v] = fmaf(p1, y4.y, acc[v]);
+      acc[v] = fmaf(p2, y4.z, acc[v]);
+      acc[v] = fmaf(p3, y4.w, acc[v]);
+    }
   }
   for (int v = 0; v < nv; ++v) out[(v0 + v) * os + k] = Elem<ODT>::cvt(f16_bits_to_f32(norms[v0 + v]) * acc[v]);
 }
@@ -264,11 +281,16 @@ extern "C" int anna_mi_tq_mse_quantize(const void* x, int x_dtype, int64_t nvec,
   ANNA_CHECK(D >= 64 && D <= 1024 && D % 64 == 0, "anna_mi_tq_mse_quantize: head_dim must be a multiple of 64 in [64, 1024]");
   ANNA_CHECK(x_row_stride >= D, "anna_mi_tq_mse_quantize: row stride smaller than head_dim");
   if (nvec <= 0) return ANNA_MI_OK;
-  const size_t lds = (size_t)TQ_VB * D * 4 + (size_t)TQ_VB * D;
+  const int vb = tq_vectors_per_wg(D);
+  const size_t lds = (size_t)vb * D * 4 + (size_t)vb * D;
+  const dim3 grid((unsigned)((nvec + vb - 1) / vb));
   ANNA_DISPATCH_DTYPE(x_dtype, XDT, {
-    hipLaunchKernelGGL((tq_mse_quantize_kernel<XDT>), dim3((unsigned)((nvec + TQ_VB - 1) / TQ_VB)), dim3((unsigned)D),
-                       lds, as_stream(stream), (const typename Elem<XDT>::T*)x, nvec, D, x_row_stride, rot_t,
-                       thresholds, bits, codes, norms);
+    if (vb == 32)
+      hipLaunchKernelGGL((tq_mse_quantize_kernel<XDT, 32>), grid, dim3((unsigned)D), lds, as_stream(stream),
+                         (const typename Elem<XDT>::T*)x, nvec, D, x_row_stride, rot_t, thresholds, bits, codes, norms);
+    else
+      hipLaunchKernelGGL((tq_mse_quantize_kernel<XDT, 16>), grid, dim3((unsigned)D), lds, as_stream(stream),
+                         (const typename Elem<XDT>::T*)x, nvec, D, x_row_stride, rot_t, thresholds, bits, codes, norms);
   });
   ANNA_LAUNCH_CHECK("tq_mse_quantize_kernel");
   return ANNA_MI_OK;
@@ -282,10 +304,17 @@ extern "C" int anna_mi_tq_mse_dequant(const uint8_t* codes, const uint16_t* norm
   ANNA_CHECK(bits >= 1 && bits <= 4, "anna_mi_tq_mse_dequant: bits must be 1..4");
   ANNA_CHECK(D >= 64 && D <= 1024 && D % 64 == 0, "anna_mi_tq_mse_dequant: head_dim must be a multiple of 64 in [64, 1024]");
   if (nvec <= 0) return ANNA_MI_OK;
+  const int vb = tq_vectors_per_wg(D);
+  const dim3 grid((unsigned)((nvec + vb - 1) / vb));
   ANNA_DISPATCH_DTYPE(out_dtype, ODT, {
-    hipLaunchKernelGGL((tq_mse_dequant_kernel<ODT>), dim3((unsigned)((nvec + TQ_VB - 1) / TQ_VB)), dim3((unsigned)D),
-                       (size_t)TQ_VB * D * 4, as_stream(stream), codes, norms, nvec, D, rot, centroids, bits,
-                       (typename Elem<ODT>::T*)out, out_row_stride);
+    if (vb == 32)
+      hipLaunchKernelGGL((tq_mse_dequant_kernel<ODT, 32>), grid, dim3((unsigned)D), (size_t)vb * D * 4,
+                         as_stream(stream), codes, norms, nvec, D, rot, centroids, bits,
+                         (typename Elem<ODT>::T*)out, out_row_stride);
+    else
+      hipLaunchKernelGGL((tq_mse_dequant_kernel<ODT, 16>), grid, dim3((unsigned)D), (size_t)vb * D * 4,
+                         as_stream(stream), codes, norms, nvec, D, rot, centroids, bits,
+                         (typename Elem<ODT>::T*)out, out_row_stride);
   });
   ANNA_LAUNCH_CHECK("tq_mse_dequant_kernel");
   return ANNA_MI_OK;
