@@ -614,7 +614,10 @@ void launch_gemv(const void* x, int64_t M, int64_t K, int64_t xs, const int32_t*
 }
 
 // Tuning knobs (read once): ANNA_MI_INT4_GEMV_WAVES in {4, 8} splits K across that many
-// waves per workgroup; ANNA_MI_INT4_GEMV_TILES in {1, 2} sets 16-row tiles per wave (default 2).
+// waves per workgroup; ANNA_MI_INT4_GEMV_TILES in {1, 2, 3, 4} sets 16-row tiles per wave.
+// Default tiles: the fewest that put the whole N in one workgroup per compute unit (every
+// wave's loads then go out in a single round), e.g. 3 at N = 12288 (256 workgroups; 12.8 us at
+// M = 8 against 14.5 us for 384 two-tile workgroups) and 2 at N = 6144; 2 past 256 x 48 rows.
 
 template <int XDT, int SDT>
 void dispatch_gemv(const void* x, int64_t M, int64_t K, int64_t xs, const int32_t* qw, int64_t N, int64_t pc,
@@ -623,13 +626,22 @@ void dispatch_gemv(const void* x, int64_t M, int64_t K, int64_t xs, const int32_
   static const int env_tiles = env_int("ANNA_MI_INT4_GEMV_TILES", 0);
   const int64_t nblk = (K + 127) / 128;
   const int waves = env_waves ? env_waves : (nblk >= 32 ? 8 : 4);
-  const int tiles = env_tiles ? env_tiles : 2;
+  int tiles = 2;
+  for (int t = 1; t <= 3; ++t)
+    if ((N + 16 * t - 1) / (16 * t) <= 256) {
+      tiles = t;
+      break;
+    }
+  if (env_tiles) tiles = env_tiles;
   const bool b4 = nblk <= 4 * waves;  // one pass of 4 blocks per wave covers K
 #define ANNA_GEMV_GO(T, W)                                                                   \
   (b4 ? launch_gemv<XDT, SDT, T, W, 4>(x, M, K, xs, qw, N, pc, qs, qz, gsz, y, st)           \
       : launch_gemv<XDT, SDT, T, W, 8>(x, M, K, xs, qw, N, pc, qs, qz, gsz, y, st))
-  if (waves == 8 && tiles == 2) ANNA_GEMV_GO(2, 8);
+  if (waves == 8 && tiles == 3) ANNA_GEMV_GO(3, 8);
+  else if (waves == 8 && tiles == 4) ANNA_GEMV_GO(4, 8);
+  else if (waves == 8 && tiles == 2) ANNA_GEMV_GO(2, 8);
   else if (waves == 8) ANNA_GEMV_GO(1, 8);
+  else if (tiles >= 3) ANNA_GEMV_GO(3, 4);
   else if (tiles == 2) ANNA_GEMV_GO(2, 4);
   else ANNA_GEMV_GO(1, 4);
 #undef ANNA_GEMV_GO

@@ -44,6 +44,9 @@ LINEAR_CASES = [
     (300, 512, 400, 64, "bf16"),    # tiled GEMM: group 64, M and N tails
     (2048, 4096, 192, 128, "bf16"), # tiled GEMM at the config-2 M and K
     (64, 4096, 6144, 128, "fp32"),  # tiled GEMM, config-2 N = 6144 at M = 64
+    (8, 512, 12200, 128, "bf16"),   # MFMA GEMV, three 16-row tiles per wave, N tail
+    (4, 1024, 8000, 128, "fp32"),   # MFMA GEMV, two tiles
+    (8, 512, 2000, 128, "bf16"),    # MFMA GEMV, one tile
 ]
 
 
