@@ -57,6 +57,7 @@ __global__ __launch_bounds__(64 * KW) void int4_gemv_mfma(
   const int64_t nblk = (K + 127) >> 7;
   const u32x4 ones = {ONES, ONES, ONES, ONES};
   const u32x4 zero4 = {0u, 0u, 0u, 0u};
+  const bool bpg1 = blocks_per_group == 1;
 
   const uint32_t* wrow[NT];
   bool n_ok[NT];
@@ -76,7 +77,26 @@ __global__ __launch_bounds__(64 * KW) void int4_gemv_mfma(
   const int64_t bw0 = contiguous ? (int64_t)wave * GEMV_BPW : wave;
   const int64_t bstep = contiguous ? 1 : KW;
   // One pass = GEMV_BPW blocks per wave (one pass covers K = 4096 at 8 waves).
+  auto load_x = [&](int64_t b, int s) -> u32x4 {
+    const int64_t k = b * 128 + kq * 32 + s * 8;
+    const bool ok = b < nblk && m_ok && k < K;
+    const int64_t kc = ok ? k : 0;
+    const int64_t rc = m_ok ? r : 0;
+    const u32x4 v = *(const u32x4*)(x + rc * xs + kc);
+    return ok ? v : zero4;
+  };
+  // With 4 blocks per wave and pass, the x fragments of all of them are loaded first (64
+  // VGPRs): a fragment fetched one block ahead was sunk by the compiler next to its use, and
+  // each block then waited a full round trip for x.
+  constexpr bool XALL = GEMV_BPW <= 4;
   auto pass = [&](int64_t p0) {
+    u32x4 xall[XALL ? GEMV_BPW : 1][4];
+    if constexpr (XALL) {
+#pragma unroll
+      for (int j = 0; j < GEMV_BPW; ++j)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) xall[j][s] = load_x(p0 + bw0 + bstep * j, s);
+    }
     // Issue every global load of the pass up front: weights, scales, zero points.
     u32x4 wv[GEMV_BPW][NT];
     float scv[GEMV_BPW][NT];
@@ -87,7 +107,9 @@ __global__ __launch_bounds__(64 * KW) void int4_gemv_mfma(
     for (int j = 0; j < GEMV_BPW; ++j) {
       const int64_t b = p0 + bw0 + bstep * j;
       const int64_t bc = b < nblk ? b : nblk - 1;
-      const int64_t g = bc / blocks_per_group;
+      // 32-bit (K / 128 < 2^31 here), and none at all for 128-wide groups: a 64-bit division
+      // is ~100 instructions in front of each block's loads
+      const int64_t g = bpg1 ? bc : (int64_t)((uint32_t)bc / (uint32_t)blocks_per_group);
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const int64_t gi = g * N + (n_ok[t] ? n_base + t * 16 + r : 0);
@@ -102,25 +124,18 @@ __global__ __launch_bounds__(64 * KW) void int4_gemv_mfma(
 #pragma unroll
       for (int t = 0; t < NT; ++t)
         if (!n_ok[t]) wv[j][t] = zero4;
-    // x fragments of the next block are fetched while the current block computes.
-    auto load_x = [&](int64_t b, int s) -> u32x4 {
-      const int64_t k = b * 128 + kq * 32 + s * 8;
-      const bool ok = b < nblk && m_ok && k < K;
-      const int64_t kc = ok ? k : 0;
-      const int64_t rc = m_ok ? r : 0;
-      const u32x4 v = *(const u32x4*)(x + rc * xs + kc);
-      return ok ? v : zero4;
-    };
+    // otherwise the x fragments of the next block are fetched while the current block computes
     u32x4 xa[4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) xa[s] = load_x(p0 + bw0, s);
+    for (int s = 0; s < 4; ++s) xa[s] = XALL ? xall[0][s] : load_x(p0 + bw0, s);
 #pragma unroll
     for (int j = 0; j < GEMV_BPW; ++j) {
       const int64_t b = p0 + bw0 + bstep * j;
       if (b >= nblk) break;
       u32x4 xn[4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) xn[s] = j + 1 < GEMV_BPW ? load_x(b + bstep, s) : zero4;
+      for (int s = 0; s < 4; ++s)
+        xn[s] = j + 1 < GEMV_BPW ? (XALL ? xall[j + 1 < GEMV_BPW ? j + 1 : 0][s] : load_x(b + bstep, s)) : zero4;
       f32x4 acc[NT];
       f32x4 sx = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
