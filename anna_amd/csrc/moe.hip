@@ -323,31 +323,14 @@ typedef __attribute__((address_space(3))) void* moe_lds_ptr;
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
-// Convert 8 consecutive activations to the 16-bit MFMA type MDT.
-template <int SRC, int MDT>
-__device__ __forceinline__ u32x4 load8_as16(const void* base, int64_t idx) {
-  if constexpr (SRC == MDT) {
-    return *(const u32x4*)((const uint16_t*)base + idx);
-  } else {
-    // f32 sources (fp32 hidden states, the fp32 activation) -> bf16
-    const float* src = (const float*)base + idx;
-    const float4 lo = *(const float4*)src, hi = *(const float4*)(src + 4);
-    u32x4 v;
-    v.x = (uint32_t)f32_to_bf16_bits(lo.x) | ((uint32_t)f32_to_bf16_bits(lo.y) << 16);
-    v.y = (uint32_t)f32_to_bf16_bits(lo.z) | ((uint32_t)f32_to_bf16_bits(lo.w) << 16);
-    v.z = (uint32_t)f32_to_bf16_bits(hi.x) | ((uint32_t)f32_to_bf16_bits(hi.y) << 16);
-    v.w = (uint32_t)f32_to_bf16_bits(hi.z) | ((uint32_t)f32_to_bf16_bits(hi.w) << 16);
-    return v;
-  }
-}
-
-// One pass's worth of one wave's weights: PB blocks x NM matrices, with the scale and the
-// "off + zero" constant of each group.
-template <int NM, int GPB>
+// One pass's worth of one wave's weights: PB blocks x NM matrices, with the scale and the zero
+// point of each group kept raw (as loaded) until the pass that uses them: a conversion next to
+// the load would make the prefetch wait for its data.
+template <int SDT, int NM, int GPB>
 struct MoePass {
   u32x4 w[MOE_PB][NM];
-  float s[MOE_PB][GPB][NM];
-  float c[MOE_PB][GPB][NM];
+  typename Elem<SDT>::T s[MOE_PB][GPB][NM];
+  int8_t z[MOE_PB][GPB][NM];
 };
 
 // One sweep of a workgroup over its 64 output rows x all K for NC chunks of 16 routes.
@@ -372,7 +355,7 @@ __device__ __forceinline__ void moe_sweep(const anna_mi_moe_mlp_args& a, uint16_
   const void* xsrc = GU ? a.compact_hidden : (const void*)a.activation;
   const u32x4 ones = {ONES, ONES, ONES, ONES};
 
-  auto load_pass = [&](int64_t p, MoePass<NM, GPB>& P) {
+  auto load_pass = [&](int64_t p, MoePass<SDT, NM, GPB>& P) {
 #pragma unroll
     for (int j = 0; j < MOE_PB; ++j) {
       int64_t b = p * MOE_PB + j;
@@ -383,8 +366,8 @@ __device__ __forceinline__ void moe_sweep(const anna_mi_moe_mlp_args& a, uint16_
 #pragma unroll
         for (int q = 0; q < GPB; ++q) {
           const int64_t gi = (b * GPB + q) * N;
-          P.s[j][q][m] = Elem<SDT>::to_f32(((const ST*)sc[m])[gi]);
-          P.c[j][q][m] = OFF + (float)zp[m][gi];
+          P.s[j][q][m] = ((const ST*)sc[m])[gi];
+          P.z[j][q][m] = zp[m][gi];
         }
       }
     }
@@ -396,8 +379,21 @@ __device__ __forceinline__ void moe_sweep(const anna_mi_moe_mlp_args& a, uint16_
 #pragma unroll
     for (int m = 0; m < NM; ++m) out[c][m] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  MoePass<NM, GPB> cur, nxt;
+  MoePass<SDT, NM, GPB> cur, nxt;
   load_pass(0, cur);
+  // down: the routing weights of the lane's output routes, loaded now and kept raw (loaded
+  // at the stores, each would be a round trip of its own behind the previous store)
+  using HT = typename Elem<HDT>::T;
+  HT wraw[GU ? 1 : NC][4];
+  if constexpr (!GU) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t m = c * 16 + 4 * kq + i;
+        wraw[c][i] = ((const HT*)a.compact_weights)[c0 + (m < nrows ? m : 0)];
+      }
+  }
   // x row pitch in LDS (16-bit elements): a 512-k slice per pass, or all of K (XF)
   const int64_t xp = XF ? K + 8 : MOE_XP;
   if constexpr (XF) {
@@ -421,15 +417,38 @@ __device__ __forceinline__ void moe_sweep(const anna_mi_moe_mlp_args& a, uint16_
   for (int64_t p = 0; p < npass; ++p) {
     // x slice [NC*16 rows][512 k] of this pass (rows past the expert's routes read as zero)
     if constexpr (!XF) {
-    u32x4 xv[XPT];
+    // every load of the slice first, then the conversions (converting each chunk as it
+    // arrives would wait for it before the next chunk's load is issued)
+    typedef u32x4 Raw[SRC == ANNA_MI_F32 ? 2 : 1];
+    Raw raw[XPT];
+    bool okv[XPT];
 #pragma unroll
     for (int i = 0; i < XPT; ++i) {
       const int e = threadIdx.x + 256 * i;  // chunk index: row e / 64, 8-k column e % 64
       const int row = e >> 6, col = (e & 63) * 8;
       const int64_t k = p * MOE_PB * 128 + col;
-      const bool ok = row < nrows && k < K;
-      xv[i] = load8_as16<SRC, MDT>(xsrc, (c0 + (ok ? row : 0)) * K + (ok ? k : 0));
-      if (!ok) xv[i] = u32x4{0u, 0u, 0u, 0u};
+      okv[i] = row < nrows && k < K;
+      const int64_t idx = (c0 + (okv[i] ? row : 0)) * K + (okv[i] ? k : 0);
+      if constexpr (SRC == ANNA_MI_F32) {
+        raw[i][0] = *(const u32x4*)((const float*)xsrc + idx);
+        raw[i][1] = *(const u32x4*)((const float*)xsrc + idx + 4);
+      } else {
+        raw[i][0] = *(const u32x4*)((const uint16_t*)xsrc + idx);
+      }
+    }
+    u32x4 xv[XPT];
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+      if constexpr (SRC == ANNA_MI_F32) {
+        const float4 lo = __builtin_bit_cast(float4, raw[i][0]), hi = __builtin_bit_cast(float4, raw[i][1]);
+        xv[i].x = (uint32_t)f32_to_bf16_bits(lo.x) | ((uint32_t)f32_to_bf16_bits(lo.y) << 16);
+        xv[i].y = (uint32_t)f32_to_bf16_bits(lo.z) | ((uint32_t)f32_to_bf16_bits(lo.w) << 16);
+        xv[i].z = (uint32_t)f32_to_bf16_bits(hi.x) | ((uint32_t)f32_to_bf16_bits(hi.y) << 16);
+        xv[i].w = (uint32_t)f32_to_bf16_bits(hi.z) | ((uint32_t)f32_to_bf16_bits(hi.w) << 16);
+      } else {
+        xv[i] = raw[i][0];
+      }
+      if (!okv[i]) xv[i] = u32x4{0u, 0u, 0u, 0u};
     }
     __syncthreads();  // every wave is done with the previous slice
 #pragma unroll
@@ -473,7 +492,8 @@ __device__ __forceinline__ void moe_sweep(const anna_mi_moe_mlp_args& a, uint16_
           for (int m = 0; m < NM; ++m)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-              out[c][m][i] = fmaf(cur.s[j][0][m], acc[c][m][i] - cur.c[j][0][m] * sx[c][i], out[c][m][i]);
+              out[c][m][i] = fmaf(Elem<SDT>::to_f32(cur.s[j][0][m]), acc[c][m][i] - (OFF + (float)cur.z[j][0][m]) * sx[c][i],
+                                  out[c][m][i]);
       } else {
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
@@ -494,7 +514,8 @@ __device__ __forceinline__ void moe_sweep(const anna_mi_moe_mlp_args& a, uint16_
                 const f32x4 accq = mfma16<MDT>(xm, wf[m], f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                  out[c][m][i] = fmaf(cur.s[j][q][m], accq[i] - cur.c[j][q][m] * sxq[i], out[c][m][i]);
+                  out[c][m][i] = fmaf(Elem<SDT>::to_f32(cur.s[j][q][m]), accq[i] - (OFF + (float)cur.z[j][q][m]) * sxq[i],
+                                      out[c][m][i]);
               }
             }
           }
@@ -515,8 +536,7 @@ __device__ __forceinline__ void moe_sweep(const anna_mi_moe_mlp_args& a, uint16_
         if constexpr (GU) {
           a.activation[route * N + n] = silu(out[c][0][i]) * out[c][1][i];
         } else {
-          const float w = Elem<HDT>::load((const typename Elem<HDT>::T*)a.compact_weights, route);
-          ((typename Elem<HDT>::T*)a.compact_outputs)[route * N + n] = Elem<HDT>::cvt(out[c][0][i] * w);
+          ((HT*)a.compact_outputs)[route * N + n] = Elem<HDT>::cvt(out[c][0][i] * Elem<HDT>::to_f32(wraw[c][i]));
         }
       }
   }
@@ -577,7 +597,7 @@ __device__ __forceinline__ void moe_mlp_item(const anna_mi_moe_mlp_args& a, uint
 // compacted list, so no workgroup is dispatched for an empty expert (dispatching thousands of
 // workgroups that exit at once costs tens of microseconds here).
 template <int HDT, int SDT, bool GU, int GPB, int NCMAX, bool XF = false>
-__global__ __launch_bounds__(256) void moe_int4_mlp_kernel(const anna_mi_moe_mlp_args a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GU ? 1 : 3))) void moe_int4_mlp_kernel(const anna_mi_moe_mlp_args a) {
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];  // [sweep_chunks * 16][MOE_XP]
   if (a.items == nullptr) {
     const int64_t ai = blockIdx.y;
