@@ -128,6 +128,9 @@ __device__ __forceinline__ void tq_rotate_fragment(const anna_mi_tq_decode_args&
     qv[st] = *(const u32x4*)(qrow + st * 32);
     rv[st] = *(const u32x4*)(a.rotation_f16 + (int64_t)(tile * 16 + r) * TD + st * 32 + kq * 8);
   }
+  // no instruction moves above this point: every load is issued before the first conversion
+  // waits for its data (the scheduler otherwise interleaves them, one round trip after another)
+  __builtin_amdgcn_sched_barrier(0);
   f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int st = 0; st < 8; ++st) {
@@ -451,6 +454,9 @@ __global__ __launch_bounds__(CMB_THREADS) void tq_decode_combine_kernel(const an
         v1[k] = src[idx * IS + CMB_THREADS];
         ml[k] = *(const float2*)(stn + idx * 32);
       }
+      // all 48 loads of the batch go out before the first wait (left alone, the scheduler
+      // issues the value loads only after the statistics have arrived)
+      __builtin_amdgcn_sched_barrier(0);
       float mb = M;
 #pragma unroll
       for (int k = 0; k < 16; ++k)
