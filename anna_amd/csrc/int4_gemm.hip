@@ -260,15 +260,19 @@ __global__ __launch_bounds__(T::THREADS) void int4_gemm_tiled_kernel(
 #pragma unroll
     for (int s = 0; s < GM_BK / 32; ++s) {
       const int slot = s ? slot1 : slot0;
-      u32x4 b[FN];
+      // every fragment of the sub-step is read before the first MFMA (left alone, the
+      // scheduler reads one A fragment, waits for it and runs its MFMAs, one LDS round trip
+      // per fragment with the matrix core idle)
+      u32x4 b[FN], av[FM];
 #pragma unroll
       for (int j = 0; j < FN; ++j) b[j] = *(const u32x4*)(sB + j * 16 * GM_BK + slot);
 #pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        const u32x4 a = *(const u32x4*)(sA + i * 16 * GM_BK + slot);
+      for (int i = 0; i < FM; ++i) av[i] = *(const u32x4*)(sA + i * 16 * GM_BK + slot);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = mfma16<XDT>(a, b[j], acc[i][j]);
-      }
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = mfma16<XDT>(av[i], b[j], acc[i][j]);
     }
   };
   __syncthreads();  // step 0 is in LDS
