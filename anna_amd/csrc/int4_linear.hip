@@ -5,8 +5,8 @@
 // of word k/8 at bits 4*(k%8), qscale [G, N], qzeros int8 [G, N], w = (q - z) * s.
 //
 // Kernels
-//   int4_gemv_mfma   M <= 16.  HBM-bound.  Each wave owns NT 16-row tiles of W and a
-//                    strided share of the K blocks (KW waves split K, reduced through
+//   int4_gemv_mfma   M < 64 (16-bit x, K <= 4096 for M > 16).  HBM-bound.  Each wave owns NT
+//                    16-row tiles of W and a strided share of the K blocks (KW waves split K, reduced through
 //                    LDS at the end).  One 128-bit load per lane brings 32 nibbles of
 //                    one row; nibbles are turned into bf16/f16 "128+q" / "1024+q"
 //                    patterns with one AND-OR per pair (exact small integers), fed to
@@ -14,6 +14,8 @@
 //                    128-k block with a row sum of x that a second MFMA against an
 //                    all-ones operand produces in the same C layout:
 //                       sum_k x (q - z) s = s * (sum_k x (off + q) - (off + z) sum_k x).
+//                    For M > 16 the 16-row groups of x take turns against the weights,
+//                    which stay in registers (W is read once for all of M).
 //   (M >= 64 with 16-bit activations, K % 64 == 0: int4_gemm_tiled_kernel, int4_gemm.hip)
 //   int4_gemm_mfma   other M > 16.  LDS-tiled: a 128x128 tile of W is dequantized once per
 //                    workgroup to bf16 ((q - z) * s rounded to bf16, the reference's
@@ -40,7 +42,9 @@ namespace {
 // two 8-wave workgroups share a CU.
 
 // x is read through L1/L2 (staging it in LDS first was measured slower at every M).
-template <int XDT, int SDT, int NT, int KW, int GEMV_BPW>
+// MG > 1 (M up to 16 MG, one pass per wave only): the wave's weights stay in registers and the
+// 16-row groups of x take turns against them, so W is read from memory once for all of M.
+template <int XDT, int SDT, int NT, int KW, int GEMV_BPW, int MG = 1>
 __global__ __launch_bounds__(64 * KW) void int4_gemv_mfma(
     const uint16_t* __restrict__ x, int64_t M, int64_t K, int64_t xs,
     const uint32_t* __restrict__ qw, int64_t N, int64_t pc,
@@ -53,7 +57,6 @@ __global__ __launch_bounds__(64 * KW) void int4_gemv_mfma(
   const int r = lane & 15;
   const int kq = lane >> 4;
   const int64_t n_base = xcd_tile(blockIdx.x, gridDim.x) * (16 * NT);
-  const bool m_ok = r < M;
   const int64_t nblk = (K + 127) >> 7;
   const u32x4 ones = {ONES, ONES, ONES, ONES};
   const u32x4 zero4 = {0u, 0u, 0u, 0u};
@@ -68,20 +71,23 @@ __global__ __launch_bounds__(64 * KW) void int4_gemv_mfma(
     wrow[t] = qw + (n_ok[t] ? n : 0) * pc + kq * 4;
   }
 
-  f32x4 out[NT];
+  f32x4 out[MG][NT];
 #pragma unroll
-  for (int t = 0; t < NT; ++t) out[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int g = 0; g < MG; ++g)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) out[g][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Block j of a pass: interleaved (b = p0 + wave + KW*j) or contiguous per wave
   // (b = p0 + wave*BPW + j, so one wave reads whole 128 B lines back to back).
   const int64_t bw0 = contiguous ? (int64_t)wave * GEMV_BPW : wave;
   const int64_t bstep = contiguous ? 1 : KW;
   // One pass = GEMV_BPW blocks per wave (one pass covers K = 4096 at 8 waves).
-  auto load_x = [&](int64_t b, int s) -> u32x4 {
+  auto load_x = [&](int64_t b, int s, int g) -> u32x4 {
     const int64_t k = b * 128 + kq * 32 + s * 8;
-    const bool ok = b < nblk && m_ok && k < K;
+    const int64_t row = 16 * g + r;
+    const bool ok = b < nblk && row < M && k < K;
     const int64_t kc = ok ? k : 0;
-    const int64_t rc = m_ok ? r : 0;
+    const int64_t rc = row < M ? row : 0;
     const u32x4 v = *(const u32x4*)(x + rc * xs + kc);
     return ok ? v : zero4;
   };
@@ -89,13 +95,14 @@ __global__ __launch_bounds__(64 * KW) void int4_gemv_mfma(
   // VGPRs): a fragment fetched one block ahead was sunk by the compiler next to its use, and
   // each block then waited a full round trip for x.
   constexpr bool XALL = GEMV_BPW <= 4;
+  static_assert(MG == 1 || XALL, "several row groups need the 4-block pass");
   auto pass = [&](int64_t p0) {
     u32x4 xall[XALL ? GEMV_BPW : 1][4];
     if constexpr (XALL) {
 #pragma unroll
       for (int j = 0; j < GEMV_BPW; ++j)
 #pragma unroll
-        for (int s = 0; s < 4; ++s) xall[j][s] = load_x(p0 + bw0 + bstep * j, s);
+        for (int s = 0; s < 4; ++s) xall[j][s] = load_x(p0 + bw0 + bstep * j, s, 0);
     }
     // Issue every global load of the pass up front: weights, scales, zero points.
     u32x4 wv[GEMV_BPW][NT];
@@ -124,67 +131,87 @@ __global__ __launch_bounds__(64 * KW) void int4_gemv_mfma(
 #pragma unroll
       for (int t = 0; t < NT; ++t)
         if (!n_ok[t]) wv[j][t] = zero4;
-    // otherwise the x fragments of the next block are fetched while the current block computes
-    u32x4 xa[4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) xa[s] = XALL ? xall[0][s] : load_x(p0 + bw0, s);
+    for (int mg = 0; mg < MG; ++mg) {
+      if (mg > 0) {
+        // the next row group's x (the weights stay in registers)
+        __builtin_amdgcn_sched_barrier(0);
+        if (16 * mg >= M) break;
 #pragma unroll
-    for (int j = 0; j < GEMV_BPW; ++j) {
-      const int64_t b = p0 + bw0 + bstep * j;
-      if (b >= nblk) break;
-      u32x4 xn[4];
+        for (int j = 0; j < GEMV_BPW; ++j)
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        xn[s] = j + 1 < GEMV_BPW ? (XALL ? xall[j + 1 < GEMV_BPW ? j + 1 : 0][s] : load_x(b + bstep, s)) : zero4;
-      f32x4 acc[NT];
-      f32x4 sx = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const u32x4 a = interleave_x(xa[s]);
-        sx = mfma16<XDT>(a, ones, sx);
-#pragma unroll
-        for (int t = 0; t < NT; ++t) acc[t] = mfma16<XDT>(a, nibbles_to_frag<XDT>(wv[j][t][s]), acc[t]);
+          for (int s = 0; s < 4; ++s) xall[j][s] = load_x(p0 + bw0 + bstep * j, s, mg);
       }
-      // C layout: lane holds rows m = 4*kq + i of column n = n_base + 16t + r.
+      // otherwise the x fragments of the next block are fetched while the current block computes
+      u32x4 xa[4];
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const float c = OFF + cv[j][t];
+      for (int s = 0; s < 4; ++s) xa[s] = XALL ? xall[0][s] : load_x(p0 + bw0, s, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) out[t][i] = fmaf(scv[j][t], acc[t][i] - c * sx[i], out[t][i]);
+      for (int j = 0; j < GEMV_BPW; ++j) {
+        const int64_t b = p0 + bw0 + bstep * j;
+        if (b >= nblk) break;
+        u32x4 xn[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          xn[s] = j + 1 < GEMV_BPW ? (XALL ? xall[j + 1 < GEMV_BPW ? j + 1 : 0][s] : load_x(b + bstep, s, 0)) : zero4;
+        f32x4 acc[NT];
+        f32x4 sx = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const u32x4 a = interleave_x(xa[s]);
+          sx = mfma16<XDT>(a, ones, sx);
+#pragma unroll
+          for (int t = 0; t < NT; ++t) acc[t] = mfma16<XDT>(a, nibbles_to_frag<XDT>(wv[j][t][s]), acc[t]);
+        }
+        // C layout: lane holds rows m = 16 mg + 4 kq + i of column n = n_base + 16t + r.
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const float c = OFF + cv[j][t];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) out[mg][t][i] = fmaf(scv[j][t], acc[t][i] - c * sx[i], out[mg][t][i]);
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) xa[s] = xn[s];
       }
-#pragma unroll
-      for (int s = 0; s < 4; ++s) xa[s] = xn[s];
     }
   };
   for (int64_t p0 = 0; p0 < nblk; p0 += (int64_t)KW * GEMV_BPW) pass(p0);
 
-  if constexpr (KW > 1) {
-    __shared__ float red[KW - 1][NT * 4][64];
-    if (wave > 0) {
 #pragma unroll
-      for (int t = 0; t < NT; ++t)
+  for (int mg = 0; mg < MG; ++mg) {
+    if (16 * mg >= M) break;
+    if constexpr (KW > 1) {
+      __shared__ float red[KW - 1][NT * 4][64];
+      if (mg > 0) __syncthreads();  // wave 0 is done reading the previous group's sums
+      if (wave > 0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) red[wave - 1][t * 4 + i][lane] = out[t][i];
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) red[wave - 1][t * 4 + i][lane] = out[mg][t][i];
+      }
+      __syncthreads();
+      if (wave == 0) {
+#pragma unroll
+        for (int w = 0; w < KW - 1; ++w)
+#pragma unroll
+          for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) out[mg][t][i] += red[w][t * 4 + i][lane];
+      }
     }
-    __syncthreads();
-    if (wave != 0) return;
+    if (wave == 0) {
 #pragma unroll
-    for (int w = 0; w < KW - 1; ++w)
+      for (int t = 0; t < NT; ++t) {
+        const int64_t n = n_base + t * 16 + r;
+        if (!n_ok[t]) continue;
 #pragma unroll
-      for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) out[t][i] += red[w][t * 4 + i][lane];
-  }
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    const int64_t n = n_base + t * 16 + r;
-    if (!n_ok[t]) continue;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t m = 4 * kq + i;
-      if (m < M) y[m * N + n] = Elem<XDT>::cvt(out[t][i]);
+        for (int i = 0; i < 4; ++i) {
+          const int64_t m = 16 * mg + 4 * kq + i;
+          if (m < M) y[m * N + n] = Elem<XDT>::cvt(out[mg][t][i]);
+        }
+      }
     }
   }
 }
@@ -619,11 +646,11 @@ int env_int(const char* name, int dflt) {
 static const int g_contig = env_int("ANNA_MI_INT4_GEMV_CONTIG", 0);
 static const int g_nt = env_int("ANNA_MI_INT4_GEMV_NT", 1);
 
-template <int XDT, int SDT, int NT, int KW, int BPW>
+template <int XDT, int SDT, int NT, int KW, int BPW, int MG = 1>
 void launch_gemv(const void* x, int64_t M, int64_t K, int64_t xs, const int32_t* qw, int64_t N,
                  int64_t pc, const void* qs, const int8_t* qz, int64_t gsz, void* y, hipStream_t st) {
   dim3 grid((unsigned)((N + 16 * NT - 1) / (16 * NT)), 1, 1);
-  hipLaunchKernelGGL((int4_gemv_mfma<XDT, SDT, NT, KW, BPW>), grid, dim3(64 * KW), 0, st, (const uint16_t*)x, M, K, xs,
+  hipLaunchKernelGGL((int4_gemv_mfma<XDT, SDT, NT, KW, BPW, MG>), grid, dim3(64 * KW), 0, st, (const uint16_t*)x, M, K, xs,
                      (const uint32_t*)qw, N, pc, (const typename Elem<SDT>::T*)qs, qz, gsz / 128, (uint16_t*)y,
                      g_contig, g_nt);
 }
@@ -660,6 +687,27 @@ void dispatch_gemv(const void* x, int64_t M, int64_t K, int64_t xs, const int32_
   else if (tiles == 2) ANNA_GEMV_GO(2, 4);
   else ANNA_GEMV_GO(1, 4);
 #undef ANNA_GEMV_GO
+}
+
+// 16 < M <= 64 with one 4-block pass per wave (K <= 128 x 4 x waves): the GEMV with MG row
+// groups of x against the register-resident weights (W read once).
+template <int XDT, int SDT>
+void dispatch_gemv_mg(const void* x, int64_t M, int64_t K, int64_t xs, const int32_t* qw, int64_t N, int64_t pc,
+                      const void* qs, const int8_t* qz, int64_t gsz, void* y, hipStream_t st) {
+  const int64_t nblk = (K + 127) / 128;
+  const bool w8 = nblk > 16;
+  // at most two 16-row tiles per wave: the x fragments of a row group and the accumulators of
+  // every group must fit beside the weights in 256 VGPRs
+  const int tiles = (N + 15) / 16 <= 256 ? 1 : 2;
+  const bool mg2 = M <= 32;
+#define ANNA_GEMV_MG(T)                                                                        \
+  (w8 ? (mg2 ? launch_gemv<XDT, SDT, T, 8, 4, 2>(x, M, K, xs, qw, N, pc, qs, qz, gsz, y, st)      \
+             : launch_gemv<XDT, SDT, T, 8, 4, 4>(x, M, K, xs, qw, N, pc, qs, qz, gsz, y, st))     \
+      : (mg2 ? launch_gemv<XDT, SDT, T, 4, 4, 2>(x, M, K, xs, qw, N, pc, qs, qz, gsz, y, st)      \
+             : launch_gemv<XDT, SDT, T, 4, 4, 4>(x, M, K, xs, qw, N, pc, qs, qz, gsz, y, st)))
+  if (tiles == 1) ANNA_GEMV_MG(1);
+  else ANNA_GEMV_MG(2);
+#undef ANNA_GEMV_MG
 }
 
 }  // namespace
@@ -729,6 +777,19 @@ extern "C" int anna_mi_int4_linear(const void* x, int x_dtype, int64_t M, int64_
         dispatch_gemv<ANNA_MI_F16, SDT>(x, M, K, xs, qweight, N, pc, qscale, qzeros, gsz, y, st);
     });
     ANNA_LAUNCH_CHECK("int4_gemv_mfma");
+    return ANNA_MI_OK;
+  }
+  // 16 < M < 64: the GEMV with 16-row groups of x against register-resident weights (M = 17..48
+  // at N = 12288, K = 4096: 24-35 us, where the LDS-tiled fallback below took ~145 us); from
+  // M = 64 the tiled GEMM is faster (27.6 against 46 us at M = 64)
+  if (x16 && aligned && M < 64 && (K + 127) / 128 <= 32) {
+    ANNA_DISPATCH_DTYPE(scale_dtype, SDT, {
+      if (x_dtype == ANNA_MI_BF16)
+        dispatch_gemv_mg<ANNA_MI_BF16, SDT>(x, M, K, xs, qweight, N, pc, qscale, qzeros, gsz, y, st);
+      else
+        dispatch_gemv_mg<ANNA_MI_F16, SDT>(x, M, K, xs, qweight, N, pc, qscale, qzeros, gsz, y, st);
+    });
+    ANNA_LAUNCH_CHECK("int4_gemv_mfma (row groups)");
     return ANNA_MI_OK;
   }
   if (int4_gemm_tiled_supported(x_dtype, M, N, K, xs, x, qweight, pc, qscale, qzeros, gsz))

@@ -47,6 +47,8 @@ LINEAR_CASES = [
     (8, 512, 12200, 128, "bf16"),   # MFMA GEMV, three 16-row tiles per wave, N tail
     (4, 1024, 8000, 128, "fp32"),   # MFMA GEMV, two tiles
     (8, 512, 2000, 128, "bf16"),    # MFMA GEMV, one tile
+    (48, 4096, 3000, 128, "bf16"),  # MFMA GEMV over three 16-row groups of x (N tail)
+    (20, 2048, 4200, 128, "fp32"),  # two row groups, two tiles, four-wave K split
 ]
 
 
