@@ -1,4 +1,4 @@
-// W4A16 GEMM for M >= 64 on gfx950: y[M, N] = x[M, K] . dequant(W)[N, K]^T.
+// W4A16 GEMM for M >= 64 (and 16 < M < 64 with long K) on gfx950: y[M, N] = x[M, K] . dequant(W)[N, K]^T.
 //
 // Tile 256 (m) x 192 (n) x 64 (k) per workgroup of 12 waves with two roles (for M >= 1024; the
 // same kernel runs 128 x 96 tiles with a 4 x 2 grid of MFMA waves for M >= 256 and 64 x 48 with
@@ -308,7 +308,9 @@ bool int4_gemm_tiled_supported(int x_dtype, int64_t M, int64_t N, int64_t K, int
   const int64_t G = gsz > 0 ? (K + gsz - 1) / gsz : 0;
   const bool fits = (int64_t)TileL::BM * xs * 2 < (1ll << 31) && (int64_t)TileL::BN * pc * 4 < (1ll << 31) &&
                     G * N * 4 < (1ll << 31) && K / GM_BK < (1 << 16) && gsz / GM_BK < (1 << 16);
-  return (x_dtype == ANNA_MI_BF16 || x_dtype == ANNA_MI_F16) && M >= 64 && K % GM_BK == 0 && gsz % GM_BK == 0 &&
+  // (M < 64 works too, rows past M reading as zero: the dispatcher sends 16 < M < 64 here when K
+  // is too long for the row-group GEMV)
+  return (x_dtype == ANNA_MI_BF16 || x_dtype == ANNA_MI_F16) && M > 16 && K % GM_BK == 0 && gsz % GM_BK == 0 &&
          xs % 8 == 0 && pc % 4 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)qweight % 16 == 0 && fits;
 }
 

@@ -16,7 +16,8 @@
 //                       sum_k x (q - z) s = s * (sum_k x (off + q) - (off + z) sum_k x).
 //                    For M > 16 the 16-row groups of x take turns against the weights,
 //                    which stay in registers (W is read once for all of M).
-//   (M >= 64 with 16-bit activations, K % 64 == 0: int4_gemm_tiled_kernel, int4_gemm.hip)
+//   (M >= 64, or 16 < M < 64 with K > 4096, 16-bit activations, K % 64 == 0:
+//    int4_gemm_tiled_kernel, int4_gemm.hip)
 //   int4_gemm_mfma   other M > 16.  LDS-tiled: a 128x128 tile of W is dequantized once per
 //                    workgroup to bf16 ((q - z) * s rounded to bf16, the reference's
 //                    dequant numerics) next to a 128x128 tile of x, and 4 waves run

@@ -49,6 +49,7 @@ LINEAR_CASES = [
     (8, 512, 2000, 128, "bf16"),    # MFMA GEMV, one tile
     (48, 4096, 3000, 128, "bf16"),  # MFMA GEMV over three 16-row groups of x (N tail)
     (20, 2048, 4200, 128, "fp32"),  # two row groups, two tiles, four-wave K split
+    (40, 8192, 200, 128, "bf16"),   # 16 < M < 64 with K past the row-group GEMV: tiled GEMM
 ]
 
 
