@@ -95,8 +95,11 @@ __global__ __launch_bounds__(64 * KW) void int4_gemv_mfma(
   // With 4 blocks per wave and pass, the x fragments of all of them are loaded first (64
   // VGPRs): a fragment fetched one block ahead was sunk by the compiler next to its use, and
   // each block then waited a full round trip for x.
-  constexpr bool XALL = GEMV_BPW <= 4;
-  static_assert(MG == 1 || XALL, "several row groups need the 4-block pass");
+  // Several row groups (MG > 1): the x fragments of the next block are fetched while the
+  // current block computes instead (half the registers), pinned ahead of the MFMAs by a
+  // scheduling barrier, so that three 16-row tiles per wave still fit without spills.
+  constexpr bool XALL = GEMV_BPW <= 4 && MG == 1;
+  static_assert(MG == 1 || GEMV_BPW <= 4, "several row groups need the 4-block pass");
   auto pass = [&](int64_t p0) {
     u32x4 xall[XALL ? GEMV_BPW : 1][4];
     if constexpr (XALL) {
@@ -134,19 +137,11 @@ __global__ __launch_bounds__(64 * KW) void int4_gemv_mfma(
         if (!n_ok[t]) wv[j][t] = zero4;
 #pragma unroll
     for (int mg = 0; mg < MG; ++mg) {
-      if (mg > 0) {
-        // the next row group's x (the weights stay in registers)
-        __builtin_amdgcn_sched_barrier(0);
-        if (16 * mg >= M) break;
-#pragma unroll
-        for (int j = 0; j < GEMV_BPW; ++j)
-#pragma unroll
-          for (int s = 0; s < 4; ++s) xall[j][s] = load_x(p0 + bw0 + bstep * j, s, mg);
-      }
+      if (mg > 0 && 16 * mg >= M) break;
       // otherwise the x fragments of the next block are fetched while the current block computes
       u32x4 xa[4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) xa[s] = XALL ? xall[0][s] : load_x(p0 + bw0, s, 0);
+      for (int s = 0; s < 4; ++s) xa[s] = XALL ? xall[0][s] : load_x(p0 + bw0, s, mg);
 #pragma unroll
       for (int j = 0; j < GEMV_BPW; ++j) {
         const int64_t b = p0 + bw0 + bstep * j;
@@ -154,7 +149,8 @@ __global__ __launch_bounds__(64 * KW) void int4_gemv_mfma(
         u32x4 xn[4];
 #pragma unroll
         for (int s = 0; s < 4; ++s)
-          xn[s] = j + 1 < GEMV_BPW ? (XALL ? xall[j + 1 < GEMV_BPW ? j + 1 : 0][s] : load_x(b + bstep, s, 0)) : zero4;
+          xn[s] = j + 1 < GEMV_BPW ? (XALL ? xall[j + 1 < GEMV_BPW ? j + 1 : 0][s] : load_x(b + bstep, s, mg)) : zero4;
+        if constexpr (MG > 1) __builtin_amdgcn_sched_barrier(0);
         f32x4 acc[NT];
         f32x4 sx = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -697,9 +693,12 @@ void dispatch_gemv_mg(const void* x, int64_t M, int64_t K, int64_t xs, const int
                       const void* qs, const int8_t* qz, int64_t gsz, void* y, hipStream_t st) {
   const int64_t nblk = (K + 127) / 128;
   const bool w8 = nblk > 16;
-  // at most two 16-row tiles per wave: the x fragments of a row group and the accumulators of
-  // every group must fit beside the weights in 256 VGPRs
-  const int tiles = (N + 15) / 16 <= 256 ? 1 : 2;
+  int tiles = 3;
+  for (int t = 1; t <= 3; ++t)
+    if ((N + 16 * t - 1) / (16 * t) <= 256) {
+      tiles = t;
+      break;
+    }
   const bool mg2 = M <= 32;
 #define ANNA_GEMV_MG(T)                                                                        \
   (w8 ? (mg2 ? launch_gemv<XDT, SDT, T, 8, 4, 2>(x, M, K, xs, qw, N, pc, qs, qz, gsz, y, st)      \
@@ -707,7 +706,8 @@ void dispatch_gemv_mg(const void* x, int64_t M, int64_t K, int64_t xs, const int
       : (mg2 ? launch_gemv<XDT, SDT, T, 4, 4, 2>(x, M, K, xs, qw, N, pc, qs, qz, gsz, y, st)      \
              : launch_gemv<XDT, SDT, T, 4, 4, 4>(x, M, K, xs, qw, N, pc, qs, qz, gsz, y, st)))
   if (tiles == 1) ANNA_GEMV_MG(1);
-  else ANNA_GEMV_MG(2);
+  else if (tiles == 2) ANNA_GEMV_MG(2);
+  else ANNA_GEMV_MG(3);
 #undef ANNA_GEMV_MG
 }
 
