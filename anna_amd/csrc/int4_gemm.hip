@@ -62,9 +62,10 @@ using TileS = GemmTile<64, 48, 4, 1>;    // M < 256:   16 x 48 wave tiles, 36 KB
 #define GM_WAIT_BARRIER(n) asm volatile("s_waitcnt vmcnt(" #n ") lgkmcnt(0)\n\ts_barrier" ::: "memory")
 template <int N>
 __device__ __forceinline__ void loader_barrier() {
-  static_assert(N == 17 || N == 10 || N == 5 || N == 26 || N == 16 || N == 8,
+  static_assert(N == 17 || N == 10 || N == 5 || N == 26 || N == 16 || N == 8 || N == 0,
                 "add the wait count of a new tile shape here");
-  if constexpr (N == 17) GM_WAIT_BARRIER(17);
+  if constexpr (N == 0) GM_WAIT_BARRIER(0);
+  else if constexpr (N == 17) GM_WAIT_BARRIER(17);
   else if constexpr (N == 10) GM_WAIT_BARRIER(10);
   else if constexpr (N == 5) GM_WAIT_BARRIER(5);
   else if constexpr (N == 26) GM_WAIT_BARRIER(26);
@@ -209,7 +210,11 @@ __global__ __launch_bounds__(T::THREADS) void int4_gemm_tiled_kernel(
       }
     };
     // prologue: W of steps 0..2 and x of steps 0..1; W of step 0 to LDS; barrier once x of
-    // step 0 has landed (the loads after it: W 1, x 1, W 2)
+    // step 0 has landed.  The wait is for every load issued so far: the compiler is free to
+    // sink the loads of W 2 below the barrier (their values are first used in the loop), and
+    // then a count of "the loads after x 0" (W 1, x 1, W 2) would let x 0 still be in flight
+    // while the MFMA waves read it.  (Inside the loop each step's loads stay ahead of its
+    // barrier; the cost of waiting for everything here is paid once.)
     Stage S0, S1, S2;
     load_w(0, S0);
     load_x(0, 0);
@@ -217,7 +222,7 @@ __global__ __launch_bounds__(T::THREADS) void int4_gemm_tiled_kernel(
     load_x(1, 1);
     load_w(2, S2);
     store(S0, 0);
-    loader_barrier<2 * T::LOADS_PER_STEP - T::XLD>();
+    loader_barrier<0>();
     // step ks: W of ks + 3 into the stage that held W of ks, x of ks + 2 into the x buffer read
     // at step ks - 1, dequantize W of ks + 1, barrier once x of ks + 1 has landed
     int a2 = 2, b1 = 1;  // x buffer of step ks + 2, W buffer of step ks + 1
