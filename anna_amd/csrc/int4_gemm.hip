@@ -32,47 +32,45 @@ namespace {
 
 constexpr int GM_BK = 64, GM_LOAD_WAVES = 4;
 constexpr int GM_LT = 64 * GM_LOAD_WAVES;  // loader threads
-constexpr int GM_NA = 3, GM_NB = 2;        // LDS buffers of x and of W
+
 constexpr uint32_t GM_OOB = 0x80000000u;   // buffer offset past any num_records: the load returns 0
 
-// Tile shape: BM x BN per workgroup, an MW x NW grid of MFMA waves (wave tile BM/MW x BN/NW).
-template <int BM_, int BN_, int MW_, int NW_>
+// Tile shape: BM x BN per workgroup, an MW x NW grid of MFMA waves (wave tile BM/MW x BN/NW),
+// SPB k-steps of 64 between two workgroup barriers (a "period"): the smallest tile, whose steps
+// hold little MFMA work, pays the barrier and its waits once per two steps.  LDS holds x for
+// three periods (the one read, the one landing, the one being loaded) and W for two.
+template <int BM_, int BN_, int MW_, int NW_, int SPB_ = 1>
 struct GemmTile {
-  static constexpr int BM = BM_, BN = BN_, MW = MW_, NW = NW_;
+  static constexpr int BM = BM_, BN = BN_, MW = MW_, NW = NW_, SPB = SPB_;
+  static constexpr int NA = 3 * SPB, NB = 2 * SPB;  // LDS buffers (one k-step each) of x and of W
   static constexpr int MFMA_WAVES = MW * NW, THREADS = 64 * (MFMA_WAVES + GM_LOAD_WAVES);
   static constexpr int TM = BM / MW, TN = BN / NW, FM = TM / 16, FN = TN / 16;  // wave tile, fragments
   static constexpr int LDS_A = BM * GM_BK, LDS_B = BN * GM_BK;                   // 16-bit elements per buffer
-  static constexpr size_t LDS_BYTES = (size_t)(GM_NA * LDS_A + GM_NB * LDS_B) * 2;
+  static constexpr size_t LDS_BYTES = (size_t)(NA * LDS_A + NB * LDS_B) * 2;
   static constexpr int XLD = BM / 8 / GM_LOAD_WAVES;           // 8-row x blocks per loader wave
   static constexpr int WPT = (BN * 4 + GM_LT - 1) / GM_LT;     // W chunks (8 B = 16 nibbles) per loader thread
   // vector-memory loads one loader thread issues per k-step: the x blocks plus word, scale and
   // zero point of each W chunk; the wait before each barrier keeps exactly these outstanding
   static constexpr int LOADS_PER_STEP = XLD + 3 * WPT;
   static_assert(TM % 16 == 0 && TN % 16 == 0 && BM % (8 * GM_LOAD_WAVES) == 0, "tile shape");
+  static_assert(SPB == 1 || SPB == 2, "one or two k-steps per period");
   static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 };
-using TileL = GemmTile<256, 192, 2, 4>;  // M >= 1024: 128 x 48 wave tiles, 144 KB LDS
-using TileM = GemmTile<128, 96, 4, 2>;   // M >= 256:  32 x 48 wave tiles, 72 KB LDS
-using TileS = GemmTile<64, 48, 4, 1>;    // M < 256:   16 x 48 wave tiles, 36 KB LDS
+using TileL = GemmTile<256, 192, 2, 4, 1>;  // M >= 1024: 128 x 48 wave tiles, 144 KB LDS
+using TileM = GemmTile<128, 96, 4, 2, 1>;   // M >= 256:  32 x 48 wave tiles, 72 KB LDS
+using TileS = GemmTile<64, 48, 4, 1, 2>;    // M < 256:   16 x 48 wave tiles, 72 KB LDS, 2 steps per
+                                            // period (M = 64, N = 12288: 25.6 -> 23.9 us; the 128 x 96
+                                            // tile measured no faster with 2)
 
 // The loader's end of a k-step: all but its N most recent loads have landed (so the previous
 // step's LDS-destination x loads are in LDS), its LDS writes are done, then the workgroup
 // barrier.  __syncthreads() would also wait for the loads just issued, since its release fence
 // covers LDS-destination loads.
-#define GM_WAIT_BARRIER(n) asm volatile("s_waitcnt vmcnt(" #n ") lgkmcnt(0)\n\ts_barrier" ::: "memory")
 template <int N>
 __device__ __forceinline__ void loader_barrier() {
-  static_assert(N == 17 || N == 10 || N == 5 || N == 26 || N == 16 || N == 8 || N == 0,
-                "add the wait count of a new tile shape here");
-  if constexpr (N == 0) GM_WAIT_BARRIER(0);
-  else if constexpr (N == 17) GM_WAIT_BARRIER(17);
-  else if constexpr (N == 10) GM_WAIT_BARRIER(10);
-  else if constexpr (N == 5) GM_WAIT_BARRIER(5);
-  else if constexpr (N == 26) GM_WAIT_BARRIER(26);
-  else if constexpr (N == 16) GM_WAIT_BARRIER(16);
-  else GM_WAIT_BARRIER(8);
+  static_assert(N >= 0 && N <= 63, "vmcnt holds 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"i"(N) : "memory");
 }
-#undef GM_WAIT_BARRIER
 
 typedef float f32x2v __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
@@ -100,6 +98,7 @@ __global__ __launch_bounds__(T::THREADS) void int4_gemm_tiled_kernel(
   using ST = typename Elem<SDT>::T;
   constexpr int GM_BM = T::BM, GM_BN = T::BN, GM_LDS_A = T::LDS_A, GM_LDS_B = T::LDS_B;
   constexpr int GM_MFMA_WAVES = T::MFMA_WAVES, GM_XLD = T::XLD, GM_WPT = T::WPT;
+  constexpr int GM_NA = T::NA;
   uint16_t* const sA0 = smem;                       // GM_NA x buffers
   uint16_t* const sB0 = smem + GM_NA * GM_LDS_A;    // GM_NB W buffers
   const int tid = threadIdx.x;
@@ -209,37 +208,72 @@ __global__ __launch_bounds__(T::THREADS) void int4_gemm_tiled_kernel(
         }
       }
     };
-    // prologue: W of steps 0..2 and x of steps 0..1; W of step 0 to LDS; barrier once x of
-    // step 0 has landed.  The wait is for every load issued so far: the compiler is free to
-    // sink the loads of W 2 below the barrier (their values are first used in the loop), and
-    // then a count of "the loads after x 0" (W 1, x 1, W 2) would let x 0 still be in flight
-    // while the MFMA waves read it.  (Inside the loop each step's loads stay ahead of its
-    // barrier; the cost of waiting for everything here is paid once.)
-    Stage S0, S1, S2;
-    load_w(0, S0);
-    load_x(0, 0);
-    load_w(1, S1);
-    load_x(1, 1);
-    load_w(2, S2);
-    store(S0, 0);
-    loader_barrier<0>();
-    // step ks: W of ks + 3 into the stage that held W of ks, x of ks + 2 into the x buffer read
-    // at step ks - 1, dequantize W of ks + 1, barrier once x of ks + 1 has landed
-    int a2 = 2, b1 = 1;  // x buffer of step ks + 2, W buffer of step ks + 1
-    auto step = [&](int ks, Stage& Sfree, Stage& Snext) {
-      load_w(ks + 3, Sfree);
-      load_x(ks + 2, a2);
-      a2 = a2 == GM_NA - 1 ? 0 : a2 + 1;
-      if (ks + 1 < nk) store(Snext, b1);
-      b1 ^= 1;
-      loader_barrier<T::LOADS_PER_STEP>();
-    };
-    for (int ks = 0; ks < nk; ks += 3) {
-      step(ks, S0, S1);
-      if (ks + 1 >= nk) break;
-      step(ks + 1, S1, S2);
-      if (ks + 2 >= nk) break;
-      step(ks + 2, S2, S0);
+    if constexpr (T::SPB == 1) {
+      // prologue: W of steps 0..2 and x of steps 0..1; W of step 0 to LDS; barrier once x of
+      // step 0 has landed.  The wait is for every load issued so far: the compiler is free to
+      // sink the loads of W 2 below the barrier (their values are first used in the loop), and
+      // then a count of "the loads after x 0" (W 1, x 1, W 2) would let x 0 still be in flight
+      // while the MFMA waves read it.  (Inside the loop each step's loads stay ahead of its
+      // barrier; the cost of waiting for everything here is paid once.)
+      Stage S0, S1, S2;
+      load_w(0, S0);
+      load_x(0, 0);
+      load_w(1, S1);
+      load_x(1, 1);
+      load_w(2, S2);
+      store(S0, 0);
+      loader_barrier<0>();
+      // step ks: W of ks + 3 into the stage that held W of ks, x of ks + 2 into the x buffer read
+      // at step ks - 1, dequantize W of ks + 1, barrier once x of ks + 1 has landed
+      int a2 = 2, b1 = 1;  // x buffer of step ks + 2, W buffer of step ks + 1
+      auto step = [&](int ks, Stage& Sfree, Stage& Snext) {
+        load_w(ks + 3, Sfree);
+        load_x(ks + 2, a2);
+        a2 = a2 == GM_NA - 1 ? 0 : a2 + 1;
+        if (ks + 1 < nk) store(Snext, b1);
+        b1 ^= 1;
+        loader_barrier<T::LOADS_PER_STEP>();
+      };
+      for (int ks = 0; ks < nk; ks += 3) {
+        step(ks, S0, S1);
+        if (ks + 1 >= nk) break;
+        step(ks + 1, S1, S2);
+        if (ks + 2 >= nk) break;
+        step(ks + 2, S2, S0);
+      }
+    } else {
+      // Two k-steps per period.  Step k's W lives in register stage k % 4, its x in LDS buffer
+      // k % 6, its dequantized W in LDS buffer k % 4.  Period p: W and x of steps 2p+4, 2p+5
+      // (two periods ahead), dequantize W of steps 2p+2, 2p+3, barrier once x of steps 2p+2,
+      // 2p+3 (issued in the period before) has landed: all but this period's loads.
+      Stage S0, S1, S2, S3;
+      load_w(0, S0);
+      load_w(1, S1);
+      load_x(0, 0);
+      load_x(1, 1);
+      load_w(2, S2);
+      load_w(3, S3);
+      load_x(2, 2);
+      load_x(3, 3);
+      store(S0, 0);
+      if (1 < nk) store(S1, 1);
+      loader_barrier<0>();  // everything issued so far (see the one-step prologue)
+      const int np = (nk + 1) / 2;
+      auto period = [&](int p, Stage& La, Stage& Lb, const Stage& Sa, const Stage& Sb) {
+        const int k = 2 * p;
+        load_w(k + 4, La);
+        load_w(k + 5, Lb);
+        load_x(k + 4, (k + 4) % 6);
+        load_x(k + 5, (k + 5) % 6);
+        if (k + 2 < nk) store(Sa, (k + 2) % 4);
+        if (k + 3 < nk) store(Sb, (k + 3) % 4);
+        loader_barrier<2 * T::LOADS_PER_STEP>();
+      };
+      for (int p = 0; p < np; p += 2) {
+        period(p, S0, S1, S2, S3);
+        if (p + 1 >= np) break;
+        period(p + 1, S2, S3, S0, S1);
+      }
     }
     // the last steps' reloads land in buffers nobody reads; drain them before the wave ends
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -280,12 +314,22 @@ __global__ __launch_bounds__(T::THREADS) void int4_gemm_tiled_kernel(
         for (int j = 0; j < FN; ++j) acc[i][j] = mfma16<XDT>(av[i], b[j], acc[i][j]);
     }
   };
-  __syncthreads();  // step 0 is in LDS
-  int ab = 0;
-  for (int ks = 0; ks < nk; ++ks) {
-    compute(ab, ks & 1);
-    ab = ab == GM_NA - 1 ? 0 : ab + 1;
-    __syncthreads();
+  __syncthreads();  // step 0 (both steps of period 0) is in LDS
+  if constexpr (T::SPB == 1) {
+    int ab = 0;
+    for (int ks = 0; ks < nk; ++ks) {
+      compute(ab, ks & 1);
+      ab = ab == GM_NA - 1 ? 0 : ab + 1;
+      __syncthreads();
+    }
+  } else {
+    const int np = (nk + 1) / 2;
+    for (int p = 0; p < np; ++p) {
+      const int k = 2 * p;
+      compute(k % 6, k % 4);
+      if (k + 1 < nk) compute((k + 1) % 6, (k + 1) % 4);
+      __syncthreads();
+    }
   }
   // C layout: lane holds rows 4 kq + e of column r of each 16 x 16 block
 #pragma unroll

@@ -69,7 +69,9 @@ def test_int4_linear_matches_oracle(gpu, m, k, n, group, sdt):
 
 @pytest.mark.parametrize("tile", ["L", "M", "S"])
 @pytest.mark.parametrize("m,k,n,group,sdt", [(300, 512, 400, 64, "bf16"), (2048, 1024, 200, 128, "fp32"),
-                                             (64, 1024, 96, 128, "bf16"), (257, 256, 1000, 128, "bf16")])
+                                             (64, 1024, 96, 128, "bf16"), (257, 256, 1000, 128, "bf16"),
+                                             (100, 320, 200, 64, "bf16"),   # odd k-step count (5)
+                                             (70, 64, 96, 64, "fp32")])     # a single k-step
 def test_int4_gemm_every_tile_shape(gpu, monkeypatch, tile, m, k, n, group, sdt):
     """The tiled GEMM's three tile shapes (chosen by size in production), each forced."""
     print(f"[case] int4 tiled GEMM tile={tile} M={m} K={k} N={n} g={group} scale={sdt}", flush=True)
