@@ -38,11 +38,11 @@ __host__ __device__ constexpr int route_scratch(int64_t E) { return (int)((E + 3
 // cross-lane argmax: the probabilities go to the wave's LDS scratch sp (route_scratch(E)
 // floats), every lane counts for each of its experts how many experts beat it (a larger
 // probability, or an equal one at a lower index), and an expert of rank j < top_k is route j.
-template <int LDT>
+// MAXV: experts per lane, E <= 64 MAXV (instantiated for E <= 64, 128, 256 and 1024).
+template <int LDT, int MAXV>
 __device__ __forceinline__ void route_token(const typename Elem<LDT>::T* __restrict__ logits, int64_t t, int64_t E,
                                             int64_t ls, int64_t top_k, int normalize, int lane, float* sp,
                                             float& w_out, int64_t& e_out) {
-  constexpr int MAXV = 16;  // experts per lane (E <= 1024)
   float v[MAXV];
   float mx = -INFINITY;
 #pragma unroll
@@ -98,8 +98,18 @@ __device__ __forceinline__ void route_token(const typename Elem<LDT>::T* __restr
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Experts per lane for E experts (the route_token instantiations).
+inline int route_maxv(int64_t E) { return E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : 16; }
+#define ANNA_DISPATCH_MAXV(E, NAME, ...)                                  \
+  switch (route_maxv(E)) {                                                \
+    case 1: { constexpr int NAME = 1; __VA_ARGS__; break; }               \
+    case 2: { constexpr int NAME = 2; __VA_ARGS__; break; }               \
+    case 4: { constexpr int NAME = 4; __VA_ARGS__; break; }               \
+    default: { constexpr int NAME = 16; __VA_ARGS__; break; }             \
+  }
+
 // One wave per token.
-template <int LDT>
+template <int LDT, int MAXV>
 __global__ __launch_bounds__(256) void moe_router_kernel(const typename Elem<LDT>::T* __restrict__ logits,
                                                          int64_t T, int64_t E, int64_t ls, int64_t top_k, int normalize,
                                                          float* __restrict__ weights, int64_t* __restrict__ selected,
@@ -110,7 +120,7 @@ __global__ __launch_bounds__(256) void moe_router_kernel(const typename Elem<LDT
   if (t >= T) return;
   float w;
   int64_t e;
-  route_token<LDT>(logits, t, E, ls, top_k, normalize, lane, r_scratch + (threadIdx.x >> 6) * route_scratch(E), w, e);
+  route_token<LDT, MAXV>(logits, t, E, ls, top_k, normalize, lane, r_scratch + (threadIdx.x >> 6) * route_scratch(E), w, e);
   if (lane < top_k) {
     weights[t * top_k + lane] = w;
     selected[t * top_k + lane] = e;
@@ -147,7 +157,7 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* s, int* total) {
 // same deterministic (expert, token, k) order, plus items as moe_compact_items_kernel writes
 // them for the experts with routes (bank slot slots[e]).  Four launches become one; each of
 // them costs a few microseconds here whatever its work.
-template <int LDT>
+template <int LDT, int MAXV>
 __global__ __launch_bounds__(1024) void moe_route_small_kernel(
     const typename Elem<LDT>::T* __restrict__ logits, int64_t T, int64_t E, int64_t ls, int64_t top_k, int normalize,
     float* __restrict__ weights, int64_t* __restrict__ selected, int32_t* __restrict__ usage,
@@ -157,12 +167,14 @@ __global__ __launch_bounds__(1024) void moe_route_small_kernel(
   extern __shared__ float r_scratch[];  // 16 x route_scratch(E)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t R = T * top_k;
+  // this thread's expert's bank slot, read now so that its latency hides behind the routing
+  const int64_t my_slot = threadIdx.x < E ? slots[threadIdx.x] : 0;
   s_cnt[threadIdx.x] = 0;
   __syncthreads();
   for (int64_t t = wave; t < T; t += 16) {
     float w;
     int64_t e;
-    route_token<LDT>(logits, t, E, ls, top_k, normalize, lane, r_scratch + wave * route_scratch(E), w, e);
+    route_token<LDT, MAXV>(logits, t, E, ls, top_k, normalize, lane, r_scratch + wave * route_scratch(E), w, e);
     if (lane < top_k) {
       weights[t * top_k + lane] = w;
       selected[t * top_k + lane] = e;
@@ -181,7 +193,7 @@ __global__ __launch_bounds__(1024) void moe_route_small_kernel(
     usage[e] = cnt;
     offsets[e] = start;
     s_off[e] = start;
-    if (cnt > 0) *(int4*)(items + 4 + 4 * j) = make_int4((int)slots[e], start, start + cnt, 0);
+    if (cnt > 0) *(int4*)(items + 4 + 4 * j) = make_int4((int)my_slot, start, start + cnt, 0);
   }
   if (e == 0) {
     offsets[E] = total;
@@ -725,10 +737,12 @@ extern "C" int anna_mi_moe_router(const void* logits, int logits_dtype, int64_t 
   ANNA_LAUNCH_CHECK("fill_i32_kernel");
   if (tokens == 0) return ANNA_MI_OK;
   ANNA_DISPATCH_DTYPE(logits_dtype, LDT, {
-    hipLaunchKernelGGL((moe_router_kernel<LDT>), dim3((unsigned)((tokens + 3) / 4)), dim3(256),
-                       4 * route_scratch(num_experts) * sizeof(float), st,
-                       (const typename Elem<LDT>::T*)logits, tokens, num_experts, logits_row_stride, top_k, normalize,
-                       weights, selected, usage);
+    ANNA_DISPATCH_MAXV(num_experts, MAXV, {
+      hipLaunchKernelGGL((moe_router_kernel<LDT, MAXV>), dim3((unsigned)((tokens + 3) / 4)), dim3(256),
+                         4 * route_scratch(num_experts) * sizeof(float), st,
+                         (const typename Elem<LDT>::T*)logits, tokens, num_experts, logits_row_stride, top_k, normalize,
+                         weights, selected, usage);
+    });
   });
   ANNA_LAUNCH_CHECK("moe_router_kernel");
   return ANNA_MI_OK;
@@ -781,11 +795,13 @@ extern "C" int anna_mi_moe_route_small(const void* logits, int logits_dtype, int
              "anna_mi_moe_route_small: need 0 < tokens * top_k <= 1024 (use the router + dispatch entry points above)");
   ANNA_CHECK(num_experts <= 512, "anna_mi_moe_route_small: num_experts must be <= 512 (LDS)");
   ANNA_DISPATCH_DTYPE(logits_dtype, LDT, {
-    hipLaunchKernelGGL((moe_route_small_kernel<LDT>), dim3(1), dim3(1024), 16 * route_scratch(num_experts) * sizeof(float),
-                       as_stream(stream),
-                       (const typename Elem<LDT>::T*)logits, tokens, num_experts, logits_row_stride, top_k, normalize,
-                       weights, selected, usage, expert_offsets, sorted_token_idx, sorted_route_idx, route_pos, slots,
-                       items);
+    ANNA_DISPATCH_MAXV(num_experts, MAXV, {
+      hipLaunchKernelGGL((moe_route_small_kernel<LDT, MAXV>), dim3(1), dim3(1024),
+                         16 * route_scratch(num_experts) * sizeof(float), as_stream(stream),
+                         (const typename Elem<LDT>::T*)logits, tokens, num_experts, logits_row_stride, top_k, normalize,
+                         weights, selected, usage, expert_offsets, sorted_token_idx, sorted_route_idx, route_pos, slots,
+                         items);
+    });
   });
   ANNA_LAUNCH_CHECK("moe_route_small_kernel");
   return ANNA_MI_OK;
