@@ -264,10 +264,10 @@ __global__ __launch_bounds__(256) void moe_order_kernel(const int64_t* __restric
 }
 
 // grid (routes), 64 threads x 16 B: compact row p = hidden row of its token; the compact
-// routing weight = routing_weights[route].
-template <int HDT>
+// routing weight = routing_weights[route] (dtype WDT) rounded to the hidden dtype.
+template <int HDT, int WDT>
 __global__ __launch_bounds__(64) void moe_gather_kernel(const typename Elem<HDT>::T* __restrict__ hidden, int64_t H,
-                                                        int64_t hs, const typename Elem<HDT>::T* __restrict__ rw,
+                                                        int64_t hs, const typename Elem<WDT>::T* __restrict__ rw,
                                                         const int64_t* __restrict__ sorted_route, int64_t top_k,
                                                         typename Elem<HDT>::T* __restrict__ compact,
                                                         typename Elem<HDT>::T* __restrict__ compact_w) {
@@ -283,7 +283,7 @@ __global__ __launch_bounds__(64) void moe_gather_kernel(const typename Elem<HDT>
   } else {
     for (int64_t c = threadIdx.x; c < H; c += blockDim.x) dst[c] = src[c];
   }
-  if (threadIdx.x == 0) compact_w[p] = rw[route];
+  if (threadIdx.x == 0) compact_w[p] = HDT == WDT ? (T)rw[route] : Elem<HDT>::cvt(Elem<WDT>::load(rw, route));
 }
 
 // ------------------------------------------------------------------ scatter / combine
@@ -749,7 +749,8 @@ extern "C" int anna_mi_moe_router(const void* logits, int logits_dtype, int64_t 
 }
 
 extern "C" int anna_mi_moe_dispatch(const void* hidden, int dtype, int64_t tokens, int64_t hidden_dim,
-                                    int64_t hidden_row_stride, const void* routing_weights, const int64_t* selected,
+                                    int64_t hidden_row_stride, const void* routing_weights, int weights_dtype,
+                                    const int64_t* selected,
                                     const void* usage, int usage_is_int64, int64_t num_experts, int64_t top_k,
                                     int64_t* sorted_token_idx, int64_t* sorted_route_idx, int64_t* expert_offsets,
                                     void* compact_hidden, void* compact_weights, int64_t* route_pos, void* stream) {
@@ -758,6 +759,7 @@ extern "C" int anna_mi_moe_dispatch(const void* hidden, int dtype, int64_t token
              "anna_mi_moe_dispatch: null pointer");
   ANNA_CHECK(num_experts > 0 && top_k > 0 && hidden_dim > 0 && tokens >= 0 && hidden_row_stride >= hidden_dim,
              "anna_mi_moe_dispatch: bad shape");
+  ANNA_CHECK(valid_dtype(dtype) && valid_dtype(weights_dtype), "anna_mi_moe_dispatch: bad dtype code");
   hipStream_t st = as_stream(stream);
   const int64_t routes = tokens * top_k;
   if (usage_is_int64) {
@@ -772,10 +774,12 @@ extern "C" int anna_mi_moe_dispatch(const void* hidden, int dtype, int64_t token
   ANNA_LAUNCH_CHECK("moe_order_kernel");
   if (routes == 0) return ANNA_MI_OK;
   ANNA_DISPATCH_DTYPE(dtype, HDT, {
-    using T = typename Elem<HDT>::T;
-    hipLaunchKernelGGL((moe_gather_kernel<HDT>), dim3((unsigned)routes), dim3(64), 0, st, (const T*)hidden, hidden_dim,
-                       hidden_row_stride, (const T*)routing_weights, sorted_route_idx, top_k, (T*)compact_hidden,
-                       (T*)compact_weights);
+    ANNA_DISPATCH_DTYPE(weights_dtype, WDT, {
+      using T = typename Elem<HDT>::T;
+      hipLaunchKernelGGL((moe_gather_kernel<HDT, WDT>), dim3((unsigned)routes), dim3(64), 0, st, (const T*)hidden,
+                         hidden_dim, hidden_row_stride, (const typename Elem<WDT>::T*)routing_weights, sorted_route_idx,
+                         top_k, (T*)compact_hidden, (T*)compact_weights);
+    });
   });
   ANNA_LAUNCH_CHECK("moe_gather_kernel");
   return ANNA_MI_OK;
@@ -808,17 +812,21 @@ extern "C" int anna_mi_moe_route_small(const void* logits, int logits_dtype, int
 }
 
 extern "C" int anna_mi_moe_gather(const void* hidden, int dtype, int64_t hidden_dim, int64_t hidden_row_stride,
-                                  const void* routing_weights, const int64_t* sorted_route_idx, int64_t routes,
+                                  const void* routing_weights, int weights_dtype, const int64_t* sorted_route_idx,
+                                  int64_t routes,
                                   int64_t top_k, void* compact_hidden, void* compact_weights, void* stream) {
   ANNA_CHECK(hidden && routing_weights && sorted_route_idx && compact_hidden && compact_weights,
              "anna_mi_moe_gather: null pointer");
   ANNA_CHECK(routes >= 0 && top_k > 0 && hidden_dim > 0 && hidden_row_stride >= hidden_dim, "anna_mi_moe_gather: bad shape");
+  ANNA_CHECK(valid_dtype(dtype) && valid_dtype(weights_dtype), "anna_mi_moe_gather: bad dtype code");
   if (routes == 0) return ANNA_MI_OK;
   ANNA_DISPATCH_DTYPE(dtype, HDT, {
-    using T = typename Elem<HDT>::T;
-    hipLaunchKernelGGL((moe_gather_kernel<HDT>), dim3((unsigned)routes), dim3(64), 0, as_stream(stream), (const T*)hidden,
-                       hidden_dim, hidden_row_stride, (const T*)routing_weights, sorted_route_idx, top_k,
-                       (T*)compact_hidden, (T*)compact_weights);
+    ANNA_DISPATCH_DTYPE(weights_dtype, WDT, {
+      using T = typename Elem<HDT>::T;
+      hipLaunchKernelGGL((moe_gather_kernel<HDT, WDT>), dim3((unsigned)routes), dim3(64), 0, as_stream(stream),
+                         (const T*)hidden, hidden_dim, hidden_row_stride, (const typename Elem<WDT>::T*)routing_weights,
+                         sorted_route_idx, top_k, (T*)compact_hidden, (T*)compact_weights);
+    });
   });
   ANNA_LAUNCH_CHECK("moe_gather_kernel");
   return ANNA_MI_OK;

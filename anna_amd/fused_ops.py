@@ -609,6 +609,15 @@ def moe_route_small(router_logits, top_k, normalize_topk_prob, slots):
     return w, sel, usage, offsets, sti, sri, route_pos, items
 
 
+def _weights_for_gather(routing_weights):
+    """Routing weights as the gather reads them: bf16 / fp16 / fp32 as given (the kernel rounds
+    them to the hidden dtype, no separate cast launch), other dtypes via fp32."""
+    rw = routing_weights
+    if rw.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        rw = rw.float()
+    return rw.contiguous()
+
+
 def moe_gather(hidden_states, routing_weights, sorted_route_idx, top_k):
     """The gathering half of moe_dispatch: (compact_hidden [R,H], compact_routing_weights [R,1])
     for routes already ordered by moe_route_small."""
@@ -616,12 +625,12 @@ def moe_gather(hidden_states, routing_weights, sorted_route_idx, top_k):
         raise RuntimeError("moe_gather: expected hidden [T,H] and routing_weights [T,k]")
     _check_same_device("moe_gather", hidden_states, routing_weights, sorted_route_idx)
     hs = hidden_states if hidden_states.stride(1) == 1 else hidden_states.contiguous()
-    rw = routing_weights.to(hs.dtype).contiguous()
+    rw = _weights_for_gather(routing_weights)
     r, h = sorted_route_idx.numel(), hs.shape[1]
     compact = torch.empty((r, h), dtype=hs.dtype, device=hs.device)
     cw = torch.empty((r, 1), dtype=hs.dtype, device=hs.device)
     _lib.call("anna_mi_moe_gather", hs.data_ptr(), _lib.dtype_code(hs.dtype), h, hs.stride(0), rw.data_ptr(),
-              sorted_route_idx.contiguous().data_ptr(), r, int(top_k), compact.data_ptr(), cw.data_ptr(),
+              _lib.dtype_code(rw.dtype), sorted_route_idx.contiguous().data_ptr(), r, int(top_k), compact.data_ptr(), cw.data_ptr(),
               _lib.stream_of(hs))
     return compact, cw
 
@@ -639,7 +648,7 @@ def moe_dispatch(hidden_states, routing_weights, selected_experts, expert_usage,
     k = routing_weights.shape[1]
     e = expert_usage.shape[0]
     hs = hidden_states if hidden_states.stride(1) == 1 else hidden_states.contiguous()
-    rw = routing_weights.to(hs.dtype).contiguous()
+    rw = _weights_for_gather(routing_weights)
     sel = selected_experts.contiguous()
     usage = expert_usage.contiguous()
     dev = hs.device
@@ -649,8 +658,8 @@ def moe_dispatch(hidden_states, routing_weights, selected_experts, expert_usage,
     compact = torch.empty((t * k, h), dtype=hs.dtype, device=dev)
     cw = torch.empty((t * k, 1), dtype=hs.dtype, device=dev)
     _lib.call("anna_mi_moe_dispatch", hs.data_ptr(), _lib.dtype_code(hs.dtype), t, h, hs.stride(0), rw.data_ptr(),
-              sel.data_ptr(), usage.data_ptr(), int(usage.dtype == torch.int64), e, k, sti.data_ptr(), sri.data_ptr(),
-              offsets.data_ptr(), compact.data_ptr(), cw.data_ptr(),
+              _lib.dtype_code(rw.dtype), sel.data_ptr(), usage.data_ptr(), int(usage.dtype == torch.int64), e, k,
+              sti.data_ptr(), sri.data_ptr(), offsets.data_ptr(), compact.data_ptr(), cw.data_ptr(),
               None if route_pos is None else route_pos.data_ptr(), _lib.stream_of(hs))
     return sti, offsets, compact, cw
 

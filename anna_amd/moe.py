@@ -94,8 +94,7 @@ class SparseMoeInt4:
         else:
             w, sel, usage = fused_ops.moe_router(router_logits, self.top_k, self.norm_topk_prob)
             route_pos = torch.empty((t * self.top_k,), dtype=torch.int64, device=hidden_states.device)
-            _, offsets, compact, cw = fused_ops.moe_dispatch(hidden_states, w.to(hidden_states.dtype), sel, usage,
-                                                              route_pos=route_pos)
+            _, offsets, compact, cw = fused_ops.moe_dispatch(hidden_states, w, sel, usage, route_pos=route_pos)
             # every expert is passed as active; the device lists the ones with routes (items)
             items = torch.empty((4 + 4 * self.num_experts,), dtype=torch.int32, device=hidden_states.device)
         compact_out = torch.empty_like(compact)

@@ -289,10 +289,12 @@ int anna_mi_moe_router(const void* logits, int logits_dtype, int64_t tokens, int
  * (prefix sum of usage, int32 or int64), routes sorted by (expert, token, k) -- the CPU
  * path's order, deterministic: sorted_token_idx / sorted_route_idx int64 [tokens*top_k];
  * compact_hidden [routes][hidden] and compact_weights [routes] in the hidden dtype
- * (routing_weights [tokens][top_k] contiguous, hidden dtype).  route_pos (optional, may be
- * NULL) receives the compact position of route t*top_k + j. */
+ * (routing_weights [tokens][top_k] contiguous, dtype weights_dtype: the router's fp32 weights
+ * are rounded to the hidden dtype here, as the reference's cast does).  route_pos (optional,
+ * may be NULL) receives the compact position of route t*top_k + j. */
 int anna_mi_moe_dispatch(const void* hidden, int dtype, int64_t tokens, int64_t hidden_dim,
-                         int64_t hidden_row_stride, const void* routing_weights, const int64_t* selected,
+                         int64_t hidden_row_stride, const void* routing_weights, int weights_dtype,
+                         const int64_t* selected,
                          const void* usage, int usage_is_int64, int64_t num_experts, int64_t top_k,
                          int64_t* sorted_token_idx, int64_t* sorted_route_idx, int64_t* expert_offsets,
                          void* compact_hidden, void* compact_weights, int64_t* route_pos, void* stream);
@@ -312,9 +314,10 @@ int anna_mi_moe_route_small(const void* logits, int logits_dtype, int64_t tokens
 
 /* The gathering half of moe_dispatch_fused (sycl:3867-3965): compact_hidden[p] =
  * hidden[sorted_route_idx[p] / top_k], compact_weights[p] = routing_weights[sorted_route_idx[p]]
- * (hidden dtype), after anna_mi_moe_route_small. */
+ * (rounded to the hidden dtype from weights_dtype), after anna_mi_moe_route_small. */
 int anna_mi_moe_gather(const void* hidden, int dtype, int64_t hidden_dim, int64_t hidden_row_stride,
-                       const void* routing_weights, const int64_t* sorted_route_idx, int64_t routes, int64_t top_k,
+                       const void* routing_weights, int weights_dtype, const int64_t* sorted_route_idx,
+                       int64_t routes, int64_t top_k,
                        void* compact_hidden, void* compact_weights, void* stream);
 
 /* moe_scatter_fused (sycl:3967-4037; CPU path ops.py:3359-3376): out[t] = sum of the compact
