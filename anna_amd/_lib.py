@@ -98,7 +98,8 @@ class MoeMlpArgs(ctypes.Structure):
 
 PROTOTYPES.update({
     "anna_mi_moe_router": [_P, _I, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _P],
-    "anna_mi_moe_dispatch": [_P, _I, _I64, _I64, _I64, _P, _I, _P, _P, _I, _I64, _I64, _P, _P, _P, _P, _P, _P, _P],
+    "anna_mi_moe_dispatch": [_P, _I, _I64, _I64, _I64, _P, _I, _P, _P, _I, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P,
+                             _P],
     "anna_mi_moe_route_small": [_P, _I, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P],
     "anna_mi_moe_gather": [_P, _I, _I64, _I64, _P, _I, _P, _I64, _I64, _P, _P, _P],
     "anna_mi_moe_scatter": [_P, _I, _I64, _I64, _P, _I64, _P, _P, _P],

@@ -220,26 +220,54 @@ __global__ void fill_i32_kernel(int32_t* p, int64_t n) {
 
 // ------------------------------------------------------------------ dispatch
 
+// With items (and slots) set, also the grouped MLP's list of experts with routes, as
+// moe_compact_items_kernel writes it: workgroup e counts the experts before it that have routes
+// (workgroup 0 counts all of them), so no separate launch builds the list.
 template <typename U>
 __global__ __launch_bounds__(256) void moe_order_kernel(const int64_t* __restrict__ selected, int64_t routes,
                                                         int64_t top_k, const U* __restrict__ usage, int64_t E,
                                                         int64_t* __restrict__ offsets, int64_t* __restrict__ sorted_token,
-                                                        int64_t* __restrict__ sorted_route, int64_t* __restrict__ route_pos) {
+                                                        int64_t* __restrict__ sorted_route, int64_t* __restrict__ route_pos,
+                                                        const int64_t* __restrict__ slots, int32_t* __restrict__ items) {
   __shared__ int64_t s_part[4];
+  __shared__ int s_act[4], s_all[4];
   __shared__ int s_cnt[4];
   const int64_t e = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int64_t part = 0;
-  for (int64_t i = threadIdx.x; i < e; i += blockDim.x) part += (int64_t)usage[i];
+  int act = 0, all = 0;  // experts with routes before e / in all (the latter for workgroup 0)
+  const int64_t lim = items && e == 0 ? E : e;
+  for (int64_t i = threadIdx.x; i < lim; i += blockDim.x) {
+    const int64_t u = (int64_t)usage[i];
+    if (i < e) {
+      part += u;
+      act += u > 0;
+    }
+    all += u > 0;
+  }
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off, 64);
-  if (lane == 0) s_part[wave] = part;
+  for (int off = 32; off >= 1; off >>= 1) {
+    part += __shfl_xor(part, off, 64);
+    act += __shfl_xor(act, off, 64);
+    all += __shfl_xor(all, off, 64);
+  }
+  if (lane == 0) {
+    s_part[wave] = part;
+    s_act[wave] = act;
+    s_all[wave] = all;
+  }
   __syncthreads();
   const int64_t base = s_part[0] + s_part[1] + s_part[2] + s_part[3];
   const int64_t cnt = (int64_t)usage[e];
   if (threadIdx.x == 0) {
     offsets[e + 1] = base + cnt;
     if (e == 0) offsets[0] = 0;
+    if (items) {
+      if (e == 0) items[0] = s_all[0] + s_all[1] + s_all[2] + s_all[3];
+      if (cnt > 0)
+        *(int4*)(items + 4 + 4 * (s_act[0] + s_act[1] + s_act[2] + s_act[3])) =
+            make_int4((int)slots[e], (int)base, (int)(base + cnt), 0);
+    }
   }
   if (cnt == 0) return;
   int64_t running = 0;
@@ -753,23 +781,26 @@ extern "C" int anna_mi_moe_dispatch(const void* hidden, int dtype, int64_t token
                                     const int64_t* selected,
                                     const void* usage, int usage_is_int64, int64_t num_experts, int64_t top_k,
                                     int64_t* sorted_token_idx, int64_t* sorted_route_idx, int64_t* expert_offsets,
-                                    void* compact_hidden, void* compact_weights, int64_t* route_pos, void* stream) {
+                                    void* compact_hidden, void* compact_weights, int64_t* route_pos,
+                                    const int64_t* slots, int32_t* items, void* stream) {
   ANNA_CHECK(selected && usage && sorted_token_idx && sorted_route_idx && expert_offsets && compact_hidden &&
                  compact_weights && (hidden || tokens == 0) && (routing_weights || tokens == 0),
              "anna_mi_moe_dispatch: null pointer");
   ANNA_CHECK(num_experts > 0 && top_k > 0 && hidden_dim > 0 && tokens >= 0 && hidden_row_stride >= hidden_dim,
              "anna_mi_moe_dispatch: bad shape");
   ANNA_CHECK(valid_dtype(dtype) && valid_dtype(weights_dtype), "anna_mi_moe_dispatch: bad dtype code");
+  ANNA_CHECK((items == nullptr) == (slots == nullptr), "anna_mi_moe_dispatch: items and slots go together");
+  ANNA_CHECK(num_experts < (1ll << 30) && tokens * top_k < (1ll << 31), "anna_mi_moe_dispatch: too many routes");
   hipStream_t st = as_stream(stream);
   const int64_t routes = tokens * top_k;
   if (usage_is_int64) {
     hipLaunchKernelGGL((moe_order_kernel<int64_t>), dim3((unsigned)num_experts), dim3(256), 0, st, selected, routes,
                        top_k, (const int64_t*)usage, num_experts, expert_offsets, sorted_token_idx, sorted_route_idx,
-                       route_pos);
+                       route_pos, slots, items);
   } else {
     hipLaunchKernelGGL((moe_order_kernel<int32_t>), dim3((unsigned)num_experts), dim3(256), 0, st, selected, routes,
                        top_k, (const int32_t*)usage, num_experts, expert_offsets, sorted_token_idx, sorted_route_idx,
-                       route_pos);
+                       route_pos, slots, items);
   }
   ANNA_LAUNCH_CHECK("moe_order_kernel");
   if (routes == 0) return ANNA_MI_OK;

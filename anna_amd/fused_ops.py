@@ -635,10 +635,12 @@ def moe_gather(hidden_states, routing_weights, sorted_route_idx, top_k):
     return compact, cw
 
 
-def moe_dispatch(hidden_states, routing_weights, selected_experts, expert_usage, *, route_pos=None):
+def moe_dispatch(hidden_states, routing_weights, selected_experts, expert_usage, *, route_pos=None, slots=None,
+                 items=None):
     """Returns (sorted_token_idx [R], expert_offsets [E+1], compact_hidden [R,H],
     compact_routing_weights [R,1]) with routes ordered by (expert, token, k)
-    (moe_dispatch_fused, sycl:3867-3965; order of ops.py:3301-3332)."""
+    (moe_dispatch_fused, sycl:3867-3965; order of ops.py:3301-3332).  With slots / items, also
+    writes the grouped MLP's list of experts with routes (items_prefilled for the MLP)."""
     if hidden_states.dim() != 2 or routing_weights.dim() != 2 or selected_experts.shape != routing_weights.shape:
         raise RuntimeError("moe_dispatch: expected hidden [T,H], routing_weights/selected_experts [T,k]")
     if selected_experts.dtype != torch.int64 or expert_usage.dtype not in (torch.int32, torch.int64):
@@ -647,6 +649,14 @@ def moe_dispatch(hidden_states, routing_weights, selected_experts, expert_usage,
     t, h = hidden_states.shape
     k = routing_weights.shape[1]
     e = expert_usage.shape[0]
+    if (slots is None) != (items is None):
+        raise RuntimeError("moe_dispatch: slots and items go together")
+    if items is not None:
+        if slots.dtype != torch.int64 or slots.numel() != e or not slots.is_contiguous():
+            raise RuntimeError("moe_dispatch: slots must be contiguous int64 [num_experts]")
+        if items.dtype != torch.int32 or items.numel() < 4 + 4 * e or not items.is_contiguous():
+            raise RuntimeError("moe_dispatch: items must be contiguous int32 [4 + 4 * num_experts]")
+        _check_same_device("moe_dispatch", hidden_states, slots, items)
     hs = hidden_states if hidden_states.stride(1) == 1 else hidden_states.contiguous()
     rw = _weights_for_gather(routing_weights)
     sel = selected_experts.contiguous()
@@ -660,7 +670,8 @@ def moe_dispatch(hidden_states, routing_weights, selected_experts, expert_usage,
     _lib.call("anna_mi_moe_dispatch", hs.data_ptr(), _lib.dtype_code(hs.dtype), t, h, hs.stride(0), rw.data_ptr(),
               _lib.dtype_code(rw.dtype), sel.data_ptr(), usage.data_ptr(), int(usage.dtype == torch.int64), e, k,
               sti.data_ptr(), sri.data_ptr(), offsets.data_ptr(), compact.data_ptr(), cw.data_ptr(),
-              None if route_pos is None else route_pos.data_ptr(), _lib.stream_of(hs))
+              None if route_pos is None else route_pos.data_ptr(), None if slots is None else slots.data_ptr(),
+              None if items is None else items.data_ptr(), _lib.stream_of(hs))
     return sti, offsets, compact, cw
 
 

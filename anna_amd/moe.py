@@ -94,16 +94,17 @@ class SparseMoeInt4:
         else:
             w, sel, usage = fused_ops.moe_router(router_logits, self.top_k, self.norm_topk_prob)
             route_pos = torch.empty((t * self.top_k,), dtype=torch.int64, device=hidden_states.device)
-            _, offsets, compact, cw = fused_ops.moe_dispatch(hidden_states, w, sel, usage, route_pos=route_pos)
-            # every expert is passed as active; the device lists the ones with routes (items)
+            # every expert is passed as active; the dispatch lists the ones with routes (items)
             items = torch.empty((4 + 4 * self.num_experts,), dtype=torch.int32, device=hidden_states.device)
+            _, offsets, compact, cw = fused_ops.moe_dispatch(hidden_states, w, sel, usage, route_pos=route_pos,
+                                                              slots=self.active_slots, items=items)
         compact_out = torch.empty_like(compact)
         # Routes per expert are only known on the device; the kernels sweep an expert's routes in
         # as many passes as it needs, so this hint (twice the mean load) only sizes the sweep.
         hint = min(t * self.top_k, 2 * -(-t * self.top_k // self.num_experts) + 8)
         fused_ops.moe_grouped_int4_mlp_out(compact, cw, compact_out, offsets, self.active_experts, self.active_slots,
                                            *self.bank.tensors(), self.bank.group_size, max(1, hint), items=items,
-                                           items_prefilled=small)
+                                           items_prefilled=True)
         return fused_ops.moe_combine(compact_out, route_pos, t, self.top_k)
 
     __call__ = forward

@@ -291,13 +291,17 @@ int anna_mi_moe_router(const void* logits, int logits_dtype, int64_t tokens, int
  * compact_hidden [routes][hidden] and compact_weights [routes] in the hidden dtype
  * (routing_weights [tokens][top_k] contiguous, dtype weights_dtype: the router's fp32 weights
  * are rounded to the hidden dtype here, as the reference's cast does).  route_pos (optional,
- * may be NULL) receives the compact position of route t*top_k + j. */
+ * may be NULL) receives the compact position of route t*top_k + j.  items and slots (optional,
+ * both or neither): the grouped MLP's list of experts with routes (see
+ * anna_mi_moe_mlp_args.items) for bank slots slots[e] [E], written here so that the MLP can
+ * take it prefilled. */
 int anna_mi_moe_dispatch(const void* hidden, int dtype, int64_t tokens, int64_t hidden_dim,
                          int64_t hidden_row_stride, const void* routing_weights, int weights_dtype,
                          const int64_t* selected,
                          const void* usage, int usage_is_int64, int64_t num_experts, int64_t top_k,
                          int64_t* sorted_token_idx, int64_t* sorted_route_idx, int64_t* expert_offsets,
-                         void* compact_hidden, void* compact_weights, int64_t* route_pos, void* stream);
+                         void* compact_hidden, void* compact_weights, int64_t* route_pos, const int64_t* slots,
+                         int32_t* items, void* stream);
 
 /* No single counterpart in the reference: moe_router_fused (sycl:3731-3865) followed by the
  * ordering half of moe_dispatch_fused (sycl:3867-3965), for small batches (tokens * top_k <=

@@ -157,6 +157,16 @@ def test_route_small_matches_router_and_dispatch(gpu, tokens, experts, top_k, ld
     assert int(it[0]) == len(have)
     for j, e in enumerate(have):
         assert [int(v) for v in it[4 + 4 * j: 7 + 4 * j]] == [int(sl[e]), int(offc[e]), int(offc[e + 1])]
+    # the dispatch writes the same list when given the slots, and takes the router's fp32
+    # weights directly (rounded to bf16 in the gather, as the cast above did)
+    items_d = torch.full((4 + 4 * experts,), -1, dtype=torch.int32, device=gpu)
+    rp3 = torch.empty_like(route_pos)
+    sti3, off3, compact3, cw3 = fused_ops.moe_dispatch(hidden, w, sel, usage, route_pos=rp3, slots=slots, items=items_d)
+    assert torch.equal(sti, sti3) and torch.equal(off, off3) and torch.equal(route_pos, rp3)
+    assert torch.equal(compact, compact3) and torch.equal(cw, cw3)
+    n = 4 + 4 * len(have)
+    assert int(items_d[0]) == len(have)
+    assert torch.equal(items_d[4:n].reshape(-1, 4)[:, :3].cpu(), it[4:n].reshape(-1, 4)[:, :3])
 
 
 def test_scatter_and_combine(gpu):
