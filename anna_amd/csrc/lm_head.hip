@@ -10,9 +10,11 @@
 //                           each word is one T x 4-byte coalesced load (8 k of T rows) used
 //                           against 8 activations of up to MR rows; fp32 accumulation
 //                           (s * (sum x q - z sum x) per word), wave reduction at the end.
-//   topk_rows_kernel        per row: 128 threads keep sorted top-k lists of their strided share
-//                           of the logits, merged pairwise in LDS (descending, ties to the
-//                           lower index).
+//   topk_rows_kernel        per row: up to 1024 threads keep sorted top-k lists of their strided
+//                           share of the logits, merged pairwise in LDS (descending, ties to
+//                           the lower index).
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace anna {
@@ -61,7 +63,74 @@ __global__ __launch_bounds__(256) void int4_gemv_tiled_kernel(
     for (int m = 0; m < TG_MR; ++m)
 #pragma unroll
       for (int t = 0; t < T; ++t) acc[m][t] = 0.f;
-    for (int64_t w = lane; w < words; w += 64) {
+    bool fast = false;
+    if constexpr (XDT != ANNA_MI_F32) {
+      if (vec_x) {
+        // Words w and w + 64 of the lane alternate between two register sets: the loads of the
+        // next word (weights, raw scales and zero points, x) are issued before the current one
+        // is used, pinned there by a scheduling barrier (converted right at their loads, each
+        // word cost a full round trip)
+        using ST = typename Elem<SDT>::T;
+        struct Word {
+          TileWords<T> q;
+          ST s[T];
+          int8_t z[T];
+          u32x4 x[TG_MR];
+        };
+        auto load = [&](int64_t w, Word& D) {
+          D.q = load_tile_words<T>(tw + w * T);
+          const int64_t g = (w * 8) / gsz;
+#pragma unroll
+          for (int t = 0; t < T; ++t) {
+            const int64_t n = tile * T + t;
+            const int64_t nc = n < N ? n : 0;
+            D.s[t] = qs[g * ss_g + nc * ss_n];
+            D.z[t] = qz[g * ss_g + nc * ss_n];
+          }
+#pragma unroll
+          for (int m = 0; m < TG_MR; ++m) {
+            const int64_t mr = m0 + m < M ? m0 + m : m0;
+            D.x[m] = *(const u32x4*)((const uint16_t*)x + mr * xs + w * 8);
+          }
+        };
+        auto compute = [&](const Word& D) {
+#pragma unroll
+          for (int m = 0; m < TG_MR; ++m) {
+            if (m0 + m >= M) continue;
+            float xv[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              xv[2 * e] = Elem<XDT>::to_f32((uint16_t)(D.x[m][e] & 0xFFFFu));
+              xv[2 * e + 1] = Elem<XDT>::to_f32((uint16_t)(D.x[m][e] >> 16));
+            }
+            float sx = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sx += xv[e];
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+              float d = 0.f;
+#pragma unroll
+              for (int e = 0; e < 8; ++e) d = fmaf(xv[e], (float)((D.q.v[t] >> (4 * e)) & 0xFu), d);
+              acc[m][t] = fmaf(Elem<SDT>::to_f32(D.s[t]), d - (float)D.z[t] * sx, acc[m][t]);
+            }
+          }
+        };
+        Word A, B;
+        int64_t w = lane;
+        if (w < words) load(w, A);
+        for (; w < words; w += 128) {
+          if (w + 64 < words) load(w + 64, B);
+          __builtin_amdgcn_sched_barrier(0);
+          compute(A);
+          if (w + 64 >= words) break;
+          if (w + 128 < words) load(w + 128, A);
+          __builtin_amdgcn_sched_barrier(0);
+          compute(B);
+        }
+        fast = true;
+      }
+    }
+    for (int64_t w = lane; !fast && w < words; w += 64) {
       const TileWords<T> q = load_tile_words<T>(tw + w * T);
       const int64_t k0 = w * 8;
       const int64_t g = k0 / gsz;
@@ -124,57 +193,226 @@ __global__ __launch_bounds__(256) void int4_gemv_tiled_kernel(
 
 // ------------------------------------------------------------------ top-k
 
-constexpr int TK_THREADS = 128;
-constexpr int TK_MAX = 32;  // top_k handled per call (larger k: error)
+constexpr int TK_MAX = 32;         // top_k handled per call (larger k: error)
+constexpr int TK_LDS = 64 * 1024;  // bytes of the per-thread lists (value + index, KT each)
+constexpr int TK_BATCH = 16;       // values one thread loads before it looks at any
 
 __device__ __forceinline__ bool tk_better(float va, int32_t ia, float vb, int32_t ib) {
   return va > vb || (va == vb && ia < ib);
 }
 
-// grid (rows), 128 threads.  The values are fp32 [rows][ld]; out values in ODT.
-template <int ODT>
-__global__ __launch_bounds__(TK_THREADS) void topk_rows_kernel(const float* __restrict__ logits, int64_t V, int64_t ld,
-                                                              int k, typename Elem<ODT>::T* __restrict__ out_v,
-                                                              int64_t* __restrict__ out_i) {
-  __shared__ float s_v[TK_THREADS][TK_MAX];
-  __shared__ int32_t s_i[TK_THREADS][TK_MAX];
-  const int tid = threadIdx.x;
+// compare-exchange: (a) ends up the better of the two
+__device__ __forceinline__ void tk_ce(float& va, int32_t& ia, float& vb, int32_t& ib) {
+  if (tk_better(vb, ib, va, ia)) {
+    const float tv = va;
+    const int32_t ti = ia;
+    va = vb, ia = ib, vb = tv, ib = ti;
+  }
+}
+
+// Threads per row for register lists of KT entries: the most (a power of two, <= 1024) whose
+// lists fit TK_LDS.
+inline int tk_threads(int kt) { return TK_LDS / (kt * 8) < 1024 ? TK_LDS / (kt * 8) : 1024; }
+
+// k <= 8 (KT = 8).  grid (rows), tk_threads(KT) threads, dynamic LDS nt * KT * 8 bytes.  The values are fp32
+// [rows][ld]; out values in ODT.  Order: descending, ties to the lower index (a strict total
+// order, so the networks below give exactly the sorted top-k).
+//   bound  a first pass finds each thread's best; the k-th best of those bounds the answer;
+//   scan   each thread keeps the KT best of its strided share that pass the bound, sorted in
+//          registers (a new entry replaces the last and bubbles up: static indices, no LDS),
+//          loading TK_BATCH values before it compares any;
+//   merge  pairwise tree over the threads' lists through LDS: a thread reads its partner's list
+//          (independent loads), keeps the better of A[i] and B[KT-1-i] (the top half of the
+//          bitonic A ++ reverse(B)) and sorts that half with a bitonic network, in registers.
+// The earlier form (lists in LDS, a two-pointer merge) spent its time in chains of dependent
+// LDS reads: 24 us at V = 31, 240 us at V = 151936.
+template <int ODT, int KT>
+__global__ __launch_bounds__(1024) void topk_rows_kernel(const float* __restrict__ logits, int64_t V, int64_t ld,
+                                                         int k, typename Elem<ODT>::T* __restrict__ out_v,
+                                                         int64_t* __restrict__ out_i) {
+  extern __shared__ float tk_lists[];  // values [nt][KT], then indices [nt][KT]
+  const int nt = blockDim.x, tid = threadIdx.x;
   const int64_t row = blockIdx.x;
   const float* lg = logits + row * ld;
-  // thread-local sorted list in LDS (descending; ties to the lower index)
-  float* lv = s_v[tid];
-  int32_t* li = s_i[tid];
-  for (int j = 0; j < k; ++j) lv[j] = -INFINITY, li[j] = INT32_MAX;
-  for (int32_t n = tid; n < V; n += TK_THREADS) {
-    const float v = lg[n];
-    if (!tk_better(v, n, lv[k - 1], li[k - 1])) continue;
-    int j = k - 1;
-    while (j > 0 && tk_better(v, n, lv[j - 1], li[j - 1])) {
-      lv[j] = lv[j - 1], li[j] = li[j - 1];
-      --j;
-    }
-    lv[j] = v, li[j] = n;
-  }
-  __syncthreads();
-  // pairwise merge: list tid += list tid + half
-  for (int half = TK_THREADS / 2; half >= 1; half >>= 1) {
-    if (tid < half) {
-      float mv[TK_MAX];
-      int32_t mi[TK_MAX];
-      const float* bv = s_v[tid + half];
-      const int32_t* bi = s_i[tid + half];
-      int a = 0, b = 0;
-      for (int j = 0; j < k; ++j) {
-        if (tk_better(lv[a], li[a], bv[b], bi[b])) mv[j] = lv[a], mi[j] = li[a], ++a;
-        else mv[j] = bv[b], mi[j] = bi[b], ++b;
-      }
-      for (int j = 0; j < k; ++j) lv[j] = mv[j], li[j] = mi[j];
-    }
+  float* lv = tk_lists;
+  int32_t* li = (int32_t*)(tk_lists + nt * KT);
+  float rv[KT];
+  int32_t ri[KT];
+  auto clear = [&]() {
+#pragma unroll
+    for (int j = 0; j < KT; ++j) rv[j] = -INFINITY, ri[j] = INT32_MAX;
+  };
+  // the threads' register lists -> thread 0's list (in LDS too) holds the best KT of them all
+  auto merge_tree = [&]() {
+#pragma unroll
+    for (int j = 0; j < KT; ++j) lv[tid * KT + j] = rv[j], li[tid * KT + j] = ri[j];
     __syncthreads();
+    for (int half = nt / 2; half >= 1; half >>= 1) {
+      if (tid < half) {
+        float bv[KT];
+        int32_t bi[KT];
+#pragma unroll
+        for (int j = 0; j < KT; ++j) bv[j] = lv[(tid + half) * KT + j], bi[j] = li[(tid + half) * KT + j];
+#pragma unroll
+        for (int j = 0; j < KT; ++j) {
+          if (tk_better(bv[KT - 1 - j], bi[KT - 1 - j], rv[j], ri[j])) rv[j] = bv[KT - 1 - j], ri[j] = bi[KT - 1 - j];
+        }
+#pragma unroll
+        for (int s = KT / 2; s >= 1; s >>= 1)
+#pragma unroll
+          for (int j = 0; j < KT; ++j)
+            if ((j & s) == 0) tk_ce(rv[j], ri[j], rv[j + s], ri[j + s]);
+#pragma unroll
+        for (int j = 0; j < KT; ++j) lv[tid * KT + j] = rv[j], li[tid * KT + j] = ri[j];
+      }
+      __syncthreads();
+    }
+  };
+  // pass 1: the k-th best of the threads' maxima bounds the row's k-th best from below (k
+  // distinct elements are at least as good), so pass 2 skips everything worse than it and its
+  // lists rarely change (a wave whose lanes insert often walks the insertion for all of them)
+  float mxv = -INFINITY;
+  int32_t mxi = INT32_MAX;
+  for (int64_t n0 = tid; n0 < V; n0 += (int64_t)TK_BATCH * nt) {
+    float v[TK_BATCH];
+#pragma unroll
+    for (int b = 0; b < TK_BATCH; ++b) {
+      const int64_t n = n0 + (int64_t)b * nt;
+      v[b] = lg[n < V ? n : 0];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int b = 0; b < TK_BATCH; ++b) {
+      const int64_t n = n0 + (int64_t)b * nt;
+      if (n < V && tk_better(v[b], (int32_t)n, mxv, mxi)) mxv = v[b], mxi = (int32_t)n;
+    }
   }
-  if (tid < k) {
-    out_v[row * k + tid] = Elem<ODT>::cvt(s_v[0][tid]);
-    out_i[row * k + tid] = s_i[0][tid];
+  clear();
+  rv[0] = mxv, ri[0] = mxi;
+  merge_tree();
+  const float tau_v = lv[k - 1];
+  const int32_t tau_i = li[k - 1];
+  __syncthreads();  // everyone has read the bound before the lists are rewritten
+  // pass 2: each thread keeps the KT best of its share that are not worse than the bound,
+  // sorted in registers (a new entry replaces the last and bubbles up)
+  clear();
+  for (int64_t n0 = tid; n0 < V; n0 += (int64_t)TK_BATCH * nt) {
+    float v[TK_BATCH];
+#pragma unroll
+    for (int b = 0; b < TK_BATCH; ++b) {
+      const int64_t n = n0 + (int64_t)b * nt;
+      v[b] = lg[n < V ? n : 0];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int b = 0; b < TK_BATCH; ++b) {
+      const int64_t n = n0 + (int64_t)b * nt;
+      if (n >= V || tk_better(tau_v, tau_i, v[b], (int32_t)n) || !tk_better(v[b], (int32_t)n, rv[KT - 1], ri[KT - 1]))
+        continue;
+      rv[KT - 1] = v[b], ri[KT - 1] = (int32_t)n;
+#pragma unroll
+      for (int j = KT - 1; j >= 1; --j) tk_ce(rv[j - 1], ri[j - 1], rv[j], ri[j]);
+    }
+  }
+  merge_tree();
+  if (tid < k) {  // the merged list is thread 0's
+    out_v[row * k + tid] = Elem<ODT>::cvt(lv[tid]);
+    out_i[row * k + tid] = li[tid];
+  }
+}
+
+// k > 8: the lists stay in LDS (a register list of 16 or 32 entries and its partner spill), with
+// the same bound, batched loads and a register copy of the list's last entry; merged pairwise
+// with a two-pointer merge into registers (loops over the compile-time TK_MAX keep them there).
+template <int ODT>
+__global__ __launch_bounds__(1024) void topk_rows_lds_kernel(const float* __restrict__ logits, int64_t V, int64_t ld,
+                                                             int k, typename Elem<ODT>::T* __restrict__ out_v,
+                                                             int64_t* __restrict__ out_i) {
+  extern __shared__ float tk_lists[];  // values [nt][k], then indices [nt][k]
+  const int nt = blockDim.x, tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const float* lg = logits + row * ld;
+  float* lv = tk_lists + tid * k;
+  int32_t* li = (int32_t*)(tk_lists + nt * k) + tid * k;
+  auto clear = [&]() {
+    for (int j = 0; j < k; ++j) lv[j] = -INFINITY, li[j] = INT32_MAX;
+  };
+  // thread 0's list becomes the best k of all lists
+  auto merge_tree = [&]() {
+    __syncthreads();
+    for (int half = nt / 2; half >= 1; half >>= 1) {
+      if (tid < half) {
+        float mv[TK_MAX];
+        int32_t mi[TK_MAX];
+        const float* bv = tk_lists + (tid + half) * k;
+        const int32_t* bi = (const int32_t*)(tk_lists + nt * k) + (tid + half) * k;
+        int a = 0, b = 0;
+#pragma unroll
+        for (int j = 0; j < TK_MAX; ++j) {
+          if (j < k) {
+            if (tk_better(lv[a], li[a], bv[b], bi[b])) mv[j] = lv[a], mi[j] = li[a], ++a;
+            else mv[j] = bv[b], mi[j] = bi[b], ++b;
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < TK_MAX; ++j)
+          if (j < k) lv[j] = mv[j], li[j] = mi[j];
+      }
+      __syncthreads();
+    }
+  };
+  // pass 1: the bound (the k-th best of the threads' maxima), as in topk_rows_kernel
+  float mxv = -INFINITY;
+  int32_t mxi = INT32_MAX;
+  for (int64_t n0 = tid; n0 < V; n0 += (int64_t)TK_BATCH * nt) {
+    float v[TK_BATCH];
+#pragma unroll
+    for (int b = 0; b < TK_BATCH; ++b) {
+      const int64_t n = n0 + (int64_t)b * nt;
+      v[b] = lg[n < V ? n : 0];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int b = 0; b < TK_BATCH; ++b) {
+      const int64_t n = n0 + (int64_t)b * nt;
+      if (n < V && tk_better(v[b], (int32_t)n, mxv, mxi)) mxv = v[b], mxi = (int32_t)n;
+    }
+  }
+  clear();
+  lv[0] = mxv, li[0] = mxi;
+  merge_tree();
+  const float tau_v = tk_lists[k - 1];
+  const int32_t tau_i = ((const int32_t*)(tk_lists + nt * k))[k - 1];
+  __syncthreads();
+  // pass 2: the elements not worse than the bound, into the thread's sorted LDS list
+  clear();
+  float last_v = -INFINITY;
+  int32_t last_i = INT32_MAX;
+  for (int64_t n0 = tid; n0 < V; n0 += (int64_t)TK_BATCH * nt) {
+    float v[TK_BATCH];
+#pragma unroll
+    for (int b = 0; b < TK_BATCH; ++b) {
+      const int64_t n = n0 + (int64_t)b * nt;
+      v[b] = lg[n < V ? n : 0];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int b = 0; b < TK_BATCH; ++b) {
+      const int64_t n = n0 + (int64_t)b * nt;
+      if (n >= V || tk_better(tau_v, tau_i, v[b], (int32_t)n) || !tk_better(v[b], (int32_t)n, last_v, last_i)) continue;
+      int j = k - 1;
+      while (j > 0 && tk_better(v[b], (int32_t)n, lv[j - 1], li[j - 1])) {
+        lv[j] = lv[j - 1], li[j] = li[j - 1];
+        --j;
+      }
+      lv[j] = v[b], li[j] = (int32_t)n;
+      last_v = lv[k - 1], last_i = li[k - 1];
+    }
+  }
+  merge_tree();
+  if (tid < k) {  // the merged list is thread 0's
+    out_v[row * k + tid] = Elem<ODT>::cvt(tk_lists[tid]);
+    out_i[row * k + tid] = ((const int32_t*)(tk_lists + nt * k))[tid];
   }
 }
 
@@ -246,8 +484,16 @@ extern "C" int anna_mi_topk_rows(const float* values, int64_t rows, int64_t V, i
   ANNA_CHECK(rows >= 0 && ld >= V && V < INT32_MAX, "anna_mi_topk_rows: bad shape");
   if (rows == 0) return ANNA_MI_OK;
   ANNA_DISPATCH_DTYPE(out_dtype, ODT, {
-    hipLaunchKernelGGL((topk_rows_kernel<ODT>), dim3((unsigned)rows), dim3(TK_THREADS), 0, as_stream(stream), values, V,
-                       ld, (int)top_k, (typename Elem<ODT>::T*)out_values, out_indices);
+    if (top_k <= 8) {
+      const int nt = tk_threads(8);
+      hipLaunchKernelGGL((topk_rows_kernel<ODT, 8>), dim3((unsigned)rows), dim3((unsigned)nt), (size_t)nt * 8 * 8,
+                         as_stream(stream), values, V, ld, (int)top_k, (typename Elem<ODT>::T*)out_values, out_indices);
+    } else {
+      int nt = 1024;
+      while (nt > 64 && (int64_t)nt * top_k * 8 > TK_LDS) nt >>= 1;
+      hipLaunchKernelGGL((topk_rows_lds_kernel<ODT>), dim3((unsigned)rows), dim3((unsigned)nt), (size_t)nt * top_k * 8,
+                         as_stream(stream), values, V, ld, (int)top_k, (typename Elem<ODT>::T*)out_values, out_indices);
+    }
   });
   ANNA_LAUNCH_CHECK("topk_rows_kernel");
   return ANNA_MI_OK;

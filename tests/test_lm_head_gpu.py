@@ -76,3 +76,23 @@ def test_lm_head_topk_errors(gpu):
     with pytest.raises(RuntimeError, match="in_features"):
         fused_ops.run_lm_head_int4_topk_fused(hidden_states=x, qweight=q.qweight, qscale=q.qscale, qzeros=q.qzeros,
                                               group_size=32, in_features=8, top_k=3)
+
+
+@pytest.mark.parametrize("v,rows,k", [(31, 1, 5), (5000, 3, 8), (20000, 2, 16), (3000, 1, 32), (40, 2, 32)])
+def test_topk_rows_exact_with_ties(gpu, v, rows, k):
+    """The row top-k (both kernels: k <= 8 in registers, k > 8 in LDS) against a CPU sort by
+    (value descending, index ascending), with many exact ties."""
+    from anna_amd import _lib
+    print(f"[case] topk_rows V={v} rows={rows} k={k}", flush=True)
+    g = torch.Generator().manual_seed(v + k)
+    vals = torch.randn(rows, v, generator=g)
+    vals[:, ::7] = vals[:, :1]  # every 7th value ties with the first
+    dev_vals = vals.to(gpu)
+    out_v = torch.empty((rows, k), dtype=torch.float32, device=gpu)
+    out_i = torch.empty((rows, k), dtype=torch.int64, device=gpu)
+    _lib.call("anna_mi_topk_rows", dev_vals.data_ptr(), rows, v, v, k, out_v.data_ptr(), _lib.dtype_code(torch.float32),
+              out_i.data_ptr(), _lib.stream_of(dev_vals))
+    for r in range(rows):
+        order = sorted(range(v), key=lambda i: (-float(vals[r, i]), i))[:k]
+        assert out_i[r].cpu().tolist() == order
+        assert torch.equal(out_v[r].cpu(), vals[r, order])
