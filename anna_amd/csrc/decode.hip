@@ -18,11 +18,29 @@ namespace anna {
 namespace {
 
 constexpr int DEC_WAVES = 4;
+constexpr int MERGE_CHUNK = 1024;  // block weights staged in LDS per pass of the merge
 
 __device__ __forceinline__ float ldv(const void* p, int64_t i, int dt) {
   if (dt == ANNA_MI_BF16) return bf16_bits_to_f32(((const uint16_t*)p)[i]);
   if (dt == ANNA_MI_F16) return f16_bits_to_f32(((const uint16_t*)p)[i]);
   return ((const float*)p)[i];
+}
+
+// Compile-time-dtype load: the hot loop's loads carry no branch, so they can all be in flight.
+template <int DT>
+__device__ __forceinline__ float ldt(const void* p, int64_t i) {
+  if constexpr (DT == ANNA_MI_BF16) return bf16_bits_to_f32(((const uint16_t*)p)[i]);
+  else if constexpr (DT == ANNA_MI_F16) return f16_bits_to_f32(((const uint16_t*)p)[i]);
+  else return ((const float*)p)[i];
+}
+
+// v_mov_b32 with a DPP lane pattern (all rows and banks enabled).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_f32(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
 __device__ __forceinline__ void stv(const void* p, int64_t i, int dt, float v) {
@@ -48,7 +66,7 @@ __global__ __launch_bounds__(1024) void decode_rotate_query_kernel(const anna_mi
   a.query_rot[(b * a.q_heads + h) * D + i] = acc;
 }
 
-template <int KF, int VF, int DPL, int GM>  // GM: max q-heads per KV group held in registers
+template <int KF, int VF, int DPL, int GM, int DT>  // GM: max q-heads per KV group held in registers; DT: activation dtype
 __global__ __launch_bounds__(64 * DEC_WAVES) void decode_split_kernel(const anna_mi_decode_args a, const Split sp) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t blk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
@@ -98,82 +116,149 @@ __global__ __launch_bounds__(64 * DEC_WAVES) void decode_split_kernel(const anna
 
   const int ksb = sbits(a.key_bits), kper = 8 / ksb;
   const int vsb = sbits(a.value_bits), vper = 8 / vsb;
-  for (int64_t t = t0 + wave; t < t1; t += DEC_WAVES) {
-    const bool res = t >= L1;
-    const int64_t tr = t - L1;
-    float kv[DPL], vv[DPL];
-    if (!res) {
+  // Per-lane element offsets within one token's row.  They do not depend on the token, so
+  // the divisions (packed codes per byte, scale group) are done once, outside the loop.
+  int64_t koff[DPL], voff[DPL], soff[DPL], zoff[DPL], rkoff[DPL], rvoff[DPL];
+  int kshift[DPL], vshift[DPL];
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) {
+    const int64_t d = lane * DPL + j;
+    if constexpr (KF == ANNA_MI_KEYS_TQ_MSE) {
+      koff[j] = (d / kper) * a.key.s3;
+      kshift[j] = ksb * (int)(d % kper);
+    } else {
+      koff[j] = d * a.key.s3;
+      kshift[j] = 0;
+    }
+    if constexpr (VF == ANNA_MI_VALUES_DENSE) {
+      voff[j] = d * a.value.s3;
+      vshift[j] = 0;
+    } else {
+      voff[j] = (d / vper) * a.value.s3;
+      vshift[j] = vsb * (int)(d % vper);
+    }
+    if constexpr (VF == ANNA_MI_VALUES_MINMAX) {
+      const int64_t g = d / a.value_group_size;
+      soff[j] = g * a.value_scales.s3;
+      zoff[j] = g * a.value_zeros.s3;
+    } else {
+      soff[j] = zoff[j] = 0;
+    }
+    rkoff[j] = d * a.residual_key.s3;
+    rvoff[j] = d * a.residual_value.s3;
+  }
+  const uint32_t kmask = (1u << ksb) - 1u, vmask = (1u << vsb) - 1u;
+  const float scale2 = a.scaling * 1.4426950408889634f;  // scores in log2 units
+  // Loads one token's K and V rows (dequantized) into registers: every load of the token is
+  // issued before any value is used.
+  auto load_packed = [&](int64_t t, float (&kv)[DPL], float (&vv)[DPL]) {
+    {
+      const int64_t kb = b * a.key.s0 + kvh * a.key.s1 + t * a.key.s2;
+      const int64_t vb = b * a.value.s0 + kvh * a.value.s1 + t * a.value.s2;
       if constexpr (KF == ANNA_MI_KEYS_TQ_MSE) {
-        const int64_t cb = b * a.key.s0 + kvh * a.key.s1 + t * a.key.s2;
         const float nk = f16_bits_to_f32(((const uint16_t*)a.key_norms.ptr)[b * a.key_norms.s0 + kvh * a.key_norms.s1 +
                                                                             t * a.key_norms.s2]);
+        uint32_t kc[DPL];
 #pragma unroll
-        for (int j = 0; j < DPL; ++j) {
-          const int64_t d = lane * DPL + j;
-          const uint32_t byte = ((const uint8_t*)a.key.ptr)[cb + (d / kper) * a.key.s3];
-          kv[j] = a.key_centroids[(byte >> (ksb * (d % kper))) & ((1u << ksb) - 1u)] * nk;
-        }
+        for (int j = 0; j < DPL; ++j) kc[j] = ((const uint8_t*)a.key.ptr)[kb + koff[j]];
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) kv[j] = a.key_centroids[(kc[j] >> kshift[j]) & kmask] * nk;
       } else {
 #pragma unroll
-        for (int j = 0; j < DPL; ++j)
-          kv[j] = ldv(a.key.ptr, b * a.key.s0 + kvh * a.key.s1 + t * a.key.s2 + (lane * DPL + j) * a.key.s3, dt);
+        for (int j = 0; j < DPL; ++j) kv[j] = ldt<DT>(a.key.ptr, kb + koff[j]);
       }
       if constexpr (VF == ANNA_MI_VALUES_DENSE) {
 #pragma unroll
-        for (int j = 0; j < DPL; ++j)
-          vv[j] = ldv(a.value.ptr, b * a.value.s0 + kvh * a.value.s1 + t * a.value.s2 + (lane * DPL + j) * a.value.s3, dt);
+        for (int j = 0; j < DPL; ++j) vv[j] = ldt<DT>(a.value.ptr, vb + voff[j]);
       } else if constexpr (VF == ANNA_MI_VALUES_MINMAX) {
-        const int64_t cb = b * a.value.s0 + kvh * a.value.s1 + t * a.value.s2;
         const int64_t sb0 = b * a.value_scales.s0 + kvh * a.value_scales.s1 + t * a.value_scales.s2;
         const int64_t zb0 = b * a.value_zeros.s0 + kvh * a.value_zeros.s1 + t * a.value_zeros.s2;
+        uint32_t vc[DPL];
+        float sc[DPL], zc[DPL];
 #pragma unroll
         for (int j = 0; j < DPL; ++j) {
-          const int64_t d = lane * DPL + j;
-          const uint32_t byte = ((const uint8_t*)a.value.ptr)[cb + (d / vper) * a.value.s3];
-          const uint32_t q = (byte >> (vsb * (d % vper))) & ((1u << vsb) - 1u);
-          const int64_t g = d / a.value_group_size;
-          vv[j] = (float)q * ldv(a.value_scales.ptr, sb0 + g * a.value_scales.s3, dt) +
-                  ldv(a.value_zeros.ptr, zb0 + g * a.value_zeros.s3, dt);
+          vc[j] = ((const uint8_t*)a.value.ptr)[vb + voff[j]];
+          sc[j] = ldt<DT>(a.value_scales.ptr, sb0 + soff[j]);
+          zc[j] = ldt<DT>(a.value_zeros.ptr, zb0 + zoff[j]);
         }
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) vv[j] = (float)((vc[j] >> vshift[j]) & vmask) * sc[j] + zc[j];
       } else {
-        const int64_t cb = b * a.value.s0 + kvh * a.value.s1 + t * a.value.s2;
         const float nv = f16_bits_to_f32(((const uint16_t*)a.value_scales.ptr)[b * a.value_scales.s0 +
                                                                                kvh * a.value_scales.s1 +
                                                                                t * a.value_scales.s2]);
+        uint32_t vc[DPL];
 #pragma unroll
-        for (int j = 0; j < DPL; ++j) {
-          const int64_t d = lane * DPL + j;
-          const uint32_t byte = ((const uint8_t*)a.value.ptr)[cb + (d / vper) * a.value.s3];
-          vv[j] = a.value_centroids[(byte >> (vsb * (d % vper))) & ((1u << vsb) - 1u)] * nv;
-        }
-      }
-    } else {
-      const anna_mi_view& rk = a.residual_key;
-      const anna_mi_view& rv = a.residual_value;
+        for (int j = 0; j < DPL; ++j) vc[j] = ((const uint8_t*)a.value.ptr)[vb + voff[j]];
 #pragma unroll
-      for (int j = 0; j < DPL; ++j) {
-        const int64_t d = lane * DPL + j;
-        kv[j] = ldv(rk.ptr, b * rk.s0 + kvh * rk.s1 + tr * rk.s2 + d * rk.s3, dt);
-        vv[j] = ldv(rv.ptr, b * rv.s0 + kvh * rv.s1 + tr * rv.s2 + d * rv.s3, dt);
+        for (int j = 0; j < DPL; ++j) vv[j] = a.value_centroids[(vc[j] >> vshift[j]) & vmask] * nv;
       }
     }
+  };
+  auto load_residual = [&](int64_t t, float (&kv)[DPL], float (&vv)[DPL]) {
+    {
+      const anna_mi_view& rk = a.residual_key;
+      const anna_mi_view& rv = a.residual_value;
+      const int64_t tr = t - L1;
+      const int64_t kb = b * rk.s0 + kvh * rk.s1 + tr * rk.s2, vb = b * rv.s0 + kvh * rv.s1 + tr * rv.s2;
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) {
+        kv[j] = ldt<DT>(rk.ptr, kb + rkoff[j]);
+        vv[j] = ldt<DT>(rv.ptr, vb + rvoff[j]);
+      }
+    }
+  };
+  // Online-softmax update of every q-head of the group with one token.
+  auto score_token = [&](const float (&kv)[DPL], const float (&vv)[DPL]) {
+    // Dot products reduced over the wave: DPP steps leave every 16-lane row holding its row
+    // sum, then the four row sums are read as scalars.  Scores are kept in log2 units
+    // (scaled by log2(e)) so the exponentials are single v_exp_f32 instructions.
+    float p[GM];
+#pragma unroll
+    for (int h = 0; h < GM; ++h) {
+      p[h] = 0.f;
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) p[h] = fmaf(qv[h][j], kv[j], p[h]);
+    }
+#pragma unroll
+    for (int h = 0; h < GM; ++h) p[h] += dpp_f32<0xB1>(p[h]);   // quad_perm [1,0,3,2]
+#pragma unroll
+    for (int h = 0; h < GM; ++h) p[h] += dpp_f32<0x4E>(p[h]);   // quad_perm [2,3,0,1]
+#pragma unroll
+    for (int h = 0; h < GM; ++h) p[h] += dpp_f32<0x141>(p[h]);  // row_half_mirror
+#pragma unroll
+    for (int h = 0; h < GM; ++h) p[h] += dpp_f32<0x140>(p[h]);  // row_mirror
 #pragma unroll
     for (int h = 0; h < GM; ++h) {
       if (h >= G) continue;
-      float p = 0.f;
-#pragma unroll
-      for (int j = 0; j < DPL; ++j)
-        p = fmaf(qv[h][j], kv[j], p);
-      const float s = wave_sum(p) * a.scaling;
+      const float tot = (lane_f32(p[h], 0) + lane_f32(p[h], 16)) + (lane_f32(p[h], 32) + lane_f32(p[h], 48));
+      const float s = tot * scale2;
       const float nm = fmaxf(m[h], s);
-      const float alpha = l[h] == 0.f ? 0.f : expf(m[h] - nm);
-      const float e = expf(s - nm);
+      const float alpha = l[h] == 0.f ? 0.f : __builtin_amdgcn_exp2f(m[h] - nm);
+      const float e = __builtin_amdgcn_exp2f(s - nm);
       l[h] = l[h] * alpha + e;
 #pragma unroll
       for (int j = 0; j < DPL; ++j) acc[h][j] = acc[h][j] * alpha + e * vv[j];
       m[h] = nm;
     }
-  }
+  };
+  // Wave w scores tokens t0 + w, t0 + w + 4, ... in ascending order.  The packed segment
+  // and the residual segment run as two loops so neither loop body branches on the segment;
+  // each step loads two tokens before scoring either.
+  auto sweep = [&](int64_t lo, int64_t hi, auto&& load) {
+    int64_t t = t0 + wave;
+    if (t < lo) t += (lo - t + DEC_WAVES - 1) / DEC_WAVES * DEC_WAVES;
+    for (; t < hi; t += 2 * DEC_WAVES) {
+      float kv0[DPL], vv0[DPL], kv1[DPL], vv1[DPL];
+      const bool two = t + DEC_WAVES < hi;
+      load(t, kv0, vv0);
+      load(two ? t + DEC_WAVES : t, kv1, vv1);  // unconditional: no branch between the loads
+      score_token(kv0, vv0);
+      if (two) score_token(kv1, vv1);
+    }
+  };
+  sweep(t0, t1 < L1 ? t1 : L1, load_packed);
+  sweep(t0 > L1 ? t0 : L1, t1, load_residual);
   // merge the 4 waves: common max, rescale, ordered sum in LDS
   if (lane == 0) {
 #pragma unroll
@@ -192,7 +277,7 @@ __global__ __launch_bounds__(64 * DEC_WAVES) void decode_split_kernel(const anna
         if (h >= G) continue;
         float M = -INFINITY;
         for (int w2 = 0; w2 < DEC_WAVES; ++w2) M = fmaxf(M, s_m[w2][h]);
-        const float f = l[h] == 0.f ? 0.f : expf(m[h] - M);
+        const float f = l[h] == 0.f ? 0.f : __builtin_amdgcn_exp2f(m[h] - M);
 #pragma unroll
         for (int j = 0; j < DPL; ++j) s_acc[h * D + lane * DPL + j] += acc[h][j] * f;
       }
@@ -210,10 +295,10 @@ __global__ __launch_bounds__(64 * DEC_WAVES) void decode_split_kernel(const anna
     float M = -INFINITY, S = 0.f;
     for (int w = 0; w < DEC_WAVES; ++w) M = fmaxf(M, s_m[w][h]);
     for (int w = 0; w < DEC_WAVES; ++w)
-      if (s_l[w][h] != 0.f) S += s_l[w][h] * expf(s_m[w][h] - M);
+      if (s_l[w][h] != 0.f) S += s_l[w][h] * __builtin_amdgcn_exp2f(s_m[w][h] - M);
     const anna_mi_view& ps = a.partial_stats;
     const int64_t base = b * ps.s0 + (kvh * G + h) * ps.s1 + blk * ps.s2;
-    ((float*)ps.ptr)[base] = M;
+    ((float*)ps.ptr)[base] = M * 0.6931471805599453f;  // back to natural-log units
     ((float*)ps.ptr)[base + ps.s3] = S;
   }
 }
@@ -249,25 +334,50 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const anna_mi_decode_
     __syncthreads();
   }
   const float denom = s_red[0];
-  float accr[4] = {0.f, 0.f, 0.f, 0.f};  // D <= 1024 -> at most 4 dims per thread
+  // Block weights exp(m_k - M) go through LDS a chunk at a time (0 for empty blocks); each
+  // thread then sums its dims over the chunk's blocks in ascending order, with the loads of
+  // several blocks in flight.
+  __shared__ float s_w[MERGE_CHUNK];
+  float accr[4] = {0.f, 0.f, 0.f, 0.f}, accq[4] = {0.f, 0.f, 0.f, 0.f};  // D <= 1024 -> at most 4 dims per thread
+  for (int64_t kc = 0; kc < nblk; kc += MERGE_CHUNK) {
+    const int64_t kn = nblk - kc < MERGE_CHUNK ? nblk - kc : MERGE_CHUNK;
+    for (int64_t k = threadIdx.x; k < kn; k += blockDim.x) {
+      const int64_t kk = kc + k;
+      const float dk = st[kk * ps.s2 + ps.s3];
+      s_w[k] = dk == 0.f ? 0.f : expf(st[kk * ps.s2] - M);
+    }
+    __syncthreads();
+    const int64_t kr = nrot - kc < 0 ? 0 : (nrot - kc < kn ? nrot - kc : kn);  // [0, kr) rotated blocks
+    for (int j = 0; j < 4; ++j) {
+      const int64_t d = threadIdx.x + (int64_t)j * blockDim.x;
+      if (d >= D) break;
+      const float* vd = va + kc * pv.s2 + d * pv.s3;
+      float ar = accr[j], aq = accq[j];
+#pragma unroll 8
+      for (int64_t k = 0; k < kr; ++k) {
+        const float w = s_w[k], v = vd[k * pv.s2];
+        ar = w != 0.f ? ar + w * v : ar;
+      }
+#pragma unroll 8
+      for (int64_t k = kr; k < kn; ++k) {
+        const float w = s_w[k], v = vd[k * pv.s2];
+        aq = w != 0.f ? aq + w * v : aq;
+      }
+      accr[j] = ar;
+      accq[j] = aq;
+    }
+    __syncthreads();
+  }
   for (int j = 0; j < 4; ++j) {
     const int64_t d = threadIdx.x + (int64_t)j * blockDim.x;
     if (d >= D) break;
-    float ar = 0.f, aq = 0.f;
-    for (int64_t k = 0; k < nblk; ++k) {
-      const float dk = st[k * ps.s2 + ps.s3];
-      if (dk == 0.f) continue;
-      const float c = expf(st[k * ps.s2] - M) * va[k * pv.s2 + d * pv.s3];
-      if (k < nrot) ar += c; else aq += c;
-    }
-    if (nrot > 0) s_rot[d] = ar;
-    accr[j] = aq;
+    if (nrot > 0) s_rot[d] = accr[j];
   }
   if (nrot > 0) __syncthreads();
   for (int j = 0; j < 4; ++j) {
     const int64_t d = threadIdx.x + (int64_t)j * blockDim.x;
     if (d >= D) break;
-    float o = accr[j];
+    float o = accq[j];
     if (nrot > 0) {
       float u = 0.f;
       for (int64_t i = 0; i < D; ++i) u = fmaf(a.rotation[i * D + d], s_rot[i], u);
@@ -306,13 +416,13 @@ int64_t total_blocks(const anna_mi_decode_args& a, const Split& sp) {
   return (L + sp.eb - 1) / sp.eb;
 }
 
-template <int KF, int VF>
-void launch_split(const anna_mi_decode_args& a, const Split& sp, int64_t nblk, hipStream_t st) {
+template <int KF, int VF, int DT>
+void launch_split_dt(const anna_mi_decode_args& a, const Split& sp, int64_t nblk, hipStream_t st) {
   dim3 grid((unsigned)nblk, (unsigned)a.kv_heads, (unsigned)a.batch);
   const int64_t G = a.q_heads / a.kv_heads;
   const size_t lds = (size_t)G * a.head_dim * 4;
   const dim3 blk(64 * DEC_WAVES);
-#define ANNA_SPLIT(DPL, GM) hipLaunchKernelGGL((decode_split_kernel<KF, VF, DPL, GM>), grid, blk, lds, st, a, sp)
+#define ANNA_SPLIT(DPL, GM) hipLaunchKernelGGL((decode_split_kernel<KF, VF, DPL, GM, DT>), grid, blk, lds, st, a, sp)
   const bool small = G <= 8;
   switch (a.head_dim) {
     case 64: if (small) ANNA_SPLIT(1, 8); else ANNA_SPLIT(1, 16); break;
@@ -321,6 +431,13 @@ void launch_split(const anna_mi_decode_args& a, const Split& sp, int64_t nblk, h
     default: ANNA_SPLIT(8, 8); break;
   }
 #undef ANNA_SPLIT
+}
+
+template <int KF, int VF>
+void launch_split(const anna_mi_decode_args& a, const Split& sp, int64_t nblk, hipStream_t st) {
+  if (a.dtype == ANNA_MI_BF16) launch_split_dt<KF, VF, ANNA_MI_BF16>(a, sp, nblk, st);
+  else if (a.dtype == ANNA_MI_F16) launch_split_dt<KF, VF, ANNA_MI_F16>(a, sp, nblk, st);
+  else launch_split_dt<KF, VF, ANNA_MI_F32>(a, sp, nblk, st);
 }
 
 }  // namespace
