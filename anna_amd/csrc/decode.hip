@@ -18,7 +18,9 @@ namespace anna {
 namespace {
 
 constexpr int DEC_WAVES = 4;
-constexpr int MERGE_CHUNK = 1024;  // block weights staged in LDS per pass of the merge
+constexpr int DEC_TOKENS = 4;  // tokens per wave whose loads are in flight together
+constexpr int MERGE_CHUNK = 1024;
+constexpr int MERGE_THREADS = 1024;  // merge workgroup: MERGE_THREADS / head_dim block slices per dim  // block weights staged in LDS per pass of the merge
 
 __device__ __forceinline__ float ldv(const void* p, int64_t i, int dt) {
   if (dt == ANNA_MI_BF16) return bf16_bits_to_f32(((const uint16_t*)p)[i]);
@@ -72,7 +74,6 @@ __global__ __launch_bounds__(64 * DEC_WAVES) void decode_split_kernel(const anna
   const int64_t blk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int G = (int)(a.q_heads / a.kv_heads);
   const int64_t D = a.head_dim, L1 = a.len1, L = a.len1 + a.len2;
-  const int dt = a.dtype;
 
   int64_t t0, t1;
   if (sp.aligned && blk >= sp.nb1) {
@@ -91,61 +92,71 @@ __global__ __launch_bounds__(64 * DEC_WAVES) void decode_split_kernel(const anna
   // With TQ-MSE keys blocks never straddle the segments: the whole block scores either
   // rotated codes (against q' = R q) or dense residual keys (against q).
   const bool rot_block = KF == ANNA_MI_KEYS_TQ_MSE && t0 < L1;
+  // All query loads are issued before any is used (heads beyond G read head G-1 and are
+  // then zeroed), so their latencies overlap.
   float qv[GM][DPL];
+  if (rot_block) {
+#pragma unroll
+    for (int h = 0; h < GM; ++h) {
+      const int64_t hq = kvh * G + (h < G ? h : G - 1);
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) qv[h][j] = a.query_rot[(b * a.q_heads + hq) * D + lane * DPL + j];
+    }
+  } else {
+#pragma unroll
+    for (int h = 0; h < GM; ++h) {
+      const int64_t hq = kvh * G + (h < G ? h : G - 1);
+#pragma unroll
+      for (int j = 0; j < DPL; ++j)
+        qv[h][j] = ldt<DT>(a.query.ptr, b * a.query.s0 + hq * a.query.s1 + (lane * DPL + j) * a.query.s3);
+    }
+  }
 #pragma unroll
   for (int h = 0; h < GM; ++h)
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) {
-      const int64_t d = lane * DPL + j;
-      const int64_t hq = kvh * G + h;
-      float v = 0.f;
-      if (h < G) {
-        v = rot_block ? a.query_rot[(b * a.q_heads + hq) * D + d]
-                      : ldv(a.query.ptr, b * a.query.s0 + hq * a.query.s1 + d * a.query.s3, dt);
-      }
-      qv[h][j] = v;
-    }
-  float m[GM], l[GM], acc[GM][DPL];
+    for (int j = 0; j < DPL; ++j)
+      if (h >= G) qv[h][j] = 0.f;
+  // Online-softmax state: lane L keeps the running max and denominator of head L % GM
+  // (log2 units); every lane keeps the accumulators of its dims for all heads.
+  float m_run = -INFINITY, l_run = 0.f, acc[GM][DPL];
 #pragma unroll
-  for (int h = 0; h < GM; ++h) {
-    m[h] = -INFINITY;
-    l[h] = 0.f;
+  for (int h = 0; h < GM; ++h)
 #pragma unroll
     for (int j = 0; j < DPL; ++j) acc[h][j] = 0.f;
-  }
 
   const int ksb = sbits(a.key_bits), kper = 8 / ksb;
   const int vsb = sbits(a.value_bits), vper = 8 / vsb;
   // Per-lane element offsets within one token's row.  They do not depend on the token, so
   // the divisions (packed codes per byte, scale group) are done once, outside the loop.
-  int64_t koff[DPL], voff[DPL], soff[DPL], zoff[DPL], rkoff[DPL], rvoff[DPL];
+  // 32-bit: the host checks head_dim * stride < 2^31 for every view read here.
+  int32_t koff[DPL], voff[DPL], soff[DPL], zoff[DPL], rkoff[DPL], rvoff[DPL];
   int kshift[DPL], vshift[DPL];
 #pragma unroll
   for (int j = 0; j < DPL; ++j) {
     const int64_t d = lane * DPL + j;
     if constexpr (KF == ANNA_MI_KEYS_TQ_MSE) {
-      koff[j] = (d / kper) * a.key.s3;
+      koff[j] = (int32_t)((d / kper) * a.key.s3);
       kshift[j] = ksb * (int)(d % kper);
     } else {
-      koff[j] = d * a.key.s3;
+      koff[j] = (int32_t)(d * a.key.s3);
       kshift[j] = 0;
     }
     if constexpr (VF == ANNA_MI_VALUES_DENSE) {
-      voff[j] = d * a.value.s3;
+      voff[j] = (int32_t)(d * a.value.s3);
       vshift[j] = 0;
     } else {
-      voff[j] = (d / vper) * a.value.s3;
+      voff[j] = (int32_t)((d / vper) * a.value.s3);
       vshift[j] = vsb * (int)(d % vper);
     }
     if constexpr (VF == ANNA_MI_VALUES_MINMAX) {
       const int64_t g = d / a.value_group_size;
-      soff[j] = g * a.value_scales.s3;
-      zoff[j] = g * a.value_zeros.s3;
+      soff[j] = (int32_t)(g * a.value_scales.s3);
+      zoff[j] = (int32_t)(g * a.value_zeros.s3);
     } else {
       soff[j] = zoff[j] = 0;
     }
-    rkoff[j] = d * a.residual_key.s3;
-    rvoff[j] = d * a.residual_value.s3;
+    rkoff[j] = (int32_t)(d * a.residual_key.s3);
+    rvoff[j] = (int32_t)(d * a.residual_value.s3);
   }
   const uint32_t kmask = (1u << ksb) - 1u, vmask = (1u << vsb) - 1u;
   const float scale2 = a.scaling * 1.4426950408889634f;  // scores in log2 units
@@ -208,65 +219,91 @@ __global__ __launch_bounds__(64 * DEC_WAVES) void decode_split_kernel(const anna
       }
     }
   };
-  // Online-softmax update of every q-head of the group with one token.
-  auto score_token = [&](const float (&kv)[DPL], const float (&vv)[DPL]) {
-    // Dot products reduced over the wave: DPP steps leave every 16-lane row holding its row
-    // sum, then the four row sums are read as scalars.  Scores are kept in log2 units
-    // (scaled by log2(e)) so the exponentials are single v_exp_f32 instructions.
-    float p[GM];
+  // Scores DEC_TOKENS tokens (token u valid when t + u * DEC_WAVES < hi) for every head.
+  // The NV = DEC_TOKENS * GM per-lane partial dot products are summed over the wave by a
+  // transposed butterfly: stage k exchanges across lane bit k and halves the list (a lane
+  // keeps the half selected by that bit), so after log2(NV) stages lane L holds the full dot
+  // product of value (L % NV) = u * GM + h.  The softmax update then runs one (u, h) per lane
+  // and the weights reach all lanes as scalars (readlane).
+  constexpr int NV = DEC_TOKENS * GM;
+  static_assert(NV == 32 || NV == 64, "butterfly sized for 32 or 64 values");
+  const int my_h = lane % GM, my_u = (lane / GM) % DEC_TOKENS;
+  auto score_step = [&](const float (&kv)[DEC_TOKENS][DPL], const float (&vv)[DEC_TOKENS][DPL], int64_t t,
+                        int64_t hi) {
+    float v[NV];
 #pragma unroll
-    for (int h = 0; h < GM; ++h) {
-      p[h] = 0.f;
+    for (int u = 0; u < DEC_TOKENS; ++u)
 #pragma unroll
-      for (int j = 0; j < DPL; ++j) p[h] = fmaf(qv[h][j], kv[j], p[h]);
+      for (int h = 0; h < GM; ++h) {
+        float p = 0.f;
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) p = fmaf(qv[h][j], kv[u][j], p);
+        v[u * GM + h] = p;
+      }
+#pragma unroll
+    for (int k = 0; (NV >> k) > 1; ++k) {
+      const bool hi_half = (lane >> k) & 1;
+#pragma unroll
+      for (int i = 0; i < (NV >> k) / 2; ++i) {
+        const float keep = hi_half ? v[2 * i + 1] : v[2 * i];
+        const float send = hi_half ? v[2 * i] : v[2 * i + 1];
+        float got;
+        if (k == 0) got = dpp_f32<0xB1>(send);       // lane ^ 1 (quad_perm [1,0,3,2])
+        else if (k == 1) got = dpp_f32<0x4E>(send);  // lane ^ 2 (quad_perm [2,3,0,1])
+        else got = __shfl_xor(send, 1 << k, 64);
+        v[i] = keep + got;
+      }
     }
-#pragma unroll
-    for (int h = 0; h < GM; ++h) p[h] += dpp_f32<0xB1>(p[h]);   // quad_perm [1,0,3,2]
-#pragma unroll
-    for (int h = 0; h < GM; ++h) p[h] += dpp_f32<0x4E>(p[h]);   // quad_perm [2,3,0,1]
-#pragma unroll
-    for (int h = 0; h < GM; ++h) p[h] += dpp_f32<0x141>(p[h]);  // row_half_mirror
-#pragma unroll
-    for (int h = 0; h < GM; ++h) p[h] += dpp_f32<0x140>(p[h]);  // row_mirror
+    float sc = v[0];
+    if constexpr (NV == 32) sc += __shfl_xor(sc, 32, 64);  // the two half-waves hold partial sums
+    sc = t + my_u * DEC_WAVES < hi ? sc * scale2 : -INFINITY;
+    float mb = fmaxf(sc, __shfl_xor(sc, GM, 64));
+    mb = fmaxf(mb, __shfl_xor(mb, 2 * GM, 64));
+    const float nm = fmaxf(m_run, mb);
+    const float alpha = l_run == 0.f ? 0.f : __builtin_amdgcn_exp2f(m_run - nm);
+    const float e = __builtin_amdgcn_exp2f(sc - nm);
+    float es = e + __shfl_xor(e, GM, 64);
+    es = es + __shfl_xor(es, 2 * GM, 64);
+    l_run = l_run * alpha + es;
+    m_run = nm;
 #pragma unroll
     for (int h = 0; h < GM; ++h) {
       if (h >= G) continue;
-      const float tot = (lane_f32(p[h], 0) + lane_f32(p[h], 16)) + (lane_f32(p[h], 32) + lane_f32(p[h], 48));
-      const float s = tot * scale2;
-      const float nm = fmaxf(m[h], s);
-      const float alpha = l[h] == 0.f ? 0.f : __builtin_amdgcn_exp2f(m[h] - nm);
-      const float e = __builtin_amdgcn_exp2f(s - nm);
-      l[h] = l[h] * alpha + e;
+      const float ah = lane_f32(alpha, h);
+      float eu[DEC_TOKENS];
 #pragma unroll
-      for (int j = 0; j < DPL; ++j) acc[h][j] = acc[h][j] * alpha + e * vv[j];
-      m[h] = nm;
+      for (int u = 0; u < DEC_TOKENS; ++u) eu[u] = lane_f32(e, u * GM + h);
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) {
+        float x = acc[h][j] * ah;
+#pragma unroll
+        for (int u = 0; u < DEC_TOKENS; ++u) x = fmaf(eu[u], vv[u][j], x);
+        acc[h][j] = x;
+      }
     }
   };
   // Wave w scores tokens t0 + w, t0 + w + 4, ... in ascending order.  The packed segment
   // and the residual segment run as two loops so neither loop body branches on the segment;
-  // each step loads two tokens before scoring either.
+  // each step loads DEC_TOKENS tokens, then scores them together.
   auto sweep = [&](int64_t lo, int64_t hi, auto&& load) {
     int64_t t = t0 + wave;
     if (t < lo) t += (lo - t + DEC_WAVES - 1) / DEC_WAVES * DEC_WAVES;
-    for (; t < hi; t += 2 * DEC_WAVES) {
-      float kv0[DPL], vv0[DPL], kv1[DPL], vv1[DPL];
-      const bool two = t + DEC_WAVES < hi;
-      load(t, kv0, vv0);
-      load(two ? t + DEC_WAVES : t, kv1, vv1);  // unconditional: no branch between the loads
-      score_token(kv0, vv0);
-      if (two) score_token(kv1, vv1);
+    for (; t < hi; t += DEC_TOKENS * DEC_WAVES) {
+      float kv[DEC_TOKENS][DPL], vv[DEC_TOKENS][DPL];
+#pragma unroll
+      for (int u = 0; u < DEC_TOKENS; ++u) {
+        const int64_t tu = t + u * DEC_WAVES;
+        load(tu < hi ? tu : t, kv[u], vv[u]);  // unconditional: no branch between the loads
+      }
+      score_step(kv, vv, t, hi);
     }
   };
   sweep(t0, t1 < L1 ? t1 : L1, load_packed);
   sweep(t0 > L1 ? t0 : L1, t1, load_residual);
   // merge the 4 waves: common max, rescale, ordered sum in LDS
-  if (lane == 0) {
-#pragma unroll
-    for (int h = 0; h < GM; ++h)
-      if (h < G) {
-        s_m[wave][h] = m[h];
-        s_l[wave][h] = l[h];
-      }
+  if (lane < G) {  // lane h < GM holds head h's state
+    s_m[wave][lane] = m_run;
+    s_l[wave][lane] = l_run;
   }
   __syncthreads();
   // waves add in a fixed order (deterministic sums; each lane owns its entries)
@@ -277,7 +314,7 @@ __global__ __launch_bounds__(64 * DEC_WAVES) void decode_split_kernel(const anna
         if (h >= G) continue;
         float M = -INFINITY;
         for (int w2 = 0; w2 < DEC_WAVES; ++w2) M = fmaxf(M, s_m[w2][h]);
-        const float f = l[h] == 0.f ? 0.f : __builtin_amdgcn_exp2f(m[h] - M);
+        const float f = s_l[wave][h] == 0.f ? 0.f : __builtin_amdgcn_exp2f(s_m[wave][h] - M);
 #pragma unroll
         for (int j = 0; j < DPL; ++j) s_acc[h * D + lane * DPL + j] += acc[h][j] * f;
       }
@@ -303,81 +340,86 @@ __global__ __launch_bounds__(64 * DEC_WAVES) void decode_split_kernel(const anna
   }
 }
 
-// grid (Hq, B), 256 threads.  Blocks [0, nrot) hold rotated (TQ-MSE) value accumulators.
-__global__ __launch_bounds__(256) void decode_merge_kernel(const anna_mi_decode_args a, int64_t nblk, int64_t nrot) {
+// grid (Hq, B), MERGE_THREADS threads.  Blocks [0, nrot) hold rotated (TQ-MSE) value
+// accumulators.  Thread t owns dim t % D and the blocks k = t / D (mod MERGE_THREADS / D);
+// the slices are then added in slice order, so the result does not depend on timing.
+__global__ __launch_bounds__(MERGE_THREADS) void decode_merge_kernel(const anna_mi_decode_args a, int64_t nblk,
+                                                                     int64_t nrot) {
   extern __shared__ float s_rot[];  // [D] rotated accumulator
-  __shared__ float s_red[256];
+  __shared__ float s_red[MERGE_THREADS];
+  __shared__ float s_w[MERGE_CHUNK];
+  __shared__ float s_part[2][MERGE_THREADS];
   const int64_t h = blockIdx.x, b = blockIdx.y, D = a.head_dim;
+  const int tid = threadIdx.x;
   const anna_mi_view& ps = a.partial_stats;
   const anna_mi_view& pv = a.partial_values;
   const float* st = (const float*)ps.ptr + b * ps.s0 + h * ps.s1;
   const float* va = (const float*)pv.ptr + b * pv.s0 + h * pv.s1;
   float mx = -INFINITY;
-  for (int64_t k = threadIdx.x; k < nblk; k += blockDim.x) mx = fmaxf(mx, st[k * ps.s2]);
-  s_red[threadIdx.x] = mx;
+  for (int64_t k = tid; k < nblk; k += MERGE_THREADS) mx = fmaxf(mx, st[k * ps.s2]);
+  s_red[tid] = mx;
   __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if ((int)threadIdx.x < s) s_red[threadIdx.x] = fmaxf(s_red[threadIdx.x], s_red[threadIdx.x + s]);
+  for (int s = MERGE_THREADS / 2; s > 0; s >>= 1) {
+    if (tid < s) s_red[tid] = fmaxf(s_red[tid], s_red[tid + s]);
     __syncthreads();
   }
   const float M = s_red[0];
   __syncthreads();
   float den = 0.f;
-  for (int64_t k = threadIdx.x; k < nblk; k += blockDim.x) {
+  for (int64_t k = tid; k < nblk; k += MERGE_THREADS) {
     const float dk = st[k * ps.s2 + ps.s3];
     if (dk != 0.f) den += dk * expf(st[k * ps.s2] - M);
   }
-  s_red[threadIdx.x] = den;
+  s_red[tid] = den;
   __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if ((int)threadIdx.x < s) s_red[threadIdx.x] += s_red[threadIdx.x + s];
+  for (int s = MERGE_THREADS / 2; s > 0; s >>= 1) {
+    if (tid < s) s_red[tid] += s_red[tid + s];
     __syncthreads();
   }
   const float denom = s_red[0];
-  // Block weights exp(m_k - M) go through LDS a chunk at a time (0 for empty blocks); each
-  // thread then sums its dims over the chunk's blocks in ascending order, with the loads of
-  // several blocks in flight.
-  __shared__ float s_w[MERGE_CHUNK];
-  float accr[4] = {0.f, 0.f, 0.f, 0.f}, accq[4] = {0.f, 0.f, 0.f, 0.f};  // D <= 1024 -> at most 4 dims per thread
+  // Block weights exp(m_k - M) go through LDS a chunk at a time (0 for empty blocks).
+  const int ks = (int)(MERGE_THREADS / D), slice = tid / (int)D;
+  const int64_t d = tid % D;
+  const float* vd = va + d * pv.s3;
+  float ar = 0.f, aq = 0.f;
   for (int64_t kc = 0; kc < nblk; kc += MERGE_CHUNK) {
     const int64_t kn = nblk - kc < MERGE_CHUNK ? nblk - kc : MERGE_CHUNK;
-    for (int64_t k = threadIdx.x; k < kn; k += blockDim.x) {
+    for (int64_t k = tid; k < kn; k += MERGE_THREADS) {
       const int64_t kk = kc + k;
       const float dk = st[kk * ps.s2 + ps.s3];
       s_w[k] = dk == 0.f ? 0.f : expf(st[kk * ps.s2] - M);
     }
     __syncthreads();
     const int64_t kr = nrot - kc < 0 ? 0 : (nrot - kc < kn ? nrot - kc : kn);  // [0, kr) rotated blocks
-    for (int j = 0; j < 4; ++j) {
-      const int64_t d = threadIdx.x + (int64_t)j * blockDim.x;
-      if (d >= D) break;
-      const float* vd = va + kc * pv.s2 + d * pv.s3;
-      float ar = accr[j], aq = accq[j];
 #pragma unroll 8
-      for (int64_t k = 0; k < kr; ++k) {
-        const float w = s_w[k], v = vd[k * pv.s2];
-        ar = w != 0.f ? ar + w * v : ar;
-      }
+    for (int64_t k = slice; k < kr; k += ks) {
+      const float w = s_w[k], v = vd[(kc + k) * pv.s2];
+      ar = w != 0.f ? ar + w * v : ar;
+    }
+    int64_t k0 = slice;
+    if (k0 < kr) k0 += (kr - k0 + ks - 1) / ks * ks;
 #pragma unroll 8
-      for (int64_t k = kr; k < kn; ++k) {
-        const float w = s_w[k], v = vd[k * pv.s2];
-        aq = w != 0.f ? aq + w * v : aq;
-      }
-      accr[j] = ar;
-      accq[j] = aq;
+    for (int64_t k = k0; k < kn; k += ks) {
+      const float w = s_w[k], v = vd[(kc + k) * pv.s2];
+      aq = w != 0.f ? aq + w * v : aq;
     }
     __syncthreads();
   }
-  for (int j = 0; j < 4; ++j) {
-    const int64_t d = threadIdx.x + (int64_t)j * blockDim.x;
-    if (d >= D) break;
-    if (nrot > 0) s_rot[d] = accr[j];
+  s_part[0][tid] = ar;
+  s_part[1][tid] = aq;
+  __syncthreads();
+  if (tid < D) {
+    float r = 0.f, q = 0.f;
+    for (int i = 0; i < ks; ++i) {
+      r += s_part[0][i * D + tid];
+      q += s_part[1][i * D + tid];
+    }
+    if (nrot > 0) s_rot[tid] = r;
+    aq = q;
   }
   if (nrot > 0) __syncthreads();
-  for (int j = 0; j < 4; ++j) {
-    const int64_t d = threadIdx.x + (int64_t)j * blockDim.x;
-    if (d >= D) break;
-    float o = accq[j];
+  if (tid < D) {
+    float o = aq;
     if (nrot > 0) {
       float u = 0.f;
       for (int64_t i = 0; i < D; ++i) u = fmaf(a.rotation[i * D + d], s_rot[i], u);
@@ -481,6 +523,9 @@ extern "C" int anna_mi_gqa_decode_splitkv(const anna_mi_decode_args* ap, void* s
   if (a.value_format == ANNA_MI_VALUES_TQ_MSE && a.len1 > 0)
     ANNA_CHECK(a.value_scales.ptr && a.rotation && a.value_centroids, "TQ-MSE values need norms, rotation and centroids");
   if (a.gate_layout != ANNA_MI_GATE_NONE) ANNA_CHECK(a.gate.ptr != nullptr, "null gate");
+  for (const anna_mi_view* v : {&a.key, &a.value, &a.value_scales, &a.value_zeros, &a.residual_key, &a.residual_value})
+    ANNA_CHECK(v->s3 >= 0 && v->s3 < ((int64_t)1 << 31) / a.head_dim,
+               "anna_mi_gqa_decode_splitkv: innermost stride %lld too large", (long long)v->s3);
   const Split sp = make_split(a);
   const int64_t nblk = total_blocks(a, sp);
   ANNA_CHECK(nblk <= a.partial_capacity, "partial_stats/partial_values capacity %lld is smaller than %lld blocks",
@@ -505,7 +550,7 @@ extern "C" int anna_mi_gqa_decode_splitkv(const anna_mi_decode_args* ap, void* s
   }
   ANNA_LAUNCH_CHECK("decode_split_kernel");
   const int64_t nrot = a.value_format == ANNA_MI_VALUES_TQ_MSE ? sp.nb1 : 0;
-  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)a.q_heads, (unsigned)a.batch), dim3(256),
+  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)a.q_heads, (unsigned)a.batch), dim3(MERGE_THREADS),
                      (size_t)a.head_dim * 4, st, a, nblk, nrot);
   ANNA_LAUNCH_CHECK("decode_merge_kernel");
   return ANNA_MI_OK;
