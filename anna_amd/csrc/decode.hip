@@ -12,6 +12,8 @@
 //
 // Reference: launch_gqa_decode_splitkv_fused_xpu (gated_delta_fused_op.sycl:4494-4706)
 // and launch_gqa_decode_splitkv_turboquant_fused_xpu (sycl:4771-5094).
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace anna {
@@ -56,6 +58,8 @@ __device__ __forceinline__ int sbits(int bits) { return bits == 2 ? 2 : 4; }
 struct Split {
   int64_t eb, nb1, eb2;  // block size (segment 1 or whole range), blocks of segment 1, residual block size
   int aligned;           // 1: blocks never straddle the two segments
+  int vec;               // 1: dense key rows contiguous and aligned for one vector load per lane, and
+                         //    a lane's dims share one value scale group
 };
 
 // q' = R q for every (b, q-head); grid (Hq, B), D threads.
@@ -162,7 +166,10 @@ __global__ __launch_bounds__(64 * DEC_WAVES) void decode_split_kernel(const anna
   const float scale2 = a.scaling * 1.4426950408889634f;  // scores in log2 units
   // Loads one token's K and V rows (dequantized) into registers: every load of the token is
   // issued before any value is used.
-  auto load_packed = [&](int64_t t, float (&kv)[DPL], float (&vv)[DPL]) {
+  // VEC: the key row slice of a lane is one aligned vector load (dense keys) and the lane's
+  // dims share one scale/zero (min/max values); the host sets it when the views allow it.
+  auto load_packed = [&](int64_t t, float (&kv)[DPL], float (&vv)[DPL], auto vec_tag) {
+    constexpr bool VEC = decltype(vec_tag)::value;
     {
       const int64_t kb = b * a.key.s0 + kvh * a.key.s1 + t * a.key.s2;
       const int64_t vb = b * a.value.s0 + kvh * a.value.s1 + t * a.value.s2;
@@ -174,6 +181,16 @@ __global__ __launch_bounds__(64 * DEC_WAVES) void decode_split_kernel(const anna
         for (int j = 0; j < DPL; ++j) kc[j] = ((const uint8_t*)a.key.ptr)[kb + koff[j]];
 #pragma unroll
         for (int j = 0; j < DPL; ++j) kv[j] = a.key_centroids[(kc[j] >> kshift[j]) & kmask] * nk;
+      } else if constexpr (VEC) {
+        using E = typename std::conditional<DT == ANNA_MI_F32, uint32_t, uint16_t>::type;
+        struct alignas(sizeof(E) * DPL) Row { E x[DPL]; };
+        const Row r = *(const Row*)((const E*)a.key.ptr + kb + lane * DPL);
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) {
+          if constexpr (DT == ANNA_MI_BF16) kv[j] = bf16_bits_to_f32(r.x[j]);
+          else if constexpr (DT == ANNA_MI_F16) kv[j] = f16_bits_to_f32(r.x[j]);
+          else kv[j] = __uint_as_float(r.x[j]);
+        }
       } else {
 #pragma unroll
         for (int j = 0; j < DPL; ++j) kv[j] = ldt<DT>(a.key.ptr, kb + koff[j]);
@@ -186,11 +203,21 @@ __global__ __launch_bounds__(64 * DEC_WAVES) void decode_split_kernel(const anna
         const int64_t zb0 = b * a.value_zeros.s0 + kvh * a.value_zeros.s1 + t * a.value_zeros.s2;
         uint32_t vc[DPL];
         float sc[DPL], zc[DPL];
+        if constexpr (VEC) {
+          const float s0 = ldt<DT>(a.value_scales.ptr, sb0 + soff[0]), z0 = ldt<DT>(a.value_zeros.ptr, zb0 + zoff[0]);
 #pragma unroll
-        for (int j = 0; j < DPL; ++j) {
-          vc[j] = ((const uint8_t*)a.value.ptr)[vb + voff[j]];
-          sc[j] = ldt<DT>(a.value_scales.ptr, sb0 + soff[j]);
-          zc[j] = ldt<DT>(a.value_zeros.ptr, zb0 + zoff[j]);
+          for (int j = 0; j < DPL; ++j) {
+            vc[j] = ((const uint8_t*)a.value.ptr)[vb + voff[j]];
+            sc[j] = s0;
+            zc[j] = z0;
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) {
+            vc[j] = ((const uint8_t*)a.value.ptr)[vb + voff[j]];
+            sc[j] = ldt<DT>(a.value_scales.ptr, sb0 + soff[j]);
+            zc[j] = ldt<DT>(a.value_zeros.ptr, zb0 + zoff[j]);
+          }
         }
 #pragma unroll
         for (int j = 0; j < DPL; ++j) vv[j] = (float)((vc[j] >> vshift[j]) & vmask) * sc[j] + zc[j];
@@ -298,7 +325,12 @@ __global__ __launch_bounds__(64 * DEC_WAVES) void decode_split_kernel(const anna
       score_step(kv, vv, t, hi);
     }
   };
-  sweep(t0, t1 < L1 ? t1 : L1, load_packed);
+  if (sp.vec)
+    sweep(t0, t1 < L1 ? t1 : L1,
+          [&](int64_t t, float (&kv)[DPL], float (&vv)[DPL]) { load_packed(t, kv, vv, std::true_type{}); });
+  else
+    sweep(t0, t1 < L1 ? t1 : L1,
+          [&](int64_t t, float (&kv)[DPL], float (&vv)[DPL]) { load_packed(t, kv, vv, std::false_type{}); });
   sweep(t0 > L1 ? t0 : L1, t1, load_residual);
   // merge the 4 waves: common max, rescale, ordered sum in LDS
   if (lane < G) {  // lane h < GM holds head h's state
@@ -526,7 +558,16 @@ extern "C" int anna_mi_gqa_decode_splitkv(const anna_mi_decode_args* ap, void* s
   for (const anna_mi_view* v : {&a.key, &a.value, &a.value_scales, &a.value_zeros, &a.residual_key, &a.residual_value})
     ANNA_CHECK(v->s3 >= 0 && v->s3 < ((int64_t)1 << 31) / a.head_dim,
                "anna_mi_gqa_decode_splitkv: innermost stride %lld too large", (long long)v->s3);
-  const Split sp = make_split(a);
+  Split sp = make_split(a);
+  {
+    const int64_t dpl = a.head_dim / 64, esz = a.dtype == ANNA_MI_F32 ? 4 : 2;
+    const anna_mi_view& k = a.key;
+    const bool kvec = a.key_format != ANNA_MI_KEYS_DENSE ||
+                      (k.s3 == 1 && k.s0 % dpl == 0 && k.s1 % dpl == 0 && k.s2 % dpl == 0 &&
+                       (uintptr_t)k.ptr % (uintptr_t)(dpl * esz) == 0);
+    const bool svec = a.value_format != ANNA_MI_VALUES_MINMAX || a.value_group_size % dpl == 0;
+    sp.vec = kvec && svec;
+  }
   const int64_t nblk = total_blocks(a, sp);
   ANNA_CHECK(nblk <= a.partial_capacity, "partial_stats/partial_values capacity %lld is smaller than %lld blocks",
              (long long)a.partial_capacity, (long long)nblk);

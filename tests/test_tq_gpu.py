@@ -167,6 +167,36 @@ def test_splitkv_turboquant_matches_dequantized_reference(gpu, value_bits):
     assert rel_err(f32(out), ref) <= BF16_TOL
 
 
+@pytest.mark.parametrize("key_stride", [1, 2])
+def test_splitkv_turboquant_scalar_and_vector_loads(gpu, key_stride):
+    """D=256, batch 2: contiguous keys with group 32 take the kernel's vector loads; keys
+    strided in the last dim with group 2 (not a multiple of a lane's 4 dims) take the
+    per-element loads.  Both against the oracle on the dequantized cache."""
+    torch.manual_seed(40 + key_stride)
+    b, hq, hkv, d, qlen, rlen, bits, bs = 2, 8, 2, 256, 203, 9, 4, 64
+    group = 32 if key_stride == 1 else 2
+    q = torch.randn(b, hq, 1, d, device=gpu, dtype=torch.bfloat16)
+    qk = torch.randn(b, hkv, qlen, d * key_stride, device=gpu, dtype=torch.bfloat16)[..., ::key_stride]
+    assert qk.stride(-1) == key_stride
+    st = quantize_turboquant_values(torch.randn(b * hkv, qlen, d, device=gpu, dtype=torch.bfloat16), bits=bits,
+                                    group_size=group)
+    rk = torch.randn(b, hkv, rlen, d, device=gpu, dtype=torch.bfloat16)
+    rv = torch.randn(b, hkv, rlen, d, device=gpu, dtype=torch.bfloat16)
+    out = torch.empty_like(q)
+    nb = -(-(qlen + rlen) // bs) + 1
+    ps = torch.empty(b, hq, nb, 2, device=gpu)
+    pv = torch.empty(b, hq, nb, d, device=gpu)
+    torch.ops.anna.gqa_decode_splitkv_turboquant_fused_out(
+        q, qk, st.data.view(b, hkv, qlen, -1), st.scales.view(b, hkv, qlen, -1), st.zeros.view(b, hkv, qlen, -1),
+        rk, rv, out, ps, pv, d ** -0.5, bits, group, bs, None)
+    vq = orc.tq_values_dequant(st.data.cpu().numpy(), bits_of(st.scales), bits_of(st.zeros), orc.BF16, bits,
+                               group).reshape(b, hkv, qlen, d)
+    kk = np.concatenate([f32(qk), f32(rk)], axis=2)
+    vv = np.concatenate([vq, f32(rv)], axis=2)
+    ref = _oracle_attention(f32(q), kk, vv, d ** -0.5)
+    assert rel_err(f32(out), ref) <= BF16_TOL
+
+
 @pytest.mark.parametrize("vfmt", ["minmax", "mse"])
 def test_splitkv_tq_mse_keys(gpu, vfmt):
     """Packed TQ-MSE keys (scored against R q) with min/max or TQ-MSE values, batch 2."""
