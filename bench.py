@@ -244,6 +244,45 @@ def section_tq_decode(args, device):
     return r
 
 
+def section_row_decode(args, device):
+    """The reference's per-row op (gqa_decode_splitkv_turboquant_fused_out): B=8, Hq=16, Hkv=2,
+    D=256, 4096 packed tokens (2-bit min/max values, group 32, dense bf16 keys) + 128 bf16
+    residual tokens, block 64."""
+    from anna_amd.turboquant import quantize_turboquant_values
+
+    B, HQ, HKV, D, L, R, BITS, GROUP, BS = 8, 16, 2, 256, 4096, 128, 2, 32, 64
+    gen = torch.Generator(device=device)
+    gen.manual_seed(46)
+    q = torch.randn((B, HQ, 1, D), device=device, generator=gen).to(torch.bfloat16)
+
+    def make():
+        k = torch.randn((B, HKV, L, D), device=device, generator=gen).to(torch.bfloat16)
+        st = quantize_turboquant_values(torch.randn((B * HKV, L, D), device=device, generator=gen).to(torch.bfloat16),
+                                        bits=BITS, group_size=GROUP)
+        rk = torch.randn((B, HKV, R, D), device=device, generator=gen).to(torch.bfloat16)
+        rv = torch.randn((B, HKV, R, D), device=device, generator=gen).to(torch.bfloat16)
+        return (k, st.data.view(B, HKV, L, -1), st.scales.view(B, HKV, L, -1), st.zeros.view(B, HKV, L, -1), rk, rv)
+
+    first = make()
+    per_call = sum(t.numel() * t.element_size() for t in first)
+    caches = [first] + [make() for _ in range(max(1, math.ceil(ROTATE_BYTES / per_call)) - 1)]
+    nblk = -(-(L + R) // BS)
+    out = torch.empty_like(q)
+    ps = torch.empty((B, HQ, nblk, 2), device=device)
+    pv = torch.empty((B, HQ, nblk, D), device=device)
+    op = torch.ops.anna.gqa_decode_splitkv_turboquant_fused_out
+    fns = [(lambda c=c: op(q, *c, out, ps, pv, D ** -0.5, BITS, GROUP, BS, None)) for c in caches]
+    ms = time_graph(fns, args.steps, args.warmup)
+    sec = ms / 1e3
+    r = {"B": B, "Hq": HQ, "Hkv": HKV, "D": D, "L": L, "residual": R, "value_bits": BITS, "group": GROUP,
+         "block_size": BS, "ms": ms, "us": ms * 1e3, "tokens/s": B / sec, "bytes": per_call,
+         "GB/s": per_call / sec / 1e9, "roofline_frac": per_call / sec / 1e9 / HBM_PEAK_GBS,
+         "distinct_cache_copies": len(caches)}
+    log(f"row-API decode B=8 L={L}+{R}: {r['us']:.2f} us/call  {r['GB/s']:.0f} GB/s  "
+        f"{100 * r['roofline_frac']:.1f}% of HBM peak")
+    return r
+
+
 def section_tq_pack(args, device):
     """K, V bf16 [8192, 2, 256] with 1% outlier channels x8 -> 2-bit TQ-MSE
     codes + fp16 norms, last 128 tokens kept bf16."""
@@ -443,7 +482,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=60)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--sections", default="int4,tq_decode,tq_pack,moe")
+    ap.add_argument("--sections", default="int4,tq_decode,row_decode,tq_pack,moe")
     ap.add_argument("--tq-tokens-per-item", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -472,6 +511,8 @@ def main() -> int:
         sections["int4_sweep"] = section_int4(args, device)
     if "tq_decode" in wanted:
         sections["tq_decode"] = section_tq_decode(args, device)
+    if "row_decode" in wanted:
+        sections["row_decode"] = section_row_decode(args, device)
     if "tq_pack" in wanted:
         sections["tq_pack"] = section_tq_pack(args, device)
     if "moe" in wanted:
