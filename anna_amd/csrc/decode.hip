@@ -22,7 +22,8 @@ namespace {
 constexpr int DEC_WAVES = 4;
 constexpr int DEC_TOKENS = 4;  // tokens per wave whose loads are in flight together
 constexpr int MERGE_CHUNK = 1024;
-constexpr int MERGE_THREADS = 1024;  // merge workgroup: MERGE_THREADS / head_dim block slices per dim  // block weights staged in LDS per pass of the merge
+constexpr int MERGE_THREADS = 1024;
+constexpr int MERGE_PRE = 8;  // partial values per merge thread loaded before the reductions  // merge workgroup: MERGE_THREADS / head_dim block slices per dim  // block weights staged in LDS per pass of the merge
 
 __device__ __forceinline__ float ldv(const void* p, int64_t i, int dt) {
   if (dt == ANNA_MI_BF16) return bf16_bits_to_f32(((const uint16_t*)p)[i]);
@@ -387,8 +388,25 @@ __global__ __launch_bounds__(MERGE_THREADS) void decode_merge_kernel(const anna_
   const anna_mi_view& pv = a.partial_values;
   const float* st = (const float*)ps.ptr + b * ps.s0 + h * ps.s1;
   const float* va = (const float*)pv.ptr + b * pv.s0 + h * pv.s1;
-  float mx = -INFINITY;
-  for (int64_t k = tid; k < nblk; k += MERGE_THREADS) mx = fmaxf(mx, st[k * ps.s2]);
+  // Block tid's stats and this thread's first MERGE_PRE partial values are loaded up front,
+  // so their latency overlaps the reductions below (later blocks are read as needed).
+  const int ks = (int)(MERGE_THREADS / D), slice = tid / (int)D;
+  const int64_t d = tid % D;
+  const float* vd = va + d * pv.s3;
+  const int64_t kn0 = nblk < MERGE_CHUNK ? nblk : MERGE_CHUNK;
+  float pre[MERGE_PRE];
+#pragma unroll
+  for (int i = 0; i < MERGE_PRE; ++i) {
+    const int64_t k = slice + (int64_t)i * ks;
+    pre[i] = k < kn0 ? vd[k * pv.s2] : 0.f;
+  }
+  float m0 = -INFINITY, d0 = 0.f;
+  if (tid < nblk) {
+    m0 = st[(int64_t)tid * ps.s2];
+    d0 = st[(int64_t)tid * ps.s2 + ps.s3];
+  }
+  float mx = m0;
+  for (int64_t k = tid + MERGE_THREADS; k < nblk; k += MERGE_THREADS) mx = fmaxf(mx, st[k * ps.s2]);
   s_red[tid] = mx;
   __syncthreads();
   for (int s = MERGE_THREADS / 2; s > 0; s >>= 1) {
@@ -397,8 +415,9 @@ __global__ __launch_bounds__(MERGE_THREADS) void decode_merge_kernel(const anna_
   }
   const float M = s_red[0];
   __syncthreads();
-  float den = 0.f;
-  for (int64_t k = tid; k < nblk; k += MERGE_THREADS) {
+  const float w0 = d0 == 0.f ? 0.f : expf(m0 - M);  // weight of block tid
+  float den = d0 == 0.f ? 0.f : d0 * w0;
+  for (int64_t k = tid + MERGE_THREADS; k < nblk; k += MERGE_THREADS) {
     const float dk = st[k * ps.s2 + ps.s3];
     if (dk != 0.f) den += dk * expf(st[k * ps.s2] - M);
   }
@@ -409,32 +428,37 @@ __global__ __launch_bounds__(MERGE_THREADS) void decode_merge_kernel(const anna_
     __syncthreads();
   }
   const float denom = s_red[0];
-  // Block weights exp(m_k - M) go through LDS a chunk at a time (0 for empty blocks).
-  const int ks = (int)(MERGE_THREADS / D), slice = tid / (int)D;
-  const int64_t d = tid % D;
-  const float* vd = va + d * pv.s3;
+  // Block weights exp(m_k - M) go through LDS a chunk at a time (0 for empty blocks).  Thread
+  // (slice, d) sums blocks slice, slice + ks, ... in ascending order.
   float ar = 0.f, aq = 0.f;
   for (int64_t kc = 0; kc < nblk; kc += MERGE_CHUNK) {
     const int64_t kn = nblk - kc < MERGE_CHUNK ? nblk - kc : MERGE_CHUNK;
-    for (int64_t k = tid; k < kn; k += MERGE_THREADS) {
-      const int64_t kk = kc + k;
-      const float dk = st[kk * ps.s2 + ps.s3];
-      s_w[k] = dk == 0.f ? 0.f : expf(st[kk * ps.s2] - M);
+    if (kc == 0) {
+      if (tid < kn) s_w[tid] = w0;
+    } else {
+      for (int64_t k = tid; k < kn; k += MERGE_THREADS) {
+        const int64_t kk = kc + k;
+        const float dk = st[kk * ps.s2 + ps.s3];
+        s_w[k] = dk == 0.f ? 0.f : expf(st[kk * ps.s2] - M);
+      }
     }
     __syncthreads();
     const int64_t kr = nrot - kc < 0 ? 0 : (nrot - kc < kn ? nrot - kc : kn);  // [0, kr) rotated blocks
-#pragma unroll 8
-    for (int64_t k = slice; k < kr; k += ks) {
-      const float w = s_w[k], v = vd[(kc + k) * pv.s2];
-      ar = w != 0.f ? ar + w * v : ar;
+    auto add = [&](int64_t k, float v) {
+      const float w = s_w[k];
+      if (w != 0.f) {
+        if (k < kr) ar += w * v;
+        else aq += w * v;
+      }
+    };
+    int64_t k = slice;
+    if (kc == 0) {
+#pragma unroll
+      for (int i = 0; i < MERGE_PRE; ++i, k += ks)
+        if (k < kn) add(k, pre[i]);
     }
-    int64_t k0 = slice;
-    if (k0 < kr) k0 += (kr - k0 + ks - 1) / ks * ks;
 #pragma unroll 8
-    for (int64_t k = k0; k < kn; k += ks) {
-      const float w = s_w[k], v = vd[(kc + k) * pv.s2];
-      aq = w != 0.f ? aq + w * v : aq;
-    }
+    for (; k < kn; k += ks) add(k, vd[(kc + k) * pv.s2]);
     __syncthreads();
   }
   s_part[0][tid] = ar;
