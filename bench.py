@@ -494,7 +494,7 @@ def main() -> int:
     EAGER = args.eager
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the sharding plan is described in DESIGN.md); run with --gpus 1.", file=sys.stderr)
+              "(one GPU's share of the work is what it times); run with --gpus 1.", file=sys.stderr)
         return 2
     if not torch.cuda.is_available():
         print("bench.py needs an MI355X (no ROCm device visible)", file=sys.stderr)
