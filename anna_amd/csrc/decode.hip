@@ -3,12 +3,15 @@
 // Kernel 1 (decode_split_kernel): one workgroup per (block of tokens, KV head, batch).
 //   All G = Hq/Hkv query heads of the KV head are processed together, so each K/V
 //   element is read (and dequantized) once for the whole group instead of once per
-//   q-head.  4 waves share the block's tokens; a lane owns D/64 consecutive dims; each
-//   wave keeps an online softmax per head, and the waves are merged through LDS.
+//   q-head.  4 waves share the block's tokens, 4 tokens per wave per step; a lane owns D/64
+//   consecutive dims.  The step's token x head dot products are reduced over the wave
+//   together (transposed butterfly), the online-softmax state of head h lives in lanes
+//   h, h + GM, ..., and the waves are merged through LDS.
 //   Output: per (b, q-head, block) the running max, the denominator and the
 //   unnormalized accumulator, in the reference's partial_stats / partial_values layout.
-// Kernel 2 (decode_merge_kernel): log-sum-exp merge of the blocks per (b, q-head),
-//   optional un-rotation of TQ-MSE value accumulators, optional sigmoid gate.
+// Kernel 2 (decode_merge_kernel): log-sum-exp merge of the blocks per (b, q-head) by 1024
+//   threads (dims x block slices), optional un-rotation of TQ-MSE value accumulators,
+//   optional sigmoid gate.
 //
 // Reference: launch_gqa_decode_splitkv_fused_xpu (gated_delta_fused_op.sycl:4494-4706)
 // and launch_gqa_decode_splitkv_turboquant_fused_xpu (sycl:4771-5094).

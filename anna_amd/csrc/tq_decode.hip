@@ -10,21 +10,21 @@
 //   residual_key     bf16 [B][Hkv][R][256]  newest tokens, dense, token-major
 //   residual_value_t bf16 [B][Hkv][256][R]  dense, dim-major
 //
-// One launch, one 512-thread workgroup per work item (b, kv-head, pool range) or per residual
-// window (see anna_mi_tq_decode_plan):
-//   prologue  q' = R q for the item's G q-heads (MFMA, fp16; R is read from L2), kept in LDS as
-//     the B operand of the score product; the first block of each wave already in flight.
-//   loop      8 waves take 32-token blocks (the next block prefetched).  Scores are formed
-//     transposed, S^T = Khat Q'^T, by v_mfma_f32_16x16x32_f16 on codes turned into fp16
+// Three launches per call (work items come from anna_mi_tq_decode_plan):
+//   tq_rotate_query   q' = R q for every (b, kv-head)'s G q-heads (MFMA, fp16), written in the
+//     B-operand fragment order of the score product.
+//   tq_decode_split   one 512-thread workgroup per work item (b, kv-head, pool range) or per
+//     residual window.  8 waves take 32-token blocks (the next block prefetched).  Scores are
+//     formed transposed, S^T = Khat Q'^T, by v_mfma_f32_16x16x32_f16 on codes turned into fp16
 //     centroids with one v_perm per pair (the 2-bit centroids are fp16 values sharing their
 //     low byte); S^T's accumulator layout is the B operand of O'^T = Vhat^T P^T, so the
 //     probabilities never leave registers.  Online softmax in base 2 with lazy rescaling
-//     (the running max only moves when a block exceeds it by 2^4).
-//   reduce    the 8 waves' accumulators are summed through LDS; per item and q-head the
-//     (max, denominator) and the unnormalized accumulator go to the workspace.
-//   tail      the last workgroup of a (b, kv-head) to finish (a counter that it resets)
-//     combines the items with log-sum-exp weights and applies R^T to the rotated sum
-//     (MFMA), adds the residual window's part and writes bf16.
+//     (the running max only moves when a block exceeds it by 2^4).  The 8 waves' accumulators
+//     are summed through LDS; per item and q-head the (max, denominator) and the unnormalized
+//     accumulator go to the workspace.
+//   tq_decode_combine 8 workgroups per (b, kv-head), one per 32 output dims: log-sum-exp merge
+//     of the items over the rotated dims, R^T for the tile's dims (MFMA), plus the residual
+//     window's part, written as bf16.
 #include <vector>
 
 #include "common.hpp"
