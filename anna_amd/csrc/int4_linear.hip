@@ -5,7 +5,12 @@
 // of word k/8 at bits 4*(k%8), qscale [G, N], qzeros int8 [G, N], w = (q - z) * s.
 //
 // Kernels
-//   int4_gemv_mfma   M < 64 (16-bit x, K <= 4096 for M > 16).  HBM-bound.  Each wave owns NT
+//   int4_gemv_dot2   M <= 2 (16-bit x).  HBM-bound.  Each wave owns 4 output rows; a lane
+//                    loads 16 bytes (32 weights) of a row per buffer load, turns nibble pairs
+//                    into bf16/f16 "off + q" with one AND-OR, accumulates v_dot2 in fp32 against
+//                    the pre-interleaved x and removes the zero point once per group; partials
+//                    are reduced with swizzle/DPP steps.  XCD-aware workgroup -> row map.
+//   int4_gemv_mfma   other M < 64 (16-bit x, K <= 4096 for M > 16).  HBM-bound.  Each wave owns NT
 //                    16-row tiles of W and a strided share of the K blocks (KW waves split K, reduced through
 //                    LDS at the end).  One 128-bit load per lane brings 32 nibbles of
 //                    one row; nibbles are turned into bf16/f16 "128+q" / "1024+q"

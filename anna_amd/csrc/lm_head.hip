@@ -10,9 +10,12 @@
 //                           each word is one T x 4-byte coalesced load (8 k of T rows) used
 //                           against 8 activations of up to MR rows; fp32 accumulation
 //                           (s * (sum x q - z sum x) per word), wave reduction at the end.
-//   topk_rows_kernel        per row: up to 1024 threads keep sorted top-k lists of their strided
-//                           share of the logits, merged pairwise in LDS (descending, ties to
-//                           the lower index).
+//   topk_rows_kernel        k <= 8, per row, 1024 threads: pass 1 takes each thread's maximum and
+//                           merges the maxima into a top-k list; its k-th entry bounds the row's
+//                           k-th best from below.  Pass 2 keeps only the logits at or above that
+//                           bound in sorted register lists, merged pairwise through LDS by a
+//                           bitonic merge (value descending, ties to the lower index).
+//   topk_rows_lds_kernel    k > 8: the same bound, the sorted lists in LDS.
 #include <type_traits>
 
 #include "common.hpp"

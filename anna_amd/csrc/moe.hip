@@ -3,10 +3,13 @@
 //   moe_router_kernel     one wave per token: fp32 softmax over the experts, top-k by repeated
 //                         wave arg-max (ties go to the lower expert index, the order of the
 //                         reference's insertion sort), optional renormalisation, usage counts.
+//   moe_route_small_kernel  routes <= 1024: router, dispatch order and the MLP's expert list
+//                         in one workgroup (same outputs and order as the kernels below).
 //   moe_order_kernel      one workgroup per expert: expert offsets (prefix sum of usage) and
 //                         the compact route order sorted by (expert, token, k) -- the order
 //                         of the reference's CPU path -- by a ballot prefix scan over the
-//                         routes in token-major order.  Deterministic (no atomics).
+//                         routes in token-major order; optionally the list of experts with
+//                         routes that the grouped MLP walks.  Deterministic (no atomics).
 //   moe_gather_kernel     compact_hidden[p] = hidden[sorted_token_idx[p]].
 //   moe_int4_mlp_kernel   grouped W4A16 expert MLP.  grid (64-row output tiles, active
 //                         experts); each workgroup takes the routes of its expert 16 at a
