@@ -120,6 +120,20 @@ RAW_PROTOTYPES: dict[str, tuple] = {
 }
 
 _lock = threading.Lock()
+
+
+def _check_stamp(lib: ctypes.CDLL) -> None:
+    """Refuses a library built from other sources than the csrc/ next to it."""
+    from . import build
+
+    if not build.CSRC.is_dir():
+        return  # installed without sources: nothing to compare against
+    built = lib.anna_mi_source_hash().decode()
+    want = build.source_hash()
+    if built != want:
+        raise RuntimeError(
+            f"{LIB_PATH.name} is stale: built from sources {built[:12]}, the tree holds {want[:12]}; "
+            "run `python -m anna_amd.build`")
 _lib: ctypes.CDLL | None = None
 
 
@@ -137,6 +151,9 @@ def load() -> ctypes.CDLL:
         lib = ctypes.CDLL(str(LIB_PATH))
         lib.anna_mi_last_error.restype = ctypes.c_char_p
         lib.anna_mi_last_error.argtypes = []
+        lib.anna_mi_source_hash.restype = ctypes.c_char_p
+        lib.anna_mi_source_hash.argtypes = []
+        _check_stamp(lib)
         lib.anna_mi_abi_version.restype = ctypes.c_int
         for name, argtypes in PROTOTYPES.items():
             fn = getattr(lib, name)

@@ -8,6 +8,7 @@ travels with the source tree.
 from __future__ import annotations
 
 import concurrent.futures
+import hashlib
 import os
 import shutil
 import subprocess
@@ -47,9 +48,39 @@ def _sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
 
 
-def _compile(src: Path) -> Path:
+def source_hash() -> str:
+    """sha256 over every file of csrc/ and include/ (names and contents, sorted).
+
+    The library is stamped with it (anna_mi_source_hash) and the loader refuses a binary
+    whose stamp differs from the sources next to it, so a run provably uses the kernels of
+    the tree it ships with."""
+    h = hashlib.sha256()
+    inc = PKG_DIR.parent / "include"
+    files = sorted(p for p in CSRC.iterdir() if p.is_file() and p.suffix in (".hip", ".cpp", ".hpp", ".h"))
+    if inc.is_dir():
+        files += sorted(p for p in inc.iterdir() if p.is_file() and p.suffix == ".h")
+    for p in files:
+        h.update(p.name.encode())
+        h.update(b"\0")
+        h.update(p.read_bytes())
+        h.update(b"\0")
+    return h.hexdigest()
+
+
+def _up_to_date(src: Path, obj: Path) -> bool:
+    if not obj.exists():
+        return False
+    deps = [src, *CSRC.glob("*.hpp"), *(PKG_DIR.parent / "include").glob("*.h")]
+    return obj.stat().st_mtime > max(p.stat().st_mtime for p in deps)
+
+
+def _compile(src: Path, stamp: str, force: bool = True) -> Path:
     obj = OBJ_DIR / (src.stem + ".o")
+    if not force and src.name != "runtime.cpp" and _up_to_date(src, obj):
+        return obj
     cmd = [_hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    if src.name == "runtime.cpp":
+        cmd.insert(-4, f'-DANNA_MI_SOURCE_HASH="{stamp}"')
     proc = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass warns about the device-only feature flag; drop that noise.
     noise = "is not a recognized feature for this target"
@@ -61,12 +92,15 @@ def _compile(src: Path) -> Path:
     return obj
 
 
-def build(verbose: bool = True) -> Path:
+def build(verbose: bool = True, force: bool = True) -> Path:
+    """Compiles every source (force=False reuses objects newer than their sources and the
+    shared headers; the stamped runtime.cpp is always rebuilt) and links the library."""
     OBJ_DIR.mkdir(exist_ok=True)
     sources = _sources()
     workers = min(len(sources), max(1, min(8, os.cpu_count() or 1)))
     with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as ex:
-        objs = list(ex.map(_compile, sources))
+        stamp = source_hash()
+        objs = list(ex.map(lambda src: _compile(src, stamp, force), sources))
     tmp = LIB_PATH.with_suffix(".so.tmp")
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -79,4 +113,4 @@ def build(verbose: bool = True) -> Path:
 
 
 if __name__ == "__main__":
-    build()
+    build(force="--incremental" not in sys.argv)

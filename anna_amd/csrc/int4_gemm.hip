@@ -65,10 +65,13 @@ using TileS = GemmTile<64, 48, 4, 1, 2>;    // M < 256:   16 x 48 wave tiles, 72
 // The loader's end of a k-step: all but its N most recent loads have landed (so the previous
 // step's LDS-destination x loads are in LDS), its LDS writes are done, then the workgroup
 // barrier.  __syncthreads() would also wait for the loads just issued, since its release fence
-// covers LDS-destination loads.
+// covers LDS-destination loads.  The scheduling barrier in front keeps the machine scheduler
+// from moving any load of this step below the wait (a count-based wait is right only while
+// every load it counts was issued before it).
 template <int N>
 __device__ __forceinline__ void loader_barrier() {
   static_assert(N >= 0 && N <= 63, "vmcnt holds 6 bits");
+  __builtin_amdgcn_sched_barrier(0);
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"i"(N) : "memory");
 }
 

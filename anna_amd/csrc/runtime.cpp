@@ -27,4 +27,9 @@ const char* anna_mi_last_error(void) { return anna::g_last_error; }
 
 int anna_mi_abi_version(void) { return ANNA_MI_ABI_VERSION; }
 
+#ifndef ANNA_MI_SOURCE_HASH
+#define ANNA_MI_SOURCE_HASH "unstamped"
+#endif
+const char* anna_mi_source_hash(void) { return ANNA_MI_SOURCE_HASH; }
+
 }  // extern "C"

@@ -198,16 +198,31 @@ VALUES_DENSE, VALUES_MINMAX, VALUES_TQ_MSE = 0, 1, 2
 GATE_NONE, GATE_FLAT, GATE_HEADS = 0, 1, 2
 
 
-def _gate_view(gate, num_heads, head_dim):
+def _check_gate(gate, query):
+    """validate_gqa_decode_optional_gate (sycl:1605-1629): dtype, batch and the two layouts."""
+    if gate is None:
+        return GATE_NONE
+    if gate.dtype != query.dtype:
+        raise RuntimeError("gate must match query dtype")
+    if gate.size(0) != query.size(0):
+        raise RuntimeError("gate batch size mismatch")
+    num_heads, head_dim = query.size(1), query.size(3)
+    if gate.dim() == 3 and gate.size(1) == 1 and gate.size(2) == num_heads * head_dim:
+        return GATE_FLAT
+    if gate.dim() == 4 and gate.size(1) == num_heads and gate.size(2) == 1 and gate.size(3) == head_dim:
+        return GATE_HEADS
+    raise RuntimeError("gate must be [batch, 1, heads * head_dim] or [batch, heads, 1, head_dim]")
+
+
+def _gate_view(gate, query):
     """Accepts the reference's two gate layouts (prepare_gqa_decode_gate, sycl:1631-1669):
     flat [B, 1, Hq*D] or query-aligned [B, Hq, 1, D]."""
-    if gate is None:
+    layout = _check_gate(gate, query)
+    if layout == GATE_NONE:
         return GATE_NONE, _lib.view(None)
-    if gate.dim() == 3 and gate.size(1) == 1 and gate.size(2) == num_heads * head_dim:
+    if layout == GATE_FLAT:
         return GATE_FLAT, _lib.view(gate, (0, 1, 2, -1))
-    if gate.dim() == 4 and gate.size(1) == num_heads and gate.size(2) == 1 and gate.size(3) == head_dim:
-        return GATE_HEADS, _lib.view(gate)
-    raise RuntimeError("gate must be [batch, 1, heads * head_dim] or [batch, heads, 1, head_dim]")
+    return GATE_HEADS, _lib.view(gate)
 
 
 def _splitkv_num_blocks(key_len: int, block_size: int) -> int:
@@ -224,7 +239,7 @@ def decode_args(*, query, len1, key=None, key_format=KEYS_DENSE, key_norms=None,
     b, hq, _, d = query.shape
     hkv = (key if key is not None else residual_key).size(1)
     len2 = 0 if residual_key is None else residual_key.size(2)
-    gl, gv = _gate_view(gate, hq, d)
+    gl, gv = _gate_view(gate, query)
     a = _lib.DecodeArgs()
     a.dtype = _lib.dtype_code(query.dtype)
     a.batch, a.q_heads, a.kv_heads, a.head_dim = b, hq, hkv, d
@@ -313,6 +328,7 @@ def _gqa_decode_splitkv_fused_out_impl(query, key, value, output, partial_stats,
     name = "gqa_decode_splitkv_fused_out"
     _check_decode_common(query, key, value, block_size, name)
     _check_workspace(query, key.size(2), block_size, output, partial_stats, partial_values, name)
+    _check_gate(gate, query)
     _lib.require_device(query, key, value, output, partial_stats, partial_values, gate)
     a = decode_args(query=query, len1=key.size(2), key=key, value=value, scaling=scaling, block_size=block_size,
                     gate=gate, output=output, partial_stats=partial_stats, partial_values=partial_values)
@@ -329,46 +345,68 @@ def _gqa_decode_splitkv_fused_impl(query, key, value, scaling, block_size, gate=
     return _gqa_decode_splitkv_fused_out_impl(query, key, value, out, ps, pv, scaling, block_size, gate)
 
 
+def _check_turboquant_inputs(query, quantized_key, value_data, value_scales, value_zeros, residual_key,
+                             residual_value, value_bits, value_group_size, block_size):
+    """Shape/dtype checks of validate_gqa_decode_splitkv_turboquant_inputs (sycl:1447-1501).
+
+    Runs before any pointer reaches the library: the C entry point sees only pointers and
+    strides, so a short value tensor or a smaller-batch cache must be refused here."""
+    def check(cond, msg):
+        if not cond:
+            raise RuntimeError(msg)
+
+    check(query.dim() == 4, "query must be [batch, heads, 1, head_dim]")
+    check(quantized_key.dim() == 4, "quantized_key must be [batch, kv_heads, quantized_len, head_dim]")
+    check(value_data.dim() == 4, "value_data must be [batch, kv_heads, quantized_len, packed_dim]")
+    check(value_scales.dim() == 4, "value_scales must be [batch, kv_heads, quantized_len, value_groups]")
+    check(value_zeros.dim() == 4, "value_zeros must be [batch, kv_heads, quantized_len, value_groups]")
+    check(residual_key.dim() == 4, "residual_key must be [batch, kv_heads, residual_len, head_dim]")
+    check(residual_value.dim() == 4, "residual_value must be [batch, kv_heads, residual_len, head_dim]")
+    check(query.size(2) == 1, "gqa_decode_splitkv_turboquant_fused only supports single-token query")
+    check(query.size(0) == quantized_key.size(0), "query/quantized_key batch size mismatch")
+    check(query.size(0) == residual_key.size(0), "query/residual_key batch size mismatch")
+    check(residual_key.shape == residual_value.shape, "residual_key and residual_value must share the same shape")
+    check(quantized_key.size(1) == residual_key.size(1), "quantized and residual KV head count mismatch")
+    check(quantized_key.size(1) >= 1, "kv_heads must be positive")
+    check(query.size(1) % quantized_key.size(1) == 0, "query heads must be divisible by kv_heads")
+    check(query.size(3) == quantized_key.size(3), "query/quantized_key head_dim mismatch")
+    check(query.size(3) == residual_key.size(3), "query/residual_key head_dim mismatch")
+    check(quantized_key.size(2) >= 1,
+          "gqa_decode_splitkv_turboquant_fused requires a non-empty quantized prefix")
+    check(value_data.size(0) == quantized_key.size(0), "value_data batch size mismatch")
+    check(value_data.size(1) == quantized_key.size(1), "value_data kv head count mismatch")
+    check(value_data.size(2) == quantized_key.size(2), "value_data quantized_len mismatch")
+    check(value_scales.size(0) == quantized_key.size(0), "value_scales batch size mismatch")
+    check(value_scales.size(1) == quantized_key.size(1), "value_scales kv head count mismatch")
+    check(value_scales.size(2) == quantized_key.size(2), "value_scales quantized_len mismatch")
+    check(value_zeros.shape == value_scales.shape, "value_zeros shape must match value_scales")
+    check(value_bits in (2, 3, 4), "TurboQuant value_bits must be 2, 3, or 4")
+    check(value_group_size > 0, "TurboQuant value_group_size must be positive")
+    d = query.size(3)
+    check(d % value_group_size == 0, "TurboQuant value_group_size must evenly divide head_dim")
+    check(value_scales.size(3) * value_group_size == d, "TurboQuant value group count/head_dim mismatch")
+    per = 4 if value_bits == 2 else 2
+    check(value_data.size(3) * per >= d, "TurboQuant packed value width is smaller than head_dim")
+    check(block_size >= 16, "gqa_decode_splitkv_turboquant_fused block_size must be at least 16")
+    check(value_data.dtype == torch.uint8, "TurboQuant value_data must be uint8")
+    check(query.dtype == quantized_key.dtype == residual_key.dtype == residual_value.dtype
+          == value_scales.dtype == value_zeros.dtype,
+          "query, keys, residual values, value_scales, and value_zeros must share the same dtype")
+    check(query.dtype in (torch.float16, torch.bfloat16, torch.float32),
+          "gqa_decode_splitkv_turboquant_fused XPU kernel supports float16, bfloat16, and float32 inputs")
+
+
 def _gqa_decode_splitkv_turboquant_fused_out_impl(query, quantized_key, value_data, value_scales, value_zeros,
                                                   residual_key, residual_value, output, partial_stats,
                                                   partial_values, scaling, value_bits, value_group_size,
                                                   block_size, gate=None):
-    # checks of validate_gqa_decode_splitkv_turboquant_inputs (sycl:1412-1500)
+    # checks of validate_gqa_decode_splitkv_turboquant_inputs (sycl:1447-1501), same order and messages
     name = "gqa_decode_splitkv_turboquant_fused_out"
-    for t, what in ((query, "query"), (quantized_key, "quantized_key"), (value_data, "value_data"),
-                    (value_scales, "value_scales"), (value_zeros, "value_zeros"), (residual_key, "residual_key"),
-                    (residual_value, "residual_value")):
-        if t.dim() != 4:
-            raise RuntimeError(f"{what} must be 4-D")
-    if query.size(2) != 1:
-        raise RuntimeError("gqa_decode_splitkv_turboquant_fused only supports single-token query")
-    if residual_key.shape != residual_value.shape:
-        raise RuntimeError("residual_key and residual_value must share the same shape")
-    if quantized_key.size(1) != residual_key.size(1):
-        raise RuntimeError("quantized and residual KV head count mismatch")
-    if query.size(1) % quantized_key.size(1) != 0:
-        raise RuntimeError("query heads must be divisible by kv_heads")
-    if quantized_key.size(2) < 1:
-        raise RuntimeError("gqa_decode_splitkv_turboquant_fused requires a non-empty quantized prefix")
-    if value_bits not in (2, 3, 4):
-        raise RuntimeError("TurboQuant value_bits must be 2, 3, or 4")
-    d = query.size(3)
-    if value_group_size <= 0 or d % value_group_size != 0:
-        raise RuntimeError("TurboQuant value_group_size must evenly divide head_dim")
-    if value_scales.size(3) * value_group_size != d:
-        raise RuntimeError("TurboQuant value group count/head_dim mismatch")
-    per = 4 if value_bits == 2 else 2
-    if value_data.size(3) * per < d:
-        raise RuntimeError("TurboQuant packed value width is smaller than head_dim")
-    if value_data.dtype != torch.uint8:
-        raise RuntimeError("TurboQuant value_data must be uint8")
-    if block_size < 16:
-        raise RuntimeError("gqa_decode_splitkv_turboquant_fused block_size must be at least 16")
-    if not (query.dtype == quantized_key.dtype == residual_key.dtype == residual_value.dtype
-            == value_scales.dtype == value_zeros.dtype):
-        raise RuntimeError("query, keys, residual values, value_scales, and value_zeros must share the same dtype")
+    _check_turboquant_inputs(query, quantized_key, value_data, value_scales, value_zeros, residual_key,
+                             residual_value, value_bits, value_group_size, block_size)
     key_len = quantized_key.size(2) + residual_key.size(2)
     _check_workspace(query, key_len, block_size, output, partial_stats, partial_values, name)
+    _check_gate(gate, query)
     _lib.require_device(query, quantized_key, value_data, value_scales, value_zeros, residual_key, residual_value,
                         output, partial_stats, partial_values, gate)
     a = decode_args(query=query, len1=quantized_key.size(2), key=quantized_key, value=value_data,
@@ -691,8 +729,17 @@ def moe_scatter(compact_outputs, sorted_token_idx, num_tokens):
 
 
 def moe_combine(compact_outputs, route_pos, num_tokens, top_k, out=None):
-    """Deterministic scatter through the route positions kept from moe_dispatch."""
+    """Deterministic scatter through the route positions kept from moe_dispatch
+    (route_pos int64 [num_tokens * top_k]: the compact row of token t's k-th route)."""
+    if compact_outputs.dim() != 2:
+        raise RuntimeError("moe_combine: compact_outputs must be [routes, hidden]")
+    if route_pos.dtype != torch.int64 or route_pos.numel() != int(num_tokens) * int(top_k):
+        raise RuntimeError("moe_combine: route_pos must be int64 with num_tokens * top_k elements")
+    if int(num_tokens) * int(top_k) > compact_outputs.shape[0]:
+        raise RuntimeError("moe_combine: fewer compact rows than num_tokens * top_k")
+    _check_same_device("moe_combine", compact_outputs, route_pos)
     co = compact_outputs.contiguous()
+    route_pos = route_pos.contiguous()
     h = co.shape[1]
     if out is None:
         out = torch.empty((num_tokens, h), dtype=co.dtype, device=co.device)
@@ -768,10 +815,14 @@ def moe_grouped_int4_mlp_out(compact_hidden_states, compact_routing_weights, com
     if items is not None and (items.dtype != torch.int32 or not items.is_contiguous()
                               or items.numel() < 4 + 4 * active_experts.numel() or items.device != x.device):
         raise RuntimeError("items must be a contiguous int32 tensor of >= 4 + 4 * active experts on the device")
-    a = moe_mlp_args(x, cw, compact_outputs, expert_offsets.contiguous(), active_experts.contiguous(),
-                     active_slots.contiguous(), *bank, group_size, activation, max_routes_per_expert, items,
-                     items_prefilled)
+    # every tensor whose pointer goes into the args stays bound to a local until the launch
+    offsets = expert_offsets.contiguous()
+    experts = active_experts.contiguous()
+    slots = active_slots.contiguous()
+    a = moe_mlp_args(x, cw, compact_outputs, offsets, experts, slots, *bank, group_size, activation,
+                     max_routes_per_expert, items, items_prefilled)
     _lib.call("anna_mi_moe_grouped_int4_mlp", ctypes.byref(a), _lib.stream_of(x))
+    del offsets, experts, slots, bank, cw, x
     return compact_outputs
 
 

@@ -38,6 +38,9 @@ extern "C" {
 
 const char* anna_mi_last_error(void);
 int anna_mi_abi_version(void);
+/* sha256 (hex) of the csrc/ and include/ files the library was built from; no
+ * counterpart in the reference (provenance of the shipped binary). */
+const char* anna_mi_source_hash(void);
 
 /* ------------------------------------------------------------------ int4 linear
  * Weight layout (XPUInt4Linear buffers, src/anna/model/quantization.py:460-487):

@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_every_declared_symbol_has_a_binding():
     for name in declared_symbols():
-        if name in ("anna_mi_last_error", "anna_mi_abi_version"):
+        if name in ("anna_mi_last_error", "anna_mi_abi_version", "anna_mi_source_hash"):
             continue
         assert name in _lib.PROTOTYPES or name in _lib.RAW_PROTOTYPES, f"{name} has no ctypes prototype"
 
@@ -37,6 +37,13 @@ def test_decode_args_binding_matches_the_c_struct():
 
     assert _lib.load().anna_mi_sizeof_decode_args() == ctypes.sizeof(_lib.DecodeArgs)
     assert _lib.load().anna_mi_sizeof_tq_decode_args() == ctypes.sizeof(_lib.TQDecodeArgs)
+    assert _lib.load().anna_mi_sizeof_moe_mlp_args() == ctypes.sizeof(_lib.MoeMlpArgs)
+
+
+def test_library_is_stamped_with_the_tree_sources():
+    from anna_amd import build
+
+    assert _lib.load().anna_mi_source_hash().decode() == build.source_hash()
 
 
 def test_abi_version_matches_header():

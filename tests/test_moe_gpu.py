@@ -200,3 +200,36 @@ def test_sparse_moe_block_matches_cpu_chain(gpu, tokens):
     co = cp.moe_grouped_mlp(compact, cw, off, dequant_experts(bank, range(e)), torch.float64)
     ref = torch.zeros(tokens, h, dtype=torch.float64).index_add_(0, tok, co)
     assert rel_err(out.cpu().double().numpy(), ref.numpy()) <= BF16_TOL
+
+
+@pytest.mark.parametrize("tokens", [8, 64, 512])
+def test_sparse_moe_block_config5_dims(gpu, tokens):
+    """BASELINE config 5 at its own dims: 128 experts, top-8 of softmax(N(0,1) logits),
+    H=2048, I=512, group 128, bf16 scales.  T=512 gives ~32 routes per expert (multi-sweep
+    experts); T=8 and 64 take the one-launch routing path.  Both the block (device item list)
+    and the op with a host-known max_routes_per_expert (the reference caller's form) are
+    checked against the fp64 brute force over the dequantized bank."""
+    print(f"[case] moe config5 dims tokens={tokens}", flush=True)
+    torch.manual_seed(500 + tokens)
+    e, k, h, i, group = 128, 8, 2048, 512, 128
+    bank = make_bank(e, h, i, group, torch.bfloat16, gpu, seed=77)
+    block = SparseMoeInt4(bank, num_experts=e, top_k=k)
+    hidden = torch.randn(tokens, h, device=gpu, dtype=torch.bfloat16)
+    logits = torch.randn(tokens, e, device=gpu, dtype=torch.float32)
+    out = block(hidden, logits)
+    w, sel, usage = cp.moe_route(logits.cpu(), k, True)
+    tok, rte, off = cp.moe_sorted_assignments(sel, usage, e)
+    active = [x for x in range(e) if int(usage[x]) > 0]
+    deq = dequant_experts(bank, active)
+    compact = hidden.cpu().index_select(0, tok)
+    cw = w.to(torch.bfloat16)[tok, rte].unsqueeze(1)
+    co = cp.moe_grouped_mlp(compact, cw, off, deq, torch.float64)
+    ref = torch.zeros(tokens, h, dtype=torch.float64).index_add_(0, tok, co)
+    assert rel_err(out.cpu().double().numpy(), ref.numpy()) <= BF16_TOL
+    # the op itself, every active expert listed by the host, max_routes from the usage
+    gw, gsel, gusage = fused_ops.moe_router(logits, k, True)
+    sti, goff, gcompact, gcw = fused_ops.moe_dispatch(hidden, gw.to(torch.bfloat16), gsel, gusage)
+    act_t = torch.tensor(active, dtype=torch.int64, device=gpu)
+    res = torch.ops.anna.moe_grouped_int4_mlp_fused(gcompact, gcw, torch.empty_like(gcompact), goff, act_t, act_t,
+                                                   *bank.tensors(), group, int(gusage.max()))
+    assert rel_err(res.cpu().double().numpy(), co.numpy()) <= BF16_TOL

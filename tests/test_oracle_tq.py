@@ -111,19 +111,43 @@ def test_mse_distortion_matches_turboquant_paper(bits, expected):
     assert abs(mse - expected) / expected < 0.12, mse
 
 
-def test_mse_quantizer_special_cases():
-    d = 64
-    r = fused_ops.tq_rotation(d, 42).numpy()
-    cent, thr = (t.numpy() for t in fused_ops.tq_codebook(2, d))
-    x = np.zeros((2, d), np.float32)
-    x[1, 3] = 2.0  # basis vector: y = 2 * R[:, 3]
-    codes, norms = orc.tq_mse_quantize(x, orc.F32, r, thr, 2)
-    assert orc.f16_to_f32(norms).tolist() == [0.0, 2.0]
-    # zero vector: every threshold scales to 0 and 0 >= 0 -> top code everywhere (norm 0)
-    assert codes[0].tolist() == [0xFF] * (d // 4)
-    y = 2.0 * r[:, 3]
-    expect = (y[:, None] >= thr[None, :] * np.float32(2.0)).sum(1)
-    got = np.stack([(codes[1] >> (2 * k)) & 3 for k in range(4)], -1).reshape(-1)
-    np.testing.assert_array_equal(got, expect)
-    xh = orc.tq_mse_dequant(codes, norms, r, cent, 2)
-    assert np.abs(xh[0]).max() == 0.0
+def test_mse_quantizer_hand_computed_codes():
+    """Identity rotation and hand-chosen thresholds, so every code below is worked out by hand:
+    code_i = number of thresholds t_j with x_i >= t_j * |x|, packed 4 per byte (2-bit, element
+    i at bits 2i) or 2 per byte (4-bit); the norm is |x| in fp16."""
+    eye = np.eye(4, dtype=np.float32)
+    thr = np.array([-0.5, 0.0, 0.5], np.float32)
+    # |x| = 5: thresholds scale to -2.5, 0, 2.5
+    x = np.array([[3.0, 4.0, 0.0, 0.0],    # 3 >= 2.5 -> 3; 4 -> 3; 0 >= 0 -> 2; 0 -> 2
+                  [-3.0, 0.0, -4.0, 0.0],  # -3 < -2.5 -> 0; 0 -> 2; -4 -> 0; 0 -> 2
+                  [2.5, -2.5, 0.0, 0.0],   # ties: 2.5 >= 2.5 -> 3; -2.5 >= -2.5 -> 1
+                  [0.0, 0.0, 0.0, 0.0]],   # zero vector: 0 >= 0 for every threshold -> 3
+                 np.float32)
+    x[2, 2] = np.sqrt(np.float32(25.0) - np.float32(12.5))  # keep |x| = 5 (3.5355...) -> 3
+    codes, norms = orc.tq_mse_quantize(x, orc.F32, eye, thr, 2)
+    want = [[3, 3, 2, 2], [0, 2, 0, 2], [3, 1, 3, 2], [3, 3, 3, 3]]
+    packed = [c[0] | (c[1] << 2) | (c[2] << 4) | (c[3] << 6) for c in want]
+    assert codes[:, 0].tolist() == packed
+    assert orc.f16_to_f32(norms).tolist() == [5.0, 5.0, float(np.float16(np.sqrt(np.float32(25.0)))), 0.0]
+    # dequant: |x|_fp16 * centroid[code], rotation back by the identity
+    cent = np.array([-0.75, -0.25, 0.25, 0.75], np.float32)
+    xh = orc.tq_mse_dequant(codes, norms, eye, cent, 2)
+    np.testing.assert_array_equal(xh[0], [3.75, 3.75, 1.25, 1.25])
+    np.testing.assert_array_equal(xh[1], [-3.75, 1.25, -3.75, 1.25])
+    np.testing.assert_array_equal(xh[3], [0.0, 0.0, 0.0, 0.0])
+
+
+def test_mse_quantizer_hand_computed_four_bit():
+    # 4-bit: 15 thresholds -7/16 .. 7/16 (times |x| = 1): code = #{t_j <= x_i}
+    eye = np.eye(2, dtype=np.float32)
+    thr = (np.arange(-7, 8, dtype=np.float32) / 16).astype(np.float32)
+    x = np.array([[0.6, 0.8]], np.float32)  # |x| rounds to 1 in fp32
+    codes, norms = orc.tq_mse_quantize(x, orc.F32, eye, thr, 4)
+    nrm = np.float32(np.sqrt(np.float32(0.6) * np.float32(0.6) + np.float32(0.8) * np.float32(0.8)))
+    c0 = int((x[0, 0] >= thr * nrm).sum())  # 0.6 >= 7/16: all 15
+    c1 = int((x[0, 1] >= thr * nrm).sum())
+    assert (c0, c1) == (15, 15)
+    assert codes.tolist() == [[15 | (15 << 4)]]
+    x = np.array([[0.1, -0.995]], np.float32)  # 0.1: t <= 0.1 for t in -7/16..1/16 -> 9; -0.995 -> 0
+    codes, _ = orc.tq_mse_quantize(x, orc.F32, eye, thr, 4)
+    assert codes.tolist() == [[9 | (0 << 4)]]
