@@ -77,6 +77,7 @@ PROTOTYPES.update({
     "anna_mi_tq_values_quantize": [_P, _I, _I64, _I64, _I64, _I64, _I64, _I, _I64, _P, _P, _P, _P],
     "anna_mi_tq_values_dequant": [_P, _P, _P, _I, _I64, _I64, _I, _I64, _P, _I, _P],
     "anna_mi_gqa_decode_splitkv": [ctypes.POINTER(DecodeArgs), _P],
+    "anna_mi_gqa_decode_splitkv_noalloc": [ctypes.POINTER(DecodeArgs), _P],
 })
 
 
@@ -116,6 +117,7 @@ RAW_PROTOTYPES: dict[str, tuple] = {
     "anna_mi_sizeof_moe_mlp_args": (_I64, []),
     "anna_mi_decode_num_blocks": (_I64, [ctypes.POINTER(DecodeArgs)]),
     "anna_mi_sizeof_decode_args": (_I64, []),
+    "anna_mi_gqa_decode_splitkv_noalloc_capacity": (_I64, []),
     "anna_mi_sizeof_tq_decode_args": (_I64, []),
 }
 

@@ -15,6 +15,7 @@
 //
 // Reference: launch_gqa_decode_splitkv_fused_xpu (gated_delta_fused_op.sycl:4494-4706)
 // and launch_gqa_decode_splitkv_turboquant_fused_xpu (sycl:4771-5094).
+#include <mutex>
 #include <type_traits>
 
 #include "common.hpp"
@@ -553,9 +554,7 @@ extern "C" int64_t anna_mi_decode_num_blocks(const anna_mi_decode_args* a) {
   return total_blocks(*a, make_split(*a));
 }
 
-extern "C" int anna_mi_gqa_decode_splitkv(const anna_mi_decode_args* ap, void* stream) {
-  ANNA_CHECK(ap != nullptr, "anna_mi_gqa_decode_splitkv: null args");
-  const anna_mi_decode_args& a = *ap;
+static int gqa_decode_splitkv_impl(const anna_mi_decode_args& a, void* stream) {
   ANNA_CHECK(valid_dtype(a.dtype), "anna_mi_gqa_decode_splitkv: bad dtype code");
   ANNA_CHECK(a.batch > 0 && a.q_heads > 0 && a.kv_heads > 0, "anna_mi_gqa_decode_splitkv: empty batch or heads");
   ANNA_CHECK(a.q_heads % a.kv_heads == 0, "query heads must be divisible by kv_heads");
@@ -622,4 +621,77 @@ extern "C" int anna_mi_gqa_decode_splitkv(const anna_mi_decode_args* ap, void* s
                      (size_t)a.head_dim * 4, st, a, nblk, nrot);
   ANNA_LAUNCH_CHECK("decode_merge_kernel");
   return ANNA_MI_OK;
+}
+
+extern "C" int anna_mi_gqa_decode_splitkv(const anna_mi_decode_args* ap, void* stream) {
+  ANNA_CHECK(ap != nullptr, "anna_mi_gqa_decode_splitkv: null args");
+  return gqa_decode_splitkv_impl(*ap, stream);
+}
+
+// ------------------------------------------------------------------ allocation-free variant
+//
+// The workspace of anna_mi_gqa_decode_splitkv (partial stats, partial values and, with TQ-MSE
+// keys, the rotated query) lives in one file-scope device array per GPU instead of caller
+// tensors.  Every call on a GPU shares that GPU's array: calls that overlap on one GPU (two
+// streams, two threads) race.  Nothing in it has to start at zero: the split kernel writes
+// every partial the merge reads, and the rotation kernel every rotated query entry.
+namespace {
+
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;  // 32 MiB per GPU
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+unsigned char* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (looked up once per device; the array's
+// host-side name is not a device address).
+int scratch_of_current_device(unsigned char** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail_hip(e, "anna_mi_gqa_decode_splitkv_noalloc: hipGetDevice");
+  ANNA_CHECK(dev >= 0 && dev < kMaxDevices, "anna_mi_gqa_decode_splitkv_noalloc: device index %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return fail_hip(e, "anna_mi_gqa_decode_splitkv_noalloc: hipGetSymbolAddress(scratch)");
+    ANNA_CHECK(p != nullptr, "anna_mi_gqa_decode_splitkv_noalloc: no device address for the scratch array");
+    g_scratch_ptr[dev] = (unsigned char*)p;
+  }
+  *out = g_scratch_ptr[dev];
+  return ANNA_MI_OK;
+}
+
+}  // namespace
+
+extern "C" int64_t anna_mi_gqa_decode_splitkv_noalloc_capacity(void) { return (int64_t)kNoAllocScratchBytes; }
+
+extern "C" int anna_mi_gqa_decode_splitkv_noalloc(const anna_mi_decode_args* ap, void* stream) {
+  ANNA_CHECK(ap != nullptr, "anna_mi_gqa_decode_splitkv_noalloc: null args");
+  anna_mi_decode_args a = *ap;
+  ANNA_CHECK(a.batch > 0 && a.q_heads > 0 && a.head_dim > 0 && a.len1 >= 0 && a.len2 >= 0 && a.len1 + a.len2 >= 1,
+             "anna_mi_gqa_decode_splitkv_noalloc: empty batch, heads or keys");
+  const int64_t nblk = total_blocks(a, make_split(a));
+  const int64_t rows = a.batch * a.q_heads;
+  const bool qrot = a.key_format == ANNA_MI_KEYS_TQ_MSE && a.len1 > 0;
+  // [B][Hq][nblk][2] stats, [B][Hq][nblk][D] values, [B][Hq][D] rotated query (fp32, 256-byte aligned parts)
+  auto up = [](int64_t n) { return (n + 63) / 64 * 64; };
+  const int64_t n_stats = up(rows * nblk * 2), n_values = up(rows * nblk * a.head_dim);
+  const int64_t n_qrot = qrot ? up(rows * a.head_dim) : 0;
+  const int64_t need = (n_stats + n_values + n_qrot) * 4;
+  ANNA_CHECK(need <= (int64_t)kNoAllocScratchBytes,
+             "anna_mi_gqa_decode_splitkv_noalloc: workspace of %lld bytes (batch %lld, %lld heads, %lld blocks, head_dim "
+             "%lld) exceeds the %lld-byte static scratch; use anna_mi_gqa_decode_splitkv with a caller workspace",
+             (long long)need, (long long)a.batch, (long long)a.q_heads, (long long)nblk, (long long)a.head_dim,
+             (long long)kNoAllocScratchBytes);
+  unsigned char* base = nullptr;
+  int rc = scratch_of_current_device(&base);
+  if (rc != ANNA_MI_OK) return rc;
+  float* f = (float*)base;
+  a.partial_stats = anna_mi_view{f, a.q_heads * nblk * 2, nblk * 2, 2, 1};
+  a.partial_values = anna_mi_view{f + n_stats, a.q_heads * nblk * a.head_dim, nblk * a.head_dim, a.head_dim, 1};
+  a.partial_capacity = nblk;
+  a.query_rot = qrot ? f + n_stats + n_values : nullptr;
+  return gqa_decode_splitkv_impl(a, stream);
 }

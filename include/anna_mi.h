@@ -195,6 +195,18 @@ int64_t anna_mi_decode_num_blocks(const anna_mi_decode_args* args);
  * All q-heads of a KV group share one workgroup and one read of each K/V token. */
 int anna_mi_gqa_decode_splitkv(const anna_mi_decode_args* args, void* stream);
 
+/* Allocation-free form of anna_mi_gqa_decode_splitkv.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  The partial_stats, partial_values,
+ * partial_capacity and query_rot fields of args are ignored; that workspace lives in a static
+ * device array of anna_mi_gqa_decode_splitkv_noalloc_capacity() bytes (32 MiB) per GPU, held
+ * until the process ends.  The call fails with ANNA_MI_EINVAL when the workspace
+ * (4 * (B*Hq*nblk*(D+2) + B*Hq*D) bytes, nblk = anna_mi_decode_num_blocks) does not fit.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU race.  It
+ * allocates nothing and launches the same kernels, so results equal anna_mi_gqa_decode_splitkv's. */
+int anna_mi_gqa_decode_splitkv_noalloc(const anna_mi_decode_args* args, void* stream);
+int64_t anna_mi_gqa_decode_splitkv_noalloc_capacity(void);
+
 /* ------------------------------------------------------------------ batched TQ decode
  * Batched, variable-length single-token GQA decode over a 2-bit TQ-MSE K/V cache
  * (head_dim 256): the batched replacement of the per-row loop of
