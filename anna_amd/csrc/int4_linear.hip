@@ -262,24 +262,30 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
 }
 
-// Butterfly step within 32-lane groups: value of lane (lane ^ MASK).
-template <int MASK>
-__device__ __forceinline__ float swz_xor(float v) {
-  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), (MASK << 10) | 0x1F));
+// v_mov_b32 with a DPP lane pattern (all rows and banks enabled).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
-template <int XDT, int SDT, int MR, int RG>
-__global__ __launch_bounds__(64 * DOT2_MAX_WAVES) void int4_gemv_dot2(
+// Lane (sub, c) of a wave: c = lane % 16 owns k [k0 + 32 c, k0 + 32 c + 32) of the wave's
+// 512-k slice, sub = lane / 16 the rows n0 + 4 sub + g of its four row groups g.  One load
+// instruction (fixed g) covers 4 rows x 256 contiguous bytes; a lane's 4 rows are consecutive,
+// so its 4 scales and 4 zero points are one 8- (16-bit scales) or 16-byte (fp32) load and one
+// 4-byte load.  Every load of a slice is issued before any value is converted: a conversion
+// placed right after its load made the compiler wait for that load before issuing the next.
+template <int XDT, int SDT, int MR, int WMAX, bool VEC_SZ>
+__global__ __launch_bounds__(64 * WMAX) void int4_gemv_dot2(
     const uint16_t* __restrict__ x, int64_t M, int64_t K, int64_t xs,
     const uint32_t* __restrict__ qw, int64_t N, int64_t pc,
     const typename Elem<SDT>::T* __restrict__ qs, const int8_t* __restrict__ qz,
     int gshift, uint16_t* __restrict__ y) {
-  constexpr int RPI = 4;        // rows per load instruction: 16 lanes x 16 B per row
-  constexpr int RW = RPI * RG;  // rows per workgroup
+  constexpr int RG = 4;         // row groups (loads of W) per lane and slice
+  constexpr int RW = 4 * RG;    // rows per workgroup
   constexpr int KSL = 512;      // k per wave slice
   constexpr float OFF = XDT == ANNA_MI_BF16 ? 128.0f : 1024.0f;
   constexpr uint32_t ONES = XDT == ANNA_MI_BF16 ? 0x3F803F80u : 0x3C003C00u;
-  static_assert(RG == 4 || RG == 8 || RG == 16, "row groups");
+  constexpr int SB = (int)sizeof(typename Elem<SDT>::T);
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int kw = blockDim.x >> 6;
@@ -289,9 +295,10 @@ __global__ __launch_bounds__(64 * DOT2_MAX_WAVES) void int4_gemv_dot2(
   // Weight rows of this workgroup; rows >= N fall outside num_records and read 0.
   const int64_t rows_here = N - n0 < RW ? N - n0 : RW;
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(qw + n0 * pc, (uint32_t)(rows_here * pc * 4));
-  const __amdgpu_buffer_rsrc_t rs = make_rsrc(qs, (uint32_t)(G * N * sizeof(typename Elem<SDT>::T)));
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(qs, (uint32_t)(G * N * SB));
   const __amdgpu_buffer_rsrc_t rz = make_rsrc(qz, (uint32_t)(G * N));
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)(((M - 1) * xs + K) * 2));
+  // VEC_SZ: one vector load of a lane's 4 scales / zero points (N % 4 == 0: 4-row aligned rows)
 
   float yacc[MR][RG];
 #pragma unroll
@@ -299,54 +306,102 @@ __global__ __launch_bounds__(64 * DOT2_MAX_WAVES) void int4_gemv_dot2(
 #pragma unroll
     for (int g = 0; g < RG; ++g) yacc[m][g] = 0.f;
 
-  for (int64_t k0 = (int64_t)wave * KSL; k0 < K; k0 += (int64_t)kw * KSL) {
+  // x of a pass (kw * 512 k) is staged in LDS once per workgroup, already in nibble-pair order,
+  // with the sum of every 32-k chunk (the zero-point term): thread t loads x[8 t .. 8 t + 7].
+  __shared__ u32x4 s_x[MR][64 * WMAX];
+  __shared__ float s_xsum[MR][16 * WMAX];
+  auto pass = [&](int64_t p0) {
+    const int64_t k0 = p0 + (int64_t)wave * KSL;
     const int64_t kl = k0 + c * 32;
     const bool k_ok = kl < K;
-    // x first (in-order returns: it never waits behind the weights).
-    u32x4 xv[MR][4];
+    u32x4 xg[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
-      const uint32_t xo = (k_ok && m < M) ? (uint32_t)((m * xs + kl) * 2) : OOB;
+      const int64_t kx = p0 + 8 * (int64_t)threadIdx.x;
+      const uint32_t xo = (kx < K && m < M) ? (uint32_t)((m * xs + kx) * 2) : OOB;
+      xg[m] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0));
+    }
+    // scales and zero points (small, ahead of the weights they scale), kept raw
+    const int64_t grp = k_ok ? kl >> gshift : 0;
+    const uint32_t so = k_ok ? (uint32_t)(grp * N + n0 + 4 * sub) : OOB / 4;
+    u32x4 svec = {0u, 0u, 0u, 0u};
+    uint32_t zvec = 0, sg[RG], zg[RG];
+    if constexpr (VEC_SZ) {
+      if constexpr (SDT == ANNA_MI_F32) {
+        svec = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, so * 4, 0, 0));
+      } else {
+        const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, so * 2, 0, 0));
+        svec.x = v.x, svec.y = v.y;
+      }
+      zvec = __builtin_amdgcn_raw_buffer_load_b32(rz, so, 0, 0);
+    } else {
 #pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4)
-        xv[m][s4] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, xo, s4 * 16, 0));
+      for (int g = 0; g < RG; ++g) {
+        sg[g] = SDT == ANNA_MI_F32 ? __builtin_amdgcn_raw_buffer_load_b32(rs, so * 4, g * 4, 0)
+                                   : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, so * 2, g * 2, 0);
+        zg[g] = __builtin_amdgcn_raw_buffer_load_b8(rz, so, g, 0);
+      }
     }
     u32x4 wv[RG];
+    const uint32_t wo = k_ok ? (uint32_t)((4 * sub * pc + (kl >> 3)) * 4) : OOB;
+#pragma unroll
+    for (int g = 0; g < RG; ++g)
+      wv[g] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            rw, wo, (int)(g * pc * 4), 2 /* slc: streamed once */));
+    __builtin_amdgcn_sched_barrier(0);
+    if (p0 > 0) __syncthreads();  // the previous pass is done reading s_x
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      const u32x4 iv = interleave_x(xg[m]);
+      s_x[m][threadIdx.x] = iv;
+      float t = dot2_acc<XDT>(iv.x, ONES, 0.f);
+      t = dot2_acc<XDT>(iv.y, ONES, t);
+      t = dot2_acc<XDT>(iv.z, ONES, t);
+      t = dot2_acc<XDT>(iv.w, ONES, t);
+      t += dpp_f32<0xB1>(t);  // quad_perm [1, 0, 3, 2]
+      t += dpp_f32<0x4E>(t);  // quad_perm [2, 3, 0, 1]
+      if ((threadIdx.x & 3) == 0) s_xsum[m][threadIdx.x >> 2] = t;
+    }
+    __syncthreads();
+    uint32_t sraw[RG];
+    uint32_t zraw = 0;
+    if constexpr (VEC_SZ) {
+      if constexpr (SDT == ANNA_MI_F32) {
+        sraw[0] = svec.x, sraw[1] = svec.y, sraw[2] = svec.z, sraw[3] = svec.w;
+      } else {
+        sraw[0] = svec.x, sraw[1] = svec.x >> 16, sraw[2] = svec.y, sraw[3] = svec.y >> 16;
+      }
+      zraw = zvec;
+    } else {
+#pragma unroll
+      for (int g = 0; g < RG; ++g) {
+        sraw[g] = sg[g];
+        zraw |= (zg[g] & 0xFFu) << (8 * g);
+      }
+    }
     float sc[RG], cz[RG];
-    const uint32_t wo = k_ok ? (uint32_t)((sub * pc + (kl >> 3)) * 4) : OOB;
-    const int64_t grp = k_ok ? kl >> gshift : 0;
-    const uint32_t so = k_ok ? (uint32_t)(grp * N + n0 + sub) : OOB / 4;
 #pragma unroll
     for (int g = 0; g < RG; ++g) {
-      wv[g] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                            rw, wo, (int)(g * RPI * pc * 4), 2 /* slc: streamed once */));
-      if constexpr (SDT == ANNA_MI_F32) {
-        sc[g] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, so * 4, g * RPI * 4, 0));
-      } else {
-        const uint32_t h = __builtin_amdgcn_raw_buffer_load_b16(rs, so * 2, g * RPI * 2, 0);
-        sc[g] = SDT == ANNA_MI_BF16 ? __uint_as_float(h << 16) : f16_bits_to_f32((uint16_t)h);
-      }
-      cz[g] = OFF + (float)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(rz, so, g * RPI, 0);
+      if constexpr (SDT == ANNA_MI_F32) sc[g] = __uint_as_float(sraw[g]);
+      else if constexpr (SDT == ANNA_MI_BF16) sc[g] = __uint_as_float(sraw[g] << 16);
+      else sc[g] = f16_bits_to_f32((uint16_t)(sraw[g] & 0xFFFFu));
+      cz[g] = OFF + (float)(int8_t)(zraw >> (8 * g));
     }
-    // x to nibble-pair order; its sum by dot2 against ones (the zero-point term)
+    // this lane's 32 k: threads 4 (16 wave + c) .. + 3 of the staging
+    const int xi = 4 * (16 * wave + c);
     uint32_t xp[MR][16];
     float sx[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
-      float t = 0.f;
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4) {
-        const u32x4 iv = interleave_x(xv[m][s4]);
+        const u32x4 iv = s_x[m][xi + s4];
         xp[m][s4 * 4 + 0] = iv.x;
         xp[m][s4 * 4 + 1] = iv.y;
         xp[m][s4 * 4 + 2] = iv.z;
         xp[m][s4 * 4 + 3] = iv.w;
-        t = dot2_acc<XDT>(iv.x, ONES, t);
-        t = dot2_acc<XDT>(iv.y, ONES, t);
-        t = dot2_acc<XDT>(iv.z, ONES, t);
-        t = dot2_acc<XDT>(iv.w, ONES, t);
       }
-      sx[m] = t;
+      sx[m] = s_xsum[m][16 * wave + c];
     }
 #pragma unroll
     for (int g = 0; g < RG; ++g) {
@@ -367,44 +422,46 @@ __global__ __launch_bounds__(64 * DOT2_MAX_WAVES) void int4_gemv_dot2(
 #pragma unroll
       for (int m = 0; m < MR; ++m) yacc[m][g] = fmaf(sc[g], fmaf(-cz[g], sx[m], acc[m]), yacc[m][g]);
     }
+  };
+  // one pass covers K when the workgroup has enough waves (the common case): straight-line code
+  if (K <= (int64_t)kw * KSL) {
+    pass(0);
+  } else {
+    for (int64_t p0 = 0; p0 < K; p0 += (int64_t)kw * KSL) pass(p0);
   }
-  // Reduce-scatter across the 16 lanes of a row: after the butterfly, lane c holds the
-  // full sum of row group (c >> (4 - log2 RG)) ... see index below.
+  // Reduce-scatter over the 16 lanes of a DPP row (the lanes c of one sub): each stage pairs a
+  // lane with one whose bit b of c differs (row_mirror flips bit 3, row_half_mirror bit 2, quad
+  // permutations bits 1 and 0), keeps the half of the list that bit selects and adds the
+  // partner's copy of it.  Afterwards lane c holds row group (c >> 3 & 1) * 2 + (c >> 2 & 1)
+  // summed over the row.
   float red_v[MR];
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
     float v[RG];
 #pragma unroll
     for (int g = 0; g < RG; ++g) v[g] = yacc[m][g];
-    // stage on lane bit 3: keep the half selected by that bit
-    auto stage = [&](auto mask_tag, int half, float* vals) {
-      constexpr int MASK = decltype(mask_tag)::value;
-      const bool upper = (c & MASK) != 0;
-      for (int i = 0; i < half; ++i) {
-        const float mine = upper ? vals[i + half] : vals[i];
-        const float give = upper ? vals[i] : vals[i + half];
-        vals[i] = mine + swz_xor<MASK>(give);
+    {
+      const bool up = (c >> 3) & 1;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const float mine = up ? v[i + 2] : v[i], give = up ? v[i] : v[i + 2];
+        v[i] = mine + dpp_f32<0x140>(give);  // row_mirror
       }
-    };
-    using M8 = std::integral_constant<int, 8>;
-    using M4 = std::integral_constant<int, 4>;
-    using M2 = std::integral_constant<int, 2>;
-    using M1 = std::integral_constant<int, 1>;
-    if constexpr (RG == 16) { stage(M8{}, 8, v); stage(M4{}, 4, v); stage(M2{}, 2, v); stage(M1{}, 1, v); }
-    if constexpr (RG == 8) { stage(M8{}, 4, v); stage(M4{}, 2, v); stage(M2{}, 1, v); v[0] += swz_xor<1>(v[0]); }
-    if constexpr (RG == 4) { stage(M8{}, 2, v); stage(M4{}, 1, v); v[0] += swz_xor<2>(v[0]); v[0] += swz_xor<1>(v[0]); }
+    }
+    {
+      const bool up = (c >> 2) & 1;
+      const float mine = up ? v[1] : v[0], give = up ? v[0] : v[1];
+      v[0] = mine + dpp_f32<0x141>(give);  // row_half_mirror
+    }
+    v[0] += dpp_f32<0x4E>(v[0]);  // quad_perm [2, 3, 0, 1]
+    v[0] += dpp_f32<0xB1>(v[0]);  // quad_perm [1, 0, 3, 2]
     red_v[m] = v[0];
   }
-  // Row group held by lane c: bits 3,2,1,0 of c select halves in order (MSB first).
-  int gsel;
-  if constexpr (RG == 16) gsel = ((c >> 3) & 1) * 8 + ((c >> 2) & 1) * 4 + ((c >> 1) & 1) * 2 + (c & 1);
-  else if constexpr (RG == 8) gsel = ((c >> 3) & 1) * 4 + ((c >> 2) & 1) * 2 + ((c >> 1) & 1);
-  else gsel = ((c >> 3) & 1) * 2 + ((c >> 2) & 1);
-  const bool writer = RG == 16 ? true : RG == 8 ? (c & 1) == 0 : (c & 3) == 0;
-  __shared__ float red[DOT2_MAX_WAVES][MR][RW];
-  if (writer) {
+  const int gsel = ((c >> 3) & 1) * 2 + ((c >> 2) & 1);
+  __shared__ float red[WMAX][MR][RW];
+  if ((c & 3) == 0) {
 #pragma unroll
-    for (int m = 0; m < MR; ++m) red[wave][m][gsel * RPI + sub] = red_v[m];
+    for (int m = 0; m < MR; ++m) red[wave][m][4 * sub + gsel] = red_v[m];
   }
   __syncthreads();
   for (int i = threadIdx.x; i < MR * RW; i += blockDim.x) {
@@ -741,36 +798,35 @@ extern "C" int anna_mi_int4_linear(const void* x, int x_dtype, int64_t M, int64_
   const bool gsz_pow2 = gsz >= 32 && (gsz & (gsz - 1)) == 0;
   if (x16 && aligned && M <= 2 && K % 32 == 0 && gsz_pow2) {
     const int gshift = __builtin_ctzll((unsigned long long)gsz);
-    static const int env_dot2_rg = env_int("ANNA_MI_INT4_DOT2_RG", 4);
     const int64_t ksl = 16 * 32;
     int64_t waves = (K + ksl - 1) / ksl;
     waves = waves > DOT2_MAX_WAVES ? DOT2_MAX_WAVES : waves;
     ANNA_DISPATCH_DTYPE(scale_dtype, SDT, {
-      auto go = [&](auto xdt_tag, auto mr_tag, auto rg_tag) {
-        constexpr int XDT = decltype(xdt_tag)::value, MR = decltype(mr_tag)::value, RG = decltype(rg_tag)::value;
-        dim3 grid((unsigned)((N + 4 * RG - 1) / (4 * RG)));
-        hipLaunchKernelGGL((int4_gemv_dot2<XDT, SDT, MR, RG>), grid, dim3((unsigned)(64 * waves)), 0, st,
-                           (const uint16_t*)x, M, K, xs, (const uint32_t*)qweight, N, pc,
-                           (const typename Elem<SDT>::T*)qscale, qzeros, gshift, (uint16_t*)y);
+      auto go = [&](auto xdt_tag, auto mr_tag) {
+        constexpr int XDT = decltype(xdt_tag)::value, MR = decltype(mr_tag)::value;
+        dim3 grid((unsigned)((N + 15) / 16));
+        // 8-wave bound where K allows: a 1024-thread bound and LDS sized for 16 waves cost
+        // registers at K = 4096
+        auto launch = [&](auto kern) {
+          hipLaunchKernelGGL(kern, grid, dim3((unsigned)(64 * waves)), 0, st, (const uint16_t*)x, M, K, xs,
+                             (const uint32_t*)qweight, N, pc, (const typename Elem<SDT>::T*)qscale, qzeros, gshift,
+                             (uint16_t*)y);
+        };
+        const bool vec = (N & 3) == 0;
+        if (waves <= 8) {
+          if (vec) launch(int4_gemv_dot2<XDT, SDT, MR, 8, true>);
+          else launch(int4_gemv_dot2<XDT, SDT, MR, 8, false>);
+        } else {
+          if (vec) launch(int4_gemv_dot2<XDT, SDT, MR, DOT2_MAX_WAVES, true>);
+          else launch(int4_gemv_dot2<XDT, SDT, MR, DOT2_MAX_WAVES, false>);
+        }
       };
       using I1 = std::integral_constant<int, 1>;
       using I2 = std::integral_constant<int, 2>;
-      using I4 = std::integral_constant<int, 4>;
-      using I8 = std::integral_constant<int, 8>;
-      using I16 = std::integral_constant<int, 16>;
       using XB = std::integral_constant<int, ANNA_MI_BF16>;
       using XH = std::integral_constant<int, ANNA_MI_F16>;
-      const bool bf = x_dtype == ANNA_MI_BF16;
-      if (env_dot2_rg == 4) {
-        if (bf) { if (M == 1) go(XB{}, I1{}, I4{}); else go(XB{}, I2{}, I4{}); }
-        else { if (M == 1) go(XH{}, I1{}, I4{}); else go(XH{}, I2{}, I4{}); }
-      } else if (env_dot2_rg == 16) {
-        if (bf) { if (M == 1) go(XB{}, I1{}, I16{}); else go(XB{}, I2{}, I16{}); }
-        else { if (M == 1) go(XH{}, I1{}, I16{}); else go(XH{}, I2{}, I16{}); }
-      } else {
-        if (bf) { if (M == 1) go(XB{}, I1{}, I8{}); else go(XB{}, I2{}, I8{}); }
-        else { if (M == 1) go(XH{}, I1{}, I8{}); else go(XH{}, I2{}, I8{}); }
-      }
+      if (x_dtype == ANNA_MI_BF16) { if (M == 1) go(XB{}, I1{}); else go(XB{}, I2{}); }
+      else { if (M == 1) go(XH{}, I1{}); else go(XH{}, I2{}); }
     });
     ANNA_LAUNCH_CHECK("int4_gemv_dot2");
     return ANNA_MI_OK;

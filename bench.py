@@ -49,6 +49,7 @@ def cpu_model() -> str:
 
 
 EAGER = False  # --eager: launch the steps directly (for counter collection runs)
+REPLAYS = 5  # timed replays of each step graph; the median is reported
 
 
 def time_graph(fns, steps: int, warmup: int) -> float:
@@ -80,14 +81,21 @@ def time_graph(fns, steps: int, warmup: int) -> float:
     for _ in range(max(1, warmup // max(1, steps) + 1)):
         graph.replay()
     torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(stream):
-        start.record(stream)
-        graph.replay()
-        end.record(stream)
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+    # median of REPLAYS timed replays of the K-step graph (each bracketed by HIP events on the
+    # stream the kernels run on)
+    times = []
+    for _ in range(REPLAYS):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            start.record(stream)
+            graph.replay()
+            end.record(stream)
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(end))
+    times.sort()
+    ms = times[len(times) // 2]
+    return ms / steps
 
 
 # ---------------------------------------------------------------- int4 linear

@@ -41,6 +41,9 @@ LINEAR_CASES = [
     (1, 96, 40, 32, "fp32"),        # group 32 on the dot2 GEMV, partial k-slice
     (2, 9216, 72, 128, "bf16"),     # dot2 GEMV with more k-slices than waves
     (1, 4096, 12288, 128, "bf16"),  # benchmark config 2, M = 1
+    (1, 512, 102, 128, "bf16"),     # dot2 GEMV, N % 4 != 0: per-row scale / zero loads
+    (2, 1024, 37, 128, "fp32"),     # the same with fp32 scales, M = 2
+    (1, 1024, 4100, 128, "fp32"),   # dot2 GEMV, fp32 scales as one 16-byte load
     (300, 512, 400, 64, "bf16"),    # tiled GEMM: group 64, M and N tails
     (2048, 4096, 192, 128, "bf16"), # tiled GEMM at the config-2 M and K
     (64, 4096, 6144, 128, "fp32"),  # tiled GEMM, config-2 N = 6144 at M = 64
