@@ -72,6 +72,8 @@ PROTOTYPES.update({
     "anna_mi_tq_block_values": [_P, _I64, _P, _P],
     "anna_mi_tq_rotation": [_I64, ctypes.c_uint64, _P],
     "anna_mi_tq_codebook": [_I, _I64, _P, _P],
+    "anna_mi_tq_hadamard_signs": [_I64, ctypes.c_uint64, _P],
+    "anna_mi_tq_hadamard_quantize": [_P, _I, _I64, _I64, _I64, _P, _P, _I, _P, _P, _P],
     "anna_mi_tq_mse_quantize": [_P, _I, _I64, _I64, _I64, _P, _P, _I, _P, _P, _P],
     "anna_mi_tq_mse_dequant": [_P, _P, _I64, _I64, _P, _P, _I, _P, _I, _I64, _P],
     "anna_mi_tq_values_quantize": [_P, _I, _I64, _I64, _I64, _I64, _I64, _I, _I64, _P, _P, _P, _P],

@@ -6,18 +6,23 @@
 //     zero = min stored in the value dtype, codes packed 4 per byte (2-bit) or 2 per byte
 //     (3/4-bit), element i at bits sb*(i % per_byte).
 //   TQ-MSE (this build's definition of the absent `turboquant` package's MSE quantizer,
-//     turboquant.py:75-82): y = R x with a seeded Haar rotation R, code_i = number of
-//     codebook thresholds t_j with y_i >= t_j * |x|, norm |x| stored as fp16; the
-//     reconstruction is |x|_fp16 * R^T c[code].  Codes pack like the values.
+//     turboquant.py:75-82): y = R x with a seeded rotation R, code_i = number of codebook
+//     thresholds t_j with y_i >= t_j * |x|, norm |x| stored as fp16; the reconstruction is
+//     |x|_fp16 * R^T c[code].  Codes pack like the values.  R is the randomized Hadamard
+//     rotation (1/sqrt(D)) H diag(s) for power-of-two D (tq_hadamard.hpp: an O(D log D)
+//     transform in registers), a seeded Haar matrix otherwise.
 //
 // Numerics of the MSE quantizer are fixed so that the GPU reproduces the CPU oracle bit
-// for bit: |x|^2 and every y_i are fma chains in ascending k, sqrt is correctly rounded.
+// for bit: dense R: |x|^2 and every y_i are fma chains in ascending k; Hadamard R: the order
+// of tq_hadamard.hpp; sqrt is correctly rounded.
 #include <math.h>
 #include <stdlib.h>
 
+#include <type_traits>
 #include <vector>
 
 #include "common.hpp"
+#include "tq_hadamard.hpp"
 
 namespace anna {
 namespace {
@@ -26,22 +31,27 @@ __host__ __device__ inline int storage_bits(int bits) { return bits == 2 ? 2 : 4
 
 // ------------------------------------------------------------------ host: rotation, codebook
 
-uint64_t splitmix64(uint64_t& s) {
-  uint64_t z = (s += 0x9E3779B97F4A7C15ull);
-  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
-  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-  return z ^ (z >> 31);
-}
 
-// Haar-distributed orthogonal D x D matrix: a seeded standard-normal matrix (splitmix64
-// stream, Box-Muller) whose rows are orthonormalized by modified Gram-Schmidt applied
-// twice, in fp64, then rounded to fp32.  Row i of the result is R[i][:], y = R x.
+// Power-of-two D: the randomized Hadamard rotation R[i][j] = s_j (-1)^popcount(i & j) / sqrt(D)
+// in fp32.  Otherwise a Haar-distributed orthogonal D x D matrix: a seeded standard-normal
+// matrix (splitmix64 stream, Box-Muller) whose rows are orthonormalized by modified
+// Gram-Schmidt applied twice, in fp64, then rounded to fp32.  Row i of the result is R[i][:],
+// y = R x.
 void make_rotation(int64_t D, uint64_t seed, float* out) {
+  if (tq_is_pow2(D)) {
+    std::vector<float> sg((size_t)D);
+    tq_hadamard_signs(D, seed, sg.data());
+    const float inv = tq_inv_sqrt(D);
+    for (int64_t i = 0; i < D; ++i)
+      for (int64_t j = 0; j < D; ++j)
+        out[i * D + j] = (__builtin_popcountll((unsigned long long)(i & j)) & 1) ? -sg[(size_t)j] * inv : sg[(size_t)j] * inv;
+    return;
+  }
   std::vector<double> g((size_t)(D * D));
   uint64_t s = seed;
   for (int64_t i = 0; i < D * D; i += 2) {
-    double u1 = ((double)(splitmix64(s) >> 11) + 0.5) * (1.0 / 9007199254740992.0);
-    double u2 = ((double)(splitmix64(s) >> 11) + 0.5) * (1.0 / 9007199254740992.0);
+    double u1 = ((double)(tq_splitmix64(s) >> 11) + 0.5) * (1.0 / 9007199254740992.0);
+    double u2 = ((double)(tq_splitmix64(s) >> 11) + 0.5) * (1.0 / 9007199254740992.0);
     double r = sqrt(-2.0 * log(u1));
     g[(size_t)i] = r * cos(6.283185307179586 * u2);
     if (i + 1 < D * D) g[(size_t)i + 1] = r * sin(6.283185307179586 * u2);
@@ -158,6 +168,39 @@ __global__ __launch_bounds__(1024) void tq_mse_quantize_kernel(
   }
 }
 
+// Hadamard TQ-MSE quantizer: one wave per vector (4 per 256-thread workgroup), lane l holds
+// elements l*E .. l*E + E - 1 (E = D / 64).
+template <int XDT, int E>
+__global__ __launch_bounds__(256) void tq_hadamard_quantize_kernel(
+    const typename Elem<XDT>::T* __restrict__ x, int64_t nvec, int64_t D, int64_t xs,
+    const float* __restrict__ signs, const float* __restrict__ thr, int bits, uint8_t* __restrict__ codes,
+    uint16_t* __restrict__ norms) {
+  const int lane = threadIdx.x & 63;
+  const int64_t v = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (v >= nvec) return;  // whole wave
+  float xv[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) xv[e] = Elem<XDT>::load(x, v * xs + lane * E + e);
+  uint32_t code[E];
+  const float nrm = hadamard_codes_wave<E>(xv, signs, thr, (1 << bits) - 1, tq_inv_sqrt(D), code);
+  if (lane == 0) norms[v] = f32_to_f16_bits(nrm);
+  const int sb = storage_bits(bits);
+  const int64_t pb = D * sb / 8;  // packed bytes per vector
+  uint64_t pk = 0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) pk |= (uint64_t)code[e] << (sb * e);
+  const int nbits = E * sb;
+  uint8_t* dst = codes + v * pb;
+  if (nbits >= 8) {
+    for (int k = 0; k < nbits / 8; ++k) dst[lane * (nbits / 8) + k] = (uint8_t)(pk >> (8 * k));
+  } else {
+    const int per = 8 / nbits;  // lanes per byte
+    uint32_t b = (uint32_t)pk << (nbits * (lane % per));
+    for (int m = 1; m < per; m <<= 1) b |= (uint32_t)__shfl_xor((int)b, m, 64);
+    if (lane % per == 0) dst[lane / per] = (uint8_t)b;
+  }
+}
+
 // out[v][k] = norm_v * sum_i R[i][k] c[code_i]  (fp32 accumulation)
 template <int ODT, int TQ_VB>
 __global__ __launch_bounds__(1024) void tq_mse_dequant_kernel(
@@ -263,6 +306,41 @@ using namespace anna;
 extern "C" int anna_mi_tq_rotation(int64_t D, uint64_t seed, float* out) {
   ANNA_CHECK(out != nullptr && D > 0 && D <= 4096, "anna_mi_tq_rotation: bad arguments");
   make_rotation(D, seed, out);
+  return ANNA_MI_OK;
+}
+
+extern "C" int anna_mi_tq_hadamard_signs(int64_t D, uint64_t seed, float* out) {
+  ANNA_CHECK(out != nullptr && D > 0 && D <= 4096, "anna_mi_tq_hadamard_signs: bad arguments");
+  tq_hadamard_signs(D, seed, out);
+  return ANNA_MI_OK;
+}
+
+extern "C" int anna_mi_tq_hadamard_quantize(const void* x, int x_dtype, int64_t nvec, int64_t D, int64_t x_row_stride,
+                                           const float* signs, const float* thresholds, int bits, uint8_t* codes,
+                                           uint16_t* norms, void* stream) {
+  ANNA_CHECK(x && signs && thresholds && codes && norms, "anna_mi_tq_hadamard_quantize: null pointer");
+  ANNA_CHECK(valid_dtype(x_dtype), "anna_mi_tq_hadamard_quantize: bad dtype code");
+  ANNA_CHECK(bits >= 1 && bits <= 4, "anna_mi_tq_hadamard_quantize: bits must be 1..4");
+  ANNA_CHECK(D == 64 || D == 128 || D == 256 || D == 512 || D == 1024,
+             "anna_mi_tq_hadamard_quantize: head_dim must be a power of two in [64, 1024]");
+  ANNA_CHECK(x_row_stride >= D, "anna_mi_tq_hadamard_quantize: row stride smaller than head_dim");
+  if (nvec <= 0) return ANNA_MI_OK;
+  const dim3 grid((unsigned)((nvec + 3) / 4));
+  ANNA_DISPATCH_DTYPE(x_dtype, XDT, {
+    auto go = [&](auto e_tag) {
+      constexpr int E = decltype(e_tag)::value;
+      hipLaunchKernelGGL((tq_hadamard_quantize_kernel<XDT, E>), grid, dim3(256), 0, as_stream(stream),
+                         (const typename Elem<XDT>::T*)x, nvec, D, x_row_stride, signs, thresholds, bits, codes, norms);
+    };
+    switch (D) {
+      case 64: go(std::integral_constant<int, 1>{}); break;
+      case 128: go(std::integral_constant<int, 2>{}); break;
+      case 256: go(std::integral_constant<int, 4>{}); break;
+      case 512: go(std::integral_constant<int, 8>{}); break;
+      default: go(std::integral_constant<int, 16>{}); break;
+    }
+  });
+  ANNA_LAUNCH_CHECK("tq_hadamard_quantize_kernel");
   return ANNA_MI_OK;
 }
 

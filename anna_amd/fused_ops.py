@@ -428,7 +428,8 @@ def _meta_out(query, *args, **kwargs):
 
 
 def tq_rotation(head_dim: int, seed: int = 42) -> torch.Tensor:
-    """Seeded Haar rotation R (fp32 [D, D], host), generated by the native library."""
+    """Seeded rotation R (fp32 [D, D], host), generated by the native library: the randomized
+    Hadamard H diag(s) / sqrt(D) for power-of-two D, a Haar matrix otherwise."""
     out = torch.empty((head_dim, head_dim), dtype=torch.float32)
     _lib.call("anna_mi_tq_rotation", head_dim, seed, out.data_ptr())
     return out
@@ -439,6 +440,27 @@ def tq_codebook(bits: int, head_dim: int) -> tuple[torch.Tensor, torch.Tensor]:
     t = torch.empty((1 << bits) - 1, dtype=torch.float32)
     _lib.call("anna_mi_tq_codebook", bits, head_dim, c.data_ptr(), t.data_ptr())
     return c, t
+
+
+def tq_hadamard_signs(head_dim: int, seed: int = 42) -> torch.Tensor:
+    """Sign vector s (fp32 +-1 [D], host) of the randomized Hadamard rotation."""
+    out = torch.empty((head_dim,), dtype=torch.float32)
+    _lib.call("anna_mi_tq_hadamard_signs", head_dim, seed, out.data_ptr())
+    return out
+
+
+def tq_hadamard_quantize(x2d, signs, thresholds, bits):
+    """x [nvec, D] (D a power of two in [64, 1024]) -> (codes uint8 [nvec, D*sb/8], norms fp16 [nvec])."""
+    _lib.require_device(x2d, signs, thresholds)
+    nvec, d = x2d.shape
+    if x2d.stride(1) != 1:
+        x2d = x2d.contiguous()
+    sb = 2 if bits == 2 else 4
+    codes = torch.empty((nvec, d * sb // 8), dtype=torch.uint8, device=x2d.device)
+    norms = torch.empty((nvec,), dtype=torch.float16, device=x2d.device)
+    _lib.call("anna_mi_tq_hadamard_quantize", x2d.data_ptr(), _lib.dtype_code(x2d.dtype), nvec, d, x2d.stride(0),
+              signs.data_ptr(), thresholds.data_ptr(), bits, codes.data_ptr(), norms.data_ptr(), _lib.stream_of(x2d))
+    return codes, norms
 
 
 def tq_mse_quantize(x2d, rotation_t, thresholds, bits):

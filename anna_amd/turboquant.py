@@ -100,6 +100,10 @@ class TurboQuantMSE:
 
     quantize(x [n, D]) -> (codes uint8 [n, D*sb/8], norms fp16 [n]);
     dequantize(codes, norms) -> [n, D] = norm * R^T c[codes].
+    The rotation is the seeded randomized Hadamard H diag(s) / sqrt(D) when D is a power of
+    two in [64, 1024] (kind "hadamard": quantized by an in-register fast transform), a seeded
+    Haar matrix otherwise (kind "haar": a dense D x D product).  `rotation` is the dense fp32
+    form of either.
     """
 
     def __init__(self, dim: int, bits: int, device, seed: int = _MSE_SEED):
@@ -107,15 +111,20 @@ class TurboQuantMSE:
         self.bits = int(bits)
         self.seed = int(seed)
         self.device = torch.device(device)
+        d = self.dim
+        self.kind = "hadamard" if d in (64, 128, 256, 512, 1024) else "haar"
         rot = fused_ops.tq_rotation(self.dim, self.seed)
         cent, thr = fused_ops.tq_codebook(self.bits, self.dim)
         self.rotation = rot.to(self.device)
         self.rotation_t = rot.t().contiguous().to(self.device)
         self.centroids = cent.to(self.device)
         self.thresholds = thr.to(self.device)
+        self.signs = fused_ops.tq_hadamard_signs(d, self.seed).to(self.device) if self.kind == "hadamard" else None
 
     def quantize(self, x: torch.Tensor):
         _require_rocm(x, "TurboQuant MSE quantization")
+        if self.kind == "hadamard":
+            return fused_ops.tq_hadamard_quantize(x.reshape(-1, self.dim), self.signs, self.thresholds, self.bits)
         return fused_ops.tq_mse_quantize(x.reshape(-1, self.dim), self.rotation_t, self.thresholds, self.bits)
 
     def dequantize(self, codes: torch.Tensor, norms: torch.Tensor, dtype=torch.float32) -> torch.Tensor:

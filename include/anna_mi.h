@@ -95,13 +95,27 @@ int anna_mi_autoround_to_int4(const int32_t* gptq_qweight, const int32_t* gptq_q
  *   thr_j * |x|}, norm |x| as fp16 bits, codes packed like the values; reconstruction
  *   |x| * R^T c[code]. */
 
-/* Seeded Haar rotation R (fp32 [D, D] row-major, host memory, y = R x).  Replaces
- * TurboQuantMSE(dim, bits, seed=42)'s rotation (turboquant.py:80). */
+/* Seeded rotation R (fp32 [D, D] row-major, host memory, y = R x): the randomized Hadamard
+ * H diag(s) / sqrt(D) (signs of anna_mi_tq_hadamard_signs) for power-of-two D, a seeded Haar
+ * matrix otherwise.  Replaces TurboQuantMSE(dim, bits, seed=42)'s rotation (turboquant.py:80). */
 int anna_mi_tq_rotation(int64_t D, uint64_t seed, float* out_host);
 
 /* Codebook of the MSE quantizer: 2^bits ascending centroids (Gaussian Lloyd-Max levels
  * scaled by 1/sqrt(D); the 2-bit pair is fp16-structured, see turboquant.hip) and the
  * 2^bits - 1 midpoint thresholds, host memory. */
+/* Sign vector s (fp32 +-1, host) of the randomized Hadamard rotation R = H diag(s) / sqrt(D)
+ * used by TQ-MSE for power-of-two head_dim: s_i = -1 where bit i % 64 of the (i / 64)-th
+ * splitmix64 output of `seed` is set.  Stands in for the rotation of the absent `turboquant`
+ * package's TurboQuantMSE (turboquant.py:75-82). */
+int anna_mi_tq_hadamard_signs(int64_t D, uint64_t seed, float* out);
+
+/* TQ-MSE quantize with the Hadamard rotation (D a power of two in [64, 1024]): codes and fp16
+ * norms as anna_mi_tq_mse_quantize, computed by an in-register fast Walsh-Hadamard transform
+ * (O(D log D) per vector instead of the dense D x D product).  signs, thresholds: device. */
+int anna_mi_tq_hadamard_quantize(const void* x, int x_dtype, int64_t nvec, int64_t D, int64_t x_row_stride,
+                                 const float* signs, const float* thresholds, int bits, uint8_t* codes,
+                                 uint16_t* norms, void* stream);
+
 int anna_mi_tq_codebook(int bits, int64_t D, float* centroids_host, float* thresholds_host);
 
 /* MSE quantizer (the quantize step of TurboQuantTensorRow.append, turboquant.py:382-394):

@@ -20,6 +20,9 @@
  *   orc_int4_dequant/linear  brute-force textbook dequant+matmul in fp64
  *   orc_tq_values_*          closed form, round-trip bound, bit layout
  *   orc_tq_codebook          published Lloyd-Max levels (Max 1960)
+ *   orc_tq_hadamard_*        textbook pins: the transform equals the dense matrix
+ *                            H diag(s)/sqrt(D) in fp64, orthogonality, hand-computed
+ *                            codes at D = 4; same PARITY UNPINNED note as below
  *   orc_tq_mse_*             PARITY UNPINNED against the reference: the
  *                            reference delegates to the absent third-party
  *                            `turboquant>=0.2,<0.3` package; pinned here only by
@@ -413,4 +416,97 @@ void orc_tq_mse_dequant(const uint8_t* codes, const uint16_t* norms, int64_t nve
         }
     }
     free(yr);
+}
+
+/* ------------------------------------------------------------------ */
+/* TurboQuant-MSE with the randomized Hadamard rotation                 */
+/* (this build's rotation for power-of-two head_dim; the reference's    */
+/*  is inside the absent `turboquant` package, turboquant.py:75-82)     */
+/* ------------------------------------------------------------------ */
+
+static uint64_t orc_splitmix64(uint64_t* s) {
+    uint64_t z = (*s += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+/* s_i = -1 where bit i % 64 of the (i / 64)-th splitmix64 output of the seed is set */
+void orc_tq_hadamard_signs(int64_t D, uint64_t seed, float* out) {
+    uint64_t st = seed, w = 0;
+    for (int64_t i = 0; i < D; ++i) {
+        if (i % 64 == 0) w = orc_splitmix64(&st);
+        out[i] = ((w >> (i % 64)) & 1u) ? -1.0f : 1.0f;
+    }
+}
+
+/* fp32(1/sqrt(D)): exact 2^-k for D = 4^k, else the double quotient rounded once */
+float orc_tq_inv_sqrt(int64_t D) {
+    int l = 0;
+    while (((int64_t)1 << l) < D) ++l;
+    if ((l & 1) == 0) return 1.0f / (float)((int64_t)1 << (l / 2));
+    return (float)(1.0 / sqrt((double)D));
+}
+
+/* y = fl(1/sqrt(D)) * FWHT(s .* x): butterfly stages over index bits 0, 1, ... in ascending
+ * order, pair (i, i | 2^b) with bit b of i clear -> (x_i + x_j, x_i - x_j). */
+void orc_tq_hadamard_rotate(const float* x, const float* signs, int64_t D, float* y) {
+    for (int64_t i = 0; i < D; ++i) y[i] = x[i] * signs[i];
+    for (int64_t h = 1; h < D; h <<= 1)
+        for (int64_t i = 0; i < D; ++i)
+            if ((i & h) == 0) {
+                float a = y[i], c = y[i + h];
+                y[i] = a + c;
+                y[i + h] = a - c;
+            }
+    const float inv = orc_tq_inv_sqrt(D);
+    for (int64_t i = 0; i < D; ++i) y[i] = y[i] * inv;
+}
+
+/* |x|^2 in the GPU wave's order: 64 lanes, lane l holds elements l*E .. l*E+E-1 (E = D/64,
+ * D >= 64) and forms an fma chain over them from 0; then p_l <- p_l + p_{l^m} for
+ * m = 1, 2, 4, 8, 16, 32.  (D < 64, used by hand-computed tests only: a plain fma chain.) */
+static float hadamard_sumsq(const float* x, int64_t D) {
+    if (D < 64) {
+        float p = 0.0f;
+        for (int64_t k = 0; k < D; ++k) p = fmaf(x[k], x[k], p);
+        return p;
+    }
+    const int64_t E = D / 64;
+    float p[64], q[64];
+    for (int l = 0; l < 64; ++l) {
+        float a = 0.0f;
+        for (int64_t e = 0; e < E; ++e) a = fmaf(x[l * E + e], x[l * E + e], a);
+        p[l] = a;
+    }
+    for (int m = 1; m < 64; m <<= 1) {
+        for (int l = 0; l < 64; ++l) q[l] = p[l] + p[l ^ m];
+        memcpy(p, q, sizeof(p));
+    }
+    return p[0];
+}
+
+/* codes / fp16 norms as orc_tq_mse_quantize, with y from orc_tq_hadamard_rotate */
+void orc_tq_hadamard_quantize(const void* x, int dtype, int64_t nvec, int64_t D, const float* signs,
+                              const float* thr, int bits, uint8_t* codes, uint16_t* norms) {
+    int sb = storage_bits_of(bits);
+    int per_byte = 8 / sb;
+    int nthr = (1 << bits) - 1;
+    int64_t packed = D / per_byte;
+    float* xv = (float*)malloc(sizeof(float) * (size_t)D);
+    float* y = (float*)malloc(sizeof(float) * (size_t)D);
+    for (int64_t v = 0; v < nvec; ++v) {
+        for (int64_t k = 0; k < D; ++k) xv[k] = load_any(x, dtype, v * D + k);
+        float nrm = sqrtf(hadamard_sumsq(xv, D));
+        norms[v] = orc_f32_to_f16(nrm);
+        orc_tq_hadamard_rotate(xv, signs, D, y);
+        memset(codes + v * packed, 0, (size_t)packed);
+        for (int64_t i = 0; i < D; ++i) {
+            uint32_t c = 0;
+            for (int j = 0; j < nthr; ++j) c += (y[i] >= thr[j] * nrm) ? 1u : 0u;
+            codes[v * packed + i / per_byte] |= (uint8_t)(c << (sb * (i % per_byte)));
+        }
+    }
+    free(y);
+    free(xv);
 }

@@ -48,6 +48,9 @@ def lib():
             "orc_lloyd_max_gaussian": [_I, _P],
             "orc_tq_mse_quantize": [_P, _I, _I64, _I64, _P, _P, _I, _P, _P],
             "orc_tq_mse_dequant": [_P, _P, _I64, _I64, _P, _P, _I, _P],
+            "orc_tq_hadamard_signs": [_I64, ctypes.c_uint64, _P],
+            "orc_tq_hadamard_rotate": [_P, _P, _I64, _P],
+            "orc_tq_hadamard_quantize": [_P, _I, _I64, _I64, _P, _P, _I, _P, _P],
         }
         for name, argtypes in sig.items():
             fn = getattr(L, name)
@@ -208,6 +211,42 @@ def tq_mse_dequant(codes, norms_f16_bits, rotation, centroids, bits: int) -> np.
     out = np.zeros((nvec, d), np.float32)
     lib().orc_tq_mse_dequant(_p(codes), _p(norms), nvec, d, _p(P), _p(c), bits, _p(out))
     return out
+
+
+def tq_hadamard_signs(d: int, seed: int = 42) -> np.ndarray:
+    out = np.zeros(d, np.float32)
+    lib().orc_tq_hadamard_signs(d, seed, _p(out))
+    return out
+
+
+def tq_hadamard_rotate(x: np.ndarray, signs: np.ndarray) -> np.ndarray:
+    """y = fl(1/sqrt(D)) * FWHT(s * x) in the fixed fp32 order (one vector)."""
+    x = np.ascontiguousarray(x, np.float32)
+    s = np.ascontiguousarray(signs, np.float32)
+    y = np.zeros_like(x)
+    lib().orc_tq_hadamard_rotate(_p(x), _p(s), x.shape[0], _p(y))
+    return y
+
+
+def tq_hadamard_matrix(signs: np.ndarray) -> np.ndarray:
+    """The dense fp64 matrix H diag(s) / sqrt(D) (numpy, Sylvester construction)."""
+    d = signs.shape[0]
+    h = np.array([[1.0]])
+    while h.shape[0] < d:
+        h = np.block([[h, h], [h, -h]])
+    return h * signs.astype(np.float64)[None, :] / np.sqrt(d)
+
+
+def tq_hadamard_quantize(x_bits: np.ndarray, dtype: int, signs: np.ndarray, thresholds: np.ndarray, bits: int):
+    """x [nvec, D] -> (codes, fp16 norm bits) with the Hadamard rotation."""
+    x = np.ascontiguousarray(x_bits)
+    nvec, d = x.shape
+    s = np.ascontiguousarray(signs, np.float32)
+    thr = np.ascontiguousarray(thresholds, np.float32)
+    codes = np.zeros((nvec, d * _storage_bits(bits) // 8), np.uint8)
+    norms = np.zeros((nvec,), np.uint16)
+    lib().orc_tq_hadamard_quantize(_p(x), dtype, nvec, d, _p(s), _p(thr), bits, _p(codes), _p(norms))
+    return codes, norms
 
 
 # ---------------------------------------------------------------- attention (a13) -- textbook, fp64

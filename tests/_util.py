@@ -31,3 +31,14 @@ def int4_payload(rng: np.random.Generator, n: int, kp: int, group: int, *, scale
         scales = orc.bf16_to_f32(orc.bf16_bits(scales))
     zeros = rng.integers(0, 16, size=(g, n)).astype(np.int8)
     return qweight, scales, zeros
+
+
+def oracle_tq_quantize(qn, x_bits, dtype):
+    """The oracle quantizer matching a TurboQuantMSE's rotation kind (codes, fp16 norm bits)."""
+    from oracle import oracle as orc
+
+    x = np.ascontiguousarray(x_bits)
+    thr = qn.thresholds.cpu().numpy()
+    if qn.kind == "hadamard":
+        return orc.tq_hadamard_quantize(x, dtype, qn.signs.cpu().numpy(), thr, qn.bits)
+    return orc.tq_mse_quantize(x, dtype, qn.rotation.cpu().numpy(), thr, qn.bits)

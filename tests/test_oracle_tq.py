@@ -151,3 +151,80 @@ def test_mse_quantizer_hand_computed_four_bit():
     x = np.array([[0.1, -0.995]], np.float32)  # 0.1: t <= 0.1 for t in -7/16..1/16 -> 9; -0.995 -> 0
     codes, _ = orc.tq_mse_quantize(x, orc.F32, eye, thr, 4)
     assert codes.tolist() == [[9 | (0 << 4)]]
+
+
+# ---------------------------------------------------------------- Hadamard rotation (power-of-two D)
+
+
+@pytest.mark.parametrize("d", [64, 128, 256, 1024])
+def test_hadamard_transform_equals_the_dense_matrix(d):
+    """The fixed-order FWHT is the matrix H diag(s) / sqrt(D) (Sylvester H, built independently
+    in numpy), to fp32 rounding; the matrix is orthogonal."""
+    s = orc.tq_hadamard_signs(d, 42)
+    m = orc.tq_hadamard_matrix(s)
+    np.testing.assert_allclose(m @ m.T, np.eye(d), atol=1e-12)
+    rng = np.random.default_rng(d)
+    for _ in range(3):
+        x = rng.normal(size=d).astype(np.float32)
+        y = orc.tq_hadamard_rotate(x, s)
+        np.testing.assert_allclose(y, m @ x.astype(np.float64), rtol=0, atol=2e-6 * np.abs(x).sum() / np.sqrt(d))
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_native_rotation_and_signs_match_the_oracle(d):
+    s = orc.tq_hadamard_signs(d, 42)
+    np.testing.assert_array_equal(fused_ops.tq_hadamard_signs(d, 42).numpy(), s)
+    assert 0.3 < (s < 0).mean() < 0.7
+    assert not np.array_equal(fused_ops.tq_hadamard_signs(d, 43).numpy(), s)
+    np.testing.assert_array_equal(fused_ops.tq_rotation(d, 42).numpy(), orc.tq_hadamard_matrix(s).astype(np.float32))
+
+
+def test_hadamard_spreads_a_basis_vector_evenly():
+    # an outlier channel (a basis vector) lands as +-1/sqrt(D) on every coordinate
+    s = orc.tq_hadamard_signs(256, 42)
+    for k in (0, 7, 255):
+        x = np.zeros(256, np.float32)
+        x[k] = 3.0
+        np.testing.assert_array_equal(np.abs(orc.tq_hadamard_rotate(x, s)), np.full(256, 3.0 / 16, np.float32))
+
+
+def test_hadamard_quantizer_hand_computed_codes():
+    """D = 4, signs (+1, -1, +1, +1), thresholds (-1/2, 0, 1/2):
+    x = e0 -> s x = (1,0,0,0) -> FWHT (1,1,1,1) -> /2 -> 0.5 each, |x| = 1: 0.5 >= 0.5 -> code 3;
+    x = (1,1,0,0) -> s x = (1,-1,0,0) -> bit 0: (0,2,0,0) -> bit 1: (0,2,0,2) -> /2 -> (0,1,0,1),
+    |x| = sqrt 2: thresholds scale to (-0.707, 0, 0.707): codes (2, 3, 2, 3)."""
+    s = np.array([1, -1, 1, 1], np.float32)
+    thr = np.array([-0.5, 0.0, 0.5], np.float32)
+    x = np.array([[1, 0, 0, 0], [1, 1, 0, 0]], np.float32)
+    np.testing.assert_array_equal(orc.tq_hadamard_rotate(x[1], s), [0.0, 1.0, 0.0, 1.0])
+    codes, norms = orc.tq_hadamard_quantize(x, orc.F32, s, thr, 2)
+    assert codes[:, 0].tolist() == [0xFF, 2 | (3 << 2) | (2 << 4) | (3 << 6)]
+    assert orc.f16_to_f32(norms).tolist() == [1.0, float(np.float16(np.sqrt(2.0)))]
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_hadamard_quantizer_agrees_with_the_dense_quantizer(bits):
+    """Same rotation as a dense matrix through orc_tq_mse_quantize: codes differ only where y
+    lands within fp32 rounding of a threshold (the two round y differently)."""
+    d = 256
+    s = orc.tq_hadamard_signs(d, 42)
+    r = orc.tq_hadamard_matrix(s).astype(np.float32)
+    cent, thr = (t.numpy() for t in fused_ops.tq_codebook(bits, d))
+    x = np.random.default_rng(bits).normal(size=(64, d)).astype(np.float32)
+    c1, n1 = orc.tq_hadamard_quantize(x, orc.F32, s, thr, bits)
+    c2, n2 = orc.tq_mse_quantize(x, orc.F32, r, thr, bits)
+    assert (c1 == c2).mean() > 0.995
+    assert np.abs(orc.f16_to_f32(n1) - orc.f16_to_f32(n2)).max() <= 2 ** -10 * orc.f16_to_f32(n1).max()
+
+
+@pytest.mark.parametrize("bits,expected", [(2, 0.1175), (3, 0.0345), (4, 0.0095)])
+def test_hadamard_mse_distortion_matches_turboquant_paper(bits, expected):
+    d = 256
+    x = np.random.default_rng(10 + bits).normal(size=(400, d)).astype(np.float32)
+    x /= np.linalg.norm(x, axis=1, keepdims=True)
+    s = orc.tq_hadamard_signs(d, 42)
+    cent, thr = (t.numpy() for t in fused_ops.tq_codebook(bits, d))
+    codes, norms = orc.tq_hadamard_quantize(x, orc.F32, s, thr, bits)
+    xh = orc.tq_mse_dequant(codes, norms, orc.tq_hadamard_matrix(s).astype(np.float32), cent, bits)
+    mse = float(((xh - x) ** 2).sum(1).mean())
+    assert abs(mse - expected) / expected < 0.12, mse

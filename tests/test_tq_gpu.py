@@ -14,7 +14,7 @@ from anna_amd import fused_ops
 from anna_amd.turboquant import (TurboQuantKVRow, TurboQuantTensorRow, dequantize_turboquant_values,
                                  get_turboquant_quantizer, quantize_turboquant_values)
 from oracle import oracle as orc
-from tests._util import BF16_TOL, rel_err
+from tests._util import BF16_TOL, oracle_tq_quantize, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -52,9 +52,11 @@ def test_values_quantize_bit_exact(gpu, dtype, bits, group):
 
 
 @pytest.mark.parametrize("bits", [1, 2, 3, 4])
-@pytest.mark.parametrize("d", [64, 256])
+@pytest.mark.parametrize("d", [64, 128, 192, 256, 512])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_mse_quantize_bit_exact(gpu, bits, d, dtype):
+    """Power-of-two D takes the Hadamard kernel (oracle: orc_tq_hadamard_quantize), D = 192 the
+    dense Haar one (oracle: orc_tq_mse_quantize); codes and norms bit-exact either way."""
     print(f"[case] mse bits={bits} D={d} {dtype}", flush=True)
     g = torch.Generator().manual_seed(bits + d)
     x = torch.randn(37, d, generator=g)
@@ -64,8 +66,8 @@ def test_mse_quantize_bit_exact(gpu, bits, d, dtype):
     qn = get_turboquant_quantizer(head_dim=d, bits=bits, device=gpu)
     codes, norms = qn.quantize(x.to(gpu))
     xin = bits_of(x) if dtype == torch.bfloat16 else x.numpy()
-    ref_codes, ref_norms = orc.tq_mse_quantize(xin, orc.BF16 if dtype == torch.bfloat16 else orc.F32,
-                                               qn.rotation.cpu().numpy(), qn.thresholds.cpu().numpy(), bits)
+    assert qn.kind == ("haar" if d == 192 else "hadamard")
+    ref_codes, ref_norms = oracle_tq_quantize(qn, xin, orc.BF16 if dtype == torch.bfloat16 else orc.F32)
     np.testing.assert_array_equal(codes.cpu().numpy(), ref_codes)
     np.testing.assert_array_equal(bits_of(norms), ref_norms)
     deq = qn.dequantize(codes, norms, dtype=torch.float32)
@@ -265,8 +267,7 @@ def test_kv_row_lengths_storage_reuse_and_residual(gpu):
     assert torch.equal(keys[:, 8:], kk[:, 8:]) and torch.equal(values[:, 8:], vv[:, 8:])
     # packed prefix is bit-exact with the oracle quantizers
     qn = get_turboquant_quantizer(head_dim=64, bits=2, device=gpu)
-    ref_codes, ref_norms = orc.tq_mse_quantize(bits_of(kk[:, :8].reshape(-1, 64)), orc.BF16,
-                                               qn.rotation.cpu().numpy(), qn.thresholds.cpu().numpy(), 2)
+    ref_codes, ref_norms = oracle_tq_quantize(qn, bits_of(kk[:, :8].reshape(-1, 64)), orc.BF16)
     np.testing.assert_array_equal(row._kcodes[:, :8].reshape(16, -1).cpu().numpy(), ref_codes)
     np.testing.assert_array_equal(bits_of(row._knorms[:, :8].reshape(-1)), ref_norms)
     data, scales, zeros = orc.tq_values_quantize(bits_of(vv[:, :8]), orc.BF16, 2, 32)
@@ -303,7 +304,6 @@ def test_tensor_row_materialize(gpu):
     mat = row.materialize()
     assert torch.equal(mat[:, 8:], x[:, 8:])
     qn = get_turboquant_quantizer(head_dim=64, bits=2, device=gpu)
-    codes, norms = orc.tq_mse_quantize(bits_of(x[:, :8].reshape(-1, 64)), orc.BF16, qn.rotation.cpu().numpy(),
-                                       qn.thresholds.cpu().numpy(), 2)
+    codes, norms = oracle_tq_quantize(qn, bits_of(x[:, :8].reshape(-1, 64)), orc.BF16)
     ref = orc.tq_mse_dequant(codes, norms, qn.rotation.cpu().numpy(), qn.centroids.cpu().numpy(), 2)
     assert rel_err(f32(mat[:, :8]).reshape(-1, 64), ref) <= BF16_TOL
