@@ -58,17 +58,28 @@ class TQDecodeArgs(ctypes.Structure):
 
     _fields_ = [
         ("batch", _I64), ("q_heads", _I64), ("kv_heads", _I64), ("head_dim", _I64), ("key_bits", _I),
-        ("value_bits", _I), ("query", _P), ("key_codes", _P), ("key_norms", _P), ("value_codes", _P),
+        ("value_bits", _I), ("query", _P), ("gate", _P), ("key_codes", _P), ("key_norms", _P), ("value_codes", _P),
         ("value_norms", _P), ("pool_tokens", _I64), ("residual_key", _P), ("residual_value_t", _P),
-        ("residual_capacity", _I64), ("rotation_f16", _P), ("rotation_t_f16", _P), ("key_scale", _F),
-        ("value_scale", _F), ("scaling", _F), ("items", _P), ("num_items", _I64), ("bh_items", _P),
-        ("query_frag", _P), ("partial_stats", _P), ("partial_values", _P), ("out", _P),
+        ("residual_capacity", _I64), ("seq_offsets", _P), ("seq_lengths", _P), ("signs", _P), ("key_scale", _F),
+        ("value_scale", _F), ("scaling", _F), ("blocks_per_item", _I64), ("num_workgroups", _I64),
+        ("partial_stats", _P), ("partial_values", _P), ("tickets", _P), ("out", _P),
+    ]
+
+
+class TQAppendArgs(ctypes.Structure):
+    """anna_mi_tq_append_args."""
+
+    _fields_ = [
+        ("batch", _I64), ("kv_heads", _I64), ("head_dim", _I64), ("new_key", _P), ("new_value", _P),
+        ("key_codes", _P), ("key_norms", _P), ("value_codes", _P), ("value_norms", _P), ("pool_tokens", _I64),
+        ("residual_key", _P), ("residual_value_t", _P), ("residual_capacity", _I64), ("seq_offsets", _P),
+        ("seq_capacity", _P), ("seq_lengths", _P), ("overflow", _P), ("signs", _P), ("thresholds", _P),
     ]
 
 
 PROTOTYPES.update({
-    "anna_mi_tq_decode_plan": [_I64, _I64, _P, _P, _P, _I64, _P, _I64, _P, _P],
     "anna_mi_tq_decode": [ctypes.POINTER(TQDecodeArgs), _P],
+    "anna_mi_tq_append": [ctypes.POINTER(TQAppendArgs), _P],
     "anna_mi_tq_block_values": [_P, _I64, _P, _P],
     "anna_mi_tq_rotation": [_I64, ctypes.c_uint64, _P],
     "anna_mi_tq_codebook": [_I, _I64, _P, _P],
@@ -121,6 +132,8 @@ RAW_PROTOTYPES: dict[str, tuple] = {
     "anna_mi_sizeof_decode_args": (_I64, []),
     "anna_mi_gqa_decode_splitkv_noalloc_capacity": (_I64, []),
     "anna_mi_sizeof_tq_decode_args": (_I64, []),
+    "anna_mi_sizeof_tq_append_args": (_I64, []),
+    "anna_mi_tq_decode_workgroups": (_I64, [_I64, _I64, _P, _I64]),
 }
 
 _lock = threading.Lock()

@@ -1,33 +1,44 @@
-// Batched varlen GQA decode over a 2-bit TurboQuant-MSE KV cache (head_dim 256), MFMA.
+// Batched varlen GQA decode over a 2-bit TurboQuant-MSE KV cache (head_dim 256), MFMA, one
+// launch per step; and the append of one token per sequence.
 //
-// Cache layout (per KV head, a pool of `pool_tokens` token slots; a sequence owns a range
-// of slots starting at a multiple of 32):
+// Cache layout (per KV head, a pool of `pool_tokens` token slots; sequence b owns the slots
+// from seq_offsets[b], a multiple of 32):
 //   key_codes   uint8 [Hkv][pool][64]       token-major, dim i at bits 2(i%4) of byte i/4
 //   key_norms   fp16  [Hkv][pool]
 //   value_codes uint8 [Hkv][pool/32][2048]  32-token blocks, byte ((t%16)/4)*512 + dim*2 + t/16,
 //                                           token t at bits 2(t%4) (see tq_block_values_kernel)
 //   value_norms fp16  [Hkv][pool]
-//   residual_key     bf16 [B][Hkv][R][256]  newest tokens, dense, token-major
-//   residual_value_t bf16 [B][Hkv][256][R]  dense, dim-major
+//   residual_key     bf16 [B][Hkv][R][256]  ring of the newest tokens, token-major
+//   residual_value_t bf16 [B][Hkv][256][R]  the same ring, dim-major
+// Token j of sequence b sits in ring slot j % R while it is among the newest R; the older ones
+// are the quantized prefix, pool slots seq_offsets[b] .. + length - R.  Codes are TQ-MSE with
+// the randomized Hadamard rotation R = H diag(s) / 16 (tq_hadamard.hpp).
 //
-// Three launches per call (work items come from anna_mi_tq_decode_plan):
-//   tq_rotate_query   q' = R q for every (b, kv-head)'s G q-heads (MFMA, fp16), written in the
-//     B-operand fragment order of the score product.
-//   tq_decode_split   one 512-thread workgroup per work item (b, kv-head, pool range) or per
-//     residual window.  8 waves take 32-token blocks (the next block prefetched).  Scores are
-//     formed transposed, S^T = Khat Q'^T, by v_mfma_f32_16x16x32_f16 on codes turned into fp16
-//     centroids with one v_perm per pair (the 2-bit centroids are fp16 values sharing their
-//     low byte); S^T's accumulator layout is the B operand of O'^T = Vhat^T P^T, so the
-//     probabilities never leave registers.  Online softmax in base 2 with lazy rescaling
-//     (the running max only moves when a block exceeds it by 2^4).  The 8 waves' accumulators
-//     are summed through LDS; per item and q-head the (max, denominator) and the unnormalized
-//     accumulator go to the workspace.
-//   tq_decode_combine 8 workgroups per (b, kv-head), one per 32 output dims: log-sum-exp merge
-//     of the items over the rotated dims, R^T for the tile's dims (MFMA), plus the residual
-//     window's part, written as bf16.
+// tq_decode_kernel, one 512-thread workgroup per work item:
+//   * plan (every workgroup, from seq_lengths): B*Hkv window items, then per sequence
+//     ceil(blocks / bpi) items per KV head over its quantized prefix, bpi chosen so that all
+//     items fit the grid.  No host round trip: the grid is fixed, spare workgroups exit.
+//   * a packed item rotates its G query heads itself, q' = R q (FWHT in registers, one wave
+//     per head), into the B-operand fragments of the score product; 8 waves take 32-token blocks
+//     (the next block prefetched).  Scores are formed transposed, S^T = Khat Q'^T, by
+//     v_mfma_f32_16x16x32_f16 on codes turned into fp16 centroids with one v_perm per pair (the
+//     2-bit centroids are fp16 values sharing their low byte); S^T's accumulator layout is the
+//     B operand of O'^T = Vhat^T P^T, so the probabilities never leave registers.  Online
+//     softmax in base 2 with lazy rescaling (the running max moves only by > 2^4).  The window
+//     item does the same on the dense bf16 ring with the unrotated q.
+//   * each item writes (max, denominator) and its unnormalized accumulator to the workspace;
+//     a ticket per (b, kv head) (a global atomic counter) elects the last item to finish,
+//     which merges all items of its (b, kv head) with log-sum-exp weights, rotates the packed
+//     part back (R^T o' = s * FWHT(o') / 16), adds the window part, applies the sigmoid gate,
+//     writes bf16 and resets the ticket.
+//
+// tq_append_kernel, one workgroup per sequence: quantizes the token leaving the ring into the
+// pool (bit-exact with anna_mi_tq_hadamard_quantize), writes the new token into its ring slot
+// and increments the sequence length.
 #include <vector>
 
 #include "common.hpp"
+#include "tq_hadamard.hpp"
 
 namespace anna {
 namespace {
@@ -71,6 +82,32 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
 }
 
+// Device-coherent (agent-scope) stores and loads of the split partials: the stores write
+// through to the point of coherence of all XCDs and the loads read from there, so the items of
+// one (b, kv head), which may run on different XCDs, exchange partials without an L2
+// write-back or invalidate (fences that write the whole L2 back, once per item, cost more
+// than the decode itself).
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_coherent4(f32x4* p, f32x4 v) {
+  float* f = (float*)p;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) store_coherent(f + i, v[i]);
+}
+__device__ __forceinline__ uint64_t load_coherent64(const void* p) {
+  return __hip_atomic_load((const uint64_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ f32x4 load_coherent4(const f32x4* p) {
+  const uint64_t lo = load_coherent64(p), hi = load_coherent64((const uint64_t*)p + 1);
+  return f32x4{__uint_as_float((uint32_t)lo), __uint_as_float((uint32_t)(lo >> 32)), __uint_as_float((uint32_t)hi),
+               __uint_as_float((uint32_t)(hi >> 32))};
+}
+__device__ __forceinline__ float2 load_coherent2(const float* p) {
+  const uint64_t v = load_coherent64(p);
+  return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
+}
+
 // ------------------------------------------------------------------ decode kernel
 
 constexpr int SWAVES = 8;      // waves per work item
@@ -109,51 +146,6 @@ __device__ __forceinline__ uint32_t f16x2_of_bf16x2(uint32_t v) {
 
 __device__ __forceinline__ uint32_t pkrtz(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
-}
-
-// q' = R q for one tile of 16 dims of the G heads of one (b, kv-head), written into the B
-// operand fragments of the score product: frag[step s][lane][e] (fp16) holds q'[head lane % 16][dim],
-// dim = 64 (lane / 16) + 16 (s >> 1) + 4 (s & 1) + w', e = 2 (w' & 3) + (w' >> 3), w' in
-// {0..3, 8..11} (the pair order of codes_to_f16).  One wave: A = R rows (16 dims x 32), B = q^T
-// (32 x 16 heads, bf16 -> fp16); C lane: head r, dims 16 tile + 4 kq + i.
-__device__ __forceinline__ void tq_rotate_fragment(const anna_mi_tq_decode_args& a, const uint16_t* qg, int G, int tile,
-                                                   int lane, uint16_t* frag) {
-  const int r = lane & 15, kq = lane >> 4;
-  // unconditional loads (row clamped, value zeroed) so that they issue back to back
-  const uint16_t* qrow = qg + (r < G ? r : 0) * TD + kq * 8;
-  const uint32_t keep = r < G ? 0xFFFFFFFFu : 0u;
-  u32x4 qv[8], rv[8];
-#pragma unroll
-  for (int st = 0; st < 8; ++st) {
-    qv[st] = *(const u32x4*)(qrow + st * 32);
-    rv[st] = *(const u32x4*)(a.rotation_f16 + (int64_t)(tile * 16 + r) * TD + st * 32 + kq * 8);
-  }
-  // no instruction moves above this point: every load is issued before the first conversion
-  // waits for its data (the scheduler otherwise interleaves them, one round trip after another)
-  __builtin_amdgcn_sched_barrier(0);
-  f32x4 c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int st = 0; st < 8; ++st) {
-    u32x4 qb;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) qb[w] = f16x2_of_bf16x2(qv[st][w] & keep);
-    c = mfma_f16(rv[st], qb, c);
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int dim = tile * 16 + 4 * kq + i;
-    const int kq2 = dim >> 6, rem = dim & 63, w = rem & 15;
-    const int sx = 2 * (rem >> 4) + ((rem >> 2) & 1), e = 2 * (w & 3) + (w >> 3);
-    frag[((sx * 64) + kq2 * 16 + r) * 8 + e] = f32_to_f16_bits(c[i]);
-  }
-}
-
-// grid (B * Hkv, 16 dim tiles), one wave: q' fragments of every (b, kv-head) into
-// query_frag[b][h] (4096 fp16 each).
-__global__ __launch_bounds__(64) void tq_rotate_query_kernel(const anna_mi_tq_decode_args a) {
-  const int64_t bh = blockIdx.x, b = bh / a.kv_heads, h = bh % a.kv_heads;
-  const int G = (int)(a.q_heads / a.kv_heads);
-  tq_rotate_fragment(a, a.query + (b * a.q_heads + h * G) * TD, G, blockIdx.y, threadIdx.x, a.query_frag + bh * 4096);
 }
 
 // One 32-token block of one wave (slot / window position tb): scores, online softmax, and
@@ -311,32 +303,195 @@ __device__ __forceinline__ void run_blocks(const anna_mi_tq_decode_args& a, cons
   }
 }
 
+
+constexpr int MAX_SEQS = 1024;  // sequences per call (the plan keeps their block counts in LDS)
+
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int t = __shfl_up(v, d, 64);
+    if (lane >= d) v += t;
+  }
+  return v;
+}
+
+__device__ __forceinline__ int wave_sum_int(int v) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+struct ItemInfo {
+  int kind;    // 0 packed, 1 window, 2 zero output (empty sequence), -1 none
+  int b, h;
+  int tb0, tend;      // packed: pool slots [tb0, tend); window: [0, window length)
+  int kb;             // packed items of each (b, kv head) of this sequence
+  int first_packed;   // workgroup index of item 0 of (b, h = 0)
+  int n_bh;           // items of (b, h): kb + 1
+};
+
+// Work item of this workgroup (computed by wave 0, broadcast through LDS).
+__device__ void plan_item(const anna_mi_tq_decode_args& a, int lane, int* s_nb, int* s_len, int* s_off,
+                          ItemInfo* out) {
+  const int B = (int)a.batch, H = (int)a.kv_heads, R = (int)a.residual_capacity;
+  const int w = (int)blockIdx.x, nwg = (int)a.num_workgroups;
+  int T = 0;
+  for (int c = 0; c < B; c += 64) {
+    const int b = c + lane;
+    int nb = 0;
+    if (b < B) {
+      const int len = a.seq_lengths[b], off = a.seq_offsets[b];  // the plan's only global loads
+      s_len[b] = len;
+      s_off[b] = off;
+      int q = len > R ? len - R : 0;
+      const int room = (int)a.pool_tokens - off;  // never read past the pool
+      q = q < room ? q : (room > 0 ? room : 0);
+      nb = (q + TBT - 1) / TBT;
+      s_nb[b] = len > 0 ? nb : -1;  // -1: empty sequence
+    }
+    T += wave_sum_int(nb);
+  }
+  T *= H;
+  // blocks per item: the caller's, if its items fit the grid (lengths within the capacities the
+  // grid was sized for), else the smallest count that fits (always possible: the grid holds at
+  // least 2 B Hkv + 1 workgroups, and sum_b ceil(nb_b / bpi) <= T / (Hkv bpi) + B)
+  int bpi = (int)a.blocks_per_item;
+  if (bpi > 0) {
+    int items = 0;
+    for (int c = 0; c < B; c += 64) {
+      const int b = c + lane;
+      const int nb = b < B ? s_nb[b] : 0;
+      items += wave_sum_int(nb > 0 ? (nb + bpi - 1) / bpi : 0);
+    }
+    if (items * H > nwg - B * H) bpi = 0;
+  }
+  if (bpi <= 0) {
+    int avail = nwg - 2 * B * H;
+    avail = avail < 1 ? 1 : avail;
+    bpi = (T + avail - 1) / avail;
+    bpi = bpi < 1 ? 1 : bpi;
+  }
+  // target: the sequence of a window workgroup, or the item index p of a packed one
+  const bool window = w < B * H;
+  const int p = w - B * H;
+  int base = 0, found_b = window ? w / H : -1, found_excl = 0, found_kb = 0;
+  for (int c = 0; c < B; c += 64) {
+    const int b = c + lane;
+    const int nb = b < B ? s_nb[b] : 0;
+    const int kb = nb > 0 ? (nb + bpi - 1) / bpi : 0;
+    const int incl = wave_incl_scan(kb * H, lane);
+    const int excl = incl - kb * H;
+    if (window) {
+      if (b == found_b) {
+        found_excl = base + excl;
+        found_kb = kb;
+      }
+    } else {
+      const bool hit = b < B && kb > 0 && p >= base + excl && p < base + incl;
+      const unsigned long long m = __ballot(hit);
+      if (m && found_b < 0) {
+        const int src = __ffsll((long long)m) - 1;
+        found_b = __shfl(b, src, 64);
+        found_excl = __shfl(base + excl, src, 64);
+        found_kb = __shfl(kb, src, 64);
+      }
+    }
+    base += __shfl(incl, 63, 64);
+  }
+  if (window) {
+    // the lane that held found_b published it; take it from there
+    const int src = found_b % 64;
+    found_excl = __shfl(found_excl, src, 64);
+    found_kb = __shfl(found_kb, src, 64);
+  }
+  if (lane != 0) return;
+  ItemInfo it{};
+  it.kind = -1;
+  if (found_b >= 0) {
+    const int b = found_b;
+    const int len = s_len[b];
+    it.b = b;
+    it.kb = found_kb;
+    it.first_packed = B * H + found_excl;
+    it.n_bh = found_kb + 1;
+    if (window) {
+      it.h = w % H;
+      it.kind = len > 0 ? 1 : 2;
+      it.tb0 = 0;
+      it.tend = len < R ? len : R;
+    } else {
+      const int q = p - found_excl;
+      it.h = q / found_kb;
+      const int i = q % found_kb;
+      const int nb = s_nb[b];
+      const int blk0 = (int)((int64_t)nb * i / found_kb), blk1 = (int)((int64_t)nb * (i + 1) / found_kb);
+      const int off = s_off[b];
+      int qlen = len - R;
+      qlen = qlen < (int)a.pool_tokens - off ? qlen : (int)a.pool_tokens - off;
+      it.kind = 0;
+      it.tb0 = off + blk0 * TBT;
+      it.tend = off + (blk1 * TBT < qlen ? blk1 * TBT : qlen);
+    }
+  }
+  *out = it;
+}
+
+constexpr int MRG_BATCH = 16;  // items whose partials the merge loads together
+
 __global__ __launch_bounds__(64 * SWAVES) __attribute__((amdgpu_waves_per_eu(2, 8)))
-void tq_decode_split_kernel(const anna_mi_tq_decode_args a) {
-  // B operand of S^T = Khat Q'^T per dim-step and lane (fp16 q' or bf16 q)
-  __shared__ u32x4 s_qf[8][64];
+void tq_decode_kernel(const anna_mi_tq_decode_args a) {
+  // one 64 KB buffer, used in turn for the rotated query (fp32 [16][256]), the cross-wave sums
+  // ([wave][tile j][kq * 8 + head % 8] f32x4) and the merge's two [16][256] fp32 results
+  __shared__ __attribute__((aligned(16))) float s_big[SWAVES * 16 * 32 * 4];
+  __shared__ u32x4 s_qf[8][64];  // B operand of S^T = Khat Q'^T per dim-step and lane
   __shared__ float s_m[SWAVES][16], s_l[SWAVES][16];
-  // cross-wave sums: [wave][tile j][kq * 8 + head % 8]
-  __shared__ f32x4 s_red[SWAVES][16][32];
+  __shared__ int s_nb[MAX_SEQS], s_len[MAX_SEQS], s_off[MAX_SEQS];
+  __shared__ ItemInfo s_it;
+  __shared__ int s_last;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, kq = lane >> 4;
-  const int64_t item = blockIdx.x;
-  const int32_t* it = a.items + item * 4;
-  const int64_t b = it[0], h = it[1];
-  const bool resid = it[2] < 0;
-  const int64_t tb0 = resid ? 0 : it[2];
-  const int64_t tend = it[3];  // end slot (packed) or window length (residual)
+  if (wave == 0) plan_item(a, lane, s_nb, s_len, s_off, &s_it);
+  __syncthreads();
+  const ItemInfo it = s_it;
+  if (it.kind < 0) return;
   const int G = (int)(a.q_heads / a.kv_heads);
-  const int64_t Rc = a.residual_capacity;
+  const int64_t b = it.b, h = it.h, bh = b * a.kv_heads + h;
+  if (it.kind == 2) {  // empty sequence: zeros
+    for (int i = threadIdx.x; i < G * TD; i += blockDim.x) a.out[(b * a.q_heads + h * G) * TD + i] = 0;
+    return;
+  }
+  const bool resid = it.kind == 1;
+  const int64_t tb0 = it.tb0, tend = it.tend;
   const int64_t nblk = (tend - tb0 + TBT - 1) / TBT;
   const uint16_t* qg = a.query + (b * a.q_heads + h * G) * TD;
-  const int64_t bh = b * a.kv_heads + h;
+  const float inv = 1.0f / 16.0f;  // fp32(1/sqrt(256)), exact
 
   BlockRaw cur;
   if (!resid)  // in flight during the prologue (clamped: a wave without blocks reloads the last)
     load_block(a, h, tb0 + (wave < nblk ? wave : nblk - 1) * TBT, r, kq, cur);
   if (!resid) {
-    s_qf[wave][lane] = *(const u32x4*)(a.query_frag + bh * 4096 + (wave * 64 + lane) * 8);
+    // q' = R q: wave w rotates heads w and w + 8 (lane: dims 4 lane .. 4 lane + 3)
+    float* s_q = s_big;  // [16][TD]
+    for (int n = wave; n < 16; n += SWAVES) {
+      float v[4] = {0.f, 0.f, 0.f, 0.f};
+      if (n < G) {
+        const uint2 raw = *(const uint2*)(qg + n * TD + 4 * lane);
+        v[0] = bf16_bits_to_f32((uint16_t)(raw.x & 0xFFFFu)) * a.signs[4 * lane + 0];
+        v[1] = bf16_bits_to_f32((uint16_t)(raw.x >> 16)) * a.signs[4 * lane + 1];
+        v[2] = bf16_bits_to_f32((uint16_t)(raw.y & 0xFFFFu)) * a.signs[4 * lane + 2];
+        v[3] = bf16_bits_to_f32((uint16_t)(raw.y >> 16)) * a.signs[4 * lane + 3];
+        fwht_wave<4>(v);
+      }
+      *(float4*)(s_q + n * TD + 4 * lane) = make_float4(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
+    }
+    __syncthreads();
+    // fragment of step st = wave: element e holds dim 64 kq + 16 (st >> 1) + 4 (st & 1) + (e >> 1) + 8 (e & 1)
+    const int dim0 = 64 * kq + 16 * (wave >> 1) + 4 * (wave & 1);
+    const float* qr = s_q + r * TD + dim0;
+    u32x4 f;
+#pragma unroll
+    for (int e2 = 0; e2 < 4; ++e2) f[e2] = pack_f16x2(qr[e2], qr[e2 + 8]);
+    s_qf[wave][lane] = f;
   } else {
     const u32x4 v = *(const u32x4*)(qg + (r < G ? r : 0) * TD + wave * 32 + kq * 8);
     s_qf[wave][lane] = r < G ? v : u32x4{0u, 0u, 0u, 0u};
@@ -352,7 +507,8 @@ void tq_decode_split_kernel(const anna_mi_tq_decode_args a) {
   else
     run_blocks<false>(a, s_qf, b, h, tb0, tend, nblk, wave, lane, cur, acc, m_run, l_run);
 
-  // ---- reduce the waves
+  // ---- reduce the waves, write this item's partials (workgroup index = item slot)
+  const int64_t item = blockIdx.x;
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);
   if (kq == 0) {
@@ -370,19 +526,20 @@ void tq_decode_split_kernel(const anna_mi_tq_decode_args a) {
   }
   // partial_values[item] as f32x4 [head block hb/8][tile j][kq * 8 + head % 8]; element i of
   // entry (j, kq) is dim (4 kq + i) * 16 + j (the accumulator layout of O'^T)
+  f32x4* s_red = (f32x4*)s_big;  // [SWAVES][16][32]
   f32x4* pvi = (f32x4*)(a.partial_values + item * 16 * TD);
   for (int hb = 0; hb < G; hb += 8) {
     if (r >= hb && r < hb + 8) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) s_red[wave][j][kq * 8 + r - hb] = acc[j];
+      for (int j = 0; j < 16; ++j) s_red[(wave * 16 + j) * 32 + kq * 8 + r - hb] = acc[j];
     }
     __syncthreads();
     const int t = threadIdx.x, j = t >> 5, e = t & 31;
     if (hb + (e & 7) < G) {
-      f32x4 sum = s_red[0][j][e];
+      f32x4 sum = s_red[j * 32 + e];
 #pragma unroll
-      for (int w = 1; w < SWAVES; ++w) sum += s_red[w][j][e];
-      pvi[(hb / 8) * 512 + t] = sum;
+      for (int w = 1; w < SWAVES; ++w) sum += s_red[(w * 16 + j) * 32 + e];
+      store_coherent4(pvi + (hb / 8) * 512 + t, sum);
     }
     __syncthreads();
   }
@@ -392,123 +549,162 @@ void tq_decode_split_kernel(const anna_mi_tq_decode_args a) {
     for (int w = 0; w < SWAVES; ++w) Mx = fmaxf(Mx, s_m[w][n]);
     for (int w = 0; w < SWAVES; ++w)
       if (s_l[w][n] > 0.f) L += s_l[w][n] * __builtin_amdgcn_exp2f(s_m[w][n] - Mx);
-    a.partial_stats[(item * 16 + n) * 2] = Mx;
-    a.partial_stats[(item * 16 + n) * 2 + 1] = L;
+    store_coherent(a.partial_stats + (item * 16 + n) * 2, Mx);
+    store_coherent(a.partial_stats + (item * 16 + n) * 2 + 1, L);
   }
-}
 
-// ------------------------------------------------------------------ combine
-
-// grid (B * Hkv, 8 tiles of 32 output dims), 256 threads: combines the items of one
-// (b, kv-head) with log-sum-exp weights over all 256 rotated dims, applies R^T for the tile's
-// 32 output dims (MFMA), adds the residual window's part and writes bf16.  Each of the 8 tile
-// workgroups of a (b, kv-head) merges all dims itself: 8x the (L2-resident) partial reads, but
-// 8x the compute units pulling them, which is what bounds this kernel.
-constexpr int CMB_THREADS = 256, CMB_OT = 32;  // threads, output dims per workgroup
-__global__ __launch_bounds__(CMB_THREADS) void tq_decode_combine_kernel(const anna_mi_tq_decode_args a) {
-  constexpr int RP = TD + 8;  // padded fp16 rows of the rotated sum
-  __shared__ uint16_t s_rot[16 * RP];
-  __shared__ float s_res[16][CMB_OT];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int r = lane & 15, kq = lane >> 4;
-  const int64_t bh = blockIdx.x, b = bh / a.kv_heads, h = bh % a.kv_heads;
-  const int d0 = blockIdx.y * CMB_OT;
-  const int G = (int)(a.q_heads / a.kv_heads);
-  // R^T rows of the wave's output tile (waves 0 and 1): they depend on nothing, so they go first
-  u32x4 bfr[8];
-  if (wave < CMB_OT / 16) {
-#pragma unroll
-    for (int st = 0; st < 8; ++st)
-      bfr[st] = *(const u32x4*)(a.rotation_t_f16 + (int64_t)(d0 + wave * 16 + r) * TD + st * 32 + kq * 8);
+  // ---- ticket: the last item of (b, h) to arrive merges.  Every wave waits until its
+  // coherent partial stores are acknowledged, then one thread counts the item in.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int old = __hip_atomic_fetch_add(a.tickets + bh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = old == it.n_bh - 1;
   }
-  const int4 info = *(const int4*)(a.bh_items + bh * 4);  // first item, packed items, residual item
-  const int i0 = info.x, npk = info.y, ires = info.z;
-  const bool has_res = ires >= 0;
-  constexpr int64_t IS = 16 * TD / 4;  // item stride of partial_values in f32x4
-  // Entries (tile j, e) and (j + 8, e) of head n = hb + e % 8 in every item (512 entries per
-  // head block; both of this thread's entries share n and so the stats): the thread combines the
-  // items itself with an online log-sum-exp over batches of 16, every load of a batch issued
-  // together (one round trip per 16 items).
-  for (int hb = 0; hb < G; hb += 8) {
-    const int t = tid, j = t >> 5, e = t & 31;
-    const int n = hb + (e & 7), ekq = e >> 3;
-    if (n >= G) continue;
-    const f32x4* src = (const f32x4*)a.partial_values + (hb / 8) * 512 + t;
-    const float* stn = a.partial_stats + n * 2;
-    f32x4 vr0 = {0.f, 0.f, 0.f, 0.f}, vr1 = vr0;
-    float2 mlr = {-INFINITY, 0.f};
-    if (has_res) {
-      vr0 = src[(int64_t)ires * IS];
-      vr1 = src[(int64_t)ires * IS + CMB_THREADS];
-      mlr = *(const float2*)(stn + (int64_t)ires * 32);
-    }
-    f32x4 sr0 = {0.f, 0.f, 0.f, 0.f}, sr1 = sr0;
-    float M = -INFINITY, L = 0.f;
-    for (int k0 = 0; k0 < npk; k0 += 16) {
-      f32x4 v0[16], v1[16];
-      float2 ml[16];
+  __syncthreads();
+  if (!s_last) return;
+
+  // ---- merge: thread t owns entry (tile j, e) of each head block: head hb + e % 8, dims
+  // (4 (e / 8) + i) * 16 + j, i = 0..3
+  float* s_o = s_big;            // [16][TD] packed part, rotated, normalized
+  float* s_w = s_big + 16 * TD;  // [16][TD] window part, normalized
+  {
+    const int t = threadIdx.x, j = t >> 5, e = t & 31, ekq = e >> 3;
+    constexpr int64_t IS = 16 * TD / 4;  // item stride of partial_values in f32x4
+    const f32x4* pv = (const f32x4*)a.partial_values;
+    const int64_t wr = bh;  // window item
+    const int64_t first = it.first_packed + h * it.kb;
+    const int kb = it.kb;
+    for (int hb = 0; hb < G; hb += 8) {
+      const int n = hb + (e & 7);
+      if (n >= G) continue;
+      const int64_t ent = (hb / 8) * 512 + t;
+      const float2 mlr = load_coherent2(a.partial_stats + (wr * 16 + n) * 2);
+      const f32x4 vr = load_coherent4(pv + wr * IS + ent);
+      // online log-sum-exp over the packed items, MRG_BATCH at a time with every load issued first
+      float M = mlr.y > 0.f ? mlr.x : -INFINITY, L = 0.f;
+      f32x4 sp = {0.f, 0.f, 0.f, 0.f};
+      for (int k0 = 0; k0 < kb; k0 += MRG_BATCH) {
+        f32x4 v[MRG_BATCH];
+        float2 ml[MRG_BATCH];
 #pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        const int64_t idx = i0 + (k0 + k < npk ? k0 + k : 0);
-        v0[k] = src[idx * IS];
-        v1[k] = src[idx * IS + CMB_THREADS];
-        ml[k] = *(const float2*)(stn + idx * 32);
+        for (int k = 0; k < MRG_BATCH; ++k) {
+          const int64_t slot = first + (k0 + k < kb ? k0 + k : 0);
+          v[k] = load_coherent4(pv + slot * IS + ent);
+          ml[k] = load_coherent2(a.partial_stats + (slot * 16 + n) * 2);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        float mb = M;
+#pragma unroll
+        for (int k = 0; k < MRG_BATCH; ++k)
+          if (k0 + k < kb && ml[k].y > 0.f) mb = fmaxf(mb, ml[k].x);
+        const float f = mb == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - mb);  // 0 while M is -inf
+        sp *= f;
+        L *= f;
+#pragma unroll
+        for (int k = 0; k < MRG_BATCH; ++k) {
+          const float wgt = (k0 + k < kb && ml[k].y > 0.f) ? __builtin_amdgcn_exp2f(ml[k].x - mb) : 0.f;
+          sp += v[k] * wgt;
+          L += ml[k].y * wgt;
+        }
+        M = mb;
       }
-      // all 48 loads of the batch go out before the first wait (left alone, the scheduler
-      // issues the value loads only after the statistics have arrived)
-      __builtin_amdgcn_sched_barrier(0);
-      float mb = M;
+      const float wr_w = mlr.y > 0.f ? __builtin_amdgcn_exp2f(mlr.x - M) : 0.f;
+      L += mlr.y * wr_w;
+      const float invL = L > 0.f ? 1.0f / L : 0.f;
 #pragma unroll
-      for (int k = 0; k < 16; ++k)
-        if (k0 + k < npk && ml[k].y > 0.f) mb = fmaxf(mb, ml[k].x);
-      if (mb == -INFINITY) continue;
-      const float f = __builtin_amdgcn_exp2f(M - mb);  // 0 while M is -inf
-      sr0 *= f;
-      sr1 *= f;
-      L *= f;
-#pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        const float w = (k0 + k < npk && ml[k].y > 0.f) ? __builtin_amdgcn_exp2f(ml[k].x - mb) : 0.f;
-        sr0 += v0[k] * w;
-        sr1 += v1[k] * w;
-        L += ml[k].y * w;
-      }
-      M = mb;
-    }
-    const float Mt = fmaxf(M, mlr.y > 0.f ? mlr.x : -INFINITY);
-    const float fp = L > 0.f ? __builtin_amdgcn_exp2f(M - Mt) : 0.f;
-    const float fr = mlr.y > 0.f ? __builtin_amdgcn_exp2f(mlr.x - Mt) : 0.f;
-    const float inv = 1.0f / (L * fp + mlr.y * fr);
-    sr0 *= fp * inv;
-    sr1 *= fp * inv;
-    vr0 *= fr * inv;
-    vr1 *= fr * inv;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        const int dim = (4 * ekq + i) * 16 + j + 8 * hf;
-        s_rot[n * RP + dim] = f32_to_f16_bits(hf ? sr1[i] : sr0[i]);
-        if (dim >= d0 && dim < d0 + CMB_OT) s_res[n][dim - d0] = hf ? vr1[i] : vr0[i];
+      for (int i = 0; i < 4; ++i) {
+        const int dim = (4 * ekq + i) * 16 + j;
+        s_o[n * TD + dim] = sp[i] * invL;
+        s_w[n * TD + dim] = vr[i] * wr_w * invL;
       }
     }
   }
   __syncthreads();
-  // out = rot R + res: wave w < 2 takes output dims [d0 + 16 w, d0 + 16 w + 16); A = rot (16 heads
-  // x 32), B[k][d] = R[k][d] = R^T[d][k]; C lane: dim col r, heads 4 kq + i
-  if (wave < CMB_OT / 16) {
-    f32x4 c = {0.f, 0.f, 0.f, 0.f};
+  // out = R^T o' + window part = s * FWHT(o') / 16 + w, times sigmoid(gate); wave w: heads w, w + 8
+  for (int n = wave; n < G; n += SWAVES) {
+    float v[4];
+    const float4 o4 = *(const float4*)(s_o + n * TD + 4 * lane);
+    v[0] = o4.x, v[1] = o4.y, v[2] = o4.z, v[3] = o4.w;
+    fwht_wave<4>(v);
+    const float4 w4 = *(const float4*)(s_w + n * TD + 4 * lane);
+    const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
+    const int64_t orow = (b * a.q_heads + h * G + n) * TD + 4 * lane;
+    float o[4];
 #pragma unroll
-    for (int st = 0; st < 8; ++st) {
-      const u32x4 af = *(const u32x4*)(s_rot + r * RP + st * 32 + kq * 8);
-      c = mfma_f16(af, bfr[st], c);
+    for (int e = 0; e < 4; ++e) o[e] = v[e] * a.signs[4 * lane + e] * inv + wv[e];
+    if (a.gate) {
+      const uint2 g = *(const uint2*)(a.gate + orow);
+      const float gv[4] = {bf16_bits_to_f32((uint16_t)(g.x & 0xFFFFu)), bf16_bits_to_f32((uint16_t)(g.x >> 16)),
+                           bf16_bits_to_f32((uint16_t)(g.y & 0xFFFFu)), bf16_bits_to_f32((uint16_t)(g.y >> 16))};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = o[e] / (1.0f + __expf(-gv[e]));
     }
+    *(uint2*)(a.out + orow) = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(a.tickets + bh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // for the next call
+}
+
+// ------------------------------------------------------------------ append
+
+// One workgroup (4 waves) per sequence.  Wave w quantizes vector w of {K, V} x kv heads that
+// leaves the ring (when length >= R), all waves then write the new token into the ring slot,
+// thread 0 increments the length.
+__global__ __launch_bounds__(256) void tq_append_kernel(const anna_mi_tq_append_args a) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t b = blockIdx.x, H = a.kv_heads, R = a.residual_capacity, T = a.pool_tokens;
+  const int n = a.seq_lengths[b];
+  const int64_t rpos = n % R;
+  if (n >= R) {
+    const int64_t q = n - R;
+    const bool room = q < a.seq_capacity[b];
+    if (!room) {
+      if (threadIdx.x == 0 && a.overflow) *a.overflow = 1;
+    } else {
+      const int64_t slot = a.seq_offsets[b] + q;
+      for (int64_t vi = wave; vi < 2 * H; vi += 4) {
+        const int64_t h = vi >> 1;
+        const bool is_v = vi & 1;
+        float x[4];
+        if (!is_v) {
+          const uint2 raw = *(const uint2*)(a.residual_key + ((b * H + h) * R + rpos) * TD + 4 * lane);
+          x[0] = bf16_bits_to_f32((uint16_t)(raw.x & 0xFFFFu));
+          x[1] = bf16_bits_to_f32((uint16_t)(raw.x >> 16));
+          x[2] = bf16_bits_to_f32((uint16_t)(raw.y & 0xFFFFu));
+          x[3] = bf16_bits_to_f32((uint16_t)(raw.y >> 16));
+        } else {
+          const uint16_t* col = a.residual_value_t + (b * H + h) * TD * R + rpos;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int n = 4 * kq + i, dl = wave * 16 + r;
-      if (n < G) a.out[(b * a.q_heads + h * G + n) * TD + d0 + dl] = f32_to_bf16_bits(c[i] + s_res[n][dl]);
+          for (int e = 0; e < 4; ++e) x[e] = bf16_bits_to_f32(col[(4 * lane + e) * R]);
+        }
+        uint32_t code[4];
+        const float nrm = hadamard_codes_wave<4>(x, a.signs, a.thresholds, 3, 1.0f / 16.0f, code);
+        const uint16_t nb16 = f32_to_f16_bits(nrm);
+        if (!is_v) {
+          a.key_codes[(h * T + slot) * 64 + lane] =
+              (uint8_t)(code[0] | (code[1] << 2) | (code[2] << 4) | (code[3] << 6));
+          if (lane == 0) a.key_norms[h * T + slot] = nb16;
+        } else {
+          const int64_t t = slot % TBT;
+          uint8_t* blk = a.value_codes + (h * (T / TBT) + slot / TBT) * 2048 + ((t % 16) / 4) * 512 + (t / 16);
+          const int sh = 2 * (int)(t % 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            uint8_t* p = blk + (4 * lane + e) * 2;
+            *p = (uint8_t)(sh == 0 ? code[e] : (*p | (code[e] << sh)));
+          }
+          if (lane == 0) a.value_norms[h * T + slot] = nb16;
+        }
+      }
     }
   }
+  __syncthreads();  // the leaving token is read before its slot is overwritten
+  for (int64_t i = threadIdx.x; i < H * TD; i += blockDim.x) {
+    const int64_t h = i / TD, d = i % TD;
+    a.residual_key[((b * H + h) * R + rpos) * TD + d] = a.new_key[(b * H + h) * TD + d];
+    a.residual_value_t[((b * H + h) * TD + d) * R + rpos] = a.new_value[(b * H + h) * TD + d];
+  }
+  if (threadIdx.x == 0) a.seq_lengths[b] = n + 1;
 }
 
 // ------------------------------------------------------------------ value blocking
@@ -537,72 +733,23 @@ __global__ __launch_bounds__(256) void tq_block_values_kernel(const uint8_t* __r
 using namespace anna;
 
 extern "C" int64_t anna_mi_sizeof_tq_decode_args(void) { return (int64_t)sizeof(anna_mi_tq_decode_args); }
+extern "C" int64_t anna_mi_sizeof_tq_append_args(void) { return (int64_t)sizeof(anna_mi_tq_append_args); }
 
-// Blocks of 32 tokens per item for `slots` concurrent workgroups: the smallest count for which
-// the items of every (b, kv-head) fit (an item of nb blocks puts at most ceil(nb / 4) of them on
-// one SIMD, so no rounding to whole passes of the 8 waves).
-static int64_t auto_blocks_per_item(int64_t batch, int64_t kv_heads, const int64_t* qlens, const int64_t* rlens) {
-  constexpr int64_t SLOTS = 256;  // MI355X compute units: one 512-thread workgroup each
-  int64_t total = 0, resid = 0;
-  for (int64_t b = 0; b < batch; ++b) {
-    total += (qlens[b] + TBT - 1) / TBT;
-    resid += rlens[b] > 0;
-  }
-  total *= kv_heads;
-  resid *= kv_heads;
-  const int64_t slots = SLOTS - resid > kv_heads * batch ? SLOTS - resid : kv_heads * batch;
-  int64_t bpi = (total + slots - 1) / slots;
-  if (bpi < 1) bpi = 1;
-  for (;; ++bpi) {
-    int64_t n = 0;
-    for (int64_t b = 0; b < batch; ++b) n += ((qlens[b] + TBT - 1) / TBT + bpi - 1) / bpi;
-    if (n * kv_heads <= slots) return bpi;
-  }
-}
-
-extern "C" int anna_mi_tq_decode_plan(int64_t batch, int64_t kv_heads, const int64_t* quantized_lens,
-                                      const int64_t* residual_lens, const int64_t* seq_offsets,
-                                      int64_t tokens_per_item, int32_t* items, int64_t items_capacity,
-                                      int32_t* bh_items, int64_t* num_items) {
-  ANNA_CHECK(items && bh_items && num_items && quantized_lens && residual_lens && seq_offsets,
-             "anna_mi_tq_decode_plan: null pointer");
-  ANNA_CHECK(tokens_per_item >= 0 && tokens_per_item % TBT == 0,
-             "tokens_per_item must be 0 (automatic) or a positive multiple of 32");
-  for (int64_t b = 0; b < batch; ++b) {
-    ANNA_CHECK(quantized_lens[b] >= 0 && residual_lens[b] >= 0, "anna_mi_tq_decode_plan: negative length");
-    ANNA_CHECK(quantized_lens[b] + residual_lens[b] > 0, "anna_mi_tq_decode_plan: a sequence has no tokens");
-    ANNA_CHECK(seq_offsets[b] % TBT == 0, "anna_mi_tq_decode_plan: sequence offsets must be multiples of 32");
-    ANNA_CHECK(seq_offsets[b] + quantized_lens[b] < ((int64_t)1 << 31), "anna_mi_tq_decode_plan: pool slot exceeds int32");
-  }
-  const int64_t bpi = tokens_per_item > 0 ? tokens_per_item / TBT
-                                          : auto_blocks_per_item(batch, kv_heads, quantized_lens, residual_lens);
+extern "C" int64_t anna_mi_tq_decode_workgroups(int64_t batch, int64_t kv_heads, const int64_t* pool_capacity,
+                                                int64_t blocks_per_item) {
+  if (batch <= 0 || kv_heads <= 0) return 0;
+  const int64_t bh = batch * kv_heads;
+  // one 512-thread item per MI355X compute unit at a time (232 VGPRs: two waves per SIMD), so
+  // 256 workgroups run in one round; >= 2 bh + 1 so that any lengths fit (see plan_item)
+  constexpr int64_t SLOTS = 256;
+  const int64_t automatic = SLOTS > 2 * bh ? SLOTS : 2 * bh + 1;
+  if (blocks_per_item <= 0) return automatic;
   int64_t n = 0;
-  for (int64_t b = 0; b < batch; ++b)
-    for (int64_t h = 0; h < kv_heads; ++h) {
-      int32_t* info = bh_items + (b * kv_heads + h) * 4;
-      info[0] = (int32_t)n, info[2] = -1, info[3] = 0;
-      const int64_t q = quantized_lens[b], nb = (q + TBT - 1) / TBT;
-      const int64_t k = (nb + bpi - 1) / bpi;  // items, with the blocks spread evenly over them
-      for (int64_t i = 0; i < k; ++i) {
-        ANNA_CHECK(n < items_capacity, "anna_mi_tq_decode_plan: items capacity too small");
-        const int64_t b0 = nb * i / k, b1 = nb * (i + 1) / k;
-        const int64_t t1 = b1 * TBT < q ? b1 * TBT : q;
-        int32_t* it = items + n * 4;
-        it[0] = (int32_t)b, it[1] = (int32_t)h;
-        it[2] = (int32_t)(seq_offsets[b] + b0 * TBT), it[3] = (int32_t)(seq_offsets[b] + t1);
-        ++n;
-      }
-      info[1] = (int32_t)k;
-      if (residual_lens[b] > 0) {
-        ANNA_CHECK(n < items_capacity, "anna_mi_tq_decode_plan: items capacity too small");
-        info[2] = (int32_t)n;
-        int32_t* it = items + n * 4;
-        it[0] = (int32_t)b, it[1] = (int32_t)h, it[2] = -1, it[3] = (int32_t)residual_lens[b];
-        ++n;
-      }
-    }
-  *num_items = n;
-  return ANNA_MI_OK;
+  for (int64_t b = 0; b < batch; ++b) {
+    const int64_t nb = (pool_capacity[b] + TBT - 1) / TBT;
+    n += (nb + blocks_per_item - 1) / blocks_per_item;
+  }
+  return bh + n * kv_heads > automatic ? bh + n * kv_heads : automatic;
 }
 
 extern "C" int anna_mi_tq_decode(const anna_mi_tq_decode_args* ap, void* stream) {
@@ -610,22 +757,37 @@ extern "C" int anna_mi_tq_decode(const anna_mi_tq_decode_args* ap, void* stream)
   const anna_mi_tq_decode_args& a = *ap;
   ANNA_CHECK(a.head_dim == TD, "anna_mi_tq_decode: head_dim must be 256");
   ANNA_CHECK(a.key_bits == 2 && a.value_bits == 2, "anna_mi_tq_decode: 2-bit codes only (use anna_mi_gqa_decode_splitkv)");
+  ANNA_CHECK(a.batch > 0 && a.batch <= MAX_SEQS, "anna_mi_tq_decode: batch must be in [1, %d]", MAX_SEQS);
   ANNA_CHECK(a.kv_heads > 0 && a.q_heads % a.kv_heads == 0 && a.q_heads / a.kv_heads <= 16,
              "anna_mi_tq_decode: need q_heads = G * kv_heads with G <= 16");
-  ANNA_CHECK(a.pool_tokens % TBT == 0 && a.residual_capacity % TBT == 0, "pool and residual capacity must be multiples of 32");
-  ANNA_CHECK(a.query && a.out && a.query_frag && a.partial_stats && a.partial_values && a.items && a.bh_items,
+  ANNA_CHECK(a.pool_tokens % TBT == 0 && a.residual_capacity % TBT == 0 && a.residual_capacity > 0,
+             "pool and residual capacity must be positive multiples of 32");
+  ANNA_CHECK(a.pool_tokens < ((int64_t)1 << 31), "anna_mi_tq_decode: pool slots exceed int32");
+  ANNA_CHECK(a.num_workgroups > 2 * a.batch * a.kv_heads && a.num_workgroups < ((int64_t)1 << 31),
+             "anna_mi_tq_decode: num_workgroups must come from anna_mi_tq_decode_workgroups");
+  ANNA_CHECK(a.query && a.out && a.partial_stats && a.partial_values && a.tickets && a.seq_offsets && a.seq_lengths &&
+                 a.signs,
              "anna_mi_tq_decode: null pointer");
-  ANNA_CHECK(a.rotation_f16 && a.rotation_t_f16 && a.key_codes && a.key_norms && a.value_codes && a.value_norms,
+  ANNA_CHECK(a.key_codes && a.key_norms && a.value_codes && a.value_norms && a.residual_key && a.residual_value_t,
              "anna_mi_tq_decode: null cache pointer");
-  if (a.num_items <= 0) return ANNA_MI_OK;
-  hipStream_t st = as_stream(stream);
-  hipLaunchKernelGGL(tq_rotate_query_kernel, dim3((unsigned)(a.batch * a.kv_heads), 16), dim3(64), 0, st, a);
-  ANNA_LAUNCH_CHECK("tq_rotate_query_kernel");
-  hipLaunchKernelGGL(tq_decode_split_kernel, dim3((unsigned)a.num_items), dim3(64 * SWAVES), 0, st, a);
-  ANNA_LAUNCH_CHECK("tq_decode_split_kernel");
-  hipLaunchKernelGGL(tq_decode_combine_kernel, dim3((unsigned)(a.batch * a.kv_heads), TD / CMB_OT), dim3(CMB_THREADS), 0,
-                     st, a);
-  ANNA_LAUNCH_CHECK("tq_decode_combine_kernel");
+  hipLaunchKernelGGL(tq_decode_kernel, dim3((unsigned)a.num_workgroups), dim3(64 * SWAVES), 0, as_stream(stream), a);
+  ANNA_LAUNCH_CHECK("tq_decode_kernel");
+  return ANNA_MI_OK;
+}
+
+extern "C" int anna_mi_tq_append(const anna_mi_tq_append_args* ap, void* stream) {
+  ANNA_CHECK(ap != nullptr, "anna_mi_tq_append: null args");
+  const anna_mi_tq_append_args& a = *ap;
+  ANNA_CHECK(a.head_dim == TD, "anna_mi_tq_append: head_dim must be 256");
+  ANNA_CHECK(a.batch > 0 && a.kv_heads > 0, "anna_mi_tq_append: empty batch or heads");
+  ANNA_CHECK(a.pool_tokens % TBT == 0 && a.residual_capacity % TBT == 0 && a.residual_capacity > 0,
+             "pool and residual capacity must be positive multiples of 32");
+  ANNA_CHECK(a.new_key && a.new_value && a.key_codes && a.key_norms && a.value_codes && a.value_norms &&
+                 a.residual_key && a.residual_value_t && a.seq_offsets && a.seq_capacity && a.seq_lengths && a.signs &&
+                 a.thresholds,
+             "anna_mi_tq_append: null pointer");
+  hipLaunchKernelGGL(tq_append_kernel, dim3((unsigned)a.batch), dim3(256), 0, as_stream(stream), a);
+  ANNA_LAUNCH_CHECK("tq_append_kernel");
   return ANNA_MI_OK;
 }
 

@@ -1,13 +1,19 @@
 """Batched, variable-length TurboQuant KV cache for decode (2-bit TQ-MSE keys and values).
 
-One launch sequence decodes every sequence of the batch: this replaces the per-row Python
-loop of the reference (Qwen3DynamicCache.turboquant_single_token_decode_attention,
-src/anna/model/ops.py:1024-1072, calling TurboQuantKVRow.decode_attention per row).
+One launch appends a token to every sequence and one launch decodes every sequence: this
+replaces the per-row loops of the reference, the append of
+Qwen3DynamicCache._update_turboquant_layer (src/anna/model/ops.py:618-661, calling
+TurboQuantKVRow.append, turboquant.py:1027-1140) and the decode of
+turboquant_single_token_decode_attention (ops.py:1024-1072, calling
+TurboQuantKVRow.decode_attention per row, turboquant.py:1181-1346).
 
-Pool layout per KV head (see anna_amd/csrc/tq_decode.hip): sequence b owns the slots
-[offsets[b], offsets[b] + capacity[b]) (capacities rounded up to 32 tokens); keys are
-token-major codes, values 32-token blocked codes; the newest `residual_capacity` tokens
-of each sequence stay bf16 (keys token-major, values dim-major).
+Layout (see anna_amd/csrc/tq_decode.hip): per KV head a pool of token slots, sequence b owning
+the slots [offsets[b], offsets[b] + capacity[b]) (capacities rounded up to 32 tokens); keys as
+token-major codes, values as 32-token blocked codes; the newest `residual_capacity` tokens of
+each sequence stay bf16 in a ring (token j at ring slot j % R), so a sequence of length L has
+max(0, L - R) quantized tokens, as in the reference's residual window.  Sequence lengths live
+on the device: neither append nor decode needs the host, and both can be captured in a HIP
+graph.  The host keeps a mirror of the lengths only to refuse an append past a capacity.
 """
 
 from __future__ import annotations
@@ -16,7 +22,7 @@ import ctypes
 
 import torch
 
-from . import _lib, fused_ops
+from . import _lib
 from .turboquant import get_turboquant_quantizer
 
 _A16 = 1.123046875  # fp16 LUT magnitude that maps to the centroid a of the 2-bit codebook
@@ -27,10 +33,17 @@ def _round32(n: int) -> int:
 
 
 class TurboQuantBatchCache:
+    """capacities[b]: pool slots (quantized tokens) of sequence b; a sequence holds at most
+    capacities[b] + residual_capacity tokens."""
+
     def __init__(self, *, batch: int, kv_heads: int, q_heads: int, capacities, residual_capacity: int = 128,
                  head_dim: int = 256, bits: int = 2, device="cuda", tokens_per_item: int = 0):
         if head_dim != 256 or bits != 2:
             raise ValueError("TurboQuantBatchCache supports head_dim 256 with 2-bit codes")
+        if q_heads % kv_heads != 0 or q_heads // kv_heads > 16:
+            raise ValueError("q_heads must be G * kv_heads with G <= 16")
+        if tokens_per_item % 32 != 0 or tokens_per_item < 0:
+            raise ValueError("tokens_per_item must be 0 (automatic) or a positive multiple of 32")
         self.batch, self.kv_heads, self.q_heads, self.head_dim, self.bits = batch, kv_heads, q_heads, head_dim, bits
         self.device = torch.device(device)
         self.capacities = [_round32(c) for c in capacities]
@@ -40,7 +53,7 @@ class TurboQuantBatchCache:
             acc += c
         self.pool_tokens = max(32, acc)
         self.offsets = offs
-        self.residual_capacity = _round32(residual_capacity)
+        self.residual_capacity = _round32(max(1, residual_capacity))
         self.tokens_per_item = tokens_per_item
         dev = self.device
         T, R, D = self.pool_tokens, self.residual_capacity, head_dim
@@ -50,23 +63,42 @@ class TurboQuantBatchCache:
         self.value_norms = torch.zeros((kv_heads, T), dtype=torch.float16, device=dev)
         self.residual_key = torch.zeros((batch, kv_heads, R, D), dtype=torch.bfloat16, device=dev)
         self.residual_value_t = torch.zeros((batch, kv_heads, D, R), dtype=torch.bfloat16, device=dev)
-        self.quantized_lens = [0] * batch
-        self.residual_lens = [0] * batch
+        self.seq_offsets = torch.tensor(offs, dtype=torch.int32, device=dev)
+        self.seq_capacity = torch.tensor(self.capacities, dtype=torch.int32, device=dev)
+        self.seq_lengths = torch.zeros((batch,), dtype=torch.int32, device=dev)
+        self.overflow = torch.zeros((1,), dtype=torch.int32, device=dev)
+        self.lengths = [0] * batch  # host mirror
         self.qn = get_turboquant_quantizer(head_dim=D, bits=bits, device=dev)
-        self.rotation_f16 = self.qn.rotation.to(torch.float16)
-        self.rotation_t_f16 = self.qn.rotation_t.to(torch.float16)
+        if self.qn.kind != "hadamard":
+            raise RuntimeError("the batched cache needs the Hadamard rotation (power-of-two head_dim)")
         self.key_scale = float(self.qn.centroids[2].item()) / _A16
         self.value_scale = self.key_scale
-        self._plan = None
+        bpi = tokens_per_item // 32
+        caps = torch.tensor(self.capacities, dtype=torch.int64)
+        self.num_workgroups = int(_lib.load().anna_mi_tq_decode_workgroups(batch, kv_heads, caps.data_ptr(), bpi))
+        nwg = self.num_workgroups
+        self.partial_stats = torch.empty((nwg, 16, 2), dtype=torch.float32, device=dev)
+        self.partial_values = torch.empty((nwg, 16, D), dtype=torch.float32, device=dev)
+        self.tickets = torch.zeros((batch * kv_heads,), dtype=torch.int32, device=dev)
 
-    # ---- filling
-    def load_sequence(self, b: int, keys: torch.Tensor, values: torch.Tensor, residual: int) -> None:
-        """keys/values [Hkv, L, D] (bf16): the first L - residual tokens are packed, the last
-        `residual` tokens stay dense."""
+    # ---- lengths
+    @property
+    def quantized_lens(self) -> list[int]:
+        return [max(0, n - self.residual_capacity) for n in self.lengths]
+
+    @property
+    def residual_lens(self) -> list[int]:
+        return [min(n, self.residual_capacity) for n in self.lengths]
+
+    # ---- filling (prefill)
+    def load_sequence(self, b: int, keys: torch.Tensor, values: torch.Tensor) -> None:
+        """keys/values bf16 [Hkv, L, D]: the sequence's whole history.  Its first
+        max(0, L - R) tokens are packed into the pool, the newest min(L, R) go to the ring."""
         h, L, D = keys.shape
-        q = L - residual
-        if q > self.capacities[b] or residual > self.residual_capacity:
-            raise ValueError("sequence does not fit its capacity")
+        R = self.residual_capacity
+        q = max(0, L - R)
+        if q > self.capacities[b]:
+            raise ValueError(f"sequence {b}: {q} quantized tokens exceed its capacity {self.capacities[b]}")
         off = self.offsets[b]
         if q > 0:
             kc, kn = self.qn.quantize(keys[:, :q].reshape(-1, D))
@@ -80,72 +112,82 @@ class TurboQuantBatchCache:
             for hh in range(h):
                 blk = self.value_codes[hh, off // 32: (off + qp) // 32]
                 _lib.call("anna_mi_tq_block_values", nat[hh].data_ptr(), qp, blk.data_ptr(), _lib.stream_of(nat))
-        if residual > 0:
-            self.residual_key[b, :, :residual].copy_(keys[:, q:])
-            self.residual_value_t[b, :, :, :residual].copy_(values[:, q:].transpose(1, 2))
-        self.quantized_lens[b] = q
-        self.residual_lens[b] = residual
-        self._plan = None
+        if L > q:
+            slots = torch.arange(q, L, device=self.device) % R
+            self.residual_key[b][:, slots] = keys[:, q:]
+            self.residual_value_t[b][:, :, slots] = values[:, q:].transpose(1, 2)
+        self.seq_lengths[b] = L
+        self.lengths[b] = L
 
-    # ---- decode
-    def _make_plan(self):
-        B, H = self.batch, self.kv_heads
-        if self.tokens_per_item > 0:
-            cap = sum(-(-q // self.tokens_per_item) for q in self.quantized_lens) * H + B * H + 1
-        else:
-            cap = max(256, B * H) + B * H + 1
-        items = torch.empty((cap, 4), dtype=torch.int32)
-        ranges = torch.empty((B * H, 4), dtype=torch.int32)
-        ql = torch.tensor(self.quantized_lens, dtype=torch.int64)
-        rl = torch.tensor(self.residual_lens, dtype=torch.int64)
-        so = torch.tensor(self.offsets, dtype=torch.int64)
-        n = ctypes.c_int64(0)
-        _lib.call("anna_mi_tq_decode_plan", B, H, ql.data_ptr(), rl.data_ptr(), so.data_ptr(), self.tokens_per_item,
-                  items.data_ptr(), cap, ranges.data_ptr(), ctypes.addressof(n))
-        n = n.value
-        dev = self.device
-        self._plan = dict(
-            items=items[:n].to(dev), ranges=ranges.to(dev), n=n,
-            ps=torch.empty((max(n, 1), 16, 2), dtype=torch.float32, device=dev),
-            pv=torch.empty((max(n, 1), 16, self.head_dim), dtype=torch.float32, device=dev),
-            qf=torch.empty((B, H, 4096), dtype=torch.float16, device=dev),
-        )
-        return self._plan
+    # ---- decode step
+    def append(self, keys: torch.Tensor, values: torch.Tensor) -> None:
+        """One token per sequence: keys/values bf16 [B, Hkv, D]."""
+        B, H, D = self.batch, self.kv_heads, self.head_dim
+        if keys.dtype != torch.bfloat16 or tuple(keys.shape) != (B, H, D) or values.shape != keys.shape:
+            raise ValueError("append expects bf16 keys/values of shape [batch, kv_heads, 256]")
+        _lib.require_device(keys, values)
+        R = self.residual_capacity
+        for b, n in enumerate(self.lengths):
+            if n >= R and n - R >= self.capacities[b]:
+                raise RuntimeError(f"sequence {b} is full: {self.capacities[b]} pool slots + {R} window tokens")
+        keys, values = keys.contiguous(), values.contiguous()
+        a = _lib.TQAppendArgs()
+        a.batch, a.kv_heads, a.head_dim = B, H, D
+        a.new_key, a.new_value = keys.data_ptr(), values.data_ptr()
+        a.key_codes, a.key_norms = self.key_codes.data_ptr(), self.key_norms.data_ptr()
+        a.value_codes, a.value_norms = self.value_codes.data_ptr(), self.value_norms.data_ptr()
+        a.pool_tokens = self.pool_tokens
+        a.residual_key, a.residual_value_t = self.residual_key.data_ptr(), self.residual_value_t.data_ptr()
+        a.residual_capacity = R
+        a.seq_offsets, a.seq_capacity = self.seq_offsets.data_ptr(), self.seq_capacity.data_ptr()
+        a.seq_lengths, a.overflow = self.seq_lengths.data_ptr(), self.overflow.data_ptr()
+        a.signs, a.thresholds = self.qn.signs.data_ptr(), self.qn.thresholds.data_ptr()
+        _lib.call("anna_mi_tq_append", ctypes.byref(a), _lib.stream_of(keys))
+        self.lengths = [n + 1 for n in self.lengths]
 
-    def decode_args(self, query: torch.Tensor, out: torch.Tensor, scaling: float) -> _lib.TQDecodeArgs:
-        p = self._plan or self._make_plan()
+    def decode_args(self, query: torch.Tensor, out: torch.Tensor, scaling: float,
+                    gate: torch.Tensor | None = None) -> _lib.TQDecodeArgs:
         a = _lib.TQDecodeArgs()
         a.batch, a.q_heads, a.kv_heads, a.head_dim = self.batch, self.q_heads, self.kv_heads, self.head_dim
         a.key_bits = a.value_bits = self.bits
         a.query = query.data_ptr()
+        a.gate = None if gate is None else gate.data_ptr()
         a.key_codes, a.key_norms = self.key_codes.data_ptr(), self.key_norms.data_ptr()
         a.value_codes, a.value_norms = self.value_codes.data_ptr(), self.value_norms.data_ptr()
         a.pool_tokens = self.pool_tokens
         a.residual_key, a.residual_value_t = self.residual_key.data_ptr(), self.residual_value_t.data_ptr()
         a.residual_capacity = self.residual_capacity
-        a.rotation_f16, a.rotation_t_f16 = self.rotation_f16.data_ptr(), self.rotation_t_f16.data_ptr()
+        a.seq_offsets, a.seq_lengths = self.seq_offsets.data_ptr(), self.seq_lengths.data_ptr()
+        a.signs = self.qn.signs.data_ptr()
         a.key_scale, a.value_scale, a.scaling = self.key_scale, self.value_scale, float(scaling)
-        a.items, a.num_items, a.bh_items = p["items"].data_ptr(), p["n"], p["ranges"].data_ptr()
-        a.query_frag = p["qf"].data_ptr()
-        a.partial_stats, a.partial_values = p["ps"].data_ptr(), p["pv"].data_ptr()
+        a.blocks_per_item = self.tokens_per_item // 32
+        a.num_workgroups = self.num_workgroups
+        a.partial_stats, a.partial_values = self.partial_stats.data_ptr(), self.partial_values.data_ptr()
+        a.tickets = self.tickets.data_ptr()
         a.out = out.data_ptr()
         return a
 
-    def decode(self, query: torch.Tensor, *, scaling: float, out: torch.Tensor | None = None) -> torch.Tensor:
-        """query bf16 [B, Hq, D] -> attention output bf16 [B, Hq, D]."""
-        if query.dtype != torch.bfloat16 or tuple(query.shape) != (self.batch, self.q_heads, self.head_dim):
+    def decode(self, query: torch.Tensor, *, scaling: float, out: torch.Tensor | None = None,
+               gate: torch.Tensor | None = None) -> torch.Tensor:
+        """query bf16 [B, Hq, D] -> attention output bf16 [B, Hq, D]; gate (optional, bf16, same
+        shape as query): out *= sigmoid(gate) (the reference's gated decode, sycl:1605-1669)."""
+        shape = (self.batch, self.q_heads, self.head_dim)
+        if query.dtype != torch.bfloat16 or tuple(query.shape) != shape:
             raise ValueError("query must be bf16 [batch, q_heads, 256]")
-        _lib.require_device(query)
+        if gate is not None and (gate.dtype != torch.bfloat16 or tuple(gate.shape) != shape):
+            raise ValueError("gate must be bf16 [batch, q_heads, 256] (the query's shape)")
+        _lib.require_device(query, gate)
         query = query.contiguous()
+        gate = None if gate is None else gate.contiguous()
         if out is None:
             out = torch.empty_like(query)
-        a = self.decode_args(query, out, scaling)
+        a = self.decode_args(query, out, scaling, gate)
         _lib.call("anna_mi_tq_decode", ctypes.byref(a), _lib.stream_of(query))
         return out
 
     def bytes_per_decode(self) -> int:
         """Algorithmic HBM bytes of one decode call: codes + norms of every packed token
-        (K and V), the dense residual window, the query and the output."""
+        (K and V), the dense window, the query and the output."""
         h, d = self.kv_heads, self.head_dim
         packed = sum(self.quantized_lens) * h * 2 * (d // 4 + 2)
         resid = sum(self.residual_lens) * h * 2 * d * 2

@@ -193,8 +193,10 @@ def _clone_cache(c):
     import copy
 
     n = copy.copy(c)
-    for name in ("key_codes", "key_norms", "value_codes", "value_norms", "residual_key", "residual_value_t"):
+    for name in ("key_codes", "key_norms", "value_codes", "value_norms", "residual_key", "residual_value_t",
+                 "seq_lengths", "tickets", "partial_stats", "partial_values"):
         setattr(n, name, getattr(c, name).clone())
+    n.lengths = list(c.lengths)
     return n
 
 
@@ -215,11 +217,10 @@ def section_tq_decode(args, device):
     for b in range(B):
         k = torch.randn((HKV, lens[b] + R, D), device=device, generator=gen).to(torch.bfloat16)
         v = torch.randn((HKV, lens[b] + R, D), device=device, generator=gen).to(torch.bfloat16)
-        base.load_sequence(b, k, v, R)
+        base.load_sequence(b, k, v)
         dense.append((k, v))
     q = torch.randn((B, HQ, D), device=device, generator=gen).to(torch.bfloat16)
     out = torch.empty_like(q)
-    base.decode(q, scaling=1.0 / 16, out=out)  # builds the plan
     per_call = base.bytes_per_decode()
     copies = [base] + [_clone_cache(base) for _ in range(max(1, math.ceil(ROTATE_BYTES / per_call)) - 1)]
     fns = [(lambda c=c: c.decode(q, scaling=1.0 / 16, out=out)) for c in copies]
@@ -230,6 +231,25 @@ def section_tq_decode(args, device):
          "distinct_cache_copies": len(copies), "tokens_per_item": args.tq_tokens_per_item}
     log(f"tq decode B=8 mean L={sum(lens) / 8:.0f}: {r['us']:.2f} us/call  {r['tokens/s']:.0f} tokens/s  "
         f"{r['GB/s']:.0f} GB/s  {100 * r['roofline_frac']:.1f}% of HBM peak")
+    # a whole decode step: append one token per sequence (the oldest window token of each
+    # sequence is quantized into the pool), then decode; on a copy sized for the added tokens
+    steps = max(4, args.steps // 4)
+    # (the graph is replayed warm-up + REPLAYS times, each replay appending `steps` tokens)
+    grow = TurboQuantBatchCache(batch=B, kv_heads=HKV, q_heads=HQ,
+                                capacities=[n + (REPLAYS + 3) * steps + 8 for n in lens],
+                                residual_capacity=R, device=device)
+    for b in range(B):
+        grow.load_sequence(b, dense[b][0], dense[b][1])
+    nk = torch.randn((B, HKV, D), device=device, generator=gen).to(torch.bfloat16)
+    nv = torch.randn((B, HKV, D), device=device, generator=gen).to(torch.bfloat16)
+
+    def step():
+        grow.append(nk, nv)
+        grow.decode(q, scaling=1.0 / 16, out=out)
+
+    ms_step = time_graph([step], steps, 0)
+    r["append_decode_step_us"] = ms_step * 1e3
+    log(f"tq append+decode step: {ms_step * 1e3:.2f} us")
     cpu = None
     if not args.no_cpu:
         from oracle.cpu_paths import tq_decode_rows

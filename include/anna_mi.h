@@ -223,56 +223,90 @@ int64_t anna_mi_gqa_decode_splitkv_noalloc_capacity(void);
 
 /* ------------------------------------------------------------------ batched TQ decode
  * Batched, variable-length single-token GQA decode over a 2-bit TQ-MSE K/V cache
- * (head_dim 256): the batched replacement of the per-row loop of
+ * (head_dim 256, Hadamard rotation): the batched replacement of the per-row loop of
  * Qwen3DynamicCache.turboquant_single_token_decode_attention (src/anna/model/ops.py:1024-1072)
- * over TurboQuantKVRow.decode_attention (turboquant.py:1181-1346).  Layout of the cache:
- * see tq_decode.hip.  Work items come from anna_mi_tq_decode_plan. */
+ * over TurboQuantKVRow.decode_attention (turboquant.py:1181-1346), and of the per-row append of
+ * _update_turboquant_layer (ops.py:618-661) over TurboQuantKVRow.append (turboquant.py:1027-1140).
+ *
+ * Cache per KV head: a pool of token slots (sequence b owns pool slots seq_offsets[b] ..
+ * + its capacity, offsets multiples of 32) holding the quantized prefix, and per sequence a
+ * ring of R dense bf16 tokens holding the newest min(length, R) tokens (token j at ring slot
+ * j % R).  seq_lengths[b] (device) is the total token count; the quantized prefix is
+ * max(0, length - R) tokens.  Layout details: tq_decode.hip. */
 typedef struct {
   int64_t batch, q_heads, kv_heads, head_dim;
-  int key_bits, value_bits;
+  int key_bits, value_bits;         /* 2, 2 */
   const uint16_t* query;            /* bf16 [B][Hq][D] */
+  const uint16_t* gate;             /* bf16 [B][Hq][D] or NULL: out *= sigmoid(gate) */
   const uint8_t* key_codes;         /* [Hkv][pool][D/4] */
   const uint16_t* key_norms;        /* fp16 [Hkv][pool] */
   const uint8_t* value_codes;       /* [Hkv][pool/32][32*D/4] blocked */
   const uint16_t* value_norms;      /* fp16 [Hkv][pool] */
   int64_t pool_tokens;
-  const uint16_t* residual_key;     /* bf16 [B][Hkv][R][D] */
-  const uint16_t* residual_value_t; /* bf16 [B][Hkv][D][R] */
+  const uint16_t* residual_key;     /* bf16 [B][Hkv][R][D] ring */
+  const uint16_t* residual_value_t; /* bf16 [B][Hkv][D][R] ring */
   int64_t residual_capacity;        /* R, multiple of 32 */
-  const uint16_t* rotation_f16;     /* R as fp16 [D][D] */
-  const uint16_t* rotation_t_f16;   /* R^T as fp16 [D][D] */
+  const int32_t* seq_offsets;       /* device [B] */
+  const int32_t* seq_lengths;       /* device [B] */
+  const float* signs;               /* device [D]: the rotation's sign vector */
   float key_scale, value_scale;     /* centroid c = key_scale * fp16 LUT value */
   float scaling;
-  const int32_t* items;             /* [num_items][4] device, from anna_mi_tq_decode_plan */
-  int64_t num_items;
-  const int32_t* bh_items;          /* [B*Hkv][4] device: first item, packed items, residual item or -1, 0 */
-  uint16_t* query_frag;             /* workspace fp16 [B][Hkv][4096]: q' = R q as MFMA fragments */
-  float* partial_stats;             /* workspace [num_items][16][2] */
-  float* partial_values;            /* workspace [num_items][16][D] */
+  int64_t blocks_per_item;          /* 32-token blocks per work item; 0 = sized to fill the GPU */
+  int64_t num_workgroups;           /* grid size, from anna_mi_tq_decode_workgroups */
+  float* partial_stats;             /* workspace [num_workgroups][16][2] */
+  float* partial_values;            /* workspace [num_workgroups][16][D] */
+  int32_t* tickets;                 /* workspace [B*Hkv] int32, zero before the first call (left zero) */
   uint16_t* out;                    /* bf16 [B][Hq][D] */
 } anna_mi_tq_decode_args;
 
-/* Host: split each sequence's quantized prefix (pool slots seq_offsets[b] ..
- * + quantized_lens[b]) into work items (b, kv_head, first slot, end slot) of about
- * tokens_per_item tokens (a multiple of 32; 0 = sized so that all items run at once on the
- * GPU), and add one item (b, kv_head, -1, residual length) per (b, kv_head) with a residual.
- * The packed items of (b, h) are consecutive; bh_items[b*Hkv + h] = {first item, number of
- * packed items, residual item or -1, 0}. */
-int anna_mi_tq_decode_plan(int64_t batch, int64_t kv_heads, const int64_t* quantized_lens_host,
-                           const int64_t* residual_lens_host, const int64_t* seq_offsets_host,
-                           int64_t tokens_per_item, int32_t* items_host, int64_t items_capacity,
-                           int32_t* bh_items_host, int64_t* num_items);
+/* Grid size (workgroups) of anna_mi_tq_decode for sequences of at most pool_capacity[b]
+ * quantized tokens (host array): B*Hkv window workgroups plus enough work-item workgroups for
+ * any lengths up to those capacities. */
+int64_t anna_mi_tq_decode_workgroups(int64_t batch, int64_t kv_heads, const int64_t* pool_capacity_host,
+                                     int64_t blocks_per_item);
+
+/* One launch: every (b, kv head) is split into work items of 32-token blocks of its quantized
+ * prefix plus one window item; the split is planned on the device from seq_lengths (no host
+ * round trip, capturable in a graph).  Each item rotates q itself (FWHT), scores the 2-bit codes
+ * by MFMA and writes log-sum-exp partials; the last item of a (b, kv head) to finish (a ticket
+ * counter) merges them, rotates the result back, adds the window part, applies the gate and
+ * writes bf16.  Sequences of length 0 give zeros.  Calls that share workspaces must not
+ * overlap. */
+int anna_mi_tq_decode(const anna_mi_tq_decode_args* args, void* stream);
+
+typedef struct {
+  int64_t batch, kv_heads, head_dim;
+  const uint16_t* new_key;          /* bf16 [B][Hkv][D]: one token per sequence */
+  const uint16_t* new_value;        /* bf16 [B][Hkv][D] */
+  uint8_t* key_codes;               /* pool, as anna_mi_tq_decode_args */
+  uint16_t* key_norms;
+  uint8_t* value_codes;
+  uint16_t* value_norms;
+  int64_t pool_tokens;
+  uint16_t* residual_key;           /* ring, as anna_mi_tq_decode_args */
+  uint16_t* residual_value_t;
+  int64_t residual_capacity;
+  const int32_t* seq_offsets;       /* device [B] */
+  const int32_t* seq_capacity;      /* device [B]: pool slots of each sequence */
+  int32_t* seq_lengths;             /* device [B], incremented by one */
+  int32_t* overflow;                /* device int32 or NULL: set to 1 when a sequence had no pool slot left */
+  const float* signs;               /* device [D] */
+  const float* thresholds;          /* device [3]: the 2-bit codebook's thresholds */
+} anna_mi_tq_append_args;
+
+/* Appends one token per sequence for all sequences in one launch: the token leaving the ring
+ * (when length >= R) is quantized into the pool (key codes + norm, value codes in the 32-token
+ * blocked layout + norm, bit-exact with anna_mi_tq_hadamard_quantize), the new token takes its
+ * ring slot, and seq_lengths[b] grows by one. */
+int anna_mi_tq_append(const anna_mi_tq_append_args* args, void* stream);
+
+/* Reorders natural 2-bit codes [tokens][64] (D = 256) of one KV head into the blocked value
+ * layout [tokens/32][2048] read by anna_mi_tq_decode (tokens % 32 == 0).  Pure permutation. */
+int anna_mi_tq_block_values(const uint8_t* codes, int64_t tokens, uint8_t* blocked, void* stream);
 
 /* sizeof(anna_mi_tq_decode_args), for binding checks. */
 int64_t anna_mi_sizeof_tq_decode_args(void);
-
-/* Three launches: q' = R q, the split over work items, the combine.  Calls that share
- * workspaces must not overlap. */
-int anna_mi_tq_decode(const anna_mi_tq_decode_args* args, void* stream);
-
-/* Reorders natural 2-bit codes [tokens][64] (D = 256) of one KV head into the blocked
- * value layout [tokens/32][2048] read by anna_mi_tq_decode.  Pure permutation. */
-int anna_mi_tq_block_values(const uint8_t* codes, int64_t tokens, uint8_t* blocked, void* stream);
+int64_t anna_mi_sizeof_tq_append_args(void);
 
 /* ------------------------------------------------------------------ tiled int4 GEMV, LM-head top-k */
 

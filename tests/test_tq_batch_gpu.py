@@ -1,8 +1,9 @@
-"""Batched varlen decode over the 2-bit TQ-MSE pool (the MFMA fast path) against the oracle.
+"""Batched varlen TQ decode and append (the one-launch MFMA path) against the oracle.
 
-Codes and norms in the pool are bit-exact with the oracle quantizer (values after undoing
-the 32-token blocking); the attention output is within normwise max relative error 1e-2
-of the oracle's fp64 attention over the oracle-dequantized cache plus the dense window.
+Pool codes and norms are bit-exact with the oracle's Hadamard quantizer (values after undoing
+the 32-token blocking), the ring holds exactly the newest min(L, R) tokens, and the attention
+output is within normwise max relative error 1e-2 of the oracle's fp64 attention (times
+sigmoid(gate) where given) over the dequantized pool plus the dense window.
 """
 
 import numpy as np
@@ -21,7 +22,7 @@ def bits_of(t):
 
 
 def unblock(blocked: np.ndarray, tokens: int) -> np.ndarray:
-    """[tokens/32][2048] blocked value codes -> natural [tokens][64] (numpy restatement)."""
+    """[tokens/32][2048] blocked value codes -> natural [tokens][64] (loop restatement)."""
     out = np.zeros((tokens, 64), np.uint8)
     for blk in range(tokens // 32):
         for t in range(32):
@@ -30,112 +31,6 @@ def unblock(blocked: np.ndarray, tokens: int) -> np.ndarray:
                 c = (blocked[blk, kq * 512 + dim * 2 + half] >> (2 * e)) & 3
                 out[blk * 32 + t, dim // 4] |= c << (2 * (dim % 4))
     return out
-
-
-@pytest.mark.parametrize("tokens_per_item", [0, 64, 512])
-def test_batched_decode_matches_oracle(gpu, tokens_per_item):
-    torch.manual_seed(60)
-    hkv, g, d = 2, 8, 256
-    lens = [75, 140, 33, 20]
-    resid = [5, 0, 32, 20]  # last sequence: residual only
-    cache = TurboQuantBatchCache(batch=4, kv_heads=hkv, q_heads=hkv * g, capacities=[l - r for l, r in zip(lens, resid)],
-                                 residual_capacity=32, device=gpu, tokens_per_item=tokens_per_item)
-    keys = [torch.randn(hkv, L, d, device=gpu).to(torch.bfloat16) for L in lens]
-    vals = [torch.randn(hkv, L, d, device=gpu).to(torch.bfloat16) for L in lens]
-    for b in range(4):
-        cache.load_sequence(b, keys[b], vals[b], resid[b])
-    q = torch.randn(4, hkv * g, d, device=gpu).to(torch.bfloat16)
-    out = cache.decode(q, scaling=1.0 / 16)
-    R = cache.qn.rotation.cpu().numpy()
-    cent = cache.qn.centroids.cpu().numpy()
-    thr = cache.qn.thresholds.cpu().numpy()
-    kc_pool = cache.key_codes.cpu().numpy()
-    vc_pool = cache.value_codes.cpu().numpy()
-    for b in range(4):
-        ql, off = lens[b] - resid[b], cache.offsets[b]
-        kk, vv = [], []
-        for h in range(hkv):
-            parts_k, parts_v = [], []
-            if ql > 0:
-                kcodes, knorms = orc.tq_mse_quantize(bits_of(keys[b][h, :ql]), orc.BF16, R, thr, 2)
-                vcodes, vnorms = orc.tq_mse_quantize(bits_of(vals[b][h, :ql]), orc.BF16, R, thr, 2)
-                np.testing.assert_array_equal(kc_pool[h, off:off + ql], kcodes)
-                np.testing.assert_array_equal(bits_of(cache.key_norms[h, off:off + ql]), knorms)
-                np.testing.assert_array_equal(bits_of(cache.value_norms[h, off:off + ql]), vnorms)
-                qp = -(-ql // 32) * 32
-                nat = unblock(vc_pool[h, off // 32:(off + qp) // 32], qp)
-                np.testing.assert_array_equal(nat[:ql], vcodes)
-                parts_k.append(orc.tq_mse_dequant(kcodes, knorms, R, cent, 2))
-                parts_v.append(orc.tq_mse_dequant(vcodes, vnorms, R, cent, 2))
-            if resid[b] > 0:
-                parts_k.append(keys[b][h, ql:].float().cpu().numpy())
-                parts_v.append(vals[b][h, ql:].float().cpu().numpy())
-            kk.append(np.concatenate(parts_k))
-            vv.append(np.concatenate(parts_v))
-        ref = orc.gqa_decode(q[b].float().cpu().numpy(), np.stack(kk), np.stack(vv), 1.0 / 16)
-        assert rel_err(out[b].float().cpu().numpy(), ref) <= BF16_TOL, b
-
-
-def np_dequant(codes: np.ndarray, norms_bits: np.ndarray, R: np.ndarray, cent: np.ndarray) -> np.ndarray:
-    """x_hat = |x|_fp16 * R^T c[code] for natural 2-bit codes [n, 64] (fp64, vectorized; the
-    same map as orc.tq_mse_dequant, which is checked against it on a slice below)."""
-    c = np.stack([(codes >> (2 * e)) & 3 for e in range(4)], -1).reshape(codes.shape[0], 256)
-    y = cent.astype(np.float64)[c]
-    return (y @ R.astype(np.float64)) * orc.f16_to_f32(norms_bits).astype(np.float64)[:, None]
-
-
-@pytest.mark.parametrize("tokens_per_item", [0, 512, 2048])
-def test_batched_decode_config4_sizes(gpu, tokens_per_item):
-    """BASELINE config 4 at its own sizes: B=8, Hq=16, Hkv=2, D=256, a full 128-token window on
-    every sequence and packed lengths up to 16,384 (two sequences above 4,000).  tokens_per_item
-    512 gives 32 items for the longest (b, kv-head) (the combine merges > 16 items, in batches),
-    2048 gives 64 blocks per item (each of the 8 split waves runs 4 ping-pong pair iterations).
-    Codes are checked bit-exact on sampled tokens of every (b, kv-head); the output against
-    fp64 attention over the dequantized pool plus the window."""
-    print(f"[case] tq batch config4 tokens_per_item={tokens_per_item}", flush=True)
-    torch.manual_seed(4)
-    B, HKV, G, D, R = 8, 2, 8, 256, 128
-    qlens = [16384, 4100, 1024, 7777, 2048, 1500, 12000, 3001]
-    cache = TurboQuantBatchCache(batch=B, kv_heads=HKV, q_heads=HKV * G, capacities=qlens, residual_capacity=R,
-                                 device=gpu, tokens_per_item=tokens_per_item)
-    keys = [torch.randn(HKV, L + R, D, device=gpu).to(torch.bfloat16) for L in qlens]
-    vals = [torch.randn(HKV, L + R, D, device=gpu).to(torch.bfloat16) for L in qlens]
-    for b in range(B):
-        cache.load_sequence(b, keys[b], vals[b], R)
-    q = torch.randn(B, HKV * G, D, device=gpu).to(torch.bfloat16)
-    out = cache.decode(q, scaling=1.0 / 16).float().cpu().numpy()
-    Rm = cache.qn.rotation.cpu().numpy()
-    cent = cache.qn.centroids.cpu().numpy()
-    thr = cache.qn.thresholds.cpu().numpy()
-    kc_pool = cache.key_codes.cpu().numpy()
-    kn_pool = bits_of(cache.key_norms)
-    vn_pool = bits_of(cache.value_norms)
-    vc_pool = cache.value_codes.cpu().numpy()
-    rng = np.random.default_rng(0)
-    for b in range(B):
-        ql, off = qlens[b], cache.offsets[b]
-        qp = -(-ql // 32) * 32
-        kk, vv = [], []
-        for h in range(HKV):
-            vnat = unblock_fast(vc_pool[h, off // 32:(off + qp) // 32], qp)[:ql]
-            kcodes, vcodes = kc_pool[h, off:off + ql], vnat
-            knorms, vnorms = kn_pool[h, off:off + ql], vn_pool[h, off:off + ql]
-            pick = np.sort(rng.choice(ql, size=min(ql, 96), replace=False))
-            kb, vb = bits_of(keys[b][h, :ql])[pick], bits_of(vals[b][h, :ql])[pick]
-            oc, on = orc.tq_mse_quantize(np.ascontiguousarray(kb), orc.BF16, Rm, thr, 2)
-            np.testing.assert_array_equal(kcodes[pick], oc)
-            np.testing.assert_array_equal(knorms[pick], on)
-            oc, on = orc.tq_mse_quantize(np.ascontiguousarray(vb), orc.BF16, Rm, thr, 2)
-            np.testing.assert_array_equal(vcodes[pick], oc)
-            np.testing.assert_array_equal(vnorms[pick], on)
-            kd = np_dequant(kcodes, knorms, Rm, cent)
-            if b == 0 and h == 0:
-                np.testing.assert_allclose(kd[:64], orc.tq_mse_dequant(kcodes[:64], knorms[:64], Rm, cent, 2),
-                                           rtol=1e-5, atol=1e-6)
-            kk.append(np.concatenate([kd, keys[b][h, ql:].float().cpu().numpy()]))
-            vv.append(np.concatenate([np_dequant(vcodes, vnorms, Rm, cent), vals[b][h, ql:].float().cpu().numpy()]))
-        ref = orc.gqa_decode(q[b].float().cpu().numpy(), np.stack(kk), np.stack(vv), 1.0 / 16)
-        assert rel_err(out[b], ref) <= BF16_TOL, b
 
 
 def unblock_fast(blocked: np.ndarray, tokens: int) -> np.ndarray:
@@ -148,3 +43,195 @@ def unblock_fast(blocked: np.ndarray, tokens: int) -> np.ndarray:
     codes = (sel >> (2 * e)[None, :, None].astype(np.uint8)) & 3
     codes = codes.reshape(tokens, 64, 4)
     return (codes[..., 0] | (codes[..., 1] << 2) | (codes[..., 2] << 4) | (codes[..., 3] << 6)).astype(np.uint8)
+
+
+def test_unblock_fast_matches_loop():
+    b = np.random.default_rng(0).integers(0, 256, size=(3, 2048), dtype=np.uint8)
+    np.testing.assert_array_equal(unblock(b, 96), unblock_fast(b, 96))
+
+
+def np_dequant(codes: np.ndarray, norms_bits: np.ndarray, rot: np.ndarray, cent: np.ndarray) -> np.ndarray:
+    """x_hat = |x|_fp16 * R^T c[code] for natural 2-bit codes [n, 64] (fp64)."""
+    c = np.stack([(codes >> (2 * e)) & 3 for e in range(4)], -1).reshape(codes.shape[0], 256)
+    return (cent.astype(np.float64)[c] @ rot) * orc.f16_to_f32(norms_bits).astype(np.float64)[:, None]
+
+
+def check_against_oracle(cache, hist_k, hist_v, q, out, gate=None, sample=None, seed=0):
+    """hist_k/hist_v[b]: the dense bf16 history [Hkv, L_b, D] of sequence b (GPU tensors).
+    Checks pool codes (all tokens, or `sample` random tokens per (b, h)), the ring, and the
+    output against fp64 attention over dequantized pool + ring."""
+    R = cache.residual_capacity
+    signs = cache.qn.signs.cpu().numpy()
+    rot = orc.tq_hadamard_matrix(signs)
+    cent = cache.qn.centroids.cpu().numpy()
+    thr = cache.qn.thresholds.cpu().numpy()
+    kc_pool, vc_pool = cache.key_codes.cpu().numpy(), cache.value_codes.cpu().numpy()
+    kn_pool, vn_pool = bits_of(cache.key_norms), bits_of(cache.value_norms)
+    ring_k, ring_v = cache.residual_key.cpu(), cache.residual_value_t.cpu()
+    assert cache.seq_lengths.cpu().tolist() == [k.shape[1] for k in hist_k] == cache.lengths
+    out = out.float().cpu().numpy()
+    rng = np.random.default_rng(seed)
+    for b in range(cache.batch):
+        L = hist_k[b].shape[1]
+        ql, off = max(0, L - R), cache.offsets[b]
+        if L == 0:
+            assert not out[b].any()
+            continue
+        qp = -(-ql // 32) * 32
+        kk, vv = [], []
+        hk, hv = hist_k[b].cpu(), hist_v[b].cpu()
+        for h in range(cache.kv_heads):
+            parts_k, parts_v = [], []
+            if ql > 0:
+                kcodes, knorms = kc_pool[h, off:off + ql], kn_pool[h, off:off + ql]
+                vcodes = unblock_fast(vc_pool[h, off // 32:(off + qp) // 32], qp)[:ql]
+                vnorms = vn_pool[h, off:off + ql]
+                pick = np.arange(ql) if sample is None else np.sort(rng.choice(ql, size=min(ql, sample), replace=False))
+                kb = bits_of(hk[h, :ql])[pick]
+                vb = bits_of(hv[h, :ql])[pick]
+                oc, on = orc.tq_hadamard_quantize(np.ascontiguousarray(kb), orc.BF16, signs, thr, 2)
+                np.testing.assert_array_equal(kcodes[pick], oc)
+                np.testing.assert_array_equal(knorms[pick], on)
+                oc, on = orc.tq_hadamard_quantize(np.ascontiguousarray(vb), orc.BF16, signs, thr, 2)
+                np.testing.assert_array_equal(vcodes[pick], oc)
+                np.testing.assert_array_equal(vnorms[pick], on)
+                parts_k.append(np_dequant(kcodes, knorms, rot, cent))
+                parts_v.append(np_dequant(vcodes, vnorms, rot, cent))
+            slots = np.arange(ql, L) % R
+            np.testing.assert_array_equal(bits_of(ring_k[b, h][slots]), bits_of(hk[h, ql:]))
+            np.testing.assert_array_equal(bits_of(ring_v[b, h][:, slots].t()), bits_of(hv[h, ql:]))
+            parts_k.append(hk[h, ql:].float().numpy())
+            parts_v.append(hv[h, ql:].float().numpy())
+            kk.append(np.concatenate(parts_k))
+            vv.append(np.concatenate(parts_v))
+        g = None if gate is None else gate[b].float().cpu().numpy()
+        ref = orc.gqa_decode(q[b].float().cpu().numpy(), np.stack(kk), np.stack(vv), 1.0 / 16, g)
+        assert rel_err(out[b], ref) <= BF16_TOL, b
+
+
+@pytest.mark.parametrize("tokens_per_item,gated", [(0, False), (64, True), (512, False), (32, True)])
+def test_batched_decode_matches_oracle(gpu, tokens_per_item, gated):
+    """Four sequences of 75 / 140 / 33 / 20 tokens with a 32-token window (the last one is
+    window-only); items of 1 to 16 blocks, a gate on two of the cases."""
+    print(f"[case] tq batch small tokens_per_item={tokens_per_item} gate={gated}", flush=True)
+    torch.manual_seed(60)
+    hkv, g, d, R = 2, 8, 256, 32
+    lens = [75, 140, 33, 20]
+    cache = TurboQuantBatchCache(batch=4, kv_heads=hkv, q_heads=hkv * g, capacities=[l - R for l in lens],
+                                 residual_capacity=R, device=gpu, tokens_per_item=tokens_per_item)
+    keys = [torch.randn(hkv, L, d, device=gpu).to(torch.bfloat16) for L in lens]
+    vals = [torch.randn(hkv, L, d, device=gpu).to(torch.bfloat16) for L in lens]
+    for b in range(4):
+        cache.load_sequence(b, keys[b], vals[b])
+    q = torch.randn(4, hkv * g, d, device=gpu).to(torch.bfloat16)
+    gate = torch.randn(4, hkv * g, d, device=gpu).to(torch.bfloat16) if gated else None
+    out = cache.decode(q, scaling=1.0 / 16, gate=gate)
+    check_against_oracle(cache, keys, vals, q, out, gate)
+    assert int(cache.tickets.abs().sum()) == 0  # every ticket left at zero for the next call
+    out2 = cache.decode(q, scaling=1.0 / 16, gate=gate)
+    assert torch.equal(out, out2)  # the merge order is fixed: the same bits every call
+
+
+@pytest.mark.parametrize("tokens_per_item", [0, 512, 2048])
+def test_batched_decode_config4_sizes(gpu, tokens_per_item):
+    """BASELINE config 4 at its own sizes: B=8, Hq=16, Hkv=2, D=256, a full 128-token window on
+    every sequence and packed lengths up to 16,384 (two sequences above 4,000).  tokens_per_item
+    512 gives 32 items for the longest (b, kv-head) (the merge runs 4 batches of 8 items), 2048
+    gives 64 blocks per item (each of the 8 split waves runs 4 ping-pong pair iterations).
+    Codes are checked bit-exact on sampled tokens of every (b, kv-head); the output against
+    fp64 attention over the dequantized pool plus the window."""
+    print(f"[case] tq batch config4 tokens_per_item={tokens_per_item}", flush=True)
+    torch.manual_seed(4)
+    B, HKV, G, D, R = 8, 2, 8, 256, 128
+    qlens = [16384, 4100, 1024, 7777, 2048, 1500, 12000, 3001]
+    cache = TurboQuantBatchCache(batch=B, kv_heads=HKV, q_heads=HKV * G, capacities=qlens, residual_capacity=R,
+                                 device=gpu, tokens_per_item=tokens_per_item)
+    keys = [torch.randn(HKV, L + R, D, device=gpu).to(torch.bfloat16) for L in qlens]
+    vals = [torch.randn(HKV, L + R, D, device=gpu).to(torch.bfloat16) for L in qlens]
+    for b in range(B):
+        cache.load_sequence(b, keys[b], vals[b])
+    q = torch.randn(B, HKV * G, D, device=gpu).to(torch.bfloat16)
+    out = cache.decode(q, scaling=1.0 / 16)
+    check_against_oracle(cache, keys, vals, q, out, sample=96)
+
+
+def test_append_decode_loop_matches_oracle(gpu):
+    """40 decode steps of one append + one decode launch each, from prefilled lengths 0 / 10 /
+    40 / 100 with a 32-token window: tokens leave the ring into the pool from the first step on
+    (bit-exact codes, blocked values written token by token), an empty sequence decodes to
+    zeros, and after 10, 25 and 40 steps the cache and the output match the oracle."""
+    print("[case] tq batch append+decode loop", flush=True)
+    torch.manual_seed(9)
+    B, HKV, G, D, R = 4, 2, 8, 256, 32
+    pre = [0, 10, 40, 100]
+    cache = TurboQuantBatchCache(batch=B, kv_heads=HKV, q_heads=HKV * G, capacities=[64, 64, 64, 128],
+                                 residual_capacity=R, device=gpu)
+    hist_k = [torch.randn(HKV, n, D, device=gpu).to(torch.bfloat16) for n in pre]
+    hist_v = [torch.randn(HKV, n, D, device=gpu).to(torch.bfloat16) for n in pre]
+    for b in range(B):
+        cache.load_sequence(b, hist_k[b], hist_v[b])
+    q = torch.randn(B, HKV * G, D, device=gpu).to(torch.bfloat16)
+    out = cache.decode(q, scaling=1.0 / 16)
+    check_against_oracle(cache, hist_k, hist_v, q, out)
+    for step in range(1, 41):
+        nk = torch.randn(B, HKV, D, device=gpu).to(torch.bfloat16)
+        nv = torch.randn(B, HKV, D, device=gpu).to(torch.bfloat16)
+        cache.append(nk, nv)
+        hist_k = [torch.cat([hist_k[b], nk[b, :, None]], 1) for b in range(B)]
+        hist_v = [torch.cat([hist_v[b], nv[b, :, None]], 1) for b in range(B)]
+        q = torch.randn(B, HKV * G, D, device=gpu).to(torch.bfloat16)
+        out = cache.decode(q, scaling=1.0 / 16)
+        if step in (10, 25, 40):
+            check_against_oracle(cache, hist_k, hist_v, q, out, seed=step)
+    assert int(cache.overflow.item()) == 0
+
+
+def test_append_decode_graph_replays_match_eager(gpu):
+    """One step (append + decode) captured in a HIP graph and replayed 5 times, with eager
+    work and synchronizations in between, gives the same bits as the same steps run eagerly
+    on a twin cache."""
+    print("[case] tq batch graph replay", flush=True)
+    torch.manual_seed(12)
+    B, HKV, G, D, R = 3, 2, 8, 256, 32
+    pre = [5, 31, 70]
+    caches = [TurboQuantBatchCache(batch=B, kv_heads=HKV, q_heads=HKV * G, capacities=[64] * B,
+                                   residual_capacity=R, device=gpu) for _ in range(2)]
+    for b in range(B):
+        k = torch.randn(HKV, pre[b], D, device=gpu).to(torch.bfloat16)
+        v = torch.randn(HKV, pre[b], D, device=gpu).to(torch.bfloat16)
+        for c in caches:
+            c.load_sequence(b, k, v)
+    nk = torch.empty(B, HKV, D, device=gpu, dtype=torch.bfloat16)
+    nv = torch.empty_like(nk)
+    q = torch.empty(B, HKV * G, D, device=gpu, dtype=torch.bfloat16)
+    out_g = torch.empty_like(q)
+    graph_cache, eager_cache = caches
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        graph_cache.append(nk, nv)
+        graph_cache.decode(q, scaling=1.0 / 16, out=out_g)
+    graph_cache.lengths = list(pre)  # capture ran no kernel: the host mirror rolls back
+    for step in range(5):
+        nk.copy_(torch.randn(B, HKV, D, device=gpu).to(torch.bfloat16))
+        nv.copy_(torch.randn(B, HKV, D, device=gpu).to(torch.bfloat16))
+        q.copy_(torch.randn(B, HKV * G, D, device=gpu).to(torch.bfloat16))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        eager_cache.append(nk, nv)
+        ref = eager_cache.decode(q, scaling=1.0 / 16)
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, ref), step
+        assert torch.equal(graph_cache.seq_lengths, eager_cache.seq_lengths)
+        assert torch.equal(graph_cache.key_codes, eager_cache.key_codes)
+        assert torch.equal(graph_cache.value_codes, eager_cache.value_codes)
+
+
+def test_append_refuses_a_full_sequence(gpu):
+    cache = TurboQuantBatchCache(batch=1, kv_heads=1, q_heads=8, capacities=[32], residual_capacity=32, device=gpu)
+    k = torch.randn(1, 64, 256, device=gpu).to(torch.bfloat16)
+    cache.load_sequence(0, k, k)
+    with pytest.raises(RuntimeError, match="sequence 0 is full"):
+        cache.append(k[:, :1], k[:, :1])
