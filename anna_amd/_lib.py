@@ -77,7 +77,18 @@ class TQAppendArgs(ctypes.Structure):
     ]
 
 
+class TQPackArgs(ctypes.Structure):
+    """anna_mi_tq_pack_args."""
+
+    _fields_ = [
+        ("kv_heads", _I64), ("head_dim", _I64), ("tokens", _I64), ("keys", _P), ("values", _P),
+        ("stride_head", _I64), ("stride_token", _I64), ("key_codes", _P), ("key_norms", _P), ("value_codes", _P),
+        ("value_norms", _P), ("pool_tokens", _I64), ("slot_offset", _I64), ("signs", _P), ("thresholds", _P),
+    ]
+
+
 PROTOTYPES.update({
+    "anna_mi_tq_pack_kv": [ctypes.POINTER(TQPackArgs), _P],
     "anna_mi_tq_decode": [ctypes.POINTER(TQDecodeArgs), _P],
     "anna_mi_tq_append": [ctypes.POINTER(TQAppendArgs), _P],
     "anna_mi_tq_block_values": [_P, _I64, _P, _P],
@@ -133,6 +144,7 @@ RAW_PROTOTYPES: dict[str, tuple] = {
     "anna_mi_gqa_decode_splitkv_noalloc_capacity": (_I64, []),
     "anna_mi_sizeof_tq_decode_args": (_I64, []),
     "anna_mi_sizeof_tq_append_args": (_I64, []),
+    "anna_mi_sizeof_tq_pack_args": (_I64, []),
     "anna_mi_tq_decode_workgroups": (_I64, [_I64, _I64, _P, _I64]),
 }
 

@@ -707,6 +707,62 @@ __global__ __launch_bounds__(256) void tq_append_kernel(const anna_mi_tq_append_
   if (threadIdx.x == 0) a.seq_lengths[b] = n + 1;
 }
 
+
+// ------------------------------------------------------------------ pack (prefill)
+
+// K and V of `tokens` tokens of every KV head into the pool (one launch): wave w of the grid
+// takes 4 consecutive tokens t0 .. t0 + 3 of one (head, K or V) (the four tokens of one byte of
+// the blocked value layout), quantizes them with the Hadamard quantizer (bit-exact with
+// anna_mi_tq_hadamard_quantize) and writes key codes token-major, value codes in the 32-token
+// blocked layout, and the fp16 norms.
+__global__ __launch_bounds__(256) void tq_pack_kv_kernel(const anna_mi_tq_pack_args a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t quads = (a.tokens + 3) / 4;
+  const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wid >= 2 * a.kv_heads * quads) return;  // whole wave
+  const int64_t q4 = wid % quads, hv = wid / quads, h = hv >> 1;
+  const bool is_v = hv & 1;
+  const int64_t t0 = q4 * 4;
+  const uint16_t* src = (is_v ? a.values : a.keys) + h * a.stride_head;
+  float xv[4][4];
+#pragma unroll
+  for (int n = 0; n < 4; ++n) {
+    const int64_t t = t0 + n < a.tokens ? t0 + n : a.tokens - 1;  // tail: repeats the last token
+    const uint2 raw = *(const uint2*)(src + t * a.stride_token + 4 * lane);
+    xv[n][0] = bf16_bits_to_f32((uint16_t)(raw.x & 0xFFFFu));
+    xv[n][1] = bf16_bits_to_f32((uint16_t)(raw.x >> 16));
+    xv[n][2] = bf16_bits_to_f32((uint16_t)(raw.y & 0xFFFFu));
+    xv[n][3] = bf16_bits_to_f32((uint16_t)(raw.y >> 16));
+  }
+  uint32_t code[4][4];
+  float nrm[4];
+  hadamard_codes_wave_n<4, 4>(xv, a.signs, a.thresholds, 3, 1.0f / 16.0f, code, nrm);
+  const int64_t T = a.pool_tokens, slot0 = a.slot_offset + t0;
+  const int nvalid = a.tokens - t0 < 4 ? (int)(a.tokens - t0) : 4;
+  const float nrm_lane = lane == 0 ? nrm[0] : lane == 1 ? nrm[1] : lane == 2 ? nrm[2] : nrm[3];  // lanes 0..3 store
+  if (!is_v) {
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+      if (n < nvalid)
+        a.key_codes[(h * T + slot0 + n) * 64 + lane] =
+            (uint8_t)(code[n][0] | (code[n][1] << 2) | (code[n][2] << 4) | (code[n][3] << 6));
+    if (lane < nvalid) a.key_norms[h * T + slot0 + lane] = f32_to_f16_bits(nrm_lane);
+  } else {
+    // slot0 % 4 == 0: the quad fills bits 0..7 of one byte per dim
+    const int64_t t = slot0 % TBT;
+    uint8_t* blk = a.value_codes + (h * (T / TBT) + slot0 / TBT) * 2048 + ((t % 16) / 4) * 512 + (t / 16);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      uint32_t byte = 0;
+#pragma unroll
+      for (int n = 0; n < 4; ++n)
+        if (n < nvalid) byte |= code[n][e] << (2 * n);
+      blk[(4 * lane + e) * 2] = (uint8_t)byte;
+    }
+    if (lane < nvalid) a.value_norms[h * T + slot0 + lane] = f32_to_f16_bits(nrm_lane);
+  }
+}
+
 // ------------------------------------------------------------------ value blocking
 
 // natural codes [tokens][64] -> blocked [tokens/32][2048]; one thread per output byte.
@@ -788,6 +844,28 @@ extern "C" int anna_mi_tq_append(const anna_mi_tq_append_args* ap, void* stream)
              "anna_mi_tq_append: null pointer");
   hipLaunchKernelGGL(tq_append_kernel, dim3((unsigned)a.batch), dim3(256), 0, as_stream(stream), a);
   ANNA_LAUNCH_CHECK("tq_append_kernel");
+  return ANNA_MI_OK;
+}
+
+extern "C" int64_t anna_mi_sizeof_tq_pack_args(void) { return (int64_t)sizeof(anna_mi_tq_pack_args); }
+
+extern "C" int anna_mi_tq_pack_kv(const anna_mi_tq_pack_args* ap, void* stream) {
+  ANNA_CHECK(ap != nullptr, "anna_mi_tq_pack_kv: null args");
+  const anna_mi_tq_pack_args& a = *ap;
+  ANNA_CHECK(a.head_dim == TD, "anna_mi_tq_pack_kv: head_dim must be 256");
+  ANNA_CHECK(a.keys && a.values && a.key_codes && a.key_norms && a.value_codes && a.value_norms && a.signs &&
+                 a.thresholds,
+             "anna_mi_tq_pack_kv: null pointer");
+  ANNA_CHECK(a.kv_heads > 0 && a.tokens >= 0, "anna_mi_tq_pack_kv: bad sizes");
+  ANNA_CHECK(a.slot_offset % TBT == 0 && a.pool_tokens % TBT == 0 && a.slot_offset + a.tokens <= a.pool_tokens,
+             "anna_mi_tq_pack_kv: slots must start at a multiple of 32 and fit the pool");
+  ANNA_CHECK(a.stride_token >= TD && a.stride_token % 4 == 0 && a.stride_head % 4 == 0 &&
+                 (uintptr_t)a.keys % 8 == 0 && (uintptr_t)a.values % 8 == 0,
+             "anna_mi_tq_pack_kv: rows must be 8-byte aligned with a stride of at least 256");
+  if (a.tokens == 0) return ANNA_MI_OK;
+  const int64_t waves = 2 * a.kv_heads * ((a.tokens + 3) / 4);
+  hipLaunchKernelGGL(tq_pack_kv_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, as_stream(stream), a);
+  ANNA_LAUNCH_CHECK("tq_pack_kv_kernel");
   return ANNA_MI_OK;
 }
 

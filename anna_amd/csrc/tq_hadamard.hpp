@@ -44,65 +44,133 @@ __host__ __device__ inline float tq_inv_sqrt(int64_t D) {
   return (float)(1.0 / __builtin_sqrt((double)D));
 }
 
-// In-place FWHT of the E elements each lane holds (stages as above, no scaling).
-template <int E>
-__device__ __forceinline__ void fwht_wave(float (&v)[E]) {
+// Value of lane (lane ^ M) for the wave's 64 lanes: DPP quad permutes for M = 1, 2, LDS swizzles
+// (bit mode, inside 32-lane halves) for 4, 8, 16, a bpermute for 32.  Exact copies, so the
+// arithmetic around them is the same whichever exchange is used.
+template <int M>
+__device__ __forceinline__ float xor_lane(float v) {
+  if constexpr (M == 1) return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+  else if constexpr (M == 2) return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
+  else if constexpr (M < 32) return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), (M << 10) | 0x1F));
+  else return __shfl_xor(v, 32, 64);
+}
+
+template <int M, int NV, int E>
+__device__ __forceinline__ void fwht_lane_stage(float (&v)[NV][E], bool upper) {
+#pragma unroll
+  for (int n = 0; n < NV; ++n)
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const float p = xor_lane<M>(v[n][e]);
+      v[n][e] = upper ? p - v[n][e] : v[n][e] + p;
+    }
+}
+
+// In-place FWHT of NV vectors at once (independent chains), E elements of each per lane (stages
+// as above, no scaling).
+template <int NV, int E>
+__device__ __forceinline__ void fwht_wave_n(float (&v)[NV][E]) {
   // stages inside a lane: index bits 0 .. log2(E) - 1
 #pragma unroll
   for (int h = 1; h < E; h <<= 1) {
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      if ((e & h) == 0) {
-        const float a = v[e], c = v[e + h];
-        v[e] = a + c;
-        v[e + h] = a - c;
+    for (int n = 0; n < NV; ++n)
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        if ((e & h) == 0) {
+          const float a = v[n][e], c = v[n][e + h];
+          v[n][e] = a + c;
+          v[n][e + h] = a - c;
+        }
       }
-    }
   }
   // stages across lanes: index bits log2(E) .. log2(E) + 5 = lane bits 0 .. 5
   const int lane = threadIdx.x & 63;
+  fwht_lane_stage<1>(v, (lane & 1) != 0);
+  fwht_lane_stage<2>(v, (lane & 2) != 0);
+  fwht_lane_stage<4>(v, (lane & 4) != 0);
+  fwht_lane_stage<8>(v, (lane & 8) != 0);
+  fwht_lane_stage<16>(v, (lane & 16) != 0);
+  fwht_lane_stage<32>(v, (lane & 32) != 0);
+}
+
+template <int E>
+__device__ __forceinline__ void fwht_wave(float (&v)[E]) {
+  float w[1][E];
 #pragma unroll
-  for (int m = 1; m < 64; m <<= 1) {
-    const bool upper = (lane & m) != 0;
+  for (int e = 0; e < E; ++e) w[0][e] = v[e];
+  fwht_wave_n<1, E>(w);
+#pragma unroll
+  for (int e = 0; e < E; ++e) v[e] = w[0][e];
+}
+
+// |x|^2 of NV vectors in the fixed order above (every lane gets the totals).
+template <int NV, int E>
+__device__ __forceinline__ void sumsq_wave_n(const float (&x)[NV][E], float (&out)[NV]) {
+#pragma unroll
+  for (int n = 0; n < NV; ++n) {
+    float p = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) p = __builtin_fmaf(x[n][e], x[n][e], p);
+    out[n] = p;
+  }
+#pragma unroll
+  for (int n = 0; n < NV; ++n) out[n] = out[n] + xor_lane<1>(out[n]);
+#pragma unroll
+  for (int n = 0; n < NV; ++n) out[n] = out[n] + xor_lane<2>(out[n]);
+#pragma unroll
+  for (int n = 0; n < NV; ++n) out[n] = out[n] + xor_lane<4>(out[n]);
+#pragma unroll
+  for (int n = 0; n < NV; ++n) out[n] = out[n] + xor_lane<8>(out[n]);
+#pragma unroll
+  for (int n = 0; n < NV; ++n) out[n] = out[n] + xor_lane<16>(out[n]);
+#pragma unroll
+  for (int n = 0; n < NV; ++n) out[n] = out[n] + xor_lane<32>(out[n]);
+}
+
+// Quantize NV vectors of the wave (lane's E elements each, fp32 values of the input): the lane's
+// E codes per vector (1 byte each) and the norms (all lanes).
+template <int NV, int E>
+__device__ __forceinline__ void hadamard_codes_wave_n(const float (&x)[NV][E], const float* __restrict__ signs,
+                                                      const float* __restrict__ thr, int nthr, float inv,
+                                                      uint32_t (&code)[NV][E], float (&nrm)[NV]) {
+  const int lane = threadIdx.x & 63;
+  float ss[NV];
+  sumsq_wave_n<NV, E>(x, ss);
+#pragma unroll
+  for (int n = 0; n < NV; ++n) nrm[n] = __builtin_sqrtf(ss[n]);
+  float sg[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) sg[e] = signs[lane * E + e];
+  float v[NV][E];
+#pragma unroll
+  for (int n = 0; n < NV; ++n)
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[n][e] = x[n][e] * sg[e];
+  fwht_wave_n<NV, E>(v);
+#pragma unroll
+  for (int n = 0; n < NV; ++n)
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-      const float p = __shfl_xor(v[e], m, 64);
-      v[e] = upper ? p - v[e] : v[e] + p;
+      const float y = v[n][e] * inv;
+      uint32_t c = 0;
+      for (int j = 0; j < nthr; ++j) c += y >= __fmul_rn(thr[j], nrm[n]) ? 1u : 0u;
+      code[n][e] = c;
     }
-  }
 }
 
-// |x|^2 of the wave's vector in the fixed order above (every lane gets the total).
-template <int E>
-__device__ __forceinline__ float sumsq_wave(const float (&x)[E]) {
-  float p = 0.f;
-#pragma unroll
-  for (int e = 0; e < E; ++e) p = __builtin_fmaf(x[e], x[e], p);
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) p = p + __shfl_xor(p, m, 64);
-  return p;
-}
-
-// Quantize the wave's vector x (lane's E elements, fp32 values of the input): the lane's E codes
-// (1 byte each) and the norm (all lanes).
 template <int E>
 __device__ __forceinline__ float hadamard_codes_wave(const float (&x)[E], const float* __restrict__ signs,
                                                      const float* __restrict__ thr, int nthr, float inv,
                                                      uint32_t (&code)[E]) {
-  const int lane = threadIdx.x & 63;
-  const float nrm = __builtin_sqrtf(sumsq_wave<E>(x));
-  float v[E];
+  float xv[1][E], nrm[1];
+  uint32_t c[1][E];
 #pragma unroll
-  for (int e = 0; e < E; ++e) v[e] = x[e] * signs[lane * E + e];
-  fwht_wave<E>(v);
+  for (int e = 0; e < E; ++e) xv[0][e] = x[e];
+  hadamard_codes_wave_n<1, E>(xv, signs, thr, nthr, inv, c, nrm);
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const float y = v[e] * inv;
-    uint32_t c = 0;
-    for (int j = 0; j < nthr; ++j) c += y >= __fmul_rn(thr[j], nrm) ? 1u : 0u;
-    code[e] = c;
-  }
-  return nrm;
+  for (int e = 0; e < E; ++e) code[e] = c[0][e];
+  return nrm[0];
 }
 
 }  // namespace anna

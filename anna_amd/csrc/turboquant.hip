@@ -168,36 +168,53 @@ __global__ __launch_bounds__(1024) void tq_mse_quantize_kernel(
   }
 }
 
-// Hadamard TQ-MSE quantizer: one wave per vector (4 per 256-thread workgroup), lane l holds
-// elements l*E .. l*E + E - 1 (E = D / 64).
+// Hadamard TQ-MSE quantizer: each wave takes HNV vectors at once (their shuffle chains are
+// independent, so their latencies overlap), 4 waves per 256-thread workgroup; lane l holds
+// elements l*E .. l*E + E - 1 of each (E = D / 64).
+constexpr int HNV = 4;
+
 template <int XDT, int E>
 __global__ __launch_bounds__(256) void tq_hadamard_quantize_kernel(
     const typename Elem<XDT>::T* __restrict__ x, int64_t nvec, int64_t D, int64_t xs,
     const float* __restrict__ signs, const float* __restrict__ thr, int bits, uint8_t* __restrict__ codes,
     uint16_t* __restrict__ norms) {
   const int lane = threadIdx.x & 63;
-  const int64_t v = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (v >= nvec) return;  // whole wave
-  float xv[E];
+  const int64_t v0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * HNV;
+  if (v0 >= nvec) return;  // whole wave
+  float xv[HNV][E];
 #pragma unroll
-  for (int e = 0; e < E; ++e) xv[e] = Elem<XDT>::load(x, v * xs + lane * E + e);
-  uint32_t code[E];
-  const float nrm = hadamard_codes_wave<E>(xv, signs, thr, (1 << bits) - 1, tq_inv_sqrt(D), code);
-  if (lane == 0) norms[v] = f32_to_f16_bits(nrm);
+  for (int n = 0; n < HNV; ++n) {
+    const int64_t v = v0 + n < nvec ? v0 + n : nvec - 1;  // clamped: the tail wave repeats its last vector
+#pragma unroll
+    for (int e = 0; e < E; ++e) xv[n][e] = Elem<XDT>::load(x, v * xs + lane * E + e);
+  }
+  uint32_t code[HNV][E];
+  float nrm[HNV];
+  hadamard_codes_wave_n<HNV, E>(xv, signs, thr, (1 << bits) - 1, tq_inv_sqrt(D), code, nrm);
   const int sb = storage_bits(bits);
   const int64_t pb = D * sb / 8;  // packed bytes per vector
-  uint64_t pk = 0;
-#pragma unroll
-  for (int e = 0; e < E; ++e) pk |= (uint64_t)code[e] << (sb * e);
   const int nbits = E * sb;
-  uint8_t* dst = codes + v * pb;
-  if (nbits >= 8) {
-    for (int k = 0; k < nbits / 8; ++k) dst[lane * (nbits / 8) + k] = (uint8_t)(pk >> (8 * k));
-  } else {
-    const int per = 8 / nbits;  // lanes per byte
-    uint32_t b = (uint32_t)pk << (nbits * (lane % per));
-    for (int m = 1; m < per; m <<= 1) b |= (uint32_t)__shfl_xor((int)b, m, 64);
-    if (lane % per == 0) dst[lane / per] = (uint8_t)b;
+#pragma unroll
+  for (int n = 0; n < HNV; ++n) {
+    const int64_t v = v0 + n;
+    if (v >= nvec) break;
+    if (lane == 0) norms[v] = f32_to_f16_bits(nrm[n]);
+    uint64_t pk = 0;
+#pragma unroll
+    for (int e = 0; e < E; ++e) pk |= (uint64_t)code[n][e] << (sb * e);
+    uint8_t* dst = codes + v * pb;
+    if (nbits == 8) {
+      dst[lane] = (uint8_t)pk;
+    } else if (nbits == 16) {
+      ((uint16_t*)dst)[lane] = (uint16_t)pk;
+    } else if (nbits > 8) {
+      for (int k = 0; k < nbits / 8; ++k) dst[lane * (nbits / 8) + k] = (uint8_t)(pk >> (8 * k));
+    } else {
+      const int per = 8 / nbits;  // lanes per byte
+      uint32_t b = (uint32_t)pk << (nbits * (lane % per));
+      for (int m = 1; m < per; m <<= 1) b |= (uint32_t)__shfl_xor((int)b, m, 64);
+      if (lane % per == 0) dst[lane / per] = (uint8_t)b;
+    }
   }
 }
 
@@ -325,7 +342,7 @@ extern "C" int anna_mi_tq_hadamard_quantize(const void* x, int x_dtype, int64_t 
              "anna_mi_tq_hadamard_quantize: head_dim must be a power of two in [64, 1024]");
   ANNA_CHECK(x_row_stride >= D, "anna_mi_tq_hadamard_quantize: row stride smaller than head_dim");
   if (nvec <= 0) return ANNA_MI_OK;
-  const dim3 grid((unsigned)((nvec + 3) / 4));
+  const dim3 grid((unsigned)((nvec + 4 * HNV - 1) / (4 * HNV)));
   ANNA_DISPATCH_DTYPE(x_dtype, XDT, {
     auto go = [&](auto e_tag) {
       constexpr int E = decltype(e_tag)::value;

@@ -101,23 +101,30 @@ class TurboQuantBatchCache:
             raise ValueError(f"sequence {b}: {q} quantized tokens exceed its capacity {self.capacities[b]}")
         off = self.offsets[b]
         if q > 0:
-            kc, kn = self.qn.quantize(keys[:, :q].reshape(-1, D))
-            vc, vn = self.qn.quantize(values[:, :q].reshape(-1, D))
-            self.key_codes[:, off: off + q].copy_(kc.view(h, q, -1))
-            self.key_norms[:, off: off + q].copy_(kn.view(h, q))
-            self.value_norms[:, off: off + q].copy_(vn.view(h, q))
-            qp = _round32(q)
-            nat = torch.zeros((h, qp, D // 4), dtype=torch.uint8, device=self.device)
-            nat[:, :q].copy_(vc.view(h, q, -1))
-            for hh in range(h):
-                blk = self.value_codes[hh, off // 32: (off + qp) // 32]
-                _lib.call("anna_mi_tq_block_values", nat[hh].data_ptr(), qp, blk.data_ptr(), _lib.stream_of(nat))
+            if keys.dtype != torch.bfloat16 or values.dtype != torch.bfloat16:
+                raise ValueError("keys/values must be bf16")
+            k, v = keys, values
+            if k.stride(2) != 1 or v.stride() != k.stride():  # the pack reads both with one set of strides
+                k, v = keys.contiguous(), values.contiguous()
+            self._pack(k, v, q, off)
         if L > q:
             slots = torch.arange(q, L, device=self.device) % R
             self.residual_key[b][:, slots] = keys[:, q:]
             self.residual_value_t[b][:, :, slots] = values[:, q:].transpose(1, 2)
         self.seq_lengths[b] = L
         self.lengths[b] = L
+
+    def _pack(self, keys: torch.Tensor, values: torch.Tensor, tokens: int, slot_offset: int) -> None:
+        """One launch: the first `tokens` tokens of keys/values [Hkv, L, D] into the pool."""
+        a = _lib.TQPackArgs()
+        a.kv_heads, a.head_dim, a.tokens = keys.shape[0], self.head_dim, tokens
+        a.keys, a.values = keys.data_ptr(), values.data_ptr()
+        a.stride_head, a.stride_token = keys.stride(0), keys.stride(1)
+        a.key_codes, a.key_norms = self.key_codes.data_ptr(), self.key_norms.data_ptr()
+        a.value_codes, a.value_norms = self.value_codes.data_ptr(), self.value_norms.data_ptr()
+        a.pool_tokens, a.slot_offset = self.pool_tokens, slot_offset
+        a.signs, a.thresholds = self.qn.signs.data_ptr(), self.qn.thresholds.data_ptr()
+        _lib.call("anna_mi_tq_pack_kv", ctypes.byref(a), _lib.stream_of(keys))
 
     # ---- decode step
     def append(self, keys: torch.Tensor, values: torch.Tensor) -> None:

@@ -300,6 +300,29 @@ typedef struct {
  * ring slot, and seq_lengths[b] grows by one. */
 int anna_mi_tq_append(const anna_mi_tq_append_args* args, void* stream);
 
+typedef struct {
+  int64_t kv_heads, head_dim, tokens;
+  const uint16_t* keys;             /* bf16, element (h, t, d) at h * stride_head + t * stride_token + d */
+  const uint16_t* values;           /* bf16, same strides */
+  int64_t stride_head, stride_token;
+  uint8_t* key_codes;               /* pool, as anna_mi_tq_decode_args */
+  uint16_t* key_norms;
+  uint8_t* value_codes;
+  uint16_t* value_norms;
+  int64_t pool_tokens;
+  int64_t slot_offset;              /* first pool slot written (multiple of 32) */
+  const float* signs;               /* device [D] */
+  const float* thresholds;          /* device [3] */
+} anna_mi_tq_pack_args;
+
+/* Packs `tokens` tokens of K and V of every KV head into pool slots slot_offset .. + tokens in
+ * one launch: Hadamard TQ-MSE codes (bit-exact with anna_mi_tq_hadamard_quantize), key codes
+ * token-major, value codes in the 32-token blocked layout, fp16 norms.  The bulk (prefill)
+ * counterpart of the per-token quantization in TurboQuantKVRow.append (turboquant.py:1027-1140)
+ * and of TurboQuantTensorRow.append (turboquant.py:335-477) for BASELINE config 3. */
+int anna_mi_tq_pack_kv(const anna_mi_tq_pack_args* args, void* stream);
+int64_t anna_mi_sizeof_tq_pack_args(void);
+
 /* Reorders natural 2-bit codes [tokens][64] (D = 256) of one KV head into the blocked value
  * layout [tokens/32][2048] read by anna_mi_tq_decode (tokens % 32 == 0).  Pure permutation. */
 int anna_mi_tq_block_values(const uint8_t* codes, int64_t tokens, uint8_t* blocked, void* stream);

@@ -235,3 +235,37 @@ def test_append_refuses_a_full_sequence(gpu):
     cache.load_sequence(0, k, k)
     with pytest.raises(RuntimeError, match="sequence 0 is full"):
         cache.append(k[:, :1], k[:, :1])
+
+
+def test_pack_config3_layout_bit_exact(gpu):
+    """K, V bf16 [8192 tokens, 2 kv heads, 256] ~N(0,1) with 1% outlier
+    channels x8, read in that token-major layout (head stride 256, token stride 512) by one pack
+    launch; every key and value code and norm of the 8064 packed tokens is bit-exact with the
+    oracle's Hadamard quantizer (values after undoing the blocking)."""
+    print("[case] tq pack config3", flush=True)
+    T, H, D, R = 8192, 2, 256, 128
+    g = torch.Generator(device=gpu)
+    g.manual_seed(33)
+    outl = torch.zeros(D, dtype=torch.bool)
+    outl[torch.randperm(D, generator=torch.Generator().manual_seed(3))[: D // 100]] = True
+    kv = []
+    for _ in range(2):
+        x = torch.randn((T, H, D), device=gpu, generator=g)
+        x[..., outl.to(gpu)] *= 8.0
+        kv.append(x.to(torch.bfloat16))
+    cache = TurboQuantBatchCache(batch=1, kv_heads=H, q_heads=H * 8, capacities=[T - R], residual_capacity=R,
+                                 device=gpu)
+    cache._pack(kv[0].transpose(0, 1), kv[1].transpose(0, 1), T - R, 0)  # [H, T, D] views, strides (256, 512, 1)
+    signs = cache.qn.signs.cpu().numpy()
+    thr = cache.qn.thresholds.cpu().numpy()
+    n = T - R
+    for h in range(H):
+        for which, x in enumerate(kv):
+            oc, on = orc.tq_hadamard_quantize(np.ascontiguousarray(bits_of(x[:n, h])), orc.BF16, signs, thr, 2)
+            if which == 0:
+                np.testing.assert_array_equal(cache.key_codes[h, :n].cpu().numpy(), oc)
+                np.testing.assert_array_equal(bits_of(cache.key_norms[h, :n]), on)
+            else:
+                got = unblock_fast(cache.value_codes[h, : n // 32].cpu().numpy(), n)
+                np.testing.assert_array_equal(got, oc)
+                np.testing.assert_array_equal(bits_of(cache.value_norms[h, :n]), on)
