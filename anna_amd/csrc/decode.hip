@@ -19,6 +19,7 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "int4_frag.hpp"
 
 namespace anna {
 namespace {
@@ -495,6 +496,267 @@ __global__ __launch_bounds__(MERGE_THREADS) void decode_merge_kernel(const anna_
   }
 }
 
+// ------------------------------------------------------------------ MFMA split kernel
+//
+// Fast path of the split kernel for 16-bit activations, dense keys (packed segment and window)
+// and dense or min/max-packed values, head_dim 64/128/256, G <= 16 query heads per KV head.
+// Workgroup: 2 waves per (block, KV head, batch); each wave takes 32-token tiles of the block.
+//   * S^T = K Q^T by v_mfma_f32_16x16x32 (A = 16 key rows x 32 dims straight from memory, B = the
+//     query heads staged in LDS as fragments; two MFMAs per 32 dims for tokens r and 16 + r).
+//   * Online softmax in base 2; the probabilities' accumulator layout is already the A operand of
+//     O = P V (16 heads x 32 tokens, token k of lane (head, kq) = 4 kq + e (e < 4) or
+//     16 + 4 kq + e - 4), so P never leaves registers.
+//   * V of the tile is staged in LDS transposed, [dim][token] in the activation dtype (min/max
+//     codes dequantized as q * scale + zero on the way; window tokens copied), so that the B
+//     operand of lane (dim, kq) is two 8-byte reads.
+// The partials have the reference layout (natural-log max, denominator, unnormalized values),
+// so decode_merge_kernel merges them as for the VALU kernel.
+constexpr int MF_WAVES = 2;
+constexpr int MF_TILE = 32;              // tokens per wave tile
+constexpr int MF_VT = MF_TILE + 4;       // LDS pitch (elements) of the transposed V tile: 18 words,
+                                         // so the 16 dims of a B-operand read hit distinct banks
+
+template <int DT>
+__device__ __forceinline__ uint32_t pack2_16(float lo, float hi) {
+  if constexpr (DT == ANNA_MI_BF16) return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+  else return (uint32_t)f32_to_f16_bits(lo) | ((uint32_t)f32_to_f16_bits(hi) << 16);
+}
+
+template <int DT, int VF, int D>
+__global__ __launch_bounds__(64 * MF_WAVES) void decode_split_mfma_kernel(const anna_mi_decode_args a, const Split sp) {
+  constexpr int NST = D / 32;  // 32-dim steps of the score product
+  constexpr int NDT = D / 16;  // 16-dim tiles of the value product
+  constexpr int QD = D / 4;    // dims per lane in the V staging (a quarter of the row)
+  constexpr float LOG2E = 1.4426950408889634f;
+  constexpr float LAZY = 4.0f;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, kq = lane >> 4;
+  const int64_t blk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int G = (int)(a.q_heads / a.kv_heads);
+  const int64_t L1 = a.len1, L = a.len1 + a.len2;
+  const int64_t t0 = blk * sp.eb, t1 = t0 + sp.eb < L ? t0 + sp.eb : L;
+
+  __shared__ u32x4 s_qf[NST][64];
+  __shared__ __attribute__((aligned(16))) uint16_t s_vt[MF_WAVES][D * MF_VT];
+  __shared__ float s_m[MF_WAVES][16], s_l[MF_WAVES][16];
+  static_assert(NDT * 64 * 16 <= (int)sizeof(s_vt), "the cross-wave sums reuse the V tiles' LDS");
+  f32x4(*s_acc)[64] = (f32x4(*)[64])&s_vt[0][0];  // after the tile loop: [NDT][64]
+
+  // query fragments: lane (head r, kq) of step st holds q[head][32 st + 8 kq .. + 7]
+  for (int i = threadIdx.x; i < NST * 64; i += 64 * MF_WAVES) {
+    const int st = i >> 6, l = i & 63, hr = l & 15, hk = l >> 4;
+    u32x4 f = {0u, 0u, 0u, 0u};
+    if (hr < G) {
+      const int64_t qb = b * a.query.s0 + (kvh * G + hr) * a.query.s1;
+      const uint16_t* q = (const uint16_t*)a.query.ptr;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t d = 32 * st + 8 * hk + 2 * e;
+        f[e] = (uint32_t)q[qb + d * a.query.s3] | ((uint32_t)q[qb + (d + 1) * a.query.s3] << 16);
+      }
+    }
+    s_qf[st][l] = f;
+  }
+  __syncthreads();
+
+  const float scale2 = a.scaling * LOG2E;
+  float m_run = -INFINITY, l_run = 0.f;  // of head r (lane column), replicated over kq
+  f32x4 acc[NDT];
+#pragma unroll
+  for (int j = 0; j < NDT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  uint16_t* vt = s_vt[wave];
+
+  for (int64_t tt0 = t0 + MF_TILE * wave; tt0 < t1; tt0 += MF_TILE * MF_WAVES) {
+    // ---- key rows of tokens tt0 + r and tt0 + 16 + r (clamped into the block; masked below)
+    u32x4 ka[NST], kb[NST];
+    {
+      const int64_t ta = tt0 + r < t1 ? tt0 + r : t1 - 1, tb = tt0 + 16 + r < t1 ? tt0 + 16 + r : t1 - 1;
+      const uint16_t* ra = ta < L1 ? (const uint16_t*)a.key.ptr + b * a.key.s0 + kvh * a.key.s1 + ta * a.key.s2
+                                   : (const uint16_t*)a.residual_key.ptr + b * a.residual_key.s0 +
+                                         kvh * a.residual_key.s1 + (ta - L1) * a.residual_key.s2;
+      const uint16_t* rb = tb < L1 ? (const uint16_t*)a.key.ptr + b * a.key.s0 + kvh * a.key.s1 + tb * a.key.s2
+                                   : (const uint16_t*)a.residual_key.ptr + b * a.residual_key.s0 +
+                                         kvh * a.residual_key.s1 + (tb - L1) * a.residual_key.s2;
+#pragma unroll
+      for (int st = 0; st < NST; ++st) {
+        ka[st] = *(const u32x4*)(ra + 32 * st + 8 * kq);
+        kb[st] = *(const u32x4*)(rb + 32 * st + 8 * kq);
+      }
+    }
+    // ---- V of the tile into LDS, transposed: lane (p, quarter) takes tokens 2p, 2p + 1 and
+    // dims [QD quarter, QD quarter + QD); a 32-bit LDS word holds one dim of both tokens
+    {
+      const int p = lane & 15, qr = lane >> 4;
+      int64_t tu[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) tu[u] = tt0 + 2 * p + u < t1 ? tt0 + 2 * p + u : t1 - 1;
+      uint32_t* vw = (uint32_t*)vt;  // word (d, p) at d * MF_VT / 2 + p
+      const bool dense0 = VF == ANNA_MI_VALUES_DENSE || tu[0] >= L1, dense1 = VF == ANNA_MI_VALUES_DENSE || tu[1] >= L1;
+      if (dense0 && dense1) {
+        // 16-bit rows (window tokens, or dense values): interleave the two tokens' halves
+        const uint16_t* row[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+          row[u] = tu[u] >= L1 ? (const uint16_t*)a.residual_value.ptr + b * a.residual_value.s0 +
+                                     kvh * a.residual_value.s1 + (tu[u] - L1) * a.residual_value.s2 + QD * qr
+                               : (const uint16_t*)a.value.ptr + b * a.value.s0 + kvh * a.value.s1 +
+                                     tu[u] * a.value.s2 + QD * qr;
+#pragma unroll
+        for (int c = 0; c < QD / 8; ++c) {
+          const u32x4 w0 = *(const u32x4*)(row[0] + 8 * c), w1 = *(const u32x4*)(row[1] + 8 * c);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int d = QD * qr + 8 * c + 2 * e;
+            vw[d * (MF_VT / 2) + p] = __builtin_amdgcn_perm(w1[e], w0[e], 0x05040100u);
+            vw[(d + 1) * (MF_VT / 2) + p] = __builtin_amdgcn_perm(w1[e], w0[e], 0x07060302u);
+          }
+        }
+      } else {
+        // at least one packed token: dequantize q * scale + zero per 8 dims (one group)
+        const int sb = a.value_bits == 2 ? 2 : 4;
+        const uint32_t mask = (1u << sb) - 1u;
+#pragma unroll 2
+        for (int c = 0; c < QD / 8; ++c) {
+          const int d0 = QD * qr + 8 * c;
+          float v[2][8];
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int64_t t = tu[u];
+            if (t >= L1) {
+              const uint16_t* row = (const uint16_t*)a.residual_value.ptr + b * a.residual_value.s0 +
+                                    kvh * a.residual_value.s1 + (t - L1) * a.residual_value.s2 + d0;
+              const u32x4 w = *(const u32x4*)row;
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                const uint16_t h = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+                v[u][e] = DT == ANNA_MI_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+              }
+            } else {
+              const uint8_t* codes = (const uint8_t*)a.value.ptr + b * a.value.s0 + kvh * a.value.s1 + t * a.value.s2;
+              const int64_t g = d0 / a.value_group_size;
+              const float sc = ldt<DT>(a.value_scales.ptr, b * a.value_scales.s0 + kvh * a.value_scales.s1 +
+                                                                 t * a.value_scales.s2 + g * a.value_scales.s3);
+              const float zc = ldt<DT>(a.value_zeros.ptr, b * a.value_zeros.s0 + kvh * a.value_zeros.s1 +
+                                                                t * a.value_zeros.s2 + g * a.value_zeros.s3);
+              const uint32_t bits = sb == 2 ? (uint32_t)*(const uint16_t*)(codes + d0 / 4) : *(const uint32_t*)(codes + d0 / 2);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) v[u][e] = (float)((bits >> (sb * e)) & mask) * sc + zc;
+            }
+          }
+#pragma unroll
+          for (int e = 0; e < 8; ++e) vw[(d0 + e) * (MF_VT / 2) + p] = pack2_16<DT>(v[0][e], v[1][e]);
+        }
+      }
+    }
+    // ---- scores: st0 rows = tokens tt0 + 0..15, st1 rows = tt0 + 16..31; columns = heads
+    f32x4 st0 = {0.f, 0.f, 0.f, 0.f}, st1 = st0;
+#pragma unroll
+    for (int st = 0; st < NST; ++st) {
+      const u32x4 qf = s_qf[st][lane];
+      st0 = mfma16<DT>(ka[st], qf, st0);
+      st1 = mfma16<DT>(kb[st], qf, st1);
+    }
+    float s[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      s[i] = tt0 + 4 * kq + i < t1 ? st0[i] * scale2 : -INFINITY;
+      s[4 + i] = tt0 + 16 + 4 * kq + i < t1 ? st1[i] * scale2 : -INFINITY;
+    }
+    float mx = s[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) mx = fmaxf(mx, s[i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    if (__any(mx > m_run + LAZY)) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 while m_run is -inf
+      l_run *= alpha;
+      // acc[j][i] belongs to head 4 kq + i: its factor comes from lane column 4 kq + i
+      float al[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, (lane & ~15) | (4 * kq + i), 64);
+#pragma unroll
+      for (int j = 0; j < NDT; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[j][i] *= al[i];
+      m_run = m_new;
+    }
+    u32x4 pf;
+#pragma unroll
+    for (int i = 0; i < 4; i += 2) {
+      const float p0 = __builtin_amdgcn_exp2f(s[i] - m_run), p1 = __builtin_amdgcn_exp2f(s[i + 1] - m_run);
+      const float p2 = __builtin_amdgcn_exp2f(s[4 + i] - m_run), p3 = __builtin_amdgcn_exp2f(s[5 + i] - m_run);
+      l_run += (p0 + p1) + (p2 + p3);
+      pf[i >> 1] = pack2_16<DT>(p0, p1);
+      pf[2 + (i >> 1)] = pack2_16<DT>(p2, p3);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's V tile is in LDS
+    // ---- O[heads x dims] += P[heads x tokens] V[tokens x dims], one MFMA per 16 dims
+#pragma unroll
+    for (int j = 0; j < NDT; ++j) {
+      const uint16_t* col = vt + (16 * j + r) * MF_VT;
+      const uint2 lo = *(const uint2*)(col + 4 * kq), hi = *(const uint2*)(col + 16 + 4 * kq);
+      const u32x4 vf = {lo.x, lo.y, hi.x, hi.y};
+      acc[j] = mfma16<DT>(pf, vf, acc[j]);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the next tile's writes
+  }
+  // ---- denominators over the lanes of a column, then merge the two waves
+  l_run += __shfl_xor(l_run, 16, 64);
+  l_run += __shfl_xor(l_run, 32, 64);
+  if (kq == 0) {
+    s_m[wave][r] = m_run;
+    s_l[wave][r] = l_run;
+  }
+  __syncthreads();
+  float fw[4];  // this wave's factor for head 4 kq + i
+  {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int h = 4 * kq + i;
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < MF_WAVES; ++w) M = fmaxf(M, s_m[w][h]);
+      fw[i] = s_l[wave][h] > 0.f ? __builtin_amdgcn_exp2f(s_m[wave][h] - M) : 0.f;
+    }
+  }
+  for (int w = 0; w < MF_WAVES; ++w) {
+    if (wave == w) {
+#pragma unroll
+      for (int j = 0; j < NDT; ++j) {
+        f32x4 x = acc[j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] *= fw[i];
+        s_acc[j][lane] = w == 0 ? x : s_acc[j][lane] + x;
+      }
+    }
+    __syncthreads();
+  }
+  // ---- partials: values [b, hq, blk, d] (lane (dim 16 j + r, kq) holds heads 4 kq + i), stats
+  const anna_mi_view& pv = a.partial_values;
+  for (int idx = threadIdx.x; idx < NDT * 64; idx += 64 * MF_WAVES) {
+    const int j = idx >> 6, l = idx & 63, dr = l & 15, hk = l >> 4;
+    const f32x4 x = s_acc[j][l];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int h = 4 * hk + i;
+      if (h < G)
+        ((float*)pv.ptr)[b * pv.s0 + (kvh * G + h) * pv.s1 + blk * pv.s2 + (16 * j + dr) * pv.s3] = x[i];
+    }
+  }
+  if (threadIdx.x < (unsigned)G) {
+    const int h = threadIdx.x;
+    float M = -INFINITY, S = 0.f;
+    for (int w = 0; w < MF_WAVES; ++w) M = fmaxf(M, s_m[w][h]);
+    for (int w = 0; w < MF_WAVES; ++w)
+      if (s_l[w][h] > 0.f) S += s_l[w][h] * __builtin_amdgcn_exp2f(s_m[w][h] - M);
+    const anna_mi_view& ps = a.partial_stats;
+    const int64_t base = b * ps.s0 + (kvh * G + h) * ps.s1 + blk * ps.s2;
+    ((float*)ps.ptr)[base] = M * 0.6931471805599453f;  // back to natural-log units
+    ((float*)ps.ptr)[base + ps.s3] = S;
+  }
+}
+
 Split make_split(const anna_mi_decode_args& a) {
   Split sp{};
   const int64_t bs = a.block_size < 16 ? 16 : a.block_size;
@@ -516,6 +778,52 @@ int64_t total_blocks(const anna_mi_decode_args& a, const Split& sp) {
   if (sp.aligned) return sp.nb1 + (a.len2 > 0 ? (a.len2 + sp.eb2 - 1) / sp.eb2 : 0);
   const int64_t L = a.len1 + a.len2;
   return (L + sp.eb - 1) / sp.eb;
+}
+
+
+// The MFMA split kernel takes 16-bit activations, dense keys, dense or min/max values and
+// 16-byte aligned rows (the layouts of the reference's caches); anything else runs on the VALU
+// kernel.
+bool mfma_path_ok(const anna_mi_decode_args& a, const Split& sp) {
+  if (a.dtype == ANNA_MI_F32 || a.key_format != ANNA_MI_KEYS_DENSE || sp.aligned) return false;
+  if (a.value_format != ANNA_MI_VALUES_DENSE && a.value_format != ANNA_MI_VALUES_MINMAX) return false;
+  if (a.head_dim != 64 && a.head_dim != 128 && a.head_dim != 256) return false;
+  if (a.q_heads / a.kv_heads > 16) return false;
+  auto rows16 = [](const anna_mi_view& v) {  // 8 x 16-bit elements per aligned 16-byte load
+    return v.s3 == 1 && (uintptr_t)v.ptr % 16 == 0 && v.s0 % 8 == 0 && v.s1 % 8 == 0 && v.s2 % 8 == 0;
+  };
+  if (a.len1 > 0) {
+    if (!rows16(a.key)) return false;
+    if (a.value_format == ANNA_MI_VALUES_DENSE) {
+      if (!rows16(a.value)) return false;
+    } else {
+      const int64_t al = a.value_bits == 2 ? 2 : 4;  // the 8 codes of a group chunk in one load
+      const anna_mi_view& v = a.value;
+      if (v.s3 != 1 || (uintptr_t)v.ptr % al || v.s0 % al || v.s1 % al || v.s2 % al) return false;
+      if (a.value_group_size % 8 != 0) return false;
+    }
+  }
+  if (a.len2 > 0 && (!rows16(a.residual_key) || !rows16(a.residual_value))) return false;
+  return true;
+}
+
+void launch_split_mfma(const anna_mi_decode_args& a, const Split& sp, int64_t nblk, hipStream_t st) {
+  const dim3 grid((unsigned)nblk, (unsigned)a.kv_heads, (unsigned)a.batch), blk(64 * MF_WAVES);
+  auto go = [&](auto dt_tag, auto vf_tag) {
+    constexpr int DT = decltype(dt_tag)::value, VF = decltype(vf_tag)::value;
+    switch (a.head_dim) {
+      case 64: hipLaunchKernelGGL((decode_split_mfma_kernel<DT, VF, 64>), grid, blk, 0, st, a, sp); break;
+      case 128: hipLaunchKernelGGL((decode_split_mfma_kernel<DT, VF, 128>), grid, blk, 0, st, a, sp); break;
+      default: hipLaunchKernelGGL((decode_split_mfma_kernel<DT, VF, 256>), grid, blk, 0, st, a, sp); break;
+    }
+  };
+  using BF = std::integral_constant<int, ANNA_MI_BF16>;
+  using HF = std::integral_constant<int, ANNA_MI_F16>;
+  using VD = std::integral_constant<int, ANNA_MI_VALUES_DENSE>;
+  using VM = std::integral_constant<int, ANNA_MI_VALUES_MINMAX>;
+  const bool dense = a.value_format == ANNA_MI_VALUES_DENSE;
+  if (a.dtype == ANNA_MI_BF16) dense ? go(BF{}, VD{}) : go(BF{}, VM{});
+  else dense ? go(HF{}, VD{}) : go(HF{}, VM{});
 }
 
 template <int KF, int VF, int DT>
@@ -604,7 +912,9 @@ static int gqa_decode_splitkv_impl(const anna_mi_decode_args& a, void* stream) {
     ANNA_LAUNCH_CHECK("decode_rotate_query_kernel");
   }
   const bool kq = a.key_format == ANNA_MI_KEYS_TQ_MSE;
-  switch (a.value_format) {
+  if (mfma_path_ok(a, sp)) {
+    launch_split_mfma(a, sp, nblk, st);
+  } else switch (a.value_format) {
     case ANNA_MI_VALUES_DENSE:
       kq ? launch_split<1, 0>(a, sp, nblk, st) : launch_split<0, 0>(a, sp, nblk, st);
       break;
