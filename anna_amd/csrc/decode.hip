@@ -9,9 +9,10 @@
 //   h, h + GM, ..., and the waves are merged through LDS.
 //   Output: per (b, q-head, block) the running max, the denominator and the
 //   unnormalized accumulator, in the reference's partial_stats / partial_values layout.
-// Kernel 2 (decode_merge_kernel): log-sum-exp merge of the blocks per (b, q-head) by 1024
-//   threads (dims x block slices), optional un-rotation of TQ-MSE value accumulators,
-//   optional sigmoid gate.
+// Kernel 2: log-sum-exp merge of the blocks per (b, q-head), optional sigmoid gate.
+//   decode_merge_dims_kernel (64 dims per workgroup, the blocks split over 4 waves) when no
+//   block holds rotated values; decode_merge_kernel (1024 threads, dims x block slices, then
+//   the un-rotation of the TQ-MSE value accumulators) otherwise.
 //
 // Reference: launch_gqa_decode_splitkv_fused_xpu (gated_delta_fused_op.sycl:4494-4706)
 // and launch_gqa_decode_splitkv_turboquant_fused_xpu (sycl:4771-5094).
@@ -496,6 +497,81 @@ __global__ __launch_bounds__(MERGE_THREADS) void decode_merge_kernel(const anna_
   }
 }
 
+// grid (D / 64, Hq, B), 256 threads: the merge when no block holds rotated accumulators.  Lane l
+// of each wave owns dim 64 blockIdx.x + l; wave w sums the contiguous blocks [w n4, w n4 + n4) in
+// ascending order and the four sums are added in wave order, so the result does not depend on
+// timing.  Every wave computes the max and the denominator over all blocks itself (lane-strided
+// stats loads and a butterfly), so its first value loads are in flight before any reduction and
+// no barrier precedes them.
+constexpr int MERGE_DIM_WAVES = 4;
+constexpr int MERGE_DIM_PRE = 16;  // partial values per lane loaded before the reductions
+
+__global__ __launch_bounds__(64 * MERGE_DIM_WAVES) void decode_merge_dims_kernel(const anna_mi_decode_args a,
+                                                                                 int64_t nblk) {
+  __shared__ float s_sum[MERGE_DIM_WAVES][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t h = blockIdx.y, b = blockIdx.z, d = (int64_t)blockIdx.x * 64 + lane;
+  const anna_mi_view& ps = a.partial_stats;
+  const anna_mi_view& pv = a.partial_values;
+  const float* st = (const float*)ps.ptr + b * ps.s0 + h * ps.s1;
+  const float* vd = (const float*)pv.ptr + b * pv.s0 + h * pv.s1 + d * pv.s3;
+  const int64_t n4 = (nblk + MERGE_DIM_WAVES - 1) / MERGE_DIM_WAVES;
+  const int64_t k0 = wave * n4, k1 = k0 + n4 < nblk ? k0 + n4 : nblk;
+  float pre[MERGE_DIM_PRE];
+#pragma unroll
+  for (int i = 0; i < MERGE_DIM_PRE; ++i) pre[i] = k0 + i < k1 ? vd[(k0 + i) * pv.s2] : 0.f;
+
+  float mx = -INFINITY;
+  for (int64_t k = lane; k < nblk; k += 64) mx = fmaxf(mx, st[k * ps.s2]);
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
+  const float M = mx;
+  float den = 0.f;
+  for (int64_t k = lane; k < nblk; k += 64) {
+    const float dk = st[k * ps.s2 + ps.s3];
+    if (dk != 0.f) den += dk * expf(st[k * ps.s2] - M);
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) den += __shfl_xor(den, m, 64);
+
+  float acc = 0.f;
+  for (int64_t kc = k0; kc < k1; kc += 64) {
+    float wl = 0.f;  // weight exp(m_k - M) of block kc + lane (0 for empty blocks)
+    if (kc + lane < k1) {
+      const float dk = st[(kc + lane) * ps.s2 + ps.s3];
+      wl = dk == 0.f ? 0.f : expf(st[(kc + lane) * ps.s2] - M);
+    }
+    const int n = k1 - kc < 64 ? (int)(k1 - kc) : 64;
+    int j = 0;
+    if (kc == k0) {
+#pragma unroll
+      for (; j < MERGE_DIM_PRE; ++j) {
+        const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), j));
+        if (j < n && w != 0.f) acc += w * pre[j];
+      }
+    }
+#pragma unroll 8
+    for (; j < n; ++j) {
+      const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), j));
+      const float v = vd[(kc + j) * pv.s2];
+      if (w != 0.f) acc += w * v;
+    }
+  }
+  s_sum[wave][lane] = acc;
+  __syncthreads();
+  if (wave != 0) return;
+  float o = s_sum[0][lane];
+#pragma unroll
+  for (int w = 1; w < MERGE_DIM_WAVES; ++w) o += s_sum[w][lane];
+  o = den > 0.f ? o / den : 0.f;
+  if (a.gate_layout == ANNA_MI_GATE_FLAT) {
+    o *= 1.f / (1.f + expf(-ldv(a.gate.ptr, b * a.gate.s0 + (h * a.head_dim + d) * a.gate.s2, a.dtype)));
+  } else if (a.gate_layout == ANNA_MI_GATE_HEADS) {
+    o *= 1.f / (1.f + expf(-ldv(a.gate.ptr, b * a.gate.s0 + h * a.gate.s1 + d * a.gate.s3, a.dtype)));
+  }
+  stv(a.out.ptr, b * a.out.s0 + h * a.out.s1 + d * a.out.s3, a.dtype, o);
+}
+
 // ------------------------------------------------------------------ MFMA split kernel
 //
 // Fast path of the split kernel for 16-bit activations, dense keys (packed segment and window)
@@ -522,8 +598,9 @@ __device__ __forceinline__ uint32_t pack2_16(float lo, float hi) {
   else return (uint32_t)f32_to_f16_bits(lo) | ((uint32_t)f32_to_f16_bits(hi) << 16);
 }
 
-template <int DT, int VF, int D>
-__global__ __launch_bounds__(64 * MF_WAVES) void decode_split_mfma_kernel(const anna_mi_decode_args a, const Split sp) {
+// SB: storage bits of a min/max code (2, or 4 for 3- and 4-bit values); 0 for dense values.
+template <int DT, int VF, int SB, int D>
+__global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(2))) void decode_split_mfma_kernel(const anna_mi_decode_args a, const Split sp) {
   constexpr int NST = D / 32;  // 32-dim steps of the score product
   constexpr int NDT = D / 16;  // 16-dim tiles of the value product
   constexpr int QD = D / 4;    // dims per lane in the V staging (a quarter of the row)
@@ -542,17 +619,77 @@ __global__ __launch_bounds__(64 * MF_WAVES) void decode_split_mfma_kernel(const 
   static_assert(NDT * 64 * 16 <= (int)sizeof(s_vt), "the cross-wave sums reuse the V tiles' LDS");
   f32x4(*s_acc)[64] = (f32x4(*)[64])&s_vt[0][0];  // after the tile loop: [NDT][64]
 
+  // ---- per-tile loads.  Everything a tile reads from HBM is issued before anything waits on
+  // it: the min/max codes, scales and zeros of the lane's two staging tokens (raw), then the
+  // key rows.  The first tile's loads go out before the query prologue, the next tile's right
+  // after this tile's score MFMAs.
+  constexpr int NCH = QD / 8;                  // 8-dim chunks of the lane's quarter
+  constexpr int NSP = QD >= 32 ? QD / 32 : 1;  // 32-dim spans of the quarter
+  const int p = lane & 15, qr = lane >> 4;     // staging role: tokens 2p, 2p + 1, dims QD qr ..
+  const bool g32 = a.value_group_size % 32 == 0;
+  u32x4 ka[NST], kb[NST];
+  uint32_t vcode[2][NCH], vsc[2][NSP], vzr[2][NSP];
+  // the raw path takes tiles whose tokens are all packed (min/max); others are staged by the
+  // chunked loop below
+  auto raw_tile = [&](int64_t tt0) {
+    return VF == ANNA_MI_VALUES_MINMAX && g32 && (tt0 + MF_TILE <= L1 || t1 <= L1);
+  };
+  auto issue = [&](int64_t tt0) {
+    if (raw_tile(tt0)) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int64_t t = tt0 + 2 * p + u < t1 ? tt0 + 2 * p + u : t1 - 1;
+        const uint8_t* codes = (const uint8_t*)a.value.ptr + b * a.value.s0 + kvh * a.value.s1 + t * a.value.s2;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+          const int d0 = QD * qr + 8 * c;
+          if constexpr (SB == 2) vcode[u][c] = *(const uint16_t*)(codes + d0 / 4);
+          else vcode[u][c] = *(const uint32_t*)(codes + d0 / 2);
+        }
+#pragma unroll
+        for (int i = 0; i < NSP; ++i) {
+          const int64_t g = (QD * qr + 32 * i) / a.value_group_size;
+          vsc[u][i] = ((const uint16_t*)a.value_scales.ptr)[b * a.value_scales.s0 + kvh * a.value_scales.s1 +
+                                                           t * a.value_scales.s2 + g * a.value_scales.s3];
+          vzr[u][i] = ((const uint16_t*)a.value_zeros.ptr)[b * a.value_zeros.s0 + kvh * a.value_zeros.s1 +
+                                                          t * a.value_zeros.s2 + g * a.value_zeros.s3];
+        }
+      }
+    }
+    // key rows of tokens tt0 + r and tt0 + 16 + r (clamped into the block; masked below)
+    const int64_t ta = tt0 + r < t1 ? tt0 + r : t1 - 1, tb = tt0 + 16 + r < t1 ? tt0 + 16 + r : t1 - 1;
+    const uint16_t* ra = ta < L1 ? (const uint16_t*)a.key.ptr + b * a.key.s0 + kvh * a.key.s1 + ta * a.key.s2
+                                 : (const uint16_t*)a.residual_key.ptr + b * a.residual_key.s0 +
+                                       kvh * a.residual_key.s1 + (ta - L1) * a.residual_key.s2;
+    const uint16_t* rb = tb < L1 ? (const uint16_t*)a.key.ptr + b * a.key.s0 + kvh * a.key.s1 + tb * a.key.s2
+                                 : (const uint16_t*)a.residual_key.ptr + b * a.residual_key.s0 +
+                                       kvh * a.residual_key.s1 + (tb - L1) * a.residual_key.s2;
+#pragma unroll
+    for (int st = 0; st < NST; ++st) {
+      ka[st] = *(const u32x4*)(ra + 32 * st + 8 * kq);
+      kb[st] = *(const u32x4*)(rb + 32 * st + 8 * kq);
+    }
+  };
+  const int64_t tfirst = t0 + MF_TILE * wave;
+  if (tfirst < t1) issue(tfirst);
+  __builtin_amdgcn_sched_barrier(0);
+
   // query fragments: lane (head r, kq) of step st holds q[head][32 st + 8 kq .. + 7]
+  const bool qvec = a.query.s3 == 1 && (uintptr_t)a.query.ptr % 16 == 0 && a.query.s0 % 8 == 0 && a.query.s1 % 8 == 0;
   for (int i = threadIdx.x; i < NST * 64; i += 64 * MF_WAVES) {
     const int st = i >> 6, l = i & 63, hr = l & 15, hk = l >> 4;
     u32x4 f = {0u, 0u, 0u, 0u};
     if (hr < G) {
       const int64_t qb = b * a.query.s0 + (kvh * G + hr) * a.query.s1;
       const uint16_t* q = (const uint16_t*)a.query.ptr;
+      if (qvec) {
+        f = *(const u32x4*)(q + qb + 32 * st + 8 * hk);
+      } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t d = 32 * st + 8 * hk + 2 * e;
-        f[e] = (uint32_t)q[qb + d * a.query.s3] | ((uint32_t)q[qb + (d + 1) * a.query.s3] << 16);
+        for (int e = 0; e < 4; ++e) {
+          const int64_t d = 32 * st + 8 * hk + 2 * e;
+          f[e] = (uint32_t)q[qb + d * a.query.s3] | ((uint32_t)q[qb + (d + 1) * a.query.s3] << 16);
+        }
       }
     }
     s_qf[st][l] = f;
@@ -565,32 +702,35 @@ __global__ __launch_bounds__(64 * MF_WAVES) void decode_split_mfma_kernel(const 
 #pragma unroll
   for (int j = 0; j < NDT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   uint16_t* vt = s_vt[wave];
+  uint32_t* vw = (uint32_t*)vt;  // word (d, p) at d * MF_VT / 2 + p: dim d of tokens 2p, 2p + 1
 
-  for (int64_t tt0 = t0 + MF_TILE * wave; tt0 < t1; tt0 += MF_TILE * MF_WAVES) {
-    // ---- key rows of tokens tt0 + r and tt0 + 16 + r (clamped into the block; masked below)
-    u32x4 ka[NST], kb[NST];
-    {
-      const int64_t ta = tt0 + r < t1 ? tt0 + r : t1 - 1, tb = tt0 + 16 + r < t1 ? tt0 + 16 + r : t1 - 1;
-      const uint16_t* ra = ta < L1 ? (const uint16_t*)a.key.ptr + b * a.key.s0 + kvh * a.key.s1 + ta * a.key.s2
-                                   : (const uint16_t*)a.residual_key.ptr + b * a.residual_key.s0 +
-                                         kvh * a.residual_key.s1 + (ta - L1) * a.residual_key.s2;
-      const uint16_t* rb = tb < L1 ? (const uint16_t*)a.key.ptr + b * a.key.s0 + kvh * a.key.s1 + tb * a.key.s2
-                                   : (const uint16_t*)a.residual_key.ptr + b * a.residual_key.s0 +
-                                         kvh * a.residual_key.s1 + (tb - L1) * a.residual_key.s2;
+  for (int64_t tt0 = tfirst; tt0 < t1; tt0 += MF_TILE * MF_WAVES) {
+    // ---- V of the tile into LDS, transposed
+    if (raw_tile(tt0)) {
+      if constexpr (VF == ANNA_MI_VALUES_MINMAX) {
+        constexpr uint32_t mask = (1u << SB) - 1u;
 #pragma unroll
-      for (int st = 0; st < NST; ++st) {
-        ka[st] = *(const u32x4*)(ra + 32 * st + 8 * kq);
-        kb[st] = *(const u32x4*)(rb + 32 * st + 8 * kq);
+        for (int c = 0; c < NCH; ++c) {
+          const int i = QD >= 32 ? c / 4 : 0;
+          float v[2][8];
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const float sc = DT == ANNA_MI_BF16 ? bf16_bits_to_f32((uint16_t)vsc[u][i]) : f16_bits_to_f32((uint16_t)vsc[u][i]);
+            const float zc = DT == ANNA_MI_BF16 ? bf16_bits_to_f32((uint16_t)vzr[u][i]) : f16_bits_to_f32((uint16_t)vzr[u][i]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[u][e] = (float)((vcode[u][c] >> (SB * e)) & mask) * sc + zc;
+          }
+          const int d0 = QD * qr + 8 * c;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) vw[(d0 + e) * (MF_VT / 2) + p] = pack2_16<DT>(v[0][e], v[1][e]);
+        }
       }
-    }
-    // ---- V of the tile into LDS, transposed: lane (p, quarter) takes tokens 2p, 2p + 1 and
-    // dims [QD quarter, QD quarter + QD); a 32-bit LDS word holds one dim of both tokens
-    {
-      const int p = lane & 15, qr = lane >> 4;
+    } else {
+      // lane (p, quarter) takes tokens 2p, 2p + 1 and dims [QD quarter, QD quarter + QD); a
+      // 32-bit LDS word holds one dim of both tokens
       int64_t tu[2];
 #pragma unroll
       for (int u = 0; u < 2; ++u) tu[u] = tt0 + 2 * p + u < t1 ? tt0 + 2 * p + u : t1 - 1;
-      uint32_t* vw = (uint32_t*)vt;  // word (d, p) at d * MF_VT / 2 + p
       const bool dense0 = VF == ANNA_MI_VALUES_DENSE || tu[0] >= L1, dense1 = VF == ANNA_MI_VALUES_DENSE || tu[1] >= L1;
       if (dense0 && dense1) {
         // 16-bit rows (window tokens, or dense values): interleave the two tokens' halves
@@ -601,7 +741,7 @@ __global__ __launch_bounds__(64 * MF_WAVES) void decode_split_mfma_kernel(const 
                                      kvh * a.residual_value.s1 + (tu[u] - L1) * a.residual_value.s2 + QD * qr
                                : (const uint16_t*)a.value.ptr + b * a.value.s0 + kvh * a.value.s1 +
                                      tu[u] * a.value.s2 + QD * qr;
-#pragma unroll
+#pragma unroll 2
         for (int c = 0; c < QD / 8; ++c) {
           const u32x4 w0 = *(const u32x4*)(row[0] + 8 * c), w1 = *(const u32x4*)(row[1] + 8 * c);
 #pragma unroll
@@ -613,8 +753,8 @@ __global__ __launch_bounds__(64 * MF_WAVES) void decode_split_mfma_kernel(const 
         }
       } else {
         // at least one packed token: dequantize q * scale + zero per 8 dims (one group)
-        const int sb = a.value_bits == 2 ? 2 : 4;
-        const uint32_t mask = (1u << sb) - 1u;
+        constexpr int sb = SB == 2 ? 2 : 4;
+        constexpr uint32_t mask = (1u << sb) - 1u;
 #pragma unroll 2
         for (int c = 0; c < QD / 8; ++c) {
           const int d0 = QD * qr + 8 * c;
@@ -656,6 +796,8 @@ __global__ __launch_bounds__(64 * MF_WAVES) void decode_split_mfma_kernel(const 
       st0 = mfma16<DT>(ka[st], qf, st0);
       st1 = mfma16<DT>(kb[st], qf, st1);
     }
+    // the next tile's loads overlap this tile's softmax and value product
+    if (tt0 + MF_TILE * MF_WAVES < t1) issue(tt0 + MF_TILE * MF_WAVES);
     float s[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -809,21 +951,31 @@ bool mfma_path_ok(const anna_mi_decode_args& a, const Split& sp) {
 
 void launch_split_mfma(const anna_mi_decode_args& a, const Split& sp, int64_t nblk, hipStream_t st) {
   const dim3 grid((unsigned)nblk, (unsigned)a.kv_heads, (unsigned)a.batch), blk(64 * MF_WAVES);
-  auto go = [&](auto dt_tag, auto vf_tag) {
-    constexpr int DT = decltype(dt_tag)::value, VF = decltype(vf_tag)::value;
+  auto go = [&](auto dt_tag, auto vf_tag, auto sb_tag) {
+    constexpr int DT = decltype(dt_tag)::value, VF = decltype(vf_tag)::value, SB = decltype(sb_tag)::value;
     switch (a.head_dim) {
-      case 64: hipLaunchKernelGGL((decode_split_mfma_kernel<DT, VF, 64>), grid, blk, 0, st, a, sp); break;
-      case 128: hipLaunchKernelGGL((decode_split_mfma_kernel<DT, VF, 128>), grid, blk, 0, st, a, sp); break;
-      default: hipLaunchKernelGGL((decode_split_mfma_kernel<DT, VF, 256>), grid, blk, 0, st, a, sp); break;
+      case 64: hipLaunchKernelGGL((decode_split_mfma_kernel<DT, VF, SB, 64>), grid, blk, 0, st, a, sp); break;
+      case 128: hipLaunchKernelGGL((decode_split_mfma_kernel<DT, VF, SB, 128>), grid, blk, 0, st, a, sp); break;
+      default: hipLaunchKernelGGL((decode_split_mfma_kernel<DT, VF, SB, 256>), grid, blk, 0, st, a, sp); break;
     }
   };
+  using S0 = std::integral_constant<int, 0>;
+  using S2 = std::integral_constant<int, 2>;
+  using S4 = std::integral_constant<int, 4>;
   using BF = std::integral_constant<int, ANNA_MI_BF16>;
   using HF = std::integral_constant<int, ANNA_MI_F16>;
   using VD = std::integral_constant<int, ANNA_MI_VALUES_DENSE>;
   using VM = std::integral_constant<int, ANNA_MI_VALUES_MINMAX>;
-  const bool dense = a.value_format == ANNA_MI_VALUES_DENSE;
-  if (a.dtype == ANNA_MI_BF16) dense ? go(BF{}, VD{}) : go(BF{}, VM{});
-  else dense ? go(HF{}, VD{}) : go(HF{}, VM{});
+  const bool dense = a.value_format == ANNA_MI_VALUES_DENSE, two = a.value_bits == 2;
+  if (a.dtype == ANNA_MI_BF16) {
+    if (dense) go(BF{}, VD{}, S0{});
+    else if (two) go(BF{}, VM{}, S2{});
+    else go(BF{}, VM{}, S4{});
+  } else {
+    if (dense) go(HF{}, VD{}, S0{});
+    else if (two) go(HF{}, VM{}, S2{});
+    else go(HF{}, VM{}, S4{});
+  }
 }
 
 template <int KF, int VF, int DT>
@@ -927,9 +1079,15 @@ static int gqa_decode_splitkv_impl(const anna_mi_decode_args& a, void* stream) {
   }
   ANNA_LAUNCH_CHECK("decode_split_kernel");
   const int64_t nrot = a.value_format == ANNA_MI_VALUES_TQ_MSE ? sp.nb1 : 0;
-  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)a.q_heads, (unsigned)a.batch), dim3(MERGE_THREADS),
-                     (size_t)a.head_dim * 4, st, a, nblk, nrot);
-  ANNA_LAUNCH_CHECK("decode_merge_kernel");
+  if (nrot == 0) {
+    hipLaunchKernelGGL(decode_merge_dims_kernel, dim3((unsigned)(a.head_dim / 64), (unsigned)a.q_heads, (unsigned)a.batch),
+                       dim3(64 * MERGE_DIM_WAVES), 0, st, a, nblk);
+    ANNA_LAUNCH_CHECK("decode_merge_dims_kernel");
+  } else {
+    hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)a.q_heads, (unsigned)a.batch), dim3(MERGE_THREADS),
+                       (size_t)a.head_dim * 4, st, a, nblk, nrot);
+    ANNA_LAUNCH_CHECK("decode_merge_kernel");
+  }
   return ANNA_MI_OK;
 }
 
