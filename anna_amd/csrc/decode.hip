@@ -592,10 +592,19 @@ constexpr int MF_TILE = 32;              // tokens per wave tile
 constexpr int MF_VT = MF_TILE + 4;       // LDS pitch (elements) of the transposed V tile: 18 words,
                                          // so the 16 dims of a B-operand read hit distinct banks
 
+// Two floats rounded to nearest-even into the activation dtype, lo in bits 0..15 (one
+// v_cvt_pk_bf16_f32 for bf16).
 template <int DT>
 __device__ __forceinline__ uint32_t pack2_16(float lo, float hi) {
-  if constexpr (DT == ANNA_MI_BF16) return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
-  else return (uint32_t)f32_to_f16_bits(lo) | ((uint32_t)f32_to_f16_bits(hi) << 16);
+  if constexpr (DT == ANNA_MI_BF16) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const bf16x2 v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+  } else {
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    const f16x2 v = {(_Float16)lo, (_Float16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+  }
 }
 
 // SB: storage bits of a min/max code (2, or 4 for 3- and 4-bit values); 0 for dense values.
