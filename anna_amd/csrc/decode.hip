@@ -576,7 +576,8 @@ __global__ __launch_bounds__(64 * MERGE_DIM_WAVES) void decode_merge_dims_kernel
 //
 // Fast path of the split kernel for 16-bit activations, dense keys (packed segment and window)
 // and dense or min/max-packed values, head_dim 64/128/256, G <= 16 query heads per KV head.
-// Workgroup: 2 waves per (block, KV head, batch); each wave takes 32-token tiles of the block.
+// Workgroup: 2 waves, each owning one block of one (KV head, batch) and walking it in 32-token
+// tiles; the next tile's loads are issued right after the current tile's score MFMAs.
 //   * S^T = K Q^T by v_mfma_f32_16x16x32 (A = 16 key rows x 32 dims straight from memory, B = the
 //     query heads staged in LDS as fragments; two MFMAs per 32 dims for tokens r and 16 + r).
 //   * Online softmax in base 2; the probabilities' accumulator layout is already the A operand of
@@ -585,8 +586,8 @@ __global__ __launch_bounds__(64 * MERGE_DIM_WAVES) void decode_merge_dims_kernel
 //   * V of the tile is staged in LDS transposed, [dim][token] in the activation dtype (min/max
 //     codes dequantized as q * scale + zero on the way; window tokens copied), so that the B
 //     operand of lane (dim, kq) is two 8-byte reads.
-// The partials have the reference layout (natural-log max, denominator, unnormalized values),
-// so decode_merge_kernel merges them as for the VALU kernel.
+// Each wave writes its block's partial from registers, in the reference layout (natural-log max,
+// denominator, unnormalized values), so the merge kernels take it as they take the VALU kernel's.
 constexpr int MF_WAVES = 2;
 constexpr int MF_TILE = 32;              // tokens per wave tile
 constexpr int MF_VT = MF_TILE + 4;       // LDS pitch (elements) of the transposed V tile: 18 words,
@@ -617,16 +618,14 @@ __global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(2
   constexpr float LAZY = 4.0f;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, kq = lane >> 4;
-  const int64_t blk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int64_t blk = (int64_t)blockIdx.x * MF_WAVES + wave, kvh = blockIdx.y, b = blockIdx.z;
   const int G = (int)(a.q_heads / a.kv_heads);
   const int64_t L1 = a.len1, L = a.len1 + a.len2;
+  // a wave past the last block has no tokens (t0 >= t1): it only helps stage the query
   const int64_t t0 = blk * sp.eb, t1 = t0 + sp.eb < L ? t0 + sp.eb : L;
 
   __shared__ u32x4 s_qf[NST][64];
   __shared__ __attribute__((aligned(16))) uint16_t s_vt[MF_WAVES][D * MF_VT];
-  __shared__ float s_m[MF_WAVES][16], s_l[MF_WAVES][16];
-  static_assert(NDT * 64 * 16 <= (int)sizeof(s_vt), "the cross-wave sums reuse the V tiles' LDS");
-  f32x4(*s_acc)[64] = (f32x4(*)[64])&s_vt[0][0];  // after the tile loop: [NDT][64]
 
   // ---- per-tile loads.  Everything a tile reads from HBM is issued before anything waits on
   // it: the min/max codes, scales and zeros of the lane's two staging tokens (raw), then the
@@ -679,7 +678,7 @@ __global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(2
       kb[st] = *(const u32x4*)(rb + 32 * st + 8 * kq);
     }
   };
-  const int64_t tfirst = t0 + MF_TILE * wave;
+  const int64_t tfirst = t0;
   if (tfirst < t1) issue(tfirst);
   __builtin_amdgcn_sched_barrier(0);
 
@@ -713,7 +712,8 @@ __global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(2
   uint16_t* vt = s_vt[wave];
   uint32_t* vw = (uint32_t*)vt;  // word (d, p) at d * MF_VT / 2 + p: dim d of tokens 2p, 2p + 1
 
-  for (int64_t tt0 = tfirst; tt0 < t1; tt0 += MF_TILE * MF_WAVES) {
+  if (t0 >= t1) return;  // no barrier follows
+  for (int64_t tt0 = tfirst; tt0 < t1; tt0 += MF_TILE) {
     // ---- V of the tile into LDS, transposed
     if (raw_tile(tt0)) {
       if constexpr (VF == ANNA_MI_VALUES_MINMAX) {
@@ -806,7 +806,7 @@ __global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(2
       st1 = mfma16<DT>(kb[st], qf, st1);
     }
     // the next tile's loads overlap this tile's softmax and value product
-    if (tt0 + MF_TILE * MF_WAVES < t1) issue(tt0 + MF_TILE * MF_WAVES);
+    if (tt0 + MF_TILE < t1) issue(tt0 + MF_TILE);
     float s[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -852,59 +852,26 @@ __global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(2
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the next tile's writes
   }
-  // ---- denominators over the lanes of a column, then merge the two waves
+  // ---- the block's partial: stats of head r from lanes (r, kq = 0), values [b, hq, blk, d] from
+  // the accumulators (lane (dim 16 j + r, kq) holds heads 4 kq + i)
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);
-  if (kq == 0) {
-    s_m[wave][r] = m_run;
-    s_l[wave][r] = l_run;
-  }
-  __syncthreads();
-  float fw[4];  // this wave's factor for head 4 kq + i
-  {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int h = 4 * kq + i;
-      float M = -INFINITY;
-#pragma unroll
-      for (int w = 0; w < MF_WAVES; ++w) M = fmaxf(M, s_m[w][h]);
-      fw[i] = s_l[wave][h] > 0.f ? __builtin_amdgcn_exp2f(s_m[wave][h] - M) : 0.f;
-    }
-  }
-  for (int w = 0; w < MF_WAVES; ++w) {
-    if (wave == w) {
-#pragma unroll
-      for (int j = 0; j < NDT; ++j) {
-        f32x4 x = acc[j];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) x[i] *= fw[i];
-        s_acc[j][lane] = w == 0 ? x : s_acc[j][lane] + x;
-      }
-    }
-    __syncthreads();
-  }
-  // ---- partials: values [b, hq, blk, d] (lane (dim 16 j + r, kq) holds heads 4 kq + i), stats
-  const anna_mi_view& pv = a.partial_values;
-  for (int idx = threadIdx.x; idx < NDT * 64; idx += 64 * MF_WAVES) {
-    const int j = idx >> 6, l = idx & 63, dr = l & 15, hk = l >> 4;
-    const f32x4 x = s_acc[j][l];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int h = 4 * hk + i;
-      if (h < G)
-        ((float*)pv.ptr)[b * pv.s0 + (kvh * G + h) * pv.s1 + blk * pv.s2 + (16 * j + dr) * pv.s3] = x[i];
-    }
-  }
-  if (threadIdx.x < (unsigned)G) {
-    const int h = threadIdx.x;
-    float M = -INFINITY, S = 0.f;
-    for (int w = 0; w < MF_WAVES; ++w) M = fmaxf(M, s_m[w][h]);
-    for (int w = 0; w < MF_WAVES; ++w)
-      if (s_l[w][h] > 0.f) S += s_l[w][h] * __builtin_amdgcn_exp2f(s_m[w][h] - M);
+  if (kq == 0 && r < G) {
     const anna_mi_view& ps = a.partial_stats;
-    const int64_t base = b * ps.s0 + (kvh * G + h) * ps.s1 + blk * ps.s2;
-    ((float*)ps.ptr)[base] = M * 0.6931471805599453f;  // back to natural-log units
-    ((float*)ps.ptr)[base + ps.s3] = S;
+    const int64_t base = b * ps.s0 + (kvh * G + r) * ps.s1 + blk * ps.s2;
+    ((float*)ps.ptr)[base] = m_run * 0.6931471805599453f;  // back to natural-log units
+    ((float*)ps.ptr)[base + ps.s3] = l_run;
+  }
+  const anna_mi_view& pv = a.partial_values;
+  float* out = (float*)pv.ptr + b * pv.s0 + blk * pv.s2 + r * pv.s3;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int h = 4 * kq + i;
+    if (h < G) {
+      float* oh = out + (kvh * G + h) * pv.s1;
+#pragma unroll
+      for (int j = 0; j < NDT; ++j) oh[16 * j * pv.s3] = acc[j][i];
+    }
   }
 }
 
@@ -959,7 +926,7 @@ bool mfma_path_ok(const anna_mi_decode_args& a, const Split& sp) {
 }
 
 void launch_split_mfma(const anna_mi_decode_args& a, const Split& sp, int64_t nblk, hipStream_t st) {
-  const dim3 grid((unsigned)nblk, (unsigned)a.kv_heads, (unsigned)a.batch), blk(64 * MF_WAVES);
+  const dim3 grid((unsigned)((nblk + MF_WAVES - 1) / MF_WAVES), (unsigned)a.kv_heads, (unsigned)a.batch), blk(64 * MF_WAVES);
   auto go = [&](auto dt_tag, auto vf_tag, auto sb_tag) {
     constexpr int DT = decltype(dt_tag)::value, VF = decltype(vf_tag)::value, SB = decltype(sb_tag)::value;
     switch (a.head_dim) {
