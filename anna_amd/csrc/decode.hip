@@ -11,8 +11,8 @@
 //   unnormalized accumulator, in the reference's partial_stats / partial_values layout.
 // Kernel 2: log-sum-exp merge of the blocks per (b, q-head), optional sigmoid gate.
 //   decode_merge_dims_kernel (64 dims per workgroup, the blocks split over 4 waves) when no
-//   block holds rotated values; decode_merge_kernel (1024 threads, dims x block slices, then
-//   the un-rotation of the TQ-MSE value accumulators) otherwise.
+//   block holds rotated values and there are at most 256 blocks; decode_merge_kernel (1024
+//   threads, dims x block slices, then the un-rotation of TQ-MSE value accumulators) otherwise.
 //
 // Reference: launch_gqa_decode_splitkv_fused_xpu (gated_delta_fused_op.sycl:4494-4706)
 // and launch_gqa_decode_splitkv_turboquant_fused_xpu (sycl:4771-5094).
@@ -497,65 +497,69 @@ __global__ __launch_bounds__(MERGE_THREADS) void decode_merge_kernel(const anna_
   }
 }
 
-// grid (D / 64, Hq, B), 256 threads: the merge when no block holds rotated accumulators.  Lane l
-// of each wave owns dim 64 blockIdx.x + l; wave w sums the contiguous blocks [w n4, w n4 + n4) in
-// ascending order and the four sums are added in wave order, so the result does not depend on
-// timing.  Every wave computes the max and the denominator over all blocks itself (lane-strided
-// stats loads and a butterfly), so its first value loads are in flight before any reduction and
-// no barrier precedes them.
+// grid (D / 64, Hq, B), 256 threads: the merge when no block holds rotated accumulators and
+// there are at most MERGE_DIM_MAXBLK blocks.  Thread t loads the stats of block t while every
+// lane's first MERGE_DIM_PRE partial values are in flight; the max, the block weights
+// exp(m_k - M) (LDS) and the denominator take two barriers.  Lane l of each wave owns dim
+// 64 blockIdx.x + l; wave w sums the contiguous blocks [w n4, w n4 + n4) in ascending order and
+// the four sums are added in wave order, so the result does not depend on timing.
 constexpr int MERGE_DIM_WAVES = 4;
+constexpr int MERGE_DIM_MAXBLK = 64 * MERGE_DIM_WAVES;
 constexpr int MERGE_DIM_PRE = 16;  // partial values per lane loaded before the reductions
 
 __global__ __launch_bounds__(64 * MERGE_DIM_WAVES) void decode_merge_dims_kernel(const anna_mi_decode_args a,
                                                                                  int64_t nblk) {
+  __shared__ float s_w[MERGE_DIM_MAXBLK];
+  __shared__ float s_red[2][MERGE_DIM_WAVES];
   __shared__ float s_sum[MERGE_DIM_WAVES][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t h = blockIdx.y, b = blockIdx.z, d = (int64_t)blockIdx.x * 64 + lane;
   const anna_mi_view& ps = a.partial_stats;
   const anna_mi_view& pv = a.partial_values;
   const float* st = (const float*)ps.ptr + b * ps.s0 + h * ps.s1;
   const float* vd = (const float*)pv.ptr + b * pv.s0 + h * pv.s1 + d * pv.s3;
-  const int64_t n4 = (nblk + MERGE_DIM_WAVES - 1) / MERGE_DIM_WAVES;
-  const int64_t k0 = wave * n4, k1 = k0 + n4 < nblk ? k0 + n4 : nblk;
+  const int n = (int)nblk, n4 = (n + MERGE_DIM_WAVES - 1) / MERGE_DIM_WAVES;
+  const int k0 = wave * n4, k1 = k0 + n4 < n ? k0 + n4 : n;
   float pre[MERGE_DIM_PRE];
 #pragma unroll
-  for (int i = 0; i < MERGE_DIM_PRE; ++i) pre[i] = k0 + i < k1 ? vd[(k0 + i) * pv.s2] : 0.f;
-
-  float mx = -INFINITY;
-  for (int64_t k = lane; k < nblk; k += 64) mx = fmaxf(mx, st[k * ps.s2]);
+  for (int i = 0; i < MERGE_DIM_PRE; ++i) pre[i] = k0 + i < k1 ? vd[(int64_t)(k0 + i) * pv.s2] : 0.f;
+  float mk = -INFINITY, dk = 0.f;
+  if (tid < n) {
+    mk = st[(int64_t)tid * ps.s2];
+    dk = st[(int64_t)tid * ps.s2 + ps.s3];
+  }
+  float mx = mk;
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
-  const float M = mx;
-  float den = 0.f;
-  for (int64_t k = lane; k < nblk; k += 64) {
-    const float dk = st[k * ps.s2 + ps.s3];
-    if (dk != 0.f) den += dk * expf(st[k * ps.s2] - M);
-  }
+  if (lane == 0) s_red[0][wave] = mx;
+  __syncthreads();
+  float M = s_red[0][0];
+#pragma unroll
+  for (int w = 1; w < MERGE_DIM_WAVES; ++w) M = fmaxf(M, s_red[0][w]);
+  const float wk = dk == 0.f ? 0.f : expf(mk - M);
+  s_w[tid] = wk;
+  float den = dk * wk;
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) den += __shfl_xor(den, m, 64);
+  if (lane == 0) s_red[1][wave] = den;
+  __syncthreads();
+  den = s_red[1][0];
+#pragma unroll
+  for (int w = 1; w < MERGE_DIM_WAVES; ++w) den += s_red[1][w];
 
   float acc = 0.f;
-  for (int64_t kc = k0; kc < k1; kc += 64) {
-    float wl = 0.f;  // weight exp(m_k - M) of block kc + lane (0 for empty blocks)
-    if (kc + lane < k1) {
-      const float dk = st[(kc + lane) * ps.s2 + ps.s3];
-      wl = dk == 0.f ? 0.f : expf(st[(kc + lane) * ps.s2] - M);
-    }
-    const int n = k1 - kc < 64 ? (int)(k1 - kc) : 64;
-    int j = 0;
-    if (kc == k0) {
 #pragma unroll
-      for (; j < MERGE_DIM_PRE; ++j) {
-        const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), j));
-        if (j < n && w != 0.f) acc += w * pre[j];
-      }
+  for (int i = 0; i < MERGE_DIM_PRE; ++i) {
+    if (k0 + i < k1) {
+      const float w = s_w[k0 + i];
+      if (w != 0.f) acc += w * pre[i];
     }
+  }
 #pragma unroll 8
-    for (; j < n; ++j) {
-      const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), j));
-      const float v = vd[(kc + j) * pv.s2];
-      if (w != 0.f) acc += w * v;
-    }
+  for (int k = k0 + MERGE_DIM_PRE; k < k1; ++k) {
+    const float v = vd[(int64_t)k * pv.s2];
+    const float w = s_w[k];
+    if (w != 0.f) acc += w * v;
   }
   s_sum[wave][lane] = acc;
   __syncthreads();
@@ -642,7 +646,7 @@ __global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(2
   auto raw_tile = [&](int64_t tt0) {
     return VF == ANNA_MI_VALUES_MINMAX && g32 && (tt0 + MF_TILE <= L1 || t1 <= L1);
   };
-  auto issue = [&](int64_t tt0) {
+  auto issue_v = [&](int64_t tt0) {
     if (raw_tile(tt0)) {
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
@@ -664,6 +668,8 @@ __global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(2
         }
       }
     }
+  };
+  auto issue_k = [&](int64_t tt0) {
     // key rows of tokens tt0 + r and tt0 + 16 + r (clamped into the block; masked below)
     const int64_t ta = tt0 + r < t1 ? tt0 + r : t1 - 1, tb = tt0 + 16 + r < t1 ? tt0 + 16 + r : t1 - 1;
     const uint16_t* ra = ta < L1 ? (const uint16_t*)a.key.ptr + b * a.key.s0 + kvh * a.key.s1 + ta * a.key.s2
@@ -678,29 +684,39 @@ __global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(2
       kb[st] = *(const u32x4*)(rb + 32 * st + 8 * kq);
     }
   };
+  // Issue order of the first tile: V codes, query, keys.  The query lands first and goes to
+  // LDS, then the V tile is dequantized while the key rows are still in flight.
   const int64_t tfirst = t0;
-  if (tfirst < t1) issue(tfirst);
-  __builtin_amdgcn_sched_barrier(0);
-
+  if (tfirst < t1) issue_v(tfirst);
   // query fragments: lane (head r, kq) of step st holds q[head][32 st + 8 kq .. + 7]
+  constexpr int NQF = (NST * 64 + 64 * MF_WAVES - 1) / (64 * MF_WAVES);  // fragments per thread
   const bool qvec = a.query.s3 == 1 && (uintptr_t)a.query.ptr % 16 == 0 && a.query.s0 % 8 == 0 && a.query.s1 % 8 == 0;
-  for (int i = threadIdx.x; i < NST * 64; i += 64 * MF_WAVES) {
+  u32x4 qfr[NQF];
+#pragma unroll
+  for (int n = 0; n < NQF; ++n) {
+    const int i = threadIdx.x + n * 64 * MF_WAVES;
     const int st = i >> 6, l = i & 63, hr = l & 15, hk = l >> 4;
-    u32x4 f = {0u, 0u, 0u, 0u};
-    if (hr < G) {
+    qfr[n] = u32x4{0u, 0u, 0u, 0u};
+    if (i < NST * 64 && hr < G) {
       const int64_t qb = b * a.query.s0 + (kvh * G + hr) * a.query.s1;
       const uint16_t* q = (const uint16_t*)a.query.ptr;
       if (qvec) {
-        f = *(const u32x4*)(q + qb + 32 * st + 8 * hk);
+        qfr[n] = *(const u32x4*)(q + qb + 32 * st + 8 * hk);
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int64_t d = 32 * st + 8 * hk + 2 * e;
-          f[e] = (uint32_t)q[qb + d * a.query.s3] | ((uint32_t)q[qb + (d + 1) * a.query.s3] << 16);
+          qfr[n][e] = (uint32_t)q[qb + d * a.query.s3] | ((uint32_t)q[qb + (d + 1) * a.query.s3] << 16);
         }
       }
     }
-    s_qf[st][l] = f;
+  }
+  if (tfirst < t1) issue_k(tfirst);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int n = 0; n < NQF; ++n) {
+    const int i = threadIdx.x + n * 64 * MF_WAVES;
+    if (i < NST * 64) s_qf[i >> 6][i & 63] = qfr[n];
   }
   __syncthreads();
 
@@ -797,6 +813,8 @@ __global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(2
         }
       }
     }
+    // the next tile's V codes are in flight from here, its keys from after the scores
+    if (tt0 + MF_TILE < t1) issue_v(tt0 + MF_TILE);
     // ---- scores: st0 rows = tokens tt0 + 0..15, st1 rows = tt0 + 16..31; columns = heads
     f32x4 st0 = {0.f, 0.f, 0.f, 0.f}, st1 = st0;
 #pragma unroll
@@ -806,7 +824,7 @@ __global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(2
       st1 = mfma16<DT>(kb[st], qf, st1);
     }
     // the next tile's loads overlap this tile's softmax and value product
-    if (tt0 + MF_TILE < t1) issue(tt0 + MF_TILE);
+    if (tt0 + MF_TILE < t1) issue_k(tt0 + MF_TILE);
     float s[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -1055,7 +1073,7 @@ static int gqa_decode_splitkv_impl(const anna_mi_decode_args& a, void* stream) {
   }
   ANNA_LAUNCH_CHECK("decode_split_kernel");
   const int64_t nrot = a.value_format == ANNA_MI_VALUES_TQ_MSE ? sp.nb1 : 0;
-  if (nrot == 0) {
+  if (nrot == 0 && nblk <= MERGE_DIM_MAXBLK) {
     hipLaunchKernelGGL(decode_merge_dims_kernel, dim3((unsigned)(a.head_dim / 64), (unsigned)a.q_heads, (unsigned)a.batch),
                        dim3(64 * MERGE_DIM_WAVES), 0, st, a, nblk);
     ANNA_LAUNCH_CHECK("decode_merge_dims_kernel");

@@ -307,3 +307,71 @@ def test_tensor_row_materialize(gpu):
     codes, norms = oracle_tq_quantize(qn, bits_of(x[:, :8].reshape(-1, 64)), orc.BF16)
     ref = orc.tq_mse_dequant(codes, norms, qn.rotation.cpu().numpy(), qn.centroids.cpu().numpy(), 2)
     assert rel_err(f32(mat[:, :8]).reshape(-1, 64), ref) <= BF16_TOL
+
+
+@pytest.mark.parametrize("d,bits,group,dtype,hkv", [
+    (64, 2, 32, torch.bfloat16, 2),
+    (128, 3, 64, torch.float16, 2),
+    (256, 2, 32, torch.bfloat16, 2),
+    (256, 2, 64, torch.bfloat16, 1),
+    (256, 4, 128, torch.float16, 1),
+    (256, 3, 16, torch.bfloat16, 2),
+])
+def test_splitkv_turboquant_mfma_tiles(gpu, d, bits, group, dtype, hkv):
+    """The MFMA split kernel's tile kinds in one call: 32-token tiles wholly in the packed
+    segment (raw-code staging when group % 32 == 0, else the chunked loop), the tile that
+    straddles the packed/window boundary, window-only tiles and a short last tile; 8 or 16 query
+    heads per KV head; both 16-bit activation dtypes."""
+    torch.manual_seed(60 + d + bits + group)
+    b, hq, qlen, rlen, bs = 2, 16, 517, 43, 64
+    q = torch.randn(b, hq, 1, d, device=gpu, dtype=dtype)
+    qk = torch.randn(b, hkv, qlen, d, device=gpu, dtype=dtype)
+    st = quantize_turboquant_values(torch.randn(b * hkv, qlen, d, device=gpu, dtype=dtype), bits=bits,
+                                    group_size=group)
+    rk = torch.randn(b, hkv, rlen, d, device=gpu, dtype=dtype)
+    rv = torch.randn(b, hkv, rlen, d, device=gpu, dtype=dtype)
+    out = torch.empty_like(q)
+    nb = -(-(qlen + rlen) // bs)
+    ps = torch.empty(b, hq, nb, 2, device=gpu)
+    pv = torch.empty(b, hq, nb, d, device=gpu)
+    torch.ops.anna.gqa_decode_splitkv_turboquant_fused_out(
+        q, qk, st.data.view(b, hkv, qlen, -1), st.scales.view(b, hkv, qlen, -1), st.zeros.view(b, hkv, qlen, -1),
+        rk, rv, out, ps, pv, d ** -0.5, bits, group, bs, None)
+    odt = orc.BF16 if dtype == torch.bfloat16 else orc.F16
+    vq = orc.tq_values_dequant(st.data.cpu().numpy(), bits_of(st.scales), bits_of(st.zeros), odt, bits,
+                               group).reshape(b, hkv, qlen, d)
+    kk = np.concatenate([f32(qk), f32(rk)], axis=2)
+    vv = np.concatenate([vq, f32(rv)], axis=2)
+    ref = _oracle_attention(f32(q), kk, vv, d ** -0.5)
+    assert rel_err(f32(out), ref) <= BF16_TOL
+
+
+@pytest.mark.parametrize("value_kind", ["dense", "minmax"])
+def test_splitkv_more_blocks_than_one_merge_workgroup(gpu, value_kind):
+    """Over 256 blocks (block 16): the merge takes its general kernel; just under, the
+    one-pass kernel.  Both against the oracle."""
+    torch.manual_seed(71)
+    hq, hkv, d, bs = 8, 1, 128, 16
+    for qlen in (4101, 4080):
+        q = torch.randn(1, hq, 1, d, device=gpu, dtype=torch.bfloat16)
+        k = torch.randn(1, hkv, qlen, d, device=gpu, dtype=torch.bfloat16)
+        nb = -(-qlen // bs)
+        assert (nb > 256) == (qlen == 4101)
+        if value_kind == "dense":
+            v = torch.randn(1, hkv, qlen, d, device=gpu, dtype=torch.bfloat16)
+            out = torch.ops.anna.gqa_decode_splitkv_fused(q, k, v, d ** -0.5, bs)
+            vv = f32(v)
+        else:
+            st = quantize_turboquant_values(torch.randn(hkv, qlen, d, device=gpu, dtype=torch.bfloat16), bits=2,
+                                            group_size=32)
+            rk = torch.randn(1, hkv, 0, d, device=gpu, dtype=torch.bfloat16)
+            out = torch.empty_like(q)
+            ps = torch.empty(1, hq, nb, 2, device=gpu)
+            pv = torch.empty(1, hq, nb, d, device=gpu)
+            torch.ops.anna.gqa_decode_splitkv_turboquant_fused_out(
+                q, k, st.data.unsqueeze(0), st.scales.unsqueeze(0), st.zeros.unsqueeze(0), rk, rk, out, ps, pv,
+                d ** -0.5, 2, 32, bs, None)
+            vv = orc.tq_values_dequant(st.data.cpu().numpy(), bits_of(st.scales), bits_of(st.zeros), orc.BF16, 2,
+                                       32)[None]
+        ref = _oracle_attention(f32(q), f32(k), vv, d ** -0.5)
+        assert rel_err(f32(out), ref) <= BF16_TOL, qlen
