@@ -505,7 +505,7 @@ __global__ __launch_bounds__(MERGE_THREADS) void decode_merge_kernel(const anna_
 // the four sums are added in wave order, so the result does not depend on timing.
 constexpr int MERGE_DIM_WAVES = 4;
 constexpr int MERGE_DIM_MAXBLK = 64 * MERGE_DIM_WAVES;
-constexpr int MERGE_DIM_PRE = 16;  // partial values per lane loaded before the reductions
+constexpr int MERGE_DIM_PRE = 32;  // partial values per lane loaded before the reductions
 
 __global__ __launch_bounds__(64 * MERGE_DIM_WAVES) void decode_merge_dims_kernel(const anna_mi_decode_args a,
                                                                                  int64_t nblk) {
@@ -580,22 +580,26 @@ __global__ __launch_bounds__(64 * MERGE_DIM_WAVES) void decode_merge_dims_kernel
 //
 // Fast path of the split kernel for 16-bit activations, dense keys (packed segment and window)
 // and dense or min/max-packed values, head_dim 64/128/256, G <= 16 query heads per KV head.
-// Workgroup: 2 waves, each owning one block of one (KV head, batch) and walking it in 32-token
-// tiles; the next tile's loads are issued right after the current tile's score MFMAs.
+// One wave per workgroup owns a range of `range` tokens of one (KV head, batch) and walks it in
+// 32-token tiles.  The range is chosen on the host (a multiple of 32, about 768 waves in all, no
+// more partials than the caller's workspace holds), independently of the caller's block size.
 //   * S^T = K Q^T by v_mfma_f32_16x16x32 (A = 16 key rows x 32 dims straight from memory, B = the
-//     query heads staged in LDS as fragments; two MFMAs per 32 dims for tokens r and 16 + r).
-//   * Online softmax in base 2; the probabilities' accumulator layout is already the A operand of
-//     O = P V (16 heads x 32 tokens, token k of lane (head, kq) = 4 kq + e (e < 4) or
-//     16 + 4 kq + e - 4), so P never leaves registers.
+//     query heads' fragments, kept in registers; two MFMAs per 32 dims for tokens r and 16 + r).
+//   * Online softmax in base 2, rescaled lazily; the probabilities' accumulator layout is already
+//     the A operand of O = P V (16 heads x 32 tokens, token k of lane (head, kq) = 4 kq + e
+//     (e < 4) or 16 + 4 kq + e - 4), so P never leaves registers.
 //   * V of the tile is staged in LDS transposed, [dim][token] in the activation dtype (min/max
 //     codes dequantized as q * scale + zero on the way; window tokens copied), so that the B
 //     operand of lane (dim, kq) is two 8-byte reads.
-// Each wave writes its block's partial from registers, in the reference layout (natural-log max,
-// denominator, unnormalized values), so the merge kernels take it as they take the VALU kernel's.
-constexpr int MF_WAVES = 2;
-constexpr int MF_TILE = 32;              // tokens per wave tile
-constexpr int MF_VT = MF_TILE + 4;       // LDS pitch (elements) of the transposed V tile: 18 words,
-                                         // so the 16 dims of a B-operand read hit distinct banks
+//   * Two tiles are in flight: buffers 0 and 1 hold the key rows and raw V codes of tiles
+//     n and n + 1, and tile n + 2's loads go into buffer n % 2 right after tile n's scores.
+// Each wave writes its range's partial from registers in the reference layout (natural-log max,
+// denominator, unnormalized values), so the merge kernels take it as they take the VALU
+// kernel's blocks.
+constexpr int MF_TILE = 32;         // tokens per tile
+constexpr int MF_VT = MF_TILE + 4;  // LDS pitch (elements) of the transposed V tile: 18 words,
+                                    // so the 16 dims of a B-operand read hit distinct banks
+constexpr int64_t MF_WAVES_TARGET = 768;  // about 3 waves per CU
 
 // Two floats rounded to nearest-even into the activation dtype, lo in bits 0..15 (one
 // v_cvt_pk_bf16_f32 for bf16).
@@ -612,138 +616,183 @@ __device__ __forceinline__ uint32_t pack2_16(float lo, float hi) {
   }
 }
 
+// Loads of one tile: key rows, and the raw min/max codes of the lane's two staging tokens (the
+// lane's QD dims of a token are one CW-word vector load) with their scales and zeros (span i of
+// 32 dims, token u; one zero-extended 16-bit load each, so nothing is combined before use).
+template <int D, int SB>
+struct MfmaTileRegs {
+  static constexpr int NST = D / 32, QD = D / 4, NSP = QD >= 32 ? QD / 32 : 1;
+  static constexpr int CW = SB == 0 ? 1 : (QD * SB / 8 + 3) / 4;  // 32-bit words of codes per token
+  u32x4 ka[NST], kb[NST];
+  uint32_t vc[2][CW], vsc[NSP][2], vzr[NSP][2];
+};
+
+// n 32-bit words from p (aligned to min(4 n, 16) bytes) as whole-vector loads.
+template <int N>
+__device__ __forceinline__ void load_words(uint32_t (&w)[N], const uint8_t* p) {
+  if constexpr (N == 1) {
+    w[0] = *(const uint32_t*)p;
+  } else if constexpr (N == 2) {
+    const uint2 v = *(const uint2*)p;
+    w[0] = v.x;
+    w[1] = v.y;
+  } else {
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+      const u32x4 v = *(const u32x4*)(p + 16 * i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[4 * i + e] = v[e];
+    }
+  }
+}
+
+
 // SB: storage bits of a min/max code (2, or 4 for 3- and 4-bit values); 0 for dense values.
-template <int DT, int VF, int SB, int D>
-__global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(2))) void decode_split_mfma_kernel(const anna_mi_decode_args a, const Split sp) {
-  constexpr int NST = D / 32;  // 32-dim steps of the score product
+// NT: tiles per range, fixed (1..4: every load is issued unconditionally, from clamped rows past
+// the range's end, so the compiler waits for exactly the loads each step uses), or 0 (any count,
+// runtime loop).
+template <int DT, int VF, int SB, int D, int NT>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void decode_split_mfma_kernel(
+    const anna_mi_decode_args a, const int64_t range) {
+  using Regs = MfmaTileRegs<D, SB>;
+  constexpr int NST = Regs::NST, NSP = Regs::NSP, QD = Regs::QD, CW = Regs::CW;
   constexpr int NDT = D / 16;  // 16-dim tiles of the value product
-  constexpr int QD = D / 4;    // dims per lane in the V staging (a quarter of the row)
   constexpr float LOG2E = 1.4426950408889634f;
   constexpr float LAZY = 4.0f;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x;
   const int r = lane & 15, kq = lane >> 4;
-  const int64_t blk = (int64_t)blockIdx.x * MF_WAVES + wave, kvh = blockIdx.y, b = blockIdx.z;
+  const int p = lane & 15, qr = lane >> 4;  // staging role: tokens 2p, 2p + 1, dims QD qr ..
+  const int64_t blk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int G = (int)(a.q_heads / a.kv_heads);
   const int64_t L1 = a.len1, L = a.len1 + a.len2;
-  // a wave past the last block has no tokens (t0 >= t1): it only helps stage the query
-  const int64_t t0 = blk * sp.eb, t1 = t0 + sp.eb < L ? t0 + sp.eb : L;
+  const int64_t t0 = blk * range, t1 = t0 + range < L ? t0 + range : L;
+  const int ntiles = NT > 0 ? NT : (int)((t1 - t0 + MF_TILE - 1) / MF_TILE);
+  // raw-code staging: scale groups of whole 32-dim spans, code vectors aligned for one load
+  constexpr uintptr_t CA = 4 * CW < 16 ? 4 * CW : 16;
+  const bool rawok = VF == ANNA_MI_VALUES_MINMAX && a.value_group_size % 32 == 0 && a.value.s3 == 1 &&
+                     ((uintptr_t)a.value.ptr | (uintptr_t)a.value.s0 | (uintptr_t)a.value.s1 |
+                      (uintptr_t)a.value.s2) % CA == 0;
 
+  // Row bases and strides of this (batch, KV head), uniform: a per-lane choice between the packed
+  // segment and the window then selects between two computed addresses (a select between the
+  // views themselves would load the strides per lane).
+  const uint16_t* const key0 = (const uint16_t*)a.key.ptr + b * a.key.s0 + kvh * a.key.s1;
+  const uint16_t* const rkey0 = (const uint16_t*)a.residual_key.ptr + b * a.residual_key.s0 + kvh * a.residual_key.s1;
+  // values: 16-bit elements (dense) or code bytes (min/max); vb0 and vbs2 in bytes
+  constexpr int VESZ = VF == ANNA_MI_VALUES_DENSE ? 2 : 1;
+  const uint8_t* const vb0 = (const uint8_t*)a.value.ptr + VESZ * (b * a.value.s0 + kvh * a.value.s1);
+  const int64_t vbs2 = VESZ * a.value.s2;
+  const uint16_t* const rval0 = (const uint16_t*)a.residual_value.ptr + b * a.residual_value.s0 + kvh * a.residual_value.s1;
+  const int64_t ks2 = a.key.s2, rks2 = a.residual_key.s2, rvs2 = a.residual_value.s2;
+  auto key_row = [&](int64_t t) { return t < L1 ? key0 + t * ks2 : rkey0 + (t - L1) * rks2; };
+  // a 16-byte aligned row that is always there (the host checks the key rows' alignment when
+  // there is a packed segment, the window's otherwise): the target of loads that feed nothing
+  const uint16_t* const safe16 = L1 > 0 ? key0 : rkey0;
+
+  __shared__ __attribute__((aligned(16))) uint16_t s_vt[D * MF_VT];
   __shared__ u32x4 s_qf[NST][64];
-  __shared__ __attribute__((aligned(16))) uint16_t s_vt[MF_WAVES][D * MF_VT];
+  uint32_t* vw = (uint32_t*)s_vt;  // word (d, p) at d * MF_VT / 2 + p: dim d of tokens 2p, 2p + 1
 
-  // ---- per-tile loads.  Everything a tile reads from HBM is issued before anything waits on
-  // it: the min/max codes, scales and zeros of the lane's two staging tokens (raw), then the
-  // key rows.  The first tile's loads go out before the query prologue, the next tile's right
-  // after this tile's score MFMAs.
-  constexpr int NCH = QD / 8;                  // 8-dim chunks of the lane's quarter
-  constexpr int NSP = QD >= 32 ? QD / 32 : 1;  // 32-dim spans of the quarter
-  const int p = lane & 15, qr = lane >> 4;     // staging role: tokens 2p, 2p + 1, dims QD qr ..
-  const bool g32 = a.value_group_size % 32 == 0;
-  u32x4 ka[NST], kb[NST];
-  uint32_t vcode[2][NCH], vsc[2][NSP], vzr[2][NSP];
   // the raw path takes tiles whose tokens are all packed (min/max); others are staged by the
   // chunked loop below
-  auto raw_tile = [&](int64_t tt0) {
-    return VF == ANNA_MI_VALUES_MINMAX && g32 && (tt0 + MF_TILE <= L1 || t1 <= L1);
-  };
-  auto issue_v = [&](int64_t tt0) {
-    if (raw_tile(tt0)) {
+  auto raw_tile = [&](int64_t tt0) { return rawok && (tt0 + MF_TILE <= L1 || t1 <= L1); };
+  auto issue = [&](Regs& R, int64_t tt0) {
+    if constexpr (VF == ANNA_MI_VALUES_MINMAX) {
+      // tokens clamped into the range and the packed segment; a tile that is not staged from
+      // these registers still loads them (from the first packed token, or from safe16 when
+      // there is none or the codes are not aligned) when NT is fixed, so the load count never
+      // varies
+      if (NT > 0 || raw_tile(tt0)) {
+        const bool real = raw_tile(tt0);
+        int64_t t[2];
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int64_t t = tt0 + 2 * p + u < t1 ? tt0 + 2 * p + u : t1 - 1;
-        const uint8_t* codes = (const uint8_t*)a.value.ptr + b * a.value.s0 + kvh * a.value.s1 + t * a.value.s2;
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-          const int d0 = QD * qr + 8 * c;
-          if constexpr (SB == 2) vcode[u][c] = *(const uint16_t*)(codes + d0 / 4);
-          else vcode[u][c] = *(const uint32_t*)(codes + d0 / 2);
+        for (int u = 0; u < 2; ++u) {
+          t[u] = tt0 + 2 * p + u < t1 ? tt0 + 2 * p + u : t1 - 1;
+          t[u] = real ? t[u] : 0;
+          const uint8_t* cp = vb0 + t[u] * vbs2 + QD * qr * SB / 8;
+          load_words<CW>(R.vc[u], real || (L1 > 0 && rawok) ? cp : (const uint8_t*)safe16);
         }
+        const anna_mi_view &vs = a.value_scales, &vz = a.value_zeros;
+        const uint16_t* sp0 = (const uint16_t*)vs.ptr + b * vs.s0 + kvh * vs.s1;
+        const uint16_t* zp0 = (const uint16_t*)vz.ptr + b * vz.s0 + kvh * vz.s1;
+        const bool any = L1 > 0;
 #pragma unroll
         for (int i = 0; i < NSP; ++i) {
           const int64_t g = (QD * qr + 32 * i) / a.value_group_size;
-          vsc[u][i] = ((const uint16_t*)a.value_scales.ptr)[b * a.value_scales.s0 + kvh * a.value_scales.s1 +
-                                                           t * a.value_scales.s2 + g * a.value_scales.s3];
-          vzr[u][i] = ((const uint16_t*)a.value_zeros.ptr)[b * a.value_zeros.s0 + kvh * a.value_zeros.s1 +
-                                                          t * a.value_zeros.s2 + g * a.value_zeros.s3];
+          const uint16_t* sp = any ? sp0 + g * vs.s3 : safe16;
+          const uint16_t* zp = any ? zp0 + g * vz.s3 : safe16;
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            R.vsc[i][u] = sp[any ? t[u] * vs.s2 : 0];
+            R.vzr[i][u] = zp[any ? t[u] * vz.s2 : 0];
+          }
         }
       }
     }
-  };
-  auto issue_k = [&](int64_t tt0) {
-    // key rows of tokens tt0 + r and tt0 + 16 + r (clamped into the block; masked below)
+    // key rows of tokens tt0 + r and tt0 + 16 + r (clamped into the range; masked below)
     const int64_t ta = tt0 + r < t1 ? tt0 + r : t1 - 1, tb = tt0 + 16 + r < t1 ? tt0 + 16 + r : t1 - 1;
-    const uint16_t* ra = ta < L1 ? (const uint16_t*)a.key.ptr + b * a.key.s0 + kvh * a.key.s1 + ta * a.key.s2
-                                 : (const uint16_t*)a.residual_key.ptr + b * a.residual_key.s0 +
-                                       kvh * a.residual_key.s1 + (ta - L1) * a.residual_key.s2;
-    const uint16_t* rb = tb < L1 ? (const uint16_t*)a.key.ptr + b * a.key.s0 + kvh * a.key.s1 + tb * a.key.s2
-                                 : (const uint16_t*)a.residual_key.ptr + b * a.residual_key.s0 +
-                                       kvh * a.residual_key.s1 + (tb - L1) * a.residual_key.s2;
+    const uint16_t* ra = key_row(ta);
+    const uint16_t* rb = key_row(tb);
 #pragma unroll
     for (int st = 0; st < NST; ++st) {
-      ka[st] = *(const u32x4*)(ra + 32 * st + 8 * kq);
-      kb[st] = *(const u32x4*)(rb + 32 * st + 8 * kq);
+      R.ka[st] = *(const u32x4*)(ra + 32 * st + 8 * kq);
+      R.kb[st] = *(const u32x4*)(rb + 32 * st + 8 * kq);
     }
   };
-  // Issue order of the first tile: V codes, query, keys.  The query lands first and goes to
-  // LDS, then the V tile is dequantized while the key rows are still in flight.
-  const int64_t tfirst = t0;
-  if (tfirst < t1) issue_v(tfirst);
-  // query fragments: lane (head r, kq) of step st holds q[head][32 st + 8 kq .. + 7]
-  constexpr int NQF = (NST * 64 + 64 * MF_WAVES - 1) / (64 * MF_WAVES);  // fragments per thread
-  const bool qvec = a.query.s3 == 1 && (uintptr_t)a.query.ptr % 16 == 0 && a.query.s0 % 8 == 0 && a.query.s1 % 8 == 0;
-  u32x4 qfr[NQF];
+
+  Regs buf0, buf1;
+  issue(buf0, t0);
+  // query fragments: lane (head r, kq) of step st holds q[head][32 st + 8 kq .. + 7] (0 for
+  // r >= G); they go through registers to LDS once and are read back per tile
+  u32x4 qf[NST];
+  {
+    const bool qvec = a.query.s3 == 1 && (uintptr_t)a.query.ptr % 16 == 0 && a.query.s0 % 8 == 0 && a.query.s1 % 8 == 0;
+    const int64_t qb = b * a.query.s0 + (kvh * G + (r < G ? r : 0)) * a.query.s1;
+    const uint16_t* q = (const uint16_t*)a.query.ptr;
 #pragma unroll
-  for (int n = 0; n < NQF; ++n) {
-    const int i = threadIdx.x + n * 64 * MF_WAVES;
-    const int st = i >> 6, l = i & 63, hr = l & 15, hk = l >> 4;
-    qfr[n] = u32x4{0u, 0u, 0u, 0u};
-    if (i < NST * 64 && hr < G) {
-      const int64_t qb = b * a.query.s0 + (kvh * G + hr) * a.query.s1;
-      const uint16_t* q = (const uint16_t*)a.query.ptr;
+    for (int st = 0; st < NST; ++st) {
       if (qvec) {
-        qfr[n] = *(const u32x4*)(q + qb + 32 * st + 8 * hk);
+        qf[st] = *(const u32x4*)(q + qb + 32 * st + 8 * kq);
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int64_t d = 32 * st + 8 * hk + 2 * e;
-          qfr[n][e] = (uint32_t)q[qb + d * a.query.s3] | ((uint32_t)q[qb + (d + 1) * a.query.s3] << 16);
+          const int64_t d = 32 * st + 8 * kq + 2 * e;
+          qf[st][e] = (uint32_t)q[qb + d * a.query.s3] | ((uint32_t)q[qb + (d + 1) * a.query.s3] << 16);
         }
       }
+      if (r >= G) qf[st] = u32x4{0u, 0u, 0u, 0u};
     }
   }
-  if (tfirst < t1) issue_k(tfirst);
+  if (NT > 1 || (NT == 0 && ntiles > 1)) issue(buf1, t0 + MF_TILE);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int n = 0; n < NQF; ++n) {
-    const int i = threadIdx.x + n * 64 * MF_WAVES;
-    if (i < NST * 64) s_qf[i >> 6][i & 63] = qfr[n];
-  }
-  __syncthreads();
+  for (int st = 0; st < NST; ++st) s_qf[st][lane] = qf[st];
 
   const float scale2 = a.scaling * LOG2E;
   float m_run = -INFINITY, l_run = 0.f;  // of head r (lane column), replicated over kq
   f32x4 acc[NDT];
 #pragma unroll
   for (int j = 0; j < NDT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  uint16_t* vt = s_vt[wave];
-  uint32_t* vw = (uint32_t*)vt;  // word (d, p) at d * MF_VT / 2 + p: dim d of tokens 2p, 2p + 1
 
-  if (t0 >= t1) return;  // no barrier follows
-  for (int64_t tt0 = tfirst; tt0 < t1; tt0 += MF_TILE) {
+  auto process = [&](Regs& R, int n) {
+    const int64_t tt0 = t0 + (int64_t)MF_TILE * n;
     // ---- V of the tile into LDS, transposed
     if (raw_tile(tt0)) {
       if constexpr (VF == ANNA_MI_VALUES_MINMAX) {
         constexpr uint32_t mask = (1u << SB) - 1u;
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) {
+        for (int c = 0; c < QD / 8; ++c) {
           const int i = QD >= 32 ? c / 4 : 0;
           float v[2][8];
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
-            const float sc = DT == ANNA_MI_BF16 ? bf16_bits_to_f32((uint16_t)vsc[u][i]) : f16_bits_to_f32((uint16_t)vsc[u][i]);
-            const float zc = DT == ANNA_MI_BF16 ? bf16_bits_to_f32((uint16_t)vzr[u][i]) : f16_bits_to_f32((uint16_t)vzr[u][i]);
+            const uint16_t sh = (uint16_t)R.vsc[i][u], zh = (uint16_t)R.vzr[i][u];
+            const float sc = DT == ANNA_MI_BF16 ? bf16_bits_to_f32(sh) : f16_bits_to_f32(sh);
+            const float zc = DT == ANNA_MI_BF16 ? bf16_bits_to_f32(zh) : f16_bits_to_f32(zh);
+            // codes of dims 8c .. 8c + 7 of the lane's quarter: 8 SB bits from bit 8 SB c
+            const uint32_t w = R.vc[u][(8 * SB * c) / 32] >> ((8 * SB * c) % 32);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) v[u][e] = (float)((vcode[u][c] >> (SB * e)) & mask) * sc + zc;
+            for (int e = 0; e < 8; ++e) v[u][e] = (float)((w >> (SB * e)) & mask) * sc + zc;
           }
           const int d0 = QD * qr + 8 * c;
 #pragma unroll
@@ -762,10 +811,7 @@ __global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(2
         const uint16_t* row[2];
 #pragma unroll
         for (int u = 0; u < 2; ++u)
-          row[u] = tu[u] >= L1 ? (const uint16_t*)a.residual_value.ptr + b * a.residual_value.s0 +
-                                     kvh * a.residual_value.s1 + (tu[u] - L1) * a.residual_value.s2 + QD * qr
-                               : (const uint16_t*)a.value.ptr + b * a.value.s0 + kvh * a.value.s1 +
-                                     tu[u] * a.value.s2 + QD * qr;
+          row[u] = (tu[u] >= L1 ? rval0 + (tu[u] - L1) * rvs2 : (const uint16_t*)(vb0 + tu[u] * vbs2)) + QD * qr;
 #pragma unroll 2
         for (int c = 0; c < QD / 8; ++c) {
           const u32x4 w0 = *(const u32x4*)(row[0] + 8 * c), w1 = *(const u32x4*)(row[1] + 8 * c);
@@ -788,8 +834,7 @@ __global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(2
           for (int u = 0; u < 2; ++u) {
             const int64_t t = tu[u];
             if (t >= L1) {
-              const uint16_t* row = (const uint16_t*)a.residual_value.ptr + b * a.residual_value.s0 +
-                                    kvh * a.residual_value.s1 + (t - L1) * a.residual_value.s2 + d0;
+              const uint16_t* row = rval0 + (t - L1) * rvs2 + d0;
               const u32x4 w = *(const u32x4*)row;
 #pragma unroll
               for (int e = 0; e < 8; ++e) {
@@ -797,7 +842,7 @@ __global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(2
                 v[u][e] = DT == ANNA_MI_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
               }
             } else {
-              const uint8_t* codes = (const uint8_t*)a.value.ptr + b * a.value.s0 + kvh * a.value.s1 + t * a.value.s2;
+              const uint8_t* codes = vb0 + t * vbs2;
               const int64_t g = d0 / a.value_group_size;
               const float sc = ldt<DT>(a.value_scales.ptr, b * a.value_scales.s0 + kvh * a.value_scales.s1 +
                                                                  t * a.value_scales.s2 + g * a.value_scales.s3);
@@ -813,18 +858,16 @@ __global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(2
         }
       }
     }
-    // the next tile's V codes are in flight from here, its keys from after the scores
-    if (tt0 + MF_TILE < t1) issue_v(tt0 + MF_TILE);
     // ---- scores: st0 rows = tokens tt0 + 0..15, st1 rows = tt0 + 16..31; columns = heads
     f32x4 st0 = {0.f, 0.f, 0.f, 0.f}, st1 = st0;
 #pragma unroll
     for (int st = 0; st < NST; ++st) {
-      const u32x4 qf = s_qf[st][lane];
-      st0 = mfma16<DT>(ka[st], qf, st0);
-      st1 = mfma16<DT>(kb[st], qf, st1);
+      const u32x4 qs = s_qf[st][lane];
+      st0 = mfma16<DT>(R.ka[st], qs, st0);
+      st1 = mfma16<DT>(R.kb[st], qs, st1);
     }
-    // the next tile's loads overlap this tile's softmax and value product
-    if (tt0 + MF_TILE < t1) issue_k(tt0 + MF_TILE);
+    // this buffer is free again: tile n + 2 goes in flight
+    if (n + 2 < ntiles) issue(R, tt0 + 2 * MF_TILE);  // compile-time when NT is fixed
     float s[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -859,18 +902,32 @@ __global__ __launch_bounds__(64 * MF_WAVES) __attribute__((amdgpu_waves_per_eu(2
       pf[i >> 1] = pack2_16<DT>(p0, p1);
       pf[2 + (i >> 1)] = pack2_16<DT>(p2, p3);
     }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's V tile is in LDS
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the V tile is in LDS
     // ---- O[heads x dims] += P[heads x tokens] V[tokens x dims], one MFMA per 16 dims
 #pragma unroll
     for (int j = 0; j < NDT; ++j) {
-      const uint16_t* col = vt + (16 * j + r) * MF_VT;
+      const uint16_t* col = s_vt + (16 * j + r) * MF_VT;
       const uint2 lo = *(const uint2*)(col + 4 * kq), hi = *(const uint2*)(col + 16 + 4 * kq);
       const u32x4 vf = {lo.x, lo.y, hi.x, hi.y};
       acc[j] = mfma16<DT>(pf, vf, acc[j]);
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the next tile's writes
+  };
+
+  if constexpr (NT > 0) {
+#pragma unroll
+    for (int n = 0; n < NT; n += 2) {
+      process(buf0, n);
+      if (n + 1 < NT) process(buf1, n + 1);
+    }
+  } else {
+    for (int n = 0; n < ntiles; n += 2) {
+      process(buf0, n);
+      if (n + 1 < ntiles) process(buf1, n + 1);
+    }
   }
-  // ---- the block's partial: stats of head r from lanes (r, kq = 0), values [b, hq, blk, d] from
+
+  // ---- the range's partial: stats of head r from lanes (r, kq = 0), values [b, hq, blk, d] from
   // the accumulators (lane (dim 16 j + r, kq) holds heads 4 kq + i)
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);
@@ -943,14 +1000,36 @@ bool mfma_path_ok(const anna_mi_decode_args& a, const Split& sp) {
   return true;
 }
 
-void launch_split_mfma(const anna_mi_decode_args& a, const Split& sp, int64_t nblk, hipStream_t st) {
-  const dim3 grid((unsigned)((nblk + MF_WAVES - 1) / MF_WAVES), (unsigned)a.kv_heads, (unsigned)a.batch), blk(64 * MF_WAVES);
+// Tokens per wave of the MFMA split kernel: whole tiles, about MF_WAVES_TARGET waves over all
+// (batch, KV head) rows, and no more ranges per row than the caller's workspace holds.
+int64_t mfma_range(const anna_mi_decode_args& a) {
+  const int64_t L = a.len1 + a.len2;
+  const int64_t tiles = a.batch * a.kv_heads * ((L + MF_TILE - 1) / MF_TILE);
+  int64_t range = (tiles + MF_WAVES_TARGET - 1) / MF_WAVES_TARGET * MF_TILE;
+  const int64_t need = (L + a.partial_capacity - 1) / a.partial_capacity;
+  if (range < need) range = (need + MF_TILE - 1) / MF_TILE * MF_TILE;
+  return range;
+}
+
+void launch_split_mfma(const anna_mi_decode_args& a, int64_t range, int64_t nranges, hipStream_t st) {
+  const dim3 grid((unsigned)nranges, (unsigned)a.kv_heads, (unsigned)a.batch), blk(64);
+  const int64_t nt = range / MF_TILE;
   auto go = [&](auto dt_tag, auto vf_tag, auto sb_tag) {
     constexpr int DT = decltype(dt_tag)::value, VF = decltype(vf_tag)::value, SB = decltype(sb_tag)::value;
+    auto by_nt = [&](auto d_tag) {
+      constexpr int D = decltype(d_tag)::value;
+      switch (nt) {
+        case 1: hipLaunchKernelGGL((decode_split_mfma_kernel<DT, VF, SB, D, 1>), grid, blk, 0, st, a, range); break;
+        case 2: hipLaunchKernelGGL((decode_split_mfma_kernel<DT, VF, SB, D, 2>), grid, blk, 0, st, a, range); break;
+        case 3: hipLaunchKernelGGL((decode_split_mfma_kernel<DT, VF, SB, D, 3>), grid, blk, 0, st, a, range); break;
+        case 4: hipLaunchKernelGGL((decode_split_mfma_kernel<DT, VF, SB, D, 4>), grid, blk, 0, st, a, range); break;
+        default: hipLaunchKernelGGL((decode_split_mfma_kernel<DT, VF, SB, D, 0>), grid, blk, 0, st, a, range); break;
+      }
+    };
     switch (a.head_dim) {
-      case 64: hipLaunchKernelGGL((decode_split_mfma_kernel<DT, VF, SB, 64>), grid, blk, 0, st, a, sp); break;
-      case 128: hipLaunchKernelGGL((decode_split_mfma_kernel<DT, VF, SB, 128>), grid, blk, 0, st, a, sp); break;
-      default: hipLaunchKernelGGL((decode_split_mfma_kernel<DT, VF, SB, 256>), grid, blk, 0, st, a, sp); break;
+      case 64: by_nt(std::integral_constant<int, 64>{}); break;
+      case 128: by_nt(std::integral_constant<int, 128>{}); break;
+      default: by_nt(std::integral_constant<int, 256>{}); break;
     }
   };
   using S0 = std::integral_constant<int, 0>;
@@ -1058,8 +1137,11 @@ static int gqa_decode_splitkv_impl(const anna_mi_decode_args& a, void* stream) {
     ANNA_LAUNCH_CHECK("decode_rotate_query_kernel");
   }
   const bool kq = a.key_format == ANNA_MI_KEYS_TQ_MSE;
+  int64_t nmerge = nblk;  // partials written by the split kernel
   if (mfma_path_ok(a, sp)) {
-    launch_split_mfma(a, sp, nblk, st);
+    const int64_t range = mfma_range(a), L = a.len1 + a.len2;
+    nmerge = (L + range - 1) / range;
+    launch_split_mfma(a, range, nmerge, st);
   } else switch (a.value_format) {
     case ANNA_MI_VALUES_DENSE:
       kq ? launch_split<1, 0>(a, sp, nblk, st) : launch_split<0, 0>(a, sp, nblk, st);
@@ -1073,13 +1155,13 @@ static int gqa_decode_splitkv_impl(const anna_mi_decode_args& a, void* stream) {
   }
   ANNA_LAUNCH_CHECK("decode_split_kernel");
   const int64_t nrot = a.value_format == ANNA_MI_VALUES_TQ_MSE ? sp.nb1 : 0;
-  if (nrot == 0 && nblk <= MERGE_DIM_MAXBLK) {
+  if (nrot == 0 && nmerge <= MERGE_DIM_MAXBLK) {
     hipLaunchKernelGGL(decode_merge_dims_kernel, dim3((unsigned)(a.head_dim / 64), (unsigned)a.q_heads, (unsigned)a.batch),
-                       dim3(64 * MERGE_DIM_WAVES), 0, st, a, nblk);
+                       dim3(64 * MERGE_DIM_WAVES), 0, st, a, nmerge);
     ANNA_LAUNCH_CHECK("decode_merge_dims_kernel");
   } else {
     hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)a.q_heads, (unsigned)a.batch), dim3(MERGE_THREADS),
-                       (size_t)a.head_dim * 4, st, a, nblk, nrot);
+                       (size_t)a.head_dim * 4, st, a, nmerge, nrot);
     ANNA_LAUNCH_CHECK("decode_merge_kernel");
   }
   return ANNA_MI_OK;
