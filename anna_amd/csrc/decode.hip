@@ -591,8 +591,9 @@ __global__ __launch_bounds__(64 * MERGE_DIM_WAVES) void decode_merge_dims_kernel
 //   * V of the tile is staged in LDS transposed, [dim][token] in the activation dtype (min/max
 //     codes dequantized as q * scale + zero on the way; window tokens copied), so that the B
 //     operand of lane (dim, kq) is two 8-byte reads.
-//   * Two tiles are in flight: buffers 0 and 1 hold the key rows and raw V codes of tiles
-//     n and n + 1, and tile n + 2's loads go into buffer n % 2 right after tile n's scores.
+//   * With a fixed tile count (1..4) all of the range's loads are issued at the start, one
+//     register set per tile; otherwise two sets hold tiles n and n + 1 and tile n + 2's loads go
+//     into set n % 2 right after tile n's scores.
 // Each wave writes its range's partial from registers in the reference layout (natural-log max,
 // denominator, unnormalized values), so the merge kernels take it as they take the VALU
 // kernel's blocks.
@@ -740,8 +741,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     }
   };
 
-  Regs buf0, buf1;
-  issue(buf0, t0);
+  // fixed NT: every tile's loads are issued here, one register set per tile; otherwise two sets
+  // take turns (tile n + 2's loads go into tile n's set after its scores)
+  constexpr int NB = NT > 0 ? NT : 2;
+  Regs buf[NB];
+  issue(buf[0], t0);
   // query fragments: lane (head r, kq) of step st holds q[head][32 st + 8 kq .. + 7] (0 for
   // r >= G); they go through registers to LDS once and are read back per tile
   u32x4 qf[NST];
@@ -763,7 +767,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
       if (r >= G) qf[st] = u32x4{0u, 0u, 0u, 0u};
     }
   }
-  if (NT > 1 || (NT == 0 && ntiles > 1)) issue(buf1, t0 + MF_TILE);
+  if constexpr (NT > 0) {
+#pragma unroll
+    for (int n = 1; n < NT; ++n) issue(buf[n], t0 + (int64_t)MF_TILE * n);
+  } else {
+    if (ntiles > 1) issue(buf[1], t0 + MF_TILE);
+  }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int st = 0; st < NST; ++st) s_qf[st][lane] = qf[st];
@@ -867,7 +876,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
       st1 = mfma16<DT>(R.kb[st], qs, st1);
     }
     // this buffer is free again: tile n + 2 goes in flight
-    if (n + 2 < ntiles) issue(R, tt0 + 2 * MF_TILE);  // compile-time when NT is fixed
+    if (NT == 0 && n + 2 < ntiles) issue(R, tt0 + 2 * MF_TILE);
     float s[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -916,14 +925,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
 
   if constexpr (NT > 0) {
 #pragma unroll
-    for (int n = 0; n < NT; n += 2) {
-      process(buf0, n);
-      if (n + 1 < NT) process(buf1, n + 1);
-    }
+    for (int n = 0; n < NT; ++n) process(buf[n], n);
   } else {
     for (int n = 0; n < ntiles; n += 2) {
-      process(buf0, n);
-      if (n + 1 < ntiles) process(buf1, n + 1);
+      process(buf[0], n);
+      if (n + 1 < ntiles) process(buf[1], n + 1);
     }
   }
 
