@@ -715,49 +715,61 @@ __global__ __launch_bounds__(256) void tq_append_kernel(const anna_mi_tq_append_
 // the blocked value layout), quantizes them with the Hadamard quantizer (bit-exact with
 // anna_mi_tq_hadamard_quantize) and writes key codes token-major, value codes in the 32-token
 // blocked layout, and the fp16 norms.
+template <int QPW>  // quads of 4 tokens per wave: their vectors go through the transform together
 __global__ __launch_bounds__(256) void tq_pack_kv_kernel(const anna_mi_tq_pack_args a) {
+  constexpr int NV = 4 * QPW;
   const int lane = threadIdx.x & 63;
-  const int64_t quads = (a.tokens + 3) / 4;
+  const int64_t groups = (a.tokens + NV - 1) / NV;
   const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (wid >= 2 * a.kv_heads * quads) return;  // whole wave
-  const int64_t q4 = wid % quads, hv = wid / quads, h = hv >> 1;
+  if (wid >= 2 * a.kv_heads * groups) return;  // whole wave
+  const int64_t g = wid % groups, hv = wid / groups, h = hv >> 1;
   const bool is_v = hv & 1;
-  const int64_t t0 = q4 * 4;
+  const int64_t t0 = g * NV;
   const uint16_t* src = (is_v ? a.values : a.keys) + h * a.stride_head;
-  float xv[4][4];
+  float xv[NV][4];
+  uint2 raw[NV];
 #pragma unroll
-  for (int n = 0; n < 4; ++n) {
+  for (int n = 0; n < NV; ++n) {
     const int64_t t = t0 + n < a.tokens ? t0 + n : a.tokens - 1;  // tail: repeats the last token
-    const uint2 raw = *(const uint2*)(src + t * a.stride_token + 4 * lane);
-    xv[n][0] = bf16_bits_to_f32((uint16_t)(raw.x & 0xFFFFu));
-    xv[n][1] = bf16_bits_to_f32((uint16_t)(raw.x >> 16));
-    xv[n][2] = bf16_bits_to_f32((uint16_t)(raw.y & 0xFFFFu));
-    xv[n][3] = bf16_bits_to_f32((uint16_t)(raw.y >> 16));
+    raw[n] = *(const uint2*)(src + t * a.stride_token + 4 * lane);
   }
-  uint32_t code[4][4];
-  float nrm[4];
-  hadamard_codes_wave_n<4, 4>(xv, a.signs, a.thresholds, 3, 1.0f / 16.0f, code, nrm);
+#pragma unroll
+  for (int n = 0; n < NV; ++n) {
+    xv[n][0] = bf16_bits_to_f32((uint16_t)(raw[n].x & 0xFFFFu));
+    xv[n][1] = bf16_bits_to_f32((uint16_t)(raw[n].x >> 16));
+    xv[n][2] = bf16_bits_to_f32((uint16_t)(raw[n].y & 0xFFFFu));
+    xv[n][3] = bf16_bits_to_f32((uint16_t)(raw[n].y >> 16));
+  }
+  uint32_t code[NV][4];
+  float nrm[NV];
+  hadamard_codes_wave_n<NV, 4>(xv, a.signs, a.thresholds, 3, 1.0f / 16.0f, code, nrm);
   const int64_t T = a.pool_tokens, slot0 = a.slot_offset + t0;
-  const int nvalid = a.tokens - t0 < 4 ? (int)(a.tokens - t0) : 4;
-  const float nrm_lane = lane == 0 ? nrm[0] : lane == 1 ? nrm[1] : lane == 2 ? nrm[2] : nrm[3];  // lanes 0..3 store
+  const int nvalid = a.tokens - t0 < NV ? (int)(a.tokens - t0) : NV;
+  float nrm_lane = 0.f;  // lanes 0 .. NV - 1 store the norms
+#pragma unroll
+  for (int n = 0; n < NV; ++n) nrm_lane = lane == n ? nrm[n] : nrm_lane;
   if (!is_v) {
 #pragma unroll
-    for (int n = 0; n < 4; ++n)
+    for (int n = 0; n < NV; ++n)
       if (n < nvalid)
         a.key_codes[(h * T + slot0 + n) * 64 + lane] =
             (uint8_t)(code[n][0] | (code[n][1] << 2) | (code[n][2] << 4) | (code[n][3] << 6));
     if (lane < nvalid) a.key_norms[h * T + slot0 + lane] = f32_to_f16_bits(nrm_lane);
   } else {
-    // slot0 % 4 == 0: the quad fills bits 0..7 of one byte per dim
-    const int64_t t = slot0 % TBT;
-    uint8_t* blk = a.value_codes + (h * (T / TBT) + slot0 / TBT) * 2048 + ((t % 16) / 4) * 512 + (t / 16);
+    // slot0 % 4 == 0: quad q fills bits 0..7 of one byte per dim
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      uint32_t byte = 0;
+    for (int q = 0; q < QPW; ++q) {
+      if (4 * q >= nvalid) break;
+      const int64_t sq = slot0 + 4 * q, t = sq % TBT;
+      uint8_t* blk = a.value_codes + (h * (T / TBT) + sq / TBT) * 2048 + ((t % 16) / 4) * 512 + (t / 16);
 #pragma unroll
-      for (int n = 0; n < 4; ++n)
-        if (n < nvalid) byte |= code[n][e] << (2 * n);
-      blk[(4 * lane + e) * 2] = (uint8_t)byte;
+      for (int e = 0; e < 4; ++e) {
+        uint32_t byte = 0;
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+          if (4 * q + n < nvalid) byte |= code[4 * q + n][e] << (2 * n);
+        blk[(4 * lane + e) * 2] = (uint8_t)byte;
+      }
     }
     if (lane < nvalid) a.value_norms[h * T + slot0 + lane] = f32_to_f16_bits(nrm_lane);
   }
@@ -863,8 +875,11 @@ extern "C" int anna_mi_tq_pack_kv(const anna_mi_tq_pack_args* ap, void* stream) 
                  (uintptr_t)a.keys % 8 == 0 && (uintptr_t)a.values % 8 == 0,
              "anna_mi_tq_pack_kv: rows must be 8-byte aligned with a stride of at least 256");
   if (a.tokens == 0) return ANNA_MI_OK;
-  const int64_t waves = 2 * a.kv_heads * ((a.tokens + 3) / 4);
-  hipLaunchKernelGGL(tq_pack_kv_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, as_stream(stream), a);
+  // one quad per wave: the kernel is VALU-bound (about 600 VALU instructions per wave at 8
+  // waves per SIMD), and two quads per wave measured slower (fewer waves to hide the exchanges)
+  constexpr int QPW = 1;
+  const int64_t waves = 2 * a.kv_heads * ((a.tokens + 4 * QPW - 1) / (4 * QPW));
+  hipLaunchKernelGGL(tq_pack_kv_kernel<QPW>, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, as_stream(stream), a);
   ANNA_LAUNCH_CHECK("tq_pack_kv_kernel");
   return ANNA_MI_OK;
 }

@@ -44,26 +44,30 @@ __host__ __device__ inline float tq_inv_sqrt(int64_t D) {
   return (float)(1.0 / __builtin_sqrt((double)D));
 }
 
-// Value of lane (lane ^ M) for the wave's 64 lanes: DPP quad permutes for M = 1, 2, LDS swizzles
-// (bit mode, inside 32-lane halves) for 4, 8, 16, a bpermute for 32.  Exact copies, so the
-// arithmetic around them is the same whichever exchange is used.
+// Value of lane (lane ^ M) for the wave's 64 lanes: LDS swizzles (quad-permute mode for M = 1,
+// 2, bit mode inside 32-lane halves for 4, 8, 16) and a bpermute for 32.  They run on the LDS
+// pipe, not the VALU (a DPP move would take a VALU slot per element; the transforms here are
+// VALU-bound).  Exact copies, so the arithmetic around them is the same whichever exchange is
+// used.
 template <int M>
 __device__ __forceinline__ float xor_lane(float v) {
-  if constexpr (M == 1) return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
-  else if constexpr (M == 2) return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
+  if constexpr (M == 1) return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x80B1));
+  else if constexpr (M == 2) return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x804E));
   else if constexpr (M < 32) return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), (M << 10) | 0x1F));
   else return __shfl_xor(v, 32, 64);
 }
 
+// One butterfly stage across lanes: the lower lane of a pair keeps x_i + x_j, the upper one
+// x_i - x_j.  Written as fma(v, +-1, partner): the product is exact and the one rounding is
+// that of the add or subtract (signed zeros included: fma(x, -1, x) = +0 = x - x), so the
+// result is bit-identical to the two-branch form at one instruction per element.
 template <int M, int NV, int E>
 __device__ __forceinline__ void fwht_lane_stage(float (&v)[NV][E], bool upper) {
+  const float sg = upper ? -1.0f : 1.0f;
 #pragma unroll
   for (int n = 0; n < NV; ++n)
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const float p = xor_lane<M>(v[n][e]);
-      v[n][e] = upper ? p - v[n][e] : v[n][e] + p;
-    }
+    for (int e = 0; e < E; ++e) v[n][e] = __builtin_fmaf(v[n][e], sg, xor_lane<M>(v[n][e]));
 }
 
 // In-place FWHT of NV vectors at once (independent chains), E elements of each per lane (stages
