@@ -49,7 +49,7 @@ class DecodeArgs(ctypes.Structure):
         ("value_group_size", _I64), ("rotation", _P), ("rotation_t", _P), ("key_centroids", _P),
         ("value_centroids", _P), ("query_rot", _P), ("len2", _I64), ("residual_key", View), ("residual_value", View),
         ("scaling", _F), ("block_size", _I64), ("gate_layout", _I), ("gate", View), ("out", View),
-        ("partial_stats", View), ("partial_values", View), ("partial_capacity", _I64),
+        ("partial_stats", View), ("partial_values", View), ("partial_capacity", _I64), ("seq_lengths", _P),
     ]
 
 
@@ -87,7 +87,20 @@ class TQPackArgs(ctypes.Structure):
     ]
 
 
+class TQRowsAppendArgs(ctypes.Structure):
+    """anna_mi_tq_rows_append_args."""
+
+    _fields_ = [
+        ("dtype", _I), ("batch", _I64), ("kv_heads", _I64), ("head_dim", _I64), ("capacity", _I64),
+        ("residual_capacity", _I64), ("key_bits", _I), ("value_bits", _I), ("value_group_size", _I64),
+        ("new_key", _P), ("new_value", _P), ("key_codes", _P), ("key_norms", _P), ("value_data", _P),
+        ("value_scales", _P), ("value_zeros", _P), ("residual_key", _P), ("residual_value", _P),
+        ("seq_lengths", _P), ("overflow", _P), ("signs", _P), ("thresholds", _P),
+    ]
+
+
 PROTOTYPES.update({
+    "anna_mi_tq_rows_append": [ctypes.POINTER(TQRowsAppendArgs), _P],
     "anna_mi_tq_pack_kv": [ctypes.POINTER(TQPackArgs), _P],
     "anna_mi_tq_decode": [ctypes.POINTER(TQDecodeArgs), _P],
     "anna_mi_tq_append": [ctypes.POINTER(TQAppendArgs), _P],
@@ -145,6 +158,7 @@ RAW_PROTOTYPES: dict[str, tuple] = {
     "anna_mi_sizeof_tq_decode_args": (_I64, []),
     "anna_mi_sizeof_tq_append_args": (_I64, []),
     "anna_mi_sizeof_tq_pack_args": (_I64, []),
+    "anna_mi_sizeof_tq_rows_append_args": (_I64, []),
     "anna_mi_tq_decode_workgroups": (_I64, [_I64, _I64, _P, _I64]),
 }
 

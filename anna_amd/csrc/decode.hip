@@ -85,6 +85,13 @@ __global__ __launch_bounds__(64 * DEC_WAVES) void decode_split_kernel(const anna
   const int64_t blk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int G = (int)(a.q_heads / a.kv_heads);
   const int64_t D = a.head_dim, L1 = a.len1, L = a.len1 + a.len2;
+  // tokens of this row in the two segments (the segments' capacities without seq_lengths)
+  int64_t n1 = L1, n2 = a.len2;
+  if (a.seq_lengths) {
+    const int64_t n = a.seq_lengths[b];
+    n2 = n < a.len2 ? n : a.len2;
+    n1 = n - n2 < L1 ? n - n2 : L1;
+  }
 
   int64_t t0, t1;
   if (sp.aligned && blk >= sp.nb1) {
@@ -333,12 +340,12 @@ __global__ __launch_bounds__(64 * DEC_WAVES) void decode_split_kernel(const anna
     }
   };
   if (sp.vec)
-    sweep(t0, t1 < L1 ? t1 : L1,
+    sweep(t0, t1 < n1 ? t1 : n1,
           [&](int64_t t, float (&kv)[DPL], float (&vv)[DPL]) { load_packed(t, kv, vv, std::true_type{}); });
   else
-    sweep(t0, t1 < L1 ? t1 : L1,
+    sweep(t0, t1 < n1 ? t1 : n1,
           [&](int64_t t, float (&kv)[DPL], float (&vv)[DPL]) { load_packed(t, kv, vv, std::false_type{}); });
-  sweep(t0 > L1 ? t0 : L1, t1, load_residual);
+  sweep(t0 > L1 ? t0 : L1, t1 < L1 + n2 ? t1 : L1 + n2, load_residual);
   // merge the 4 waves: common max, rescale, ordered sum in LDS
   if (lane < G) {  // lane h < GM holds head h's state
     s_m[wave][lane] = m_run;
@@ -984,6 +991,7 @@ int64_t total_blocks(const anna_mi_decode_args& a, const Split& sp) {
 // 16-byte aligned rows (the layouts of the reference's caches); anything else runs on the VALU
 // kernel.
 bool mfma_path_ok(const anna_mi_decode_args& a, const Split& sp) {
+  if (a.seq_lengths) return false;  // per-row lengths: the VALU kernel
   if (a.dtype == ANNA_MI_F32 || a.key_format != ANNA_MI_KEYS_DENSE || sp.aligned) return false;
   if (a.value_format != ANNA_MI_VALUES_DENSE && a.value_format != ANNA_MI_VALUES_MINMAX) return false;
   if (a.head_dim != 64 && a.head_dim != 128 && a.head_dim != 256) return false;

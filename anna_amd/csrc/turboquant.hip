@@ -168,6 +168,28 @@ __global__ __launch_bounds__(1024) void tq_mse_quantize_kernel(
   }
 }
 
+// The E codes of every lane of a wave (lane l: elements l*E ..), sb bits each, packed in element
+// order into dst (D * sb / 8 bytes).  The whole wave takes part (sub-byte lanes combine by shuffles).
+template <int E>
+__device__ __forceinline__ void store_codes_wave(const uint32_t (&code)[E], int sb, uint8_t* dst, int lane) {
+  const int nbits = E * sb;
+  uint64_t pk = 0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) pk |= (uint64_t)code[e] << (sb * e);
+  if (nbits == 8) {
+    dst[lane] = (uint8_t)pk;
+  } else if (nbits == 16) {
+    ((uint16_t*)dst)[lane] = (uint16_t)pk;
+  } else if (nbits > 8) {
+    for (int k = 0; k < nbits / 8; ++k) dst[lane * (nbits / 8) + k] = (uint8_t)(pk >> (8 * k));
+  } else {
+    const int per = 8 / nbits;  // lanes per byte
+    uint32_t b = (uint32_t)pk << (nbits * (lane % per));
+    for (int m = 1; m < per; m <<= 1) b |= (uint32_t)__shfl_xor((int)b, m, 64);
+    if (lane % per == 0) dst[lane / per] = (uint8_t)b;
+  }
+}
+
 // Hadamard TQ-MSE quantizer: each wave takes HNV vectors at once (their shuffle chains are
 // independent, so their latencies overlap), 4 waves per 256-thread workgroup; lane l holds
 // elements l*E .. l*E + E - 1 of each (E = D / 64).
@@ -193,28 +215,12 @@ __global__ __launch_bounds__(256) void tq_hadamard_quantize_kernel(
   hadamard_codes_wave_n<HNV, E>(xv, signs, thr, (1 << bits) - 1, tq_inv_sqrt(D), code, nrm);
   const int sb = storage_bits(bits);
   const int64_t pb = D * sb / 8;  // packed bytes per vector
-  const int nbits = E * sb;
 #pragma unroll
   for (int n = 0; n < HNV; ++n) {
     const int64_t v = v0 + n;
     if (v >= nvec) break;
     if (lane == 0) norms[v] = f32_to_f16_bits(nrm[n]);
-    uint64_t pk = 0;
-#pragma unroll
-    for (int e = 0; e < E; ++e) pk |= (uint64_t)code[n][e] << (sb * e);
-    uint8_t* dst = codes + v * pb;
-    if (nbits == 8) {
-      dst[lane] = (uint8_t)pk;
-    } else if (nbits == 16) {
-      ((uint16_t*)dst)[lane] = (uint16_t)pk;
-    } else if (nbits > 8) {
-      for (int k = 0; k < nbits / 8; ++k) dst[lane * (nbits / 8) + k] = (uint8_t)(pk >> (8 * k));
-    } else {
-      const int per = 8 / nbits;  // lanes per byte
-      uint32_t b = (uint32_t)pk << (nbits * (lane % per));
-      for (int m = 1; m < per; m <<= 1) b |= (uint32_t)__shfl_xor((int)b, m, 64);
-      if (lane % per == 0) dst[lane / per] = (uint8_t)b;
-    }
+    store_codes_wave<E>(code[n], sb, codes + v * pb, lane);
   }
 }
 
@@ -259,21 +265,15 @@ __global__ __launch_bounds__(1024) void tq_mse_dequant_kernel(
 // One thread per (row, run of `gpt` groups); rows = H*T with row strides (sh, st).  A run
 // always ends on a packed-byte boundary (gpt = 1 when group_size is a multiple of the
 // pack width, else the whole row), so no two threads write the same byte.
+// Groups g0 .. g0 + gpt - 1 of one vector (`src`, D elements): min/max, scale and zero point
+// (rounded to the value dtype), codes packed into `data` (the vector's packed row).  The run
+// ends on a packed-byte boundary, so runs of one vector can be done by different threads.
 template <int DT>
-__global__ __launch_bounds__(256) void tq_values_quantize_kernel(
-    const typename Elem<DT>::T* __restrict__ v, int64_t H, int64_t T, int64_t D, int64_t sh, int64_t st,
-    int bits, int64_t gsz, int64_t gpt, uint8_t* __restrict__ data, typename Elem<DT>::T* __restrict__ scales,
-    typename Elem<DT>::T* __restrict__ zeros) {
-  const int64_t ng = D / gsz;
-  const int64_t runs = ng / gpt;
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= H * T * runs) return;
-  const int64_t row = idx / runs, g0 = (idx % runs) * gpt;
-  const int64_t h = row / T, t = row % T;
-  const typename Elem<DT>::T* src = v + h * sh + t * st;
+__device__ void quantize_value_run(const typename Elem<DT>::T* __restrict__ src, int64_t D, int bits, int64_t gsz,
+                                   int64_t g0, int64_t gpt, uint8_t* __restrict__ data,
+                                   typename Elem<DT>::T* __restrict__ scales, typename Elem<DT>::T* __restrict__ zeros) {
   const float levels = (float)((1 << bits) - 1);
   const int sb = storage_bits(bits), per = 8 / sb;
-  const int64_t pb = D / per;
   uint32_t byte = 0;
   for (int64_t g = g0; g < g0 + gpt; ++g) {
     float vmin = INFINITY, vmax = -INFINITY;
@@ -285,8 +285,8 @@ __global__ __launch_bounds__(256) void tq_values_quantize_kernel(
     float sc = __fdiv_rn(__fsub_rn(vmax, vmin), levels);
     sc = sc < 1e-8f ? 1e-8f : sc;
     const typename Elem<DT>::T sc_s = Elem<DT>::cvt(sc), z_s = Elem<DT>::cvt(vmin);
-    scales[row * ng + g] = sc_s;
-    zeros[row * ng + g] = z_s;
+    scales[g] = sc_s;
+    zeros[g] = z_s;
     const float scf = Elem<DT>::to_f32(sc_s), zf = Elem<DT>::to_f32(z_s);
     for (int64_t j = 0; j < gsz; ++j) {
       const int64_t d = g * gsz + j;
@@ -294,11 +294,31 @@ __global__ __launch_bounds__(256) void tq_values_quantize_kernel(
       q = fminf(fmaxf(q, 0.f), levels);
       byte |= (uint32_t)q << (sb * (d % per));
       if (d % per == per - 1) {
-        data[row * pb + d / per] = (uint8_t)byte;
+        data[d / per] = (uint8_t)byte;
         byte = 0;
       }
     }
   }
+}
+
+// Groups per run: 1 when a group fills whole packed bytes, else the whole vector.
+__host__ __device__ inline int64_t value_groups_per_run(int bits, int64_t D, int64_t gsz) {
+  return gsz % (8 / storage_bits(bits)) == 0 ? 1 : D / gsz;
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void tq_values_quantize_kernel(
+    const typename Elem<DT>::T* __restrict__ v, int64_t H, int64_t T, int64_t D, int64_t sh, int64_t st,
+    int bits, int64_t gsz, int64_t gpt, uint8_t* __restrict__ data, typename Elem<DT>::T* __restrict__ scales,
+    typename Elem<DT>::T* __restrict__ zeros) {
+  const int64_t ng = D / gsz;
+  const int64_t runs = ng / gpt;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= H * T * runs) return;
+  const int64_t row = idx / runs, g0 = (idx % runs) * gpt;
+  const int64_t h = row / T, t = row % T;
+  const int64_t pb = D * storage_bits(bits) / 8;
+  quantize_value_run<DT>(v + h * sh + t * st, D, bits, gsz, g0, gpt, data + row * pb, scales + row * ng, zeros + row * ng);
 }
 
 template <int DT, int ODT>
@@ -313,6 +333,56 @@ __global__ __launch_bounds__(256) void tq_values_dequant_kernel(
   const uint32_t q = (data[row * (D / per) + d / per] >> (sb * (d % per))) & ((1u << sb) - 1u);
   const int64_t gi = row * (D / gsz) + d / gsz;
   out[idx] = Elem<ODT>::cvt((float)q * Elem<DT>::to_f32(scales[gi]) + Elem<DT>::to_f32(zeros[gi]));
+}
+
+// One token per sequence into a cache with one region per (sequence, KV head) -- the general
+// form of the batched cache (any head_dim the Hadamard rotation takes, key bits 1..4, value bits
+// 2..4): one workgroup per sequence, waves 2h and 2h + 1 take KV head h's key and value.  When
+// the window is full the token leaving it (ring slot n % R) is quantized into packed slot n - R
+// -- keys as Hadamard TQ-MSE codes + norm (bit-exact with anna_mi_tq_hadamard_quantize), values
+// as min/max groups (bit-exact with anna_mi_tq_values_quantize) -- then, after a barrier, the
+// new token takes the slot and the length grows by one.  A sequence whose packed region is full
+// is left as it is and raises the overflow flag.
+template <int XDT, int E>
+__global__ __launch_bounds__(1024) void tq_rows_append_kernel(const anna_mi_tq_rows_append_args a) {
+  using T = typename Elem<XDT>::T;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t b = blockIdx.x, h = wave >> 1;
+  const bool is_v = wave & 1;
+  const int64_t H = a.kv_heads, D = a.head_dim, R = a.residual_capacity, C = a.capacity;
+  const int n = a.seq_lengths[b];
+  const bool evict = n >= R;
+  if (evict && (int64_t)n - R >= C) {  // uniform over the workgroup
+    if (threadIdx.x == 0) *a.overflow = 1;
+    return;
+  }
+  const int64_t row = b * H + h, slot = n % R;
+  T* ring = (T*)(is_v ? a.residual_value : a.residual_key) + (row * R + slot) * D;
+  if (evict) {
+    const int64_t q = n - R;
+    if (!is_v) {
+      float x[E];
+#pragma unroll
+      for (int e = 0; e < E; ++e) x[e] = Elem<XDT>::to_f32(ring[lane * E + e]);
+      uint32_t code[E];
+      const float nrm = hadamard_codes_wave<E>(x, a.signs, a.thresholds, (1 << a.key_bits) - 1, tq_inv_sqrt(D), code);
+      const int sb = storage_bits(a.key_bits);
+      store_codes_wave<E>(code, sb, a.key_codes + (row * C + q) * (D * sb / 8), lane);
+      if (lane == 0) a.key_norms[row * C + q] = f32_to_f16_bits(nrm);
+    } else {
+      const int64_t gs = a.value_group_size, ng = D / gs;
+      const int64_t gpt = value_groups_per_run(a.value_bits, D, gs);
+      const int64_t pb = D * storage_bits(a.value_bits) / 8;
+      for (int64_t r = lane; r < ng / gpt; r += 64)
+        quantize_value_run<XDT>(ring, D, a.value_bits, gs, r * gpt, gpt, a.value_data + (row * C + q) * pb,
+                                (T*)a.value_scales + (row * C + q) * ng, (T*)a.value_zeros + (row * C + q) * ng);
+    }
+  }
+  __syncthreads();  // every read of the leaving token is done before its slot is overwritten
+  const T* src = (const T*)(is_v ? a.new_value : a.new_key) + row * D;
+  for (int64_t i = lane; i < D; i += 64) ring[i] = src[i];
+  __syncthreads();
+  if (threadIdx.x == 0) a.seq_lengths[b] = n + 1;
 }
 
 }  // namespace
@@ -424,8 +494,7 @@ extern "C" int anna_mi_tq_values_quantize(const void* values, int dtype, int64_t
   ANNA_CHECK(group_size > 0 && D % group_size == 0,
              "TurboQuant value group_size=%lld must evenly divide head_dim=%lld.", (long long)group_size, (long long)D);
   ANNA_CHECK(D % (8 / storage_bits(bits)) == 0, "packed TurboQuant values need head_dim divisible by the pack width");
-  const int per = 8 / storage_bits(bits);
-  const int64_t gpt = group_size % per == 0 ? 1 : D / group_size;
+  const int64_t gpt = value_groups_per_run(bits, D, group_size);
   const int64_t n = H * T * (D / group_size / gpt);
   if (n <= 0) return ANNA_MI_OK;
   ANNA_DISPATCH_DTYPE(dtype, DT, {
@@ -455,5 +524,41 @@ extern "C" int anna_mi_tq_values_dequant(const uint8_t* data, const void* scales
     });
   });
   ANNA_LAUNCH_CHECK("tq_values_dequant_kernel");
+  return ANNA_MI_OK;
+}
+
+extern "C" int64_t anna_mi_sizeof_tq_rows_append_args(void) { return (int64_t)sizeof(anna_mi_tq_rows_append_args); }
+
+extern "C" int anna_mi_tq_rows_append(const anna_mi_tq_rows_append_args* ap, void* stream) {
+  ANNA_CHECK(ap != nullptr, "anna_mi_tq_rows_append: null args");
+  const anna_mi_tq_rows_append_args& a = *ap;
+  ANNA_CHECK(valid_dtype(a.dtype), "anna_mi_tq_rows_append: bad dtype code");
+  ANNA_CHECK(a.head_dim == 64 || a.head_dim == 128 || a.head_dim == 256 || a.head_dim == 512 || a.head_dim == 1024,
+             "anna_mi_tq_rows_append: head_dim must be a power of two in [64, 1024]");
+  ANNA_CHECK(a.key_bits >= 1 && a.key_bits <= 4, "anna_mi_tq_rows_append: key bits must be 1..4");
+  ANNA_CHECK(a.value_bits >= 2 && a.value_bits <= 4, "anna_mi_tq_rows_append: value bits must be 2..4");
+  ANNA_CHECK(a.value_group_size > 0 && a.head_dim % a.value_group_size == 0,
+             "anna_mi_tq_rows_append: value_group_size must divide head_dim");
+  ANNA_CHECK(a.batch > 0 && a.kv_heads > 0 && a.kv_heads <= 8, "anna_mi_tq_rows_append: 1..8 KV heads");
+  ANNA_CHECK(a.capacity >= 0 && a.residual_capacity > 0, "anna_mi_tq_rows_append: bad capacities");
+  ANNA_CHECK(a.new_key && a.new_value && a.residual_key && a.residual_value && a.seq_lengths && a.overflow && a.signs &&
+                 a.thresholds && (a.capacity == 0 || (a.key_codes && a.key_norms && a.value_data && a.value_scales &&
+                                                      a.value_zeros)),
+             "anna_mi_tq_rows_append: null pointer");
+  const dim3 grid((unsigned)a.batch), blk((unsigned)(128 * a.kv_heads));
+  ANNA_DISPATCH_DTYPE(a.dtype, XDT, {
+    auto go = [&](auto e_tag) {
+      constexpr int E = decltype(e_tag)::value;
+      hipLaunchKernelGGL((tq_rows_append_kernel<XDT, E>), grid, blk, 0, as_stream(stream), a);
+    };
+    switch (a.head_dim) {
+      case 64: go(std::integral_constant<int, 1>{}); break;
+      case 128: go(std::integral_constant<int, 2>{}); break;
+      case 256: go(std::integral_constant<int, 4>{}); break;
+      case 512: go(std::integral_constant<int, 8>{}); break;
+      default: go(std::integral_constant<int, 16>{}); break;
+    }
+  });
+  ANNA_LAUNCH_CHECK("tq_rows_append_kernel");
   return ANNA_MI_OK;
 }

@@ -234,8 +234,10 @@ def decode_args(*, query, len1, key=None, key_format=KEYS_DENSE, key_norms=None,
                 value=None, value_format=VALUES_DENSE, value_scales=None, value_zeros=None, value_bits=0,
                 value_group_size=1, rotation=None, rotation_t=None, key_centroids=None, value_centroids=None,
                 query_rot=None, residual_key=None, residual_value=None, scaling, block_size, gate=None, output,
-                partial_stats, partial_values):
-    """Fills anna_mi_decode_args from tensors (query/out [B, Hq, 1, D], K/V [B, Hkv, L, ...])."""
+                partial_stats, partial_values, seq_lengths=None):
+    """Fills anna_mi_decode_args from tensors (query/out [B, Hq, 1, D], K/V [B, Hkv, L, ...]).
+    seq_lengths (optional, device int32 [B]): per-row token counts; len1 and the residual's
+    length are then capacities (see include/anna_mi.h)."""
     b, hq, _, d = query.shape
     hkv = (key if key is not None else residual_key).size(1)
     len2 = 0 if residual_key is None else residual_key.size(2)
@@ -274,6 +276,11 @@ def decode_args(*, query, len1, key=None, key_format=KEYS_DENSE, key_norms=None,
     a.partial_stats = _lib.view(partial_stats)
     a.partial_values = _lib.view(partial_values)
     a.partial_capacity = min(partial_stats.size(2), partial_values.size(2))
+    if seq_lengths is not None:
+        if seq_lengths.dtype != torch.int32 or seq_lengths.numel() != b or not seq_lengths.is_contiguous():
+            raise RuntimeError("seq_lengths must be a contiguous int32 tensor with one entry per batch row")
+        _lib.require_device(seq_lengths)
+    a.seq_lengths = _lib.ptr(seq_lengths)
     return a
 
 

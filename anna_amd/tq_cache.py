@@ -1,4 +1,4 @@
-"""Batched, variable-length TurboQuant KV cache for decode (2-bit TQ-MSE keys and values).
+"""Batched, variable-length TurboQuant KV cache for decode.
 
 One launch appends a token to every sequence and one launch decodes every sequence: this
 replaces the per-row loops of the reference, the append of
@@ -7,7 +7,13 @@ TurboQuantKVRow.append, turboquant.py:1027-1140) and the decode of
 turboquant_single_token_decode_attention (ops.py:1024-1072, calling
 TurboQuantKVRow.decode_attention per row, turboquant.py:1181-1346).
 
-Layout (see anna_amd/csrc/tq_decode.hip): per KV head a pool of token slots, sequence b owning
+Two forms behind one class.  head_dim 256 with 2-bit codes (the BASELINE shape) takes the
+single-launch MFMA decode of anna_amd/csrc/tq_decode.hip over TQ-MSE keys and values.  Every
+other shape (power-of-two head_dim 64..1024, key/value bits 2..4) takes TurboQuantRowsCache:
+TQ-MSE keys and min/max values (the reference row's value format, turboquant.py:199-230) in one
+region per sequence, one append launch, and the split-KV decode with per-row lengths.
+
+Layout of the 2-bit / 256 form (see anna_amd/csrc/tq_decode.hip): per KV head a pool of token slots, sequence b owning
 the slots [offsets[b], offsets[b] + capacity[b]) (capacities rounded up to 32 tokens); keys as
 token-major codes, values as 32-token blocked codes; the newest `residual_capacity` tokens of
 each sequence stay bf16 in a ring (token j at ring slot j % R), so a sequence of length L has
@@ -23,7 +29,8 @@ import ctypes
 import torch
 
 from . import _lib
-from .turboquant import get_turboquant_quantizer
+from . import fused_ops
+from .turboquant import _resolve_value_group_size, get_turboquant_quantizer
 
 _A16 = 1.123046875  # fp16 LUT magnitude that maps to the centroid a of the 2-bit codebook
 
@@ -34,7 +41,13 @@ def _round32(n: int) -> int:
 
 class TurboQuantBatchCache:
     """capacities[b]: pool slots (quantized tokens) of sequence b; a sequence holds at most
-    capacities[b] + residual_capacity tokens."""
+    capacities[b] + residual_capacity tokens.  Shapes other than head_dim 256 with 2-bit codes
+    construct a TurboQuantRowsCache (same methods)."""
+
+    def __new__(cls, *args, head_dim: int = 256, bits: int = 2, **kwargs):
+        if cls is TurboQuantBatchCache and (head_dim != 256 or bits != 2):
+            cls = TurboQuantRowsCache
+        return super().__new__(cls)
 
     def __init__(self, *, batch: int, kv_heads: int, q_heads: int, capacities, residual_capacity: int = 128,
                  head_dim: int = 256, bits: int = 2, device="cuda", tokens_per_item: int = 0):
@@ -197,5 +210,145 @@ class TurboQuantBatchCache:
         (K and V), the dense window, the query and the output."""
         h, d = self.kv_heads, self.head_dim
         packed = sum(self.quantized_lens) * h * 2 * (d // 4 + 2)
+        resid = sum(self.residual_lens) * h * 2 * d * 2
+        return packed + resid + 2 * self.batch * self.q_heads * d * 2
+
+
+class TurboQuantRowsCache(TurboQuantBatchCache):
+    """The batched cache for any power-of-two head_dim in [64, 1024] and bits 2..4 (keys and
+    values).  Per (sequence, KV head) a region of `capacity` packed slots -- keys as Hadamard
+    TQ-MSE codes + fp16 norm, values as min/max groups of `value_group_size` -- and a bf16 ring of
+    the newest `residual_capacity` tokens (token j at slot j % R).  Lengths live on the device.
+    append: one launch (anna_mi_tq_rows_append); decode: the split-KV decode with per-row lengths
+    (query rotation, split, merge)."""
+
+    def __init__(self, *, batch: int, kv_heads: int, q_heads: int, capacities, residual_capacity: int = 128,
+                 head_dim: int = 256, bits: int = 2, device="cuda", tokens_per_item: int = 0,
+                 value_group_size: int | None = None, block_size: int = 64):
+        if head_dim not in (64, 128, 256, 512, 1024):
+            raise ValueError("TurboQuantBatchCache needs a power-of-two head_dim in [64, 1024]")
+        if bits not in (2, 3, 4):
+            raise ValueError(f"Unsupported TurboQuant KV bit-width: {bits}. Expected 2, 3, or 4.")
+        if q_heads % kv_heads != 0 or q_heads // kv_heads > (8 if head_dim >= 512 else 16) or kv_heads > 8:
+            raise ValueError("q_heads must be G * kv_heads with G <= 16 (8 at head_dim 512+), kv_heads <= 8")
+        self.batch, self.kv_heads, self.q_heads, self.head_dim, self.bits = batch, kv_heads, q_heads, head_dim, bits
+        self.device = torch.device(device)
+        self.capacities = [int(c) for c in capacities]
+        self.capacity = max([1] + self.capacities)
+        self.residual_capacity = max(1, int(residual_capacity))
+        self.value_group_size = int(value_group_size or _resolve_value_group_size(head_dim))
+        if head_dim % self.value_group_size != 0:
+            raise ValueError("value_group_size must divide head_dim")
+        self.block_size = int(block_size)
+        dev, B, H, C, R, D = self.device, batch, kv_heads, self.capacity, self.residual_capacity, head_dim
+        pb = D * (2 if bits == 2 else 4) // 8
+        self.key_codes = torch.zeros((B, H, C, pb), dtype=torch.uint8, device=dev)
+        self.key_norms = torch.zeros((B, H, C), dtype=torch.float16, device=dev)
+        self.value_data = torch.zeros((B, H, C, pb), dtype=torch.uint8, device=dev)
+        self.value_scales = torch.zeros((B, H, C, D // self.value_group_size), dtype=torch.bfloat16, device=dev)
+        self.value_zeros = torch.zeros_like(self.value_scales)
+        self.residual_key = torch.zeros((B, H, R, D), dtype=torch.bfloat16, device=dev)
+        self.residual_value = torch.zeros_like(self.residual_key)
+        self.seq_lengths = torch.zeros((B,), dtype=torch.int32, device=dev)
+        self.overflow = torch.zeros((1,), dtype=torch.int32, device=dev)
+        self.lengths = [0] * B
+        self.qn = get_turboquant_quantizer(head_dim=D, bits=bits, device=dev)
+        self.query_rot = torch.empty((B, q_heads, D), dtype=torch.float32, device=dev)
+        self._partials(1)
+
+    def _partials(self, n: int) -> None:
+        self.partial_stats = torch.empty((self.batch, self.q_heads, n, 2), dtype=torch.float32, device=self.device)
+        self.partial_values = torch.empty((self.batch, self.q_heads, n, self.head_dim), dtype=torch.float32,
+                                          device=self.device)
+
+    def load_sequence(self, b: int, keys: torch.Tensor, values: torch.Tensor) -> None:
+        """keys/values bf16 [Hkv, L, D]: the first max(0, L - R) tokens are quantized into the
+        sequence's region, the newest min(L, R) go to the ring."""
+        h, L, D = keys.shape
+        R = self.residual_capacity
+        q = max(0, L - R)
+        if q > self.capacities[b]:
+            raise ValueError(f"sequence {b}: {q} quantized tokens exceed its capacity {self.capacities[b]}")
+        if keys.dtype != torch.bfloat16 or values.dtype != torch.bfloat16:
+            raise ValueError("keys/values must be bf16")
+        if q > 0:
+            codes, norms = self.qn.quantize(keys[:, :q].reshape(-1, D))
+            self.key_codes[b, :, :q] = codes.view(h, q, -1)
+            self.key_norms[b, :, :q] = norms.view(h, q)
+            data, sc, zr = fused_ops.tq_values_quantize(values[:, :q], self.bits, self.value_group_size)
+            self.value_data[b, :, :q] = data
+            self.value_scales[b, :, :q] = sc
+            self.value_zeros[b, :, :q] = zr
+        if L > q:
+            slots = torch.arange(q, L, device=self.device) % R
+            self.residual_key[b][:, slots] = keys[:, q:]
+            self.residual_value[b][:, slots] = values[:, q:]
+        self.seq_lengths[b] = L
+        self.lengths[b] = L
+
+    def append(self, keys: torch.Tensor, values: torch.Tensor) -> None:
+        """One token per sequence: keys/values bf16 [B, Hkv, D]."""
+        B, H, D, R = self.batch, self.kv_heads, self.head_dim, self.residual_capacity
+        if keys.dtype != torch.bfloat16 or tuple(keys.shape) != (B, H, D) or values.shape != keys.shape:
+            raise ValueError(f"append expects bf16 keys/values of shape [batch, kv_heads, {D}]")
+        _lib.require_device(keys, values)
+        for b, n in enumerate(self.lengths):
+            if n >= R and n - R >= self.capacities[b]:
+                raise RuntimeError(f"sequence {b} is full: {self.capacities[b]} packed slots + {R} window tokens")
+        keys, values = keys.contiguous(), values.contiguous()
+        a = _lib.TQRowsAppendArgs()
+        a.dtype = _lib.dtype_code(torch.bfloat16)
+        a.batch, a.kv_heads, a.head_dim, a.capacity, a.residual_capacity = B, H, D, self.capacity, R
+        a.key_bits = a.value_bits = self.bits
+        a.value_group_size = self.value_group_size
+        a.new_key, a.new_value = keys.data_ptr(), values.data_ptr()
+        a.key_codes, a.key_norms = self.key_codes.data_ptr(), self.key_norms.data_ptr()
+        a.value_data, a.value_scales, a.value_zeros = (self.value_data.data_ptr(), self.value_scales.data_ptr(),
+                                                       self.value_zeros.data_ptr())
+        a.residual_key, a.residual_value = self.residual_key.data_ptr(), self.residual_value.data_ptr()
+        a.seq_lengths, a.overflow = self.seq_lengths.data_ptr(), self.overflow.data_ptr()
+        a.signs, a.thresholds = self.qn.signs.data_ptr(), self.qn.thresholds.data_ptr()
+        _lib.call("anna_mi_tq_rows_append", ctypes.byref(a), _lib.stream_of(keys))
+        self.lengths = [n + 1 for n in self.lengths]
+
+    def decode(self, query: torch.Tensor, *, scaling: float, out: torch.Tensor | None = None,
+               gate: torch.Tensor | None = None) -> torch.Tensor:
+        """query bf16 [B, Hq, D] -> attention output bf16 [B, Hq, D]; gate (optional, same shape):
+        out *= sigmoid(gate)."""
+        shape = (self.batch, self.q_heads, self.head_dim)
+        if query.dtype != torch.bfloat16 or tuple(query.shape) != shape:
+            raise ValueError(f"query must be bf16 [batch, q_heads, {self.head_dim}]")
+        if gate is not None and (gate.dtype != torch.bfloat16 or tuple(gate.shape) != shape):
+            raise ValueError(f"gate must be bf16 [batch, q_heads, {self.head_dim}] (the query's shape)")
+        _lib.require_device(query, gate)
+        q4 = query.contiguous().unsqueeze(2)
+        if out is None:
+            out = torch.empty_like(query)
+        o4 = out.unsqueeze(2)
+        qn = self.qn
+        args = fused_ops.decode_args(
+            query=q4, len1=self.capacity, key=self.key_codes, key_format=fused_ops.KEYS_TQ_MSE,
+            key_norms=self.key_norms, key_bits=self.bits, value=self.value_data,
+            value_format=fused_ops.VALUES_MINMAX, value_scales=self.value_scales, value_zeros=self.value_zeros,
+            value_bits=self.bits, value_group_size=self.value_group_size, rotation=qn.rotation,
+            rotation_t=qn.rotation_t, key_centroids=qn.centroids, query_rot=self.query_rot,
+            residual_key=self.residual_key, residual_value=self.residual_value, scaling=scaling,
+            block_size=self.block_size, gate=None if gate is None else gate.contiguous().unsqueeze(2), output=o4,
+            partial_stats=self.partial_stats, partial_values=self.partial_values, seq_lengths=self.seq_lengths)
+        nblk = fused_ops.decode_num_blocks(args)
+        if nblk > self.partial_stats.size(2):
+            self._partials(nblk)
+            args.partial_stats = _lib.view(self.partial_stats)
+            args.partial_values = _lib.view(self.partial_values)
+            args.partial_capacity = nblk
+        fused_ops.run_decode(args, query)
+        return out
+
+    def bytes_per_decode(self) -> int:
+        """Algorithmic HBM bytes of one decode call: codes, norms, scales and zeros of every packed
+        token (K and V), the dense window, the query and the output."""
+        h, d = self.kv_heads, self.head_dim
+        pb = d * (2 if self.bits == 2 else 4) // 8
+        packed = sum(self.quantized_lens) * h * (2 * pb + 2 + 2 * 2 * (d // self.value_group_size))
         resid = sum(self.residual_lens) * h * 2 * d * 2
         return packed + resid + 2 * self.batch * self.q_heads * d * 2

@@ -191,6 +191,12 @@ typedef struct {
   anna_mi_view partial_stats;  /* fp32 [B, Hq, capacity, 2] */
   anna_mi_view partial_values; /* fp32 [B, Hq, capacity, D] */
   int64_t partial_capacity;
+  /* Optional (NULL: every row holds len1 + len2 tokens).  Per-row token counts, device int32
+   * [B]: row b holds n = seq_lengths[b] tokens, the newest min(n, len2) in the residual segment
+   * (its first positions, in any order: a ring of capacity len2) and the min(max(n - len2, 0),
+   * len1) before them in the main segment; len1 and len2 are then the segments' capacities.  The
+   * batched form of the reference's per-row decode loop (ops.py:1055-1071). */
+  const int32_t* seq_lengths;
 } anna_mi_decode_args;
 
 /* sizeof(anna_mi_decode_args), so that bindings can check their struct layout. */
@@ -299,6 +305,40 @@ typedef struct {
  * blocked layout + norm, bit-exact with anna_mi_tq_hadamard_quantize), the new token takes its
  * ring slot, and seq_lengths[b] grows by one. */
 int anna_mi_tq_append(const anna_mi_tq_append_args* args, void* stream);
+
+/* The general batched cache (one region per sequence and KV head; any power-of-two head_dim in
+ * [64, 1024], key bits 1..4, value bits 2..4): one token per sequence, the form of
+ * Qwen3DynamicCache._update_turboquant_layer looping TurboQuantKVRow.append (ops.py:618-661,
+ * turboquant.py:1027-1140) in one launch.  The token leaving the bf16 window (ring slot n % R)
+ * is quantized into packed slot n - R: keys as Hadamard TQ-MSE codes + fp16 norm (as
+ * anna_mi_tq_hadamard_quantize), values as min/max groups (as anna_mi_tq_values_quantize,
+ * turboquant.py:199-230); the new token takes the ring slot and the length grows by one.  A
+ * sequence whose packed region is full is left unchanged and sets *overflow.  Decode with
+ * anna_mi_gqa_decode_splitkv and seq_lengths. */
+typedef struct {
+  int dtype; /* new tokens, ring, value scales/zeros */
+  int64_t batch, kv_heads, head_dim;
+  int64_t capacity;          /* packed slots per (sequence, KV head) */
+  int64_t residual_capacity; /* R, ring slots per (sequence, KV head) */
+  int key_bits, value_bits;
+  int64_t value_group_size;
+  const void* new_key;       /* [B, Hkv, D] contiguous */
+  const void* new_value;
+  uint8_t* key_codes;        /* [B, Hkv, capacity, D * sbits / 8] (sbits = 2 for 2-bit codes, else 4) */
+  uint16_t* key_norms;       /* fp16 [B, Hkv, capacity] */
+  uint8_t* value_data;       /* [B, Hkv, capacity, D * sbits / 8] */
+  void* value_scales;        /* [B, Hkv, capacity, D / group] */
+  void* value_zeros;
+  void* residual_key;        /* [B, Hkv, R, D], token j of a sequence at slot j % R */
+  void* residual_value;
+  int32_t* seq_lengths;      /* device [B] */
+  int32_t* overflow;         /* device, set to 1 when a sequence is full */
+  const float* signs;        /* Hadamard signs [D] */
+  const float* thresholds;   /* key codebook thresholds [2^key_bits - 1] */
+} anna_mi_tq_rows_append_args;
+
+int64_t anna_mi_sizeof_tq_rows_append_args(void);
+int anna_mi_tq_rows_append(const anna_mi_tq_rows_append_args* args, void* stream);
 
 typedef struct {
   int64_t kv_heads, head_dim, tokens;

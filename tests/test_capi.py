@@ -40,6 +40,7 @@ def test_decode_args_binding_matches_the_c_struct():
     assert _lib.load().anna_mi_sizeof_moe_mlp_args() == ctypes.sizeof(_lib.MoeMlpArgs)
     assert _lib.load().anna_mi_sizeof_tq_append_args() == ctypes.sizeof(_lib.TQAppendArgs)
     assert _lib.load().anna_mi_sizeof_tq_pack_args() == ctypes.sizeof(_lib.TQPackArgs)
+    assert _lib.load().anna_mi_sizeof_tq_rows_append_args() == ctypes.sizeof(_lib.TQRowsAppendArgs)
 
 
 def test_library_is_stamped_with_the_tree_sources():
