@@ -62,7 +62,7 @@ class TQDecodeArgs(ctypes.Structure):
         ("value_norms", _P), ("pool_tokens", _I64), ("residual_key", _P), ("residual_value_t", _P),
         ("residual_capacity", _I64), ("seq_offsets", _P), ("seq_lengths", _P), ("signs", _P), ("key_scale", _F),
         ("value_scale", _F), ("scaling", _F), ("blocks_per_item", _I64), ("num_workgroups", _I64),
-        ("partial_stats", _P), ("partial_values", _P), ("tickets", _P), ("out", _P),
+        ("partial_stats", _P), ("partial_values", _P), ("item_table", _P), ("out", _P),
     ]
 
 

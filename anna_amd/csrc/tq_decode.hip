@@ -1,5 +1,5 @@
-// Batched varlen GQA decode over a 2-bit TurboQuant-MSE KV cache (head_dim 256), MFMA, one
-// launch per step; and the append of one token per sequence.
+// Batched varlen GQA decode over a 2-bit TurboQuant-MSE KV cache (head_dim 256), MFMA, a split
+// and a merge launch per step; and the append of one token per sequence.
 //
 // Cache layout (per KV head, a pool of `pool_tokens` token slots; sequence b owns the slots
 // from seq_offsets[b], a multiple of 32):
@@ -27,10 +27,12 @@
 //     softmax in base 2 with lazy rescaling (the running max moves only by > 2^4).  The window
 //     item does the same on the dense bf16 ring with the unrotated q.
 //   * each item writes (max, denominator) and its unnormalized accumulator to the workspace;
-//     a ticket per (b, kv head) (a global atomic counter) elects the last item to finish,
-//     which merges all items of its (b, kv head) with log-sum-exp weights, rotates the packed
-//     part back (R^T o' = s * FWHT(o') / 16), adds the window part, applies the sigmoid gate,
-//     writes bf16 and resets the ticket.
+//     the window item of (b, kv head) also writes where that pair's packed items are.
+// tq_merge_kernel, one wave per (b, kv head, q head): merges the items with log-sum-exp weights,
+// rotates the packed part back (R^T o' = s * FWHT(o') / 16), adds the window part, applies the
+// sigmoid gate and writes bf16.  (A last-arriving-item merge inside the split kernel measured
+// slower: its coherent partial stores, ticket and merge loads were a chain of round trips after
+// the split, 27.2 against 24.2 us at config 4.)
 //
 // tq_append_kernel, one workgroup per sequence: quantizes the token leaving the ring into the
 // pool (bit-exact with anna_mi_tq_hadamard_quantize), writes the new token into its ring slot
@@ -80,32 +82,6 @@ __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
 }
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
-}
-
-// Device-coherent (agent-scope) stores and loads of the split partials: the stores write
-// through to the point of coherence of all XCDs and the loads read from there, so the items of
-// one (b, kv head), which may run on different XCDs, exchange partials without an L2
-// write-back or invalidate (fences that write the whole L2 back, once per item, cost more
-// than the decode itself).
-__device__ __forceinline__ void store_coherent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void store_coherent4(f32x4* p, f32x4 v) {
-  float* f = (float*)p;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) store_coherent(f + i, v[i]);
-}
-__device__ __forceinline__ uint64_t load_coherent64(const void* p) {
-  return __hip_atomic_load((const uint64_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ f32x4 load_coherent4(const f32x4* p) {
-  const uint64_t lo = load_coherent64(p), hi = load_coherent64((const uint64_t*)p + 1);
-  return f32x4{__uint_as_float((uint32_t)lo), __uint_as_float((uint32_t)(lo >> 32)), __uint_as_float((uint32_t)hi),
-               __uint_as_float((uint32_t)(hi >> 32))};
-}
-__device__ __forceinline__ float2 load_coherent2(const float* p) {
-  const uint64_t v = load_coherent64(p);
-  return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
 }
 
 // ------------------------------------------------------------------ decode kernel
@@ -327,7 +303,6 @@ struct ItemInfo {
   int tb0, tend;      // packed: pool slots [tb0, tend); window: [0, window length)
   int kb;             // packed items of each (b, kv head) of this sequence
   int first_packed;   // workgroup index of item 0 of (b, h = 0)
-  int n_bh;           // items of (b, h): kb + 1
 };
 
 // Work item of this workgroup (computed by wave 0, broadcast through LDS).
@@ -413,7 +388,6 @@ __device__ void plan_item(const anna_mi_tq_decode_args& a, int lane, int* s_nb, 
     it.b = b;
     it.kb = found_kb;
     it.first_packed = B * H + found_excl;
-    it.n_bh = found_kb + 1;
     if (window) {
       it.h = w % H;
       it.kind = len > 0 ? 1 : 2;
@@ -447,7 +421,6 @@ void tq_decode_kernel(const anna_mi_tq_decode_args a) {
   __shared__ float s_m[SWAVES][16], s_l[SWAVES][16];
   __shared__ int s_nb[MAX_SEQS], s_len[MAX_SEQS], s_off[MAX_SEQS];
   __shared__ ItemInfo s_it;
-  __shared__ int s_last;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, kq = lane >> 4;
   if (wave == 0) plan_item(a, lane, s_nb, s_len, s_off, &s_it);
@@ -456,6 +429,11 @@ void tq_decode_kernel(const anna_mi_tq_decode_args a) {
   if (it.kind < 0) return;
   const int G = (int)(a.q_heads / a.kv_heads);
   const int64_t b = it.b, h = it.h, bh = b * a.kv_heads + h;
+  if (it.kind != 0 && threadIdx.x == 0) {
+    // the window item of (b, h) tells the merge where its packed items are (-1: empty sequence)
+    a.item_table[2 * bh] = it.kind == 2 ? -1 : it.first_packed + (int)h * it.kb;
+    a.item_table[2 * bh + 1] = it.kb;
+  }
   if (it.kind == 2) {  // empty sequence: zeros
     for (int i = threadIdx.x; i < G * TD; i += blockDim.x) a.out[(b * a.q_heads + h * G) * TD + i] = 0;
     return;
@@ -539,7 +517,7 @@ void tq_decode_kernel(const anna_mi_tq_decode_args a) {
       f32x4 sum = s_red[j * 32 + e];
 #pragma unroll
       for (int w = 1; w < SWAVES; ++w) sum += s_red[(w * 16 + j) * 32 + e];
-      store_coherent4(pvi + (hb / 8) * 512 + t, sum);
+      pvi[(hb / 8) * 512 + t] = sum;
     }
     __syncthreads();
   }
@@ -549,100 +527,92 @@ void tq_decode_kernel(const anna_mi_tq_decode_args a) {
     for (int w = 0; w < SWAVES; ++w) Mx = fmaxf(Mx, s_m[w][n]);
     for (int w = 0; w < SWAVES; ++w)
       if (s_l[w][n] > 0.f) L += s_l[w][n] * __builtin_amdgcn_exp2f(s_m[w][n] - Mx);
-    store_coherent(a.partial_stats + (item * 16 + n) * 2, Mx);
-    store_coherent(a.partial_stats + (item * 16 + n) * 2 + 1, L);
+    a.partial_stats[(item * 16 + n) * 2] = Mx;
+    a.partial_stats[(item * 16 + n) * 2 + 1] = L;
   }
+}
 
-  // ---- ticket: the last item of (b, h) to arrive merges.  Every wave waits until its
-  // coherent partial stores are acknowledged, then one thread counts the item in.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int old = __hip_atomic_fetch_add(a.tickets + bh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = old == it.n_bh - 1;
-  }
-  __syncthreads();
-  if (!s_last) return;
-
-  // ---- merge: thread t owns entry (tile j, e) of each head block: head hb + e % 8, dims
-  // (4 (e / 8) + i) * 16 + j, i = 0..3
-  float* s_o = s_big;            // [16][TD] packed part, rotated, normalized
-  float* s_w = s_big + 16 * TD;  // [16][TD] window part, normalized
-  {
-    const int t = threadIdx.x, j = t >> 5, e = t & 31, ekq = e >> 3;
-    constexpr int64_t IS = 16 * TD / 4;  // item stride of partial_values in f32x4
-    const f32x4* pv = (const f32x4*)a.partial_values;
-    const int64_t wr = bh;  // window item
-    const int64_t first = it.first_packed + h * it.kb;
-    const int kb = it.kb;
-    for (int hb = 0; hb < G; hb += 8) {
-      const int n = hb + (e & 7);
-      if (n >= G) continue;
-      const int64_t ent = (hb / 8) * 512 + t;
-      const float2 mlr = load_coherent2(a.partial_stats + (wr * 16 + n) * 2);
-      const f32x4 vr = load_coherent4(pv + wr * IS + ent);
-      // online log-sum-exp over the packed items, MRG_BATCH at a time with every load issued first
-      float M = mlr.y > 0.f ? mlr.x : -INFINITY, L = 0.f;
-      f32x4 sp = {0.f, 0.f, 0.f, 0.f};
-      for (int k0 = 0; k0 < kb; k0 += MRG_BATCH) {
-        f32x4 v[MRG_BATCH];
-        float2 ml[MRG_BATCH];
+// grid (B * Hkv * G), one wave per (b, h, query head n): the merge of (b, h)'s items -- the window
+// item bh and the packed items item_table[2 bh] .. + item_table[2 bh + 1] - 1 -- for head n, with
+// log-sum-exp weights; the packed part is rotated back (R^T o' = s * FWHT(o') / 16), the window
+// part added, the sigmoid gate applied.  Lane (j, kq) owns entry (tile j, kq) of the head in the
+// partials' layout, dims (4 kq + i) * 16 + j; an LDS transpose puts dims 4 l .. 4 l + 3 in lane l
+// for the FWHT.  One wave per head spreads the partial reads over many CUs (one workgroup per
+// (b, h) had read all of a sequence's partials through one CU).
+__global__ __launch_bounds__(64) void tq_merge_kernel(const anna_mi_tq_decode_args a) {
+  __shared__ __attribute__((aligned(16))) float s_o[TD], s_w[TD];
+  const int lane = threadIdx.x;
+  const int G = (int)(a.q_heads / a.kv_heads);
+  const int64_t bh = blockIdx.x / G, b = bh / a.kv_heads, h = bh % a.kv_heads;
+  const int n = (int)(blockIdx.x % G);
+  const int first_item = a.item_table[2 * bh], kb = a.item_table[2 * bh + 1];
+  if (first_item < 0) return;  // empty sequence: its window workgroup wrote the zeros
+  const int j = lane & 15, kq = lane >> 4;
+  constexpr int64_t IS = 16 * TD / 4;  // item stride of partial_values in f32x4
+  const int64_t ent = (n / 8) * 512 + j * 32 + kq * 8 + (n % 8);
+  const f32x4* pv = (const f32x4*)a.partial_values;
+  const int64_t orow = (b * a.q_heads + h * G + n) * TD + 4 * lane;
+  // everything the output needs besides the partials, loaded first
+  const float4 sg = *(const float4*)(a.signs + 4 * lane);
+  uint2 graw = make_uint2(0u, 0u);
+  if (a.gate) graw = *(const uint2*)(a.gate + orow);
+  const float2 mlr = *(const float2*)(a.partial_stats + (bh * 16 + n) * 2);
+  const f32x4 vr = pv[bh * IS + ent];
+  // online log-sum-exp over the packed items, MRG_BATCH at a time with every load issued first
+  float M = mlr.y > 0.f ? mlr.x : -INFINITY, L = 0.f;
+  f32x4 sp = {0.f, 0.f, 0.f, 0.f};
+  for (int k0 = 0; k0 < kb; k0 += MRG_BATCH) {
+    f32x4 v[MRG_BATCH];
+    float2 ml[MRG_BATCH];
 #pragma unroll
-        for (int k = 0; k < MRG_BATCH; ++k) {
-          const int64_t slot = first + (k0 + k < kb ? k0 + k : 0);
-          v[k] = load_coherent4(pv + slot * IS + ent);
-          ml[k] = load_coherent2(a.partial_stats + (slot * 16 + n) * 2);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        float mb = M;
-#pragma unroll
-        for (int k = 0; k < MRG_BATCH; ++k)
-          if (k0 + k < kb && ml[k].y > 0.f) mb = fmaxf(mb, ml[k].x);
-        const float f = mb == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - mb);  // 0 while M is -inf
-        sp *= f;
-        L *= f;
-#pragma unroll
-        for (int k = 0; k < MRG_BATCH; ++k) {
-          const float wgt = (k0 + k < kb && ml[k].y > 0.f) ? __builtin_amdgcn_exp2f(ml[k].x - mb) : 0.f;
-          sp += v[k] * wgt;
-          L += ml[k].y * wgt;
-        }
-        M = mb;
-      }
-      const float wr_w = mlr.y > 0.f ? __builtin_amdgcn_exp2f(mlr.x - M) : 0.f;
-      L += mlr.y * wr_w;
-      const float invL = L > 0.f ? 1.0f / L : 0.f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int dim = (4 * ekq + i) * 16 + j;
-        s_o[n * TD + dim] = sp[i] * invL;
-        s_w[n * TD + dim] = vr[i] * wr_w * invL;
-      }
+    for (int k = 0; k < MRG_BATCH; ++k) {
+      const int64_t slot = first_item + (k0 + k < kb ? k0 + k : 0);
+      v[k] = pv[slot * IS + ent];
+      ml[k] = *(const float2*)(a.partial_stats + (slot * 16 + n) * 2);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    float mb = M;
+#pragma unroll
+    for (int k = 0; k < MRG_BATCH; ++k)
+      if (k0 + k < kb && ml[k].y > 0.f) mb = fmaxf(mb, ml[k].x);
+    const float f = mb == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - mb);  // 0 while M is -inf
+    sp *= f;
+    L *= f;
+#pragma unroll
+    for (int k = 0; k < MRG_BATCH; ++k) {
+      const float wgt = (k0 + k < kb && ml[k].y > 0.f) ? __builtin_amdgcn_exp2f(ml[k].x - mb) : 0.f;
+      sp += v[k] * wgt;
+      L += ml[k].y * wgt;
+    }
+    M = mb;
+  }
+  const float wr_w = mlr.y > 0.f ? __builtin_amdgcn_exp2f(mlr.x - M) : 0.f;
+  L += mlr.y * wr_w;
+  const float invL = L > 0.f ? 1.0f / L : 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int dim = (4 * kq + i) * 16 + j;
+    s_o[dim] = sp[i] * invL;
+    s_w[dim] = vr[i] * wr_w * invL;
   }
   __syncthreads();
-  // out = R^T o' + window part = s * FWHT(o') / 16 + w, times sigmoid(gate); wave w: heads w, w + 8
-  for (int n = wave; n < G; n += SWAVES) {
-    float v[4];
-    const float4 o4 = *(const float4*)(s_o + n * TD + 4 * lane);
-    v[0] = o4.x, v[1] = o4.y, v[2] = o4.z, v[3] = o4.w;
-    fwht_wave<4>(v);
-    const float4 w4 = *(const float4*)(s_w + n * TD + 4 * lane);
-    const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
-    const int64_t orow = (b * a.q_heads + h * G + n) * TD + 4 * lane;
-    float o[4];
+  // out = R^T o' + window part = s * FWHT(o') / 16 + w, times sigmoid(gate)
+  float v[4];
+  const float4 o4 = *(const float4*)(s_o + 4 * lane);
+  v[0] = o4.x, v[1] = o4.y, v[2] = o4.z, v[3] = o4.w;
+  fwht_wave<4>(v);
+  const float4 w4 = *(const float4*)(s_w + 4 * lane);
+  const float sgv[4] = {sg.x, sg.y, sg.z, sg.w}, wv[4] = {w4.x, w4.y, w4.z, w4.w};
+  float o[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) o[e] = v[e] * a.signs[4 * lane + e] * inv + wv[e];
-    if (a.gate) {
-      const uint2 g = *(const uint2*)(a.gate + orow);
-      const float gv[4] = {bf16_bits_to_f32((uint16_t)(g.x & 0xFFFFu)), bf16_bits_to_f32((uint16_t)(g.x >> 16)),
-                           bf16_bits_to_f32((uint16_t)(g.y & 0xFFFFu)), bf16_bits_to_f32((uint16_t)(g.y >> 16))};
+  for (int e = 0; e < 4; ++e) o[e] = v[e] * sgv[e] * (1.0f / 16.0f) + wv[e];
+  if (a.gate) {
+    const float gv[4] = {bf16_bits_to_f32((uint16_t)(graw.x & 0xFFFFu)), bf16_bits_to_f32((uint16_t)(graw.x >> 16)),
+                         bf16_bits_to_f32((uint16_t)(graw.y & 0xFFFFu)), bf16_bits_to_f32((uint16_t)(graw.y >> 16))};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = o[e] / (1.0f + __expf(-gv[e]));
-    }
-    *(uint2*)(a.out + orow) = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+    for (int e = 0; e < 4; ++e) o[e] = o[e] / (1.0f + __expf(-gv[e]));
   }
-  if (threadIdx.x == 0) __hip_atomic_store(a.tickets + bh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // for the next call
+  *(uint2*)(a.out + orow) = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
 }
 
 // ------------------------------------------------------------------ append
@@ -833,13 +803,15 @@ extern "C" int anna_mi_tq_decode(const anna_mi_tq_decode_args* ap, void* stream)
   ANNA_CHECK(a.pool_tokens < ((int64_t)1 << 31), "anna_mi_tq_decode: pool slots exceed int32");
   ANNA_CHECK(a.num_workgroups > 2 * a.batch * a.kv_heads && a.num_workgroups < ((int64_t)1 << 31),
              "anna_mi_tq_decode: num_workgroups must come from anna_mi_tq_decode_workgroups");
-  ANNA_CHECK(a.query && a.out && a.partial_stats && a.partial_values && a.tickets && a.seq_offsets && a.seq_lengths &&
+  ANNA_CHECK(a.query && a.out && a.partial_stats && a.partial_values && a.item_table && a.seq_offsets && a.seq_lengths &&
                  a.signs,
              "anna_mi_tq_decode: null pointer");
   ANNA_CHECK(a.key_codes && a.key_norms && a.value_codes && a.value_norms && a.residual_key && a.residual_value_t,
              "anna_mi_tq_decode: null cache pointer");
   hipLaunchKernelGGL(tq_decode_kernel, dim3((unsigned)a.num_workgroups), dim3(64 * SWAVES), 0, as_stream(stream), a);
   ANNA_LAUNCH_CHECK("tq_decode_kernel");
+  hipLaunchKernelGGL(tq_merge_kernel, dim3((unsigned)(a.q_heads * a.batch)), dim3(64), 0, as_stream(stream), a);
+  ANNA_LAUNCH_CHECK("tq_merge_kernel");
   return ANNA_MI_OK;
 }
 

@@ -92,7 +92,7 @@ class TurboQuantBatchCache:
         nwg = self.num_workgroups
         self.partial_stats = torch.empty((nwg, 16, 2), dtype=torch.float32, device=dev)
         self.partial_values = torch.empty((nwg, 16, D), dtype=torch.float32, device=dev)
-        self.tickets = torch.zeros((batch * kv_heads,), dtype=torch.int32, device=dev)
+        self.item_table = torch.zeros((2 * batch * kv_heads,), dtype=torch.int32, device=dev)
 
     # ---- lengths
     @property
@@ -183,7 +183,7 @@ class TurboQuantBatchCache:
         a.blocks_per_item = self.tokens_per_item // 32
         a.num_workgroups = self.num_workgroups
         a.partial_stats, a.partial_values = self.partial_stats.data_ptr(), self.partial_values.data_ptr()
-        a.tickets = self.tickets.data_ptr()
+        a.item_table = self.item_table.data_ptr()
         a.out = out.data_ptr()
         return a
 

@@ -194,7 +194,7 @@ def _clone_cache(c):
 
     n = copy.copy(c)
     for name in ("key_codes", "key_norms", "value_codes", "value_norms", "residual_key", "residual_value_t",
-                 "seq_lengths", "tickets", "partial_stats", "partial_values"):
+                 "seq_lengths", "item_table", "partial_stats", "partial_values"):
         setattr(n, name, getattr(c, name).clone())
     n.lengths = list(c.lengths)
     return n

@@ -261,7 +261,7 @@ typedef struct {
   int64_t num_workgroups;           /* grid size, from anna_mi_tq_decode_workgroups */
   float* partial_stats;             /* workspace [num_workgroups][16][2] */
   float* partial_values;            /* workspace [num_workgroups][16][D] */
-  int32_t* tickets;                 /* workspace [B*Hkv] int32, zero before the first call (left zero) */
+  int32_t* item_table;              /* workspace [2*B*Hkv] int32 (the split tells the merge its items) */
   uint16_t* out;                    /* bf16 [B][Hq][D] */
 } anna_mi_tq_decode_args;
 
@@ -271,13 +271,12 @@ typedef struct {
 int64_t anna_mi_tq_decode_workgroups(int64_t batch, int64_t kv_heads, const int64_t* pool_capacity_host,
                                      int64_t blocks_per_item);
 
-/* One launch: every (b, kv head) is split into work items of 32-token blocks of its quantized
- * prefix plus one window item; the split is planned on the device from seq_lengths (no host
- * round trip, capturable in a graph).  Each item rotates q itself (FWHT), scores the 2-bit codes
- * by MFMA and writes log-sum-exp partials; the last item of a (b, kv head) to finish (a ticket
- * counter) merges them, rotates the result back, adds the window part, applies the gate and
- * writes bf16.  Sequences of length 0 give zeros.  Calls that share workspaces must not
- * overlap. */
+/* Two launches: every (b, kv head) is split into work items of 32-token blocks of its
+ * quantized prefix plus one window item; the split is planned on the device from seq_lengths (no
+ * host round trip, capturable in a graph).  Each item rotates q itself (FWHT), scores the 2-bit
+ * codes by MFMA and writes log-sum-exp partials; the merge launch (one wave per q head) merges
+ * them, rotates the result back, adds the window part, applies the gate and writes bf16.
+ * Sequences of length 0 give zeros.  Calls that share workspaces must not overlap. */
 int anna_mi_tq_decode(const anna_mi_tq_decode_args* args, void* stream);
 
 typedef struct {

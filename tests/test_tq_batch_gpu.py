@@ -127,7 +127,6 @@ def test_batched_decode_matches_oracle(gpu, tokens_per_item, gated):
     gate = torch.randn(4, hkv * g, d, device=gpu).to(torch.bfloat16) if gated else None
     out = cache.decode(q, scaling=1.0 / 16, gate=gate)
     check_against_oracle(cache, keys, vals, q, out, gate)
-    assert int(cache.tickets.abs().sum()) == 0  # every ticket left at zero for the next call
     out2 = cache.decode(q, scaling=1.0 / 16, gate=gate)
     assert torch.equal(out, out2)  # the merge order is fixed: the same bits every call
 
