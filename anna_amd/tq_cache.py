@@ -1,6 +1,6 @@
 """Batched, variable-length TurboQuant KV cache for decode.
 
-One launch appends a token to every sequence and one launch decodes every sequence: this
+One launch appends a token to every sequence and one call (split + merge launches) decodes every sequence: this
 replaces the per-row loops of the reference, the append of
 Qwen3DynamicCache._update_turboquant_layer (src/anna/model/ops.py:618-661, calling
 TurboQuantKVRow.append, turboquant.py:1027-1140) and the decode of
@@ -8,7 +8,7 @@ turboquant_single_token_decode_attention (ops.py:1024-1072, calling
 TurboQuantKVRow.decode_attention per row, turboquant.py:1181-1346).
 
 Two forms behind one class.  head_dim 256 with 2-bit codes (the BASELINE shape) takes the
-single-launch MFMA decode of anna_amd/csrc/tq_decode.hip over TQ-MSE keys and values.  Every
+MFMA decode of anna_amd/csrc/tq_decode.hip over TQ-MSE keys and values.  Every
 other shape (power-of-two head_dim 64..1024, key/value bits 2..4) takes TurboQuantRowsCache:
 TQ-MSE keys and min/max values (the reference row's value format, turboquant.py:199-230) in one
 region per sequence, one append launch, and the split-KV decode with per-row lengths.
