@@ -588,7 +588,7 @@ __global__ __launch_bounds__(64 * MERGE_DIM_WAVES) void decode_merge_dims_kernel
 // Fast path of the split kernel for 16-bit activations, dense keys (packed segment and window)
 // and dense or min/max-packed values, head_dim 64/128/256, G <= 16 query heads per KV head.
 // One wave per workgroup owns a range of `range` tokens of one (KV head, batch) and walks it in
-// 32-token tiles.  The range is chosen on the host (a multiple of 32, about 768 waves in all, no
+// 32-token tiles.  The range is chosen on the host (a multiple of 32, about 1536 waves in all, no
 // more partials than the caller's workspace holds), independently of the caller's block size.
 //   * S^T = K Q^T by v_mfma_f32_16x16x32 (A = 16 key rows x 32 dims straight from memory, B = the
 //     query heads' fragments, kept in registers; two MFMAs per 32 dims for tokens r and 16 + r).
@@ -600,14 +600,15 @@ __global__ __launch_bounds__(64 * MERGE_DIM_WAVES) void decode_merge_dims_kernel
 //     operand of lane (dim, kq) is two 8-byte reads.
 //   * With a fixed tile count (1..4) all of the range's loads are issued at the start, one
 //     register set per tile; otherwise two sets hold tiles n and n + 1 and tile n + 2's loads go
-//     into set n % 2 right after tile n's scores.
+//     into set n % 2 right after tile n's scores.  Two tiles per wave run two waves per SIMD
+//     (228 registers); three or four run one.
 // Each wave writes its range's partial from registers in the reference layout (natural-log max,
 // denominator, unnormalized values), so the merge kernels take it as they take the VALU
 // kernel's blocks.
 constexpr int MF_TILE = 32;         // tokens per tile
 constexpr int MF_VT = MF_TILE + 4;  // LDS pitch (elements) of the transposed V tile: 18 words,
                                     // so the 16 dims of a B-operand read hit distinct banks
-constexpr int64_t MF_WAVES_TARGET = 768;  // about 3 waves per CU
+constexpr int64_t MF_WAVES_TARGET = 1536;  // about 6 waves per CU (NT = 2 runs two waves per SIMD)
 
 // Two floats rounded to nearest-even into the activation dtype, lo in bits 0..15 (one
 // v_cvt_pk_bf16_f32 for bf16).
@@ -660,7 +661,7 @@ __device__ __forceinline__ void load_words(uint32_t (&w)[N], const uint8_t* p) {
 // the range's end, so the compiler waits for exactly the loads each step uses), or 0 (any count,
 // runtime loop).
 template <int DT, int VF, int SB, int D, int NT>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void decode_split_mfma_kernel(
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 : 1, NT == 2 ? 2 : 1))) void decode_split_mfma_kernel(
     const anna_mi_decode_args a, const int64_t range) {
   using Regs = MfmaTileRegs<D, SB>;
   constexpr int NST = Regs::NST, NSP = Regs::NSP, QD = Regs::QD, CW = Regs::CW;
@@ -771,7 +772,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
           qf[st][e] = (uint32_t)q[qb + d * a.query.s3] | ((uint32_t)q[qb + (d + 1) * a.query.s3] << 16);
         }
       }
-      if (r >= G) qf[st] = u32x4{0u, 0u, 0u, 0u};
     }
   }
   if constexpr (NT > 0) {
@@ -780,9 +780,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
   } else {
     if (ntiles > 1) issue(buf[1], t0 + MF_TILE);
   }
+  // the first use of a loaded value (the padding heads' zeros included) stays below every load:
+  // a use above them made the compiler wait for all loads issued so far before issuing the rest
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int st = 0; st < NST; ++st) s_qf[st][lane] = qf[st];
+  for (int st = 0; st < NST; ++st) s_qf[st][lane] = r < G ? qf[st] : u32x4{0u, 0u, 0u, 0u};
 
   const float scale2 = a.scaling * LOG2E;
   float m_run = -INFINITY, l_run = 0.f;  // of head r (lane column), replicated over kq
