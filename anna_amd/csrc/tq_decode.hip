@@ -445,19 +445,32 @@ void tq_decode_kernel(const anna_mi_tq_decode_args a) {
   const float inv = 1.0f / 16.0f;  // fp32(1/sqrt(256)), exact
 
   BlockRaw cur;
-  if (!resid)  // in flight during the prologue (clamped: a wave without blocks reloads the last)
-    load_block(a, h, tb0 + (wave < nblk ? wave : nblk - 1) * TBT, r, kq, cur);
+  // the query rows and signs first: issued behind the block loads they would wait for the
+  // whole first wave of block data
+  uint2 qraw[2] = {make_uint2(0u, 0u), make_uint2(0u, 0u)};
+  float4 sg4 = make_float4(0.f, 0.f, 0.f, 0.f);
   if (!resid) {
+    sg4 = *(const float4*)(a.signs + 4 * lane);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int n = wave + SWAVES * k;
+      if (n < G) qraw[k] = *(const uint2*)(qg + n * TD + 4 * lane);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    load_block(a, h, tb0 + (wave < nblk ? wave : nblk - 1) * TBT, r, kq, cur);
+    __builtin_amdgcn_sched_barrier(0);
     // q' = R q: wave w rotates heads w and w + 8 (lane: dims 4 lane .. 4 lane + 3)
     float* s_q = s_big;  // [16][TD]
-    for (int n = wave; n < 16; n += SWAVES) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int n = wave + SWAVES * k;
       float v[4] = {0.f, 0.f, 0.f, 0.f};
       if (n < G) {
-        const uint2 raw = *(const uint2*)(qg + n * TD + 4 * lane);
-        v[0] = bf16_bits_to_f32((uint16_t)(raw.x & 0xFFFFu)) * a.signs[4 * lane + 0];
-        v[1] = bf16_bits_to_f32((uint16_t)(raw.x >> 16)) * a.signs[4 * lane + 1];
-        v[2] = bf16_bits_to_f32((uint16_t)(raw.y & 0xFFFFu)) * a.signs[4 * lane + 2];
-        v[3] = bf16_bits_to_f32((uint16_t)(raw.y >> 16)) * a.signs[4 * lane + 3];
+        const uint2 raw = qraw[k];
+        v[0] = bf16_bits_to_f32((uint16_t)(raw.x & 0xFFFFu)) * sg4.x;
+        v[1] = bf16_bits_to_f32((uint16_t)(raw.x >> 16)) * sg4.y;
+        v[2] = bf16_bits_to_f32((uint16_t)(raw.y & 0xFFFFu)) * sg4.z;
+        v[3] = bf16_bits_to_f32((uint16_t)(raw.y >> 16)) * sg4.w;
         fwht_wave<4>(v);
       }
       *(float4*)(s_q + n * TD + 4 * lane) = make_float4(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
