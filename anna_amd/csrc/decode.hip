@@ -960,7 +960,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
     if (h < G) {
       float* oh = out + (kvh * G + h) * pv.s1;
 #pragma unroll
-      for (int j = 0; j < NDT; ++j) oh[16 * j * pv.s3] = acc[j][i];
+      for (int j = 0; j < NDT; ++j) __builtin_nontemporal_store(acc[j][i], oh + 16 * j * pv.s3);  // read once, by the merge
     }
   }
 }

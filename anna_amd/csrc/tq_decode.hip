@@ -530,7 +530,7 @@ void tq_decode_kernel(const anna_mi_tq_decode_args a) {
       f32x4 sum = s_red[j * 32 + e];
 #pragma unroll
       for (int w = 1; w < SWAVES; ++w) sum += s_red[(w * 16 + j) * 32 + e];
-      pvi[(hb / 8) * 512 + t] = sum;
+      __builtin_nontemporal_store(sum, pvi + (hb / 8) * 512 + t);  // streamed: read once, by the merge
     }
     __syncthreads();
   }
