@@ -39,6 +39,12 @@
 namespace anna {
 namespace {
 
+constexpr uint32_t OOB = 0x80000000u;  // buffer offset past any num_records: the load returns 0
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+
 // ------------------------------------------------------------------ GEMV (M <= 16)
 
 // K blocks (128 k each) one wave keeps in flight per pass (BPW, a template parameter: 8, or 4
@@ -88,14 +94,17 @@ __global__ __launch_bounds__(64 * KW) void int4_gemv_mfma(
   const int64_t bw0 = contiguous ? (int64_t)wave * GEMV_BPW : wave;
   const int64_t bstep = contiguous ? 1 : KW;
   // One pass = GEMV_BPW blocks per wave (one pass covers K = 4096 at 8 waves).
+  // Buffer loads: lanes of padding rows (row >= M) and past K take an offset beyond the
+  // buffer and read 0 without touching memory (a clamped load plus a select had fetched a real
+  // row for them: at M = 8, x traffic through L1 exceeded the weights').  The host keeps the
+  // buffer below 2^31 bytes.
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)(((M - 1) * xs + K) * 2));
   auto load_x = [&](int64_t b, int s, int g) -> u32x4 {
     const int64_t k = b * 128 + kq * 32 + s * 8;
     const int64_t row = 16 * g + r;
     const bool ok = b < nblk && row < M && k < K;
-    const int64_t kc = ok ? k : 0;
-    const int64_t rc = row < M ? row : 0;
-    const u32x4 v = *(const u32x4*)(x + rc * xs + kc);
-    return ok ? v : zero4;
+    const uint32_t off = ok ? (uint32_t)((row * xs + k) * 2) : OOB;
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
   };
   // With 4 blocks per wave and pass, the x fragments of all of them are loaded first (64
   // VGPRs): a fragment fetched one block ahead was sunk by the compiler next to its use, and
@@ -256,11 +265,6 @@ __device__ __forceinline__ float sum8_16bit(u32x4 v) {
 }
 
 constexpr int DOT2_MAX_WAVES = 16;
-constexpr uint32_t OOB = 0x80000000u;  // buffer offset past any num_records: the load returns 0
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
-}
 
 // v_mov_b32 with a DPP lane pattern (all rows and banks enabled).
 template <int CTRL>
@@ -831,7 +835,8 @@ extern "C" int anna_mi_int4_linear(const void* x, int x_dtype, int64_t M, int64_
     ANNA_LAUNCH_CHECK("int4_gemv_dot2");
     return ANNA_MI_OK;
   }
-  if (x16 && aligned && M <= 16) {
+  const bool x31 = ((M - 1) * xs + K) * 2 < ((int64_t)1 << 31);  // x fits one buffer resource
+  if (x16 && aligned && x31 && M <= 16) {
     ANNA_DISPATCH_DTYPE(scale_dtype, SDT, {
       if (x_dtype == ANNA_MI_BF16)
         dispatch_gemv<ANNA_MI_BF16, SDT>(x, M, K, xs, qweight, N, pc, qscale, qzeros, gsz, y, st);
@@ -844,7 +849,7 @@ extern "C" int anna_mi_int4_linear(const void* x, int x_dtype, int64_t M, int64_
   // 16 < M < 64: the GEMV with 16-row groups of x against register-resident weights (M = 17..48
   // at N = 12288, K = 4096: 24-35 us, where the LDS-tiled fallback below took ~145 us); from
   // M = 64 the tiled GEMM is faster (27.6 against 46 us at M = 64)
-  if (x16 && aligned && M < 64 && (K + 127) / 128 <= 32) {
+  if (x16 && aligned && x31 && M < 64 && (K + 127) / 128 <= 32) {
     ANNA_DISPATCH_DTYPE(scale_dtype, SDT, {
       if (x_dtype == ANNA_MI_BF16)
         dispatch_gemv_mg<ANNA_MI_BF16, SDT>(x, M, K, xs, qweight, N, pc, qscale, qzeros, gsz, y, st);
