@@ -26,7 +26,8 @@
 //     B operand of O'^T = Vhat^T P^T, so the probabilities never leave registers.  Online
 //     softmax in base 2 with lazy rescaling (the running max moves only by > 2^4).  The window
 //     item does the same on the dense bf16 ring with the unrotated q.
-//   * each item writes (max, denominator) and its unnormalized accumulator to the workspace;
+//   * each item writes (max, denominator) and its values divided by the denominator (fp16) to
+//     the workspace;
 //     the window item of (b, kv head) also writes where that pair's packed items are.
 // tq_merge_kernel, one wave per (b, kv head, q head): merges the items with log-sum-exp weights,
 // rotates the packed part back (R^T o' = s * FWHT(o') / 16), adds the window part, applies the
@@ -44,6 +45,8 @@
 
 namespace anna {
 namespace {
+
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
 
 constexpr int TD = 256;              // head_dim
 constexpr int TBT = 32;              // tokens per block
@@ -515,10 +518,13 @@ void tq_decode_kernel(const anna_mi_tq_decode_args a) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) acc[j] *= f;
   }
-  // partial_values[item] as f32x4 [head block hb/8][tile j][kq * 8 + head % 8]; element i of
-  // entry (j, kq) is dim (4 kq + i) * 16 + j (the accumulator layout of O'^T)
+  // partial_values[item] as 4 x fp16 entries [head block hb/8][tile j][kq * 8 + head % 8];
+  // element i of entry (j, kq) is dim (4 kq + i) * 16 + j (the accumulator layout of O'^T).
+  // The values are divided by the item's denominator: a convex combination of dequantized
+  // values, whose magnitude the fp16 value norms bound, so fp16 holds them (2^-11 relative,
+  // below the bf16 output's rounding) at half the bytes the merge reads.
   f32x4* s_red = (f32x4*)s_big;  // [SWAVES][16][32]
-  f32x4* pvi = (f32x4*)(a.partial_values + item * 16 * TD);
+  u32x2v* pvi = (u32x2v*)(a.partial_values + item * 16 * TD);
   for (int hb = 0; hb < G; hb += 8) {
     if (r >= hb && r < hb + 8) {
 #pragma unroll
@@ -527,10 +533,19 @@ void tq_decode_kernel(const anna_mi_tq_decode_args a) {
     __syncthreads();
     const int t = threadIdx.x, j = t >> 5, e = t & 31;
     if (hb + (e & 7) < G) {
+      const int n = hb + (e & 7);
+      float Mx = -INFINITY, L = 0.f;
+#pragma unroll
+      for (int w = 0; w < SWAVES; ++w) Mx = fmaxf(Mx, s_m[w][n]);
+#pragma unroll
+      for (int w = 0; w < SWAVES; ++w)
+        if (s_l[w][n] > 0.f) L += s_l[w][n] * __builtin_amdgcn_exp2f(s_m[w][n] - Mx);
+      const float inv = L > 0.f ? 1.0f / L : 0.f;
       f32x4 sum = s_red[j * 32 + e];
 #pragma unroll
       for (int w = 1; w < SWAVES; ++w) sum += s_red[(w * 16 + j) * 32 + e];
-      __builtin_nontemporal_store(sum, pvi + (hb / 8) * 512 + t);  // streamed: read once, by the merge
+      const u32x2v o = {pack_f16x2(sum[0] * inv, sum[1] * inv), pack_f16x2(sum[2] * inv, sum[3] * inv)};
+      __builtin_nontemporal_store(o, pvi + (hb / 8) * 512 + t);  // streamed: read once, by the merge
     }
     __syncthreads();
   }
@@ -561,21 +576,25 @@ __global__ __launch_bounds__(64) void tq_merge_kernel(const anna_mi_tq_decode_ar
   const int first_item = a.item_table[2 * bh], kb = a.item_table[2 * bh + 1];
   if (first_item < 0) return;  // empty sequence: its window workgroup wrote the zeros
   const int j = lane & 15, kq = lane >> 4;
-  constexpr int64_t IS = 16 * TD / 4;  // item stride of partial_values in f32x4
+  constexpr int64_t IS = 16 * TD / 2;  // item stride of partial_values in 4 x fp16 entries
   const int64_t ent = (n / 8) * 512 + j * 32 + kq * 8 + (n % 8);
-  const f32x4* pv = (const f32x4*)a.partial_values;
+  const u32x2v* pv = (const u32x2v*)a.partial_values;
+  auto f16x4 = [](u32x2v w) {
+    return f32x4{f16_bits_to_f32((uint16_t)(w[0] & 0xFFFFu)), f16_bits_to_f32((uint16_t)(w[0] >> 16)),
+                 f16_bits_to_f32((uint16_t)(w[1] & 0xFFFFu)), f16_bits_to_f32((uint16_t)(w[1] >> 16))};
+  };
   const int64_t orow = (b * a.q_heads + h * G + n) * TD + 4 * lane;
   // everything the output needs besides the partials, loaded first
   const float4 sg = *(const float4*)(a.signs + 4 * lane);
   uint2 graw = make_uint2(0u, 0u);
   if (a.gate) graw = *(const uint2*)(a.gate + orow);
   const float2 mlr = *(const float2*)(a.partial_stats + (bh * 16 + n) * 2);
-  const f32x4 vr = pv[bh * IS + ent];
+  const u32x2v vr = pv[bh * IS + ent];
   // online log-sum-exp over the packed items, MRG_BATCH at a time with every load issued first
   float M = mlr.y > 0.f ? mlr.x : -INFINITY, L = 0.f;
   f32x4 sp = {0.f, 0.f, 0.f, 0.f};
   for (int k0 = 0; k0 < kb; k0 += MRG_BATCH) {
-    f32x4 v[MRG_BATCH];
+    u32x2v v[MRG_BATCH];
     float2 ml[MRG_BATCH];
 #pragma unroll
     for (int k = 0; k < MRG_BATCH; ++k) {
@@ -594,7 +613,7 @@ __global__ __launch_bounds__(64) void tq_merge_kernel(const anna_mi_tq_decode_ar
 #pragma unroll
     for (int k = 0; k < MRG_BATCH; ++k) {
       const float wgt = (k0 + k < kb && ml[k].y > 0.f) ? __builtin_amdgcn_exp2f(ml[k].x - mb) : 0.f;
-      sp += v[k] * wgt;
+      sp += f16x4(v[k]) * (wgt * ml[k].y);  // the partials are normalized by their denominators
       L += ml[k].y * wgt;
     }
     M = mb;
@@ -606,7 +625,7 @@ __global__ __launch_bounds__(64) void tq_merge_kernel(const anna_mi_tq_decode_ar
   for (int i = 0; i < 4; ++i) {
     const int dim = (4 * kq + i) * 16 + j;
     s_o[dim] = sp[i] * invL;
-    s_w[dim] = vr[i] * wr_w * invL;
+    s_w[dim] = f16x4(vr)[i] * (wr_w * mlr.y) * invL;
   }
   __syncthreads();
   // out = R^T o' + window part = s * FWHT(o') / 16 + w, times sigmoid(gate)

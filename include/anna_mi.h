@@ -260,7 +260,7 @@ typedef struct {
   int64_t blocks_per_item;          /* 32-token blocks per work item; 0 = sized to fill the GPU */
   int64_t num_workgroups;           /* grid size, from anna_mi_tq_decode_workgroups */
   float* partial_stats;             /* workspace [num_workgroups][16][2] */
-  float* partial_values;            /* workspace [num_workgroups][16][D] */
+  float* partial_values;            /* workspace, sized as float [num_workgroups][16][D] (internal layout) */
   int32_t* item_table;              /* workspace [2*B*Hkv] int32 (the split tells the merge its items) */
   uint16_t* out;                    /* bf16 [B][Hq][D] */
 } anna_mi_tq_decode_args;
