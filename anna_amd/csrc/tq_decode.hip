@@ -521,8 +521,9 @@ void tq_decode_kernel(const anna_mi_tq_decode_args a) {
   // partial_values[item] as 4 x fp16 entries [head block hb/8][tile j][kq * 8 + head % 8];
   // element i of entry (j, kq) is dim (4 kq + i) * 16 + j (the accumulator layout of O'^T).
   // The values are divided by the item's denominator: a convex combination of dequantized
-  // values, whose magnitude the fp16 value norms bound, so fp16 holds them (2^-11 relative,
-  // below the bf16 output's rounding) at half the bytes the merge reads.
+  // values, whose magnitude the fp16 value norms bound (the window's tokens too: each enters the
+  // pool with an fp16 norm), so fp16 holds them (2^-11 relative, below the bf16 output's
+  // rounding) at half the bytes the merge reads.
   f32x4* s_red = (f32x4*)s_big;  // [SWAVES][16][32]
   u32x2v* pvi = (u32x2v*)(a.partial_values + item * 16 * TD);
   for (int hb = 0; hb < G; hb += 8) {
