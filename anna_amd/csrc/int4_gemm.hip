@@ -39,14 +39,17 @@ constexpr uint32_t GM_OOB = 0x80000000u;   // buffer offset past any num_records
 // SPB k-steps of 64 between two workgroup barriers (a "period"): the smallest tile, whose steps
 // hold little MFMA work, pays the barrier and its waits once per two steps.  LDS holds x for
 // three periods (the one read, the one landing, the one being loaded) and W for two.
-template <int BM_, int BN_, int MW_, int NW_, int SPB_ = 1>
+// KS_ = 2: the workgroup holds two such sets of waves (and LDS), each over half of K; the halves
+// meet at the same barriers, and the second hands its accumulators to the first at the end.
+template <int BM_, int BN_, int MW_, int NW_, int SPB_ = 1, int KS_ = 1>
 struct GemmTile {
-  static constexpr int BM = BM_, BN = BN_, MW = MW_, NW = NW_, SPB = SPB_;
+  static constexpr int BM = BM_, BN = BN_, MW = MW_, NW = NW_, SPB = SPB_, KS = KS_;
   static constexpr int NA = 3 * SPB, NB = 2 * SPB;  // LDS buffers (one k-step each) of x and of W
-  static constexpr int MFMA_WAVES = MW * NW, THREADS = 64 * (MFMA_WAVES + GM_LOAD_WAVES);
+  static constexpr int MFMA_WAVES = MW * NW, HALF_WAVES = MFMA_WAVES + GM_LOAD_WAVES, THREADS = 64 * KS * HALF_WAVES;
   static constexpr int TM = BM / MW, TN = BN / NW, FM = TM / 16, FN = TN / 16;  // wave tile, fragments
   static constexpr int LDS_A = BM * GM_BK, LDS_B = BN * GM_BK;                   // 16-bit elements per buffer
-  static constexpr size_t LDS_BYTES = (size_t)(NA * LDS_A + NB * LDS_B) * 2;
+  static constexpr size_t HALF_ELEMS = (size_t)(NA * LDS_A + NB * LDS_B);  // 16-bit elements of one half
+  static constexpr size_t LDS_BYTES = KS * HALF_ELEMS * 2;
   static constexpr int XLD = BM / 8 / GM_LOAD_WAVES;           // 8-row x blocks per loader wave
   static constexpr int WPT = (BN * 4 + GM_LT - 1) / GM_LT;     // W chunks (8 B = 16 nibbles) per loader thread
   // vector-memory loads one loader thread issues per k-step: the x blocks plus word, scale and
@@ -54,6 +57,7 @@ struct GemmTile {
   static constexpr int LOADS_PER_STEP = XLD + 3 * WPT;
   static_assert(TM % 16 == 0 && TN % 16 == 0 && BM % (8 * GM_LOAD_WAVES) == 0, "tile shape");
   static_assert(SPB == 1 || SPB == 2, "one or two k-steps per period");
+  static_assert(KS == 1 || KS == 2, "one or two halves of K");
   static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 };
 using TileL = GemmTile<256, 192, 2, 4, 1>;  // M >= 1024: 128 x 48 wave tiles, 144 KB LDS
@@ -61,6 +65,8 @@ using TileM = GemmTile<128, 96, 4, 2, 1>;   // M >= 256:  32 x 48 wave tiles, 72
 using TileS = GemmTile<64, 48, 4, 1, 2>;    // M < 256:   16 x 48 wave tiles, 72 KB LDS, 2 steps per
                                             // period (M = 64, N = 12288: 25.6 -> 23.9 us; the 128 x 96
                                             // tile measured no faster with 2)
+using TileS2 = GemmTile<64, 48, 4, 1, 2, 2>;  // TileS with K split over two halves of a 16-wave
+                                              // workgroup (K a multiple of 256), 144 KB LDS
 
 // The loader's end of a k-step: all but its N most recent loads have landed (so the previous
 // step's LDS-destination x loads are in LDS), its LDS writes are done, then the workgroup
@@ -102,17 +108,21 @@ __global__ __launch_bounds__(T::THREADS) void int4_gemm_tiled_kernel(
   constexpr int GM_BM = T::BM, GM_BN = T::BN, GM_LDS_A = T::LDS_A, GM_LDS_B = T::LDS_B;
   constexpr int GM_MFMA_WAVES = T::MFMA_WAVES, GM_XLD = T::XLD, GM_WPT = T::WPT;
   constexpr int GM_NA = T::NA;
-  uint16_t* const sA0 = smem;                       // GM_NA x buffers
-  uint16_t* const sB0 = smem + GM_NA * GM_LDS_A;    // GM_NB W buffers
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = threadIdx.x & 63;
+  // k-half of this wave (uniform), its wave and thread index within the half
+  const int half = T::KS > 1 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6) / T::HALF_WAVES) : 0;
+  const int wave = (int)(threadIdx.x >> 6) - half * T::HALF_WAVES;
+  const int tid = (int)threadIdx.x - 64 * T::HALF_WAVES * half;
+  uint16_t* const sA0 = smem + half * T::HALF_ELEMS;  // GM_NA x buffers
+  uint16_t* const sB0 = sA0 + GM_NA * GM_LDS_A;       // GM_NB W buffers
   // tile coordinates in 32-bit scalar registers: a value the compiler cannot prove uniform
   // would turn every buffer load below into a loop over distinct descriptors
   const int t = __builtin_amdgcn_readfirstlane((int)xcd_tile(blockIdx.x, tiles_m * tiles_n));
   const int tn32 = (int)tiles_n;
   const int64_t m0 = (int64_t)__builtin_amdgcn_readfirstlane((t / tn32) * GM_BM);
   const int64_t n0 = (int64_t)__builtin_amdgcn_readfirstlane((t % tn32) * GM_BN);
-  const int nk = (int)(K / GM_BK);
+  const int nk = (int)(K / GM_BK) / T::KS;  // k-steps of this half (the launcher makes both equal)
+  const int kb = half * nk;                  // its first k-step
 
   if (wave >= GM_MFMA_WAVES) {
     // ---------------- loader waves
@@ -164,10 +174,10 @@ __global__ __launch_bounds__(T::THREADS) void int4_gemm_tiled_kernel(
 #pragma unroll
       for (int j = 0; j < GM_XLD; ++j)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(dst + j * 8 * GM_BK), 16, xo,
-                                                 (int)((8 * (GM_XLD * lw + j)) * xs * 2) + ks * (GM_BK * 2), 0, 0);
+                                                 (int)((8 * (GM_XLD * lw + j)) * xs * 2) + (kb + ks) * (GM_BK * 2), 0, 0);
     };
     auto load_w = [&](int ks, Stage& S) {
-      ks = ks < nk ? ks : nk - 1;
+      ks = (ks < nk ? ks : nk - 1) + kb;
       const int g = spg == 1 ? ks : (int)__umulhi((uint32_t)ks, ginv);
 #pragma unroll
       for (int i = 0; i < GM_WPT; ++i) {
@@ -280,6 +290,7 @@ __global__ __launch_bounds__(T::THREADS) void int4_gemm_tiled_kernel(
     }
     // the last steps' reloads land in buffers nobody reads; drain them before the wave ends
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if constexpr (T::KS > 1) __syncthreads();  // the MFMA waves' accumulator hand-off barrier
     return;
   }
 
@@ -334,6 +345,29 @@ __global__ __launch_bounds__(T::THREADS) void int4_gemm_tiled_kernel(
       __syncthreads();
     }
   }
+  if constexpr (T::KS > 1) {
+    // the second half's accumulators to the first through LDS (every MFMA read of the loop is
+    // done: its last barrier has passed; the loader waves have drained and meet this barrier)
+    float* const s_c = (float*)smem;  // [MFMA wave][fragment element][lane]
+    constexpr int NE = FM * FN * 4;
+    static_assert((size_t)T::MFMA_WAVES * NE * 64 * 4 <= T::HALF_ELEMS * 2, "accumulator hand-off exceeds LDS");
+    if (half == 1) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s_c[(wave * NE + (i * FN + j) * 4 + e) * 64 + lane] = acc[i][j][e];
+    }
+    __syncthreads();
+    if (half == 1) return;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[i][j][e] += s_c[(wave * NE + (i * FN + j) * 4 + e) * 64 + lane];
+  }
   // C layout: lane holds rows 4 kq + e of column r of each 16 x 16 block
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
@@ -375,6 +409,12 @@ int int4_gemm_tiled_launch(const void* x, int x_dtype, int64_t M, int64_t K, int
     return ((M + TT::BM - 1) / TT::BM) * ((N + TT::BN - 1) / TT::BN);
   };
   int shape = tiles(TileL{}) >= 256 ? 0 : tiles(TileM{}) >= 256 ? 1 : 2;
+  // the small tile splits K over two halves of the workgroup when its tiles fit one round of
+  // workgroups (the 16-wave, 144 KB workgroup takes a whole compute unit: with more tiles, two
+  // plain ones per unit are faster) and both halves get the same number of two-step periods
+  // (their barriers must pair up).  M = 64, K = 4096: N = 12288 24.1 -> 21.9 us, N = 6144
+  // 22.5 -> 19.0 us; M = 256, N = 6144 (512 tiles) split 39.3 against 35 us.
+  const bool split = tiles(TileS{}) <= 256 && (K / GM_BK) % (2 * TileS2::SPB) == 0;
   // ANNA_MI_INT4_GEMM_TILE = L / M / S forces a tile shape (read on every call; the tests run
   // every shape on shapes small enough for the CPU oracle)
   if (const char* f = getenv("ANNA_MI_INT4_GEMM_TILE"); f && *f) shape = f[0] == 'L' ? 0 : f[0] == 'M' ? 1 : 2;
@@ -400,7 +440,7 @@ int int4_gemm_tiled_launch(const void* x, int x_dtype, int64_t M, int64_t K, int
       return x_dtype == ANNA_MI_BF16 ? go(std::integral_constant<int, ANNA_MI_BF16>{}, tile_tag)
                                      : go(std::integral_constant<int, ANNA_MI_F16>{}, tile_tag);
     };
-    const int rc = shape == 0 ? go_x(TileL{}) : shape == 1 ? go_x(TileM{}) : go_x(TileS{});
+    const int rc = shape == 0 ? go_x(TileL{}) : shape == 1 ? go_x(TileM{}) : split ? go_x(TileS2{}) : go_x(TileS{});
     if (rc != ANNA_MI_OK) return rc;
   });
   ANNA_LAUNCH_CHECK("int4_gemm_tiled_kernel");
