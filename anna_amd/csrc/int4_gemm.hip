@@ -403,12 +403,16 @@ bool int4_gemm_tiled_supported(int x_dtype, int64_t M, int64_t N, int64_t K, int
 int int4_gemm_tiled_launch(const void* x, int x_dtype, int64_t M, int64_t K, int64_t xs, const int32_t* qweight,
                            int64_t N, int64_t pc, const void* qscale, int scale_dtype, const int8_t* qzeros, int64_t gsz,
                            void* y, hipStream_t st) {
-  // the largest tile that still gives every compute unit a workgroup (256 of them)
+  // the largest tile that still gives (about) every compute unit a workgroup (256 of them)
   auto tiles = [&](auto t) {
     using TT = decltype(t);
     return ((M + TT::BM - 1) / TT::BM) * ((N + TT::BN - 1) / TT::BN);
   };
-  int shape = tiles(TileL{}) >= 256 ? 0 : tiles(TileM{}) >= 256 ? 1 : 2;
+  // The large tile also wins from 192 tiles, or 128 whose m-tiles are all full (N = 12288,
+  // K = 4096: M = 768 99 against 125 us with the middle tile; M = 1024, N = 6144: 84 against
+  // 87 us; M = 384 (128 tiles, the last half empty) 85 against 74 us).
+  const int64_t tl = tiles(TileL{});
+  int shape = (tl >= 192 || (tl >= 128 && M % TileL::BM == 0)) ? 0 : tiles(TileM{}) >= 256 ? 1 : 2;
   // the small tile splits K over two halves of the workgroup when its tiles fit one round of
   // workgroups (the 16-wave, 144 KB workgroup takes a whole compute unit: with more tiles, two
   // plain ones per unit are faster) and both halves get the same number of two-step periods
