@@ -65,6 +65,8 @@ using TileM = GemmTile<128, 96, 4, 2, 1>;   // M >= 256:  32 x 48 wave tiles, 72
 using TileS = GemmTile<64, 48, 4, 1, 2>;    // M < 256:   16 x 48 wave tiles, 72 KB LDS, 2 steps per
                                             // period (M = 64, N = 12288: 25.6 -> 23.9 us; the 128 x 96
                                             // tile measured no faster with 2)
+using TileM2 = GemmTile<128, 96, 2, 2, 1, 2>;  // TileM's tile with K split over two halves of a
+                                               // 16-wave workgroup, 4 MFMA waves of 64 x 48 each
 using TileS2 = GemmTile<64, 48, 4, 1, 2, 2>;  // TileS with K split over two halves of a 16-wave
                                               // workgroup (K a multiple of 256), 144 KB LDS
 
@@ -419,6 +421,9 @@ int int4_gemm_tiled_launch(const void* x, int x_dtype, int64_t M, int64_t K, int
   // (their barriers must pair up).  M = 64, K = 4096: N = 12288 24.1 -> 21.9 us, N = 6144
   // 22.5 -> 19.0 us; M = 256, N = 6144 (512 tiles) split 39.3 against 35 us.
   const bool split = tiles(TileS{}) <= 256 && (K / GM_BK) % (2 * TileS2::SPB) == 0;
+  // likewise the middle tile at exactly one round (M = 256, N = 12288: 52.4 -> 46.4 us; M = 192:
+  // 51.3 -> 43.9 us), whose one-step periods need an even step count
+  const bool msplit = tiles(TileM{}) <= 256 && (K / GM_BK) % (2 * TileM2::SPB) == 0;
   // ANNA_MI_INT4_GEMM_TILE = L / M / S forces a tile shape (read on every call; the tests run
   // every shape on shapes small enough for the CPU oracle)
   if (const char* f = getenv("ANNA_MI_INT4_GEMM_TILE"); f && *f) shape = f[0] == 'L' ? 0 : f[0] == 'M' ? 1 : 2;
@@ -444,7 +449,7 @@ int int4_gemm_tiled_launch(const void* x, int x_dtype, int64_t M, int64_t K, int
       return x_dtype == ANNA_MI_BF16 ? go(std::integral_constant<int, ANNA_MI_BF16>{}, tile_tag)
                                      : go(std::integral_constant<int, ANNA_MI_F16>{}, tile_tag);
     };
-    const int rc = shape == 0 ? go_x(TileL{}) : shape == 1 ? go_x(TileM{}) : split ? go_x(TileS2{}) : go_x(TileS{});
+    const int rc = shape == 0 ? go_x(TileL{}) : shape == 1 ? (msplit ? go_x(TileM2{}) : go_x(TileM{})) : split ? go_x(TileS2{}) : go_x(TileS{});
     if (rc != ANNA_MI_OK) return rc;
   });
   ANNA_LAUNCH_CHECK("int4_gemm_tiled_kernel");
