@@ -104,6 +104,7 @@ PROTOTYPES.update({
     "anna_mi_tq_pack_kv": [ctypes.POINTER(TQPackArgs), _P],
     "anna_mi_tq_decode": [ctypes.POINTER(TQDecodeArgs), _P],
     "anna_mi_tq_append": [ctypes.POINTER(TQAppendArgs), _P],
+    "anna_mi_tq_append_decode": [ctypes.POINTER(TQDecodeArgs), ctypes.POINTER(TQAppendArgs), _P],
     "anna_mi_tq_block_values": [_P, _I64, _P, _P],
     "anna_mi_tq_rotation": [_I64, ctypes.c_uint64, _P],
     "anna_mi_tq_codebook": [_I, _I64, _P, _P],

@@ -87,6 +87,51 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
 }
 
+// The token leaving sequence b's ring (its length n >= R, so ring slot n % R holds token n - R):
+// vector is_v (K or V) of KV head h quantized by one wave into pool slot `slot` -- key codes
+// token-major, value codes into their 2 bits of the 32-token blocked layout -- with its fp16
+// norm (bit-exact with anna_mi_tq_hadamard_quantize).
+// rec (or nullptr): also the code byte of the lane's 4 dims at rec[64 is_v + lane] and the norm
+// at rec + 128 + 2 is_v.
+__device__ __forceinline__ void evict_token(const anna_mi_tq_append_args& a, int64_t b, int64_t h, int n, int64_t slot,
+                                            bool is_v, int lane, uint8_t* rec = nullptr) {
+  const int64_t H = a.kv_heads, R = a.residual_capacity, T = a.pool_tokens, rpos = n % R;
+  float x[4];
+  if (!is_v) {
+    const uint2 raw = *(const uint2*)(a.residual_key + ((b * H + h) * R + rpos) * TD + 4 * lane);
+    x[0] = bf16_bits_to_f32((uint16_t)(raw.x & 0xFFFFu));
+    x[1] = bf16_bits_to_f32((uint16_t)(raw.x >> 16));
+    x[2] = bf16_bits_to_f32((uint16_t)(raw.y & 0xFFFFu));
+    x[3] = bf16_bits_to_f32((uint16_t)(raw.y >> 16));
+  } else {
+    const uint16_t* col = a.residual_value_t + (b * H + h) * TD * R + rpos;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = bf16_bits_to_f32(col[(4 * lane + e) * R]);
+  }
+  uint32_t code[4];
+  const float nrm = hadamard_codes_wave<4>(x, a.signs, a.thresholds, 3, 1.0f / 16.0f, code);
+  const uint16_t nb16 = f32_to_f16_bits(nrm);
+  const uint8_t byte = (uint8_t)(code[0] | (code[1] << 2) | (code[2] << 4) | (code[3] << 6));
+  if (rec) {
+    rec[64 * is_v + lane] = byte;
+    if (lane == 0) ((uint16_t*)(rec + 128))[is_v] = nb16;
+  }
+  if (!is_v) {
+    a.key_codes[(h * T + slot) * 64 + lane] = byte;
+    if (lane == 0) a.key_norms[h * T + slot] = nb16;
+  } else {
+    const int64_t t = slot % TBT;
+    uint8_t* blk = a.value_codes + (h * (T / TBT) + slot / TBT) * 2048 + ((t % 16) / 4) * 512 + (t / 16);
+    const int sh = 2 * (int)(t % 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      uint8_t* p = blk + (4 * lane + e) * 2;
+      *p = (uint8_t)(sh == 0 ? code[e] : (*p | (code[e] << sh)));
+    }
+    if (lane == 0) a.value_norms[h * T + slot] = nb16;
+  }
+}
+
 // ------------------------------------------------------------------ decode kernel
 
 constexpr int SWAVES = 8;      // waves per work item
@@ -134,8 +179,8 @@ __device__ __forceinline__ uint32_t pkrtz(float lo, float hi) {
 // (the residual path reads s_qf and passes nullptr)
 template <bool RESID>
 __device__ __forceinline__ void block_step(const anna_mi_tq_decode_args& a, const u32x4 (*s_qf)[64], const u32x4* qf,
-                                           int64_t b, int64_t h, int64_t tb, int64_t tend, int lane, const BlockRaw& cur,
-                                           f32x4 (&acc)[16], float& m_run, float& l_run) {
+                                           int64_t b, int64_t h, int64_t tb, int64_t tend, int64_t skip, int lane,
+                                           const BlockRaw& cur, f32x4 (&acc)[16], float& m_run, float& l_run) {
   const int r = lane & 15, kq = lane >> 4;
   const int64_t Rc = a.residual_capacity;
   const uint32_t lut_hi = vconst(0x433CBCC3u), lut_lo = vconst(0x7E7E7E7Eu), or_c = vconst(0x04000400u);
@@ -205,6 +250,17 @@ __device__ __forceinline__ void block_step(const anna_mi_tq_decode_args& a, cons
         }
       }
     }
+    if (RESID && skip >= tb && skip < tb + TBT) {
+      // the window slot whose token has just left the ring (the fused append + decode)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int64_t t = tb + (i >> 2) * 16 + 4 * kq + (i & 3);
+        if (t == skip) {
+          s[i] = -INFINITY;
+          nv[i] = 0.f;
+        }
+      }
+    }
     float mx = s[0];
 #pragma unroll
     for (int i = 1; i < 8; ++i) mx = fmaxf(mx, s[i]);
@@ -221,7 +277,11 @@ __device__ __forceinline__ void block_step(const anna_mi_tq_decode_args& a, cons
     u32x4 pf;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float p0 = __builtin_amdgcn_exp2f(s[i] - m_run), p1 = __builtin_amdgcn_exp2f(s[4 + i] - m_run);
+      float p0 = __builtin_amdgcn_exp2f(s[i] - m_run), p1 = __builtin_amdgcn_exp2f(s[4 + i] - m_run);
+      if (RESID) {  // a window block can be all masked (the skipped slot alone), m_run still -inf
+        p0 = s[i] == -INFINITY ? 0.f : p0;
+        p1 = s[4 + i] == -INFINITY ? 0.f : p1;
+      }
       l_run += p0 + p1;
       pf[i] = RESID ? pack_bf16x2(p0 * nv[i], p1 * nv[4 + i]) : pkrtz(p0 * nv[i], p1 * nv[4 + i]);
     }
@@ -255,12 +315,12 @@ __device__ __forceinline__ void block_step(const anna_mi_tq_decode_args& a, cons
 // to the last block) so that no wait for it is forced before the current block is consumed.
 template <bool RESID>
 __device__ __forceinline__ void run_blocks(const anna_mi_tq_decode_args& a, const u32x4 (*s_qf)[64], int64_t b, int64_t h,
-                                           int64_t tb0, int64_t tend, int64_t nblk, int wave, int lane, BlockRaw& A,
-                                           f32x4 (&acc)[16], float& m_run, float& l_run) {
+                                           int64_t tb0, int64_t tend, int64_t skip, int64_t nblk, int wave, int lane,
+                                           BlockRaw& A, f32x4 (&acc)[16], float& m_run, float& l_run) {
   const int r = lane & 15, kq = lane >> 4;
   if constexpr (RESID) {
     for (int64_t blk = wave; blk < nblk; blk += SWAVES)
-      block_step<true>(a, s_qf, nullptr, b, h, tb0 + blk * TBT, tend, lane, A, acc, m_run, l_run);
+      block_step<true>(a, s_qf, nullptr, b, h, tb0 + blk * TBT, tend, skip, lane, A, acc, m_run, l_run);
   } else {
     u32x4 qf[8];
 #pragma unroll
@@ -274,11 +334,11 @@ __device__ __forceinline__ void run_blocks(const anna_mi_tq_decode_args& a, cons
     int64_t i = 0;
     for (; i + 1 < cnt; i += 2) {
       load_block(a, h, slot(i + 1), r, kq, B);
-      block_step<false>(a, s_qf, qf, b, h, slot(i), tend, lane, A, acc, m_run, l_run);
+      block_step<false>(a, s_qf, qf, b, h, slot(i), tend, -1, lane, A, acc, m_run, l_run);
       load_block(a, h, slot(i + 2), r, kq, A);
-      block_step<false>(a, s_qf, qf, b, h, slot(i + 1), tend, lane, B, acc, m_run, l_run);
+      block_step<false>(a, s_qf, qf, b, h, slot(i + 1), tend, -1, lane, B, acc, m_run, l_run);
     }
-    if (i < cnt) block_step<false>(a, s_qf, qf, b, h, slot(i), tend, lane, A, acc, m_run, l_run);
+    if (i < cnt) block_step<false>(a, s_qf, qf, b, h, slot(i), tend, -1, lane, A, acc, m_run, l_run);
   }
 }
 
@@ -415,8 +475,25 @@ __device__ void plan_item(const anna_mi_tq_decode_args& a, int lane, int* s_nb, 
 
 constexpr int MRG_BATCH = 16;  // items whose partials the merge loads together
 
+// The fused step's record of the token leaving (b, h)'s ring, in the unused upper half of the
+// window item's partial slot (the window items are workgroups 0 .. B Hkv - 1): key code bytes
+// [64], value code bytes [64] (lane l: dims 4 l .. 4 l + 3, 2 bits each), the two fp16 norms,
+// and whether the token was stored (int32 at byte 132).  The merge reads it at an address that
+// does not depend on the item table.
+__device__ __forceinline__ uint8_t* evict_record(const anna_mi_tq_decode_args& a, int64_t bh) {
+  return (uint8_t*)(a.partial_values + bh * 16 * TD) + 12288;
+}
+
+// FUSED: the step's append as well (ap describes the same cache).  The plan and the packed items
+// see the lengths before the append; the window workgroup of (b, h) quantizes the token leaving
+// its ring into the pool slot just past the packed items' range and leaves that ring slot out
+// of its own attention; the merge launch adds the leaving token (from its fresh codes) and the
+// new one, then writes the new token into the ring and the new length.  Item table entries are
+// 4 per (b, h): first packed item, item count, length before the append, whether the leaving
+// token was stored.
+template <bool FUSED>
 __global__ __launch_bounds__(64 * SWAVES) __attribute__((amdgpu_waves_per_eu(2, 8)))
-void tq_decode_kernel(const anna_mi_tq_decode_args a) {
+void tq_decode_kernel(const anna_mi_tq_decode_args a, const anna_mi_tq_append_args ap) {
   // one 64 KB buffer, used in turn for the rotated query (fp32 [16][256]), the cross-wave sums
   // ([wave][tile j][kq * 8 + head % 8] f32x4) and the merge's two [16][256] fp32 results
   __shared__ __attribute__((aligned(16))) float s_big[SWAVES * 16 * 32 * 4];
@@ -432,16 +509,37 @@ void tq_decode_kernel(const anna_mi_tq_decode_args a) {
   if (it.kind < 0) return;
   const int G = (int)(a.q_heads / a.kv_heads);
   const int64_t b = it.b, h = it.h, bh = b * a.kv_heads + h;
-  if (it.kind != 0 && threadIdx.x == 0) {
-    // the window item of (b, h) tells the merge where its packed items are (-1: empty sequence)
-    a.item_table[2 * bh] = it.kind == 2 ? -1 : it.first_packed + (int)h * it.kb;
-    a.item_table[2 * bh + 1] = it.kb;
+  int64_t skip = -1;  // window slot left out (the fused append's leaving token)
+  if constexpr (FUSED) {
+    if (it.kind != 0) {
+      const int n = s_len[b];
+      const int64_t R = a.residual_capacity;
+      const bool room = n >= R && n - R < ap.seq_capacity[b];
+      if (n >= R) {
+        skip = n % R;
+        if (!room && threadIdx.x == 0 && ap.overflow) *ap.overflow = 1;
+      }
+      if (threadIdx.x == 0) {
+        *(int*)(evict_record(a, bh) + 132) = room ? 1 : 0;
+        a.item_table[4 * bh] = it.first_packed + (int)h * it.kb;
+        a.item_table[4 * bh + 1] = it.kb;
+        a.item_table[4 * bh + 2] = n;
+        a.item_table[4 * bh + 3] = room ? 1 : 0;
+      }
+    }
+  } else {
+    if (it.kind != 0 && threadIdx.x == 0) {
+      // the window item of (b, h) tells the merge where its packed items are (-1: empty sequence)
+      a.item_table[2 * bh] = it.kind == 2 ? -1 : it.first_packed + (int)h * it.kb;
+      a.item_table[2 * bh + 1] = it.kb;
+    }
+    if (it.kind == 2) {  // empty sequence: zeros
+      for (int i = threadIdx.x; i < G * TD; i += blockDim.x) a.out[(b * a.q_heads + h * G) * TD + i] = 0;
+      return;
+    }
   }
-  if (it.kind == 2) {  // empty sequence: zeros
-    for (int i = threadIdx.x; i < G * TD; i += blockDim.x) a.out[(b * a.q_heads + h * G) * TD + i] = 0;
-    return;
-  }
-  const bool resid = it.kind == 1;
+  // (fused: an empty sequence's window item runs with no slots and writes empty stats)
+  const bool resid = it.kind != 0;
   const int64_t tb0 = it.tb0, tend = it.tend;
   const int64_t nblk = (tend - tb0 + TBT - 1) / TBT;
   const uint16_t* qg = a.query + (b * a.q_heads + h * G) * TD;
@@ -497,10 +595,20 @@ void tq_decode_kernel(const anna_mi_tq_decode_args a) {
   for (int j = 0; j < 16; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
   if (resid)
-    run_blocks<true>(a, s_qf, b, h, tb0, tend, nblk, wave, lane, cur, acc, m_run, l_run);
+    run_blocks<true>(a, s_qf, b, h, tb0, tend, skip, nblk, wave, lane, cur, acc, m_run, l_run);
   else
-    run_blocks<false>(a, s_qf, b, h, tb0, tend, nblk, wave, lane, cur, acc, m_run, l_run);
+    run_blocks<false>(a, s_qf, b, h, tb0, tend, -1, nblk, wave, lane, cur, acc, m_run, l_run);
 
+  if constexpr (FUSED) {
+    // the window workgroup quantizes the token leaving the ring into the pool slot just past its
+    // sequence's packed items (which do not read it), after its own attention loop
+    if (resid && skip >= 0 && wave < 2) {
+      const int n = s_len[b];
+      const int64_t R = a.residual_capacity;
+      if (n - R < ap.seq_capacity[b])
+        evict_token(ap, b, h, n, s_off[b] + (n - R), wave == 1, lane, evict_record(a, bh));
+    }
+  }
   // ---- reduce the waves, write this item's partials (workgroup index = item slot)
   const int64_t item = blockIdx.x;
   l_run += __shfl_xor(l_run, 16, 64);
@@ -568,14 +676,24 @@ void tq_decode_kernel(const anna_mi_tq_decode_args a) {
 // partials' layout, dims (4 kq + i) * 16 + j; an LDS transpose puts dims 4 l .. 4 l + 3 in lane l
 // for the FWHT.  One wave per head spreads the partial reads over many CUs (one workgroup per
 // (b, h) had read all of a sequence's partials through one CU).
-__global__ __launch_bounds__(64) void tq_merge_kernel(const anna_mi_tq_decode_args a) {
+template <bool FUSED>
+__global__ __launch_bounds__(64) void tq_merge_kernel(const anna_mi_tq_decode_args a, const anna_mi_tq_append_args ap) {
   __shared__ __attribute__((aligned(16))) float s_o[TD], s_w[TD];
   const int lane = threadIdx.x;
   const int G = (int)(a.q_heads / a.kv_heads);
   const int64_t bh = blockIdx.x / G, b = bh / a.kv_heads, h = bh % a.kv_heads;
   const int n = (int)(blockIdx.x % G);
-  const int first_item = a.item_table[2 * bh], kb = a.item_table[2 * bh + 1];
-  if (first_item < 0) return;  // empty sequence: its window workgroup wrote the zeros
+  const int64_t orow = (b * a.q_heads + h * G + n) * TD + 4 * lane;
+  // fused: the query row and the new token (independent of the item table), loaded first
+  uint2 qraw = make_uint2(0u, 0u), nkraw = make_uint2(0u, 0u), nvraw = make_uint2(0u, 0u);
+  if constexpr (FUSED) {
+    qraw = *(const uint2*)(a.query + orow);
+    nkraw = *(const uint2*)(ap.new_key + bh * TD + 4 * lane);
+    nvraw = *(const uint2*)(ap.new_value + bh * TD + 4 * lane);
+  }
+  constexpr int TS = FUSED ? 4 : 2;  // item table entries per (b, h)
+  const int first_item = a.item_table[TS * bh], kb = a.item_table[TS * bh + 1];
+  if (!FUSED && first_item < 0) return;  // empty sequence: its window workgroup wrote the zeros
   const int j = lane & 15, kq = lane >> 4;
   constexpr int64_t IS = 16 * TD / 2;  // item stride of partial_values in 4 x fp16 entries
   const int64_t ent = (n / 8) * 512 + j * 32 + kq * 8 + (n % 8);
@@ -584,13 +702,27 @@ __global__ __launch_bounds__(64) void tq_merge_kernel(const anna_mi_tq_decode_ar
     return f32x4{f16_bits_to_f32((uint16_t)(w[0] & 0xFFFFu)), f16_bits_to_f32((uint16_t)(w[0] >> 16)),
                  f16_bits_to_f32((uint16_t)(w[1] & 0xFFFFu)), f16_bits_to_f32((uint16_t)(w[1] >> 16))};
   };
-  const int64_t orow = (b * a.q_heads + h * G + n) * TD + 4 * lane;
   // everything the output needs besides the partials, loaded first
   const float4 sg = *(const float4*)(a.signs + 4 * lane);
   uint2 graw = make_uint2(0u, 0u);
   if (a.gate) graw = *(const uint2*)(a.gate + orow);
   const float2 mlr = *(const float2*)(a.partial_stats + (bh * 16 + n) * 2);
   const u32x2v vr = pv[bh * IS + ent];
+  // fused: the codes of the token that left the ring, in its pool slot (written by the split
+  // launch): lane l's dims 4 l .. 4 l + 3
+  int len0 = 0, stored = 0;
+  uint32_t kcode = 0, vcode[4] = {0u, 0u, 0u, 0u}, norms = 0;
+  if constexpr (FUSED) {
+    const uint8_t* rec = evict_record(a, bh);
+    stored = *(const int*)(rec + 132);
+    kcode = rec[lane];
+    const uint32_t vb = rec[64 + lane];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) vcode[e] = vb >> (2 * e);
+    norms = *(const uint32_t*)(rec + 128);
+    len0 = a.item_table[4 * bh + 2];
+  }
+  const uint16_t knorm = (uint16_t)(norms & 0xFFFFu), vnorm = (uint16_t)(norms >> 16);
   // online log-sum-exp over the packed items, MRG_BATCH at a time with every load issued first
   float M = mlr.y > 0.f ? mlr.x : -INFINITY, L = 0.f;
   f32x4 sp = {0.f, 0.f, 0.f, 0.f};
@@ -619,6 +751,47 @@ __global__ __launch_bounds__(64) void tq_merge_kernel(const anna_mi_tq_decode_ar
     }
     M = mb;
   }
+  // fused: the two tokens of the append, one score each (log2 units): the new one against the
+  // query as the window scores it, the leaving one from its codes against the rotated query as
+  // the packed items score it; both enter the log-sum-exp with denominator 1
+  float we = 0.f, wn = 0.f, vev[4] = {0.f, 0.f, 0.f, 0.f}, vnew[4] = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (FUSED) {
+    const float q[4] = {bf16_bits_to_f32((uint16_t)(qraw.x & 0xFFFFu)), bf16_bits_to_f32((uint16_t)(qraw.x >> 16)),
+                        bf16_bits_to_f32((uint16_t)(qraw.y & 0xFFFFu)), bf16_bits_to_f32((uint16_t)(qraw.y >> 16))};
+    const float kn[4] = {bf16_bits_to_f32((uint16_t)(nkraw.x & 0xFFFFu)), bf16_bits_to_f32((uint16_t)(nkraw.x >> 16)),
+                         bf16_bits_to_f32((uint16_t)(nkraw.y & 0xFFFFu)), bf16_bits_to_f32((uint16_t)(nkraw.y >> 16))};
+    vnew[0] = bf16_bits_to_f32((uint16_t)(nvraw.x & 0xFFFFu));
+    vnew[1] = bf16_bits_to_f32((uint16_t)(nvraw.x >> 16));
+    vnew[2] = bf16_bits_to_f32((uint16_t)(nvraw.y & 0xFFFFu));
+    vnew[3] = bf16_bits_to_f32((uint16_t)(nvraw.y >> 16));
+    // q' = R q (lane: dims 4 lane .. 4 lane + 3), as the packed items rotate it
+    float qr[4] = {q[0] * sg.x, q[1] * sg.y, q[2] * sg.z, q[3] * sg.w};
+    fwht_wave<4>(qr);
+    // the 2-bit centroids, as the score product's fp16 table holds them
+    constexpr float C2[4] = {-3.74609375f, -TQ2_A16, TQ2_A16, 3.74609375f};
+    float dn = 0.f, de = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      dn = __builtin_fmaf(q[e], kn[e], dn);
+      de = __builtin_fmaf(qr[e] * (1.0f / 16.0f), C2[(kcode >> (2 * e)) & 3u], de);
+      vev[e] = C2[vcode[e] & 3u];
+    }
+    dn = wave_sum(dn);
+    de = wave_sum(de);
+    const float sn = dn * (a.scaling * LOG2E);
+    const float se = de * (f16_bits_to_f32(knorm) * a.key_scale * a.scaling * LOG2E);
+    const float M2 = fmaxf(fmaxf(M, sn), stored ? se : -INFINITY);
+    const float f = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - M2);
+    sp *= f;
+    L *= f;
+    M = M2;
+    wn = __builtin_amdgcn_exp2f(sn - M);
+    we = stored ? __builtin_amdgcn_exp2f(se - M) : 0.f;
+    L += wn + we;
+    const float vs = stored ? f16_bits_to_f32(vnorm) * a.value_scale : 0.f;  // the record is stale otherwise
+#pragma unroll
+    for (int e = 0; e < 4; ++e) vev[e] *= vs;
+  }
   const float wr_w = mlr.y > 0.f ? __builtin_amdgcn_exp2f(mlr.x - M) : 0.f;
   L += mlr.y * wr_w;
   const float invL = L > 0.f ? 1.0f / L : 0.f;
@@ -633,9 +806,18 @@ __global__ __launch_bounds__(64) void tq_merge_kernel(const anna_mi_tq_decode_ar
   float v[4];
   const float4 o4 = *(const float4*)(s_o + 4 * lane);
   v[0] = o4.x, v[1] = o4.y, v[2] = o4.z, v[3] = o4.w;
+  if constexpr (FUSED) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] += vev[e] * (we * invL);
+  }
   fwht_wave<4>(v);
   const float4 w4 = *(const float4*)(s_w + 4 * lane);
-  const float sgv[4] = {sg.x, sg.y, sg.z, sg.w}, wv[4] = {w4.x, w4.y, w4.z, w4.w};
+  const float sgv[4] = {sg.x, sg.y, sg.z, sg.w};
+  float wv[4] = {w4.x, w4.y, w4.z, w4.w};
+  if constexpr (FUSED) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) wv[e] += vnew[e] * (wn * invL);
+  }
   float o[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) o[e] = v[e] * sgv[e] * (1.0f / 16.0f) + wv[e];
@@ -646,6 +828,20 @@ __global__ __launch_bounds__(64) void tq_merge_kernel(const anna_mi_tq_decode_ar
     for (int e = 0; e < 4; ++e) o[e] = o[e] / (1.0f + __expf(-gv[e]));
   }
   *(uint2*)(a.out + orow) = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+  if constexpr (FUSED) {
+    // the new token takes the ring slot the leaving one had; the length grows (no wave of this
+    // launch reads the ring or the lengths)
+    if (n == 0) {
+      const int64_t R = a.residual_capacity, rpos = len0 % R;
+      *(uint2*)(ap.residual_key + (bh * R + rpos) * TD + 4 * lane) = nkraw;
+      uint16_t* col = ap.residual_value_t + bh * TD * R + rpos;
+      col[(4 * lane + 0) * R] = (uint16_t)(nvraw.x & 0xFFFFu);
+      col[(4 * lane + 1) * R] = (uint16_t)(nvraw.x >> 16);
+      col[(4 * lane + 2) * R] = (uint16_t)(nvraw.y & 0xFFFFu);
+      col[(4 * lane + 3) * R] = (uint16_t)(nvraw.y >> 16);
+      if (h == 0 && lane == 0) ap.seq_lengths[b] = len0 + 1;
+    }
+  }
 }
 
 // ------------------------------------------------------------------ append
@@ -654,8 +850,8 @@ __global__ __launch_bounds__(64) void tq_merge_kernel(const anna_mi_tq_decode_ar
 // leaves the ring (when length >= R), all waves then write the new token into the ring slot,
 // thread 0 increments the length.
 __global__ __launch_bounds__(256) void tq_append_kernel(const anna_mi_tq_append_args a) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t b = blockIdx.x, H = a.kv_heads, R = a.residual_capacity, T = a.pool_tokens;
+  const int wave = threadIdx.x >> 6;
+  const int64_t b = blockIdx.x, H = a.kv_heads, R = a.residual_capacity;
   const int n = a.seq_lengths[b];
   const int64_t rpos = n % R;
   if (n >= R) {
@@ -664,41 +860,8 @@ __global__ __launch_bounds__(256) void tq_append_kernel(const anna_mi_tq_append_
     if (!room) {
       if (threadIdx.x == 0 && a.overflow) *a.overflow = 1;
     } else {
-      const int64_t slot = a.seq_offsets[b] + q;
-      for (int64_t vi = wave; vi < 2 * H; vi += 4) {
-        const int64_t h = vi >> 1;
-        const bool is_v = vi & 1;
-        float x[4];
-        if (!is_v) {
-          const uint2 raw = *(const uint2*)(a.residual_key + ((b * H + h) * R + rpos) * TD + 4 * lane);
-          x[0] = bf16_bits_to_f32((uint16_t)(raw.x & 0xFFFFu));
-          x[1] = bf16_bits_to_f32((uint16_t)(raw.x >> 16));
-          x[2] = bf16_bits_to_f32((uint16_t)(raw.y & 0xFFFFu));
-          x[3] = bf16_bits_to_f32((uint16_t)(raw.y >> 16));
-        } else {
-          const uint16_t* col = a.residual_value_t + (b * H + h) * TD * R + rpos;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) x[e] = bf16_bits_to_f32(col[(4 * lane + e) * R]);
-        }
-        uint32_t code[4];
-        const float nrm = hadamard_codes_wave<4>(x, a.signs, a.thresholds, 3, 1.0f / 16.0f, code);
-        const uint16_t nb16 = f32_to_f16_bits(nrm);
-        if (!is_v) {
-          a.key_codes[(h * T + slot) * 64 + lane] =
-              (uint8_t)(code[0] | (code[1] << 2) | (code[2] << 4) | (code[3] << 6));
-          if (lane == 0) a.key_norms[h * T + slot] = nb16;
-        } else {
-          const int64_t t = slot % TBT;
-          uint8_t* blk = a.value_codes + (h * (T / TBT) + slot / TBT) * 2048 + ((t % 16) / 4) * 512 + (t / 16);
-          const int sh = 2 * (int)(t % 4);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            uint8_t* p = blk + (4 * lane + e) * 2;
-            *p = (uint8_t)(sh == 0 ? code[e] : (*p | (code[e] << sh)));
-          }
-          if (lane == 0) a.value_norms[h * T + slot] = nb16;
-        }
-      }
+      for (int64_t vi = wave; vi < 2 * H; vi += 4)
+        evict_token(a, b, vi >> 1, n, a.seq_offsets[b] + q, vi & 1, threadIdx.x & 63);
     }
   }
   __syncthreads();  // the leaving token is read before its slot is overwritten
@@ -823,9 +986,8 @@ extern "C" int64_t anna_mi_tq_decode_workgroups(int64_t batch, int64_t kv_heads,
   return bh + n * kv_heads > automatic ? bh + n * kv_heads : automatic;
 }
 
-extern "C" int anna_mi_tq_decode(const anna_mi_tq_decode_args* ap, void* stream) {
-  ANNA_CHECK(ap != nullptr, "anna_mi_tq_decode: null args");
-  const anna_mi_tq_decode_args& a = *ap;
+namespace {
+int check_decode_args(const anna_mi_tq_decode_args& a) {
   ANNA_CHECK(a.head_dim == TD, "anna_mi_tq_decode: head_dim must be 256");
   ANNA_CHECK(a.key_bits == 2 && a.value_bits == 2, "anna_mi_tq_decode: 2-bit codes only (use anna_mi_gqa_decode_splitkv)");
   ANNA_CHECK(a.batch > 0 && a.batch <= MAX_SEQS, "anna_mi_tq_decode: batch must be in [1, %d]", MAX_SEQS);
@@ -841,16 +1003,10 @@ extern "C" int anna_mi_tq_decode(const anna_mi_tq_decode_args* ap, void* stream)
              "anna_mi_tq_decode: null pointer");
   ANNA_CHECK(a.key_codes && a.key_norms && a.value_codes && a.value_norms && a.residual_key && a.residual_value_t,
              "anna_mi_tq_decode: null cache pointer");
-  hipLaunchKernelGGL(tq_decode_kernel, dim3((unsigned)a.num_workgroups), dim3(64 * SWAVES), 0, as_stream(stream), a);
-  ANNA_LAUNCH_CHECK("tq_decode_kernel");
-  hipLaunchKernelGGL(tq_merge_kernel, dim3((unsigned)(a.q_heads * a.batch)), dim3(64), 0, as_stream(stream), a);
-  ANNA_LAUNCH_CHECK("tq_merge_kernel");
   return ANNA_MI_OK;
 }
 
-extern "C" int anna_mi_tq_append(const anna_mi_tq_append_args* ap, void* stream) {
-  ANNA_CHECK(ap != nullptr, "anna_mi_tq_append: null args");
-  const anna_mi_tq_append_args& a = *ap;
+int check_append_args(const anna_mi_tq_append_args& a) {
   ANNA_CHECK(a.head_dim == TD, "anna_mi_tq_append: head_dim must be 256");
   ANNA_CHECK(a.batch > 0 && a.kv_heads > 0, "anna_mi_tq_append: empty batch or heads");
   ANNA_CHECK(a.pool_tokens % TBT == 0 && a.residual_capacity % TBT == 0 && a.residual_capacity > 0,
@@ -859,6 +1015,51 @@ extern "C" int anna_mi_tq_append(const anna_mi_tq_append_args* ap, void* stream)
                  a.residual_key && a.residual_value_t && a.seq_offsets && a.seq_capacity && a.seq_lengths && a.signs &&
                  a.thresholds,
              "anna_mi_tq_append: null pointer");
+  return ANNA_MI_OK;
+}
+}  // namespace
+
+extern "C" int anna_mi_tq_decode(const anna_mi_tq_decode_args* ap, void* stream) {
+  ANNA_CHECK(ap != nullptr, "anna_mi_tq_decode: null args");
+  const anna_mi_tq_decode_args& a = *ap;
+  if (const int rc = check_decode_args(a)) return rc;
+  const anna_mi_tq_append_args none{};
+  hipLaunchKernelGGL(tq_decode_kernel<false>, dim3((unsigned)a.num_workgroups), dim3(64 * SWAVES), 0, as_stream(stream),
+                     a, none);
+  ANNA_LAUNCH_CHECK("tq_decode_kernel");
+  hipLaunchKernelGGL(tq_merge_kernel<false>, dim3((unsigned)(a.q_heads * a.batch)), dim3(64), 0, as_stream(stream), a,
+                     none);
+  ANNA_LAUNCH_CHECK("tq_merge_kernel");
+  return ANNA_MI_OK;
+}
+
+extern "C" int anna_mi_tq_append_decode(const anna_mi_tq_decode_args* dp, const anna_mi_tq_append_args* app,
+                                        void* stream) {
+  ANNA_CHECK(dp != nullptr && app != nullptr, "anna_mi_tq_append_decode: null args");
+  const anna_mi_tq_decode_args& a = *dp;
+  const anna_mi_tq_append_args& p = *app;
+  if (const int rc = check_decode_args(a)) return rc;
+  if (const int rc = check_append_args(p)) return rc;
+  ANNA_CHECK(p.batch == a.batch && p.kv_heads == a.kv_heads && p.head_dim == a.head_dim &&
+                 p.pool_tokens == a.pool_tokens && p.residual_capacity == a.residual_capacity,
+             "anna_mi_tq_append_decode: the append and decode arguments describe different caches");
+  ANNA_CHECK(p.key_codes == a.key_codes && p.key_norms == a.key_norms && p.value_codes == a.value_codes &&
+                 p.value_norms == a.value_norms && p.residual_key == a.residual_key &&
+                 p.residual_value_t == a.residual_value_t && p.seq_offsets == a.seq_offsets &&
+                 p.seq_lengths == a.seq_lengths && p.signs == a.signs,
+             "anna_mi_tq_append_decode: the append and decode arguments describe different caches");
+  hipLaunchKernelGGL(tq_decode_kernel<true>, dim3((unsigned)a.num_workgroups), dim3(64 * SWAVES), 0, as_stream(stream),
+                     a, p);
+  ANNA_LAUNCH_CHECK("tq_decode_kernel (fused append)");
+  hipLaunchKernelGGL(tq_merge_kernel<true>, dim3((unsigned)(a.q_heads * a.batch)), dim3(64), 0, as_stream(stream), a, p);
+  ANNA_LAUNCH_CHECK("tq_merge_kernel (fused append)");
+  return ANNA_MI_OK;
+}
+
+extern "C" int anna_mi_tq_append(const anna_mi_tq_append_args* ap, void* stream) {
+  ANNA_CHECK(ap != nullptr, "anna_mi_tq_append: null args");
+  const anna_mi_tq_append_args& a = *ap;
+  if (const int rc = check_append_args(a)) return rc;
   hipLaunchKernelGGL(tq_append_kernel, dim3((unsigned)a.batch), dim3(256), 0, as_stream(stream), a);
   ANNA_LAUNCH_CHECK("tq_append_kernel");
   return ANNA_MI_OK;

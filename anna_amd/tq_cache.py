@@ -92,7 +92,7 @@ class TurboQuantBatchCache:
         nwg = self.num_workgroups
         self.partial_stats = torch.empty((nwg, 16, 2), dtype=torch.float32, device=dev)
         self.partial_values = torch.empty((nwg, 16, D), dtype=torch.float32, device=dev)
-        self.item_table = torch.zeros((2 * batch * kv_heads,), dtype=torch.int32, device=dev)
+        self.item_table = torch.zeros((4 * batch * kv_heads,), dtype=torch.int32, device=dev)  # 4 per (b, h): fused step
 
     # ---- lengths
     @property
@@ -140,8 +140,9 @@ class TurboQuantBatchCache:
         _lib.call("anna_mi_tq_pack_kv", ctypes.byref(a), _lib.stream_of(keys))
 
     # ---- decode step
-    def append(self, keys: torch.Tensor, values: torch.Tensor) -> None:
-        """One token per sequence: keys/values bf16 [B, Hkv, D]."""
+    def _append_args(self, keys: torch.Tensor, values: torch.Tensor) -> _lib.TQAppendArgs:
+        """Checks one token per sequence (keys/values bf16 [B, Hkv, D], contiguous) and builds
+        the append arguments."""
         B, H, D = self.batch, self.kv_heads, self.head_dim
         if keys.dtype != torch.bfloat16 or tuple(keys.shape) != (B, H, D) or values.shape != keys.shape:
             raise ValueError("append expects bf16 keys/values of shape [batch, kv_heads, 256]")
@@ -150,7 +151,6 @@ class TurboQuantBatchCache:
         for b, n in enumerate(self.lengths):
             if n >= R and n - R >= self.capacities[b]:
                 raise RuntimeError(f"sequence {b} is full: {self.capacities[b]} pool slots + {R} window tokens")
-        keys, values = keys.contiguous(), values.contiguous()
         a = _lib.TQAppendArgs()
         a.batch, a.kv_heads, a.head_dim = B, H, D
         a.new_key, a.new_value = keys.data_ptr(), values.data_ptr()
@@ -162,6 +162,12 @@ class TurboQuantBatchCache:
         a.seq_offsets, a.seq_capacity = self.seq_offsets.data_ptr(), self.seq_capacity.data_ptr()
         a.seq_lengths, a.overflow = self.seq_lengths.data_ptr(), self.overflow.data_ptr()
         a.signs, a.thresholds = self.qn.signs.data_ptr(), self.qn.thresholds.data_ptr()
+        return a
+
+    def append(self, keys: torch.Tensor, values: torch.Tensor) -> None:
+        """One token per sequence: keys/values bf16 [B, Hkv, D]."""
+        keys, values = keys.contiguous(), values.contiguous()
+        a = self._append_args(keys, values)
         _lib.call("anna_mi_tq_append", ctypes.byref(a), _lib.stream_of(keys))
         self.lengths = [n + 1 for n in self.lengths]
 
@@ -187,22 +193,40 @@ class TurboQuantBatchCache:
         a.out = out.data_ptr()
         return a
 
-    def decode(self, query: torch.Tensor, *, scaling: float, out: torch.Tensor | None = None,
-               gate: torch.Tensor | None = None) -> torch.Tensor:
-        """query bf16 [B, Hq, D] -> attention output bf16 [B, Hq, D]; gate (optional, bf16, same
-        shape as query): out *= sigmoid(gate) (the reference's gated decode, sycl:1605-1669)."""
+    def _check_query(self, query: torch.Tensor, gate: torch.Tensor | None) -> torch.Tensor:
         shape = (self.batch, self.q_heads, self.head_dim)
         if query.dtype != torch.bfloat16 or tuple(query.shape) != shape:
             raise ValueError("query must be bf16 [batch, q_heads, 256]")
         if gate is not None and (gate.dtype != torch.bfloat16 or tuple(gate.shape) != shape):
             raise ValueError("gate must be bf16 [batch, q_heads, 256] (the query's shape)")
         _lib.require_device(query, gate)
-        query = query.contiguous()
+        return query.contiguous()
+
+    def decode(self, query: torch.Tensor, *, scaling: float, out: torch.Tensor | None = None,
+               gate: torch.Tensor | None = None) -> torch.Tensor:
+        """query bf16 [B, Hq, D] -> attention output bf16 [B, Hq, D]; gate (optional, bf16, same
+        shape as query): out *= sigmoid(gate) (the reference's gated decode, sycl:1605-1669)."""
+        query = self._check_query(query, gate)
         gate = None if gate is None else gate.contiguous()
         if out is None:
             out = torch.empty_like(query)
         a = self.decode_args(query, out, scaling, gate)
         _lib.call("anna_mi_tq_decode", ctypes.byref(a), _lib.stream_of(query))
+        return out
+
+    def append_decode(self, keys: torch.Tensor, values: torch.Tensor, query: torch.Tensor, *, scaling: float,
+                      out: torch.Tensor | None = None, gate: torch.Tensor | None = None) -> torch.Tensor:
+        """One decode step in the decode's two launches: append(keys, values) then
+        decode(query), same results and cache state, without the append's own launch."""
+        query = self._check_query(query, gate)
+        gate = None if gate is None else gate.contiguous()
+        keys, values = keys.contiguous(), values.contiguous()
+        ap = self._append_args(keys, values)
+        if out is None:
+            out = torch.empty_like(query)
+        a = self.decode_args(query, out, scaling, gate)
+        _lib.call("anna_mi_tq_append_decode", ctypes.byref(a), ctypes.byref(ap), _lib.stream_of(query))
+        self.lengths = [n + 1 for n in self.lengths]
         return out
 
     def bytes_per_decode(self) -> int:
@@ -342,6 +366,21 @@ class TurboQuantRowsCache(TurboQuantBatchCache):
             args.partial_values = _lib.view(self.partial_values)
             args.partial_capacity = nblk
         fused_ops.run_decode(args, query)
+        return out
+
+    def append_decode(self, keys: torch.Tensor, values: torch.Tensor, query: torch.Tensor, *, scaling: float,
+                      out: torch.Tensor | None = None, gate: torch.Tensor | None = None) -> torch.Tensor:
+        """One decode step in the decode's two launches: append(keys, values) then
+        decode(query), same results and cache state, without the append's own launch."""
+        query = self._check_query(query, gate)
+        gate = None if gate is None else gate.contiguous()
+        keys, values = keys.contiguous(), values.contiguous()
+        ap = self._append_args(keys, values)
+        if out is None:
+            out = torch.empty_like(query)
+        a = self.decode_args(query, out, scaling, gate)
+        _lib.call("anna_mi_tq_append_decode", ctypes.byref(a), ctypes.byref(ap), _lib.stream_of(query))
+        self.lengths = [n + 1 for n in self.lengths]
         return out
 
     def bytes_per_decode(self) -> int:

@@ -250,6 +250,15 @@ def section_tq_decode(args, device):
     ms_step = time_graph([step], steps, 0)
     r["append_decode_step_us"] = ms_step * 1e3
     log(f"tq append+decode step: {ms_step * 1e3:.2f} us")
+    # the same step with the append inside the decode's two launches (anna_mi_tq_append_decode)
+    fused = TurboQuantBatchCache(batch=B, kv_heads=HKV, q_heads=HQ,
+                                 capacities=[n + (REPLAYS + 3) * steps + 8 for n in lens],
+                                 residual_capacity=R, device=device)
+    for b in range(B):
+        fused.load_sequence(b, dense[b][0], dense[b][1])
+    ms_fused = time_graph([lambda: fused.append_decode(nk, nv, q, scaling=1.0 / 16, out=out)], steps, 0)
+    r["fused_append_decode_step_us"] = ms_fused * 1e3
+    log(f"tq fused append+decode step: {ms_fused * 1e3:.2f} us")
     cpu = None
     if not args.no_cpu:
         from oracle.cpu_paths import tq_decode_rows

@@ -261,7 +261,8 @@ typedef struct {
   int64_t num_workgroups;           /* grid size, from anna_mi_tq_decode_workgroups */
   float* partial_stats;             /* workspace [num_workgroups][16][2] */
   float* partial_values;            /* workspace, sized as float [num_workgroups][16][D] (internal layout) */
-  int32_t* item_table;              /* workspace [2*B*Hkv] int32 (the split tells the merge its items) */
+  int32_t* item_table;              /* workspace [2*B*Hkv] int32, [4*B*Hkv] for anna_mi_tq_append_decode
+                                       (the split tells the merge its items) */
   uint16_t* out;                    /* bf16 [B][Hq][D] */
 } anna_mi_tq_decode_args;
 
@@ -304,6 +305,20 @@ typedef struct {
  * blocked layout + norm, bit-exact with anna_mi_tq_hadamard_quantize), the new token takes its
  * ring slot, and seq_lengths[b] grows by one. */
 int anna_mi_tq_append(const anna_mi_tq_append_args* args, void* stream);
+
+/* One decode step in two launches: the append above and the decode of anna_mi_tq_decode, with
+ * the same results and the same cache state afterwards (pool codes, ring, lengths, overflow) as
+ * anna_mi_tq_append followed by anna_mi_tq_decode, without the append's launch.  The split
+ * launch plans on the lengths before the append; the window workgroup of each (b, kv head)
+ * quantizes the token leaving its ring into the pool slot just past the planned items and
+ * leaves that slot out of its window; the merge launch scores the leaving token (from its codes)
+ * and the new one itself, then writes the new token into the ring and the new length.  Both
+ * argument blocks must describe the one cache (checked); args->item_table holds 4 * batch *
+ * kv_heads entries.  Replaces the pair of calls the reference makes per step and layer,
+ * Qwen3DynamicCache._update_turboquant_layer (ops.py:618-661) and the decode (ops.py:1055-1071);
+ * no single reference function does both. */
+int anna_mi_tq_append_decode(const anna_mi_tq_decode_args* args, const anna_mi_tq_append_args* append,
+                             void* stream);
 
 /* The general batched cache (one region per sequence and KV head; any power-of-two head_dim in
  * [64, 1024], key bits 1..4, value bits 2..4): one token per sequence, the form of

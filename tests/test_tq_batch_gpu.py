@@ -228,6 +228,85 @@ def test_append_decode_graph_replays_match_eager(gpu):
         assert torch.equal(graph_cache.value_codes, eager_cache.value_codes)
 
 
+@pytest.mark.parametrize("gated", [False, True])
+def test_fused_append_decode_matches_two_calls_and_oracle(gpu, gated):
+    """anna_mi_tq_append_decode (the step's append inside the decode's two launches) against
+    append + decode on a twin cache, 40 steps from prefilled lengths 0 / 10 / 40 / 100 with a
+    32-token window: the caches stay equal bit for bit (pool codes and norms, ring, lengths),
+    the outputs agree (the two tokens the merge scores itself are the only difference in
+    arithmetic), and after 1, 10, 25 and 40 steps the fused output matches the oracle."""
+    print(f"[case] tq batch fused append+decode gate={gated}", flush=True)
+    torch.manual_seed(19 + gated)
+    B, HKV, G, D, R = 4, 2, 8, 256, 32
+    pre = [0, 10, 40, 100]
+    caches = [TurboQuantBatchCache(batch=B, kv_heads=HKV, q_heads=HKV * G, capacities=[64, 64, 64, 128],
+                                   residual_capacity=R, device=gpu) for _ in range(2)]
+    hist_k = [torch.randn(HKV, n, D, device=gpu).to(torch.bfloat16) for n in pre]
+    hist_v = [torch.randn(HKV, n, D, device=gpu).to(torch.bfloat16) for n in pre]
+    for c in caches:
+        for b in range(B):
+            c.load_sequence(b, hist_k[b], hist_v[b])
+    fused, split = caches
+    for step in range(1, 41):
+        nk = torch.randn(B, HKV, D, device=gpu).to(torch.bfloat16)
+        nv = torch.randn(B, HKV, D, device=gpu).to(torch.bfloat16)
+        q = torch.randn(B, HKV * G, D, device=gpu).to(torch.bfloat16)
+        gate = torch.randn(B, HKV * G, D, device=gpu).to(torch.bfloat16) if gated else None
+        out_f = fused.append_decode(nk, nv, q, scaling=1.0 / 16, gate=gate)
+        split.append(nk, nv)
+        out_s = split.decode(q, scaling=1.0 / 16, gate=gate)
+        hist_k = [torch.cat([hist_k[b], nk[b, :, None]], 1) for b in range(B)]
+        hist_v = [torch.cat([hist_v[b], nv[b, :, None]], 1) for b in range(B)]
+        for name in ("key_codes", "key_norms", "value_codes", "value_norms", "residual_key", "residual_value_t",
+                     "seq_lengths"):
+            assert torch.equal(getattr(fused, name), getattr(split, name)), (step, name)
+        assert fused.lengths == split.lengths
+        assert rel_err(out_f.float().cpu().numpy(), out_s.float().cpu().numpy().astype(np.float64)) <= BF16_TOL, step
+        if step in (1, 10, 25, 40):
+            check_against_oracle(fused, hist_k, hist_v, q, out_f, gate=gate, seed=step)
+    assert int(fused.overflow.item()) == 0
+
+
+def test_fused_append_decode_graph_replays_match_eager(gpu):
+    """The fused step captured once and replayed 5 times, with eager work in between, gives the
+    same bits as the same fused steps run eagerly on a twin cache."""
+    print("[case] tq batch fused graph replay", flush=True)
+    torch.manual_seed(23)
+    B, HKV, G, D, R = 3, 2, 8, 256, 32
+    pre = [0, 31, 70]
+    caches = [TurboQuantBatchCache(batch=B, kv_heads=HKV, q_heads=HKV * G, capacities=[64] * B,
+                                   residual_capacity=R, device=gpu) for _ in range(2)]
+    for b in range(B):
+        k = torch.randn(HKV, pre[b], D, device=gpu).to(torch.bfloat16)
+        v = torch.randn(HKV, pre[b], D, device=gpu).to(torch.bfloat16)
+        for c in caches:
+            c.load_sequence(b, k, v)
+    nk = torch.empty(B, HKV, D, device=gpu, dtype=torch.bfloat16)
+    nv = torch.empty_like(nk)
+    q = torch.empty(B, HKV * G, D, device=gpu, dtype=torch.bfloat16)
+    out_g = torch.empty_like(q)
+    graph_cache, eager_cache = caches
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        graph_cache.append_decode(nk, nv, q, scaling=1.0 / 16, out=out_g)
+    graph_cache.lengths = list(pre)  # capture ran no kernel: the host mirror rolls back
+    for step in range(5):
+        nk.copy_(torch.randn(B, HKV, D, device=gpu).to(torch.bfloat16))
+        nv.copy_(torch.randn(B, HKV, D, device=gpu).to(torch.bfloat16))
+        q.copy_(torch.randn(B, HKV * G, D, device=gpu).to(torch.bfloat16))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        graph_cache.lengths = [n + 1 for n in graph_cache.lengths]
+        ref = eager_cache.append_decode(nk, nv, q, scaling=1.0 / 16)
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, ref), step
+        for name in ("seq_lengths", "key_codes", "value_codes", "residual_key", "residual_value_t"):
+            assert torch.equal(getattr(graph_cache, name), getattr(eager_cache, name)), (step, name)
+
+
 def test_append_refuses_a_full_sequence(gpu):
     cache = TurboQuantBatchCache(batch=1, kv_heads=1, q_heads=8, capacities=[32], residual_capacity=32, device=gpu)
     k = torch.randn(1, 64, 256, device=gpu).to(torch.bfloat16)
