@@ -1,4 +1,5 @@
-// Shared int4 -> MFMA fragment helpers (W4A16 kernels of int4_linear.hip and moe.hip).
+// Shared int4 -> MFMA / dot2 fragment helpers (W4A16 kernels of int4_linear.hip, lm_head.hip
+// and moe.hip).
 #pragma once
 
 #include "common.hpp"
@@ -32,6 +33,18 @@ __device__ __forceinline__ u32x4 interleave_x(u32x4 v) {
   r.z = __builtin_amdgcn_perm(v.w, v.y, 0x05040100u);
   r.w = __builtin_amdgcn_perm(v.w, v.y, 0x07060302u);
   return r;
+}
+
+// c + a.lo * b.lo + a.hi * b.hi over two packed 16-bit values (bf16 or f16), fp32 accumulation.
+template <int XDT>
+__device__ __forceinline__ float dot2_acc(uint32_t a, uint32_t b, float c) {
+  if constexpr (XDT == ANNA_MI_BF16) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+  } else {
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);
+  }
 }
 
 template <int XDT>

@@ -238,16 +238,6 @@ __global__ __launch_bounds__(64 * KW) void int4_gemv_mfma(
 // and scale are applied as s * (acc - (128 + z) * sum(x)).  Lanes of a row and the waves of
 // the workgroup are reduced at the end.
 
-template <int XDT>
-__device__ __forceinline__ float dot2_acc(uint32_t a, uint32_t b, float c) {
-  if constexpr (XDT == ANNA_MI_BF16) {
-    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
-  } else {
-    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);
-  }
-}
 
 template <int XDT>
 __device__ __forceinline__ float sum8_16bit(u32x4 v) {

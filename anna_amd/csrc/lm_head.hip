@@ -19,6 +19,7 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "int4_frag.hpp"
 
 namespace anna {
 namespace {
@@ -96,25 +97,28 @@ __global__ __launch_bounds__(256) void int4_gemv_tiled_kernel(
             D.x[m] = *(const u32x4*)((const uint16_t*)x + mr * xs + w * 8);
           }
         };
+        // Nibble pairs become 16-bit "off + q" values with one AND-OR (exact), dot2 accumulates them
+        // in fp32 against x reordered to the same pairs, and the zero point comes off once per
+        // word and row: s * (sum x (off + q) - (off + z) sum x).
+        constexpr float OFF = XDT == ANNA_MI_BF16 ? 128.0f : 1024.0f;
+        constexpr uint32_t ONES = XDT == ANNA_MI_BF16 ? 0x3F803F80u : 0x3C003C00u;
         auto compute = [&](const Word& D) {
 #pragma unroll
           for (int m = 0; m < TG_MR; ++m) {
             if (m0 + m >= M) continue;
-            float xv[8];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              xv[2 * e] = Elem<XDT>::to_f32((uint16_t)(D.x[m][e] & 0xFFFFu));
-              xv[2 * e + 1] = Elem<XDT>::to_f32((uint16_t)(D.x[m][e] >> 16));
-            }
-            float sx = 0.f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) sx += xv[e];
+            const u32x4 xi = interleave_x(D.x[m]);
+            float sx = dot2_acc<XDT>(xi.x, ONES, 0.f);
+            sx = dot2_acc<XDT>(xi.y, ONES, sx);
+            sx = dot2_acc<XDT>(xi.z, ONES, sx);
+            sx = dot2_acc<XDT>(xi.w, ONES, sx);
 #pragma unroll
             for (int t = 0; t < T; ++t) {
-              float d = 0.f;
-#pragma unroll
-              for (int e = 0; e < 8; ++e) d = fmaf(xv[e], (float)((D.q.v[t] >> (4 * e)) & 0xFu), d);
-              acc[m][t] = fmaf(Elem<SDT>::to_f32(D.s[t]), d - (float)D.z[t] * sx, acc[m][t]);
+              const u32x4 f = nibbles_to_frag<XDT>(D.q.v[t]);
+              float d = dot2_acc<XDT>(xi.x, f.x, 0.f);
+              d = dot2_acc<XDT>(xi.y, f.y, d);
+              d = dot2_acc<XDT>(xi.z, f.z, d);
+              d = dot2_acc<XDT>(xi.w, f.w, d);
+              acc[m][t] = fmaf(Elem<SDT>::to_f32(D.s[t]), d - (OFF + (float)D.z[t]) * sx, acc[m][t]);
             }
           }
         };

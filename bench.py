@@ -485,6 +485,36 @@ def section_moe(args, device):
     return out
 
 
+def section_lm_head(args, device):
+    """The fused int4 LM-head top-k (not a BASELINE config): one token's hidden
+    state [1, 2048] against a 151936-row int4 head (group 128) in the reference's top-k layout,
+    top 8.  Two weight copies (2 x 163 MB) alternate, more than the Infinity Cache."""
+    from anna_amd import fused_ops
+    from anna_amd.quantization import XPUInt4Linear
+
+    K, V, TOPK = 2048, 151936, 8
+    torch.manual_seed(31)
+    dense = torch.nn.Linear(K, V, bias=False, dtype=torch.float32, device=device)
+    q = XPUInt4Linear.from_linear(dense, group_size=128, compute_dtype=torch.bfloat16, device=device)
+    del dense
+    q.prepare_lm_head_topk_layout()
+    base = (q.lm_head_qweight, q.lm_head_qscale, q.lm_head_qzeros)
+    copies = [base, tuple(t.clone() for t in base)]
+    x = torch.randn((1, K), device=device).to(torch.bfloat16)
+    fused_ops.register_ops()
+    fns = [(lambda c=c: torch.ops.anna.lm_head_int4_topk_fused(x, *c, 128, K, TOPK)) for c in copies]
+    ms = time_graph(fns, args.steps, args.warmup)
+    wbytes = V * K // 2 + V * (K // 128) * 3
+    byts = wbytes + K * 2 + V * 4 * 2  # weights, x, fp32 logits written and read by the top-k
+    r = {"K": K, "V": V, "top_k": TOPK, "us": ms * 1e3, "bytes": byts, "GB/s": byts / ms / 1e6,
+         "roofline_frac": byts / ms / 1e6 / HBM_PEAK_GBS, "distinct_weight_copies": len(copies)}
+    log(f"lm_head top-{TOPK} V={V} K={K}: {r['us']:.1f} us  {r['GB/s']:.0f} GB/s  "
+        f"{100 * r['roofline_frac']:.1f}% of HBM peak")
+    del copies, q, base
+    torch.cuda.empty_cache()
+    return r
+
+
 def calibrate_copy(device, steps: int = 5) -> dict:
     """A plain elementwise kernel of known traffic (reads and writes COPY_BYTES each), run so
     that a counter collection run can scale FETCH_SIZE / WRITE_SIZE to bytes."""
@@ -518,7 +548,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=60)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--sections", default="int4,tq_decode,row_decode,tq_pack,moe")
+    ap.add_argument("--sections", default="int4,tq_decode,row_decode,tq_pack,moe,lm_head")
     ap.add_argument("--tq-tokens-per-item", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -553,6 +583,8 @@ def main() -> int:
         sections["tq_pack"] = section_tq_pack(args, device)
     if "moe" in wanted:
         sections["moe"] = section_moe(args, device)
+    if "lm_head" in wanted:
+        sections["lm_head"] = section_lm_head(args, device)
     if "int4_sweep" not in sections:
         print(json.dumps({"sections": sections}))
         return 0
