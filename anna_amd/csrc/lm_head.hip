@@ -233,14 +233,18 @@ inline int tk_threads(int kt) { return TK_LDS / (kt * 8) < 1024 ? TK_LDS / (kt *
 //          bitonic A ++ reverse(B)) and sorts that half with a bitonic network, in registers.
 // The earlier form (lists in LDS, a two-pointer merge) spent its time in chains of dependent
 // LDS reads: 24 us at V = 31, 240 us at V = 151936.
+// Chunked form (gridDim.x > 1, few rows): workgroup c takes elements [c S, c S + S) of its row
+// and writes its sorted top KT back over the first 2 KT floats of that range (values, then the
+// indices' bits; the range has been read by then), for topk_merge_chunks_kernel.
 template <int ODT, int KT>
-__global__ __launch_bounds__(1024) void topk_rows_kernel(const float* __restrict__ logits, int64_t V, int64_t ld,
-                                                         int k, typename Elem<ODT>::T* __restrict__ out_v,
-                                                         int64_t* __restrict__ out_i) {
+__global__ __launch_bounds__(1024) void topk_rows_kernel(float* __restrict__ logits, int64_t V, int64_t ld, int k,
+                                                         typename Elem<ODT>::T* __restrict__ out_v,
+                                                         int64_t* __restrict__ out_i, int64_t S) {
   extern __shared__ float tk_lists[];  // values [nt][KT], then indices [nt][KT]
   const int nt = blockDim.x, tid = threadIdx.x;
-  const int64_t row = blockIdx.x;
-  const float* lg = logits + row * ld;
+  const int64_t row = blockIdx.y;
+  float* const lg = logits + row * ld;
+  const int64_t lo = (int64_t)blockIdx.x * S, hi = lo + S < V ? lo + S : V;
   float* lv = tk_lists;
   int32_t* li = (int32_t*)(tk_lists + nt * KT);
   float rv[KT];
@@ -280,18 +284,18 @@ __global__ __launch_bounds__(1024) void topk_rows_kernel(const float* __restrict
   // lists rarely change (a wave whose lanes insert often walks the insertion for all of them)
   float mxv = -INFINITY;
   int32_t mxi = INT32_MAX;
-  for (int64_t n0 = tid; n0 < V; n0 += (int64_t)TK_BATCH * nt) {
+  for (int64_t n0 = lo + tid; n0 < hi; n0 += (int64_t)TK_BATCH * nt) {
     float v[TK_BATCH];
 #pragma unroll
     for (int b = 0; b < TK_BATCH; ++b) {
       const int64_t n = n0 + (int64_t)b * nt;
-      v[b] = lg[n < V ? n : 0];
+      v[b] = lg[n < hi ? n : lo];
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int b = 0; b < TK_BATCH; ++b) {
       const int64_t n = n0 + (int64_t)b * nt;
-      if (n < V && tk_better(v[b], (int32_t)n, mxv, mxi)) mxv = v[b], mxi = (int32_t)n;
+      if (n < hi && tk_better(v[b], (int32_t)n, mxv, mxi)) mxv = v[b], mxi = (int32_t)n;
     }
   }
   clear();
@@ -303,18 +307,18 @@ __global__ __launch_bounds__(1024) void topk_rows_kernel(const float* __restrict
   // pass 2: each thread keeps the KT best of its share that are not worse than the bound,
   // sorted in registers (a new entry replaces the last and bubbles up)
   clear();
-  for (int64_t n0 = tid; n0 < V; n0 += (int64_t)TK_BATCH * nt) {
+  for (int64_t n0 = lo + tid; n0 < hi; n0 += (int64_t)TK_BATCH * nt) {
     float v[TK_BATCH];
 #pragma unroll
     for (int b = 0; b < TK_BATCH; ++b) {
       const int64_t n = n0 + (int64_t)b * nt;
-      v[b] = lg[n < V ? n : 0];
+      v[b] = lg[n < hi ? n : lo];
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int b = 0; b < TK_BATCH; ++b) {
       const int64_t n = n0 + (int64_t)b * nt;
-      if (n >= V || tk_better(tau_v, tau_i, v[b], (int32_t)n) || !tk_better(v[b], (int32_t)n, rv[KT - 1], ri[KT - 1]))
+      if (n >= hi || tk_better(tau_v, tau_i, v[b], (int32_t)n) || !tk_better(v[b], (int32_t)n, rv[KT - 1], ri[KT - 1]))
         continue;
       rv[KT - 1] = v[b], ri[KT - 1] = (int32_t)n;
 #pragma unroll
@@ -322,7 +326,61 @@ __global__ __launch_bounds__(1024) void topk_rows_kernel(const float* __restrict
     }
   }
   merge_tree();
-  if (tid < k) {  // the merged list is thread 0's
+  if (gridDim.x > 1) {  // the chunk's list over the start of the chunk (every read of it is done)
+    if (tid < KT) {
+      lg[lo + tid] = lv[tid];
+      lg[lo + KT + tid] = __int_as_float(li[tid]);
+    }
+  } else if (tid < k) {  // the merged list is thread 0's
+    out_v[row * k + tid] = Elem<ODT>::cvt(lv[tid]);
+    out_i[row * k + tid] = li[tid];
+  }
+}
+
+// grid (rows), a power of two >= max(C, 64) threads: the C chunk lists of topk_rows_kernel's chunked
+// form, merged by the same tree.
+template <int ODT, int KT>
+__global__ __launch_bounds__(1024) void topk_merge_chunks_kernel(const float* __restrict__ logits, int64_t ld,
+                                                                 int64_t C, int64_t S, int k,
+                                                                 typename Elem<ODT>::T* __restrict__ out_v,
+                                                                 int64_t* __restrict__ out_i) {
+  extern __shared__ float tk_lists[];
+  const int nt = blockDim.x, tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const float* lg = logits + row * ld;
+  float* lv = tk_lists;
+  int32_t* li = (int32_t*)(tk_lists + nt * KT);
+  float rv[KT];
+  int32_t ri[KT];
+#pragma unroll
+  for (int j = 0; j < KT; ++j) {
+    rv[j] = tid < C ? lg[tid * S + j] : -INFINITY;
+    ri[j] = tid < C ? __float_as_int(lg[tid * S + KT + j]) : INT32_MAX;
+  }
+#pragma unroll
+  for (int j = 0; j < KT; ++j) lv[tid * KT + j] = rv[j], li[tid * KT + j] = ri[j];
+  __syncthreads();
+  for (int half = nt / 2; half >= 1; half >>= 1) {
+    if (tid < half) {
+      float bv[KT];
+      int32_t bi[KT];
+#pragma unroll
+      for (int j = 0; j < KT; ++j) bv[j] = lv[(tid + half) * KT + j], bi[j] = li[(tid + half) * KT + j];
+#pragma unroll
+      for (int j = 0; j < KT; ++j) {
+        if (tk_better(bv[KT - 1 - j], bi[KT - 1 - j], rv[j], ri[j])) rv[j] = bv[KT - 1 - j], ri[j] = bi[KT - 1 - j];
+      }
+#pragma unroll
+      for (int s = KT / 2; s >= 1; s >>= 1)
+#pragma unroll
+        for (int j = 0; j < KT; ++j)
+          if ((j & s) == 0) tk_ce(rv[j], ri[j], rv[j + s], ri[j + s]);
+#pragma unroll
+      for (int j = 0; j < KT; ++j) lv[tid * KT + j] = rv[j], li[tid * KT + j] = ri[j];
+    }
+    __syncthreads();
+  }
+  if (tid < k) {
     out_v[row * k + tid] = Elem<ODT>::cvt(lv[tid]);
     out_i[row * k + tid] = li[tid];
   }
@@ -484,17 +542,38 @@ extern "C" int anna_mi_int4_gemv_tiled(const void* x, int x_dtype, int64_t M, in
   return ANNA_MI_OK;
 }
 
-extern "C" int anna_mi_topk_rows(const float* values, int64_t rows, int64_t V, int64_t ld, int64_t top_k,
-                                 void* out_values, int out_dtype, int64_t* out_indices, void* stream) {
+namespace anna {
+namespace {
+// scratch_ok: values may be overwritten (the LM head's own logits), which lets few long rows
+// split over several workgroups
+int topk_rows(const float* values, int64_t rows, int64_t V, int64_t ld, int64_t top_k, void* out_values, int out_dtype,
+              int64_t* out_indices, void* stream, bool scratch_ok) {
   ANNA_CHECK(values && out_values && out_indices, "anna_mi_topk_rows: null pointer");
   ANNA_CHECK(top_k >= 1 && top_k <= TK_MAX && top_k <= V, "top_k must be in [1, min(vocab_size, 32)]");
   ANNA_CHECK(rows >= 0 && ld >= V && V < INT32_MAX, "anna_mi_topk_rows: bad shape");
   if (rows == 0) return ANNA_MI_OK;
   ANNA_DISPATCH_DTYPE(out_dtype, ODT, {
     if (top_k <= 8) {
-      const int nt = tk_threads(8);
-      hipLaunchKernelGGL((topk_rows_kernel<ODT, 8>), dim3((unsigned)rows), dim3((unsigned)nt), (size_t)nt * 8 * 8,
-                         as_stream(stream), values, V, ld, (int)top_k, (typename Elem<ODT>::T*)out_values, out_indices);
+      // few long rows: each row is split over C workgroups whose lists a second launch merges
+      // (one workgroup per row of V = 151936 took ~50 us, a chain of dependent passes)
+      const int64_t C = scratch_ok && rows <= 16 && V >= 8192 ? (V / 2048 < 128 ? V / 2048 : 128) : 1;
+      if (C > 1) {
+        const int64_t S = (V + C - 1) / C;  // >= 2048 > 2 KT
+        const int nt = 256;
+        hipLaunchKernelGGL((topk_rows_kernel<ODT, 8>), dim3((unsigned)C, (unsigned)rows), dim3(nt), (size_t)nt * 8 * 8,
+                           as_stream(stream), const_cast<float*>(values), V, ld, (int)top_k,
+                           (typename Elem<ODT>::T*)out_values, out_indices, S);
+        int mt = 64;  // a power of two >= C, and >= k: thread j writes output j
+        while (mt < C) mt <<= 1;
+        hipLaunchKernelGGL((topk_merge_chunks_kernel<ODT, 8>), dim3((unsigned)rows), dim3((unsigned)mt),
+                           (size_t)mt * 8 * 8, as_stream(stream), values, ld, C, S, (int)top_k,
+                           (typename Elem<ODT>::T*)out_values, out_indices);
+      } else {
+        const int nt = tk_threads(8);
+        hipLaunchKernelGGL((topk_rows_kernel<ODT, 8>), dim3(1u, (unsigned)rows), dim3((unsigned)nt), (size_t)nt * 8 * 8,
+                           as_stream(stream), const_cast<float*>(values), V, ld, (int)top_k,
+                           (typename Elem<ODT>::T*)out_values, out_indices, V);
+      }
     } else {
       int nt = 1024;
       while (nt > 64 && (int64_t)nt * top_k * 8 > TK_LDS) nt >>= 1;
@@ -504,6 +583,13 @@ extern "C" int anna_mi_topk_rows(const float* values, int64_t rows, int64_t V, i
   });
   ANNA_LAUNCH_CHECK("topk_rows_kernel");
   return ANNA_MI_OK;
+}
+}  // namespace
+}  // namespace anna
+
+extern "C" int anna_mi_topk_rows(const float* values, int64_t rows, int64_t V, int64_t ld, int64_t top_k,
+                                 void* out_values, int out_dtype, int64_t* out_indices, void* stream) {
+  return topk_rows(values, rows, V, ld, top_k, out_values, out_dtype, out_indices, stream, false);
 }
 
 extern "C" int anna_mi_lm_head_int4_topk(const void* x, int x_dtype, int64_t rows, int64_t K, int64_t x_row_stride,
@@ -517,5 +603,5 @@ extern "C" int anna_mi_lm_head_int4_topk(const void* x, int x_dtype, int64_t row
                                    scale_dtype, qzeros, group_count, scale_stride_group, scale_stride_row, group_size,
                                    vocab, logits, 1, vocab, stream);
   if (rc != ANNA_MI_OK) return rc;
-  return anna_mi_topk_rows(logits, rows, vocab, vocab, top_k, values, x_dtype, indices, stream);
+  return topk_rows(logits, rows, vocab, vocab, top_k, values, x_dtype, indices, stream, true);
 }

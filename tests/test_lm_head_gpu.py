@@ -25,7 +25,9 @@ def dense_logits(q, x):
 
 
 @pytest.mark.parametrize("k,n,seed,layout", [(16, 31, 0, "plain"), (64, 96, 8, "lm_head"), (96, 192, 5, "plain"),
-                                             (2048, 1000, 3, "lm_head")])
+                                             (2048, 1000, 3, "lm_head"),
+                                             (128, 20000, 4, "lm_head"),    # rows split over chunks (V >= 8192)
+                                             (64, 8193, 6, "plain")])
 def test_lm_head_int4_topk_matches_quantized_reference(gpu, k, n, seed, layout):
     q = quantized_linear(k, n, seed, gpu)
     x = torch.randn(2, 3, k, device=gpu, dtype=torch.float16)
