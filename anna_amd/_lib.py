@@ -114,6 +114,11 @@ PROTOTYPES.update({
     "anna_mi_tq_mse_dequant": [_P, _P, _I64, _I64, _P, _P, _I, _P, _I, _I64, _P],
     "anna_mi_tq_values_quantize": [_P, _I, _I64, _I64, _I64, _I64, _I64, _I, _I64, _P, _P, _P, _P],
     "anna_mi_tq_values_dequant": [_P, _P, _P, _I, _I64, _I64, _I, _I64, _P, _I, _P],
+    "anna_mi_tq_ip_gaussian": [_I64, ctypes.c_uint64, _P],
+    "anna_mi_tq_ip_quantize": [_P, _I, _I64, _I64, _I64, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P],
+    "anna_mi_tq_ip_dequant": [_P, _P, _P, _P, _I64, _I64, _P, _P, _P, _I, _P, _I, _I64, _P],
+    "anna_mi_tq_ip_scores": [_P, _I, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _I64, _P, _P, _P, _I,
+                             _F, _P, _P, _P],
     "anna_mi_gqa_decode_splitkv": [ctypes.POINTER(DecodeArgs), _P],
     "anna_mi_gqa_decode_splitkv_noalloc": [ctypes.POINTER(DecodeArgs), _P],
 })

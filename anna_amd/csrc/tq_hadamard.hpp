@@ -34,6 +34,20 @@ inline void tq_hadamard_signs(int64_t D, uint64_t seed, float* out) {
   }
 }
 
+// n standard-normal values from the splitmix64 stream of `seed` by Box-Muller in fp64: each
+// pair (u1, u2) of 53-bit uniforms in (0, 1) gives r cos(2 pi u2), r sin(2 pi u2) with
+// r = sqrt(-2 ln u1).
+inline void tq_gaussian(int64_t n, uint64_t seed, double* g) {
+  uint64_t s = seed;
+  for (int64_t i = 0; i < n; i += 2) {
+    double u1 = ((double)(tq_splitmix64(s) >> 11) + 0.5) * (1.0 / 9007199254740992.0);
+    double u2 = ((double)(tq_splitmix64(s) >> 11) + 0.5) * (1.0 / 9007199254740992.0);
+    double r = __builtin_sqrt(-2.0 * __builtin_log(u1));
+    g[i] = r * __builtin_cos(6.283185307179586 * u2);
+    if (i + 1 < n) g[i + 1] = r * __builtin_sin(6.283185307179586 * u2);
+  }
+}
+
 __host__ __device__ constexpr bool tq_is_pow2(int64_t d) { return d > 0 && (d & (d - 1)) == 0; }
 
 // fp32(1/sqrt(D)) (exact for D a power of 4)

@@ -48,14 +48,7 @@ void make_rotation(int64_t D, uint64_t seed, float* out) {
     return;
   }
   std::vector<double> g((size_t)(D * D));
-  uint64_t s = seed;
-  for (int64_t i = 0; i < D * D; i += 2) {
-    double u1 = ((double)(tq_splitmix64(s) >> 11) + 0.5) * (1.0 / 9007199254740992.0);
-    double u2 = ((double)(tq_splitmix64(s) >> 11) + 0.5) * (1.0 / 9007199254740992.0);
-    double r = sqrt(-2.0 * log(u1));
-    g[(size_t)i] = r * cos(6.283185307179586 * u2);
-    if (i + 1 < D * D) g[(size_t)i + 1] = r * sin(6.283185307179586 * u2);
-  }
+  tq_gaussian(D * D, seed, g.data());
   for (int64_t i = 0; i < D; ++i) {
     double* gi = &g[(size_t)(i * D)];
     for (int pass = 0; pass < 2; ++pass)

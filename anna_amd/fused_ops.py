@@ -526,6 +526,70 @@ def tq_values_dequant(data, scales, zeros, bits, group_size, out_dtype):
 
 
 
+# ---------------------------------------------------------------- TurboQuant inner-product keys
+# (the TurboQuantIP quantizer behind turboquant.py:255-332)
+
+
+def tq_ip_gaussian(head_dim: int, seed: int) -> torch.Tensor:
+    """QJL matrix G (fp32 [D, D], host): seeded standard normals from the native library."""
+    out = torch.empty((head_dim, head_dim), dtype=torch.float32)
+    _lib.call("anna_mi_tq_ip_gaussian", head_dim, seed, out.data_ptr())
+    return out
+
+
+def tq_ip_quantize(x2d, signs, thresholds, centroids, gaussian_t, bits):
+    """x [nvec, D] -> (mse_indices uint8 [nvec, D], norms fp32 [nvec], qjl_signs uint8 [nvec, D],
+    residual_norms fp32 [nvec])."""
+    _lib.require_device(x2d, signs, thresholds, centroids, gaussian_t)
+    nvec, d = x2d.shape
+    if x2d.stride(1) != 1:
+        x2d = x2d.contiguous()
+    dev = x2d.device
+    idx = torch.empty((nvec, d), dtype=torch.uint8, device=dev)
+    qjl = torch.empty((nvec, d), dtype=torch.uint8, device=dev)
+    norms = torch.empty((nvec,), dtype=torch.float32, device=dev)
+    rn = torch.empty((nvec,), dtype=torch.float32, device=dev)
+    _lib.call("anna_mi_tq_ip_quantize", x2d.data_ptr(), _lib.dtype_code(x2d.dtype), nvec, d, max(x2d.stride(0), d),
+              signs.data_ptr(), thresholds.data_ptr(), centroids.data_ptr(), gaussian_t.data_ptr(), bits,
+              idx.data_ptr(), qjl.data_ptr(), norms.data_ptr(), rn.data_ptr(), _lib.stream_of(x2d))
+    return idx, norms, qjl, rn
+
+
+def tq_ip_dequant(idx, norms, qjl, rn, signs, centroids, gaussian, bits, out_dtype=torch.float32):
+    """-> [nvec, D] reconstruction (flattened state of nvec vectors)."""
+    _lib.require_device(idx, norms, qjl, rn, signs, centroids, gaussian)
+    d = idx.size(-1)
+    idx, qjl = idx.reshape(-1, d).contiguous(), qjl.reshape(-1, d).contiguous()
+    norms, rn = norms.reshape(-1).float().contiguous(), rn.reshape(-1).float().contiguous()
+    nvec = idx.size(0)
+    if qjl.size(0) != nvec or norms.numel() != nvec or rn.numel() != nvec:
+        raise RuntimeError("TurboQuant key state: mse_indices, qjl_signs, norms and residual_norms disagree")
+    out = torch.empty((nvec, d), dtype=out_dtype, device=idx.device)
+    _lib.call("anna_mi_tq_ip_dequant", idx.data_ptr(), qjl.data_ptr(), norms.data_ptr(), rn.data_ptr(), nvec, d,
+              signs.data_ptr(), centroids.data_ptr(), gaussian.data_ptr(), bits, out.data_ptr(),
+              _lib.dtype_code(out_dtype), d, _lib.stream_of(idx))
+    return out
+
+
+def tq_ip_scores(query, idx, norms, qjl, rn, signs, centroids, gaussian_t, bits, scaling):
+    """query [Hq, Lq, D], state [Hkv, T, D] / [Hkv, T(, 1)] -> fp32 [Hkv, Hq/Hkv, Lq, T]."""
+    _lib.require_device(query, idx, norms, qjl, rn, signs, centroids, gaussian_t)
+    hq, lq, d = query.shape
+    hkv, t = idx.shape[0], idx.shape[1]
+    if query.stride(2) != 1:
+        query = query.contiguous()
+    idx, qjl = idx.contiguous(), qjl.contiguous()
+    norms, rn = norms.reshape(hkv, t).float().contiguous(), rn.reshape(hkv, t).float().contiguous()
+    dev = query.device
+    out = torch.empty((hkv, hq // hkv, lq, t), dtype=torch.float32, device=dev)
+    ws = torch.empty((max(2 * hq * lq * d, 1),), dtype=torch.float32, device=dev)
+    _lib.call("anna_mi_tq_ip_scores", query.data_ptr(), _lib.dtype_code(query.dtype), hq, lq, d, query.stride(0),
+              query.stride(1), idx.data_ptr(), qjl.data_ptr(), norms.data_ptr(), rn.data_ptr(), hkv, t,
+              signs.data_ptr(), centroids.data_ptr(), gaussian_t.data_ptr(), bits, float(scaling), ws.data_ptr(),
+              out.data_ptr(), _lib.stream_of(query))
+    return out
+
+
 # ---------------------------------------------------------------- tiled int4 GEMV, LM-head top-k
 # (sycl:3272-3343 xpu_int4_gemv_tiled, sycl:2137-2572 lm_head_int4_topk_fused)
 

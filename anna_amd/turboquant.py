@@ -3,8 +3,10 @@
 Public surface kept from the reference: ``TurboQuantKVRow`` (append / decode_attention /
 materialize / clone / to, length properties), ``TurboQuantTensorRow`` (append /
 materialize), ``quantize_turboquant_values`` / ``dequantize_turboquant_values``,
-``TurboQuantValueState``, ``VALID_KV_CACHE_QUANT_BITS``, ``turboquant_is_available`` and
-``get_turboquant_quantizer``.
+``TurboQuantValueState``, ``VALID_KV_CACHE_QUANT_BITS``, ``turboquant_is_available``,
+``get_turboquant_quantizer``, and the inner-product keys: ``TurboQuantKeyState``,
+``get_turboquant_ip_quantizer``, ``_quantize_turboquant_keys``, ``dequantize_turboquant_keys``,
+``turboquant_key_attention_scores``.
 
 Differences by design:
   * The MSE quantizer (rotation + Lloyd-Max codebook + norm) is this build's own
@@ -42,10 +44,13 @@ class TurboQuantValueState(NamedTuple):
 
 
 class TurboQuantKeyState(NamedTuple):
-    """Packed TQ-MSE keys: codes uint8 [H, T, D*sb/8] and fp16 norms [H, T]."""
+    """TurboQuant inner-product key state (reference turboquant.py:27-31): mse_indices uint8
+    [H, T, D], norms fp32 [H, T, 1], qjl_signs uint8 0/1 [H, T, D], residual_norms fp32 [H, T, 1]."""
 
-    codes: torch.Tensor
+    mse_indices: torch.Tensor
     norms: torch.Tensor
+    qjl_signs: torch.Tensor
+    residual_norms: torch.Tensor
 
 
 def turboquant_is_available() -> bool:
@@ -142,6 +147,109 @@ def get_turboquant_quantizer(*, head_dim: int, bits: int, device) -> TurboQuantM
         q = TurboQuantMSE(head_dim, bits, device)
         _quantizers[key] = q
     return q
+
+
+class TurboQuantIP:
+    """TurboQuant_prod quantizer (this build's definition of the absent package's TurboQuantIP
+    that the reference builds at turboquant.py:84-92; Zandieh et al. 2025, Algorithm 2).
+
+    MSE stage with bits - 1 bits (the Hadamard rotation R and Lloyd-Max codebook of
+    `TurboQuantMSE`), then the signs of G (x / |x| - R^T c[idx]) rotated (G a seeded D x D
+    standard-normal matrix) and the residual norm.  ``S`` = G R is the reference's projection
+    matrix, so its score formula (turboquant.py:311-332) holds with these tensors.
+
+    quantize(x [n, D]) -> (mse_indices uint8 [n, D], norms fp32 [n], qjl_signs uint8 [n, D],
+    residual_norms fp32 [n]);  dequantize(...) -> [n, D].  D: a power of two in [64, 1024].
+    """
+
+    QJL_SEED_SALT = 0x514A4C
+
+    def __init__(self, dim: int, bits: int, device, seed: int = _MSE_SEED):
+        if bits not in VALID_KV_CACHE_QUANT_BITS:
+            raise ValueError(f"TurboQuantIP bits must be one of {sorted(VALID_KV_CACHE_QUANT_BITS)}, got {bits}")
+        if dim not in (64, 128, 256, 512, 1024):
+            raise ValueError(f"TurboQuantIP head_dim must be a power of two in [64, 1024], got {dim}")
+        self.dim, self.bits, self.seed = int(dim), int(bits), int(seed)
+        self.device = torch.device(device)
+        cent, thr = fused_ops.tq_codebook(self.bits - 1, self.dim)
+        self.centroids = cent.to(self.device)
+        self.thresholds = thr.to(self.device)
+        signs = fused_ops.tq_hadamard_signs(self.dim, self.seed)
+        self.signs = signs.to(self.device)
+        g = fused_ops.tq_ip_gaussian(self.dim, self.seed ^ self.QJL_SEED_SALT)
+        self.gaussian = g.to(self.device)
+        self.gaussian_t = g.t().contiguous().to(self.device)
+        rot = fused_ops.tq_rotation(self.dim, self.seed)
+        self.S = (g.double() @ rot.double()).float().to(self.device)
+
+    def quantize(self, x: torch.Tensor):
+        _require_rocm(x, "TurboQuant key quantization")
+        return fused_ops.tq_ip_quantize(x.reshape(-1, self.dim), self.signs, self.thresholds, self.centroids,
+                                        self.gaussian_t, self.bits)
+
+    def dequantize(self, mse_indices, norms, qjl_signs, residual_norms, dtype=torch.float32) -> torch.Tensor:
+        _require_rocm(mse_indices, "TurboQuant key dequantization")
+        out = fused_ops.tq_ip_dequant(mse_indices, norms, qjl_signs, residual_norms, self.signs, self.centroids,
+                                      self.gaussian, self.bits, out_dtype=dtype)
+        return out.reshape(*mse_indices.shape[:-1], self.dim)
+
+
+_ip_quantizers: dict[tuple[int, int, str], TurboQuantIP] = {}
+
+
+def get_turboquant_ip_quantizer(*, head_dim: int, bits: int, device) -> TurboQuantIP:
+    key = (int(head_dim), int(bits), str(torch.device(device)))
+    q = _ip_quantizers.get(key)
+    if q is None:
+        q = TurboQuantIP(head_dim, bits, device)
+        _ip_quantizers[key] = q
+    return q
+
+
+def _quantize_turboquant_keys(tensor: torch.Tensor, *, bits: int, device) -> TurboQuantKeyState:
+    """Keys [heads, tokens, dim] -> TurboQuantKeyState (reference turboquant.py:255-272)."""
+    if tensor.ndim != 3:
+        raise ValueError(f"TurboQuant key quantization expects [heads, tokens, dim], got {tuple(tensor.shape)}")
+    quantizer = get_turboquant_ip_quantizer(head_dim=int(tensor.shape[-1]), bits=bits, device=device)
+    h, t, d = tensor.shape
+    idx, norms, qjl, rn = quantizer.quantize(tensor.reshape(-1, d))
+    return TurboQuantKeyState(mse_indices=idx.reshape(h, t, d), norms=norms.reshape(h, t, 1),
+                              qjl_signs=qjl.reshape(h, t, d), residual_norms=rn.reshape(h, t, 1))
+
+
+def dequantize_turboquant_keys(state: TurboQuantKeyState, *, bits: int, device, dtype=None) -> torch.Tensor:
+    """Reconstructed keys [heads, tokens, dim] (reference turboquant.py:275-287)."""
+    head_dim = int(state.mse_indices.shape[-1])
+    quantizer = get_turboquant_ip_quantizer(head_dim=head_dim, bits=bits, device=device)
+    out_dtype = dtype if dtype in (torch.bfloat16, torch.float16, torch.float32) else torch.float32
+    keys = quantizer.dequantize(state.mse_indices, state.norms, state.qjl_signs, state.residual_norms,
+                                dtype=out_dtype)
+    if dtype is not None and keys.dtype != dtype:
+        keys = keys.to(dtype=dtype)
+    return keys
+
+
+def turboquant_key_attention_scores(*, query: torch.Tensor, state: TurboQuantKeyState, bits: int, device,
+                                    num_key_value_groups: int, scaling: float) -> torch.Tensor:
+    """scaling * (q . k_mse + QJL correction), fp32 [kv_heads, groups, query_len, tokens]
+    (reference turboquant.py:290-332), from the codes: the query is rotated and projected once
+    per row and the keys are never expanded."""
+    if query.ndim != 3:
+        raise ValueError(f"TurboQuant key attention expects [query_heads, tokens, dim], got {tuple(query.shape)}")
+    num_key_value_heads = int(state.mse_indices.shape[0])
+    query_heads, _, head_dim = query.shape
+    if query_heads % num_key_value_heads != 0:
+        raise ValueError(
+            f"Query head count {query_heads} is not compatible with TurboQuant KV heads {num_key_value_heads}.")
+    if query_heads != num_key_value_heads * num_key_value_groups:
+        raise ValueError(f"Expected {num_key_value_heads * num_key_value_groups} query heads, got {query_heads}.")
+    if head_dim != int(state.mse_indices.shape[-1]):
+        raise ValueError(
+            f"TurboQuant key attention head_dim mismatch: expected {state.mse_indices.shape[-1]}, got {head_dim}.")
+    _require_rocm(query, "TurboQuant key attention")
+    quantizer = get_turboquant_ip_quantizer(head_dim=head_dim, bits=bits, device=device)
+    return fused_ops.tq_ip_scores(query, state.mse_indices, state.norms, state.qjl_signs, state.residual_norms,
+                                  quantizer.signs, quantizer.centroids, quantizer.gaussian_t, bits, scaling)
 
 
 def _next_capacity(current: int, required: int) -> int:

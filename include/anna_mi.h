@@ -131,6 +131,43 @@ int anna_mi_tq_mse_dequant(const uint8_t* codes, const uint16_t* norms, int64_t 
                            const float* rot, const float* centroids, int bits, void* out, int out_dtype,
                            int64_t out_row_stride, void* stream);
 
+/* TurboQuant inner-product keys (TurboQuant_prod: MSE stage of bits-1 bits + 1-bit QJL sketch of
+ * its residual), this build's definition of the absent package's TurboQuantIP that the reference
+ * calls in _quantize_turboquant_keys / dequantize_turboquant_keys / turboquant_key_attention_scores
+ * (src/anna/model/turboquant.py:84-92, 255-332).  D a power of two in [64, 1024].  State per vector:
+ * mse_indices uint8 [D] (one code per byte), qjl_signs uint8 [D] (0/1), norms fp32, residual_norms
+ * fp32 (|residual| / norm).  signs: the Hadamard sign vector (anna_mi_tq_hadamard_signs);
+ * thresholds / centroids: anna_mi_tq_codebook(bits - 1, D); gaussian / gaussian_t: the QJL matrix G
+ * of anna_mi_tq_ip_gaussian and its transpose, device fp32 [D, D]. */
+
+/* G (fp32 [D, D] row-major, host): standard normals (splitmix64 + Box-Muller in fp64) of `seed`.
+ * The reference's quantizer.S is G R (R the Hadamard rotation). */
+int anna_mi_tq_ip_gaussian(int64_t D, uint64_t seed, float* out_host);
+
+/* TurboQuantIP.quantize (turboquant.py:262-264): x [nvec, D] (row stride x_row_stride, bf16/f16/
+ * f32) -> mse_indices, qjl_signs [nvec, D], norms, residual_norms [nvec]. */
+int anna_mi_tq_ip_quantize(const void* x, int x_dtype, int64_t nvec, int64_t D, int64_t x_row_stride,
+                           const float* signs, const float* thresholds, const float* centroids,
+                           const float* gaussian_t, int bits, uint8_t* mse_indices, uint8_t* qjl_signs,
+                           float* norms, float* residual_norms, void* stream);
+
+/* TurboQuantIP.dequantize (dequantize_turboquant_keys, turboquant.py:275-287): out [nvec, D]
+ * (row stride out_row_stride, out_dtype) = norm * R^T (c[idx] + sqrt(pi/2)/D * rn * G^T (2 qjl - 1)). */
+int anna_mi_tq_ip_dequant(const uint8_t* mse_indices, const uint8_t* qjl_signs, const float* norms,
+                          const float* residual_norms, int64_t nvec, int64_t D, const float* signs,
+                          const float* centroids, const float* gaussian, int bits, void* out, int out_dtype,
+                          int64_t out_row_stride, void* stream);
+
+/* turboquant_key_attention_scores (turboquant.py:290-332): query [Hq, Lq, D] (strides q_stride_h,
+ * q_stride_l, 1), key state [Hkv, T, D] / [Hkv, T] -> out fp32 [Hkv, Hq/Hkv, Lq, T] = scaling *
+ * (MSE scores + QJL scores), without expanding the keys.  workspace: fp32 [2 * Hq * Lq * D]. */
+int anna_mi_tq_ip_scores(const void* query, int q_dtype, int64_t Hq, int64_t Lq, int64_t D,
+                         int64_t q_stride_h, int64_t q_stride_l, const uint8_t* mse_indices,
+                         const uint8_t* qjl_signs, const float* norms, const float* residual_norms,
+                         int64_t Hkv, int64_t T, const float* signs, const float* centroids,
+                         const float* gaussian_t, int bits, float scaling, float* workspace, float* out,
+                         void* stream);
+
 /* quantize_turboquant_values + _pack_value_data (turboquant.py:164-175, 199-230):
  * values [H, T, D] with strides (stride_h, stride_t, 1) -> data/scales/zeros (contiguous). */
 int anna_mi_tq_values_quantize(const void* values, int dtype, int64_t H, int64_t T, int64_t D,

@@ -510,3 +510,93 @@ void orc_tq_hadamard_quantize(const void* x, int dtype, int64_t nvec, int64_t D,
     free(y);
     free(xv);
 }
+
+/* ------------------------------------------------------------------ */
+/* TurboQuant inner-product keys (TurboQuant_prod, Zandieh et al. 2025,  */
+/* Algorithm 2): this build's definition of the absent package's        */
+/* TurboQuantIP behind turboquant.py:255-332.  PARITY UNPINNED against  */
+/* the reference (the package is absent); pinned by the inner-product   */
+/* identity with the reference's score formula, unbiasedness over QJL   */
+/* matrices, the MSE stage against orc_tq_hadamard_quantize and a brute */
+/* force fp64 residual / projection (tests/test_oracle_tq_ip.py).       */
+/* ------------------------------------------------------------------ */
+
+/* x [nvec, D] -> mse_indices [nvec, D] (bits-1-bit codes), qjl [nvec, D] (0/1), norms, rn:
+ *   nrm = |x|, y = R x, code_i = #{j : y_i >= fl(t_j nrm)}, rho_i = fma(-c[code_i], nrm, y_i),
+ *   rn = sqrt(|rho|^2) / nrm (0 for nrm = 0), qjl_i = (sum_k G[i][k] rho_k >= 0) with the sum
+ *   one fma chain over ascending k.  |x|^2 and |rho|^2 in hadamard_sumsq's order. */
+void orc_tq_ip_quantize(const void* x, int dtype, int64_t nvec, int64_t D, const float* signs, const float* thr,
+                        const float* cent, int bits, const float* G, uint8_t* idx, uint8_t* qjl, float* norms,
+                        float* rn) {
+    int nthr = (1 << (bits - 1)) - 1;
+    float* xv = (float*)malloc(sizeof(float) * (size_t)D);
+    float* y = (float*)malloc(sizeof(float) * (size_t)D);
+    float* rho = (float*)malloc(sizeof(float) * (size_t)D);
+    for (int64_t v = 0; v < nvec; ++v) {
+        for (int64_t k = 0; k < D; ++k) xv[k] = load_any(x, dtype, v * D + k);
+        float nrm = sqrtf(hadamard_sumsq(xv, D));
+        orc_tq_hadamard_rotate(xv, signs, D, y);
+        for (int64_t i = 0; i < D; ++i) {
+            uint32_t c = 0;
+            for (int j = 0; j < nthr; ++j) c += (y[i] >= thr[j] * nrm) ? 1u : 0u;
+            idx[v * D + i] = (uint8_t)c;
+            rho[i] = fmaf(-cent[c], nrm, y[i]);
+        }
+        float gam = sqrtf(hadamard_sumsq(rho, D));
+        norms[v] = nrm;
+        rn[v] = nrm > 0.0f ? gam / nrm : 0.0f;
+        for (int64_t i = 0; i < D; ++i) {
+            float z = 0.0f;
+            for (int64_t k = 0; k < D; ++k) z = fmaf(G[i * D + k], rho[k], z);
+            qjl[v * D + i] = z >= 0.0f ? 1 : 0;
+        }
+    }
+    free(rho);
+    free(y);
+    free(xv);
+}
+
+/* out [nvec, D] = norm * R^T u, u_j = fma(k0 * rn, w_j, c[code_j]), w_j = sum_i G[i][j] (2 qjl_i - 1)
+ * (one fma chain over ascending i), k0 = fl(sqrt(pi/2) / D); R^T u = s .* (fl(1/sqrt(D)) * FWHT(u)). */
+void orc_tq_ip_dequant(const uint8_t* idx, const uint8_t* qjl, const float* norms, const float* rn, int64_t nvec,
+                       int64_t D, const float* signs, const float* cent, const float* G, float* out) {
+    const float k0 = (float)(1.2533141373155002512 / (double)D);
+    const float inv = orc_tq_inv_sqrt(D);
+    float* u = (float*)malloc(sizeof(float) * (size_t)D);
+    for (int64_t v = 0; v < nvec; ++v) {
+        const float coef = k0 * rn[v];
+        for (int64_t j = 0; j < D; ++j) {
+            float w = 0.0f;
+            for (int64_t i = 0; i < D; ++i) w = fmaf(G[i * D + j], qjl[v * D + i] ? 1.0f : -1.0f, w);
+            u[j] = fmaf(coef, w, cent[idx[v * D + j]]);
+        }
+        for (int64_t h = 1; h < D; h <<= 1)
+            for (int64_t i = 0; i < D; ++i)
+                if ((i & h) == 0) {
+                    float a = u[i], c = u[i + h];
+                    u[i] = a + c;
+                    u[i + h] = a - c;
+                }
+        for (int64_t k = 0; k < D; ++k) {
+            float t = u[k] * inv;
+            t = t * signs[k];
+            out[v * D + k] = norms[v] * t;
+        }
+    }
+    free(u);
+}
+
+/* G [D, D] row-major: standard normals of the splitmix64 stream of `seed`, Box-Muller in fp64
+ * (pairs (u1, u2) of 53-bit uniforms in (0, 1): r cos(2 pi u2), r sin(2 pi u2), r = sqrt(-2 ln u1)),
+ * rounded to fp32. */
+void orc_tq_ip_gaussian(int64_t D, uint64_t seed, float* out) {
+    uint64_t st = seed;
+    int64_t n = D * D;
+    for (int64_t i = 0; i < n; i += 2) {
+        double u1 = ((double)(orc_splitmix64(&st) >> 11) + 0.5) * (1.0 / 9007199254740992.0);
+        double u2 = ((double)(orc_splitmix64(&st) >> 11) + 0.5) * (1.0 / 9007199254740992.0);
+        double r = sqrt(-2.0 * log(u1));
+        out[i] = (float)(r * cos(6.283185307179586 * u2));
+        if (i + 1 < n) out[i + 1] = (float)(r * sin(6.283185307179586 * u2));
+    }
+}

@@ -51,6 +51,9 @@ def lib():
             "orc_tq_hadamard_signs": [_I64, ctypes.c_uint64, _P],
             "orc_tq_hadamard_rotate": [_P, _P, _I64, _P],
             "orc_tq_hadamard_quantize": [_P, _I, _I64, _I64, _P, _P, _I, _P, _P],
+            "orc_tq_ip_quantize": [_P, _I, _I64, _I64, _P, _P, _P, _I, _P, _P, _P, _P, _P],
+            "orc_tq_ip_dequant": [_P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P],
+            "orc_tq_ip_gaussian": [_I64, ctypes.c_uint64, _P],
         }
         for name, argtypes in sig.items():
             fn = getattr(L, name)
@@ -247,6 +250,67 @@ def tq_hadamard_quantize(x_bits: np.ndarray, dtype: int, signs: np.ndarray, thre
     norms = np.zeros((nvec,), np.uint16)
     lib().orc_tq_hadamard_quantize(_p(x), dtype, nvec, d, _p(s), _p(thr), bits, _p(codes), _p(norms))
     return codes, norms
+
+
+# ---------------------------------------------------------------- TurboQuant inner-product keys (a10)
+# This build's TurboQuantIP (the package the reference calls at turboquant.py:84-92, 255-332 is
+# absent): PARITY UNPINNED against the reference; pinned by tests/test_oracle_tq_ip.py.
+
+
+def tq_ip_gaussian(d: int, seed: int) -> np.ndarray:
+    out = np.zeros((d, d), np.float32)
+    lib().orc_tq_ip_gaussian(d, seed, _p(out))
+    return out
+
+
+def tq_ip_quantize(x_bits: np.ndarray, dtype: int, signs, thresholds, centroids, gaussian, bits: int):
+    """x [nvec, D] -> (mse_indices uint8 [nvec, D], norms f32, qjl uint8 [nvec, D], residual norms f32)."""
+    x = np.ascontiguousarray(x_bits)
+    nvec, d = x.shape
+    s = np.ascontiguousarray(signs, np.float32)
+    thr = np.ascontiguousarray(thresholds, np.float32)
+    c = np.ascontiguousarray(centroids, np.float32)
+    g = np.ascontiguousarray(gaussian, np.float32)
+    idx = np.zeros((nvec, d), np.uint8)
+    qjl = np.zeros((nvec, d), np.uint8)
+    norms = np.zeros(nvec, np.float32)
+    rn = np.zeros(nvec, np.float32)
+    lib().orc_tq_ip_quantize(_p(x), dtype, nvec, d, _p(s), _p(thr), _p(c), bits, _p(g), _p(idx), _p(qjl),
+                             _p(norms), _p(rn))
+    return idx, norms, qjl, rn
+
+
+def tq_ip_dequant(idx, norms, qjl, rn, signs, centroids, gaussian) -> np.ndarray:
+    idx = np.ascontiguousarray(idx, np.uint8)
+    nvec, d = idx.shape
+    qjl = np.ascontiguousarray(qjl, np.uint8)
+    norms = np.ascontiguousarray(norms, np.float32).reshape(-1)
+    rn = np.ascontiguousarray(rn, np.float32).reshape(-1)
+    out = np.zeros((nvec, d), np.float32)
+    lib().orc_tq_ip_dequant(_p(idx), _p(qjl), _p(norms), _p(rn), nvec, d,
+                            _p(np.ascontiguousarray(signs, np.float32)),
+                            _p(np.ascontiguousarray(centroids, np.float32)),
+                            _p(np.ascontiguousarray(gaussian, np.float32)), _p(out))
+    return out
+
+
+def tq_ip_key_scores(query, idx, norms, qjl, rn, S, signs, centroids, gaussian, groups: int, scaling: float):
+    """The reference's turboquant_key_attention_scores (turboquant.py:311-332) in fp64: MSE-only
+    keys (dequantize with zero signs and zero residual norms), plus (q S^T)(2 qjl - 1)^T scaled by
+    sqrt(pi/2)/D * norms * residual_norms.  query [Hq, Lq, D]; state [Hkv, T, D] / [Hkv, T]."""
+    hkv, t, d = idx.shape
+    hq, lq, _ = query.shape
+    flat = lambda a: a.reshape(hkv * t, -1)
+    zero = np.zeros_like(flat(rn)).reshape(-1)
+    mse = tq_ip_dequant(flat(idx), flat(norms).reshape(-1), flat(qjl), zero, signs, centroids, gaussian)
+    mse = mse.astype(np.float64).reshape(hkv, t, d)
+    gq = query.astype(np.float64).reshape(hkv, groups, lq, d)
+    mse_scores = np.einsum("hgld,htd->hglt", gq, mse)
+    sg = 2.0 * qjl.astype(np.float64) - 1.0
+    proj = gq @ S.astype(np.float64).T
+    res = (np.sqrt(np.pi / 2.0) / d) * norms.reshape(hkv, t).astype(np.float64) * rn.reshape(hkv, t)
+    qjl_scores = np.einsum("hgld,htd->hglt", proj, sg) * res[:, None, None, :]
+    return (mse_scores + qjl_scores) * scaling
 
 
 # ---------------------------------------------------------------- attention (a13) -- textbook, fp64
