@@ -385,12 +385,19 @@ class TurboQuantTensorRow:
 class TurboQuantKVRow:
     """Compressed K/V cache of one sequence (reference turboquant.py:480-1443).
 
-    Keys: TQ-MSE codes + fp16 norms; values: min/max groups (reference format); the
-    newest ``residual_len`` tokens stay dense.  ``decode_attention`` runs one split-KV
-    launch over [packed prefix ++ residual] with all q-heads of a KV head sharing reads.
+    Keys: TQ-MSE codes + fp16 norms by default; with ``key_quantizer="ip"`` the reference's
+    inner-product key state (``TurboQuantKeyState``) plus its dense reconstruction in the
+    cache dtype, which decode reads as the reference's XPU path does (turboquant.py:1098-1111).
+    Values: min/max groups (reference format); the newest ``residual_len`` tokens stay dense.
+    ``decode_attention`` runs one split-KV launch over [packed prefix ++ residual] with all
+    q-heads of a KV head sharing reads.
     """
 
-    def __init__(self, *, bits: int, residual_len: int, value_group_size: int | None = None) -> None:
+    def __init__(self, *, bits: int, residual_len: int, value_group_size: int | None = None,
+                 key_quantizer: str = "mse") -> None:
+        if key_quantizer not in ("mse", "ip"):
+            raise ValueError(f"key_quantizer must be 'mse' or 'ip', got {key_quantizer!r}")
+        self.key_quantizer = key_quantizer
         self.bits = int(bits)
         self.residual_len = max(1, int(residual_len))
         self.value_group_size = None if value_group_size is None else max(1, int(value_group_size))
@@ -399,6 +406,7 @@ class TurboQuantKVRow:
         self.head_dim = None
         self.num_heads = None
         self._kcodes = self._knorms = None
+        self._kqjl = self._krn = self._kdense = None  # inner-product keys: signs, residual norms, reconstruction
         self._vdata = self._vscales = self._vzeros = None
         self._qlen = 0
         self._residual_keys: torch.Tensor | None = None
@@ -438,8 +446,9 @@ class TurboQuantKVRow:
         h, d = self.num_heads, self.head_dim
         sb = _storage_bits(self.bits)
         g = self.value_group_size
-        kc = torch.empty((h, new_cap, d * sb // 8), dtype=torch.uint8, device=self.device)
-        kn = torch.empty((h, new_cap), dtype=torch.float16, device=self.device)
+        ip = self.key_quantizer == "ip"
+        kc = torch.empty((h, new_cap, d if ip else d * sb // 8), dtype=torch.uint8, device=self.device)
+        kn = torch.empty((h, new_cap), dtype=torch.float32 if ip else torch.float16, device=self.device)
         vd = torch.empty((h, new_cap, d * sb // 8), dtype=torch.uint8, device=self.device)
         vs = torch.empty((h, new_cap, d // g), dtype=self.dtype, device=self.device)
         vz = torch.empty((h, new_cap, d // g), dtype=self.dtype, device=self.device)
@@ -449,6 +458,15 @@ class TurboQuantKVRow:
                              (vz, self._vzeros)):
                 new[:, :n].copy_(old[:, :n])
         self._kcodes, self._knorms, self._vdata, self._vscales, self._vzeros = kc, kn, vd, vs, vz
+        if ip:
+            kq = torch.empty((h, new_cap, d), dtype=torch.uint8, device=self.device)
+            kr = torch.empty((h, new_cap), dtype=torch.float32, device=self.device)
+            kd = torch.empty((h, new_cap, d), dtype=self.dtype, device=self.device)
+            if self._qlen > 0:
+                n = self._qlen
+                for new, old in ((kq, self._kqjl), (kr, self._krn), (kd, self._kdense)):
+                    new[:, :n].copy_(old[:, :n])
+            self._kqjl, self._krn, self._kdense = kq, kr, kd
 
     def append(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
         if key_states.ndim != 3 or value_states.ndim != 3:
@@ -480,12 +498,21 @@ class TurboQuantKVRow:
             return
         ks = self._residual_keys[:, :overflow]
         vs = self._residual_values[:, :overflow]
-        codes, norms = self._quantizer().quantize(ks.reshape(-1, self.head_dim))
         vstate = quantize_turboquant_values(vs, bits=self.bits, group_size=self.value_group_size)
         self._grow(self._qlen + overflow)
         s, e, h = self._qlen, self._qlen + overflow, self.num_heads
-        self._kcodes[:, s:e].copy_(codes.view(h, overflow, -1))
-        self._knorms[:, s:e].copy_(norms.view(h, overflow))
+        if self.key_quantizer == "ip":
+            kst = _quantize_turboquant_keys(ks, bits=self.bits, device=self.device)
+            self._kcodes[:, s:e].copy_(kst.mse_indices)
+            self._knorms[:, s:e].copy_(kst.norms.view(h, overflow))
+            self._kqjl[:, s:e].copy_(kst.qjl_signs)
+            self._krn[:, s:e].copy_(kst.residual_norms.view(h, overflow))
+            self._kdense[:, s:e].copy_(dequantize_turboquant_keys(kst, bits=self.bits, device=self.device,
+                                                                  dtype=self.dtype))
+        else:
+            codes, norms = self._quantizer().quantize(ks.reshape(-1, self.head_dim))
+            self._kcodes[:, s:e].copy_(codes.view(h, overflow, -1))
+            self._knorms[:, s:e].copy_(norms.view(h, overflow))
         self._vdata[:, s:e].copy_(vstate.data)
         self._vscales[:, s:e].copy_(vstate.scales)
         self._vzeros[:, s:e].copy_(vstate.zeros)
@@ -499,9 +526,12 @@ class TurboQuantKVRow:
         kp, vp = [], []
         if self._qlen > 0:
             n, h, d = self._qlen, self.num_heads, self.head_dim
-            k = self._quantizer().dequantize(self._kcodes[:, :n].reshape(h * n, -1), self._knorms[:, :n].reshape(-1),
-                                             dtype=self.dtype)
-            kp.append(k.view(h, n, d))
+            if self.key_quantizer == "ip":
+                kp.append(self._kdense[:, :n])
+            else:
+                k = self._quantizer().dequantize(self._kcodes[:, :n].reshape(h * n, -1),
+                                                 self._knorms[:, :n].reshape(-1), dtype=self.dtype)
+                kp.append(k.view(h, n, d))
             vp.append(fused_ops.tq_values_dequant(self._vdata[:, :n], self._vscales[:, :n], self._vzeros[:, :n],
                                                   self.bits, self.value_group_size, self.dtype))
         if self.residual_length > 0:
@@ -545,10 +575,13 @@ class TurboQuantKVRow:
         n, r = self._qlen, self.residual_length
         res_k = self._residual_keys.unsqueeze(0) if r > 0 else None
         res_v = self._residual_values.unsqueeze(0) if r > 0 else None
+        if self.key_quantizer == "ip":
+            kargs = dict(key=self._kdense[:, :n].unsqueeze(0) if n > 0 else None, key_format=fused_ops.KEYS_DENSE)
+        else:
+            kargs = dict(key=self._kcodes[:, :n].unsqueeze(0) if n > 0 else None, key_format=fused_ops.KEYS_TQ_MSE,
+                         key_norms=self._knorms[:, :n].unsqueeze(0) if n > 0 else None)
         args = fused_ops.decode_args(
-            query=q4, len1=n,
-            key=self._kcodes[:, :n].unsqueeze(0) if n > 0 else None, key_format=fused_ops.KEYS_TQ_MSE,
-            key_norms=self._knorms[:, :n].unsqueeze(0) if n > 0 else None, key_bits=self.bits,
+            query=q4, len1=n, **kargs, key_bits=self.bits,
             value=self._vdata[:, :n].unsqueeze(0) if n > 0 else None, value_format=fused_ops.VALUES_MINMAX,
             value_scales=self._vscales[:, :n].unsqueeze(0) if n > 0 else None,
             value_zeros=self._vzeros[:, :n].unsqueeze(0) if n > 0 else None,
@@ -572,10 +605,11 @@ class TurboQuantKVRow:
         return out.squeeze(0)
 
     def clone(self) -> "TurboQuantKVRow":
-        c = TurboQuantKVRow(bits=self.bits, residual_len=self.residual_len, value_group_size=self.value_group_size)
+        c = TurboQuantKVRow(bits=self.bits, residual_len=self.residual_len, value_group_size=self.value_group_size,
+                            key_quantizer=self.key_quantizer)
         c.device, c.dtype, c.head_dim, c.num_heads = self.device, self.dtype, self.head_dim, self.num_heads
         c._qlen, c._length = self._qlen, self._length
-        for name in ("_kcodes", "_knorms", "_vdata", "_vscales", "_vzeros"):
+        for name in ("_kcodes", "_knorms", "_kqjl", "_krn", "_kdense", "_vdata", "_vscales", "_vzeros"):
             t = getattr(self, name)
             setattr(c, name, None if t is None else t[:, : self._qlen].clone())
         c._residual_keys = None if self._residual_keys is None else self._residual_keys.clone()
@@ -585,11 +619,11 @@ class TurboQuantKVRow:
     def to(self, *, device=None, dtype=None) -> "TurboQuantKVRow":
         if not self.initialized:
             return self
-        for name in ("_kcodes", "_knorms", "_vdata"):
+        for name in ("_kcodes", "_knorms", "_kqjl", "_krn", "_vdata"):
             t = getattr(self, name)
             if t is not None and device is not None:
                 setattr(self, name, t.to(device))
-        for name in ("_vscales", "_vzeros", "_residual_keys", "_residual_values"):
+        for name in ("_kdense", "_vscales", "_vzeros", "_residual_keys", "_residual_values"):
             t = getattr(self, name)
             if t is not None:
                 setattr(self, name, t.to(device=device, dtype=dtype))

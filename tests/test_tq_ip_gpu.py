@@ -117,3 +117,38 @@ def test_ip_key_api_checks(gpu):
     s = turboquant_key_attention_scores(query=q[:4], state=empty, bits=3, device=gpu, num_key_value_groups=2,
                                         scaling=1.0)
     assert s.shape == (2, 2, 1, 0)
+
+
+@pytest.mark.parametrize("bits", [2, 3])
+def test_kv_row_with_inner_product_keys(gpu, bits):
+    """TurboQuantKVRow(key_quantizer="ip"): the reference's key state (turboquant.py:1098-1111)
+    bit-exact with the oracle quantizer, its reconstruction as the decode keys, decode attention
+    against the oracle over [reconstructed prefix ++ window], clone equal."""
+    from anna_amd.turboquant import TurboQuantKVRow
+
+    torch.manual_seed(70 + bits)
+    hkv, groups, d, r = 2, 4, 128, 16
+    row = TurboQuantKVRow(bits=bits, residual_len=r, key_quantizer="ip")
+    ks = [torch.randn(hkv, n, d, device=gpu, dtype=torch.bfloat16) for n in (50, 1, 1, 30)]
+    vs = [torch.randn_like(k) for k in ks]
+    for k, v in zip(ks, vs):
+        row.append(k, v)
+    n = row.quantized_length
+    assert (row.length, n, row.residual_length) == (82, 66, 16)
+    kk = torch.cat(ks, 1)
+    q = get_turboquant_ip_quantizer(head_dim=d, bits=bits, device=gpu)
+    oi, on, oq, orn = _oracle_state(kk[:, :n].contiguous(), q)
+    np.testing.assert_array_equal(row._kcodes[:, :n].reshape(-1, d).cpu().numpy(), oi)
+    np.testing.assert_array_equal(row._kqjl[:, :n].reshape(-1, d).cpu().numpy(), oq)
+    np.testing.assert_array_equal(row._knorms[:, :n].reshape(-1).cpu().numpy(), on)
+    np.testing.assert_array_equal(row._krn[:, :n].reshape(-1).cpu().numpy(), orn)
+    kdeq = orc.tq_ip_dequant(oi, on, oq, orn, q.signs.cpu().numpy(), q.centroids.cpu().numpy(),
+                             q.gaussian.cpu().numpy())
+    np.testing.assert_array_equal(_host(row._kdense[:, :n]).reshape(-1, d), orc.bf16_bits(kdeq))
+    query = torch.randn(hkv * groups, 1, d, device=gpu, dtype=torch.bfloat16)
+    out = row.decode_attention(query, scaling=d ** -0.5, num_key_value_groups=groups)
+    keys, values = row.materialize(dtype=torch.float32)
+    ref = orc.gqa_decode(query.float().cpu().numpy()[:, 0], keys.cpu().numpy(), values.cpu().numpy(), d ** -0.5)
+    assert rel_err(out.float().cpu().numpy()[:, 0], ref) <= 1e-2
+    out2 = row.clone().decode_attention(query, scaling=d ** -0.5, num_key_value_groups=groups)
+    assert torch.equal(out, out2)
