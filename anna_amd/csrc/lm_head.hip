@@ -6,6 +6,8 @@
 // [G][N] (ss_g = N, ss_n = 1; also the tiled [G][N/T][T]) and the LM-head top-k layout [N][G]
 // (ss_g = 1, ss_n = G).  w = (q - z) * s.
 //
+//   int4_gemv_tiled_lds_kernel  (1..4 rows) the same with x and the tile scales and zero points
+//                           staged in LDS: one memory load per weight word
 //   int4_gemv_tiled_kernel  one wave per tile: lane l walks words l, l + 64, ... of the tile;
 //                           each word is one T x 4-byte coalesced load (8 k of T rows) used
 //                           against 8 activations of up to MR rows; fp32 accumulation
@@ -481,6 +483,142 @@ __global__ __launch_bounds__(1024) void topk_rows_lds_kernel(const float* __rest
   }
 }
 
+// LDS-staged form of the tiled GEMV (16-bit activations, K % 8 == 0, x row stride % 8 == 0, M <= TG_MR,
+// everything below fitting in LDS): the workgroup stages x once, as interleaved words with their
+// sums, and each wave stages its tile's scales (converted to fp32) and zero points, so that the
+// word loop issues one memory load per word (the weights) instead of one per weight word, x
+// word, scale and zero point (10 for T = 4).  Same arithmetic, in the same order, as the fast
+// path of int4_gemv_tiled_kernel, so the two agree bit for bit.  NW: the lane's words (words
+// lane, lane + 64, ..., at most NW of them, K <= 512 NW), all requested before the staging barrier.
+// Dynamic LDS: x words u32x4 [M][words], x sums float [M][words], scales float [4 waves][G][T],
+// zero points uint8 [4 waves][G][ZB].
+template <int XDT, int SDT, int T, int NW, bool OUT_F32>
+__global__ __launch_bounds__(256) void int4_gemv_tiled_lds_kernel(
+    const typename Elem<XDT>::T* __restrict__ x, int64_t M, int64_t K, int64_t xs, const uint32_t* __restrict__ qw,
+    int64_t tiles, int64_t pc, const typename Elem<SDT>::T* __restrict__ qs, const int8_t* __restrict__ qz,
+    int64_t ss_g, int64_t ss_n, int64_t gsz, int64_t N, void* __restrict__ y, int64_t ys) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t tl_smem[];
+  constexpr int ZB = T <= 4 ? 4 : 8;
+  constexpr float OFF = XDT == ANNA_MI_BF16 ? 128.0f : 1024.0f;
+  constexpr uint32_t ONES = XDT == ANNA_MI_BF16 ? 0x3F803F80u : 0x3C003C00u;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t tile = (int64_t)blockIdx.x * 4 + wave;
+  const bool active = tile < tiles;
+  const int64_t words = K / 8, G = (K + gsz - 1) / gsz;
+  const int64_t MW = (M * words + 3) & ~(int64_t)3;  // keeps the scale rows 16-byte aligned
+  u32x4* s_x = (u32x4*)tl_smem;
+  float* s_sx = (float*)(s_x + MW);
+  float* s_sc = s_sx + MW + (int64_t)wave * G * T;
+  uint8_t* s_z = (uint8_t*)(s_sx + MW + 4 * G * T) + (int64_t)wave * G * ZB;
+  const uint32_t* tw = qw + tile * pc * T;
+  // x words first (everything waits for them), then the tile's scales and zero points, then every
+  // weight word of the lane (clamped to the last word: no load is conditional, so no wait is
+  // widened at a join)
+  constexpr int XPT = 4;  // x words per thread (the host picks this kernel for M * words <= 1024)
+  u32x4 xw[XPT];
+#pragma unroll
+  for (int j = 0; j < XPT; ++j) {
+    const int64_t i = threadIdx.x + 256 * j;
+    const int64_t m = i / words, w = i % words;
+    xw[j] = i < M * words ? *(const u32x4*)((const uint16_t*)x + m * xs + w * 8) : u32x4{0u, 0u, 0u, 0u};
+  }
+  if (active) {
+    for (int64_t e = lane; e < G * T; e += 64) {
+      const int64_t g = e / T, t = e % T;
+      const int64_t n = tile * T + t;
+      const int64_t nc = n < N ? n : 0;
+      s_sc[e] = Elem<SDT>::load(qs, g * ss_g + nc * ss_n);
+      s_z[g * ZB + t] = (uint8_t)qz[g * ss_g + nc * ss_n];
+    }
+  }
+  TileWords<T> R[NW];
+  if (active) {
+#pragma unroll
+    for (int j = 0; j < NW; ++j) {
+      const int64_t w = lane + 64 * j;
+      R[j] = load_tile_words<T>(tw + (w < words ? w : words - 1) * T);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < XPT; ++j) {
+    const int64_t i = threadIdx.x + 256 * j;
+    if (i < M * words) {
+      const u32x4 xi = interleave_x(xw[j]);
+      s_x[i] = xi;
+      float sx = dot2_acc<XDT>(xi.x, ONES, 0.f);
+      sx = dot2_acc<XDT>(xi.y, ONES, sx);
+      sx = dot2_acc<XDT>(xi.z, ONES, sx);
+      s_sx[i] = dot2_acc<XDT>(xi.w, ONES, sx);
+    }
+  }
+  __syncthreads();
+  if (!active) return;
+  float acc[TG_MR][T];
+#pragma unroll
+  for (int m = 0; m < TG_MR; ++m)
+#pragma unroll
+    for (int t = 0; t < T; ++t) acc[m][t] = 0.f;
+  auto compute = [&](int64_t w, const TileWords<T>& q) {
+    const int64_t g = (w * 8) / gsz;
+    float sc[T];
+    uint8_t zb[ZB];
+    if constexpr (T == 4) {
+      const float4 v = *(const float4*)(s_sc + g * T);
+      sc[0] = v.x, sc[1] = v.y, sc[2] = v.z, sc[3] = v.w;
+    } else {
+#pragma unroll
+      for (int t = 0; t < T; ++t) sc[t] = s_sc[g * T + t];
+    }
+    if constexpr (ZB == 4) {
+      const uint32_t zz = *(const uint32_t*)(s_z + g * ZB);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) zb[t] = (uint8_t)(zz >> (8 * t));
+    } else {
+      const uint2 zz = *(const uint2*)(s_z + g * ZB);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) zb[t] = (uint8_t)(((t < 4) ? zz.x : zz.y) >> (8 * (t & 3)));
+    }
+#pragma unroll
+    for (int m = 0; m < TG_MR; ++m) {
+      if (m >= M) continue;
+      const u32x4 xi = s_x[m * words + w];
+      const float sx = s_sx[m * words + w];
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const u32x4 f = nibbles_to_frag<XDT>(q.v[t]);
+        float d = dot2_acc<XDT>(xi.x, f.x, 0.f);
+        d = dot2_acc<XDT>(xi.y, f.y, d);
+        d = dot2_acc<XDT>(xi.z, f.z, d);
+        d = dot2_acc<XDT>(xi.w, f.w, d);
+        acc[m][t] = fmaf(sc[t], d - (OFF + (float)(int8_t)zb[t]) * sx, acc[m][t]);
+      }
+    }
+  };
+#pragma unroll
+  for (int j = 0; j < NW; ++j)
+    if (lane + 64 * j < words) compute(lane + 64 * j, R[j]);
+#pragma unroll
+  for (int m = 0; m < TG_MR; ++m) {
+    if (m >= M) continue;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const float v = wave_sum(acc[m][t]);
+      const int64_t n = tile * T + t;
+      if (lane == 0 && n < N) {
+        if constexpr (OUT_F32) ((float*)y)[m * ys + n] = v;
+        else ((typename Elem<XDT>::T*)y)[m * ys + n] = Elem<XDT>::cvt(v);
+      }
+    }
+  }
+}
+
+// ANNA_MI_TILED_PLAIN=1 keeps the tiled GEMV off its LDS-staged form (for comparisons and tests)
+static const int g_tiled_plain = [] {
+  const char* v = getenv("ANNA_MI_TILED_PLAIN");
+  return v ? atoi(v) : 0;
+}();
+
 template <int XDT, int SDT, bool OUT_F32>
 int launch_tiled(const void* x, int64_t M, int64_t K, int64_t xs, const uint32_t* qw, int64_t tiles, int64_t pc,
                  int64_t T, const void* qs, const int8_t* qz, int64_t ssg, int64_t ssn, int64_t gsz, int64_t N, void* y,
@@ -491,6 +629,29 @@ int launch_tiled(const void* x, int64_t M, int64_t K, int64_t xs, const uint32_t
 #define ANNA_TILED_LAUNCH(TT)                                                                                  \
   hipLaunchKernelGGL((int4_gemv_tiled_kernel<XDT, SDT, TT, OUT_F32>), grid, dim3(256), 0, st, (const XT*)x, M, K, \
                      xs, qw, tiles, pc, (const ST*)qs, qz, ssg, ssn, gsz, N, y, ys)
+  // the LDS-staged form when x, its sums and four tiles' scales and zero points fit in 64 KB
+  const int64_t words = K / 8, G = (K + gsz - 1) / gsz;
+  const int64_t lds = ((M * words + 3) & ~(int64_t)3) * 20 + 4 * G * T * 4 + 4 * G * (T <= 4 ? 4 : 8);
+  if (XDT != ANNA_MI_F32 && K % 8 == 0 && xs % 8 == 0 && M >= 1 && M <= TG_MR && M * words <= 1024 &&
+      words <= 512 && lds <= 65536 && (uintptr_t)x % 16 == 0 && (uintptr_t)qw % 16 == 0 && !g_tiled_plain) {
+#define ANNA_TILED_LDS_LAUNCH(TT) \
+  if (words <= 256) \
+    hipLaunchKernelGGL((int4_gemv_tiled_lds_kernel<XDT, SDT, TT, 4, OUT_F32>), grid, dim3(256), (size_t)lds, st, \
+                       (const XT*)x, M, K, xs, qw, tiles, pc, (const ST*)qs, qz, ssg, ssn, gsz, N, y, ys); \
+  else \
+    hipLaunchKernelGGL((int4_gemv_tiled_lds_kernel<XDT, SDT, TT, 8, OUT_F32>), grid, dim3(256), (size_t)lds, st, \
+                       (const XT*)x, M, K, xs, qw, tiles, pc, (const ST*)qs, qz, ssg, ssn, gsz, N, y, ys)
+    switch (T) {
+      case 1: ANNA_TILED_LDS_LAUNCH(1); break;
+      case 2: ANNA_TILED_LDS_LAUNCH(2); break;
+      case 4: ANNA_TILED_LDS_LAUNCH(4); break;
+      case 8: ANNA_TILED_LDS_LAUNCH(8); break;
+      default: set_error("output tile must be 1, 2, 4 or 8 (got %lld)", (long long)T); return ANNA_MI_EINVAL;
+    }
+#undef ANNA_TILED_LDS_LAUNCH
+    ANNA_LAUNCH_CHECK("int4_gemv_tiled_lds_kernel");
+    return ANNA_MI_OK;
+  }
   switch (T) {
     case 1: ANNA_TILED_LAUNCH(1); break;
     case 2: ANNA_TILED_LAUNCH(2); break;

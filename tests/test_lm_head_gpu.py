@@ -47,10 +47,31 @@ def test_lm_head_int4_topk_matches_quantized_reference(gpu, k, n, seed, layout):
     assert torch.equal(indices, mi)
 
 
-@pytest.mark.parametrize("tile,sdt,m", [(1, torch.float32, 1), (2, torch.bfloat16, 3), (4, torch.float16, 5),
-                                        (8, torch.float32, 2)])
-def test_xpu_int4_gemv_tiled_matches_dequant(gpu, tile, sdt, m):
-    q = quantized_linear(256, 200, 11 + tile, gpu, group=64, dtype=torch.bfloat16)
+@pytest.mark.parametrize("k,n,seed,layout,rows", [(2048, 1000, 13, "lm_head", 1), (2048, 4096, 14, "lm_head", 4),
+                                                  (128, 20000, 15, "lm_head", 1), (200, 300, 16, "plain", 3),
+                                                  (64, 8193, 17, "plain", 2)])
+def test_lm_head_topk_few_rows(gpu, k, n, seed, layout, rows):
+    """One to four rows: the tiled GEMV's LDS-staged form (x and the tiles' scales and zero
+    points staged once per workgroup); K = 200 leaves the staged x rows unaligned to 4 words."""
+    q = quantized_linear(k, n, seed, gpu, group=32)
+    x = torch.randn(rows, k, device=gpu, dtype=torch.float16)
+    if layout == "lm_head":
+        q.prepare_lm_head_topk_layout()
+        tensors = (q.lm_head_qweight, q.lm_head_qscale, q.lm_head_qzeros)
+    else:
+        tensors = (q.qweight, q.qscale, q.qzeros)
+    values, indices = torch.ops.anna.lm_head_int4_topk_fused(x, *tensors, q.group_size, q.in_features, 6)
+    ref = dense_logits(q, x)
+    rv, ri = torch.topk(ref, 6, dim=-1)
+    assert torch.equal(indices.cpu(), ri)
+    torch.testing.assert_close(values.cpu().double(), rv, atol=2e-2, rtol=2e-2)
+
+
+@pytest.mark.parametrize("tile,sdt,m,k,group", [(1, torch.float32, 1, 256, 64), (2, torch.bfloat16, 3, 256, 64),
+                                                (4, torch.float16, 5, 256, 64), (8, torch.float32, 2, 256, 64),
+                                                (4, torch.bfloat16, 4, 200, 32), (8, torch.bfloat16, 1, 4096, 128)])
+def test_xpu_int4_gemv_tiled_matches_dequant(gpu, tile, sdt, m, k, group):
+    q = quantized_linear(k, 200, 11 + tile, gpu, group=group, dtype=torch.bfloat16)
     n, pc = q.qweight.shape
     n_pad = -(-n // tile) * tile
     qw = torch.zeros((n_pad, pc), dtype=torch.int32, device=gpu)
@@ -60,11 +81,11 @@ def test_xpu_int4_gemv_tiled_matches_dequant(gpu, tile, sdt, m):
     qz = torch.full((q.qzeros.shape[0], n_pad), 8, dtype=torch.int8, device=gpu)
     qz[:, :n] = q.qzeros
     qw_t = qw.view(n_pad // tile, tile, pc).permute(0, 2, 1).contiguous()
-    x = torch.randn(m, 256, device=gpu, dtype=torch.bfloat16)
+    x = torch.randn(m, k, device=gpu, dtype=torch.bfloat16)
     y = torch.ops.anna.xpu_int4_gemv_tiled(x, qw_t, qs.view(-1, n_pad // tile, tile), qz.view(-1, n_pad // tile, tile),
-                                           64, 256, n)
+                                           group, k, n)
     assert y.shape == (m, n) and y.dtype == torch.bfloat16
-    w = cp.int4_dequant_f32(q.qweight.cpu(), q.qscale.to(sdt).cpu(), q.qzeros.cpu(), 64, 256)
+    w = cp.int4_dequant_f32(q.qweight.cpu(), q.qscale.to(sdt).cpu(), q.qzeros.cpu(), group, k)
     ref = x.cpu().double() @ w.double().t()
     assert rel_err(y.cpu().double().numpy(), ref.numpy()) <= BF16_TOL
 
