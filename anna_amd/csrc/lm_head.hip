@@ -6,12 +6,12 @@
 // [G][N] (ss_g = N, ss_n = 1; also the tiled [G][N/T][T]) and the LM-head top-k layout [N][G]
 // (ss_g = 1, ss_n = G).  w = (q - z) * s.
 //
-//   int4_gemv_tiled_lds_kernel  (1..4 rows) the same with x and the tile scales and zero points
-//                           staged in LDS: one memory load per weight word
 //   int4_gemv_tiled_kernel  one wave per tile: lane l walks words l, l + 64, ... of the tile;
 //                           each word is one T x 4-byte coalesced load (8 k of T rows) used
 //                           against 8 activations of up to MR rows; fp32 accumulation
 //                           (s * (sum x q - z sum x) per word), wave reduction at the end.
+//   int4_gemv_tiled_lds_kernel  (1..4 rows) the same with x and the tile scales and zero points
+//                           staged in LDS: one memory load per weight word.
 //   topk_rows_kernel        k <= 8, per row, 1024 threads: pass 1 takes each thread's maximum and
 //                           merges the maxima into a top-k list; its k-th entry bounds the row's
 //                           k-th best from below.  Pass 2 keeps only the logits at or above that
