@@ -18,6 +18,10 @@
 //                           bound in sorted register lists, merged pairwise through LDS by a
 //                           bitonic merge (value descending, ties to the lower index).
 //   topk_rows_lds_kernel    k > 8: the same bound, the sorted lists in LDS.
+//   topk_chunk_wave_kernel, topk_merge_waves_kernel   k <= 8, few long rows (the fused LM head):
+//                           one wave per 1024 logits keeps register lists whose heads a
+//                           tournament across the lanes pops in order; one wave per row merges
+//                           the chunk lists the same way.
 #include <type_traits>
 
 #include "common.hpp"
@@ -235,9 +239,8 @@ inline int tk_threads(int kt) { return TK_LDS / (kt * 8) < 1024 ? TK_LDS / (kt *
 //          bitonic A ++ reverse(B)) and sorts that half with a bitonic network, in registers.
 // The earlier form (lists in LDS, a two-pointer merge) spent its time in chains of dependent
 // LDS reads: 24 us at V = 31, 240 us at V = 151936.
-// Chunked form (gridDim.x > 1, few rows): workgroup c takes elements [c S, c S + S) of its row
-// and writes its sorted top KT back over the first 2 KT floats of that range (values, then the
-// indices' bits; the range has been read by then), for topk_merge_chunks_kernel.
+// (Few long rows take the wave-level chunk kernels below instead.)  Elements [blockIdx.x S,
+// blockIdx.x S + S) of the row, clipped to V (S = V: the whole row).
 template <int ODT, int KT>
 __global__ __launch_bounds__(1024) void topk_rows_kernel(float* __restrict__ logits, int64_t V, int64_t ld, int k,
                                                          typename Elem<ODT>::T* __restrict__ out_v,
@@ -328,65 +331,123 @@ __global__ __launch_bounds__(1024) void topk_rows_kernel(float* __restrict__ log
     }
   }
   merge_tree();
-  if (gridDim.x > 1) {  // the chunk's list over the start of the chunk (every read of it is done)
-    if (tid < KT) {
-      lg[lo + tid] = lv[tid];
-      lg[lo + KT + tid] = __int_as_float(li[tid]);
-    }
-  } else if (tid < k) {  // the merged list is thread 0's
+  if (tid < k) {  // the merged list is thread 0's
     out_v[row * k + tid] = Elem<ODT>::cvt(lv[tid]);
     out_i[row * k + tid] = li[tid];
   }
 }
 
-// grid (rows), a power of two >= max(C, 64) threads: the C chunk lists of topk_rows_kernel's chunked
-// form, merged by the same tree.
-template <int ODT, int KT>
-__global__ __launch_bounds__(1024) void topk_merge_chunks_kernel(const float* __restrict__ logits, int64_t ld,
-                                                                 int64_t C, int64_t S, int k,
-                                                                 typename Elem<ODT>::T* __restrict__ out_v,
-                                                                 int64_t* __restrict__ out_i) {
-  extern __shared__ float tk_lists[];
-  const int nt = blockDim.x, tid = threadIdx.x;
-  const int64_t row = blockIdx.x;
-  const float* lg = logits + row * ld;
-  float* lv = tk_lists;
-  int32_t* li = (int32_t*)(tk_lists + nt * KT);
-  float rv[KT];
-  int32_t ri[KT];
+// Wave-level top-8 for few long rows.  Every lane keeps a sorted list (best first) of the
+// elements it reads; then eight rounds of a tournament over the lanes' list heads (a six-step
+// xor-shuffle arg-best, every lane ending with the winner) emit the wave's best 8 in order, the
+// lane that held each winner popping its head.  Order: larger value first, then smaller index
+// (tk_better); indices are unique, so the winner's lane is the one whose head carries its index.
+// (Butterfly merges of whole 8-lists between lanes cost about twice as long.)
+__device__ __forceinline__ void tk8_insert(float (&rv)[8], int32_t (&ri)[8], float v, int32_t i) {
+  if (!tk_better(v, i, rv[7], ri[7])) return;
+  rv[7] = v, ri[7] = i;
 #pragma unroll
-  for (int j = 0; j < KT; ++j) {
-    rv[j] = tid < C ? lg[tid * S + j] : -INFINITY;
-    ri[j] = tid < C ? __float_as_int(lg[tid * S + KT + j]) : INT32_MAX;
-  }
+  for (int j = 7; j >= 1; --j) tk_ce(rv[j - 1], ri[j - 1], rv[j], ri[j]);
+}
+
+__device__ __forceinline__ void tk8_wave_tournament(float (&rv)[8], int32_t (&ri)[8], float (&ov)[8], int32_t (&oi)[8]) {
 #pragma unroll
-  for (int j = 0; j < KT; ++j) lv[tid * KT + j] = rv[j], li[tid * KT + j] = ri[j];
-  __syncthreads();
-  for (int half = nt / 2; half >= 1; half >>= 1) {
-    if (tid < half) {
-      float bv[KT];
-      int32_t bi[KT];
+  for (int r = 0; r < 8; ++r) {
+    float bv = rv[0];
+    int32_t bi = ri[0];
 #pragma unroll
-      for (int j = 0; j < KT; ++j) bv[j] = lv[(tid + half) * KT + j], bi[j] = li[(tid + half) * KT + j];
-#pragma unroll
-      for (int j = 0; j < KT; ++j) {
-        if (tk_better(bv[KT - 1 - j], bi[KT - 1 - j], rv[j], ri[j])) rv[j] = bv[KT - 1 - j], ri[j] = bi[KT - 1 - j];
-      }
-#pragma unroll
-      for (int s = KT / 2; s >= 1; s >>= 1)
-#pragma unroll
-        for (int j = 0; j < KT; ++j)
-          if ((j & s) == 0) tk_ce(rv[j], ri[j], rv[j + s], ri[j + s]);
-#pragma unroll
-      for (int j = 0; j < KT; ++j) lv[tid * KT + j] = rv[j], li[tid * KT + j] = ri[j];
+    for (int m = 1; m < 64; m <<= 1) {
+      const float pv = __shfl_xor(bv, m, 64);
+      const int32_t pi = __shfl_xor(bi, m, 64);
+      if (tk_better(pv, pi, bv, bi)) bv = pv, bi = pi;
     }
-    __syncthreads();
-  }
-  if (tid < k) {
-    out_v[row * k + tid] = Elem<ODT>::cvt(lv[tid]);
-    out_i[row * k + tid] = li[tid];
+    ov[r] = bv, oi[r] = bi;
+    if (ri[0] == bi) {
+#pragma unroll
+      for (int j = 0; j < 7; ++j) rv[j] = rv[j + 1], ri[j] = ri[j + 1];
+      rv[7] = -INFINITY, ri[7] = INT32_MAX;
+    }
   }
 }
+
+// grid (C, rows), one wave per chunk: chunk c is [c S, c S + S), the last one [(C - 1) S, V)
+// (at least 16 elements: the host folds a shorter tail into it).  The chunk's best 8 are written
+// over its first 16 floats (values, then the indices' bits; the wave has read the chunk by then)
+// for topk_merge_waves_kernel.
+constexpr int TKW_PER = 16;  // elements per lane and batch of loads
+__global__ __launch_bounds__(64) void topk_chunk_wave_kernel(float* __restrict__ logits, int64_t V, int64_t ld,
+                                                             int64_t S) {
+  const int lane = threadIdx.x;
+  float* const lg = logits + (int64_t)blockIdx.y * ld;
+  const int64_t lo = (int64_t)blockIdx.x * S, hi = blockIdx.x + 1 == gridDim.x ? V : lo + S;
+  float rv[8];
+  int32_t ri[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) rv[j] = -INFINITY, ri[j] = INT32_MAX;
+  for (int64_t n0 = lo + lane; n0 < hi; n0 += 64 * TKW_PER) {
+    float v[TKW_PER];
+#pragma unroll
+    for (int j = 0; j < TKW_PER; ++j) {
+      const int64_t n = n0 + 64 * j;
+      v[j] = lg[n < hi ? n : lo];
+    }
+#pragma unroll
+    for (int j = 0; j < TKW_PER; ++j) {
+      const int64_t n = n0 + 64 * j;
+      if (n < hi) tk8_insert(rv, ri, v[j], (int32_t)n);
+    }
+  }
+  float ov[8];
+  int32_t oi[8];
+  tk8_wave_tournament(rv, ri, ov, oi);
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if (lane == j) {
+      lg[lo + j] = ov[j];
+      lg[lo + 8 + j] = __int_as_float(oi[j]);
+    }
+}
+
+// grid (rows), one wave: the C chunk lists of topk_chunk_wave_kernel merged the same way.
+template <int ODT>
+__global__ __launch_bounds__(64) void topk_merge_waves_kernel(const float* __restrict__ logits, int64_t ld, int64_t C,
+                                                              int64_t S, int k, typename Elem<ODT>::T* __restrict__ out_v,
+                                                              int64_t* __restrict__ out_i) {
+  const int lane = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const float* lg = logits + row * ld;
+  float rv[8];
+  int32_t ri[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) rv[j] = -INFINITY, ri[j] = INT32_MAX;
+  // every candidate's loads are issued before any is compared (one round trip for C <= 192;
+  // a batch of 4 per lane had taken a round trip each, 14 us at C = 148)
+  constexpr int NB = 24;
+  for (int64_t e0 = 0; e0 < C * 8; e0 += 64 * NB) {
+    float cv[NB];
+    int32_t ci[NB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int64_t e0u = e0 + lane + 64 * u, e = e0u < C * 8 ? e0u : 0;
+      const int64_t c = e / 8, j = e % 8;
+      cv[u] = lg[c * S + j];
+      ci[u] = __float_as_int(lg[c * S + 8 + j]);
+    }
+#pragma unroll
+    for (int u = 0; u < NB; ++u)
+      if (e0 + lane + 64 * u < C * 8) tk8_insert(rv, ri, cv[u], ci[u]);
+  }
+  float ov[8];
+  int32_t oi[8];
+  tk8_wave_tournament(rv, ri, ov, oi);
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if (lane == j && j < k) {
+      out_v[row * k + j] = Elem<ODT>::cvt(ov[j]);
+      out_i[row * k + j] = oi[j];
+    }
+}
+
 
 // k > 8: the lists stay in LDS (a register list of 16 or 32 entries and its partner spill), with
 // the same bound, batched loads and a register copy of the list's last entry; merged pairwise
@@ -717,18 +778,16 @@ int topk_rows(const float* values, int64_t rows, int64_t V, int64_t ld, int64_t 
     if (top_k <= 8) {
       // few long rows: each row is split over C workgroups whose lists a second launch merges
       // (one workgroup per row of V = 151936 took ~50 us, a chain of dependent passes)
-      const int64_t C = scratch_ok && rows <= 16 && V >= 8192 ? (V / 2048 < 128 ? V / 2048 : 128) : 1;
-      if (C > 1) {
-        const int64_t S = (V + C - 1) / C;  // >= 2048 > 2 KT
-        const int nt = 256;
-        hipLaunchKernelGGL((topk_rows_kernel<ODT, 8>), dim3((unsigned)C, (unsigned)rows), dim3(nt), (size_t)nt * 8 * 8,
-                           as_stream(stream), const_cast<float*>(values), V, ld, (int)top_k,
-                           (typename Elem<ODT>::T*)out_values, out_indices, S);
-        int mt = 64;  // a power of two >= C, and >= k: thread j writes output j
-        while (mt < C) mt <<= 1;
-        hipLaunchKernelGGL((topk_merge_chunks_kernel<ODT, 8>), dim3((unsigned)rows), dim3((unsigned)mt),
-                           (size_t)mt * 8 * 8, as_stream(stream), values, ld, C, S, (int)top_k,
-                           (typename Elem<ODT>::T*)out_values, out_indices);
+      // (one workgroup per row of V = 151936 took ~50 us, a chain of dependent passes; workgroup
+      // chunks merged by LDS trees ~26 us): one wave per 1024 elements, then one wave per row
+      if (scratch_ok && rows <= 16 && V >= 8192) {
+        const int64_t S = 64 * TKW_PER;
+        int64_t C = (V + S - 1) / S;
+        if (V - (C - 1) * S < 16) --C;  // the last chunk takes the short tail
+        hipLaunchKernelGGL(topk_chunk_wave_kernel, dim3((unsigned)C, (unsigned)rows), dim3(64), 0, as_stream(stream),
+                           const_cast<float*>(values), V, ld, S);
+        hipLaunchKernelGGL((topk_merge_waves_kernel<ODT>), dim3((unsigned)rows), dim3(64), 0, as_stream(stream),
+                           values, ld, C, S, (int)top_k, (typename Elem<ODT>::T*)out_values, out_indices);
       } else {
         const int nt = tk_threads(8);
         hipLaunchKernelGGL((topk_rows_kernel<ODT, 8>), dim3(1u, (unsigned)rows), dim3((unsigned)nt), (size_t)nt * 8 * 8,
