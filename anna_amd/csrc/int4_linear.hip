@@ -281,7 +281,7 @@ __global__ __launch_bounds__(64 * WMAX) void int4_gemv_dot2(
   constexpr uint32_t ONES = XDT == ANNA_MI_BF16 ? 0x3F803F80u : 0x3C003C00u;
   constexpr int SB = (int)sizeof(typename Elem<SDT>::T);
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kw = blockDim.x >> 6;
   const int sub = lane >> 4, c = lane & 15;
   const int64_t n0 = xcd_tile(blockIdx.x, gridDim.x) * RW;

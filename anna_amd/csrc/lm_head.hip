@@ -62,7 +62,7 @@ __global__ __launch_bounds__(256) void int4_gemv_tiled_kernel(
     int64_t tiles, int64_t pc, const typename Elem<SDT>::T* __restrict__ qs, const int8_t* __restrict__ qz,
     int64_t ss_g, int64_t ss_n, int64_t gsz, int64_t N, void* __restrict__ y, int64_t ys) {
   const int lane = threadIdx.x & 63;
-  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t tile = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (tile >= tiles) return;
   const int64_t words = (K + 7) / 8;
   const bool vec_x = (K % 8) == 0 && (xs % 8) == 0;
@@ -562,7 +562,7 @@ __global__ __launch_bounds__(256) void int4_gemv_tiled_lds_kernel(
   constexpr int ZB = T <= 4 ? 4 : 8;
   constexpr float OFF = XDT == ANNA_MI_BF16 ? 128.0f : 1024.0f;
   constexpr uint32_t ONES = XDT == ANNA_MI_BF16 ? 0x3F803F80u : 0x3C003C00u;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t tile = (int64_t)blockIdx.x * 4 + wave;
   const bool active = tile < tiles;
   const int64_t words = K / 8, G = (K + gsz - 1) / gsz;

@@ -850,7 +850,7 @@ __global__ __launch_bounds__(64) void tq_merge_kernel(const anna_mi_tq_decode_ar
 // leaves the ring (when length >= R), all waves then write the new token into the ring slot,
 // thread 0 increments the length.
 __global__ __launch_bounds__(256) void tq_append_kernel(const anna_mi_tq_append_args a) {
-  const int wave = threadIdx.x >> 6;
+  const int wave = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t b = blockIdx.x, H = a.kv_heads, R = a.residual_capacity;
   const int n = a.seq_lengths[b];
   const int64_t rpos = n % R;
@@ -886,7 +886,9 @@ __global__ __launch_bounds__(256) void tq_pack_kv_kernel(const anna_mi_tq_pack_a
   constexpr int NV = 4 * QPW;
   const int lane = threadIdx.x & 63;
   const int64_t groups = (a.tokens + NV - 1) / NV;
-  const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  // the wave index through readfirstlane: everything derived from it (token, head, addresses) is
+  // then wave-uniform and computed on the scalar unit, not per lane (the kernel is VALU-bound)
+  const int64_t wid = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (wid >= 2 * a.kv_heads * groups) return;  // whole wave
   const int64_t g = wid % groups, hv = wid / groups, h = hv >> 1;
   const bool is_v = hv & 1;

@@ -93,7 +93,7 @@ __global__ __launch_bounds__(256) void tq_ip_quantize_kernel(
     const float* __restrict__ gt, uint8_t* __restrict__ idx_out, uint8_t* __restrict__ qjl_out,
     float* __restrict__ norm_out, float* __restrict__ rn_out) {
   __shared__ float rl[4][IPNV * 64 * E];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int64_t v0 = ((int64_t)blockIdx.x * 4 + wave) * IPNV;
   float xv[IPNV][E];
 #pragma unroll
@@ -154,7 +154,7 @@ __global__ __launch_bounds__(256) void tq_ip_dequant_kernel(
     const float* __restrict__ cent, const float* __restrict__ g, float k0, typename Elem<ODT>::T* __restrict__ out,
     int64_t os) {
   __shared__ float sl[4][IPNV * 64 * E];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int64_t v0 = ((int64_t)blockIdx.x * 4 + wave) * IPNV;
   float* my = sl[wave];
   float c[IPNV][E];
@@ -204,7 +204,7 @@ __global__ __launch_bounds__(256) void tq_ip_query_kernel(const typename Elem<QD
                                                           const float* __restrict__ signs,
                                                           const float* __restrict__ gt, float* __restrict__ ws) {
   __shared__ float ql[4][64 * E];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int64_t r0 = (int64_t)blockIdx.x * 4 + wave;
   const int64_t r = r0 < rows ? r0 : rows - 1;
   const int64_t hq = r / Lq, lq = r % Lq;

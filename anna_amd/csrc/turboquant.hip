@@ -194,7 +194,7 @@ __global__ __launch_bounds__(256) void tq_hadamard_quantize_kernel(
     const float* __restrict__ signs, const float* __restrict__ thr, int bits, uint8_t* __restrict__ codes,
     uint16_t* __restrict__ norms) {
   const int lane = threadIdx.x & 63;
-  const int64_t v0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * HNV;
+  const int64_t v0 = ((int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * HNV;
   if (v0 >= nvec) return;  // whole wave
   float xv[HNV][E];
 #pragma unroll
@@ -339,7 +339,7 @@ __global__ __launch_bounds__(256) void tq_values_dequant_kernel(
 template <int XDT, int E>
 __global__ __launch_bounds__(1024) void tq_rows_append_kernel(const anna_mi_tq_rows_append_args a) {
   using T = typename Elem<XDT>::T;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t b = blockIdx.x, h = wave >> 1;
   const bool is_v = wave & 1;
   const int64_t H = a.kv_heads, D = a.head_dim, R = a.residual_capacity, C = a.capacity;
