@@ -119,3 +119,28 @@ def test_topk_rows_exact_with_ties(gpu, v, rows, k):
         order = sorted(range(v), key=lambda i: (-float(vals[r, i]), i))[:k]
         assert out_i[r].cpu().tolist() == order
         assert torch.equal(out_v[r].cpu(), vals[r, order])
+
+
+@pytest.mark.parametrize("layout", ["lm_head", "plain"])
+def test_lm_head_topk_exact_ties_in_wave_path(gpu, layout):
+    """Few long rows take the wave-level top-k (chunk lists and a head tournament across lanes):
+    with every weight row duplicated 6144 rows later, each logit ties exactly with its twin, and
+    the pairs must come out value-descending, lower index first."""
+    torch.manual_seed(99)
+    dense = torch.nn.Linear(256, 12288, bias=False, dtype=torch.float32)
+    with torch.no_grad():
+        dense.weight[6144:] = dense.weight[:6144]
+    q = XPUInt4Linear.from_linear(dense, group_size=32, compute_dtype=torch.float16, device=gpu)
+    x = torch.randn(2, 256, device=gpu, dtype=torch.float16)
+    if layout == "lm_head":
+        q.prepare_lm_head_topk_layout()
+        tensors = (q.lm_head_qweight, q.lm_head_qscale, q.lm_head_qzeros)
+    else:
+        tensors = (q.qweight, q.qscale, q.qzeros)
+    values, indices = torch.ops.anna.lm_head_int4_topk_fused(x, *tensors, q.group_size, q.in_features, 8)
+    ref = dense_logits(q, x)
+    for r in range(2):
+        order = sorted(range(12288), key=lambda i: (-float(ref[r, i]), i))[:8]
+        assert indices[r].cpu().tolist() == order
+        got = values[r].float().cpu()
+        assert torch.equal(got[0::2], got[1::2])  # twins carry the same value
