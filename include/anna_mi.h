@@ -443,7 +443,8 @@ int anna_mi_topk_rows(const float* values, int64_t rows, int64_t V, int64_t ld, 
 
 /* lm_head_int4_topk_fused (sycl:2137-2572; caller qwen3_5_text_model.py:65-110): fp32 logits of
  * the int4 LM head into the workspace `logits` [rows][vocab], then their top-k (values in the
- * activation dtype). */
+ * activation dtype).  `logits` is scratch: for few long rows the top-k writes its partial lists
+ * over it, so it does not hold the logits afterwards. */
 int anna_mi_lm_head_int4_topk(const void* x, int x_dtype, int64_t rows, int64_t K, int64_t x_row_stride,
                               const int32_t* qweight, int64_t tiles, int64_t packed_cols, int64_t tile,
                               const void* qscale, int scale_dtype, const int8_t* qzeros, int64_t group_count,
