@@ -486,7 +486,7 @@ def section_moe(args, device):
 
 
 def section_lm_head(args, device):
-    """The fused int4 LM-head top-k (not a BASELINE config): one token's hidden
+    """The fused int4 LM-head top-k (lm_head_int4_topk_fused, sycl:2137-2572; not a BASELINE config): one token's hidden
     state [1, 2048] against a 151936-row int4 head (group 128) in the reference's top-k layout,
     top 8.  Two weight copies (2 x 163 MB) alternate, more than the Infinity Cache."""
     from anna_amd import fused_ops
