@@ -13,10 +13,11 @@ Differences by design:
     (`TurboQuantMSE` below, seed 42 like the reference's call sites, turboquant.py:75-92);
     the third-party `turboquant` package the reference imports is not available, so its
     exact codes cannot be reproduced.
-  * ``TurboQuantKVRow`` keeps its keys as TQ-MSE codes + fp16 norms (the reference keeps
-    TurboQuantIP state and decodes keys back to bf16, turboquant.py:1104-1111) and its
-    values in the reference's min/max format; ``decode_attention`` scores the packed keys
-    against the rotated query directly, so nothing is dequantized per step.
+  * ``TurboQuantKVRow`` keeps the reference's key state by default (TurboQuantIP indices,
+    norms, QJL signs and residual norms, decoded from their reconstruction in the cache dtype,
+    turboquant.py:1098-1111) and its values in the reference's min/max format.
+    ``key_quantizer="mse"`` is an opt-in fast mode: TQ-MSE key codes + fp16 norms, scored
+    against the rotated query directly, so a key costs D/4 bytes instead of 2*D.
   * Every quantize / dequantize / attention step runs in the HIP library; host tensors
     are rejected.
 """
@@ -385,16 +386,17 @@ class TurboQuantTensorRow:
 class TurboQuantKVRow:
     """Compressed K/V cache of one sequence (reference turboquant.py:480-1443).
 
-    Keys: TQ-MSE codes + fp16 norms by default; with ``key_quantizer="ip"`` the reference's
-    inner-product key state (``TurboQuantKeyState``) plus its dense reconstruction in the
-    cache dtype, which decode reads as the reference's XPU path does (turboquant.py:1098-1111).
+    Keys: by default (``key_quantizer="ip"``, the reference's semantics) the inner-product key
+    state (``TurboQuantKeyState``) plus its dense reconstruction in the cache dtype, which decode
+    reads as the reference's XPU path does (turboquant.py:1098-1111); ``key_quantizer="mse"``
+    (opt-in fast mode) keeps TQ-MSE codes + fp16 norms and scores them from the codes.
     Values: min/max groups (reference format); the newest ``residual_len`` tokens stay dense.
     ``decode_attention`` runs one split-KV launch over [packed prefix ++ residual] with all
     q-heads of a KV head sharing reads.
     """
 
     def __init__(self, *, bits: int, residual_len: int, value_group_size: int | None = None,
-                 key_quantizer: str = "mse") -> None:
+                 key_quantizer: str = "ip") -> None:
         if key_quantizer not in ("mse", "ip"):
             raise ValueError(f"key_quantizer must be 'mse' or 'ip', got {key_quantizer!r}")
         self.key_quantizer = key_quantizer

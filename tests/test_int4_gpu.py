@@ -89,6 +89,31 @@ def test_int4_gemm_every_tile_shape(gpu, monkeypatch, tile, m, k, n, group, sdt)
     assert rel_err(y.float().cpu().numpy(), ref) <= BF16_TOL
 
 
+@pytest.mark.parametrize("m,n", [(256, 6144), (256, 12288), (2048, 6144), (2048, 12288)])
+def test_int4_gemm_config2_bench_sizes(gpu, monkeypatch, m, n):
+    """BASELINE config 2's large-M points (K = 4096, group 128, bf16 scales) at exactly the grid
+    sizes the bench times, with the production tile choice.  The oracle checks 64 random output
+    columns over every row and 16 random full rows (<= 0.8 GMAC of fp64 work)."""
+    monkeypatch.delenv("ANNA_MI_INT4_GEMM_TILE", raising=False)
+    k, group = 4096, 128
+    print(f"[case] int4 GEMM config-2 M={m} N={n} K={k}", flush=True)
+    rng = np.random.default_rng(m + n)
+    qw, qs, qz = int4_payload(rng, n, k, group, scale_dtype="bf16")
+    xb = orc.bf16_bits(rng.normal(size=(m, k)).astype(np.float32))
+    x = _x_tensor(xb, torch.bfloat16, gpu)
+    y = torch.ops.anna.xpu_int4_gemv(x, _dev(qw, gpu), _dev(qs, gpu).to(torch.bfloat16), _dev(qz, gpu), group, k)
+    torch.cuda.synchronize()
+    y = y.float().cpu().numpy()
+    cols = np.sort(rng.choice(n, size=64, replace=False))
+    ref_c = orc.int4_linear(xb, qw[cols], qs[:, cols], qz[:, cols], group)
+    assert rel_err(y[:, cols], ref_c) <= BF16_TOL
+    rows = np.sort(rng.choice(m, size=16, replace=False))
+    ref_r = orc.int4_linear(np.ascontiguousarray(xb[rows]), qw, qs, qz, group)
+    assert rel_err(y[rows], ref_r) <= BF16_TOL
+    # every column of every row is finite and non-trivial (no unwritten tile)
+    assert np.isfinite(y).all() and (np.abs(y).max(axis=0) > 0).all()
+
+
 @pytest.mark.parametrize("xdt", [torch.float16, torch.float32])
 @pytest.mark.parametrize("m", [1, 4, 128])
 def test_int4_linear_other_activation_dtypes(gpu, xdt, m):

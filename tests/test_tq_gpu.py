@@ -248,7 +248,7 @@ def test_splitkv_tq_mse_keys(gpu, vfmt):
 def test_kv_row_lengths_storage_reuse_and_residual(gpu):
     # reference tests/test_model_shapes.py:379-546 row invariants
     torch.manual_seed(40)
-    row = TurboQuantKVRow(bits=2, residual_len=4)
+    row = TurboQuantKVRow(bits=2, residual_len=4, key_quantizer="mse")
     k = torch.randn(2, 9, 64, device=gpu, dtype=torch.bfloat16)
     v = torch.randn(2, 9, 64, device=gpu, dtype=torch.bfloat16)
     row.append(k, v)
@@ -279,7 +279,7 @@ def test_kv_row_lengths_storage_reuse_and_residual(gpu):
 def test_kv_row_decode_attention_matches_oracle(gpu, bits):
     torch.manual_seed(41 + bits)
     hkv, groups, d, r = 2, 4, 128, 16
-    row = TurboQuantKVRow(bits=bits, residual_len=r)
+    row = TurboQuantKVRow(bits=bits, residual_len=r, key_quantizer="mse")
     for n in (50, 1, 1, 30):
         row.append(torch.randn(hkv, n, d, device=gpu, dtype=torch.bfloat16),
                    torch.randn(hkv, n, d, device=gpu, dtype=torch.bfloat16))
