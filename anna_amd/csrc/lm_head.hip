@@ -777,7 +777,6 @@ int topk_rows(const float* values, int64_t rows, int64_t V, int64_t ld, int64_t 
   ANNA_DISPATCH_DTYPE(out_dtype, ODT, {
     if (top_k <= 8) {
       // few long rows: each row is split over C workgroups whose lists a second launch merges
-      // (one workgroup per row of V = 151936 took ~50 us, a chain of dependent passes)
       // (one workgroup per row of V = 151936 took ~50 us, a chain of dependent passes; workgroup
       // chunks merged by LDS trees ~26 us): one wave per 1024 elements, then one wave per row
       if (scratch_ok && rows <= 16 && V >= 8192) {

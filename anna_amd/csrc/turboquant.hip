@@ -330,17 +330,18 @@ __global__ __launch_bounds__(256) void tq_values_dequant_kernel(
 
 // One token per sequence into a cache with one region per (sequence, KV head) -- the general
 // form of the batched cache (any head_dim the Hadamard rotation takes, key bits 1..4, value bits
-// 2..4): one workgroup per sequence, waves 2h and 2h + 1 take KV head h's key and value.  When
-// the window is full the token leaving it (ring slot n % R) is quantized into packed slot n - R
-// -- keys as Hadamard TQ-MSE codes + norm (bit-exact with anna_mi_tq_hadamard_quantize), values
-// as min/max groups (bit-exact with anna_mi_tq_values_quantize) -- then, after a barrier, the
-// new token takes the slot and the length grows by one.  A sequence whose packed region is full
-// is left as it is and raises the overflow flag.
+// 2..4): one workgroup per sequence of 2 * min(H, 8) waves; wave w takes the key (w even) or the
+// value (w odd) of KV heads w / 2, w / 2 + 8, ...  When the window is full the token leaving it
+// (ring slot n % R) is quantized into packed slot n - R -- keys as Hadamard TQ-MSE codes + norm
+// (bit-exact with anna_mi_tq_hadamard_quantize), values as min/max groups (bit-exact with
+// anna_mi_tq_values_quantize) -- then, after a barrier, the new token takes the slot and the
+// length grows by one.  A sequence whose packed region is full is left as it is and raises the
+// overflow flag.
 template <int XDT, int E>
 __global__ __launch_bounds__(1024) void tq_rows_append_kernel(const anna_mi_tq_rows_append_args a) {
   using T = typename Elem<XDT>::T;
   const int lane = threadIdx.x & 63, wave = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t b = blockIdx.x, h = wave >> 1;
+  const int64_t b = blockIdx.x, hstep = blockDim.x >> 7;
   const bool is_v = wave & 1;
   const int64_t H = a.kv_heads, D = a.head_dim, R = a.residual_capacity, C = a.capacity;
   const int n = a.seq_lengths[b];
@@ -349,31 +350,39 @@ __global__ __launch_bounds__(1024) void tq_rows_append_kernel(const anna_mi_tq_r
     if (threadIdx.x == 0) *a.overflow = 1;
     return;
   }
-  const int64_t row = b * H + h, slot = n % R;
-  T* ring = (T*)(is_v ? a.residual_value : a.residual_key) + (row * R + slot) * D;
+  const int64_t slot = n % R;
   if (evict) {
     const int64_t q = n - R;
-    if (!is_v) {
-      float x[E];
+    for (int64_t h = wave >> 1; h < H; h += hstep) {
+      const int64_t row = b * H + h;
+      const T* ring = (const T*)(is_v ? a.residual_value : a.residual_key) + (row * R + slot) * D;
+      if (!is_v) {
+        float x[E];
 #pragma unroll
-      for (int e = 0; e < E; ++e) x[e] = Elem<XDT>::to_f32(ring[lane * E + e]);
-      uint32_t code[E];
-      const float nrm = hadamard_codes_wave<E>(x, a.signs, a.thresholds, (1 << a.key_bits) - 1, tq_inv_sqrt(D), code);
-      const int sb = storage_bits(a.key_bits);
-      store_codes_wave<E>(code, sb, a.key_codes + (row * C + q) * (D * sb / 8), lane);
-      if (lane == 0) a.key_norms[row * C + q] = f32_to_f16_bits(nrm);
-    } else {
-      const int64_t gs = a.value_group_size, ng = D / gs;
-      const int64_t gpt = value_groups_per_run(a.value_bits, D, gs);
-      const int64_t pb = D * storage_bits(a.value_bits) / 8;
-      for (int64_t r = lane; r < ng / gpt; r += 64)
-        quantize_value_run<XDT>(ring, D, a.value_bits, gs, r * gpt, gpt, a.value_data + (row * C + q) * pb,
-                                (T*)a.value_scales + (row * C + q) * ng, (T*)a.value_zeros + (row * C + q) * ng);
+        for (int e = 0; e < E; ++e) x[e] = Elem<XDT>::to_f32(ring[lane * E + e]);
+        uint32_t code[E];
+        const float nrm =
+            hadamard_codes_wave<E>(x, a.signs, a.thresholds, (1 << a.key_bits) - 1, tq_inv_sqrt(D), code);
+        const int sb = storage_bits(a.key_bits);
+        store_codes_wave<E>(code, sb, a.key_codes + (row * C + q) * (D * sb / 8), lane);
+        if (lane == 0) a.key_norms[row * C + q] = f32_to_f16_bits(nrm);
+      } else {
+        const int64_t gs = a.value_group_size, ng = D / gs;
+        const int64_t gpt = value_groups_per_run(a.value_bits, D, gs);
+        const int64_t pb = D * storage_bits(a.value_bits) / 8;
+        for (int64_t r = lane; r < ng / gpt; r += 64)
+          quantize_value_run<XDT>(ring, D, a.value_bits, gs, r * gpt, gpt, a.value_data + (row * C + q) * pb,
+                                  (T*)a.value_scales + (row * C + q) * ng, (T*)a.value_zeros + (row * C + q) * ng);
+      }
     }
   }
   __syncthreads();  // every read of the leaving token is done before its slot is overwritten
-  const T* src = (const T*)(is_v ? a.new_value : a.new_key) + row * D;
-  for (int64_t i = lane; i < D; i += 64) ring[i] = src[i];
+  for (int64_t h = wave >> 1; h < H; h += hstep) {
+    const int64_t row = b * H + h;
+    T* ring = (T*)(is_v ? a.residual_value : a.residual_key) + (row * R + slot) * D;
+    const T* src = (const T*)(is_v ? a.new_value : a.new_key) + row * D;
+    for (int64_t i = lane; i < D; i += 64) ring[i] = src[i];
+  }
   __syncthreads();
   if (threadIdx.x == 0) a.seq_lengths[b] = n + 1;
 }
@@ -532,13 +541,13 @@ extern "C" int anna_mi_tq_rows_append(const anna_mi_tq_rows_append_args* ap, voi
   ANNA_CHECK(a.value_bits >= 2 && a.value_bits <= 4, "anna_mi_tq_rows_append: value bits must be 2..4");
   ANNA_CHECK(a.value_group_size > 0 && a.head_dim % a.value_group_size == 0,
              "anna_mi_tq_rows_append: value_group_size must divide head_dim");
-  ANNA_CHECK(a.batch > 0 && a.kv_heads > 0 && a.kv_heads <= 8, "anna_mi_tq_rows_append: 1..8 KV heads");
+  ANNA_CHECK(a.batch > 0 && a.kv_heads > 0 && a.kv_heads <= 4096, "anna_mi_tq_rows_append: 1..4096 KV heads");
   ANNA_CHECK(a.capacity >= 0 && a.residual_capacity > 0, "anna_mi_tq_rows_append: bad capacities");
   ANNA_CHECK(a.new_key && a.new_value && a.residual_key && a.residual_value && a.seq_lengths && a.overflow && a.signs &&
                  a.thresholds && (a.capacity == 0 || (a.key_codes && a.key_norms && a.value_data && a.value_scales &&
                                                       a.value_zeros)),
              "anna_mi_tq_rows_append: null pointer");
-  const dim3 grid((unsigned)a.batch), blk((unsigned)(128 * a.kv_heads));
+  const dim3 grid((unsigned)a.batch), blk((unsigned)(128 * (a.kv_heads < 8 ? a.kv_heads : 8)));
   ANNA_DISPATCH_DTYPE(a.dtype, XDT, {
     auto go = [&](auto e_tag) {
       constexpr int E = decltype(e_tag)::value;

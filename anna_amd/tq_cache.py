@@ -253,8 +253,8 @@ class TurboQuantRowsCache(TurboQuantBatchCache):
             raise ValueError("TurboQuantBatchCache needs a power-of-two head_dim in [64, 1024]")
         if bits not in (2, 3, 4):
             raise ValueError(f"Unsupported TurboQuant KV bit-width: {bits}. Expected 2, 3, or 4.")
-        if q_heads % kv_heads != 0 or q_heads // kv_heads > (8 if head_dim >= 512 else 16) or kv_heads > 8:
-            raise ValueError("q_heads must be G * kv_heads with G <= 16 (8 at head_dim 512+), kv_heads <= 8")
+        if q_heads % kv_heads != 0 or q_heads // kv_heads > (8 if head_dim >= 512 else 16):
+            raise ValueError("q_heads must be G * kv_heads with G <= 16 (8 at head_dim 512+)")
         self.batch, self.kv_heads, self.q_heads, self.head_dim, self.bits = batch, kv_heads, q_heads, head_dim, bits
         self.device = torch.device(device)
         self.capacities = [int(c) for c in capacities]

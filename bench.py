@@ -317,7 +317,40 @@ def section_row_decode(args, device):
          "distinct_cache_copies": len(caches)}
     log(f"row-API decode B=8 L={L}+{R}: {r['us']:.2f} us/call  {r['GB/s']:.0f} GB/s  "
         f"{100 * r['roofline_frac']:.1f}% of HBM peak")
+    cpu = None
+    if not args.no_cpu:
+        from anna_amd.turboquant import TurboQuantValueState, dequantize_turboquant_values
+        from oracle.cpu_paths import tq_decode_rows
+
+        k, vd, vs, vz, rk, rv = first
+        st = TurboQuantValueState(data=vd.reshape(B * HKV, L, -1), scales=vs.reshape(B * HKV, L, -1),
+                                  zeros=vz.reshape(B * HKV, L, -1), bits=BITS, group_size=GROUP)
+        vals = dequantize_turboquant_values(st, dtype=torch.bfloat16).view(B, HKV, L, D)
+        # the CPU branch decodes against its kept bf16 cache (turboquant.py:1289-1294): keys and
+        # dequantized values of the packed prefix followed by the window
+        ks = [torch.cat((k[b], rk[b]), dim=1).cpu() for b in range(B)]
+        vs_ = [torch.cat((vals[b], rv[b]), dim=1).cpu() for b in range(B)]
+        qc = q.squeeze(2).cpu()
+        cpu = _time_cpu(lambda: tq_decode_rows(qc, ks, vs_, D ** -0.5), args.cpu_seconds / 4)
+        cpu = {"value": B / cpu["sec"], "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"{cpu['iters']} calls of the reference CPU decode branch (turboquant.py:1289-1311: bf16 "
+                         f"matmuls over the kept dequantized cache, fp32 softmax), B={B} L={L}+{R}; "
+                         f"{cpu['sec'] * 1e3:.1f} ms/call"}
+        log(f"row-API decode cpu baseline: {cpu['value']:.1f} tokens/s")
+    r["cpu_baseline"] = cpu
     return r
+
+
+def _time_cpu(fn, budget_s: float, max_iters: int = 50) -> dict:
+    """Mean wall time of fn() on the host cores (one untimed warm-up call, then calls until
+    budget_s is spent or max_iters are done)."""
+    torch.set_num_threads(os.cpu_count() or 1)
+    fn()
+    iters, t0 = 0, time.perf_counter()
+    while iters < max_iters and (iters == 0 or time.perf_counter() - t0 < budget_s):
+        fn()
+        iters += 1
+    return {"sec": (time.perf_counter() - t0) / iters, "iters": iters}
 
 
 def section_tq_pack(args, device):
@@ -364,6 +397,64 @@ def section_tq_pack(args, device):
          "quantizer": qn.kind}
     log(f"tq pack K+V [8192,2,256]: {r['us']:.1f} us  {r['vectors/s'] / 1e6:.2f} M vectors/s  "
         f"{r['GB/s']:.0f} GB/s  {100 * r['roofline_frac']:.1f}% of HBM peak")
+    cpu = None
+    if not args.no_cpu:
+        from oracle.cpu_paths import tq_tensor_row_append
+
+        # the reference's CPU path: TurboQuantTensorRow.append of the prefill for K and for V,
+        # through the published quantizer with its dense D x D rotation (a seeded Haar matrix)
+        g = torch.Generator().manual_seed(42)
+        rot, _ = torch.linalg.qr(torch.randn((D, D), generator=g))
+        cent = qn.centroids.float().cpu()
+        kc, vc = kvs[0][0].cpu(), kvs[0][1].cpu()
+        t = _time_cpu(lambda: (tq_tensor_row_append(kc, R, rot, cent), tq_tensor_row_append(vc, R, rot, cent)),
+                      args.cpu_seconds / 4, max_iters=20)
+        cpu = {"value": 2 * n / t["sec"], "unit": "vectors/s", "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"{t['iters']} prefills of K and V [{H},{T},{D}] through TurboQuantTensorRow.append's "
+                         f"CPU path (turboquant.py:353-405 with the published TurboQuant-MSE quantizer: norm, dense "
+                         f"rotation, nearest centroid); {t['sec'] * 1e3:.1f} ms per prefill pair"}
+        log(f"tq pack cpu baseline: {cpu['value'] / 1e6:.3f} M vectors/s")
+    r["cpu_baseline"] = cpu
+    return r
+
+
+def section_tq_rows(args, device):
+    """The batched cache for the shapes other than head_dim 256 / 2-bit (TurboQuantRowsCache):
+    B=8, Hq=16, Hkv=2, head_dim 128, 4-bit keys and values, L ~ U[1024, 16384] + 128 bf16 window."""
+    import numpy as np
+
+    from anna_amd.tq_cache import TurboQuantRowsCache
+
+    rng = np.random.default_rng(5)
+    B, HQ, HKV, D, R, BITS = 8, 16, 2, 128, 128, 4
+    lens = [int(v) for v in rng.integers(1024, 16385, size=B)]
+    gen = torch.Generator(device=device)
+    gen.manual_seed(55)
+
+    def make():
+        c = TurboQuantRowsCache(batch=B, kv_heads=HKV, q_heads=HQ, capacities=lens, residual_capacity=R,
+                                head_dim=D, bits=BITS, device=device)
+        for b in range(B):
+            k = torch.randn((HKV, lens[b] + R, D), device=device, generator=gen).to(torch.bfloat16)
+            v = torch.randn((HKV, lens[b] + R, D), device=device, generator=gen).to(torch.bfloat16)
+            c.load_sequence(b, k, v)
+        return c
+
+    first = make()
+    per_call = first.bytes_per_decode()
+    caches = [first] + [make() for _ in range(max(1, math.ceil(ROTATE_BYTES / per_call)) - 1)]
+    q = torch.randn((B, HQ, D), device=device, generator=gen).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    for c in caches:  # size the partial buffers outside the captured region
+        c.decode(q, scaling=D ** -0.5, out=out)
+    ms = time_graph([(lambda c=c: c.decode(q, scaling=D ** -0.5, out=out)) for c in caches], args.steps, args.warmup)
+    sec = ms / 1e3
+    r = {"B": B, "Hq": HQ, "Hkv": HKV, "D": D, "bits": BITS, "lens": lens, "residual": R, "ms": ms, "us": ms * 1e3,
+         "tokens/s": B / sec, "bytes": per_call, "GB/s": per_call / sec / 1e9,
+         "roofline_frac": per_call / sec / 1e9 / HBM_PEAK_GBS, "distinct_cache_copies": len(caches),
+         "launches": 3}
+    log(f"tq rows decode D={D} {BITS}-bit: {r['us']:.2f} us/call  {r['GB/s']:.0f} GB/s  "
+        f"{100 * r['roofline_frac']:.1f}% of HBM peak")
     return r
 
 
@@ -548,7 +639,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=60)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--sections", default="int4,tq_decode,row_decode,tq_pack,moe,lm_head")
+    ap.add_argument("--sections", default="int4,tq_decode,row_decode,tq_pack,tq_rows,moe,lm_head")
     ap.add_argument("--tq-tokens-per-item", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -581,6 +672,8 @@ def main() -> int:
         sections["row_decode"] = section_row_decode(args, device)
     if "tq_pack" in wanted:
         sections["tq_pack"] = section_tq_pack(args, device)
+    if "tq_rows" in wanted:
+        sections["tq_rows"] = section_tq_rows(args, device)
     if "moe" in wanted:
         sections["moe"] = section_moe(args, device)
     if "lm_head" in wanted:

@@ -257,8 +257,10 @@ int anna_mi_gqa_decode_splitkv(const anna_mi_decode_args* args, void* stream);
  * serving loops, harnesses that forbid hipMalloc).  The partial_stats, partial_values,
  * partial_capacity and query_rot fields of args are ignored; that workspace lives in a static
  * device array of anna_mi_gqa_decode_splitkv_noalloc_capacity() bytes (32 MiB) per GPU, held
- * until the process ends.  The call fails with ANNA_MI_EINVAL when the workspace
- * (4 * (B*Hq*nblk*(D+2) + B*Hq*D) bytes, nblk = anna_mi_decode_num_blocks) does not fit.
+ * until the process ends.  The call fails with ANNA_MI_EINVAL when the workspace does not
+ * fit: 4 * (up(B*Hq*nblk*2) + up(B*Hq*nblk*D) + up(B*Hq*D)) bytes, up(n) = n rounded up to a
+ * multiple of 64 (each part 256-byte aligned), nblk = anna_mi_decode_num_blocks, the last term
+ * only for TQ-MSE keys.
  * Every call on one GPU shares that GPU's array: calls that overlap on one GPU race.  It
  * allocates nothing and launches the same kernels, so results equal anna_mi_gqa_decode_splitkv's. */
 int anna_mi_gqa_decode_splitkv_noalloc(const anna_mi_decode_args* args, void* stream);

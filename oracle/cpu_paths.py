@@ -50,6 +50,31 @@ def tq_decode_rows(query: torch.Tensor, keys: list, values: list, scaling: float
     return torch.stack(outs)
 
 
+def tq_mse_quantize(flat: torch.Tensor, rotation: torch.Tensor, centroids: torch.Tensor):
+    """The published TurboQuant-MSE quantizer the reference calls through the third-party
+    `TurboQuantMSE.quantize` (turboquant.py:75-82 builds it, TurboQuantTensorRow.append
+    turboquant.py:398-405 calls it on the tokens leaving the window): per vector the norm, the
+    unit vector rotated by the dense D x D orthogonal matrix (y = u R^T, fp32), and per
+    coordinate the index of the nearest codebook centroid.  flat [n, D] -> (int64 indices
+    [n, D], norms [n, 1] in flat's dtype)."""
+    x = flat.to(torch.float32)
+    norms = x.norm(dim=-1, keepdim=True)
+    y = (x / norms.clamp_min(1e-12)) @ rotation.t()
+    idx = torch.argmin((y.unsqueeze(-1) - centroids).abs(), dim=-1)
+    return idx, norms.to(flat.dtype)
+
+
+def tq_tensor_row_append(tensor: torch.Tensor, residual_len: int, rotation: torch.Tensor,
+                         centroids: torch.Tensor):
+    """TurboQuantTensorRow.append of a whole [H, T, D] prefill into an empty row
+    (turboquant.py:353-405): the oldest T - residual_len tokens are quantized, the newest
+    residual_len stay as they are."""
+    h, t, d = tensor.shape
+    over = max(0, t - residual_len)
+    idx, norms = tq_mse_quantize(tensor[:, :over].reshape(-1, d), rotation, centroids)
+    return idx.reshape(h, over, d), norms.reshape(h, over, 1), tensor[:, over:].contiguous()
+
+
 # ---------------------------------------------------------------- MoE (ops.py:3280-3376)
 
 

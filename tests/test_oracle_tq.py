@@ -228,3 +228,26 @@ def test_hadamard_mse_distortion_matches_turboquant_paper(bits, expected):
     xh = orc.tq_mse_dequant(codes, norms, orc.tq_hadamard_matrix(s).astype(np.float32), cent, bits)
     mse = float(((xh - x) ** 2).sum(1).mean())
     assert abs(mse - expected) / expected < 0.12, mse
+
+
+def test_cpu_path_tensor_row_append_matches_the_oracle_quantizer():
+    """The torch restatement timed as the pack's CPU baseline (nearest centroid after a dense
+    rotation) gives the oracle's codes (threshold count at the centroid midpoints) and norms,
+    and keeps the newest residual_len tokens as they are."""
+    import torch
+
+    from oracle.cpu_paths import tq_tensor_row_append
+
+    d, bits = 64, 2
+    rng = np.random.default_rng(7)
+    x = rng.normal(size=(2, 40, d)).astype(np.float32)
+    r = fused_ops.tq_rotation(d, 42).numpy()
+    cent, thr = (t.numpy() for t in fused_ops.tq_codebook(bits, d))
+    idx, norms, resid = tq_tensor_row_append(torch.from_numpy(x), 8, torch.from_numpy(r), torch.from_numpy(cent))
+    assert idx.shape == (2, 32, d) and norms.shape == (2, 32, 1)
+    np.testing.assert_array_equal(resid.numpy(), x[:, 32:])
+    codes, _ = orc.tq_mse_quantize(np.ascontiguousarray(x[:, :32].reshape(-1, d)), orc.F32, r, thr, bits)
+    unpacked = np.stack([(codes >> (2 * e)) & 3 for e in range(4)], -1).reshape(-1, d)
+    np.testing.assert_array_equal(idx.reshape(-1, d).numpy(), unpacked)
+    np.testing.assert_allclose(norms.reshape(-1).numpy(), np.linalg.norm(x[:, :32].reshape(-1, d), axis=1),
+                               rtol=1e-6)

@@ -76,15 +76,17 @@ def check_rows(cache, hist_k, hist_v, q, out, gate=None):
         assert rel_err(out[b], ref) <= BF16_TOL, b
 
 
-@pytest.mark.parametrize("d,bits,gated", [(128, 2, False), (64, 3, True), (256, 3, False), (256, 4, True),
-                                          (512, 2, False)])
-def test_rows_cache_load_append_decode(gpu, d, bits, gated):
+@pytest.mark.parametrize("d,bits,gated,hkv,g", [(128, 2, False, 2, 8), (64, 3, True, 2, 8), (256, 3, False, 2, 8),
+                                                (256, 4, True, 2, 8), (512, 2, False, 2, 8), (128, 4, False, 16, 2),
+                                                (64, 2, True, 11, 1)])
+def test_rows_cache_load_append_decode(gpu, d, bits, gated, hkv, g):
     """Three sequences (75 / 20 / 0 tokens, a 32-token window), decoded, then 12 steps of
     append + decode: sequence 0 evicts a token every step, sequence 1 fills its window and
-    starts evicting, sequence 2 grows from empty."""
-    print(f"[case] tq rows d={d} bits={bits} gate={gated}", flush=True)
-    torch.manual_seed(90 + d + bits)
-    hkv, g, R, steps = 2, 8, 32, 12
+    starts evicting, sequence 2 grows from empty.  Up to 8 KV heads take one wave pair each in
+    the append; 11 and 16 heads loop those waves over the heads."""
+    print(f"[case] tq rows d={d} bits={bits} gate={gated} hkv={hkv} g={g}", flush=True)
+    torch.manual_seed(90 + d + bits + hkv)
+    R, steps = 32, 12
     lens = [75, 20, 0]
     cache = TurboQuantBatchCache(batch=3, kv_heads=hkv, q_heads=hkv * g, capacities=[80, 40, 16],
                                  residual_capacity=R, head_dim=d, bits=bits, device=gpu)
