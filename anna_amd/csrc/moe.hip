@@ -666,6 +666,235 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GU ? 1 : 3)
   }
 }
 
+// ------------------------------------------------------------------ grouped int4 MLP, wide form
+//
+// For 16-bit hidden states and group 128 (the BASELINE bank): one 8-wave workgroup per CU walks
+// (expert, tile) items tile-major.  A gate/up item is 128 rows of the gate and the same rows of the
+// up matrix (wave w: rows 16 w .. 16 w + 15 of both), a down item 256 rows (wave w: rows 32 w ..
+// 32 w + 31, two 16-row fragments).  Every route of the expert goes through in one sweep of up to
+// 48 routes (NC chunks of 16), so each weight is loaded and turned into an MFMA fragment once per
+// sweep, not once per 16 routes.  K runs in passes of 256: the workgroup stages the pass's x rows
+// into LDS once, already in the order of the weight fragments (interleave_x), double-buffered with
+// one barrier per pass; each wave's weights (two fragments x two 128-k blocks per pass) come two
+// passes ahead in registers.  gate/up writes act = silu(x Wg^T) * (x Wu^T) rounded to bf16 (the
+// down product reads bf16 operands either way), down reads it.
+
+constexpr int W_GU_ROWS = 128, W_DN_ROWS = 256;
+constexpr int W_MAXR = 48;       // routes per sweep
+constexpr int W_PK = 256;        // k per pass
+constexpr int W_XP = W_PK + 8;   // LDS row pitch of a staged x slice (16-bit elements)
+constexpr int W_STAGES = 3;      // weight stages in LDS per wave: two passes in flight during one
+constexpr int W_XBYTES = 2 * W_MAXR * W_XP * 2;
+constexpr int W_WBYTES = 8 * W_STAGES * 4 * 1024;  // [wave][stage][block][fragment] 1 KB
+constexpr int W_LDS = W_XBYTES + W_WBYTES;
+
+template <int SDT>
+struct WideScales {
+  typename Elem<SDT>::T s[2][2];  // [block][fragment]
+  int8_t z[2][2];
+};
+
+template <int HDT, int SDT, bool GU, int NC>
+__device__ __forceinline__ void wide_sweep(const anna_mi_moe_mlp_args& a, unsigned char* lds, int64_t slot,
+                                           int64_t tile, int64_t c0, int64_t R) {
+  constexpr int MDT = GU ? HDT : ANNA_MI_BF16;  // the x operand's format (the activation is bf16)
+  constexpr float OFF = MDT == ANNA_MI_BF16 ? 128.0f : 1024.0f;
+  constexpr uint32_t ONES = MDT == ANNA_MI_BF16 ? 0x3F803F80u : 0x3C003C00u;
+  // loads per pass group, in issue order: NC x chunks, 4 weight copies into LDS, 8 scales/zeros
+  constexpr int GROUP = NC + 12;
+  using ST = typename Elem<SDT>::T;
+  uint16_t* xs = (uint16_t*)lds;
+  const int lane = threadIdx.x & 63, wave = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, kq = lane >> 4;
+  unsigned char* wl = lds + W_XBYTES + wave * (W_STAGES * 4096);
+  const int64_t N = GU ? a.intermediate_dim : a.hidden_dim;
+  const int64_t K = GU ? a.hidden_dim : a.intermediate_dim;
+  const int64_t pc = GU ? a.hidden_packed_cols : a.intermediate_packed_cols;
+  const uint16_t* x = GU ? (const uint16_t*)a.compact_hidden : (const uint16_t*)a.activation;
+  // the wave's two 16-row fragments: gate and up rows n (gate/up), or rows n and n + 16 (down)
+  int64_t nf[2];
+  if constexpr (GU) {
+    nf[0] = nf[1] = tile * W_GU_ROWS + wave * 16 + r;
+  } else {
+    nf[0] = tile * W_DN_ROWS + wave * 32 + r;
+    nf[1] = nf[0] + 16;
+  }
+  __amdgpu_buffer_rsrc_t rw[2];
+  uint32_t woff[2];
+  const ST* sc[2];
+  const int8_t* zp[2];
+  const int64_t G = K / 128;
+#pragma unroll
+  for (int f = 0; f < 2; ++f) {
+    const int64_t n = nf[f] < N ? nf[f] : N - 1;  // rows past N load row N - 1 and are not stored
+    const int32_t* qw = GU ? (f == 0 ? a.gate_qweight : a.up_qweight) : a.down_qweight;
+    const void* qs = GU ? (f == 0 ? a.gate_qscale : a.up_qscale) : a.down_qscale;
+    const int8_t* qz = GU ? (f == 0 ? a.gate_qzeros : a.up_qzeros) : a.down_qzeros;
+    rw[f] = __builtin_amdgcn_make_buffer_rsrc(const_cast<int32_t*>(qw), 0, 0x7FFFFFFF, 0x00020000);
+    woff[f] = (uint32_t)(((slot * N + n) * pc + kq * 4) * 4);
+    sc[f] = (const ST*)qs + slot * G * N + n;
+    zp[f] = qz + slot * G * N + n;
+  }
+  const int64_t npass = K / W_PK;
+  // pass q's weights: lane (r, kq) copies its 16 bytes of block 2q + j, fragment f into LDS
+  // (stage st), where it reads them back itself; scales and zero points into registers
+  auto load_pass = [&](int64_t q, int st, WideScales<SDT>& S) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int f = 0; f < 2; ++f)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw[f], (moe_lds_ptr)(wl + st * 4096 + (j * 2 + f) * 1024), 16,
+                                                 woff[f] + (uint32_t)((2 * q + j) * 64), 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+        S.s[j][f] = sc[f][(2 * q + j) * N];
+        S.z[j][f] = zp[f][(2 * q + j) * N];
+      }
+  };
+  // x chunk i of this thread: row (t + 512 i) / 32, 8-k column (t + 512 i) % 32
+  auto load_x = [&](int64_t q, u32x4 (&xr)[NC]) {
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int e = (int)threadIdx.x + 512 * i, row = e >> 5, col = (e & 31) * 8;
+      const bool ok = row < R;
+      xr[i] = *(const u32x4*)(x + (c0 + (ok ? row : 0)) * K + q * W_PK + col);
+      if (!ok) xr[i] = u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store_x = [&](const u32x4 (&xr)[NC], uint16_t* buf) {
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int e = (int)threadIdx.x + 512 * i;
+      *(u32x4*)(buf + (e >> 5) * W_XP + (e & 31) * 8) = interleave_x(xr[i]);
+    }
+  };
+  const u32x4 ones = {ONES, ONES, ONES, ONES};
+  f32x4 out[NC][2];
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int f = 0; f < 2; ++f) out[c][f] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int st, const WideScales<SDT>& S, const uint16_t* xb) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const u32x4 wq0 = *(const u32x4*)(wl + st * 4096 + (j * 2 + 0) * 1024 + lane * 16);
+      const u32x4 wq1 = *(const u32x4*)(wl + st * 4096 + (j * 2 + 1) * 1024 + lane * 16);
+      f32x4 acc[NC][2], sx[NC];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        sx[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+        acc[c][0] = acc[c][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const u32x4 w0 = nibbles_to_frag<MDT>(wq0[s]), w1 = nibbles_to_frag<MDT>(wq1[s]);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const u32x4 xa = *(const u32x4*)(xb + (c * 16 + r) * W_XP + j * 128 + kq * 32 + s * 8);
+          sx[c] = mfma16<MDT>(xa, ones, sx[c]);
+          acc[c][0] = mfma16<MDT>(xa, w0, acc[c][0]);
+          acc[c][1] = mfma16<MDT>(xa, w1, acc[c][1]);
+        }
+      }
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+        const float sf = Elem<SDT>::to_f32(S.s[j][f]), zf = OFF + (float)S.z[j][f];
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) out[c][f][i] = fmaf(sf, fmaf(-zf, sx[c][i], acc[c][f][i]), out[c][f][i]);
+      }
+    }
+  };
+  // one pass: request the x rows and the weights two passes ahead (clamped to the last pass,
+  // so that every pass issues the same GROUP loads and the counted wait below is exact), wait
+  // for this pass's weights, compute, publish the next pass's x (loaded a pass ago)
+  auto pass = [&](int64_t p, int st, const WideScales<SDT>& cur, WideScales<SDT>& ahead2, const u32x4 (&xnext)[NC],
+                  u32x4 (&xahead2)[NC]) {
+    const int64_t q = p + 2 < npass ? p + 2 : npass - 1;
+    load_x(q, xahead2);
+    load_pass(q, (st + 2) % W_STAGES, ahead2);
+    // this pass's weight copies and scales were issued two groups ago
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * GROUP) : "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    compute(st, cur, xs + (p & 1) * (W_MAXR * W_XP));
+    store_x(xnext, xs + ((p + 1) & 1) * (W_MAXR * W_XP));
+    __syncthreads();
+  };
+  WideScales<SDT> A, B, C;
+  u32x4 XA[NC], XB[NC], XC[NC];
+  // prologue: the groups of passes 0 and 1, then x of pass 0 into LDS
+  load_x(0, XA);
+  load_pass(0, 0, A);
+  load_x(npass > 1 ? 1 : 0, XB);
+  load_pass(npass > 1 ? 1 : 0, 1, B);
+  store_x(XA, xs);
+  __syncthreads();
+  for (int64_t p = 0; p < npass; p += 3) {
+    pass(p, 0, A, C, XB, XC);
+    if (p + 1 < npass) pass(p + 1, 1, B, A, XC, XA);
+    if (p + 2 < npass) pass(p + 2, 2, C, B, XA, XB);
+  }
+  // the clamped copies of the last passes are still in flight into stages no wave reads; the
+  // next sweep's first copies must not land while they do
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // C layout: lane (r, kq) element i is route c0 + 16 c + 4 kq + i of its output row
+  using HT = typename Elem<HDT>::T;
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t m = c * 16 + 4 * kq + i;
+      if (m >= R) continue;
+      const int64_t route = c0 + m;
+      if constexpr (GU) {
+        if (nf[0] < N) ((uint16_t*)a.activation)[route * N + nf[0]] = f32_to_bf16_bits(silu(out[c][0][i]) * out[c][1][i]);
+      } else {
+        const float wr = Elem<HDT>::to_f32(((const HT*)a.compact_weights)[route]);
+#pragma unroll
+        for (int f = 0; f < 2; ++f)
+          if (nf[f] < N) ((HT*)a.compact_outputs)[route * N + nf[f]] = Elem<HDT>::cvt(out[c][f][i] * wr);
+      }
+    }
+}
+
+template <int HDT, int SDT, bool GU>
+__global__ __launch_bounds__(512) void moe_int4_mlp_wide_kernel(const anna_mi_moe_mlp_args a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char wide_lds[];  // W_LDS bytes
+  const int64_t N = GU ? a.intermediate_dim : a.hidden_dim;
+  const int64_t tiles = (N + (GU ? W_GU_ROWS : W_DN_ROWS) - 1) / (GU ? W_GU_ROWS : W_DN_ROWS);
+  // tile-major items (item it: tile it / nact of list entry it % nact), so that the tiles of
+  // one expert, taken by workgroups it, it + nact, ..., land on one XCD (workgroup w runs on
+  // XCD w % 8; the grid is a multiple of 8) and share its L2 copy of the expert's x rows
+  // the list of experts with routes (a.items), or every active expert (empty ones skipped here)
+  const bool listed = a.items != nullptr;
+  const int64_t nact = listed ? a.items[0] : a.active_count;
+  const int64_t nitems = nact * tiles;
+  for (int64_t it = blockIdx.x; it < nitems; it += gridDim.x) {
+    int4 e;  // {slot, start, end, -}
+    if (listed) {
+      e = *(const int4*)(a.items + 4 + 4 * (it % nact));
+    } else {
+      const int64_t ai = it % nact, ex = a.active_experts[ai];
+      e = make_int4((int)a.active_slots[ai], (int)a.expert_offsets[ex], (int)a.expert_offsets[ex + 1], 0);
+    }
+    const int64_t tile = it / nact;
+    for (int64_t c0 = e.y; c0 < e.z; c0 += W_MAXR) {
+      const int64_t R = e.z - c0 < W_MAXR ? e.z - c0 : W_MAXR;
+      if (R <= 16)
+        wide_sweep<HDT, SDT, GU, 1>(a, wide_lds, e.x, tile, c0, R);
+      else if (R <= 32)
+        wide_sweep<HDT, SDT, GU, 2>(a, wide_lds, e.x, tile, c0, R);
+      else
+        wide_sweep<HDT, SDT, GU, 3>(a, wide_lds, e.x, tile, c0, R);
+    }
+  }
+}
+
 // items[0] = number of active experts with routes; items[4 + 4 j ..] = {bank slot, first
 // compact route, end route, 0} of the j-th of them, in active-list order.  One workgroup.
 __global__ __launch_bounds__(1024) void moe_compact_items_kernel(const int64_t* __restrict__ active_experts,
@@ -748,6 +977,34 @@ int launch_moe_mlp_nc(const anna_mi_moe_mlp_args& a, hipStream_t st, dim3 g1, di
 // their register count (one wave per SIMD) than they save: 316 -> 217 us at 512 tokens.
 template <int HDT, int SDT, int GPB>
 int launch_moe_mlp(const anna_mi_moe_mlp_args& a, hipStream_t st, dim3 g1, dim3 g2) {
+  if constexpr (GPB == 1 && HDT != ANNA_MI_F32) {
+    // the wide form pays a barrier per 256-k pass and a pipeline fill per sweep, which the
+    // one-sweep-per-expert saving only repays when experts carry many routes: at the BASELINE
+    // MoE shapes it is 1.6x faster at 32 routes per expert (T = 512) and 2x slower at 0.5 and
+    // 4 (T = 8, 64), so it is taken from 16 routes per active expert on average
+    if (a.group_size == 128 && a.hidden_dim % W_PK == 0 && a.intermediate_dim % W_PK == 0 &&
+        a.routes >= 16 * a.active_count) {
+      // one 8-wave workgroup per CU, persistent over the (expert, tile) items
+      const unsigned n1 = (unsigned)(a.active_count * ((a.intermediate_dim + W_GU_ROWS - 1) / W_GU_ROWS));
+      const unsigned n2 = (unsigned)(a.active_count * ((a.hidden_dim + W_DN_ROWS - 1) / W_DN_ROWS));
+      auto grid = [](unsigned n) { return dim3(n < 256u ? (n + 7u) / 8u * 8u : 256u); };
+      auto k1 = moe_int4_mlp_wide_kernel<HDT, SDT, true>;
+      auto k2 = moe_int4_mlp_wide_kernel<HDT, SDT, false>;
+      static bool lds_set = false;
+      if (!lds_set) {
+        ANNA_CHECK(hipFuncSetAttribute((const void*)k1, hipFuncAttributeMaxDynamicSharedMemorySize, W_LDS) == hipSuccess &&
+                       hipFuncSetAttribute((const void*)k2, hipFuncAttributeMaxDynamicSharedMemorySize, W_LDS) ==
+                           hipSuccess,
+                   "moe MLP: cannot raise the LDS limit");
+        lds_set = true;
+      }
+      hipLaunchKernelGGL(k1, grid(n1), dim3(512), W_LDS, st, a);
+      ANNA_LAUNCH_CHECK("moe_int4_mlp_wide_kernel (gate, up)");
+      hipLaunchKernelGGL(k2, grid(n2), dim3(512), W_LDS, st, a);
+      ANNA_LAUNCH_CHECK("moe_int4_mlp_wide_kernel (down)");
+      return ANNA_MI_OK;
+    }
+  }
   anna_mi_moe_mlp_args b = a;
   b.sweep_chunks = 1;
   return launch_moe_mlp_nc<HDT, SDT, GPB, 1>(b, st, g1, g2);

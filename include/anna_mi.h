@@ -544,10 +544,15 @@ typedef struct {
   const void* down_qscale;
   const int8_t* down_qzeros;
   int64_t hidden_packed_cols, hidden_groups, intermediate_packed_cols, intermediate_groups, group_size;
-  float* activation;              /* workspace fp32 [routes][intermediate] */
-  int sweep_chunks;               /* 1..4: a hint, the routes an expert may take per sweep over its
-                                     weights in chunks of 16; this build always sweeps 16 routes at
-                                     a time (measured fastest at every BASELINE shape) */
+  float* activation;              /* workspace, routes * intermediate fp32 elements (the act
+                                     between the two products; the wide form below keeps it as
+                                     bf16 in the first half) */
+  int sweep_chunks;               /* 1..4: a hint, ignored.  With 16-bit hidden states, group 128,
+                                     hidden and intermediate dims multiples of 256 and at least 16
+                                     routes per active expert on average, one 8-wave workgroup per
+                                     CU takes up to 48 routes of an expert per sweep over its
+                                     weights; otherwise sweeps are 16 routes (each form measured
+                                     fastest where it is taken) */
   int32_t* items;                 /* optional workspace int32 [4 + 4 * active_count]: when set, the
                                      active experts that have routes are listed on the device
                                      first and the MLP launches walk that list (no workgroups

@@ -81,15 +81,24 @@ def test_dispatch_matches_cpu_order(gpu, dtype):
     assert torch.equal(sti2, sti) and torch.equal(off2, off) and torch.equal(compact2, compact)
 
 
-@pytest.mark.parametrize("hdt,sdt,group,tokens", [
-    (torch.bfloat16, torch.float32, 128, 13),  # reference bank dtype (fp32 scales)
-    (torch.bfloat16, torch.bfloat16, 128, 40),  # > 16 routes per expert (chunking)
-    (torch.float16, torch.float32, 64, 9),
-    (torch.float32, torch.float32, 32, 6),
+@pytest.mark.parametrize("hdt,sdt,group,tokens,h,i", [
+    (torch.bfloat16, torch.float32, 128, 13, 256, 128),  # reference bank dtype (fp32 scales)
+    (torch.bfloat16, torch.bfloat16, 128, 40, 256, 128),  # > 16 routes per expert (chunking)
+    (torch.float16, torch.float32, 64, 9, 256, 128),
+    (torch.float32, torch.float32, 32, 6, 256, 128),
+    # dims multiple of 256, group 128, 16-bit activations and >= 16 routes per active expert: the
+    # wide kernels (one sweep of up to 48 routes per expert, K in passes of 256); 100 tokens x 3
+    # routes over 8 experts put ~37 routes on an expert (one 48-route sweep), 200 tokens ~75 (a
+    # 48-route sweep and a short one); 5 tokens stay on the 16-route kernels
+    (torch.bfloat16, torch.bfloat16, 128, 5, 512, 256),
+    (torch.bfloat16, torch.float32, 128, 100, 512, 256),
+    (torch.float16, torch.bfloat16, 128, 100, 768, 512),
+    (torch.bfloat16, torch.bfloat16, 128, 200, 512, 256),
 ])
-def test_grouped_int4_mlp_matches_oracle(gpu, hdt, sdt, group, tokens):
+def test_grouped_int4_mlp_matches_oracle(gpu, hdt, sdt, group, tokens, h, i):
+    print(f"[case] moe grouped MLP {hdt} scales {sdt} group {group} tokens {tokens} h {h} i {i}", flush=True)
     torch.manual_seed(7)
-    e, k, h, i = 8, 3, 256, 128
+    e, k = 8, 3
     bank = make_bank(e, h, i, group, sdt, gpu, seed=11 + tokens)
     hidden = torch.randn(tokens, h, device=gpu, dtype=hdt)
     w, sel, usage = fused_ops.moe_router(torch.randn(tokens, e, device=gpu), k, True)
