@@ -798,6 +798,8 @@ __device__ __forceinline__ void wide_sweep(const anna_mi_moe_mlp_args& a, unsign
           acc[c][0] = mfma16<MDT>(xa, w0, acc[c][0]);
           acc[c][1] = mfma16<MDT>(xa, w1, acc[c][1]);
         }
+        // the x fragments of later steps are not read (and held) ahead
+        __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
       for (int f = 0; f < 2; ++f) {
@@ -860,6 +862,196 @@ __device__ __forceinline__ void wide_sweep(const anna_mi_moe_mlp_args& a, unsign
           if (nf[f] < N) ((HT*)a.compact_outputs)[route * N + nf[f]] = Elem<HDT>::cvt(out[c][f][i] * wr);
       }
     }
+}
+
+// The down product when all of its K (the intermediate dim, <= W_DN_KMAX) fits: an item is
+// W_DN_TPI consecutive 256-row tiles of one expert.  The routes' activation rows (<= 48, all of
+// K) are staged into LDS once; then every wave streams its weights tile after tile, pass after
+// pass, through its own 3-stage LDS ring two steps ahead -- no barrier between the steps, as x
+// does not change -- and stores a tile's outputs after its last pass.
+constexpr int W_DN_KMAX = 512, W_DN_TPI = 4;
+static_assert(W_MAXR * (W_DN_KMAX + 8) * 2 + W_MAXR * 4 <= W_XBYTES,
+              "resident down x and routing weights must fit the x area");
+
+template <int HDT, int SDT, int NC>
+__device__ __forceinline__ void wide_down_item(const anna_mi_moe_mlp_args& a, unsigned char* lds, int64_t slot,
+                                               int64_t tile0, int64_t ntile, int64_t c0, int64_t R) {
+  constexpr int MDT = ANNA_MI_BF16;  // the activation is bf16
+  constexpr float OFF = 128.0f;
+  constexpr uint32_t ONES = 0x3F803F80u;
+  constexpr int GROUP = 12;          // loads per step: 4 weight copies into LDS, 8 scales/zeros
+  using ST = typename Elem<SDT>::T;
+  using HT = typename Elem<HDT>::T;
+  uint16_t* xs = (uint16_t*)lds;
+  const int lane = threadIdx.x & 63, wave = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, kq = lane >> 4;
+  unsigned char* wl = lds + W_XBYTES + wave * (W_STAGES * 4096);
+  const int64_t N = a.hidden_dim, K = a.intermediate_dim, pc = a.intermediate_packed_cols, G = K / 128;
+  const int64_t XP = K + 8;
+  const int64_t npass = K / W_PK, nstep = ntile * npass;
+  const uint16_t* x = (const uint16_t*)a.activation;
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<int32_t*>(a.down_qweight), 0,
+                                                                      0x7FFFFFFF, 0x00020000);
+  const ST* scb = (const ST*)a.down_qscale + slot * G * N;
+  const int8_t* zpb = a.down_qzeros + slot * G * N;
+  // step q = (tile t, pass p): the wave's rows n = 256 (tile0 + t) + 32 wave + r (+ 16); rows
+  // past N (a partial last tile) load row N - 1 and are not stored.  Byte offsets and element
+  // indices in 32 bits: the lane part once, the step part uniform.
+  const int64_t nrow0 = tile0 * W_DN_ROWS + wave * 32 + r;
+  auto row_of = [&](int64_t t, int f) {
+    const int64_t n = nrow0 + t * W_DN_ROWS + 16 * f;
+    return (uint32_t)(n < N ? n : N - 1);
+  };
+  const uint32_t wbase = (uint32_t)((slot * N * pc + kq * 4) * 4), pcb = (uint32_t)(pc * 4);
+  auto load_step = [&](int64_t q, int st, WideScales<SDT>& S) {
+    const int64_t t = q / npass, p = q % npass;
+    const uint32_t r0 = row_of(t, 0), r1 = row_of(t, 1);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int f = 0; f < 2; ++f)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (moe_lds_ptr)(wl + st * 4096 + (j * 2 + f) * 1024), 16,
+                                                 wbase + (f ? r1 : r0) * pcb, (int)((2 * p + j) * 64), 0, 0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+        const uint32_t gi = (uint32_t)((2 * p + j) * N) + (f ? r1 : r0);
+        S.s[j][f] = scb[gi];
+        S.z[j][f] = zpb[gi];
+      }
+  };
+  const u32x4 ones = {ONES, ONES, ONES, ONES};
+  f32x4 out[NC][2];
+  auto clear = [&]() {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) out[c][0] = out[c][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  clear();
+  auto compute = [&](int st, const WideScales<SDT>& S, int64_t p) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const u32x4 wq0 = *(const u32x4*)(wl + st * 4096 + (j * 2 + 0) * 1024 + lane * 16);
+      const u32x4 wq1 = *(const u32x4*)(wl + st * 4096 + (j * 2 + 1) * 1024 + lane * 16);
+      f32x4 acc[NC][2], sx[NC];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        sx[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+        acc[c][0] = acc[c][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const u32x4 w0 = nibbles_to_frag<MDT>(wq0[s4]), w1 = nibbles_to_frag<MDT>(wq1[s4]);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const u32x4 xa = *(const u32x4*)(xs + (c * 16 + r) * XP + p * W_PK + j * 128 + kq * 32 + s4 * 8);
+          sx[c] = mfma16<MDT>(xa, ones, sx[c]);
+          acc[c][0] = mfma16<MDT>(xa, w0, acc[c][0]);
+          acc[c][1] = mfma16<MDT>(xa, w1, acc[c][1]);
+        }
+        // the x fragments of later steps are not read (and held) ahead
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+        const float sf = Elem<SDT>::to_f32(S.s[j][f]), zf = OFF + (float)S.z[j][f];
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) out[c][f][i] = fmaf(sf, fmaf(-zf, sx[c][i], acc[c][f][i]), out[c][f][i]);
+      }
+    }
+  };
+  // C layout: lane (r, kq) element i is route c0 + 16 c + 4 kq + i of its output row; the
+  // routing weights come from LDS (staged with x: held in registers across the steps they
+  // would cost registers, loaded at the store a round trip per tile)
+  const float* s_wr = (const float*)(xs + W_MAXR * XP);
+  auto store_tile = [&](int64_t t) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t m = c * 16 + 4 * kq + i;
+        if (m >= R) continue;
+        const float wr = s_wr[m];
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+          const int64_t n = nrow0 + t * W_DN_ROWS + 16 * f;
+          if (n < N) ((HT*)a.compact_outputs)[(c0 + m) * N + n] = Elem<HDT>::cvt(out[c][f][i] * wr);
+        }
+      }
+  };
+  auto step = [&](int64_t q, int st, const WideScales<SDT>& cur, WideScales<SDT>& ahead2) {
+    load_step(q + 2 < nstep ? q + 2 : nstep - 1, (st + 2) % W_STAGES, ahead2);
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * GROUP) : "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    const int64_t p = q % npass;
+    compute(st, cur, p);
+    if (p == npass - 1) {
+      store_tile(q / npass);
+      clear();
+    }
+  };
+  WideScales<SDT> A, B, C;
+  // the first two steps' weights first, then x (whose stores wait for its loads, queued behind)
+  load_step(0, 0, A);
+  load_step(nstep > 1 ? 1 : 0, 1, B);
+  // x rows c0 .. c0 + R - 1, all of K, interleaved, once: chunk e = t + 512 i is row e / (K/8)
+  {
+    const int cpr = (int)(K / 8);  // 8-k chunks per row
+#pragma unroll
+    for (int i = 0; i < NC * 16 * (W_DN_KMAX / 8) / 512; ++i) {
+      const int e = (int)threadIdx.x + 512 * i, row = e / cpr, col = (e % cpr) * 8;
+      if (row >= NC * 16) break;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (row < R) v = *(const u32x4*)(x + (c0 + row) * K + col);
+      *(u32x4*)(xs + row * XP + col) = interleave_x(v);
+    }
+    if (threadIdx.x < (unsigned)R)
+      ((float*)(xs + W_MAXR * XP))[threadIdx.x] = Elem<HDT>::to_f32(((const HT*)a.compact_weights)[c0 + threadIdx.x]);
+  }
+  __syncthreads();  // x staged
+  for (int64_t q = 0; q < nstep; q += 3) {
+    step(q, 0, A, C);
+    if (q + 1 < nstep) step(q + 1, 1, B, A);
+    if (q + 2 < nstep) step(q + 2, 2, C, B);
+  }
+  // the clamped copies of the last steps land in stages no wave reads; wait for them before the
+  // LDS is reused, and for every wave before x is restaged
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+}
+
+template <int HDT, int SDT>
+__global__ __launch_bounds__(512) void moe_int4_down_resident_kernel(const anna_mi_moe_mlp_args a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char wide_lds[];  // W_LDS bytes
+  const int64_t tiles = (a.hidden_dim + W_DN_ROWS - 1) / W_DN_ROWS;
+  const int64_t groups = (tiles + W_DN_TPI - 1) / W_DN_TPI;
+  const bool listed = a.items != nullptr;
+  const int64_t nact = listed ? a.items[0] : a.active_count;
+  const int64_t nitems = nact * groups;
+  // tile-group-major items, as in moe_int4_mlp_wide_kernel: an expert's groups share an XCD
+  for (int64_t it = blockIdx.x; it < nitems; it += gridDim.x) {
+    int4 e;  // {slot, start, end, -}
+    if (listed) {
+      e = *(const int4*)(a.items + 4 + 4 * (it % nact));
+    } else {
+      const int64_t ai = it % nact, ex = a.active_experts[ai];
+      e = make_int4((int)a.active_slots[ai], (int)a.expert_offsets[ex], (int)a.expert_offsets[ex + 1], 0);
+    }
+    const int64_t t0 = (it / nact) * W_DN_TPI;
+    const int64_t nt = tiles - t0 < W_DN_TPI ? tiles - t0 : W_DN_TPI;
+    for (int64_t c0 = e.y; c0 < e.z; c0 += W_MAXR) {
+      const int64_t R = e.z - c0 < W_MAXR ? e.z - c0 : W_MAXR;
+      if (R <= 16)
+        wide_down_item<HDT, SDT, 1>(a, wide_lds, e.x, t0, nt, c0, R);
+      else if (R <= 32)
+        wide_down_item<HDT, SDT, 2>(a, wide_lds, e.x, t0, nt, c0, R);
+      else
+        wide_down_item<HDT, SDT, 3>(a, wide_lds, e.x, t0, nt, c0, R);
+    }
+  }
 }
 
 template <int HDT, int SDT, bool GU>
@@ -986,16 +1178,20 @@ int launch_moe_mlp(const anna_mi_moe_mlp_args& a, hipStream_t st, dim3 g1, dim3 
         a.routes >= 16 * a.active_count) {
       // one 8-wave workgroup per CU, persistent over the (expert, tile) items
       const unsigned n1 = (unsigned)(a.active_count * ((a.intermediate_dim + W_GU_ROWS - 1) / W_GU_ROWS));
-      const unsigned n2 = (unsigned)(a.active_count * ((a.hidden_dim + W_DN_ROWS - 1) / W_DN_ROWS));
+      const unsigned dtiles = (unsigned)((a.hidden_dim + W_DN_ROWS - 1) / W_DN_ROWS);
+      const unsigned n2 = (unsigned)a.active_count *
+                          (a.intermediate_dim <= W_DN_KMAX ? (dtiles + W_DN_TPI - 1) / W_DN_TPI : dtiles);
       auto grid = [](unsigned n) { return dim3(n < 256u ? (n + 7u) / 8u * 8u : 256u); };
       auto k1 = moe_int4_mlp_wide_kernel<HDT, SDT, true>;
-      auto k2 = moe_int4_mlp_wide_kernel<HDT, SDT, false>;
+      const bool resident = a.intermediate_dim <= W_DN_KMAX;
+      auto k2 = resident ? moe_int4_down_resident_kernel<HDT, SDT> : moe_int4_mlp_wide_kernel<HDT, SDT, false>;
       static bool lds_set = false;
       if (!lds_set) {
-        ANNA_CHECK(hipFuncSetAttribute((const void*)k1, hipFuncAttributeMaxDynamicSharedMemorySize, W_LDS) == hipSuccess &&
-                       hipFuncSetAttribute((const void*)k2, hipFuncAttributeMaxDynamicSharedMemorySize, W_LDS) ==
-                           hipSuccess,
-                   "moe MLP: cannot raise the LDS limit");
+        const void* ks[3] = {(const void*)k1, (const void*)moe_int4_down_resident_kernel<HDT, SDT>,
+                             (const void*)moe_int4_mlp_wide_kernel<HDT, SDT, false>};
+        for (const void* k : ks)
+          ANNA_CHECK(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, W_LDS) == hipSuccess,
+                     "moe MLP: cannot raise the LDS limit");
         lds_set = true;
       }
       hipLaunchKernelGGL(k1, grid(n1), dim3(512), W_LDS, st, a);
