@@ -50,6 +50,7 @@ class DecodeArgs(ctypes.Structure):
         ("value_centroids", _P), ("query_rot", _P), ("len2", _I64), ("residual_key", View), ("residual_value", View),
         ("scaling", _F), ("block_size", _I64), ("gate_layout", _I), ("gate", View), ("out", View),
         ("partial_stats", View), ("partial_values", View), ("partial_capacity", _I64), ("seq_lengths", _P),
+        ("rotation_signs", _P),
     ]
 
 

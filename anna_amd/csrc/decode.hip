@@ -21,6 +21,7 @@
 
 #include "common.hpp"
 #include "int4_frag.hpp"
+#include "tq_hadamard.hpp"
 
 namespace anna {
 namespace {
@@ -70,13 +71,49 @@ struct Split {
 };
 
 // q' = R q for every (b, q-head); grid (Hq, B), D threads.
+// q' = R q for every (b, q head), dense R: a workgroup of D threads per query, the query staged
+// in LDS, output element i = sum_k R^T[k][i] q[k] with the R^T loads (coalesced over i, not
+// dependent on the sum) issued eight at a time.
 __global__ __launch_bounds__(1024) void decode_rotate_query_kernel(const anna_mi_decode_args a) {
+  __shared__ float s_q[1024];
   const int64_t h = blockIdx.x, b = blockIdx.y, D = a.head_dim;
   const int i = threadIdx.x;
   const int64_t qb = b * a.query.s0 + h * a.query.s1;
+  s_q[i] = ldv(a.query.ptr, qb + i * a.query.s3, a.dtype);
+  __syncthreads();
   float acc = 0.f;
-  for (int64_t k = 0; k < D; ++k) acc = fmaf(a.rotation_t[k * D + i], ldv(a.query.ptr, qb + k * a.query.s3, a.dtype), acc);
+  int64_t k = 0;
+  for (; k + 8 <= D; k += 8) {
+    float r[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) r[u] = a.rotation_t[(k + u) * D + i];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc = fmaf(r[u], s_q[k + u], acc);
+  }
+  for (; k < D; ++k) acc = fmaf(a.rotation_t[k * D + i], s_q[k], acc);
   a.query_rot[(b * a.q_heads + h) * D + i] = acc;
+}
+
+// q' = R q with the randomized Hadamard R = H diag(s) / sqrt(D) (a.rotation_signs set, D a power
+// of two in [64, 1024]): one wave per (b, q head), lane l holding elements l E .. l E + E - 1 --
+// signs, the in-register fast Walsh-Hadamard transform, 1/sqrt(D).
+template <int E>
+__global__ __launch_bounds__(256) void decode_rotate_query_hadamard_kernel(const anna_mi_decode_args a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.batch * a.q_heads) return;  // whole wave
+  const int64_t b = row / a.q_heads, h = row % a.q_heads;
+  const int64_t qb = b * a.query.s0 + h * a.query.s1;
+  float v[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int64_t d = (int64_t)lane * E + e;
+    v[e] = ldv(a.query.ptr, qb + d * a.query.s3, a.dtype) * a.rotation_signs[d];
+  }
+  fwht_wave<E>(v);
+  const float inv = tq_inv_sqrt(64 * E);
+#pragma unroll
+  for (int e = 0; e < E; ++e) a.query_rot[row * 64 * E + (int64_t)lane * E + e] = v[e] * inv;
 }
 
 template <int KF, int VF, int DPL, int GM, int DT>  // GM: max q-heads per KV group held in registers; DT: activation dtype
@@ -339,12 +376,13 @@ __global__ __launch_bounds__(64 * DEC_WAVES) void decode_split_kernel(const anna
       score_step(kv, vv, t, hi);
     }
   };
-  if (sp.vec)
+  if (sp.vec) {
     sweep(t0, t1 < n1 ? t1 : n1,
           [&](int64_t t, float (&kv)[DPL], float (&vv)[DPL]) { load_packed(t, kv, vv, std::true_type{}); });
-  else
+  } else {
     sweep(t0, t1 < n1 ? t1 : n1,
           [&](int64_t t, float (&kv)[DPL], float (&vv)[DPL]) { load_packed(t, kv, vv, std::false_type{}); });
+  }
   sweep(t0 > L1 ? t0 : L1, t1 < L1 + n2 ? t1 : L1 + n2, load_residual);
   // merge the 4 waves: common max, rescale, ordered sum in LDS
   if (lane < G) {  // lane h < GM holds head h's state
@@ -1148,9 +1186,22 @@ static int gqa_decode_splitkv_impl(const anna_mi_decode_args& a, void* stream) {
              (long long)a.partial_capacity, (long long)nblk);
   hipStream_t st = as_stream(stream);
   if (a.key_format == ANNA_MI_KEYS_TQ_MSE && a.len1 > 0) {
-    hipLaunchKernelGGL(decode_rotate_query_kernel, dim3((unsigned)a.q_heads, (unsigned)a.batch), dim3((unsigned)a.head_dim),
-                       0, st, a);
-    ANNA_LAUNCH_CHECK("decode_rotate_query_kernel");
+    const int64_t D = a.head_dim;
+    if (a.rotation_signs && (D == 64 || D == 128 || D == 256 || D == 512 || D == 1024)) {
+      const dim3 grid((unsigned)((a.batch * a.q_heads + 3) / 4));
+      switch (D) {
+        case 64: hipLaunchKernelGGL(decode_rotate_query_hadamard_kernel<1>, grid, dim3(256), 0, st, a); break;
+        case 128: hipLaunchKernelGGL(decode_rotate_query_hadamard_kernel<2>, grid, dim3(256), 0, st, a); break;
+        case 256: hipLaunchKernelGGL(decode_rotate_query_hadamard_kernel<4>, grid, dim3(256), 0, st, a); break;
+        case 512: hipLaunchKernelGGL(decode_rotate_query_hadamard_kernel<8>, grid, dim3(256), 0, st, a); break;
+        default: hipLaunchKernelGGL(decode_rotate_query_hadamard_kernel<16>, grid, dim3(256), 0, st, a); break;
+      }
+      ANNA_LAUNCH_CHECK("decode_rotate_query_hadamard_kernel");
+    } else {
+      hipLaunchKernelGGL(decode_rotate_query_kernel, dim3((unsigned)a.q_heads, (unsigned)a.batch),
+                         dim3((unsigned)a.head_dim), 0, st, a);
+      ANNA_LAUNCH_CHECK("decode_rotate_query_kernel");
+    }
   }
   const bool kq = a.key_format == ANNA_MI_KEYS_TQ_MSE;
   int64_t nmerge = nblk;  // partials written by the split kernel

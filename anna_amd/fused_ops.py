@@ -234,10 +234,12 @@ def decode_args(*, query, len1, key=None, key_format=KEYS_DENSE, key_norms=None,
                 value=None, value_format=VALUES_DENSE, value_scales=None, value_zeros=None, value_bits=0,
                 value_group_size=1, rotation=None, rotation_t=None, key_centroids=None, value_centroids=None,
                 query_rot=None, residual_key=None, residual_value=None, scaling, block_size, gate=None, output,
-                partial_stats, partial_values, seq_lengths=None):
+                partial_stats, partial_values, seq_lengths=None, rotation_signs=None):
     """Fills anna_mi_decode_args from tensors (query/out [B, Hq, 1, D], K/V [B, Hkv, L, ...]).
     seq_lengths (optional, device int32 [B]): per-row token counts; len1 and the residual's
-    length are then capacities (see include/anna_mi.h)."""
+    length are then capacities (see include/anna_mi.h).  rotation_signs (optional, device fp32
+    [D]): the sign vector of a randomized Hadamard key rotation, so that the query is rotated by
+    the fast transform."""
     b, hq, _, d = query.shape
     hkv = (key if key is not None else residual_key).size(1)
     len2 = 0 if residual_key is None else residual_key.size(2)
@@ -281,6 +283,11 @@ def decode_args(*, query, len1, key=None, key_format=KEYS_DENSE, key_norms=None,
             raise RuntimeError("seq_lengths must be a contiguous int32 tensor with one entry per batch row")
         _lib.require_device(seq_lengths)
     a.seq_lengths = _lib.ptr(seq_lengths)
+    if rotation_signs is not None:
+        _lib.require_device(rotation_signs)
+        if rotation_signs.dtype != torch.float32 or rotation_signs.numel() != d:
+            raise RuntimeError("rotation_signs must be fp32 [head_dim]")
+    a.rotation_signs = _lib.ptr(rotation_signs)
     return a
 
 

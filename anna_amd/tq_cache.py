@@ -9,7 +9,7 @@ TurboQuantKVRow.decode_attention per row, turboquant.py:1181-1346).
 
 Two forms behind one class.  head_dim 256 with 2-bit codes (the BASELINE shape) takes the
 MFMA decode of anna_amd/csrc/tq_decode.hip over TQ-MSE keys and values.  Every
-other shape (power-of-two head_dim 64..1024, key/value bits 2..4) takes TurboQuantRowsCache:
+other shape (power-of-two head_dim 64..512, key/value bits 2..4) takes TurboQuantRowsCache:
 TQ-MSE keys and min/max values (the reference row's value format, turboquant.py:199-230) in one
 region per sequence, one append launch, and the split-KV decode with per-row lengths.
 
@@ -239,7 +239,7 @@ class TurboQuantBatchCache:
 
 
 class TurboQuantRowsCache(TurboQuantBatchCache):
-    """The batched cache for any power-of-two head_dim in [64, 1024] and bits 2..4 (keys and
+    """The batched cache for any power-of-two head_dim in [64, 512] and bits 2..4 (keys and
     values).  Per (sequence, KV head) a region of `capacity` packed slots -- keys as Hadamard
     TQ-MSE codes + fp16 norm, values as min/max groups of `value_group_size` -- and a bf16 ring of
     the newest `residual_capacity` tokens (token j at slot j % R).  Lengths live on the device.
@@ -249,8 +249,8 @@ class TurboQuantRowsCache(TurboQuantBatchCache):
     def __init__(self, *, batch: int, kv_heads: int, q_heads: int, capacities, residual_capacity: int = 128,
                  head_dim: int = 256, bits: int = 2, device="cuda", tokens_per_item: int = 0,
                  value_group_size: int | None = None, block_size: int = 64):
-        if head_dim not in (64, 128, 256, 512, 1024):
-            raise ValueError("TurboQuantBatchCache needs a power-of-two head_dim in [64, 1024]")
+        if head_dim not in (64, 128, 256, 512):
+            raise ValueError("TurboQuantBatchCache needs a power-of-two head_dim in [64, 512] (the split-KV decode's range)")
         if bits not in (2, 3, 4):
             raise ValueError(f"Unsupported TurboQuant KV bit-width: {bits}. Expected 2, 3, or 4.")
         if q_heads % kv_heads != 0 or q_heads // kv_heads > (8 if head_dim >= 512 else 16):
@@ -350,14 +350,20 @@ class TurboQuantRowsCache(TurboQuantBatchCache):
             out = torch.empty_like(query)
         o4 = out.unsqueeze(2)
         qn = self.qn
+        # blocks sized so that the call is ~1024 workgroups (about four per CU): one per block,
+        # KV head and sequence, each writing G partial rows the merge reads back (64-token
+        # blocks at 16K tokens made ~4000 workgroups whose partials were as large as the cache)
+        per_row = max(1, 1024 // (self.batch * self.kv_heads))
+        bs = max(self.block_size, -(-(self.capacity + self.residual_capacity) // per_row))
+        bs = -(-bs // 16) * 16
         args = fused_ops.decode_args(
             query=q4, len1=self.capacity, key=self.key_codes, key_format=fused_ops.KEYS_TQ_MSE,
             key_norms=self.key_norms, key_bits=self.bits, value=self.value_data,
             value_format=fused_ops.VALUES_MINMAX, value_scales=self.value_scales, value_zeros=self.value_zeros,
             value_bits=self.bits, value_group_size=self.value_group_size, rotation=qn.rotation,
-            rotation_t=qn.rotation_t, key_centroids=qn.centroids, query_rot=self.query_rot,
+            rotation_t=qn.rotation_t, key_centroids=qn.centroids, rotation_signs=qn.signs, query_rot=self.query_rot,
             residual_key=self.residual_key, residual_value=self.residual_value, scaling=scaling,
-            block_size=self.block_size, gate=None if gate is None else gate.contiguous().unsqueeze(2), output=o4,
+            block_size=bs, gate=None if gate is None else gate.contiguous().unsqueeze(2), output=o4,
             partial_stats=self.partial_stats, partial_values=self.partial_values, seq_lengths=self.seq_lengths)
         nblk = fused_ops.decode_num_blocks(args)
         if nblk > self.partial_stats.size(2):

@@ -203,7 +203,7 @@ class _LayerSlab:
             value=self.vdata[rows] if C else None, value_format=fused_ops.VALUES_MINMAX,
             value_scales=self.vscales[rows] if C else None, value_zeros=self.vzeros[rows] if C else None,
             value_bits=self.bits, value_group_size=self.value_group_size,
-            rotation=qn.rotation, rotation_t=qn.rotation_t, key_centroids=qn.centroids,
+            rotation=qn.rotation, rotation_t=qn.rotation_t, key_centroids=qn.centroids, rotation_signs=qn.signs,
             query_rot=self._workspace("qrot", (b, hq, D), torch.float32),
             residual_key=self.rk[rows], residual_value=self.rv[rows], scaling=scaling,
             block_size=_DECODE_BLOCK_SIZE, gate=gate, output=out,

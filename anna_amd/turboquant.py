@@ -588,7 +588,7 @@ class TurboQuantKVRow:
             value_scales=self._vscales[:, :n].unsqueeze(0) if n > 0 else None,
             value_zeros=self._vzeros[:, :n].unsqueeze(0) if n > 0 else None,
             value_bits=self.bits, value_group_size=self.value_group_size,
-            rotation=qn.rotation, rotation_t=qn.rotation_t, key_centroids=qn.centroids,
+            rotation=qn.rotation, rotation_t=qn.rotation_t, key_centroids=qn.centroids, rotation_signs=qn.signs,
             query_rot=self._workspace("qrot", (hq, self.head_dim), torch.float32),
             residual_key=res_k, residual_value=res_v, scaling=scaling, block_size=_DECODE_BLOCK_SIZE,
             gate=None if gate is None else gate.unsqueeze(0), output=out,

@@ -234,6 +234,11 @@ typedef struct {
    * len1) before them in the main segment; len1 and len2 are then the segments' capacities.  The
    * batched form of the reference's per-row decode loop (ops.py:1055-1071). */
   const int32_t* seq_lengths;
+  /* Optional (NULL: the dense rotation_t is used).  MSE keys with the randomized Hadamard
+   * rotation R = H diag(s) / sqrt(D) (power-of-two D in [64, 1024]): the sign vector s, device
+   * fp32 [D]; the query is then rotated by a fast Walsh-Hadamard transform, one wave per query,
+   * instead of the D x D product. */
+  const float* rotation_signs;
 } anna_mi_decode_args;
 
 /* sizeof(anna_mi_decode_args), so that bindings can check their struct layout. */

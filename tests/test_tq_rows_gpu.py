@@ -163,3 +163,28 @@ def test_rows_cache_graph_replay(gpu):
         torch.cuda.synchronize()
         assert graphed.seq_lengths.cpu().tolist() == eager.seq_lengths.cpu().tolist(), step
         assert torch.equal(out_g, ref), step
+
+
+@pytest.mark.parametrize("d", [64, 256, 512])
+def test_rows_cache_hadamard_query_rotation_matches_dense(gpu, d):
+    """The query rotation by the fast Walsh-Hadamard transform (the quantizer's sign vector
+    passed as rotation_signs) gives the attention of the dense D x D rotation: the same cache
+    decoded both ways agrees within the bf16 output tolerance (both rotations are fp32; they
+    differ only in summation order)."""
+    print(f"[case] tq rows query rotation d={d}", flush=True)
+    torch.manual_seed(31 + d)
+    hkv, g, R = 2, 4, 16
+    cache = TurboQuantBatchCache(batch=2, kv_heads=hkv, q_heads=hkv * g, capacities=[48, 48], residual_capacity=R,
+                                 head_dim=d, bits=4, device=gpu)
+    for b, L in enumerate((50, 17)):
+        cache.load_sequence(b, torch.randn(hkv, L, d, device=gpu).to(torch.bfloat16),
+                            torch.randn(hkv, L, d, device=gpu).to(torch.bfloat16))
+    q = torch.randn(2, hkv * g, d, device=gpu).to(torch.bfloat16)
+    fast = cache.decode(q, scaling=d ** -0.5).float()
+    signs = cache.qn.signs
+    try:
+        cache.qn.signs = None  # no rotation_signs: the dense product
+        dense = cache.decode(q, scaling=d ** -0.5).float()
+    finally:
+        cache.qn.signs = signs
+    assert rel_err(fast.cpu().numpy(), dense.cpu().numpy()) <= 1e-2
