@@ -864,42 +864,58 @@ __device__ __forceinline__ void wide_sweep(const anna_mi_moe_mlp_args& a, unsign
     }
 }
 
-// The down product when all of its K (the intermediate dim, <= W_DN_KMAX) fits: an item is
-// W_DN_TPI consecutive 256-row tiles of one expert.  The routes' activation rows (<= 48, all of
-// K) are staged into LDS once; then every wave streams its weights tile after tile, pass after
-// pass, through its own 3-stage LDS ring two steps ahead -- no barrier between the steps, as x
-// does not change -- and stores a tile's outputs after its last pass.
+// Resident forms: the routes' x rows (all of K) stay in LDS for a whole item, so the waves
+// stream their weights step after step (tile after tile, pass after pass) through their own
+// 3-stage LDS rings with no barrier between the steps, and store a tile after its last pass.
+//   down (intermediate <= 512): up to 48 routes per sweep; an item is W_DN_TPI consecutive
+//     256-row tiles of one expert (wave w: rows 32 w .. 32 w + 31, two fragments); the routing
+//     weights are staged next to x.
+//   gate/up (hidden <= 2048, few routes per expert): up to 16 routes per sweep; an item is
+//     W_GU_TPI consecutive 128-row tiles (wave w: rows 16 w .. of the gate and of the up matrix).
+// x rows are K elements apart with 16-byte chunk c of row r stored at chunk c ^ (r & 7): the 16
+// rows of an MFMA operand read then hit distinct banks without padding (padding would not let
+// 16 x 2048 of x and the weight rings fit the 160 KB).
 constexpr int W_DN_KMAX = 512, W_DN_TPI = 4;
-static_assert(W_MAXR * (W_DN_KMAX + 8) * 2 + W_MAXR * 4 <= W_XBYTES,
-              "resident down x and routing weights must fit the x area");
+constexpr int W_GU_KMAX = 2048, W_GU_TPI = 2, W_GU_RMAX = 16;
+constexpr int W_RES_LDS = 16 * W_GU_KMAX * 2 + W_WBYTES;  // the larger of the two layouts
+static_assert(W_MAXR * W_DN_KMAX * 2 + W_MAXR * 4 + W_WBYTES <= W_RES_LDS, "down layout fits");
+static_assert(W_RES_LDS <= 160 * 1024, "LDS of one workgroup");
 
-template <int HDT, int SDT, int NC>
-__device__ __forceinline__ void wide_down_item(const anna_mi_moe_mlp_args& a, unsigned char* lds, int64_t slot,
-                                               int64_t tile0, int64_t ntile, int64_t c0, int64_t R) {
-  constexpr int MDT = ANNA_MI_BF16;  // the activation is bf16
-  constexpr float OFF = 128.0f;
-  constexpr uint32_t ONES = 0x3F803F80u;
+template <int HDT, int SDT, bool GU, int NC>
+__device__ __forceinline__ void resident_item(const anna_mi_moe_mlp_args& a, unsigned char* lds, int64_t slot,
+                                              int64_t tile0, int64_t ntile, int64_t c0, int64_t R) {
+  constexpr int MDT = GU ? HDT : ANNA_MI_BF16;  // x operand format (the activation is bf16)
+  constexpr float OFF = MDT == ANNA_MI_BF16 ? 128.0f : 1024.0f;
+  constexpr uint32_t ONES = MDT == ANNA_MI_BF16 ? 0x3F803F80u : 0x3C003C00u;
   constexpr int GROUP = 12;          // loads per step: 4 weight copies into LDS, 8 scales/zeros
+  constexpr int64_t ROWS = GU ? W_GU_ROWS : W_DN_ROWS;
   using ST = typename Elem<SDT>::T;
   using HT = typename Elem<HDT>::T;
   uint16_t* xs = (uint16_t*)lds;
   const int lane = threadIdx.x & 63, wave = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, kq = lane >> 4;
-  unsigned char* wl = lds + W_XBYTES + wave * (W_STAGES * 4096);
-  const int64_t N = a.hidden_dim, K = a.intermediate_dim, pc = a.intermediate_packed_cols, G = K / 128;
-  const int64_t XP = K + 8;
+  const int64_t N = GU ? a.intermediate_dim : a.hidden_dim;
+  const int64_t K = GU ? a.hidden_dim : a.intermediate_dim;
+  const int64_t pc = GU ? a.hidden_packed_cols : a.intermediate_packed_cols, G = K / 128;
+  unsigned char* wl = lds + (GU ? 16 * W_GU_KMAX * 2 : W_MAXR * W_DN_KMAX * 2 + W_MAXR * 4) + wave * (W_STAGES * 4096);
+  float* s_wr = (float*)(xs + W_MAXR * K);  // down: routing weights after x
   const int64_t npass = K / W_PK, nstep = ntile * npass;
-  const uint16_t* x = (const uint16_t*)a.activation;
-  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<int32_t*>(a.down_qweight), 0,
-                                                                      0x7FFFFFFF, 0x00020000);
-  const ST* scb = (const ST*)a.down_qscale + slot * G * N;
-  const int8_t* zpb = a.down_qzeros + slot * G * N;
-  // step q = (tile t, pass p): the wave's rows n = 256 (tile0 + t) + 32 wave + r (+ 16); rows
-  // past N (a partial last tile) load row N - 1 and are not stored.  Byte offsets and element
-  // indices in 32 bits: the lane part once, the step part uniform.
-  const int64_t nrow0 = tile0 * W_DN_ROWS + wave * 32 + r;
+  const uint16_t* x = GU ? (const uint16_t*)a.compact_hidden : (const uint16_t*)a.activation;
+  const __amdgpu_buffer_rsrc_t rw[2] = {
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<int32_t*>(GU ? a.gate_qweight : a.down_qweight), 0, 0x7FFFFFFF,
+                                        0x00020000),
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<int32_t*>(GU ? a.up_qweight : a.down_qweight), 0, 0x7FFFFFFF,
+                                        0x00020000)};
+  const ST* scb[2] = {(const ST*)(GU ? a.gate_qscale : a.down_qscale) + slot * G * N,
+                      (const ST*)(GU ? a.up_qscale : a.down_qscale) + slot * G * N};
+  const int8_t* zpb[2] = {(GU ? a.gate_qzeros : a.down_qzeros) + slot * G * N,
+                          (GU ? a.up_qzeros : a.down_qzeros) + slot * G * N};
+  // step q = (tile t, pass p); the wave's fragment f rows: gate/up n = 128 (tile0 + t) + 16 wave + r
+  // for both matrices, down n = 256 (tile0 + t) + 32 wave + r + 16 f.  Rows past N (a partial last
+  // tile) load row N - 1 and are not stored.  Byte offsets and indices in 32 bits.
+  const int64_t nrow0 = tile0 * ROWS + wave * (GU ? 16 : 32) + r;
   auto row_of = [&](int64_t t, int f) {
-    const int64_t n = nrow0 + t * W_DN_ROWS + 16 * f;
+    const int64_t n = nrow0 + t * ROWS + (GU ? 0 : 16 * f);
     return (uint32_t)(n < N ? n : N - 1);
   };
   const uint32_t wbase = (uint32_t)((slot * N * pc + kq * 4) * 4), pcb = (uint32_t)(pc * 4);
@@ -910,15 +926,15 @@ __device__ __forceinline__ void wide_down_item(const anna_mi_moe_mlp_args& a, un
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int f = 0; f < 2; ++f)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (moe_lds_ptr)(wl + st * 4096 + (j * 2 + f) * 1024), 16,
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw[f], (moe_lds_ptr)(wl + st * 4096 + (j * 2 + f) * 1024), 16,
                                                  wbase + (f ? r1 : r0) * pcb, (int)((2 * p + j) * 64), 0, 0);
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int f = 0; f < 2; ++f) {
         const uint32_t gi = (uint32_t)((2 * p + j) * N) + (f ? r1 : r0);
-        S.s[j][f] = scb[gi];
-        S.z[j][f] = zpb[gi];
+        S.s[j][f] = scb[f][gi];
+        S.z[j][f] = zpb[f][gi];
       }
   };
   const u32x4 ones = {ONES, ONES, ONES, ONES};
@@ -942,9 +958,10 @@ __device__ __forceinline__ void wide_down_item(const anna_mi_moe_mlp_args& a, un
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4) {
         const u32x4 w0 = nibbles_to_frag<MDT>(wq0[s4]), w1 = nibbles_to_frag<MDT>(wq1[s4]);
+        const int64_t ci = p * (W_PK / 8) + j * 16 + kq * 4 + s4;  // 16-byte chunk of the row
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-          const u32x4 xa = *(const u32x4*)(xs + (c * 16 + r) * XP + p * W_PK + j * 128 + kq * 32 + s4 * 8);
+          const u32x4 xa = *(const u32x4*)(xs + (c * 16 + r) * K + ((ci ^ (r & 7)) * 8));
           sx[c] = mfma16<MDT>(xa, ones, sx[c]);
           acc[c][0] = mfma16<MDT>(xa, w0, acc[c][0]);
           acc[c][1] = mfma16<MDT>(xa, w1, acc[c][1]);
@@ -962,10 +979,7 @@ __device__ __forceinline__ void wide_down_item(const anna_mi_moe_mlp_args& a, un
       }
     }
   };
-  // C layout: lane (r, kq) element i is route c0 + 16 c + 4 kq + i of its output row; the
-  // routing weights come from LDS (staged with x: held in registers across the steps they
-  // would cost registers, loaded at the store a round trip per tile)
-  const float* s_wr = (const float*)(xs + W_MAXR * XP);
+  // C layout: lane (r, kq) element i is route c0 + 16 c + 4 kq + i of its output row
   auto store_tile = [&](int64_t t) {
 #pragma unroll
     for (int c = 0; c < NC; ++c)
@@ -973,11 +987,16 @@ __device__ __forceinline__ void wide_down_item(const anna_mi_moe_mlp_args& a, un
       for (int i = 0; i < 4; ++i) {
         const int64_t m = c * 16 + 4 * kq + i;
         if (m >= R) continue;
-        const float wr = s_wr[m];
+        if constexpr (GU) {
+          const int64_t n = nrow0 + t * ROWS;
+          if (n < N) ((uint16_t*)a.activation)[(c0 + m) * N + n] = f32_to_bf16_bits(silu(out[c][0][i]) * out[c][1][i]);
+        } else {
+          const float wr = s_wr[m];
 #pragma unroll
-        for (int f = 0; f < 2; ++f) {
-          const int64_t n = nrow0 + t * W_DN_ROWS + 16 * f;
-          if (n < N) ((HT*)a.compact_outputs)[(c0 + m) * N + n] = Elem<HDT>::cvt(out[c][f][i] * wr);
+          for (int f = 0; f < 2; ++f) {
+            const int64_t n = nrow0 + t * ROWS + 16 * f;
+            if (n < N) ((HT*)a.compact_outputs)[(c0 + m) * N + n] = Elem<HDT>::cvt(out[c][f][i] * wr);
+          }
         }
       }
   };
@@ -997,19 +1016,22 @@ __device__ __forceinline__ void wide_down_item(const anna_mi_moe_mlp_args& a, un
   // the first two steps' weights first, then x (whose stores wait for its loads, queued behind)
   load_step(0, 0, A);
   load_step(nstep > 1 ? 1 : 0, 1, B);
-  // x rows c0 .. c0 + R - 1, all of K, interleaved, once: chunk e = t + 512 i is row e / (K/8)
   {
-    const int cpr = (int)(K / 8);  // 8-k chunks per row
+    // x rows c0 .. c0 + R - 1, all of K, interleaved and chunk-swizzled: chunk e = t + 512 i is
+    // row e / (K / 8), chunk e % (K / 8)
+    const int cpr = (int)(K / 8);
+    constexpr int KMAX = GU ? W_GU_KMAX : W_DN_KMAX;
 #pragma unroll
-    for (int i = 0; i < NC * 16 * (W_DN_KMAX / 8) / 512; ++i) {
-      const int e = (int)threadIdx.x + 512 * i, row = e / cpr, col = (e % cpr) * 8;
+    for (int i = 0; i < NC * 16 * (KMAX / 8) / 512; ++i) {
+      const int e = (int)threadIdx.x + 512 * i, row = e / cpr, ch = e % cpr;
       if (row >= NC * 16) break;
       u32x4 v = {0u, 0u, 0u, 0u};
-      if (row < R) v = *(const u32x4*)(x + (c0 + row) * K + col);
-      *(u32x4*)(xs + row * XP + col) = interleave_x(v);
+      if (row < R) v = *(const u32x4*)(x + (c0 + row) * K + ch * 8);
+      *(u32x4*)(xs + row * K + ((ch ^ (row & 7)) * 8)) = interleave_x(v);
     }
-    if (threadIdx.x < (unsigned)R)
-      ((float*)(xs + W_MAXR * XP))[threadIdx.x] = Elem<HDT>::to_f32(((const HT*)a.compact_weights)[c0 + threadIdx.x]);
+    if constexpr (!GU) {
+      if (threadIdx.x < (unsigned)R) s_wr[threadIdx.x] = Elem<HDT>::to_f32(((const HT*)a.compact_weights)[c0 + threadIdx.x]);
+    }
   }
   __syncthreads();  // x staged
   for (int64_t q = 0; q < nstep; q += 3) {
@@ -1023,13 +1045,17 @@ __device__ __forceinline__ void wide_down_item(const anna_mi_moe_mlp_args& a, un
   __syncthreads();
 }
 
-template <int HDT, int SDT>
-__global__ __launch_bounds__(512) void moe_int4_down_resident_kernel(const anna_mi_moe_mlp_args a) {
-  extern __shared__ __attribute__((aligned(16))) unsigned char wide_lds[];  // W_LDS bytes
-  const int64_t tiles = (a.hidden_dim + W_DN_ROWS - 1) / W_DN_ROWS;
-  const int64_t groups = (tiles + W_DN_TPI - 1) / W_DN_TPI;
+template <int HDT, int SDT, bool GU>
+__global__ __launch_bounds__(512) void moe_int4_resident_kernel(const anna_mi_moe_mlp_args a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char wide_lds[];  // W_RES_LDS bytes
+  const int64_t N = GU ? a.intermediate_dim : a.hidden_dim;
+  const int64_t rows = GU ? W_GU_ROWS : W_DN_ROWS;
+  const int64_t rmax = GU ? W_GU_RMAX : W_MAXR;
+  const int64_t tiles = (N + rows - 1) / rows;
   const bool listed = a.items != nullptr;
   const int64_t nact = listed ? a.items[0] : a.active_count;
+  const int64_t tpi = GU ? W_GU_TPI : W_DN_TPI;
+  const int64_t groups = (tiles + tpi - 1) / tpi;
   const int64_t nitems = nact * groups;
   // tile-group-major items, as in moe_int4_mlp_wide_kernel: an expert's groups share an XCD
   for (int64_t it = blockIdx.x; it < nitems; it += gridDim.x) {
@@ -1040,16 +1066,20 @@ __global__ __launch_bounds__(512) void moe_int4_down_resident_kernel(const anna_
       const int64_t ai = it % nact, ex = a.active_experts[ai];
       e = make_int4((int)a.active_slots[ai], (int)a.expert_offsets[ex], (int)a.expert_offsets[ex + 1], 0);
     }
-    const int64_t t0 = (it / nact) * W_DN_TPI;
-    const int64_t nt = tiles - t0 < W_DN_TPI ? tiles - t0 : W_DN_TPI;
-    for (int64_t c0 = e.y; c0 < e.z; c0 += W_MAXR) {
-      const int64_t R = e.z - c0 < W_MAXR ? e.z - c0 : W_MAXR;
-      if (R <= 16)
-        wide_down_item<HDT, SDT, 1>(a, wide_lds, e.x, t0, nt, c0, R);
-      else if (R <= 32)
-        wide_down_item<HDT, SDT, 2>(a, wide_lds, e.x, t0, nt, c0, R);
-      else
-        wide_down_item<HDT, SDT, 3>(a, wide_lds, e.x, t0, nt, c0, R);
+    const int64_t t0 = (it / nact) * tpi;
+    const int64_t nt = tiles - t0 < tpi ? tiles - t0 : tpi;
+    for (int64_t c0 = e.y; c0 < e.z; c0 += rmax) {
+      const int64_t R = e.z - c0 < rmax ? e.z - c0 : rmax;
+      if constexpr (GU) {
+        resident_item<HDT, SDT, true, 1>(a, wide_lds, e.x, t0, nt, c0, R);
+      } else {
+        if (R <= 16)
+          resident_item<HDT, SDT, false, 1>(a, wide_lds, e.x, t0, nt, c0, R);
+        else if (R <= 32)
+          resident_item<HDT, SDT, false, 2>(a, wide_lds, e.x, t0, nt, c0, R);
+        else
+          resident_item<HDT, SDT, false, 3>(a, wide_lds, e.x, t0, nt, c0, R);
+      }
     }
   }
 }
@@ -1170,35 +1200,47 @@ int launch_moe_mlp_nc(const anna_mi_moe_mlp_args& a, hipStream_t st, dim3 g1, di
 template <int HDT, int SDT, int GPB>
 int launch_moe_mlp(const anna_mi_moe_mlp_args& a, hipStream_t st, dim3 g1, dim3 g2) {
   if constexpr (GPB == 1 && HDT != ANNA_MI_F32) {
-    // the wide form pays a barrier per 256-k pass and a pipeline fill per sweep, which the
-    // one-sweep-per-expert saving only repays when experts carry many routes: at the BASELINE
-    // MoE shapes it is 1.6x faster at 32 routes per expert (T = 512) and 2x slower at 0.5 and
-    // 4 (T = 8, 64), so it is taken from 16 routes per active expert on average
+    // Weights through LDS rings two steps ahead, x staged once per workgroup (16-bit hidden
+    // states, group 128, dims multiples of 256, intermediate <= 512), chosen by the routes per
+    // active expert on average (measured at config 5): from 16 (T = 512) the wide gate/up form,
+    // which sweeps up to 48 routes per weight pass at the price of a barrier per 256-k pass; from
+    // 2 (T = 64) the resident gate/up form, 16 routes with all of K in LDS and no barriers; down
+    // resident in both.  Below 2 (T = 8: ~50 of 128 experts with a route or two) the 16-route
+    // kernels, whose 64-row tiles keep more CUs busy, stay faster.
     if (a.group_size == 128 && a.hidden_dim % W_PK == 0 && a.intermediate_dim % W_PK == 0 &&
-        a.routes >= 16 * a.active_count) {
-      // one 8-wave workgroup per CU, persistent over the (expert, tile) items
-      const unsigned n1 = (unsigned)(a.active_count * ((a.intermediate_dim + W_GU_ROWS - 1) / W_GU_ROWS));
-      const unsigned dtiles = (unsigned)((a.hidden_dim + W_DN_ROWS - 1) / W_DN_ROWS);
-      const unsigned n2 = (unsigned)a.active_count *
-                          (a.intermediate_dim <= W_DN_KMAX ? (dtiles + W_DN_TPI - 1) / W_DN_TPI : dtiles);
-      auto grid = [](unsigned n) { return dim3(n < 256u ? (n + 7u) / 8u * 8u : 256u); };
-      auto k1 = moe_int4_mlp_wide_kernel<HDT, SDT, true>;
-      const bool resident = a.intermediate_dim <= W_DN_KMAX;
-      auto k2 = resident ? moe_int4_down_resident_kernel<HDT, SDT> : moe_int4_mlp_wide_kernel<HDT, SDT, false>;
-      static bool lds_set = false;
-      if (!lds_set) {
-        const void* ks[3] = {(const void*)k1, (const void*)moe_int4_down_resident_kernel<HDT, SDT>,
-                             (const void*)moe_int4_mlp_wide_kernel<HDT, SDT, false>};
-        for (const void* k : ks)
-          ANNA_CHECK(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, W_LDS) == hipSuccess,
+        a.intermediate_dim <= W_DN_KMAX && a.routes >= 2 * a.active_count) {
+      const bool many = a.routes >= 16 * a.active_count;
+      if (many || a.hidden_dim <= W_GU_KMAX) {
+        auto kgw = moe_int4_mlp_wide_kernel<HDT, SDT, true>;
+        auto kgr = moe_int4_resident_kernel<HDT, SDT, true>;
+        auto kd = moe_int4_resident_kernel<HDT, SDT, false>;
+        static bool lds_set = false;
+        if (!lds_set) {
+          ANNA_CHECK(hipFuncSetAttribute((const void*)kgw, hipFuncAttributeMaxDynamicSharedMemorySize, W_LDS) ==
+                             hipSuccess &&
+                         hipFuncSetAttribute((const void*)kgr, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             W_RES_LDS) == hipSuccess &&
+                         hipFuncSetAttribute((const void*)kd, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             W_RES_LDS) == hipSuccess,
                      "moe MLP: cannot raise the LDS limit");
-        lds_set = true;
+          lds_set = true;
+        }
+        auto grid = [](int64_t n) { return dim3((unsigned)(n < 256 ? (n + 7) / 8 * 8 : 256)); };
+        const int64_t gtiles = (a.intermediate_dim + W_GU_ROWS - 1) / W_GU_ROWS;
+        const int64_t dtiles = (a.hidden_dim + W_DN_ROWS - 1) / W_DN_ROWS;
+        if (many) {
+          hipLaunchKernelGGL(kgw, grid(a.active_count * gtiles), dim3(512), W_LDS, st, a);
+          ANNA_LAUNCH_CHECK("moe_int4_mlp_wide_kernel (gate, up)");
+        } else {
+          hipLaunchKernelGGL(kgr, grid(a.active_count * ((gtiles + W_GU_TPI - 1) / W_GU_TPI)), dim3(512), W_RES_LDS,
+                             st, a);
+          ANNA_LAUNCH_CHECK("moe_int4_resident_kernel (gate, up)");
+        }
+        hipLaunchKernelGGL(kd, grid(a.active_count * ((dtiles + W_DN_TPI - 1) / W_DN_TPI)), dim3(512), W_RES_LDS, st,
+                           a);
+        ANNA_LAUNCH_CHECK("moe_int4_resident_kernel (down)");
+        return ANNA_MI_OK;
       }
-      hipLaunchKernelGGL(k1, grid(n1), dim3(512), W_LDS, st, a);
-      ANNA_LAUNCH_CHECK("moe_int4_mlp_wide_kernel (gate, up)");
-      hipLaunchKernelGGL(k2, grid(n2), dim3(512), W_LDS, st, a);
-      ANNA_LAUNCH_CHECK("moe_int4_mlp_wide_kernel (down)");
-      return ANNA_MI_OK;
     }
   }
   anna_mi_moe_mlp_args b = a;

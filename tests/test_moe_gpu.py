@@ -118,6 +118,29 @@ def test_grouped_int4_mlp_matches_oracle(gpu, hdt, sdt, group, tokens, h, i):
     assert bool((out.cpu()[inactive] == 7.0).all())
 
 
+@pytest.mark.parametrize("hdt", [torch.bfloat16, torch.float16])
+def test_grouped_int4_mlp_skewed_routes(gpu, hdt):
+    """Few routes per expert on average (the resident gate/up form: 16 routes per sweep with all
+    of K in LDS) but one expert carrying every token (40 routes: three sweeps) against the fp64
+    oracle."""
+    print(f"[case] moe grouped MLP skewed routes {hdt}", flush=True)
+    torch.manual_seed(17)
+    e, k, h, i, tokens, group = 16, 2, 512, 256, 40, 128
+    bank = make_bank(e, h, i, group, torch.bfloat16, gpu, seed=23)
+    hidden = torch.randn(tokens, h, device=gpu, dtype=hdt)
+    logits = torch.randn(tokens, e, device=gpu)
+    logits[:, 0] += 8.0  # expert 0 is everyone's first choice
+    w, sel, usage = fused_ops.moe_router(logits, k, True)
+    assert int(usage[0]) == tokens
+    sti, off, compact, cw = fused_ops.moe_dispatch(hidden, w.to(hdt), sel, usage)
+    out = torch.full_like(compact, 7.0)
+    every = torch.arange(e, dtype=torch.int64, device=gpu)
+    fused_ops.moe_grouped_int4_mlp_out(compact, cw, out, off, every, every, *bank.tensors(), group, int(usage.max()))
+    offc = off.cpu()
+    ref = cp.moe_grouped_mlp(compact.cpu(), cw.cpu(), offc, dequant_experts(bank, range(e)), torch.float64)
+    assert rel_err(out.cpu().double().numpy(), ref.numpy()) <= BF16_TOL
+
+
 @pytest.mark.parametrize("tokens,sdt,group", [(6, torch.bfloat16, 128), (40, torch.float32, 128), (9, torch.float32, 64)])
 def test_grouped_int4_mlp_item_list_matches_grid(gpu, tokens, sdt, group):
     """The device-listed (persistent) form walks only experts with routes and gives the same
