@@ -385,6 +385,209 @@ __global__ __launch_bounds__(T::THREADS) void int4_gemm_tiled_kernel(
   }
 }
 
+// ------------------------------------------------------------------ skinny GEMM (small M)
+//
+// For a few dozen rows of x the tiled kernel's tiles are too few and too thin to keep the chip
+// busy, and splitting K over workgroups would write fp32 partials as large as the weights.  Here
+// a workgroup of SK_WAVES waves owns SK_MROWS = 32 rows of x against SK_RB = 48 rows of W over
+// all of K; the waves split K (128-k blocks) and meet once, in LDS, at the end.
+//   - W: each wave copies its rows x k-slice straight into its own LDS region, whole 128-byte
+//     lines per row per load (a load of 16 rows x 64 B, the shape an MFMA operand has in
+//     registers, ran at half the rate from HBM), and reads one dword per MFMA fragment back;
+//   - x: read from L2 into registers in MFMA layout (lane (r, kq) of load s: row r, k 32 s + 8 kq
+//     .. + 8 of the block), two blocks ahead;
+//   - W enters the MFMA as exact "off + q" fragments (one AND-OR per pair) shared by the two
+//     16-row halves of x, and the zero point and scale are applied per 128-k group as
+//     s * (sum x (off + q) - (off + z) sum x), the row sums of x coming from an MFMA against an
+//     all-ones operand in the same C layout.
+// The m-blocks of one W row block run on one XCD (workgroup w runs on XCD w % 8), so W comes from
+// HBM once and the other m-blocks read it from that XCD's L2.  A CU pulls ~130 GB/s from L2,
+// which is what bounds the x rows per workgroup (32 x K x 2 B) from above; the VALU work per
+// MFMA (the nibble conversion) bounds them from below.
+constexpr int SK_WAVES = 8, SK_PBMAX = 4, SK_NF = 3, SK_NC = 2;  // waves; blocks per pass; fragments
+constexpr int SK_RB = 16 * SK_NF, SK_MROWS = 16 * SK_NC;           // W rows, x rows per workgroup
+constexpr int SK_WREGION = SK_RB * 64 * SK_PBMAX;                  // LDS bytes per wave (12 KB)
+constexpr int SK_LDS = SK_WAVES * SK_WREGION;
+
+__device__ __forceinline__ void sk_copy_lds(__amdgpu_buffer_rsrc_t r, unsigned char* dst, uint32_t vo, int so) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)dst, 16, vo, so, 0, 0);
+}
+
+// PB: 128-k blocks per pass (1, 2 or 4: the launcher takes the fewest that cover a wave's share
+// in one pass, up to 4).  Every block a pass loads is used, those past the wave's share (clamped
+// reloads) with a zero factor: a load whose value is used only under a condition is sunk into
+// that branch by the compiler, below the counted wait for W, which then no longer covers W.
+template <int XDT, int SDT, int PB>
+__global__ __launch_bounds__(64 * SK_WAVES) void int4_gemm_skinny_kernel(
+    const uint16_t* __restrict__ x, int64_t M, int64_t K, int64_t xs, const uint32_t* __restrict__ qw, int64_t N,
+    int64_t pc, const typename Elem<SDT>::T* __restrict__ qs, const int8_t* __restrict__ qz,
+    uint16_t* __restrict__ y, int row_blocks, int m_blocks) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char sk_lds[];  // SK_LDS bytes
+  using ST = typename Elem<SDT>::T;
+  constexpr float OFF = XDT == ANNA_MI_BF16 ? 128.0f : 1024.0f;
+  constexpr uint32_t ONES = XDT == ANNA_MI_BF16 ? 0x3F803F80u : 0x3C003C00u;
+  constexpr int NF = SK_NF, NC = SK_NC;
+  // W in LDS: a pass's row span is UNITS 16-byte units (64 B per block); unit c of row R sits at
+  // slot c ^ ((R >> RSH) % UNITS), so that the 16 rows x 4 dwords of one fragment read fall on 64
+  // distinct banks
+  constexpr int UNITS = 4 * PB, ROWB = 16 * UNITS, RSH = PB == 4 ? 0 : PB == 2 ? 1 : 2;
+  constexpr int RPL = 1024 / ROWB, WLOADS = SK_RB / RPL;  // rows per 1 KB copy, copies per pass
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int r = lane & 15, kq = lane >> 4;
+  // item -> (row block, m-block); with whole octets of row blocks, the m-blocks of row block rb
+  // are workgroups 8 (m_blocks (rb / 8) + mb) + rb % 8: one XCD, launched together
+  const int b = (int)blockIdx.x;
+  int rb, mb;
+  if (row_blocks % NUM_XCD == 0) {
+    const int slot = b / NUM_XCD;
+    mb = slot % m_blocks;
+    rb = (slot / m_blocks) * NUM_XCD + b % NUM_XCD;
+  } else {
+    rb = b / m_blocks;
+    mb = b % m_blocks;
+  }
+  rb = __builtin_amdgcn_readfirstlane(rb);
+  mb = __builtin_amdgcn_readfirstlane(mb);
+  const int64_t n0 = (int64_t)rb * SK_RB, m0 = (int64_t)mb * SK_MROWS;
+  const int rows_w = (int)(N - n0 < SK_RB ? N - n0 : SK_RB);
+  const int rows_x = (int)(M - m0 < SK_MROWS ? M - m0 : SK_MROWS);
+  // buffer resources over this workgroup's rows: W rows past N and x rows past M read as zero
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(x + m0 * xs), 0, (int)(((rows_x - 1) * xs + K) * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rw =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(qw + n0 * pc), 0, (int)(rows_w * pc * 4), 0x00020000);
+  const int nblk = (int)(K / 128);
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<ST*>(qs), 0, (int)((int64_t)nblk * N * (int64_t)sizeof(ST)), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rz =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(qz), 0, (int)((int64_t)nblk * N), 0x00020000);
+  const int b_lo = wave * nblk / SK_WAVES, b_hi = (wave + 1) * nblk / SK_WAVES;
+  unsigned char* const wl = sk_lds + wave * SK_WREGION;
+  // W copy i: rows RPL i + lane / UNITS; the lane's slot lane % UNITS holds unit slot ^ key(row)
+  const int wrow0 = lane / UNITS, wslot = lane % UNITS;
+  auto w_voff = [&](int i) {
+    const int row = RPL * i + wrow0;
+    return (uint32_t)(row * pc * 4 + ((wslot ^ ((row >> RSH) & (UNITS - 1))) * 16));
+  };
+  // fragment read of (row 16 f + r, unit u, dword kq): byte offset in the wave's region
+  auto w_read = [&](int f, int u) -> uint32_t {
+    const int row = 16 * f + r;
+    return *(const uint32_t*)(wl + row * ROWB + ((u ^ ((row >> RSH) & (UNITS - 1))) * 16) + kq * 4);
+  };
+  // x of c-block c (rows 16 c + r): 16 bytes at k 32 s + 8 kq of a block
+  uint32_t xoff[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+    xoff[c] = 16 * c + r < rows_x ? (uint32_t)(((16 * c + r) * xs + kq * 8) * 2) : GM_OOB;
+  const u32x4 ones = {ONES, ONES, ONES, ONES};
+  f32x4 out[NF][NC];
+#pragma unroll
+  for (int f = 0; f < NF; ++f)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) out[f][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int p0 = b_lo; p0 < b_hi; p0 += PB) {
+    const int nb = b_hi - p0 < PB ? b_hi - p0 : PB;
+    // W of the whole pass first (a pass past the wave's share re-copies its own rows' units; the
+    // region is the wave's alone, and its reads of the previous pass are done)
+#pragma unroll
+    for (int i = 0; i < WLOADS; ++i) sk_copy_lds(rw, wl + i * 1024, w_voff(i), p0 * 64);
+    __builtin_amdgcn_sched_barrier(0);
+    // scale and zero point of group p0 + kq (lane (r, kq), row 16 f + r); block j's are taken
+    // from lane r + 16 j when it is used
+    uint32_t sraw[NF], zraw[NF];
+    const int gq = p0 + (kq < nb ? kq : nb - 1);
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      const uint32_t gi = (uint32_t)(gq * N + n0 + 16 * f + r);
+      if constexpr (sizeof(ST) == 4)
+        sraw[f] = __builtin_amdgcn_raw_buffer_load_b32(rs, gi * 4, 0, 0);
+      else
+        sraw[f] = __builtin_amdgcn_raw_buffer_load_b16(rs, gi * 2, 0, 0);
+      zraw[f] = __builtin_amdgcn_raw_buffer_load_b8(rz, gi, 0, 0);
+    }
+    u32x4 xv[PB][NC][4];
+    auto load_x = [&](int j) {
+      const int blk = p0 + (j < nb ? j : nb - 1);
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          xv[j][c][s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, xoff[c], (blk * 128 + s * 32) * 2, 0));
+    };
+    load_x(0);
+    if constexpr (PB > 1) load_x(1);
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NF + (PB > 1 ? 2 : 1) * NC * 4) : "memory");  // W is in LDS
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < PB; ++j) {
+      if (j + 2 < PB) load_x(j + 2);
+      f32x4 acc[NF][NC], sx[NC];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        sx[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int f = 0; f < NF; ++f) acc[f][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        u32x4 wf[NF];
+#pragma unroll
+        for (int f = 0; f < NF; ++f) wf[f] = nibbles_to_frag<XDT>(w_read(f, 4 * j + s));
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const u32x4 xa = interleave_x(xv[j][c][s]);
+          sx[c] = mfma16<XDT>(xa, ones, sx[c]);
+#pragma unroll
+          for (int f = 0; f < NF; ++f) acc[f][c] = mfma16<XDT>(xa, wf[f], acc[f][c]);
+        }
+      }
+      const int src = (r + 16 * j) * 4;
+#pragma unroll
+      for (int f = 0; f < NF; ++f) {
+        const uint32_t sv = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)sraw[f]);
+        const int zv = (int)(int8_t)(uint8_t)__builtin_amdgcn_ds_bpermute(src, (int)zraw[f]);
+        float sc;
+        if constexpr (sizeof(ST) == 4) sc = __uint_as_float(sv);
+        else sc = Elem<SDT>::to_f32((ST)sv);
+        if (j >= nb) sc = 0.f;  // a clamped reload of the wave's last block
+        const float zc = OFF + (float)zv;
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) out[f][c][i] = fmaf(sc, fmaf(-zc, sx[c][i], acc[f][c][i]), out[f][c][i]);
+      }
+    }
+  }
+  // the waves' partial sums through LDS (every wave's W reads are done after the barrier); wave
+  // w < NF NC sums fragment w % NF of c-block w / NF.  C layout: lane (r, kq) element i is x row
+  // m0 + 16 c + 4 kq + i, W row n0 + 16 f + r.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the clamped copies of the last pass
+  __syncthreads();
+  float* const red = (float*)sk_lds;  // [wave][fragment][c-block][element][lane]
+  static_assert(SK_WAVES * NF * NC * 4 * 64 * 4 <= SK_LDS, "reduction fits the W regions");
+#pragma unroll
+  for (int f = 0; f < NF; ++f)
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[(((wave * NF + f) * NC + c) * 4 + i) * 64 + lane] = out[f][c][i];
+  __syncthreads();
+  if (wave >= NF * NC) return;
+  const int f = wave % NF, c = wave / NF;
+  if (16 * f + r >= rows_w) return;
+  const int64_t n = n0 + 16 * f + r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < SK_WAVES; ++w) v += red[(((w * NF + f) * NC + c) * 4 + i) * 64 + lane];
+    const int m = 16 * c + 4 * kq + i;
+    if (m < rows_x) y[(m0 + m) * N + n] = Elem<XDT>::cvt(v);
+  }
+}
+
 }  // namespace
 
 bool int4_gemm_tiled_supported(int x_dtype, int64_t M, int64_t N, int64_t K, int64_t xs, const void* x, const void* qweight,
@@ -456,5 +659,53 @@ int int4_gemm_tiled_launch(const void* x, int x_dtype, int64_t M, int64_t K, int
   return ANNA_MI_OK;
 }
 
-}  // namespace anna
+int64_t int4_gemm_skinny_workgroups(int64_t M, int64_t N) {
+  return ((M + SK_MROWS - 1) / SK_MROWS) * ((N + SK_RB - 1) / SK_RB);
+}
 
+bool int4_gemm_skinny_supported(int x_dtype, int64_t M, int64_t N, int64_t K, int64_t xs, const void* x,
+                                const void* qweight, int64_t pc, int64_t gsz) {
+  // 32-bit buffer offsets: 32 x rows, 48 W rows, the scale / zero-point arrays
+  const bool fits = (SK_MROWS * xs + K) * 2 < (1ll << 31) && SK_RB * pc * 4 < (1ll << 31) && (K / 128) * N * 4 < (1ll << 31);
+  return (x_dtype == ANNA_MI_BF16 || x_dtype == ANNA_MI_F16) && M > 0 && gsz == 128 && K % 128 == 0 &&
+         K / 128 >= SK_WAVES && xs % 8 == 0 && pc % 4 == 0 && (uintptr_t)x % 16 == 0 &&
+         (uintptr_t)qweight % 16 == 0 && fits;
+}
+
+int int4_gemm_skinny_launch(const void* x, int x_dtype, int64_t M, int64_t K, int64_t xs, const int32_t* qweight,
+                            int64_t N, int64_t pc, const void* qscale, int scale_dtype, const int8_t* qzeros,
+                            void* y, hipStream_t st) {
+  // 48 W rows x 32 x rows per workgroup: N = 6144 gives 128 row blocks, 256 workgroups at M = 64
+  const int64_t m_blocks = (M + SK_MROWS - 1) / SK_MROWS, row_blocks = (N + SK_RB - 1) / SK_RB;
+  const int64_t per_wave = (K / 128 + SK_WAVES - 1) / SK_WAVES;  // the largest share of blocks
+  const int pb = per_wave <= 1 ? 1 : per_wave <= 2 ? 2 : 4;
+  ANNA_DISPATCH_DTYPE(scale_dtype, SDT, {
+    auto go = [&](auto xdt_tag, auto pb_tag) {
+      constexpr int XDT = decltype(xdt_tag)::value, PB = decltype(pb_tag)::value;
+      auto kern = int4_gemm_skinny_kernel<XDT, SDT, PB>;
+      static bool attr_set = false;
+      if (!attr_set) {
+        ANNA_CHECK(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, SK_LDS) ==
+                       hipSuccess,
+                   "int4 skinny GEMM: cannot raise the LDS limit");
+        attr_set = true;
+      }
+      hipLaunchKernelGGL(kern, dim3((unsigned)(row_blocks * m_blocks)), dim3(64 * SK_WAVES), SK_LDS, st,
+                         (const uint16_t*)x, M, K, xs, (const uint32_t*)qweight, N, pc,
+                         (const typename Elem<SDT>::T*)qscale, qzeros, (uint16_t*)y, (int)row_blocks, (int)m_blocks);
+      return ANNA_MI_OK;
+    };
+    auto go_pb = [&](auto xdt_tag) {
+      return pb == 1 ? go(xdt_tag, std::integral_constant<int, 1>{})
+             : pb == 2 ? go(xdt_tag, std::integral_constant<int, 2>{})
+                       : go(xdt_tag, std::integral_constant<int, 4>{});
+    };
+    const int rc = x_dtype == ANNA_MI_BF16 ? go_pb(std::integral_constant<int, ANNA_MI_BF16>{})
+                                           : go_pb(std::integral_constant<int, ANNA_MI_F16>{});
+    if (rc != ANNA_MI_OK) return rc;
+  });
+  ANNA_LAUNCH_CHECK("int4_gemm_skinny_kernel");
+  return ANNA_MI_OK;
+}
+
+}  // namespace anna

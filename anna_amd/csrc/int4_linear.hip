@@ -21,8 +21,9 @@
 //                       sum_k x (q - z) s = s * (sum_k x (off + q) - (off + z) sum_k x).
 //                    For M > 16 the 16-row groups of x take turns against the weights,
 //                    which stay in registers (W is read once for all of M).
-//   (M >= 64, or 16 < M < 64 with K > 4096, 16-bit activations, K % 64 == 0:
-//    int4_gemm_tiled_kernel, int4_gemm.hip)
+//   (16 < M <= 64 with group 128 and at most 256 workgroups of 32 x 48: int4_gemm_skinny_kernel;
+//    M >= 64, or 16 < M < 64 with K > 4096, 16-bit activations, K % 64 == 0:
+//    int4_gemm_tiled_kernel; both in int4_gemm.hip)
 //   int4_gemm_mfma   other M > 16.  LDS-tiled: a 128x128 tile of W is dequantized once per
 //                    workgroup to bf16 ((q - z) * s rounded to bf16, the reference's
 //                    dequant numerics) next to a 128x128 tile of x, and 4 waves run
@@ -836,6 +837,15 @@ extern "C" int anna_mi_int4_linear(const void* x, int x_dtype, int64_t M, int64_
     ANNA_LAUNCH_CHECK("int4_gemv_mfma");
     return ANNA_MI_OK;
   }
+  // 16 < M <= 64 (group 128, K a multiple of 1024) when its workgroups (32 rows of x x 48 rows of
+  // W each) fit one round of the chip: the skinny GEMM.  M = 64, K = 4096: N = 6144 (256
+  // workgroups) 14.5 us against 19.1 for the tiled GEMM; N = 12288 (512) 27 against 22.3, so
+  // larger grids stay with the tiled GEMM / the row-group GEMV.  ANNA_MI_INT4_SKINNY_MMAX moves
+  // the upper bound of M (0 turns the skinny GEMM off).
+  static const int skinny_mmax = env_int("ANNA_MI_INT4_SKINNY_MMAX", 64);
+  if (x16 && M > 16 && M <= skinny_mmax && int4_gemm_skinny_workgroups(M, N) <= 256 &&
+      int4_gemm_skinny_supported(x_dtype, M, N, K, xs, x, qweight, pc, gsz))
+    return int4_gemm_skinny_launch(x, x_dtype, M, K, xs, qweight, N, pc, qscale, scale_dtype, qzeros, y, st);
   // 16 < M < 64: the GEMV with 16-row groups of x against register-resident weights (M = 17..48
   // at N = 12288, K = 4096: 24-35 us, where the LDS-tiled fallback below took ~145 us); from
   // M = 64 the tiled GEMM is faster (27.6 against 46 us at M = 64)

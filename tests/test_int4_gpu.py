@@ -114,6 +114,33 @@ def test_int4_gemm_config2_bench_sizes(gpu, monkeypatch, m, n):
     assert np.isfinite(y).all() and (np.abs(y).max(axis=0) > 0).all()
 
 
+@pytest.mark.parametrize("m,k,n,sdt,xdt,stride", [
+    (64, 4096, 6144, "bf16", "bf16", 0),     # BASELINE config 2 at M = 64: 128 row blocks x 2 m-blocks
+    (33, 1024, 1000, "fp32", "f16", 0),      # one 128-k block per wave, partial m-block and row block
+    (17, 2048, 96, "bf16", "bf16", 0),       # one row block, a 1-row second m-block
+    (64, 1152, 200, "bf16", "f16", 0),       # 9 blocks over 8 waves: one wave takes two
+    (50, 12288, 300, "fp32", "bf16", 0),     # 12 blocks per wave: three passes of four
+    (40, 2048, 500, "bf16", "bf16", 2560),   # strided x rows
+])
+def test_int4_skinny_gemm(gpu, m, k, n, sdt, xdt, stride):
+    """The skinny GEMM (16 < M <= 64, group 128, K >= 1024, at most 256 workgroups): 32 rows of x
+    per workgroup against 48 rows of W, K split over the waves, W copied into LDS by whole lines,
+    "off + q" MFMA fragments with the zero point removed per group."""
+    print(f"[case] int4 skinny GEMM M={m} K={k} N={n} scale={sdt} x={xdt} stride={stride}", flush=True)
+    group = 128
+    rng = np.random.default_rng(m * 31 + k + n)
+    qw, qs, qz = int4_payload(rng, n, k, group, scale_dtype=sdt)
+    cols = stride or k
+    xb = orc.bf16_bits(rng.normal(size=(m, cols)).astype(np.float32))
+    ref = orc.int4_linear(np.ascontiguousarray(xb[:, :k]), qw, qs, qz, group)
+    tdt = torch.bfloat16 if xdt == "bf16" else torch.float16
+    x = _x_tensor(xb, tdt, gpu)[:, :k]
+    qs_t = _dev(qs, gpu).to(torch.bfloat16 if sdt == "bf16" else torch.float32)
+    out = torch.empty((m, n), dtype=tdt, device=gpu)
+    fused_ops.int4_linear_out(x, _dev(qw, gpu), qs_t, _dev(qz, gpu), group, k, out)
+    assert rel_err(out.float().cpu().numpy(), ref) <= BF16_TOL
+
+
 @pytest.mark.parametrize("xdt", [torch.float16, torch.float32])
 @pytest.mark.parametrize("m", [1, 4, 128])
 def test_int4_linear_other_activation_dtypes(gpu, xdt, m):
