@@ -427,11 +427,14 @@ __global__ __launch_bounds__(64 * SK_WAVES) void int4_gemm_skinny_kernel(
   constexpr float OFF = XDT == ANNA_MI_BF16 ? 128.0f : 1024.0f;
   constexpr uint32_t ONES = XDT == ANNA_MI_BF16 ? 0x3F803F80u : 0x3C003C00u;
   constexpr int NF = SK_NF, NC = SK_NC;
-  // W in LDS: a pass's row span is UNITS 16-byte units (64 B per block); unit c of row R sits at
-  // slot c ^ ((R >> RSH) % UNITS), so that the 16 rows x 4 dwords of one fragment read fall on 64
-  // distinct banks
-  constexpr int UNITS = 4 * PB, ROWB = 16 * UNITS, RSH = PB == 4 ? 0 : PB == 2 ? 1 : 2;
-  constexpr int RPL = 1024 / ROWB, WLOADS = SK_RB / RPL;  // rows per 1 KB copy, copies per pass
+  // W in LDS: a pass is copied in halves of up to two blocks (128 B of each row: whole lines),
+  // so that the first two blocks' compute need not wait for the rest of the pass.  A half's row
+  // span is UNITS 16-byte units (64 B per block); unit c of row R sits at slot c ^ ((R >> RSH) %
+  // UNITS), so that the 16 rows x 4 dwords of one fragment read fall on 64 distinct banks.
+  constexpr int HB = PB < 2 ? PB : 2, HALVES = PB / HB;  // blocks per half, halves per pass
+  constexpr int UNITS = 4 * HB, ROWB = 16 * UNITS, RSH = HB == 2 ? 1 : 2;
+  constexpr int RPL = 1024 / ROWB, WLOADS = SK_RB / RPL;  // rows per 1 KB copy, copies per half
+  constexpr int HBYTES = SK_RB * ROWB;                     // LDS bytes of one half
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int r = lane & 15, kq = lane >> 4;
   // item -> (row block, m-block); with whole octets of row blocks, the m-blocks of row block rb
@@ -469,10 +472,10 @@ __global__ __launch_bounds__(64 * SK_WAVES) void int4_gemm_skinny_kernel(
     const int row = RPL * i + wrow0;
     return (uint32_t)(row * pc * 4 + ((wslot ^ ((row >> RSH) & (UNITS - 1))) * 16));
   };
-  // fragment read of (row 16 f + r, unit u, dword kq): byte offset in the wave's region
-  auto w_read = [&](int f, int u) -> uint32_t {
+  // fragment read of (row 16 f + r, unit u of half h, dword kq)
+  auto w_read = [&](int h, int f, int u) -> uint32_t {
     const int row = 16 * f + r;
-    return *(const uint32_t*)(wl + row * ROWB + ((u ^ ((row >> RSH) & (UNITS - 1))) * 16) + kq * 4);
+    return *(const uint32_t*)(wl + h * HBYTES + row * ROWB + ((u ^ ((row >> RSH) & (UNITS - 1))) * 16) + kq * 4);
   };
   // x of c-block c (rows 16 c + r): 16 bytes at k 32 s + 8 kq of a block
   uint32_t xoff[NC];
@@ -491,7 +494,9 @@ __global__ __launch_bounds__(64 * SK_WAVES) void int4_gemm_skinny_kernel(
     // W of the whole pass first (a pass past the wave's share re-copies its own rows' units; the
     // region is the wave's alone, and its reads of the previous pass are done)
 #pragma unroll
-    for (int i = 0; i < WLOADS; ++i) sk_copy_lds(rw, wl + i * 1024, w_voff(i), p0 * 64);
+    for (int h = 0; h < HALVES; ++h)
+#pragma unroll
+      for (int i = 0; i < WLOADS; ++i) sk_copy_lds(rw, wl + h * HBYTES + i * 1024, w_voff(i), (p0 + h * HB) * 64);
     __builtin_amdgcn_sched_barrier(0);
     // scale and zero point of group p0 + kq (lane (r, kq), row 16 f + r); block j's are taken
     // from lane r + 16 j when it is used
@@ -518,10 +523,17 @@ __global__ __launch_bounds__(64 * SK_WAVES) void int4_gemm_skinny_kernel(
     load_x(0);
     if constexpr (PB > 1) load_x(1);
     __builtin_amdgcn_sched_barrier(0);
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NF + (PB > 1 ? 2 : 1) * NC * 4) : "memory");  // W is in LDS
+    // the first half of W is in LDS
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((HALVES - 1) * WLOADS + 2 * NF + (PB > 1 ? 2 : 1) * NC * 4) : "memory");
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < PB; ++j) {
+      if (j == HB) {
+        // the second half of W: all but the x loads issued since (blocks 2 and 3)
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NC * 4) : "memory");
+        __builtin_amdgcn_sched_barrier(0);
+      }
       if (j + 2 < PB) load_x(j + 2);
       f32x4 acc[NF][NC], sx[NC];
 #pragma unroll
@@ -534,7 +546,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void int4_gemm_skinny_kernel(
       for (int s = 0; s < 4; ++s) {
         u32x4 wf[NF];
 #pragma unroll
-        for (int f = 0; f < NF; ++f) wf[f] = nibbles_to_frag<XDT>(w_read(f, 4 * j + s));
+        for (int f = 0; f < NF; ++f) wf[f] = nibbles_to_frag<XDT>(w_read(j / HB, f, 4 * (j % HB) + s));
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
           const u32x4 xa = interleave_x(xv[j][c][s]);
