@@ -21,9 +21,9 @@
 //   * a packed item rotates its G query heads itself, q' = R q (FWHT in registers, one wave
 //     per head), into the B-operand fragments of the score product; 8 waves take 32-token blocks
 //     (the next block prefetched).  Scores are formed transposed, S^T = Khat Q'^T, by
-//     v_mfma_f32_16x16x32_f16 on codes turned into fp16 centroids with one v_perm per pair (the
-//     2-bit centroids are fp16 values sharing their low byte); S^T's accumulator layout is the
-//     B operand of O'^T = Vhat^T P^T, so the probabilities never leave registers.  Online
+//     v_mfma_f32_16x16x32_f16 on codes turned into fp16 centroids by a 256-entry LDS table (a
+//     code byte -> its four centroids, one 8-byte read per four codes); S^T's accumulator
+//     layout is the B operand of O'^T = Vhat^T P^T, so the probabilities never leave registers.  Online
 //     softmax in base 2 with lazy rescaling (the running max moves only by > 2^4).  The window
 //     item does the same on the dense bf16 ring with the unrotated q.
 //   * each item writes (max, denominator) and its values divided by the denominator (fp16) to
@@ -68,16 +68,23 @@ __device__ __forceinline__ f32x4 mfma_bf16(u32x4 a, u32x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-// 2-bit codes at bits 8+2p (low half) and 24+2p (high half) of x -> 4 fp16 pairs.
-// lut_hi holds the high bytes of the fp16 centroids {-b, -a, +a, +b}; lut_lo their common
-// low byte; or_c = 0x04000400 (selector offset to the lut_hi bytes).
-__device__ __forceinline__ u32x4 codes_to_f16(uint32_t x, uint32_t lut_hi, uint32_t lut_lo, uint32_t or_c) {
-  u32x4 r;
-  r.x = __builtin_amdgcn_perm(lut_hi, lut_lo, (x & 0x03000300u) | or_c);
-  r.y = __builtin_amdgcn_perm(lut_hi, lut_lo, ((x >> 2) & 0x03000300u) | or_c);
-  r.z = __builtin_amdgcn_perm(lut_hi, lut_lo, ((x >> 4) & 0x03000300u) | or_c);
-  r.w = __builtin_amdgcn_perm(lut_hi, lut_lo, ((x >> 6) & 0x03000300u) | or_c);
-  return r;
+// The fp16 2-bit centroids {-b, -a, +a, +b} (high bytes 0xC3, 0xBC, 0x3C, 0x43, common low byte
+// 0x7E: -3.74609375, -1.123046875, 1.123046875, 3.74609375) and the decode table built from
+// them: entry c of the 256 holds the centroids of the four codes of byte c (code i at bits 2i)
+// as four fp16, lowest code first.
+constexpr uint32_t TQ2_F16[4] = {0xC37Eu, 0xBC7Eu, 0x3C7Eu, 0x437Eu};
+__device__ __forceinline__ uint2 tq2_lut_entry(uint32_t c) {
+  return make_uint2(TQ2_F16[c & 3u] | (TQ2_F16[(c >> 2) & 3u] << 16),
+                    TQ2_F16[(c >> 4) & 3u] | (TQ2_F16[(c >> 6) & 3u] << 16));
+}
+
+// Two code bytes (bits 8 s .. 8 s + 15 of w) -> the 8 fp16 centroids of their codes, in code
+// order: one table read per byte.  (Turning codes into fp16 by byte permutes took 11 VALU
+// instructions per 8 codes, two thirds of a block's VALU work; a table read is 1 VALU for the
+// address and one LDS read.)
+__device__ __forceinline__ u32x4 codes_lut(const uint2* lut, uint32_t w, int s) {
+  const uint2 lo = lut[(w >> (8 * s)) & 0xFFu], hi = lut[(w >> (8 * s + 8)) & 0xFFu];
+  return u32x4{lo.x, lo.y, hi.x, hi.y};
 }
 
 __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
@@ -177,13 +184,15 @@ __device__ __forceinline__ uint32_t pkrtz(float lo, float hi) {
 // here); otherwise the 2-bit codes already loaded into cur.
 // qf: the packed path's B fragments of the score product, held in registers for the whole item
 // (the residual path reads s_qf and passes nullptr)
+// lut: the code-byte table in LDS.  Token order of the value product's k dimension (lane (r, kq),
+// element e): token 16 (e / 4) + 4 kq + e % 4, for the packed codes and the window alike.
 template <bool RESID>
 __device__ __forceinline__ void block_step(const anna_mi_tq_decode_args& a, const u32x4 (*s_qf)[64], const u32x4* qf,
-                                           int64_t b, int64_t h, int64_t tb, int64_t tend, int64_t skip, int lane,
-                                           const BlockRaw& cur, f32x4 (&acc)[16], float& m_run, float& l_run) {
+                                           const uint2* lut, int64_t b, int64_t h, int64_t tb, int64_t tend,
+                                           int64_t skip, int lane, const BlockRaw& cur, f32x4 (&acc)[16],
+                                           float& m_run, float& l_run) {
   const int r = lane & 15, kq = lane >> 4;
   const int64_t Rc = a.residual_capacity;
-  const uint32_t lut_hi = vconst(0x433CBCC3u), lut_lo = vconst(0x7E7E7E7Eu), or_c = vconst(0x04000400u);
   const float kscale = a.key_scale * a.scaling * LOG2E;
   const float vscale = a.value_scale * P_SCALE;
   {
@@ -191,12 +200,12 @@ __device__ __forceinline__ void block_step(const anna_mi_tq_decode_args& a, cons
     f32x4 st0 = {0.f, 0.f, 0.f, 0.f}, st1 = {0.f, 0.f, 0.f, 0.f};
     uint2 rlo[RESID ? 16 : 1], rhi[RESID ? 16 : 1];
     if constexpr (!RESID) {
+      // step st: code bytes 2 (st % 2), + 1 of word st / 2 (dims 64 kq + 16 (st / 2) + 8 (st % 2) ..
+      // + 7 of tokens r and 16 + r)
 #pragma unroll
       for (int st = 0; st < 8; ++st) {
-        const uint32_t w0 = cur.k0[st >> 1], w1 = cur.k1[st >> 1];
-        const uint32_t x0 = (st & 1) ? w0 : (w0 << 8), x1 = (st & 1) ? w1 : (w1 << 8);
-        st0 = mfma_f16(codes_to_f16(x0, lut_hi, lut_lo, or_c), qf[st], st0);
-        st1 = mfma_f16(codes_to_f16(x1, lut_hi, lut_lo, or_c), qf[st], st1);
+        st0 = mfma_f16(codes_lut(lut, cur.k0[st >> 1], 2 * (st & 1)), qf[st], st0);
+        st1 = mfma_f16(codes_lut(lut, cur.k1[st >> 1], 2 * (st & 1)), qf[st], st1);
         __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
@@ -274,36 +283,29 @@ __device__ __forceinline__ void block_step(const anna_mi_tq_decode_args& a, cons
       for (int j = 0; j < 16; ++j) acc[j] *= alpha;
       m_run = m_new;
     }
+    // s[i] is token 4 kq + i (i < 4) or 16 + 4 kq + i - 4: element i of the value product's B
     u32x4 pf;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float p0 = __builtin_amdgcn_exp2f(s[i] - m_run), p1 = __builtin_amdgcn_exp2f(s[4 + i] - m_run);
+    for (int i2 = 0; i2 < 4; ++i2) {
+      float p0 = __builtin_amdgcn_exp2f(s[2 * i2] - m_run), p1 = __builtin_amdgcn_exp2f(s[2 * i2 + 1] - m_run);
       if (RESID) {  // a window block can be all masked (the skipped slot alone), m_run still -inf
-        p0 = s[i] == -INFINITY ? 0.f : p0;
-        p1 = s[4 + i] == -INFINITY ? 0.f : p1;
+        p0 = s[2 * i2] == -INFINITY ? 0.f : p0;
+        p1 = s[2 * i2 + 1] == -INFINITY ? 0.f : p1;
       }
       l_run += p0 + p1;
-      pf[i] = RESID ? pack_bf16x2(p0 * nv[i], p1 * nv[4 + i]) : pkrtz(p0 * nv[i], p1 * nv[4 + i]);
+      pf[i2] = RESID ? pack_bf16x2(p0 * nv[2 * i2], p1 * nv[2 * i2 + 1]) : pkrtz(p0 * nv[2 * i2], p1 * nv[2 * i2 + 1]);
     }
     if constexpr (!RESID) {
+      // tile j: the two code bytes of dim 16 r + j (tokens 4 kq .. + 3, then 16 + 4 kq .. + 3)
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const uint32_t w = (j >> 3) ? cur.v1[(j >> 1) & 3] : cur.v0[(j >> 1) & 3];
-        const uint32_t xv = __builtin_amdgcn_perm(w, w, (j & 1) ? 0x030C020Cu : 0x010C000Cu);
-        acc[j] = mfma_f16(codes_to_f16(xv, lut_hi, lut_lo, or_c), pf, acc[j]);
+        acc[j] = mfma_f16(codes_lut(lut, w, 2 * (j & 1)), pf, acc[j]);
         __builtin_amdgcn_sched_barrier(0);
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const uint2 lo = rlo[j], hi = rhi[j];
-        u32x4 av;
-        av.x = __builtin_amdgcn_perm(hi.x, lo.x, 0x05040100u);
-        av.y = __builtin_amdgcn_perm(hi.x, lo.x, 0x07060302u);
-        av.z = __builtin_amdgcn_perm(hi.y, lo.y, 0x05040100u);
-        av.w = __builtin_amdgcn_perm(hi.y, lo.y, 0x07060302u);
-        acc[j] = mfma_bf16(av, pf, acc[j]);
-      }
+      for (int j = 0; j < 16; ++j) acc[j] = mfma_bf16(u32x4{rlo[j].x, rlo[j].y, rhi[j].x, rhi[j].y}, pf, acc[j]);
     }
   }
 }
@@ -314,13 +316,14 @@ __device__ __forceinline__ void block_step(const anna_mi_tq_decode_args& a, cons
 // accumulators two register homes and a copy per pair); the prefetch is unconditional (clamped
 // to the last block) so that no wait for it is forced before the current block is consumed.
 template <bool RESID>
-__device__ __forceinline__ void run_blocks(const anna_mi_tq_decode_args& a, const u32x4 (*s_qf)[64], int64_t b, int64_t h,
+__device__ __forceinline__ void run_blocks(const anna_mi_tq_decode_args& a, const u32x4 (*s_qf)[64], const uint2* lut,
+                                           int64_t b, int64_t h,
                                            int64_t tb0, int64_t tend, int64_t skip, int64_t nblk, int wave, int lane,
                                            BlockRaw& A, f32x4 (&acc)[16], float& m_run, float& l_run) {
   const int r = lane & 15, kq = lane >> 4;
   if constexpr (RESID) {
     for (int64_t blk = wave; blk < nblk; blk += SWAVES)
-      block_step<true>(a, s_qf, nullptr, b, h, tb0 + blk * TBT, tend, skip, lane, A, acc, m_run, l_run);
+      block_step<true>(a, s_qf, nullptr, lut, b, h, tb0 + blk * TBT, tend, skip, lane, A, acc, m_run, l_run);
   } else {
     u32x4 qf[8];
 #pragma unroll
@@ -334,11 +337,11 @@ __device__ __forceinline__ void run_blocks(const anna_mi_tq_decode_args& a, cons
     int64_t i = 0;
     for (; i + 1 < cnt; i += 2) {
       load_block(a, h, slot(i + 1), r, kq, B);
-      block_step<false>(a, s_qf, qf, b, h, slot(i), tend, -1, lane, A, acc, m_run, l_run);
+      block_step<false>(a, s_qf, qf, lut, b, h, slot(i), tend, -1, lane, A, acc, m_run, l_run);
       load_block(a, h, slot(i + 2), r, kq, A);
-      block_step<false>(a, s_qf, qf, b, h, slot(i + 1), tend, -1, lane, B, acc, m_run, l_run);
+      block_step<false>(a, s_qf, qf, lut, b, h, slot(i + 1), tend, -1, lane, B, acc, m_run, l_run);
     }
-    if (i < cnt) block_step<false>(a, s_qf, qf, b, h, slot(i), tend, -1, lane, A, acc, m_run, l_run);
+    if (i < cnt) block_step<false>(a, s_qf, qf, lut, b, h, slot(i), tend, -1, lane, A, acc, m_run, l_run);
   }
 }
 
@@ -501,9 +504,11 @@ void tq_decode_kernel(const anna_mi_tq_decode_args a, const anna_mi_tq_append_ar
   __shared__ float s_m[SWAVES][16], s_l[SWAVES][16];
   __shared__ int s_nb[MAX_SEQS], s_len[MAX_SEQS], s_off[MAX_SEQS];
   __shared__ ItemInfo s_it;
+  __shared__ uint2 s_lut[256];  // code byte -> its four fp16 centroids
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, kq = lane >> 4;
   if (wave == 0) plan_item(a, lane, s_nb, s_len, s_off, &s_it);
+  if (threadIdx.x >= 256) s_lut[threadIdx.x - 256] = tq2_lut_entry(threadIdx.x - 256);
   __syncthreads();
   const ItemInfo it = s_it;
   if (it.kind < 0) return;
@@ -577,12 +582,12 @@ void tq_decode_kernel(const anna_mi_tq_decode_args a, const anna_mi_tq_append_ar
       *(float4*)(s_q + n * TD + 4 * lane) = make_float4(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
     }
     __syncthreads();
-    // fragment of step st = wave: element e holds dim 64 kq + 16 (st >> 1) + 4 (st & 1) + (e >> 1) + 8 (e & 1)
-    const int dim0 = 64 * kq + 16 * (wave >> 1) + 4 * (wave & 1);
+    // fragment of step st = wave: element e holds dim 64 kq + 16 (st >> 1) + 8 (st & 1) + e
+    const int dim0 = 64 * kq + 16 * (wave >> 1) + 8 * (wave & 1);
     const float* qr = s_q + r * TD + dim0;
     u32x4 f;
 #pragma unroll
-    for (int e2 = 0; e2 < 4; ++e2) f[e2] = pack_f16x2(qr[e2], qr[e2 + 8]);
+    for (int e2 = 0; e2 < 4; ++e2) f[e2] = pack_f16x2(qr[2 * e2], qr[2 * e2 + 1]);
     s_qf[wave][lane] = f;
   } else {
     const u32x4 v = *(const u32x4*)(qg + (r < G ? r : 0) * TD + wave * 32 + kq * 8);
@@ -595,9 +600,9 @@ void tq_decode_kernel(const anna_mi_tq_decode_args a, const anna_mi_tq_append_ar
   for (int j = 0; j < 16; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
   if (resid)
-    run_blocks<true>(a, s_qf, b, h, tb0, tend, skip, nblk, wave, lane, cur, acc, m_run, l_run);
+    run_blocks<true>(a, s_qf, s_lut, b, h, tb0, tend, skip, nblk, wave, lane, cur, acc, m_run, l_run);
   else
-    run_blocks<false>(a, s_qf, b, h, tb0, tend, -1, nblk, wave, lane, cur, acc, m_run, l_run);
+    run_blocks<false>(a, s_qf, s_lut, b, h, tb0, tend, -1, nblk, wave, lane, cur, acc, m_run, l_run);
 
   if constexpr (FUSED) {
     // the window workgroup quantizes the token leaving the ring into the pool slot just past its
