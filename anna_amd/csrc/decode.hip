@@ -16,6 +16,7 @@
 //
 // Reference: launch_gqa_decode_splitkv_fused_xpu (gated_delta_fused_op.sycl:4494-4706)
 // and launch_gqa_decode_splitkv_turboquant_fused_xpu (sycl:4771-5094).
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 
@@ -666,12 +667,17 @@ __device__ __forceinline__ uint32_t pack2_16(float lo, float hi) {
 // Loads of one tile: key rows, and the raw min/max codes of the lane's two staging tokens (the
 // lane's QD dims of a token are one CW-word vector load) with their scales and zeros (span i of
 // 32 dims, token u; one zero-extended 16-bit load each, so nothing is combined before use).
-template <int D, int SB>
+// KSB (TQ-MSE keys): the code words of tokens r and 16 + r (the lane's D / 4 dims) and the norms
+// of the lane's eight score rows.
+template <int D, int SB, int KSB>
 struct MfmaTileRegs {
   static constexpr int NST = D / 32, QD = D / 4, NSP = QD >= 32 ? QD / 32 : 1;
   static constexpr int CW = SB == 0 ? 1 : (QD * SB / 8 + 3) / 4;  // 32-bit words of codes per token
+  static constexpr int KCW = KSB == 0 ? 1 : QD * KSB / 32;         // 32-bit words of key codes per lane
   u32x4 ka[NST], kb[NST];
   uint32_t vc[2][CW], vsc[NSP][2], vzr[NSP][2];
+  uint32_t kc[2][KCW];
+  uint32_t kn[8];
 };
 
 // n 32-bit words from p (aligned to min(4 n, 16) bytes) as whole-vector loads.
@@ -698,11 +704,19 @@ __device__ __forceinline__ void load_words(uint32_t (&w)[N], const uint8_t* p) {
 // NT: tiles per range, fixed (1..4: every load is issued unconditionally, from clamped rows past
 // the range's end, so the compiler waits for exactly the loads each step uses), or 0 (any count,
 // runtime loop).
-template <int DT, int VF, int SB, int D, int NT>
+// KSB: 0 for dense keys; 2 or 4 for TQ-MSE key codes in fields of that many bits.  Then the
+// ranges are aligned to the segments (the first nr1 cover the packed tokens, the rest the window):
+// a packed range scores its codes, turned into fp16 centroids by a 256-entry LDS table (code byte
+// -> its 2 or 4 centroids), against the rotated query q' = R q (fp16 fragments, lane (head, kq) of
+// step st: dims QD kq + 8 st .. + 7) and scales each score by its token's norm; a window range
+// runs as with dense keys.
+// SEQ: per-row lengths (a.seq_lengths): row b's valid tokens are the first n1 packed slots and
+// the first n2 window slots; a range with none of them writes an empty partial.
+template <int DT, int VF, int SB, int D, int NT, int KSB, bool SEQ>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 : 1, NT == 2 ? 2 : 1))) void decode_split_mfma_kernel(
-    const anna_mi_decode_args a, const int64_t range) {
-  using Regs = MfmaTileRegs<D, SB>;
-  constexpr int NST = Regs::NST, NSP = Regs::NSP, QD = Regs::QD, CW = Regs::CW;
+    const anna_mi_decode_args a, const int64_t range, const int64_t nr1) {
+  using Regs = MfmaTileRegs<D, SB, KSB>;
+  constexpr int NST = Regs::NST, NSP = Regs::NSP, QD = Regs::QD, CW = Regs::CW, KCW = Regs::KCW;
   constexpr int NDT = D / 16;  // 16-dim tiles of the value product
   constexpr float LOG2E = 1.4426950408889634f;
   constexpr float LAZY = 4.0f;
@@ -712,7 +726,25 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
   const int64_t blk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int G = (int)(a.q_heads / a.kv_heads);
   const int64_t L1 = a.len1, L = a.len1 + a.len2;
-  const int64_t t0 = blk * range, t1 = t0 + range < L ? t0 + range : L;
+  int64_t t0, t1;
+  bool packed_rng = false;  // (TQ-MSE keys) a range of packed tokens
+  if (KSB > 0 && blk < nr1) {
+    t0 = blk * range;
+    t1 = t0 + range < L1 ? t0 + range : L1;
+    packed_rng = true;
+  } else {
+    t0 = KSB > 0 ? L1 + (blk - nr1) * range : blk * range;
+    t1 = t0 + range < L ? t0 + range : L;
+  }
+  // row b's valid tokens: [0, n1) and [L1, L1 + n2)
+  int64_t n1 = L1, n2 = a.len2;
+  if constexpr (SEQ) {
+    const int64_t n = a.seq_lengths[b];
+    n2 = n < a.len2 ? n : a.len2;
+    n1 = n - n2 < L1 ? n - n2 : L1;
+  }
+  auto valid = [&](int64_t t) { return t < t1 && (!SEQ || t < n1 || (t >= L1 && t < L1 + n2)); };
+  const bool live = !SEQ || t0 < n1 || (t1 > L1 && t0 < L1 + n2);
   const int ntiles = NT > 0 ? NT : (int)((t1 - t0 + MF_TILE - 1) / MF_TILE);
   // raw-code staging: scale groups of whole 32-dim spans, code vectors aligned for one load
   constexpr uintptr_t CA = 4 * CW < 16 ? 4 * CW : 16;
@@ -738,6 +770,23 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
 
   __shared__ __attribute__((aligned(16))) uint16_t s_vt[D * MF_VT];
   __shared__ u32x4 s_qf[NST][64];
+  // TQ-MSE keys: code byte -> fp16 centroids of its codes, lowest field first (4-bit fields: 2 per
+  // entry; 2-bit: 4 per entry)
+  __shared__ uint32_t s_klut[KSB == 0 ? 1 : KSB == 4 ? 256 : 512];
+  if constexpr (KSB > 0) {
+    const uint32_t cmask = (1u << a.key_bits) - 1u;  // 3-bit codes in 4-bit fields stay below 8
+    auto c16 = [&](uint32_t c) { return (uint32_t)f32_to_f16_bits(a.key_centroids[c & cmask]); };
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t e = (uint32_t)(lane + 64 * i);
+      if constexpr (KSB == 4) {
+        s_klut[e] = c16(e & 15u) | (c16(e >> 4) << 16);
+      } else {
+        s_klut[2 * e] = c16(e & 3u) | (c16((e >> 2) & 3u) << 16);
+        s_klut[2 * e + 1] = c16((e >> 4) & 3u) | (c16(e >> 6) << 16);
+      }
+    }
+  }
   uint32_t* vw = (uint32_t*)s_vt;  // word (d, p) at d * MF_VT / 2 + p: dim d of tokens 2p, 2p + 1
 
   // the raw path takes tiles whose tokens are all packed (min/max); others are staged by the
@@ -778,12 +827,38 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
     }
     // key rows of tokens tt0 + r and tt0 + 16 + r (clamped into the range; masked below)
     const int64_t ta = tt0 + r < t1 ? tt0 + r : t1 - 1, tb = tt0 + 16 + r < t1 ? tt0 + 16 + r : t1 - 1;
-    const uint16_t* ra = key_row(ta);
-    const uint16_t* rb = key_row(tb);
+    if (KSB > 0 && packed_rng) {
+      // the lane's key code words of both tokens, and the norms of its score rows (tokens
+      // 4 kq + i, 16 + 4 kq + i, clamped into the range: the last tile may pass the segment)
+      const uint8_t* kc0 = (const uint8_t*)a.key.ptr + b * a.key.s0 + kvh * a.key.s1 + QD * kq * KSB / 8;
+      load_words<KCW>(R.kc[0], kc0 + ta * a.key.s2);
+      load_words<KCW>(R.kc[1], kc0 + tb * a.key.s2);
+      const uint16_t* kn0 = (const uint16_t*)a.key_norms.ptr + b * a.key_norms.s0 + kvh * a.key_norms.s1;
+      if (tt0 + MF_TILE <= t1 && a.key_norms.s2 == 1 && (uintptr_t)kn0 % 8 == 0) {
+        // a whole tile of contiguous norms: the lane's two runs of four as two 8-byte loads
 #pragma unroll
-    for (int st = 0; st < NST; ++st) {
-      R.ka[st] = *(const u32x4*)(ra + 32 * st + 8 * kq);
-      R.kb[st] = *(const u32x4*)(rb + 32 * st + 8 * kq);
+        for (int hh = 0; hh < 2; ++hh) {
+          const uint2 w = *(const uint2*)(kn0 + tt0 + 16 * hh + 4 * kq);
+          R.kn[4 * hh] = w.x & 0xFFFFu;
+          R.kn[4 * hh + 1] = w.x >> 16;
+          R.kn[4 * hh + 2] = w.y & 0xFFFFu;
+          R.kn[4 * hh + 3] = w.y >> 16;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int64_t t = tt0 + 16 * (i >> 2) + 4 * kq + (i & 3);
+          R.kn[i] = kn0[(t < t1 ? t : t1 - 1) * a.key_norms.s2];
+        }
+      }
+    } else {
+      const uint16_t* ra = key_row(ta);
+      const uint16_t* rb = key_row(tb);
+#pragma unroll
+      for (int st = 0; st < NST; ++st) {
+        R.ka[st] = *(const u32x4*)(ra + 32 * st + 8 * kq);
+        R.kb[st] = *(const u32x4*)(rb + 32 * st + 8 * kq);
+      }
     }
   };
 
@@ -791,7 +866,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
   // take turns (tile n + 2's loads go into tile n's set after its scores)
   constexpr int NB = NT > 0 ? NT : 2;
   Regs buf[NB];
-  issue(buf[0], t0);
+  if (live) issue(buf[0], t0);
   // query fragments: lane (head r, kq) of step st holds q[head][32 st + 8 kq .. + 7] (0 for
   // r >= G); they go through registers to LDS once and are read back per tile
   u32x4 qf[NST];
@@ -801,7 +876,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
     const uint16_t* q = (const uint16_t*)a.query.ptr;
 #pragma unroll
     for (int st = 0; st < NST; ++st) {
-      if (qvec) {
+      if (KSB > 0 && packed_rng) {
+        // q' = R q (fp32, written by the rotation launch) as fp16, dims QD kq + 8 st .. + 7
+        const float* qrow = a.query_rot + (b * a.q_heads + kvh * G + (r < G ? r : 0)) * D + QD * kq + 8 * st;
+        const float4 lo = *(const float4*)qrow, hi = *(const float4*)(qrow + 4);
+        qf[st] = u32x4{pack2_16<ANNA_MI_F16>(lo.x, lo.y), pack2_16<ANNA_MI_F16>(lo.z, lo.w),
+                       pack2_16<ANNA_MI_F16>(hi.x, hi.y), pack2_16<ANNA_MI_F16>(hi.z, hi.w)};
+      } else if (qvec) {
         qf[st] = *(const u32x4*)(q + qb + 32 * st + 8 * kq);
       } else {
 #pragma unroll
@@ -812,11 +893,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
       }
     }
   }
-  if constexpr (NT > 0) {
+  if (live) {
+    if constexpr (NT > 0) {
 #pragma unroll
-    for (int n = 1; n < NT; ++n) issue(buf[n], t0 + (int64_t)MF_TILE * n);
-  } else {
-    if (ntiles > 1) issue(buf[1], t0 + MF_TILE);
+      for (int n = 1; n < NT; ++n) issue(buf[n], t0 + (int64_t)MF_TILE * n);
+    } else {
+      if (ntiles > 1) issue(buf[1], t0 + MF_TILE);
+    }
   }
   // the first use of a loaded value (the padding heads' zeros included) stays below every load:
   // a use above them made the compiler wait for all loads issued so far before issuing the rest
@@ -832,7 +915,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
 
   auto process = [&](Regs& R, int n) {
     const int64_t tt0 = t0 + (int64_t)MF_TILE * n;
-    // ---- V of the tile into LDS, transposed
+    // ---- V of the tile into LDS, transposed.  With per-row lengths the slots past a row's length
+    // (stale memory, possibly not finite) stage as zeros: their probabilities are 0, but 0 * NaN
+    // would not be.
+    const bool keep0 = !SEQ || valid(tt0 + 2 * p), keep1 = !SEQ || valid(tt0 + 2 * p + 1);
     if (raw_tile(tt0)) {
       if constexpr (VF == ANNA_MI_VALUES_MINMAX) {
         constexpr uint32_t mask = (1u << SB) - 1u;
@@ -852,7 +938,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
           }
           const int d0 = QD * qr + 8 * c;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) vw[(d0 + e) * (MF_VT / 2) + p] = pack2_16<DT>(v[0][e], v[1][e]);
+          for (int e = 0; e < 8; ++e)
+            vw[(d0 + e) * (MF_VT / 2) + p] = pack2_16<DT>(keep0 ? v[0][e] : 0.f, keep1 ? v[1][e] : 0.f);
         }
       }
     } else {
@@ -870,7 +957,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
           row[u] = (tu[u] >= L1 ? rval0 + (tu[u] - L1) * rvs2 : (const uint16_t*)(vb0 + tu[u] * vbs2)) + QD * qr;
 #pragma unroll 2
         for (int c = 0; c < QD / 8; ++c) {
-          const u32x4 w0 = *(const u32x4*)(row[0] + 8 * c), w1 = *(const u32x4*)(row[1] + 8 * c);
+          u32x4 w0 = *(const u32x4*)(row[0] + 8 * c), w1 = *(const u32x4*)(row[1] + 8 * c);
+          if constexpr (SEQ) {
+            w0 = keep0 ? w0 : u32x4{0u, 0u, 0u, 0u};
+            w1 = keep1 ? w1 : u32x4{0u, 0u, 0u, 0u};
+          }
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int d = QD * qr + 8 * c + 2 * e;
@@ -910,25 +1001,51 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
             }
           }
 #pragma unroll
-          for (int e = 0; e < 8; ++e) vw[(d0 + e) * (MF_VT / 2) + p] = pack2_16<DT>(v[0][e], v[1][e]);
+          for (int e = 0; e < 8; ++e)
+            vw[(d0 + e) * (MF_VT / 2) + p] = pack2_16<DT>(keep0 ? v[0][e] : 0.f, keep1 ? v[1][e] : 0.f);
         }
       }
     }
     // ---- scores: st0 rows = tokens tt0 + 0..15, st1 rows = tt0 + 16..31; columns = heads
     f32x4 st0 = {0.f, 0.f, 0.f, 0.f}, st1 = st0;
+    float kscale[8];
+    if (KSB > 0 && packed_rng) {
+      // the codes of dims QD kq + 8 st .. + 7 through the table
+      auto frag = [&](const uint32_t (&kc)[KCW], int st) -> u32x4 {
+        if constexpr (KSB == 4) {
+          const uint32_t w = kc[st];
+          return u32x4{s_klut[w & 0xFFu], s_klut[(w >> 8) & 0xFFu], s_klut[(w >> 16) & 0xFFu], s_klut[w >> 24]};
+        } else {
+          const uint32_t w = kc[st >> 1] >> (16 * (st & 1));
+          const uint2 lo = ((const uint2*)s_klut)[w & 0xFFu], hi = ((const uint2*)s_klut)[(w >> 8) & 0xFFu];
+          return u32x4{lo.x, lo.y, hi.x, hi.y};
+        }
+      };
 #pragma unroll
-    for (int st = 0; st < NST; ++st) {
-      const u32x4 qs = s_qf[st][lane];
-      st0 = mfma16<DT>(R.ka[st], qs, st0);
-      st1 = mfma16<DT>(R.kb[st], qs, st1);
+      for (int st = 0; st < NST; ++st) {
+        const u32x4 qs = s_qf[st][lane];
+        st0 = mfma16<ANNA_MI_F16>(frag(R.kc[0], st), qs, st0);
+        st1 = mfma16<ANNA_MI_F16>(frag(R.kc[1], st), qs, st1);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) kscale[i] = f16_bits_to_f32((uint16_t)R.kn[i]) * scale2;
+    } else {
+#pragma unroll
+      for (int st = 0; st < NST; ++st) {
+        const u32x4 qs = s_qf[st][lane];
+        st0 = mfma16<DT>(R.ka[st], qs, st0);
+        st1 = mfma16<DT>(R.kb[st], qs, st1);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) kscale[i] = scale2;
     }
     // this buffer is free again: tile n + 2 goes in flight
     if (NT == 0 && n + 2 < ntiles) issue(R, tt0 + 2 * MF_TILE);
     float s[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      s[i] = tt0 + 4 * kq + i < t1 ? st0[i] * scale2 : -INFINITY;
-      s[4 + i] = tt0 + 16 + 4 * kq + i < t1 ? st1[i] * scale2 : -INFINITY;
+      s[i] = valid(tt0 + 4 * kq + i) ? st0[i] * kscale[i] : -INFINITY;
+      s[4 + i] = valid(tt0 + 16 + 4 * kq + i) ? st1[i] * kscale[4 + i] : -INFINITY;
     }
     float mx = s[0];
 #pragma unroll
@@ -952,8 +1069,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
     u32x4 pf;
 #pragma unroll
     for (int i = 0; i < 4; i += 2) {
-      const float p0 = __builtin_amdgcn_exp2f(s[i] - m_run), p1 = __builtin_amdgcn_exp2f(s[i + 1] - m_run);
-      const float p2 = __builtin_amdgcn_exp2f(s[4 + i] - m_run), p3 = __builtin_amdgcn_exp2f(s[5 + i] - m_run);
+      float p0 = __builtin_amdgcn_exp2f(s[i] - m_run), p1 = __builtin_amdgcn_exp2f(s[i + 1] - m_run);
+      float p2 = __builtin_amdgcn_exp2f(s[4 + i] - m_run), p3 = __builtin_amdgcn_exp2f(s[5 + i] - m_run);
+      if constexpr (SEQ) {  // a tile can be all masked while m_run is still -inf
+        p0 = s[i] == -INFINITY ? 0.f : p0;
+        p1 = s[i + 1] == -INFINITY ? 0.f : p1;
+        p2 = s[4 + i] == -INFINITY ? 0.f : p2;
+        p3 = s[5 + i] == -INFINITY ? 0.f : p3;
+      }
       l_run += (p0 + p1) + (p2 + p3);
       pf[i >> 1] = pack2_16<DT>(p0, p1);
       pf[2 + (i >> 1)] = pack2_16<DT>(p2, p3);
@@ -970,13 +1093,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the next tile's writes
   };
 
-  if constexpr (NT > 0) {
+  if (live) {
+    if constexpr (NT > 0) {
 #pragma unroll
-    for (int n = 0; n < NT; ++n) process(buf[n], n);
-  } else {
-    for (int n = 0; n < ntiles; n += 2) {
-      process(buf[0], n);
-      if (n + 1 < ntiles) process(buf[1], n + 1);
+      for (int n = 0; n < NT; ++n) process(buf[n], n);
+    } else {
+      for (int n = 0; n < ntiles; n += 2) {
+        process(buf[0], n);
+        if (n + 1 < ntiles) process(buf[1], n + 1);
+      }
     }
   }
 
@@ -990,6 +1115,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
     ((float*)ps.ptr)[base] = m_run * 0.6931471805599453f;  // back to natural-log units
     ((float*)ps.ptr)[base + ps.s3] = l_run;
   }
+  // a range with no valid token (per-row lengths) leaves its values unwritten: the merges weigh
+  // a block with denominator 0 by 0 and never read its values into a sum
+  if (!live) return;
   const anna_mi_view& pv = a.partial_values;
   float* out = (float*)pv.ptr + b * pv.s0 + blk * pv.s2 + r * pv.s3;
 #pragma unroll
@@ -1027,20 +1155,31 @@ int64_t total_blocks(const anna_mi_decode_args& a, const Split& sp) {
 }
 
 
-// The MFMA split kernel takes 16-bit activations, dense keys, dense or min/max values and
-// 16-byte aligned rows (the layouts of the reference's caches); anything else runs on the VALU
-// kernel.
+// The MFMA split kernel takes 16-bit activations, dense or TQ-MSE keys, dense or min/max values
+// and aligned rows (the layouts of the reference's caches and of TurboQuantRowsCache), with or
+// without per-row lengths; anything else runs on the VALU kernel.
 bool mfma_path_ok(const anna_mi_decode_args& a, const Split& sp) {
-  if (a.seq_lengths) return false;  // per-row lengths: the VALU kernel
-  if (a.dtype == ANNA_MI_F32 || a.key_format != ANNA_MI_KEYS_DENSE || sp.aligned) return false;
+  if (a.dtype == ANNA_MI_F32) return false;
   if (a.value_format != ANNA_MI_VALUES_DENSE && a.value_format != ANNA_MI_VALUES_MINMAX) return false;
   if (a.head_dim != 64 && a.head_dim != 128 && a.head_dim != 256) return false;
   if (a.q_heads / a.kv_heads > 16) return false;
+  const bool tqk = a.key_format == ANNA_MI_KEYS_TQ_MSE;
+  if (!tqk && (a.key_format != ANNA_MI_KEYS_DENSE || sp.aligned)) return false;
+  if (tqk && a.value_format != ANNA_MI_VALUES_MINMAX) return false;  // the forms instantiated
   auto rows16 = [](const anna_mi_view& v) {  // 8 x 16-bit elements per aligned 16-byte load
     return v.s3 == 1 && (uintptr_t)v.ptr % 16 == 0 && v.s0 % 8 == 0 && v.s1 % 8 == 0 && v.s2 % 8 == 0;
   };
-  if (a.len1 > 0) {
+  if (a.len1 > 0 && tqk) {
+    // code fields of 2 or 4 bits (3-bit codes take 4); the lane's D / 4 dims of a token in one
+    // aligned load of up to 16 bytes; the rotated query rows 16-byte aligned
+    if (a.key_bits < 2 || a.key_bits > 4 || !a.query_rot || !a.key_centroids || (uintptr_t)a.query_rot % 16) return false;
+    const int64_t ksb = a.key_bits == 2 ? 2 : 4, al = std::min<int64_t>(a.head_dim / 4 * ksb / 8, 16);
+    const anna_mi_view& k = a.key;
+    if (k.s3 != 1 || (uintptr_t)k.ptr % al || k.s0 % al || k.s1 % al || k.s2 % al) return false;
+  } else if (a.len1 > 0) {
     if (!rows16(a.key)) return false;
+  }
+  if (a.len1 > 0) {
     if (a.value_format == ANNA_MI_VALUES_DENSE) {
       if (!rows16(a.value)) return false;
     } else {
@@ -1055,29 +1194,43 @@ bool mfma_path_ok(const anna_mi_decode_args& a, const Split& sp) {
 }
 
 // Tokens per wave of the MFMA split kernel: whole tiles, about MF_WAVES_TARGET waves over all
-// (batch, KV head) rows, and no more ranges per row than the caller's workspace holds.
+// (batch, KV head) rows, and no more ranges per row than the caller's workspace holds.  With
+// TQ-MSE keys the ranges are aligned to the segments (mfma_ranges counts both).
+int64_t mfma_ranges(const anna_mi_decode_args& a, int64_t range, int64_t* nr1) {
+  const bool aligned = a.key_format == ANNA_MI_KEYS_TQ_MSE;
+  const int64_t L = a.len1 + a.len2;
+  *nr1 = aligned ? (a.len1 + range - 1) / range : 0;
+  return aligned ? *nr1 + (a.len2 + range - 1) / range : (L + range - 1) / range;
+}
+
 int64_t mfma_range(const anna_mi_decode_args& a) {
   const int64_t L = a.len1 + a.len2;
   const int64_t tiles = a.batch * a.kv_heads * ((L + MF_TILE - 1) / MF_TILE);
   int64_t range = (tiles + MF_WAVES_TARGET - 1) / MF_WAVES_TARGET * MF_TILE;
-  const int64_t need = (L + a.partial_capacity - 1) / a.partial_capacity;
-  if (range < need) range = (need + MF_TILE - 1) / MF_TILE * MF_TILE;
+  if (range < MF_TILE) range = MF_TILE;
+  int64_t nr1 = 0;
+  while (mfma_ranges(a, range, &nr1) > a.partial_capacity && range < L) range += MF_TILE;
   return range;
 }
 
-void launch_split_mfma(const anna_mi_decode_args& a, int64_t range, int64_t nranges, hipStream_t st) {
+void launch_split_mfma(const anna_mi_decode_args& a, int64_t range, int64_t nranges, int64_t nr1, hipStream_t st) {
   const dim3 grid((unsigned)nranges, (unsigned)a.kv_heads, (unsigned)a.batch), blk(64);
   const int64_t nt = range / MF_TILE;
-  auto go = [&](auto dt_tag, auto vf_tag, auto sb_tag) {
+  const bool seq = a.seq_lengths != nullptr, tqk = a.key_format == ANNA_MI_KEYS_TQ_MSE;
+  auto go = [&](auto dt_tag, auto vf_tag, auto sb_tag, auto ksb_tag, auto seq_tag) {
     constexpr int DT = decltype(dt_tag)::value, VF = decltype(vf_tag)::value, SB = decltype(sb_tag)::value;
+    constexpr int KSB = decltype(ksb_tag)::value;
+    constexpr bool SEQ = decltype(seq_tag)::value;
     auto by_nt = [&](auto d_tag) {
       constexpr int D = decltype(d_tag)::value;
-      switch (nt) {
-        case 1: hipLaunchKernelGGL((decode_split_mfma_kernel<DT, VF, SB, D, 1>), grid, blk, 0, st, a, range); break;
-        case 2: hipLaunchKernelGGL((decode_split_mfma_kernel<DT, VF, SB, D, 2>), grid, blk, 0, st, a, range); break;
-        case 3: hipLaunchKernelGGL((decode_split_mfma_kernel<DT, VF, SB, D, 3>), grid, blk, 0, st, a, range); break;
-        case 4: hipLaunchKernelGGL((decode_split_mfma_kernel<DT, VF, SB, D, 4>), grid, blk, 0, st, a, range); break;
-        default: hipLaunchKernelGGL((decode_split_mfma_kernel<DT, VF, SB, D, 0>), grid, blk, 0, st, a, range); break;
+      // per-row lengths or TQ-MSE keys: the runtime tile loop only (fewer instantiations)
+      const int64_t n = KSB > 0 || SEQ ? 0 : nt;
+      switch (n) {
+        case 1: hipLaunchKernelGGL((decode_split_mfma_kernel<DT, VF, SB, D, 1, 0, false>), grid, blk, 0, st, a, range, nr1); break;
+        case 2: hipLaunchKernelGGL((decode_split_mfma_kernel<DT, VF, SB, D, 2, 0, false>), grid, blk, 0, st, a, range, nr1); break;
+        case 3: hipLaunchKernelGGL((decode_split_mfma_kernel<DT, VF, SB, D, 3, 0, false>), grid, blk, 0, st, a, range, nr1); break;
+        case 4: hipLaunchKernelGGL((decode_split_mfma_kernel<DT, VF, SB, D, 4, 0, false>), grid, blk, 0, st, a, range, nr1); break;
+        default: hipLaunchKernelGGL((decode_split_mfma_kernel<DT, VF, SB, D, 0, KSB, SEQ>), grid, blk, 0, st, a, range, nr1); break;
       }
     };
     switch (a.head_dim) {
@@ -1093,15 +1246,26 @@ void launch_split_mfma(const anna_mi_decode_args& a, int64_t range, int64_t nran
   using HF = std::integral_constant<int, ANNA_MI_F16>;
   using VD = std::integral_constant<int, ANNA_MI_VALUES_DENSE>;
   using VM = std::integral_constant<int, ANNA_MI_VALUES_MINMAX>;
+  using Y = std::integral_constant<bool, true>;
+  using N = std::integral_constant<bool, false>;
   const bool dense = a.value_format == ANNA_MI_VALUES_DENSE, two = a.value_bits == 2;
+  auto go_k = [&](auto dt, auto vf, auto sb) {
+    if (!tqk) {
+      seq ? go(dt, vf, sb, S0{}, Y{}) : go(dt, vf, sb, S0{}, N{});
+    } else if constexpr (decltype(vf)::value == ANNA_MI_VALUES_MINMAX) {
+      // TQ-MSE keys come with min/max values (TurboQuantRowsCache, the row API)
+      if (a.key_bits == 2) seq ? go(dt, vf, sb, S2{}, Y{}) : go(dt, vf, sb, S2{}, N{});
+      else seq ? go(dt, vf, sb, S4{}, Y{}) : go(dt, vf, sb, S4{}, N{});
+    }
+  };
   if (a.dtype == ANNA_MI_BF16) {
-    if (dense) go(BF{}, VD{}, S0{});
-    else if (two) go(BF{}, VM{}, S2{});
-    else go(BF{}, VM{}, S4{});
+    if (dense) go_k(BF{}, VD{}, S0{});
+    else if (two) go_k(BF{}, VM{}, S2{});
+    else go_k(BF{}, VM{}, S4{});
   } else {
-    if (dense) go(HF{}, VD{}, S0{});
-    else if (two) go(HF{}, VM{}, S2{});
-    else go(HF{}, VM{}, S4{});
+    if (dense) go_k(HF{}, VD{}, S0{});
+    else if (two) go_k(HF{}, VM{}, S2{});
+    else go_k(HF{}, VM{}, S4{});
   }
 }
 
@@ -1205,10 +1369,14 @@ static int gqa_decode_splitkv_impl(const anna_mi_decode_args& a, void* stream) {
   }
   const bool kq = a.key_format == ANNA_MI_KEYS_TQ_MSE;
   int64_t nmerge = nblk;  // partials written by the split kernel
+  int64_t mf_range = 0, mf_nr1 = 0, mf_n = 0;
   if (mfma_path_ok(a, sp)) {
-    const int64_t range = mfma_range(a), L = a.len1 + a.len2;
-    nmerge = (L + range - 1) / range;
-    launch_split_mfma(a, range, nmerge, st);
+    mf_range = mfma_range(a);
+    mf_n = mfma_ranges(a, mf_range, &mf_nr1);
+  }
+  if (mf_n > 0 && mf_n <= a.partial_capacity) {  // (two aligned segments take two ranges at least)
+    nmerge = mf_n;
+    launch_split_mfma(a, mf_range, nmerge, mf_nr1, st);
   } else switch (a.value_format) {
     case ANNA_MI_VALUES_DENSE:
       kq ? launch_split<1, 0>(a, sp, nblk, st) : launch_split<0, 0>(a, sp, nblk, st);

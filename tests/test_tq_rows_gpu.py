@@ -111,6 +111,38 @@ def test_rows_cache_load_append_decode(gpu, d, bits, gated, hkv, g):
     assert int(cache.overflow.item()) == 0
 
 
+@pytest.mark.parametrize("d,bits", [(64, 2), (128, 4), (256, 3)])
+def test_rows_cache_slots_past_the_lengths_are_never_read_into_the_output(gpu, d, bits):
+    """Slots past each row's length hold whatever the memory held before (here NaN in the value
+    scales and zeros, the key norms and the window rows past the ring's fill): the decode must
+    not let them into the output (a zero probability times NaN is NaN)."""
+    print(f"[case] tq rows stale slots d={d} bits={bits}", flush=True)
+    torch.manual_seed(700 + d + bits)
+    hkv, g, R = 2, 8, 32
+    lens = [300, 70, 9]
+    cache = TurboQuantBatchCache(batch=3, kv_heads=hkv, q_heads=hkv * g, capacities=[400, 400, 400],
+                                 residual_capacity=R, head_dim=d, bits=bits, device=gpu)
+    assert isinstance(cache, TurboQuantRowsCache)
+    keys = [torch.randn(hkv, L, d, device=gpu).to(torch.bfloat16) for L in lens]
+    vals = [torch.randn(hkv, L, d, device=gpu).to(torch.bfloat16) for L in lens]
+    for b in range(3):
+        cache.load_sequence(b, keys[b], vals[b])
+    nan = float("nan")
+    for b, L in enumerate(lens):
+        ql = max(0, L - R)
+        cache.value_scales[b, :, ql:] = nan
+        cache.value_zeros[b, :, ql:] = nan
+        cache.key_norms[b, :, ql:] = nan
+        cache.value_data[b, :, ql:] = 0xFF
+        if L < R:
+            cache.residual_value[b, :, L:] = nan
+            cache.residual_key[b, :, L:] = nan
+    q = torch.randn(3, hkv * g, d, device=gpu).to(torch.bfloat16)
+    out = cache.decode(q, scaling=d ** -0.5)
+    assert torch.isfinite(out.float()).all()
+    check_rows(cache, keys, vals, q, out)
+
+
 def test_rows_cache_full_sequence_refused(gpu):
     print("[case] tq rows full sequence", flush=True)
     cache = TurboQuantBatchCache(batch=1, kv_heads=1, q_heads=2, capacities=[2], residual_capacity=4, head_dim=128,
