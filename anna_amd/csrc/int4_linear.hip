@@ -232,9 +232,10 @@ __global__ __launch_bounds__(64 * KW) void int4_gemv_mfma(
 //
 // Streaming kernel for the bandwidth-critical M = 1..2 case.  A load instruction covers
 // 64/LPR rows x (LPR x 16 B) contiguous bytes of each (whole 128 B lines).  Wave w of a
-// workgroup owns the k-slice [w*LPR*32, (w+1)*LPR*32) of RW rows; a lane keeps its 32 x
+// workgroup owns the k-slice [w*LPR*32, (w+1)*LPR*32) of RW = 4 RG rows; a lane keeps its 32 x
 // values in registers (loaded first, so they never wait behind weights) and walks RG row
-// groups whose loads are all issued up front.  Per 8 nibbles: 7 ALU ops build the bf16
+// groups whose loads are all issued up front (RG = 4, or 2 where four would leave fewer than
+// three workgroups per compute unit).  Per 8 nibbles: 7 ALU ops build the bf16
 // pairs (128+q_i, 128+q_{i+4}) and 4 v_dot2c_f32_bf16 accumulate; per 32 k the zero point
 // and scale are applied as s * (acc - (128 + z) * sum(x)).  Lanes of a row and the waves of
 // the workgroup are reduced at the end.
@@ -264,18 +265,17 @@ __device__ __forceinline__ float dpp_f32(float v) {
 }
 
 // Lane (sub, c) of a wave: c = lane % 16 owns k [k0 + 32 c, k0 + 32 c + 32) of the wave's
-// 512-k slice, sub = lane / 16 the rows n0 + 4 sub + g of its four row groups g.  One load
-// instruction (fixed g) covers 4 rows x 256 contiguous bytes; a lane's 4 rows are consecutive,
-// so its 4 scales and 4 zero points are one 8- (16-bit scales) or 16-byte (fp32) load and one
-// 4-byte load.  Every load of a slice is issued before any value is converted: a conversion
+// 512-k slice, sub = lane / 16 the rows n0 + RG sub + g of its RG (1, 2 or 4) row groups g.  One
+// load instruction (fixed g) covers 4 rows x 256 contiguous bytes; a lane's RG rows are
+// consecutive, so its scales and zero points are one load each (RG x 2 or 4 bytes, RG bytes).  Every load of a slice is issued before any value is converted: a conversion
 // placed right after its load made the compiler wait for that load before issuing the next.
-template <int XDT, int SDT, int MR, int WMAX, bool VEC_SZ>
+template <int XDT, int SDT, int MR, int WMAX, bool VEC_SZ, int RG>
 __global__ __launch_bounds__(64 * WMAX) void int4_gemv_dot2(
     const uint16_t* __restrict__ x, int64_t M, int64_t K, int64_t xs,
     const uint32_t* __restrict__ qw, int64_t N, int64_t pc,
     const typename Elem<SDT>::T* __restrict__ qs, const int8_t* __restrict__ qz,
     int gshift, uint16_t* __restrict__ y) {
-  constexpr int RG = 4;         // row groups (loads of W) per lane and slice
+  static_assert(RG == 1 || RG == 2 || RG == 4, "row groups (loads of W) per lane and slice");
   constexpr int RW = 4 * RG;    // rows per workgroup
   constexpr int KSL = 512;      // k per wave slice
   constexpr float OFF = XDT == ANNA_MI_BF16 ? 128.0f : 1024.0f;
@@ -318,17 +318,24 @@ __global__ __launch_bounds__(64 * WMAX) void int4_gemv_dot2(
     }
     // scales and zero points (small, ahead of the weights they scale), kept raw
     const int64_t grp = k_ok ? kl >> gshift : 0;
-    const uint32_t so = k_ok ? (uint32_t)(grp * N + n0 + 4 * sub) : OOB / 4;
+    const uint32_t so = k_ok ? (uint32_t)(grp * N + n0 + RG * sub) : OOB / 4;
     u32x4 svec = {0u, 0u, 0u, 0u};
     uint32_t zvec = 0, sg[RG], zg[RG];
     if constexpr (VEC_SZ) {
-      if constexpr (SDT == ANNA_MI_F32) {
-        svec = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, so * 4, 0, 0));
-      } else {
-        const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, so * 2, 0, 0));
+      // RG consecutive scales (RG * 2 or RG * 4 bytes) and zero points (RG bytes)
+      if constexpr (RG * SB == 16) {
+        svec = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, so * SB, 0, 0));
+      } else if constexpr (RG * SB == 8) {
+        const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, so * SB, 0, 0));
         svec.x = v.x, svec.y = v.y;
+      } else if constexpr (RG * SB == 4) {
+        svec.x = __builtin_amdgcn_raw_buffer_load_b32(rs, so * SB, 0, 0);
+      } else {
+        svec.x = __builtin_amdgcn_raw_buffer_load_b16(rs, so * SB, 0, 0);
       }
-      zvec = __builtin_amdgcn_raw_buffer_load_b32(rz, so, 0, 0);
+      if constexpr (RG == 4) zvec = __builtin_amdgcn_raw_buffer_load_b32(rz, so, 0, 0);
+      else if constexpr (RG == 2) zvec = __builtin_amdgcn_raw_buffer_load_b16(rz, so, 0, 0);
+      else zvec = __builtin_amdgcn_raw_buffer_load_b8(rz, so, 0, 0);
     } else {
 #pragma unroll
       for (int g = 0; g < RG; ++g) {
@@ -338,7 +345,7 @@ __global__ __launch_bounds__(64 * WMAX) void int4_gemv_dot2(
       }
     }
     u32x4 wv[RG];
-    const uint32_t wo = k_ok ? (uint32_t)((4 * sub * pc + (kl >> 3)) * 4) : OOB;
+    const uint32_t wo = k_ok ? (uint32_t)((RG * sub * pc + (kl >> 3)) * 4) : OOB;
 #pragma unroll
     for (int g = 0; g < RG; ++g)
       wv[g] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
@@ -361,10 +368,10 @@ __global__ __launch_bounds__(64 * WMAX) void int4_gemv_dot2(
     uint32_t sraw[RG];
     uint32_t zraw = 0;
     if constexpr (VEC_SZ) {
-      if constexpr (SDT == ANNA_MI_F32) {
-        sraw[0] = svec.x, sraw[1] = svec.y, sraw[2] = svec.z, sraw[3] = svec.w;
-      } else {
-        sraw[0] = svec.x, sraw[1] = svec.x >> 16, sraw[2] = svec.y, sraw[3] = svec.y >> 16;
+#pragma unroll
+      for (int g = 0; g < RG; ++g) {
+        if constexpr (SDT == ANNA_MI_F32) sraw[g] = svec[g];
+        else sraw[g] = svec[g >> 1] >> (16 * (g & 1));
       }
       zraw = zvec;
     } else {
@@ -432,31 +439,41 @@ __global__ __launch_bounds__(64 * WMAX) void int4_gemv_dot2(
   float red_v[MR];
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
-    float v[RG];
+    float v[4];
 #pragma unroll
-    for (int g = 0; g < RG; ++g) v[g] = yacc[m][g];
-    {
+    for (int g = 0; g < 4; ++g) v[g] = g < RG ? yacc[m][g] : 0.f;
+    // with fewer row groups the first stages add the whole list instead of halving it
+    if constexpr (RG == 4) {
       const bool up = (c >> 3) & 1;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const float mine = up ? v[i + 2] : v[i], give = up ? v[i] : v[i + 2];
         v[i] = mine + dpp_f32<0x140>(give);  // row_mirror
       }
+    } else if constexpr (RG == 2) {
+      const bool up = (c >> 3) & 1;
+      const float mine = up ? v[1] : v[0], give = up ? v[0] : v[1];
+      v[0] = mine + dpp_f32<0x140>(give);  // row_mirror
+    } else {
+      v[0] += dpp_f32<0x140>(v[0]);
     }
-    {
+    if constexpr (RG == 4) {
       const bool up = (c >> 2) & 1;
       const float mine = up ? v[1] : v[0], give = up ? v[0] : v[1];
       v[0] = mine + dpp_f32<0x141>(give);  // row_half_mirror
+    } else {
+      v[0] += dpp_f32<0x141>(v[0]);
     }
     v[0] += dpp_f32<0x4E>(v[0]);  // quad_perm [2, 3, 0, 1]
     v[0] += dpp_f32<0xB1>(v[0]);  // quad_perm [1, 0, 3, 2]
     red_v[m] = v[0];
   }
-  const int gsel = ((c >> 3) & 1) * 2 + ((c >> 2) & 1);
+  // the row group lane c holds: bits 3 and 2 of c for four groups, bit 3 for two
+  const int gsel = RG == 4 ? ((c >> 3) & 1) * 2 + ((c >> 2) & 1) : RG == 2 ? (c >> 3) & 1 : 0;
   __shared__ float red[WMAX][MR][RW];
-  if ((c & 3) == 0) {
+  if ((c & (RG == 4 ? 3 : RG == 2 ? 7 : 15)) == 0) {
 #pragma unroll
-    for (int m = 0; m < MR; ++m) red[wave][m][4 * sub + gsel] = red_v[m];
+    for (int m = 0; m < MR; ++m) red[wave][m][RG * sub + gsel] = red_v[m];
   }
   __syncthreads();
   for (int i = threadIdx.x; i < MR * RW; i += blockDim.x) {
@@ -808,13 +825,27 @@ extern "C" int anna_mi_int4_linear(const void* x, int x_dtype, int64_t M, int64_
                              (uint16_t*)y);
         };
         const bool vec = (N & 3) == 0;
-        if (waves <= 8) {
-          if (vec) launch(int4_gemv_dot2<XDT, SDT, MR, 8, true>);
-          else launch(int4_gemv_dot2<XDT, SDT, MR, 8, false>);
-        } else {
-          if (vec) launch(int4_gemv_dot2<XDT, SDT, MR, DOT2_MAX_WAVES, true>);
-          else launch(int4_gemv_dot2<XDT, SDT, MR, DOT2_MAX_WAVES, false>);
-        }
+        // four row groups per lane while that still gives three workgroups per compute unit, else
+        // two (twice the waves, half the chain per wave): M = 1, N = 6144, K = 2048 3.93 -> 3.72 us,
+        // K = 4096 5.25 -> 5.03 us; N = 12288 stays at four (6.8 against 7.8 us with two).
+        // ANNA_MI_INT4_DOT2_RG = 1 / 2 / 4 forces a count (read on every call, for the tests).
+        int rg = (N + 15) / 16 >= 768 ? 4 : 2;
+        if (const char* f = getenv("ANNA_MI_INT4_DOT2_RG"); f && (f[0] == '1' || f[0] == '2' || f[0] == '4'))
+          rg = f[0] - '0';
+        auto go_rg = [&](auto rg_tag) {
+          constexpr int RG = decltype(rg_tag)::value;
+          grid = dim3((unsigned)((N + 4 * RG - 1) / (4 * RG)));
+          if (waves <= 8) {
+            if (vec) launch(int4_gemv_dot2<XDT, SDT, MR, 8, true, RG>);
+            else launch(int4_gemv_dot2<XDT, SDT, MR, 8, false, RG>);
+          } else {
+            if (vec) launch(int4_gemv_dot2<XDT, SDT, MR, DOT2_MAX_WAVES, true, RG>);
+            else launch(int4_gemv_dot2<XDT, SDT, MR, DOT2_MAX_WAVES, false, RG>);
+          }
+        };
+        if (rg == 1) go_rg(std::integral_constant<int, 1>{});
+        else if (rg == 2) go_rg(std::integral_constant<int, 2>{});
+        else go_rg(std::integral_constant<int, 4>{});
       };
       using I1 = std::integral_constant<int, 1>;
       using I2 = std::integral_constant<int, 2>;

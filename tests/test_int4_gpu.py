@@ -70,6 +70,24 @@ def test_int4_linear_matches_oracle(gpu, m, k, n, group, sdt):
     assert rel_err(y.float().cpu().numpy(), ref) <= BF16_TOL
 
 
+@pytest.mark.parametrize("rg", ["1", "2", "4"])
+@pytest.mark.parametrize("m,k,n,sdt", [(1, 4096, 1000, "bf16"), (2, 2048, 998, "fp32"), (1, 8192, 300, "f16"),
+                                       (2, 512, 36, "bf16")])
+def test_int4_gemv_dot2_row_groups(gpu, monkeypatch, rg, m, k, n, sdt):
+    """The M <= 2 GEMV with 1, 2 or 4 row groups per lane (N tails, N % 4 != 0, two passes at K = 8192)."""
+    print(f"[case] int4 dot2 RG={rg} M={m} K={k} N={n} scale={sdt}", flush=True)
+    monkeypatch.setenv("ANNA_MI_INT4_DOT2_RG", rg)
+    rng = np.random.default_rng(m * 7 + k + n)
+    qw, qs, qz = int4_payload(rng, n, k, 128, scale_dtype="fp32" if sdt == "fp32" else "bf16")
+    xb = orc.bf16_bits(rng.normal(size=(m, k)).astype(np.float32))
+    ref = orc.int4_linear(xb, qw, qs, qz, 128)
+    sd = {"bf16": torch.bfloat16, "fp32": torch.float32, "f16": torch.float16}[sdt]
+    qs_t = _dev(qs, gpu).to(sd)
+    x = _x_tensor(xb, torch.bfloat16, gpu)
+    y = torch.ops.anna.xpu_int4_gemv(x, _dev(qw, gpu), qs_t, _dev(qz, gpu), 128, k)
+    assert rel_err(y.float().cpu().numpy(), ref) <= BF16_TOL
+
+
 @pytest.mark.parametrize("tile", ["L", "M", "S"])
 @pytest.mark.parametrize("m,k,n,group,sdt", [(300, 512, 400, 64, "bf16"), (2048, 1024, 200, 128, "fp32"),
                                              (64, 1024, 96, 128, "bf16"), (257, 256, 1000, 128, "bf16"),
