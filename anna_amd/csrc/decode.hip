@@ -743,7 +743,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
     n2 = n < a.len2 ? n : a.len2;
     n1 = n - n2 < L1 ? n - n2 : L1;
   }
-  auto valid = [&](int64_t t) { return t < t1 && (!SEQ || t < n1 || (t >= L1 && t < L1 + n2)); };
+  // TQ-MSE keys: the ranges are aligned to the segments, so a token of the range is valid below
+  // one limit (32-bit compares: the host keeps token indices below 2^31)
+  const int vlim = (int)(packed_rng ? (t1 < n1 ? t1 : n1) : (t1 < L1 + n2 ? t1 : L1 + n2));
+  auto valid = [&](int64_t t) {
+    if constexpr (KSB > 0) return (int)t < vlim;
+    else return t < t1 && (!SEQ || t < n1 || (t >= L1 && t < L1 + n2));
+  };
   const bool live = !SEQ || t0 < n1 || (t1 > L1 && t0 < L1 + n2);
   const int ntiles = NT > 0 ? NT : (int)((t1 - t0 + MF_TILE - 1) / MF_TILE);
   // raw-code staging: scale groups of whole 32-dim spans, code vectors aligned for one load
@@ -767,6 +773,34 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
   // a 16-byte aligned row that is always there (the host checks the key rows' alignment when
   // there is a packed segment, the window's otherwise): the target of loads that feed nothing
   const uint16_t* const safe16 = L1 > 0 ? key0 : rkey0;
+  // TQ-MSE packed ranges with raw values: per-lane 32-bit byte offsets (from the uniform row
+  // bases) of what tile 0 loads; tile n adds n tiles of stride, and the clamp into the range is a
+  // min on the offset (offsets grow with the token).  The host keeps each (batch, KV head) slice
+  // of these arrays below 2^31 bytes.
+  const bool tqfast = KSB > 0 && packed_rng;  // (the host sends TQ-MSE keys only with raw-ready values)
+  const uint8_t* const sb0 = (const uint8_t*)a.value_scales.ptr + 2 * (b * a.value_scales.s0 + kvh * a.value_scales.s1);
+  const uint8_t* const zb0 = (const uint8_t*)a.value_zeros.ptr + 2 * (b * a.value_zeros.s0 + kvh * a.value_zeros.s1);
+  const uint8_t* const kcb0 = (const uint8_t*)a.key.ptr + b * a.key.s0 + kvh * a.key.s1;
+  uint32_t o_v0 = 0, o_v1 = 0, o_s0 = 0, o_s1 = 0, o_z0 = 0, o_z1 = 0, o_ka = 0, o_kb = 0, lim_v = 0, lim_k = 0;
+  const uint32_t inc_v = (uint32_t)(MF_TILE * vbs2), inc_s = (uint32_t)(2 * MF_TILE * a.value_scales.s2),
+                 inc_z = (uint32_t)(2 * MF_TILE * a.value_zeros.s2), inc_k = (uint32_t)(MF_TILE * a.key.s2);
+  const uint32_t lim_s = (uint32_t)(2 * (t1 - 1) * a.value_scales.s2), lim_z = (uint32_t)(2 * (t1 - 1) * a.value_zeros.s2);
+  if (tqfast) {
+    const uint32_t cv = (uint32_t)(QD * qr * SB / 8), ck = (uint32_t)(QD * kq * KSB / 8);
+    const int64_t t = t0 + 2 * p;
+    o_v0 = (uint32_t)(t * vbs2) + cv;
+    o_v1 = o_v0 + (uint32_t)vbs2;
+    o_s0 = (uint32_t)(2 * t * a.value_scales.s2);
+    o_s1 = o_s0 + (uint32_t)(2 * a.value_scales.s2);
+    o_z0 = (uint32_t)(2 * t * a.value_zeros.s2);
+    o_z1 = o_z0 + (uint32_t)(2 * a.value_zeros.s2);
+    lim_v = (uint32_t)((t1 - 1) * vbs2) + cv;
+    o_ka = (uint32_t)((t0 + r) * a.key.s2) + ck;
+    o_kb = (uint32_t)((t0 + 16 + r) * a.key.s2) + ck;
+    lim_k = (uint32_t)((t1 - 1) * a.key.s2) + ck;
+  }
+  // byte offset of the lane's scale / zero group of span i (32 dims)
+  auto gofs = [&](int i, int64_t s3) { return (uint32_t)(2 * ((QD * qr + 32 * i) / a.value_group_size) * s3); };
 
   __shared__ __attribute__((aligned(16))) uint16_t s_vt[D * MF_VT];
   __shared__ u32x4 s_qf[NST][64];
@@ -792,8 +826,29 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
   // the raw path takes tiles whose tokens are all packed (min/max); others are staged by the
   // chunked loop below
   auto raw_tile = [&](int64_t tt0) { return rawok && (tt0 + MF_TILE <= L1 || t1 <= L1); };
-  auto issue = [&](Regs& R, int64_t tt0) {
-    if constexpr (VF == ANNA_MI_VALUES_MINMAX) {
+  auto issue = [&](Regs& R, int n) {
+    const int64_t tt0 = t0 + (int64_t)MF_TILE * n;
+    if constexpr (KSB > 0) {
+      // packed ranges: codes, scales and zeros of the lane's two staging tokens, the key codes of
+      // tokens r and 16 + r, one add and one min per address (window ranges: dense keys below,
+      // no value codes)
+      const uint32_t nn = packed_rng ? (uint32_t)n : 0u;
+      if (packed_rng) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const uint32_t tv = min((u ? o_v1 : o_v0) + nn * inc_v, lim_v);
+        load_words<CW>(R.vc[u], vb0 + tv);
+        const uint32_t ts = min((u ? o_s1 : o_s0) + nn * inc_s, lim_s), tz = min((u ? o_z1 : o_z0) + nn * inc_z, lim_z);
+#pragma unroll
+        for (int i = 0; i < NSP; ++i) {
+          R.vsc[i][u] = *(const uint16_t*)(sb0 + ts + gofs(i, a.value_scales.s3));
+          R.vzr[i][u] = *(const uint16_t*)(zb0 + tz + gofs(i, a.value_zeros.s3));
+        }
+      }
+      load_words<KCW>(R.kc[0], kcb0 + min(o_ka + nn * inc_k, lim_k));
+      load_words<KCW>(R.kc[1], kcb0 + min(o_kb + nn * inc_k, lim_k));
+      }
+    } else if constexpr (VF == ANNA_MI_VALUES_MINMAX) {
       // tokens clamped into the range and the packed segment; a tile that is not staged from
       // these registers still loads them (from the first packed token, or from safe16 when
       // there is none or the codes are not aligned) when NT is fixed, so the load count never
@@ -828,11 +883,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
     // key rows of tokens tt0 + r and tt0 + 16 + r (clamped into the range; masked below)
     const int64_t ta = tt0 + r < t1 ? tt0 + r : t1 - 1, tb = tt0 + 16 + r < t1 ? tt0 + 16 + r : t1 - 1;
     if (KSB > 0 && packed_rng) {
-      // the lane's key code words of both tokens, and the norms of its score rows (tokens
+      // (the key code words are loaded above) the norms of the lane's score rows (tokens
       // 4 kq + i, 16 + 4 kq + i, clamped into the range: the last tile may pass the segment)
-      const uint8_t* kc0 = (const uint8_t*)a.key.ptr + b * a.key.s0 + kvh * a.key.s1 + QD * kq * KSB / 8;
-      load_words<KCW>(R.kc[0], kc0 + ta * a.key.s2);
-      load_words<KCW>(R.kc[1], kc0 + tb * a.key.s2);
       const uint16_t* kn0 = (const uint16_t*)a.key_norms.ptr + b * a.key_norms.s0 + kvh * a.key_norms.s1;
       if (tt0 + MF_TILE <= t1 && a.key_norms.s2 == 1 && (uintptr_t)kn0 % 8 == 0) {
         // a whole tile of contiguous norms: the lane's two runs of four as two 8-byte loads
@@ -866,7 +918,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
   // take turns (tile n + 2's loads go into tile n's set after its scores)
   constexpr int NB = NT > 0 ? NT : 2;
   Regs buf[NB];
-  if (live) issue(buf[0], t0);
+  if (live) issue(buf[0], 0);
   // query fragments: lane (head r, kq) of step st holds q[head][32 st + 8 kq .. + 7] (0 for
   // r >= G); they go through registers to LDS once and are read back per tile
   u32x4 qf[NST];
@@ -896,9 +948,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
   if (live) {
     if constexpr (NT > 0) {
 #pragma unroll
-      for (int n = 1; n < NT; ++n) issue(buf[n], t0 + (int64_t)MF_TILE * n);
+      for (int n = 1; n < NT; ++n) issue(buf[n], n);
     } else {
-      if (ntiles > 1) issue(buf[1], t0 + MF_TILE);
+      if (ntiles > 1) issue(buf[1], 1);
     }
   }
   // the first use of a loaded value (the padding heads' zeros included) stays below every load:
@@ -929,17 +981,34 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
             const uint16_t sh = (uint16_t)R.vsc[i][u], zh = (uint16_t)R.vzr[i][u];
-            const float sc = DT == ANNA_MI_BF16 ? bf16_bits_to_f32(sh) : f16_bits_to_f32(sh);
-            const float zc = DT == ANNA_MI_BF16 ? bf16_bits_to_f32(zh) : f16_bits_to_f32(zh);
-            // codes of dims 8c .. 8c + 7 of the lane's quarter: 8 SB bits from bit 8 SB c
-            const uint32_t w = R.vc[u][(8 * SB * c) / 32] >> ((8 * SB * c) % 32);
+            float sc = DT == ANNA_MI_BF16 ? bf16_bits_to_f32(sh) : f16_bits_to_f32(sh);
+            float zc = DT == ANNA_MI_BF16 ? bf16_bits_to_f32(zh) : f16_bits_to_f32(zh);
+            if constexpr (SEQ) {
+              // a slot past the row's length stages as q * 0 + 0 = 0 (its scale and zero may be
+              // stale, not finite; the codes are small integers)
+              const bool k = u ? keep1 : keep0;
+              sc = k ? sc : 0.f;
+              zc = k ? zc : 0.f;
+            }
+            if constexpr (SB == 4) {
+              // one word holds the 8 codes: split into the even and odd codes' bytes, each then
+              // one byte-to-float conversion
+              const uint32_t w = R.vc[u][c], lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) v[u][e] = (float)((w >> (SB * e)) & mask) * sc + zc;
+              for (int e = 0; e < 4; ++e) {
+                v[u][2 * e] = (float)((lo >> (8 * e)) & 0xFFu) * sc + zc;
+                v[u][2 * e + 1] = (float)((hi >> (8 * e)) & 0xFFu) * sc + zc;
+              }
+            } else {
+              // codes of dims 8c .. 8c + 7 of the lane's quarter: 8 SB bits from bit 8 SB c
+              const uint32_t w = R.vc[u][(8 * SB * c) / 32] >> ((8 * SB * c) % 32);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) v[u][e] = (float)((w >> (SB * e)) & mask) * sc + zc;
+            }
           }
           const int d0 = QD * qr + 8 * c;
 #pragma unroll
-          for (int e = 0; e < 8; ++e)
-            vw[(d0 + e) * (MF_VT / 2) + p] = pack2_16<DT>(keep0 ? v[0][e] : 0.f, keep1 ? v[1][e] : 0.f);
+          for (int e = 0; e < 8; ++e) vw[(d0 + e) * (MF_VT / 2) + p] = pack2_16<DT>(v[0][e], v[1][e]);
         }
       }
     } else {
@@ -1040,7 +1109,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
       for (int i = 0; i < 8; ++i) kscale[i] = scale2;
     }
     // this buffer is free again: tile n + 2 goes in flight
-    if (NT == 0 && n + 2 < ntiles) issue(R, tt0 + 2 * MF_TILE);
+    if (NT == 0 && n + 2 < ntiles) issue(R, n + 2);
     float s[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -1176,6 +1245,21 @@ bool mfma_path_ok(const anna_mi_decode_args& a, const Split& sp) {
     const int64_t ksb = a.key_bits == 2 ? 2 : 4, al = std::min<int64_t>(a.head_dim / 4 * ksb / 8, 16);
     const anna_mi_view& k = a.key;
     if (k.s3 != 1 || (uintptr_t)k.ptr % al || k.s0 % al || k.s1 % al || k.s2 % al) return false;
+    // the packed ranges address a (batch, KV head) slice of the codes, scales and zeros with 32-bit
+    // byte offsets, and tokens with 32-bit indices
+    auto slice31 = [&](const anna_mi_view& v, int64_t esz, int64_t groups) {
+      return v.s2 >= 0 && v.s3 >= 0 && (a.len1 * v.s2 + groups * v.s3 + a.head_dim) * esz < (1ll << 31);
+    };
+    const int64_t ng = a.value_group_size > 0 ? a.head_dim / a.value_group_size + 1 : 1;
+    if (a.len1 + a.len2 >= (1ll << 31) || !slice31(k, 1, 0) || !slice31(a.value, 1, 0) ||
+        !slice31(a.value_scales, 2, ng) || !slice31(a.value_zeros, 2, ng))
+      return false;
+    // and stages the packed values from raw codes (whole 32-dim scale groups, the lane's codes of a
+    // token one aligned vector load), which the kernel then takes as given
+    const int64_t vsb = a.value_bits == 2 ? 2 : 4, vca = std::min<int64_t>((a.head_dim / 4 * vsb / 8 + 3) / 4 * 4, 16);
+    const anna_mi_view& v = a.value;
+    if (a.value_group_size % 32 != 0 || v.s3 != 1 || (uintptr_t)v.ptr % vca || v.s0 % vca || v.s1 % vca || v.s2 % vca)
+      return false;
   } else if (a.len1 > 0) {
     if (!rows16(a.key)) return false;
   }
