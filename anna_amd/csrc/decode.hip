@@ -826,14 +826,19 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
   // the raw path takes tiles whose tokens are all packed (min/max); others are staged by the
   // chunked loop below
   auto raw_tile = [&](int64_t tt0) { return rawok && (tt0 + MF_TILE <= L1 || t1 <= L1); };
-  auto issue = [&](Regs& R, int n) {
+  // PK (TQ-MSE keys): the tile belongs to a packed range.  Packed and window ranges run separate
+  // instances of the loads and of the tile step, so that neither carries the other's code.
+  using PkT = std::integral_constant<bool, true>;
+  using PkF = std::integral_constant<bool, false>;
+  auto issue = [&](Regs& R, int n, auto pk) __attribute__((always_inline)) {
+    constexpr bool PK = KSB > 0 && decltype(pk)::value;
     const int64_t tt0 = t0 + (int64_t)MF_TILE * n;
     if constexpr (KSB > 0) {
       // packed ranges: codes, scales and zeros of the lane's two staging tokens, the key codes of
       // tokens r and 16 + r, one add and one min per address (window ranges: dense keys below,
       // no value codes)
-      const uint32_t nn = packed_rng ? (uint32_t)n : 0u;
-      if (packed_rng) {
+      const uint32_t nn = (uint32_t)n;
+      if constexpr (PK) {
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const uint32_t tv = min((u ? o_v1 : o_v0) + nn * inc_v, lim_v);
@@ -882,7 +887,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
     }
     // key rows of tokens tt0 + r and tt0 + 16 + r (clamped into the range; masked below)
     const int64_t ta = tt0 + r < t1 ? tt0 + r : t1 - 1, tb = tt0 + 16 + r < t1 ? tt0 + 16 + r : t1 - 1;
-    if (KSB > 0 && packed_rng) {
+    if constexpr (PK) {
       // (the key code words are loaded above) the norms of the lane's score rows (tokens
       // 4 kq + i, 16 + 4 kq + i, clamped into the range: the last tile may pass the segment)
       const uint16_t* kn0 = (const uint16_t*)a.key_norms.ptr + b * a.key_norms.s0 + kvh * a.key_norms.s1;
@@ -918,7 +923,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
   // take turns (tile n + 2's loads go into tile n's set after its scores)
   constexpr int NB = NT > 0 ? NT : 2;
   Regs buf[NB];
-  if (live) issue(buf[0], 0);
+  auto issue_any = [&](Regs& R, int n) __attribute__((always_inline)) {
+    if (KSB > 0 && packed_rng) issue(R, n, PkT{});
+    else issue(R, n, PkF{});
+  };
+  if (live) issue_any(buf[0], 0);
   // query fragments: lane (head r, kq) of step st holds q[head][32 st + 8 kq .. + 7] (0 for
   // r >= G); they go through registers to LDS once and are read back per tile
   u32x4 qf[NST];
@@ -948,9 +957,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
   if (live) {
     if constexpr (NT > 0) {
 #pragma unroll
-      for (int n = 1; n < NT; ++n) issue(buf[n], n);
+      for (int n = 1; n < NT; ++n) issue_any(buf[n], n);
     } else {
-      if (ntiles > 1) issue(buf[1], 1);
+      if (ntiles > 1) issue_any(buf[1], 1);
     }
   }
   // the first use of a loaded value (the padding heads' zeros included) stays below every load:
@@ -965,13 +974,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
 #pragma unroll
   for (int j = 0; j < NDT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto process = [&](Regs& R, int n) {
+  auto process = [&](Regs& R, int n, auto pk) __attribute__((always_inline)) {
+    constexpr bool PK = KSB > 0 && decltype(pk)::value;
     const int64_t tt0 = t0 + (int64_t)MF_TILE * n;
     // ---- V of the tile into LDS, transposed.  With per-row lengths the slots past a row's length
     // (stale memory, possibly not finite) stage as zeros: their probabilities are 0, but 0 * NaN
     // would not be.
     const bool keep0 = !SEQ || valid(tt0 + 2 * p), keep1 = !SEQ || valid(tt0 + 2 * p + 1);
-    if (raw_tile(tt0)) {
+    // (with TQ-MSE keys exactly the packed ranges' tiles are raw: the host guarantees raw-ready
+    // values, and window tiles never are)
+    if (KSB > 0 ? PK : raw_tile(tt0)) {
       if constexpr (VF == ANNA_MI_VALUES_MINMAX) {
         constexpr uint32_t mask = (1u << SB) - 1u;
 #pragma unroll
@@ -1078,7 +1090,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
     // ---- scores: st0 rows = tokens tt0 + 0..15, st1 rows = tt0 + 16..31; columns = heads
     f32x4 st0 = {0.f, 0.f, 0.f, 0.f}, st1 = st0;
     float kscale[8];
-    if (KSB > 0 && packed_rng) {
+    if constexpr (PK) {
       // the codes of dims QD kq + 8 st .. + 7 through the table
       auto frag = [&](const uint32_t (&kc)[KCW], int st) -> u32x4 {
         if constexpr (KSB == 4) {
@@ -1109,7 +1121,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
       for (int i = 0; i < 8; ++i) kscale[i] = scale2;
     }
     // this buffer is free again: tile n + 2 goes in flight
-    if (NT == 0 && n + 2 < ntiles) issue(R, n + 2);
+    if (NT == 0 && n + 2 < ntiles) issue(R, n + 2, pk);
     float s[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -1165,12 +1177,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
   if (live) {
     if constexpr (NT > 0) {
 #pragma unroll
-      for (int n = 0; n < NT; ++n) process(buf[n], n);
+      for (int n = 0; n < NT; ++n) process(buf[n], n, PkF{});
     } else {
-      for (int n = 0; n < ntiles; n += 2) {
-        process(buf[0], n);
-        if (n + 1 < ntiles) process(buf[1], n + 1);
-      }
+      auto tiles = [&](auto pk) __attribute__((always_inline)) {
+        for (int n = 0; n < ntiles; n += 2) {
+          process(buf[0], n, pk);
+          if (n + 1 < ntiles) process(buf[1], n + 1, pk);
+        }
+      };
+      if (KSB > 0 && packed_rng) tiles(PkT{});
+      else tiles(PkF{});
     }
   }
 
