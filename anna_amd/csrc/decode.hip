@@ -933,11 +933,65 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 
   u32x4 qf[NST];
   {
     const bool qvec = a.query.s3 == 1 && (uintptr_t)a.query.ptr % 16 == 0 && a.query.s0 % 8 == 0 && a.query.s1 % 8 == 0;
+    // Packed ranges with the randomized Hadamard rotation (16-byte aligned signs: the host then
+    // launches no rotation): q' = H diag(s) q / sqrt(D) here, in the operation order of the
+    // rotation kernel (signs, butterflies over index bits 0, 1, .. in ascending order, the scale),
+    // so the same bits.  Lane (head r, kq) holds dims QD kq .. + QD - 1: index bits below
+    // log2(QD) pair up inside the lane, the top two across lanes 16 and 32 apart.
+    const bool rot_here = KSB > 0 && a.rotation_signs && (uintptr_t)a.rotation_signs % 16 == 0;
+    u32x4 qrot[NST];
+    if constexpr (KSB > 0) {
+      if (packed_rng && rot_here) {
+        float v[1][QD];
+        const int64_t qb = b * a.query.s0 + (kvh * G + (r < G ? r : 0)) * a.query.s1;
+        const uint16_t* q = (const uint16_t*)a.query.ptr;
+#pragma unroll
+        for (int j = 0; j < QD; j += 8) {
+          const int64_t d0 = QD * kq + j;
+          const float4 s0 = *(const float4*)(a.rotation_signs + d0), s1 = *(const float4*)(a.rotation_signs + d0 + 4);
+          const float sg[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+          uint16_t h[8];
+          if (qvec) {
+            const u32x4 w = *(const u32x4*)(q + qb + d0);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) h[e] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) h[e] = q[qb + (d0 + e) * a.query.s3];
+          }
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            v[0][j + e] = (DT == ANNA_MI_BF16 ? bf16_bits_to_f32(h[e]) : f16_bits_to_f32(h[e])) * sg[e];
+        }
+#pragma unroll
+        for (int hb = 1; hb < QD; hb <<= 1) {
+#pragma unroll
+          for (int e = 0; e < QD; ++e) {
+            if ((e & hb) == 0) {
+              const float x = v[0][e], y = v[0][e + hb];
+              v[0][e] = x + y;
+              v[0][e + hb] = x - y;
+            }
+          }
+        }
+        fwht_lane_stage<16>(v, (lane & 16) != 0);
+        fwht_lane_stage<32>(v, (lane & 32) != 0);
+        const float inv = tq_inv_sqrt(D);
+#pragma unroll
+        for (int st = 0; st < NST; ++st) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            qrot[st][e] = pack2_16<ANNA_MI_F16>(v[0][8 * st + 2 * e] * inv, v[0][8 * st + 2 * e + 1] * inv);
+        }
+      }
+    }
     const int64_t qb = b * a.query.s0 + (kvh * G + (r < G ? r : 0)) * a.query.s1;
     const uint16_t* q = (const uint16_t*)a.query.ptr;
 #pragma unroll
     for (int st = 0; st < NST; ++st) {
-      if (KSB > 0 && packed_rng) {
+      if (KSB > 0 && packed_rng && rot_here) {
+        qf[st] = qrot[st];
+      } else if (KSB > 0 && packed_rng) {
         // q' = R q (fp32, written by the rotation launch) as fp16, dims QD kq + 8 st .. + 7
         const float* qrow = a.query_rot + (b * a.q_heads + kvh * G + (r < G ? r : 0)) * D + QD * kq + 8 * st;
         const float4 lo = *(const float4*)qrow, hi = *(const float4*)(qrow + 4);
@@ -1449,7 +1503,18 @@ static int gqa_decode_splitkv_impl(const anna_mi_decode_args& a, void* stream) {
   ANNA_CHECK(nblk <= a.partial_capacity, "partial_stats/partial_values capacity %lld is smaller than %lld blocks",
              (long long)a.partial_capacity, (long long)nblk);
   hipStream_t st = as_stream(stream);
-  if (a.key_format == ANNA_MI_KEYS_TQ_MSE && a.len1 > 0) {
+  const bool kq = a.key_format == ANNA_MI_KEYS_TQ_MSE;
+  int64_t nmerge = nblk;  // partials written by the split kernel
+  int64_t mf_range = 0, mf_nr1 = 0, mf_n = 0;
+  if (mfma_path_ok(a, sp)) {
+    mf_range = mfma_range(a);
+    mf_n = mfma_ranges(a, mf_range, &mf_nr1);
+  }
+  const bool use_mfma = mf_n > 0 && mf_n <= a.partial_capacity;  // (two aligned segments take two ranges at least)
+  // the MFMA kernel rotates the query itself with 16-byte aligned Hadamard signs (the same
+  // condition as in the kernel)
+  const bool rot_in_split = use_mfma && kq && a.rotation_signs && (uintptr_t)a.rotation_signs % 16 == 0;
+  if (kq && a.len1 > 0 && !rot_in_split) {
     const int64_t D = a.head_dim;
     if (a.rotation_signs && (D == 64 || D == 128 || D == 256 || D == 512 || D == 1024)) {
       const dim3 grid((unsigned)((a.batch * a.q_heads + 3) / 4));
@@ -1467,14 +1532,7 @@ static int gqa_decode_splitkv_impl(const anna_mi_decode_args& a, void* stream) {
       ANNA_LAUNCH_CHECK("decode_rotate_query_kernel");
     }
   }
-  const bool kq = a.key_format == ANNA_MI_KEYS_TQ_MSE;
-  int64_t nmerge = nblk;  // partials written by the split kernel
-  int64_t mf_range = 0, mf_nr1 = 0, mf_n = 0;
-  if (mfma_path_ok(a, sp)) {
-    mf_range = mfma_range(a);
-    mf_n = mfma_ranges(a, mf_range, &mf_nr1);
-  }
-  if (mf_n > 0 && mf_n <= a.partial_capacity) {  // (two aligned segments take two ranges at least)
+  if (use_mfma) {
     nmerge = mf_n;
     launch_split_mfma(a, mf_range, nmerge, mf_nr1, st);
   } else switch (a.value_format) {
