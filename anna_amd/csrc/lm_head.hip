@@ -350,17 +350,35 @@ __device__ __forceinline__ void tk8_insert(float (&rv)[8], int32_t (&ri)[8], flo
   for (int j = 7; j >= 1; --j) tk_ce(rv[j - 1], ri[j - 1], rv[j], ri[j]);
 }
 
+// Value of a lane's DPP partner (a symmetric pairing inside 16-lane rows: quad permutes, the
+// half-row and the row mirror); one VALU move, no trip through the LDS pipe.
+template <int CTRL>
+__device__ __forceinline__ int32_t tk_dpp(int32_t v) {
+  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
+}
+
+// Arg-best over the wave, every lane ending with the winner: four DPP pairings inside each
+// 16-lane row (xor 1, xor 2, then i <-> 7 - i and i <-> 15 - i, which pair the quads and the
+// halves), then two shuffles across rows.  (Six xor shuffles chained twelve LDS-pipe round trips
+// per winner.)
+__device__ __forceinline__ void tk_wave_best(float& bv, int32_t& bi) {
+  auto take = [&](float pv, int32_t pi) {
+    if (tk_better(pv, pi, bv, bi)) bv = pv, bi = pi;
+  };
+  take(__int_as_float(tk_dpp<0xB1>(__float_as_int(bv))), tk_dpp<0xB1>(bi));    // quad_perm [1, 0, 3, 2]
+  take(__int_as_float(tk_dpp<0x4E>(__float_as_int(bv))), tk_dpp<0x4E>(bi));    // quad_perm [2, 3, 0, 1]
+  take(__int_as_float(tk_dpp<0x141>(__float_as_int(bv))), tk_dpp<0x141>(bi));  // row_half_mirror
+  take(__int_as_float(tk_dpp<0x140>(__float_as_int(bv))), tk_dpp<0x140>(bi));  // row_mirror
+  take(__shfl_xor(bv, 16, 64), __shfl_xor(bi, 16, 64));
+  take(__shfl_xor(bv, 32, 64), __shfl_xor(bi, 32, 64));
+}
+
 __device__ __forceinline__ void tk8_wave_tournament(float (&rv)[8], int32_t (&ri)[8], float (&ov)[8], int32_t (&oi)[8]) {
 #pragma unroll
   for (int r = 0; r < 8; ++r) {
     float bv = rv[0];
     int32_t bi = ri[0];
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-      const float pv = __shfl_xor(bv, m, 64);
-      const int32_t pi = __shfl_xor(bi, m, 64);
-      if (tk_better(pv, pi, bv, bi)) bv = pv, bi = pi;
-    }
+    tk_wave_best(bv, bi);
     ov[r] = bv, oi[r] = bi;
     if (ri[0] == bi) {
 #pragma unroll
