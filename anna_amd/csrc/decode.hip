@@ -640,7 +640,9 @@ __global__ __launch_bounds__(64 * MERGE_DIM_WAVES) void decode_merge_dims_kernel
 //   * With a fixed tile count (1..4) all of the range's loads are issued at the start, one
 //     register set per tile; otherwise two sets hold tiles n and n + 1 and tile n + 2's loads go
 //     into set n % 2 right after tile n's scores.  Two tiles per wave run two waves per SIMD
-//     (228 registers); three or four run one.
+//     (228 registers); three or four run one; TQ-MSE keys at head_dim <= 128 run two (within 256
+//     registers and no spills since the packed tiles' addressing is 32-bit: 28.7 -> 27.7 us for
+//     TurboQuantRowsCache at D = 128), at 256 one.
 // Each wave writes its range's partial from registers in the reference layout (natural-log max,
 // denominator, unnormalized values), so the merge kernels take it as they take the VALU
 // kernel's blocks.
@@ -713,7 +715,7 @@ __device__ __forceinline__ void load_words(uint32_t (&w)[N], const uint8_t* p) {
 // SEQ: per-row lengths (a.seq_lengths): row b's valid tokens are the first n1 packed slots and
 // the first n2 window slots; a range with none of them writes an empty partial.
 template <int DT, int VF, int SB, int D, int NT, int KSB, bool SEQ>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 ? 2 : 1, NT == 2 ? 2 : 1))) void decode_split_mfma_kernel(
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 || (KSB > 0 && D <= 128) ? 2 : 1, NT == 2 || (KSB > 0 && D <= 128) ? 2 : 1))) void decode_split_mfma_kernel(
     const anna_mi_decode_args a, const int64_t range, const int64_t nr1) {
   using Regs = MfmaTileRegs<D, SB, KSB>;
   constexpr int NST = Regs::NST, NSP = Regs::NSP, QD = Regs::QD, CW = Regs::CW, KCW = Regs::KCW;
