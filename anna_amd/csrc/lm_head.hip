@@ -357,10 +357,22 @@ __device__ __forceinline__ int32_t tk_dpp(int32_t v) {
   return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
 }
 
+// Value of lane l ^ 16 and of lane l ^ 32 (all 64 lanes active): gfx950's row swaps on the VALU.
+// v_permlane16_swap of (v, v) returns {rows 0, 0, 2, 2; rows 1, 1, 3, 3}, v_permlane32_swap of
+// (v, v) returns {lanes 0-31 twice; lanes 32-63 twice}; a lane takes the copy of the other row.
+__device__ __forceinline__ int32_t tk_xor16(int32_t v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return (threadIdx.x & 16) ? (int32_t)r[0] : (int32_t)r[1];
+}
+__device__ __forceinline__ int32_t tk_xor32(int32_t v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return (threadIdx.x & 32) ? (int32_t)r[0] : (int32_t)r[1];
+}
+
 // Arg-best over the wave, every lane ending with the winner: four DPP pairings inside each
 // 16-lane row (xor 1, xor 2, then i <-> 7 - i and i <-> 15 - i, which pair the quads and the
-// halves), then two shuffles across rows.  (Six xor shuffles chained twelve LDS-pipe round trips
-// per winner.)
+// halves), then the two row swaps.  (Six xor shuffles chained twelve LDS-pipe round trips per
+// winner.)
 __device__ __forceinline__ void tk_wave_best(float& bv, int32_t& bi) {
   auto take = [&](float pv, int32_t pi) {
     if (tk_better(pv, pi, bv, bi)) bv = pv, bi = pi;
@@ -369,8 +381,8 @@ __device__ __forceinline__ void tk_wave_best(float& bv, int32_t& bi) {
   take(__int_as_float(tk_dpp<0x4E>(__float_as_int(bv))), tk_dpp<0x4E>(bi));    // quad_perm [2, 3, 0, 1]
   take(__int_as_float(tk_dpp<0x141>(__float_as_int(bv))), tk_dpp<0x141>(bi));  // row_half_mirror
   take(__int_as_float(tk_dpp<0x140>(__float_as_int(bv))), tk_dpp<0x140>(bi));  // row_mirror
-  take(__shfl_xor(bv, 16, 64), __shfl_xor(bi, 16, 64));
-  take(__shfl_xor(bv, 32, 64), __shfl_xor(bi, 32, 64));
+  take(__int_as_float(tk_xor16(__float_as_int(bv))), tk_xor16(bi));
+  take(__int_as_float(tk_xor32(__float_as_int(bv))), tk_xor32(bi));
 }
 
 __device__ __forceinline__ void tk8_wave_tournament(float (&rv)[8], int32_t (&ri)[8], float (&ov)[8], int32_t (&oi)[8]) {
@@ -426,37 +438,54 @@ __global__ __launch_bounds__(64) void topk_chunk_wave_kernel(float* __restrict__
     }
 }
 
-// grid (rows), one wave: the C chunk lists of topk_chunk_wave_kernel merged the same way.
+// grid (rows), TKM_WAVES waves per row: the C chunk lists of topk_chunk_wave_kernel merged the same
+// way, in two levels -- wave w takes the w-th share of the C * 8 candidates (a few per lane) to its
+// best 8, and wave 0 merges those lists (one candidate per lane) -- instead of one wave inserting
+// every candidate (~19 per lane at C = 148: 10.9 us).  The union of the shares' best 8 holds the
+// row's best 8, and the order (tk_better, unique indices) is the same at both levels.
+constexpr int TKM_WAVES = 8;
 template <int ODT>
-__global__ __launch_bounds__(64) void topk_merge_waves_kernel(const float* __restrict__ logits, int64_t ld, int64_t C,
-                                                              int64_t S, int k, typename Elem<ODT>::T* __restrict__ out_v,
-                                                              int64_t* __restrict__ out_i) {
-  const int lane = threadIdx.x;
+__global__ __launch_bounds__(64 * TKM_WAVES) void topk_merge_waves_kernel(const float* __restrict__ logits, int64_t ld, int64_t C,
+                                                                          int64_t S, int k, typename Elem<ODT>::T* __restrict__ out_v,
+                                                                          int64_t* __restrict__ out_i) {
+  __shared__ float s_v[TKM_WAVES * 8];
+  __shared__ int32_t s_i[TKM_WAVES * 8];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t row = blockIdx.x;
   const float* lg = logits + row * ld;
   float rv[8];
   int32_t ri[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) rv[j] = -INFINITY, ri[j] = INT32_MAX;
-  // every candidate's loads are issued before any is compared (one round trip for C <= 192;
-  // a batch of 4 per lane had taken a round trip each, 14 us at C = 148)
-  constexpr int NB = 24;
-  for (int64_t e0 = 0; e0 < C * 8; e0 += 64 * NB) {
+  // this wave's share of the candidates; every load of a batch is issued before any is compared
+  const int64_t n = C * 8, per = (n + TKM_WAVES - 1) / TKM_WAVES;
+  const int64_t e_lo = wave * per, e_hi = e_lo + per < n ? e_lo + per : n;
+  constexpr int NB = 4;
+  for (int64_t e0 = e_lo; e0 < e_hi; e0 += 64 * NB) {
     float cv[NB];
     int32_t ci[NB];
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
-      const int64_t e0u = e0 + lane + 64 * u, e = e0u < C * 8 ? e0u : 0;
+      const int64_t e0u = e0 + lane + 64 * u, e = e0u < e_hi ? e0u : e_lo;
       const int64_t c = e / 8, j = e % 8;
       cv[u] = lg[c * S + j];
       ci[u] = __float_as_int(lg[c * S + 8 + j]);
     }
 #pragma unroll
     for (int u = 0; u < NB; ++u)
-      if (e0 + lane + 64 * u < C * 8) tk8_insert(rv, ri, cv[u], ci[u]);
+      if (e0 + lane + 64 * u < e_hi) tk8_insert(rv, ri, cv[u], ci[u]);
   }
   float ov[8];
   int32_t oi[8];
+  tk8_wave_tournament(rv, ri, ov, oi);
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if (lane == j) s_v[wave * 8 + j] = ov[j], s_i[wave * 8 + j] = oi[j];
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) rv[j] = -INFINITY, ri[j] = INT32_MAX;
+  if (lane < TKM_WAVES * 8) rv[0] = s_v[lane], ri[0] = s_i[lane];
   tk8_wave_tournament(rv, ri, ov, oi);
 #pragma unroll
   for (int j = 0; j < 8; ++j)
@@ -803,7 +832,7 @@ int topk_rows(const float* values, int64_t rows, int64_t V, int64_t ld, int64_t 
         if (V - (C - 1) * S < 16) --C;  // the last chunk takes the short tail
         hipLaunchKernelGGL(topk_chunk_wave_kernel, dim3((unsigned)C, (unsigned)rows), dim3(64), 0, as_stream(stream),
                            const_cast<float*>(values), V, ld, S);
-        hipLaunchKernelGGL((topk_merge_waves_kernel<ODT>), dim3((unsigned)rows), dim3(64), 0, as_stream(stream),
+        hipLaunchKernelGGL((topk_merge_waves_kernel<ODT>), dim3((unsigned)rows), dim3(64 * TKM_WAVES), 0, as_stream(stream),
                            values, ld, C, S, (int)top_k, (typename Elem<ODT>::T*)out_values, out_indices);
       } else {
         const int nt = tk_threads(8);
