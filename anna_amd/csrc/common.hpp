@@ -92,6 +92,21 @@ inline bool valid_dtype(int dt) { return dt == ANNA_MI_BF16 || dt == ANNA_MI_F16
   }
 
 // ---------------------------------------------------------------- wave ops
+// Value of lane l ^ 16 and of lane l ^ 32 (all 64 lanes active): gfx950's row swaps, one VALU
+// instruction and a select instead of a round trip through the LDS pipe.  v_permlane16_swap of
+// (v, v) returns {rows 0, 0, 2, 2; rows 1, 1, 3, 3} (16-lane rows), v_permlane32_swap of (v, v)
+// {lanes 0-31 twice; lanes 32-63 twice}; a lane takes the copy of the other row.
+__device__ __forceinline__ int32_t lane_xor16(int32_t v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return (threadIdx.x & 16) ? (int32_t)r[0] : (int32_t)r[1];
+}
+__device__ __forceinline__ int32_t lane_xor32(int32_t v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return (threadIdx.x & 32) ? (int32_t)r[0] : (int32_t)r[1];
+}
+__device__ __forceinline__ float lane_xor16(float v) { return __int_as_float(lane_xor16(__float_as_int(v))); }
+__device__ __forceinline__ float lane_xor32(float v) { return __int_as_float(lane_xor32(__float_as_int(v))); }
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);

@@ -1187,8 +1187,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 || (
     float mx = s[0];
 #pragma unroll
     for (int i = 1; i < 8; ++i) mx = fmaxf(mx, s[i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = fmaxf(mx, lane_xor16(mx));
+    mx = fmaxf(mx, lane_xor32(mx));
     if (__any(mx > m_run + LAZY)) {
       const float m_new = fmaxf(m_run, mx);
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 while m_run is -inf
@@ -1248,8 +1248,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 || (
 
   // ---- the range's partial: stats of head r from lanes (r, kq = 0), values [b, hq, blk, d] from
   // the accumulators (lane (dim 16 j + r, kq) holds heads 4 kq + i)
-  l_run += __shfl_xor(l_run, 16, 64);
-  l_run += __shfl_xor(l_run, 32, 64);
+  l_run += lane_xor16(l_run);
+  l_run += lane_xor32(l_run);
   if (kq == 0 && r < G) {
     const anna_mi_view& ps = a.partial_stats;
     const int64_t base = b * ps.s0 + (kvh * G + r) * ps.s1 + blk * ps.s2;

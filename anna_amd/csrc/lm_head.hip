@@ -357,18 +357,6 @@ __device__ __forceinline__ int32_t tk_dpp(int32_t v) {
   return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
 }
 
-// Value of lane l ^ 16 and of lane l ^ 32 (all 64 lanes active): gfx950's row swaps on the VALU.
-// v_permlane16_swap of (v, v) returns {rows 0, 0, 2, 2; rows 1, 1, 3, 3}, v_permlane32_swap of
-// (v, v) returns {lanes 0-31 twice; lanes 32-63 twice}; a lane takes the copy of the other row.
-__device__ __forceinline__ int32_t tk_xor16(int32_t v) {
-  const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-  return (threadIdx.x & 16) ? (int32_t)r[0] : (int32_t)r[1];
-}
-__device__ __forceinline__ int32_t tk_xor32(int32_t v) {
-  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-  return (threadIdx.x & 32) ? (int32_t)r[0] : (int32_t)r[1];
-}
-
 // Arg-best over the wave, every lane ending with the winner: four DPP pairings inside each
 // 16-lane row (xor 1, xor 2, then i <-> 7 - i and i <-> 15 - i, which pair the quads and the
 // halves), then the two row swaps.  (Six xor shuffles chained twelve LDS-pipe round trips per
@@ -381,8 +369,8 @@ __device__ __forceinline__ void tk_wave_best(float& bv, int32_t& bi) {
   take(__int_as_float(tk_dpp<0x4E>(__float_as_int(bv))), tk_dpp<0x4E>(bi));    // quad_perm [2, 3, 0, 1]
   take(__int_as_float(tk_dpp<0x141>(__float_as_int(bv))), tk_dpp<0x141>(bi));  // row_half_mirror
   take(__int_as_float(tk_dpp<0x140>(__float_as_int(bv))), tk_dpp<0x140>(bi));  // row_mirror
-  take(__int_as_float(tk_xor16(__float_as_int(bv))), tk_xor16(bi));
-  take(__int_as_float(tk_xor32(__float_as_int(bv))), tk_xor32(bi));
+  take(lane_xor16(bv), lane_xor16(bi));
+  take(lane_xor32(bv), lane_xor32(bi));
 }
 
 __device__ __forceinline__ void tk8_wave_tournament(float (&rv)[8], int32_t (&ri)[8], float (&ov)[8], int32_t (&oi)[8]) {

@@ -273,8 +273,8 @@ __device__ __forceinline__ void block_step(const anna_mi_tq_decode_args& a, cons
     float mx = s[0];
 #pragma unroll
     for (int i = 1; i < 8; ++i) mx = fmaxf(mx, s[i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = fmaxf(mx, lane_xor16(mx));
+    mx = fmaxf(mx, lane_xor32(mx));
     if (__any(mx > m_run + LAZY)) {
       const float m_new = fmaxf(m_run, mx);
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
@@ -616,8 +616,8 @@ void tq_decode_kernel(const anna_mi_tq_decode_args a, const anna_mi_tq_append_ar
   }
   // ---- reduce the waves, write this item's partials (workgroup index = item slot)
   const int64_t item = blockIdx.x;
-  l_run += __shfl_xor(l_run, 16, 64);
-  l_run += __shfl_xor(l_run, 32, 64);
+  l_run += lane_xor16(l_run);
+  l_run += lane_xor32(l_run);
   if (kq == 0) {
     s_m[wave][r] = m_run;
     s_l[wave][r] = l_run;
