@@ -220,3 +220,57 @@ def test_rows_cache_hadamard_query_rotation_matches_dense(gpu, d):
     finally:
         cache.qn.signs = signs
     assert rel_err(fast.cpu().numpy(), dense.cpu().numpy()) <= 1e-2
+
+
+@pytest.mark.parametrize("d,bits", [(128, 4), (64, 2)])
+def test_rows_cache_value_group_16_takes_the_valu_split(gpu, d, bits):
+    """Value groups of 16 dims are not whole 32-dim spans, which the MFMA split kernel's raw value
+    staging needs: the decode runs on the VALU split kernel instead, and still matches the
+    oracle after loading and after appends."""
+    print(f"[case] tq rows group 16 d={d} bits={bits}", flush=True)
+    torch.manual_seed(1600 + d + bits)
+    hkv, g, R = 2, 4, 16
+    lens = [90, 23]
+    cache = TurboQuantRowsCache(batch=2, kv_heads=hkv, q_heads=hkv * g, capacities=[96, 96], residual_capacity=R,
+                                head_dim=d, bits=bits, device=gpu, value_group_size=16)
+    keys = [torch.randn(hkv, L, d, device=gpu).to(torch.bfloat16) for L in lens]
+    vals = [torch.randn(hkv, L, d, device=gpu).to(torch.bfloat16) for L in lens]
+    for b in range(2):
+        cache.load_sequence(b, keys[b], vals[b])
+    for step in range(3):
+        if step > 0:
+            nk = torch.randn(2, hkv, d, device=gpu).to(torch.bfloat16)
+            nv = torch.randn(2, hkv, d, device=gpu).to(torch.bfloat16)
+            cache.append(nk, nv)
+            keys = [torch.cat([keys[b], nk[b][:, None]], 1) for b in range(2)]
+            vals = [torch.cat([vals[b], nv[b][:, None]], 1) for b in range(2)]
+        q = torch.randn(2, hkv * g, d, device=gpu).to(torch.bfloat16)
+        out = cache.decode(q, scaling=d ** -0.5)
+        check_rows(cache, keys, vals, q, out)
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_rows_cache_query_rotation_in_the_split_is_bit_exact(gpu, d):
+    """With 16-byte aligned Hadamard signs the MFMA split kernel rotates the query itself; with
+    signs that are not (a view one float into a buffer) the separate rotation launch does.  Both
+    follow the same operation order, so the decode outputs are identical bit for bit."""
+    print(f"[case] tq rows in-split rotation d={d}", flush=True)
+    torch.manual_seed(2700 + d)
+    hkv, g, R = 2, 8, 32
+    cache = TurboQuantRowsCache(batch=2, kv_heads=hkv, q_heads=hkv * g, capacities=[200, 200], residual_capacity=R,
+                                head_dim=d, bits=4, device=gpu)
+    for b, L in enumerate((190, 57)):
+        cache.load_sequence(b, torch.randn(hkv, L, d, device=gpu).to(torch.bfloat16),
+                            torch.randn(hkv, L, d, device=gpu).to(torch.bfloat16))
+    q = torch.randn(2, hkv * g, d, device=gpu).to(torch.bfloat16)
+    in_split = cache.decode(q, scaling=d ** -0.5).clone()
+    signs = cache.qn.signs
+    buf = torch.empty(d + 1, dtype=signs.dtype, device=gpu)
+    buf[1:] = signs
+    assert buf[1:].data_ptr() % 16 != 0
+    try:
+        cache.qn.signs = buf[1:]
+        launched = cache.decode(q, scaling=d ** -0.5).clone()
+    finally:
+        cache.qn.signs = signs
+    assert torch.equal(in_split.view(torch.int16), launched.view(torch.int16))
