@@ -1067,6 +1067,17 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 || (
                 v[u][2 * e] = (float)((lo >> (8 * e)) & 0xFFu) * sc + zc;
                 v[u][2 * e + 1] = (float)((hi >> (8 * e)) & 0xFFu) * sc + zc;
               }
+            } else if constexpr (SB == 2) {
+              // one word holds the codes of chunks 2 (c / 2) and + 1: code j sits in byte j / 4 of
+              // plane j % 4 (planes = the word's 2-bit fields masked apart), one byte-to-float
+              // conversion each; this chunk's codes are bytes 2 (c % 2) and + 1
+              const uint32_t w = R.vc[u][c >> 1];
+              const int hb = 2 * (c & 1);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                const uint32_t plane = (w >> (2 * (e & 3))) & 0x03030303u;
+                v[u][e] = (float)((plane >> (8 * (hb + (e >> 2)))) & 0xFFu) * sc + zc;
+              }
             } else {
               // codes of dims 8c .. 8c + 7 of the lane's quarter: 8 SB bits from bit 8 SB c
               const uint32_t w = R.vc[u][(8 * SB * c) / 32] >> ((8 * SB * c) % 32);
