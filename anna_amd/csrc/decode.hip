@@ -9,6 +9,11 @@
 //   h, h + GM, ..., and the waves are merged through LDS.
 //   Output: per (b, q-head, block) the running max, the denominator and the
 //   unnormalized accumulator, in the reference's partial_stats / partial_values layout.
+// Kernel 1' (decode_split_mfma_kernel): the MFMA form of kernel 1 for 16-bit activations, dense or
+//   TQ-MSE keys and dense or min/max values at head_dim 64/128/256: one wave per range of 32-token
+//   tiles (described at the kernel).  With TQ-MSE keys the query is rotated first: by the split
+//   kernel itself for the randomized Hadamard rotation (16-byte aligned signs), else by a
+//   rotation launch (decode_rotate_query_hadamard_kernel / decode_rotate_query_kernel).
 // Kernel 2: log-sum-exp merge of the blocks per (b, q-head), optional sigmoid gate.
 //   decode_merge_dims_kernel (64 dims per workgroup, the blocks split over 4 waves) when no
 //   block holds rotated values and there are at most 256 blocks; decode_merge_kernel (1024
