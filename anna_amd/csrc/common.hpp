@@ -107,6 +107,22 @@ __device__ __forceinline__ int32_t lane_xor32(int32_t v) {
 __device__ __forceinline__ float lane_xor16(float v) { return __int_as_float(lane_xor16(__float_as_int(v))); }
 __device__ __forceinline__ float lane_xor32(float v) { return __int_as_float(lane_xor32(__float_as_int(v))); }
 
+// Sum over the wave (all 64 lanes active), every lane ending with the total, with no LDS-pipe
+// round trip: DPP pairings inside 16-lane rows (quad xor 1, quad xor 2, i <-> 7 - i, i <-> 15 - i)
+// then the two row swaps.  Its summation order differs from wave_sum's xor tree.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum_rows(float v) {
+  v += dpp_move<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp_move<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp_move<0x141>(v);  // row_half_mirror
+  v += dpp_move<0x140>(v);  // row_mirror
+  v += lane_xor16(v);
+  return v + lane_xor32(v);
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);

@@ -193,7 +193,7 @@ __global__ __launch_bounds__(256) void int4_gemv_tiled_kernel(
       if (m0 + m >= M) continue;
 #pragma unroll
       for (int t = 0; t < T; ++t) {
-        const float v = wave_sum(acc[m][t]);
+        const float v = wave_sum_rows(acc[m][t]);
         const int64_t n = tile * T + t;
         if (lane == 0 && n < N) {
           if constexpr (OUT_F32) ((float*)y)[(m0 + m) * ys + n] = v;
@@ -699,7 +699,7 @@ __global__ __launch_bounds__(256) void int4_gemv_tiled_lds_kernel(
     if (m >= M) continue;
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-      const float v = wave_sum(acc[m][t]);
+      const float v = wave_sum_rows(acc[m][t]);
       const int64_t n = tile * T + t;
       if (lane == 0 && n < N) {
         if constexpr (OUT_F32) ((float*)y)[m * ys + n] = v;
