@@ -655,6 +655,7 @@ constexpr int MF_TILE = 32;         // tokens per tile
 constexpr int MF_VT = MF_TILE + 4;  // LDS pitch (elements) of the transposed V tile: 18 words,
                                     // so the 16 dims of a B-operand read hit distinct banks
 constexpr int64_t MF_WAVES_TARGET = 1536;  // about 6 waves per CU (NT = 2 runs two waves per SIMD)
+constexpr int64_t MF_WAVES_TQ2 = 2048;     // 8 per CU: the TQ-MSE-key instances at head_dim <= 128
 
 // Two floats rounded to nearest-even into the activation dtype, lo in bits 0..15 (one
 // v_cvt_pk_bf16_f32 for bf16).
@@ -1378,7 +1379,10 @@ int64_t mfma_ranges(const anna_mi_decode_args& a, int64_t range, int64_t* nr1) {
 int64_t mfma_range(const anna_mi_decode_args& a) {
   const int64_t L = a.len1 + a.len2;
   const int64_t tiles = a.batch * a.kv_heads * ((L + MF_TILE - 1) / MF_TILE);
-  int64_t range = (tiles + MF_WAVES_TARGET - 1) / MF_WAVES_TARGET * MF_TILE;
+  // TQ-MSE keys at head_dim <= 128 run two waves per SIMD: eight per CU (TurboQuantRowsCache
+  // D = 128: 26.7 -> 25.0 us against 1536 waves; 2560 no better)
+  const int64_t wt = a.key_format == ANNA_MI_KEYS_TQ_MSE && a.head_dim <= 128 ? MF_WAVES_TQ2 : MF_WAVES_TARGET;
+  int64_t range = (tiles + wt - 1) / wt * MF_TILE;
   if (range < MF_TILE) range = MF_TILE;
   int64_t nr1 = 0;
   while (mfma_ranges(a, range, &nr1) > a.partial_capacity && range < L) range += MF_TILE;
