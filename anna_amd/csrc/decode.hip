@@ -656,6 +656,7 @@ constexpr int MF_VT = MF_TILE + 4;  // LDS pitch (elements) of the transposed V 
                                     // so the 16 dims of a B-operand read hit distinct banks
 constexpr int64_t MF_WAVES_TARGET = 1536;  // about 6 waves per CU (NT = 2 runs two waves per SIMD)
 constexpr int64_t MF_WAVES_TQ2 = 2048;     // 8 per CU: the TQ-MSE-key instances at head_dim <= 128
+constexpr int64_t MF_WAVES_TQ1 = 1024;     // 4 per CU: the TQ-MSE-key instances at head_dim 256
 
 // Two floats rounded to nearest-even into the activation dtype, lo in bits 0..15 (one
 // v_cvt_pk_bf16_f32 for bf16).
@@ -1380,8 +1381,10 @@ int64_t mfma_range(const anna_mi_decode_args& a) {
   const int64_t L = a.len1 + a.len2;
   const int64_t tiles = a.batch * a.kv_heads * ((L + MF_TILE - 1) / MF_TILE);
   // TQ-MSE keys at head_dim <= 128 run two waves per SIMD: eight per CU (TurboQuantRowsCache
-  // D = 128: 26.7 -> 25.0 us against 1536 waves; 2560 no better)
-  const int64_t wt = a.key_format == ANNA_MI_KEYS_TQ_MSE && a.head_dim <= 128 ? MF_WAVES_TQ2 : MF_WAVES_TARGET;
+  // D = 128: 26.7 -> 25.0 us against 1536 waves; 2560 no better); at 256 one: four per CU (D = 256:
+  // 46.1 -> 45.1 us; 768 or 2048 waves 50.2 / 53.9)
+  const bool tqk = a.key_format == ANNA_MI_KEYS_TQ_MSE;
+  const int64_t wt = tqk ? (a.head_dim <= 128 ? MF_WAVES_TQ2 : MF_WAVES_TQ1) : MF_WAVES_TARGET;
   int64_t range = (tiles + wt - 1) / wt * MF_TILE;
   if (range < MF_TILE) range = MF_TILE;
   int64_t nr1 = 0;

@@ -420,13 +420,14 @@ def section_tq_pack(args, device):
 
 def section_tq_rows(args, device):
     """The batched cache for the shapes other than head_dim 256 / 2-bit (TurboQuantRowsCache):
-    B=8, Hq=16, Hkv=2, head_dim 128, 4-bit keys and values, L ~ U[1024, 16384] + 128 bf16 window."""
+    B=8, Hq=16, Hkv=2, head_dim 128, 4-bit keys and values (--tq-rows-dim / --tq-rows-bits change
+    them), L ~ U[1024, 16384] + 128 bf16 window."""
     import numpy as np
 
     from anna_amd.tq_cache import TurboQuantRowsCache
 
     rng = np.random.default_rng(5)
-    B, HQ, HKV, D, R, BITS = 8, 16, 2, 128, 128, 4
+    B, HQ, HKV, D, R, BITS = 8, 16, 2, args.tq_rows_dim, 128, args.tq_rows_bits
     lens = [int(v) for v in rng.integers(1024, 16385, size=B)]
     gen = torch.Generator(device=device)
     gen.manual_seed(55)
@@ -641,6 +642,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--sections", default="int4,tq_decode,row_decode,tq_pack,tq_rows,moe,lm_head")
     ap.add_argument("--tq-tokens-per-item", type=int, default=0)
+    ap.add_argument("--tq-rows-dim", type=int, default=128, help="head_dim of the tq_rows section (64, 128, 256)")
+    ap.add_argument("--tq-rows-bits", type=int, default=4, help="key/value bits of the tq_rows section (2, 3, 4)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--int4-points", default="", help="comma list of MxNxK (default: the BASELINE sweep)")
