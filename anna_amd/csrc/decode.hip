@@ -836,7 +836,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 || (
   // chunked loop below
   auto raw_tile = [&](int64_t tt0) { return rawok && (tt0 + MF_TILE <= L1 || t1 <= L1); };
   // PK (TQ-MSE keys): the tile belongs to a packed range.  Packed and window ranges run separate
-  // instances of the loads and of the tile step, so that neither carries the other's code.
+  // instances of the loads and of the tile step, so that neither carries the other's code.  (A
+  // third instance for dense-key ranges inside the packed segment pushed the row-API kernel past
+  // 256 registers into scratch: 22.2 -> 25.8 us.)
   using PkT = std::integral_constant<bool, true>;
   using PkF = std::integral_constant<bool, false>;
   auto issue = [&](Regs& R, int n, auto pk) __attribute__((always_inline)) {
@@ -932,11 +934,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 || (
   // take turns (tile n + 2's loads go into tile n's set after its scores)
   constexpr int NB = NT > 0 ? NT : 2;
   Regs buf[NB];
-  auto issue_any = [&](Regs& R, int n) __attribute__((always_inline)) {
-    if (KSB > 0 && packed_rng) issue(R, n, PkT{});
-    else issue(R, n, PkF{});
-  };
-  if (live) issue_any(buf[0], 0);
   // query fragments: lane (head r, kq) of step st holds q[head][32 st + 8 kq .. + 7] (0 for
   // r >= G); they go through registers to LDS once and are read back per tile
   u32x4 qf[NST];
@@ -1017,19 +1014,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 || (
       }
     }
   }
-  if (live) {
-    if constexpr (NT > 0) {
-#pragma unroll
-      for (int n = 1; n < NT; ++n) issue_any(buf[n], n);
-    } else {
-      if (ntiles > 1) issue_any(buf[1], 1);
-    }
-  }
-  // the first use of a loaded value (the padding heads' zeros included) stays below every load:
-  // a use above them made the compiler wait for all loads issued so far before issuing the rest
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int st = 0; st < NST; ++st) s_qf[st][lane] = r < G ? qf[st] : u32x4{0u, 0u, 0u, 0u};
 
   const float scale2 = a.scaling * LOG2E;
   float m_run = -INFINITY, l_run = 0.f;  // of head r (lane column), replicated over kq
@@ -1248,21 +1232,39 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NT == 2 || (
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the next tile's writes
   };
 
-  if (live) {
-    if constexpr (NT > 0) {
+  // The tile loads (after the query's: a wait for those never waits for the tiles), the query
+  // fragments into LDS, the tile loop -- one instance per tag, chosen once, so that the tile
+  // registers are written from one place in each (written from two branches, the compiler kept
+  // them in scratch memory).
+  auto run = [&](auto pk) __attribute__((always_inline)) {
+    if (live) {
+      if constexpr (NT > 0) {
 #pragma unroll
-      for (int n = 0; n < NT; ++n) process(buf[n], n, PkF{});
-    } else {
-      auto tiles = [&](auto pk) __attribute__((always_inline)) {
+        for (int n = 0; n < NT; ++n) issue(buf[n], n, pk);
+      } else {
+        issue(buf[0], 0, pk);
+        if (ntiles > 1) issue(buf[1], 1, pk);
+      }
+    }
+    // the first use of a loaded value (the padding heads' zeros included) stays below every load:
+    // a use above them made the compiler wait for all loads issued so far before issuing the rest
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int st = 0; st < NST; ++st) s_qf[st][lane] = r < G ? qf[st] : u32x4{0u, 0u, 0u, 0u};
+    if (live) {
+      if constexpr (NT > 0) {
+#pragma unroll
+        for (int n = 0; n < NT; ++n) process(buf[n], n, pk);
+      } else {
         for (int n = 0; n < ntiles; n += 2) {
           process(buf[0], n, pk);
           if (n + 1 < ntiles) process(buf[1], n + 1, pk);
         }
-      };
-      if (KSB > 0 && packed_rng) tiles(PkT{});
-      else tiles(PkF{});
+      }
     }
-  }
+  };
+  if (KSB > 0 && packed_rng) run(PkT{});
+  else run(PkF{});
 
   // ---- the range's partial: stats of head r from lanes (r, kq = 0), values [b, hq, blk, d] from
   // the accumulators (lane (dim 16 j + r, kq) holds heads 4 kq + i)
