@@ -354,8 +354,9 @@ class TurboQuantRowsCache(TurboQuantBatchCache):
         # kernel (other head dims): one per block, KV head and sequence, each writing G partial
         # rows the merge reads back (64-token blocks at 16K tokens made ~4000 workgroups whose
         # partials were as large as the cache).  The MFMA split kernel (head_dim 64, 128, 256)
-        # sizes its own ranges (about 1536 waves) within the partial buffer: room for ~2048 blocks
-        # keeps the buffer from lengthening them (D = 128, 4-bit: 27.8 -> 26.8 us).
+        # sizes its own ranges (about 2048 waves with TQ-MSE keys at head_dim <= 128, 1024 at 256)
+        # within the partial buffer: room for ~2048 blocks keeps the buffer from lengthening them
+        # (D = 128, 4-bit: 27.8 -> 26.8 us).
         wg = 2048 if self.head_dim in (64, 128, 256) else 1024
         per_row = max(1, wg // (self.batch * self.kv_heads))
         bs = max(self.block_size, -(-(self.capacity + self.residual_capacity) // per_row))
