@@ -827,7 +827,8 @@ extern "C" int anna_mi_int4_linear(const void* x, int x_dtype, int64_t M, int64_
         const bool vec = (N & 3) == 0;
         // four row groups per lane while that still gives three workgroups per compute unit, else
         // two (twice the waves, half the chain per wave): M = 1, N = 6144, K = 2048 3.93 -> 3.72 us,
-        // K = 4096 5.25 -> 5.03 us; N = 12288 stays at four (6.8 against 7.8 us with two).
+        // K = 4096 5.25 -> 5.03 us; N = 12288 stays at four (6.8 against 7.8 us with two); one row
+        // group per lane measured 3.86 / 5.89 us at N = 6144 (two: 3.74 / 4.83).
         // ANNA_MI_INT4_DOT2_RG = 1 / 2 / 4 forces a count (read on every call, for the tests).
         int rg = (N + 15) / 16 >= 768 ? 4 : 2;
         if (const char* f = getenv("ANNA_MI_INT4_DOT2_RG"); f && (f[0] == '1' || f[0] == '2' || f[0] == '4'))
