@@ -344,6 +344,8 @@ __global__ __launch_bounds__(64 * WMAX) void int4_gemv_dot2(
         zg[g] = __builtin_amdgcn_raw_buffer_load_b8(rz, so, g, 0);
       }
     }
+    // weights with the non-temporal hint (cache policy 2): the default policy measured 7.5 against
+    // 7.06 us at M = 1, N = 12288, K = 4096; adding sc0 or sc1 changed nothing beyond noise
     u32x4 wv[RG];
     const uint32_t wo = k_ok ? (uint32_t)((RG * sub * pc + (kl >> 3)) * 4) : OOB;
 #pragma unroll
