@@ -39,18 +39,20 @@ struct TileWords {
 
 template <int T>
 __device__ __forceinline__ TileWords<T> load_tile_words(const uint32_t* p) {
+  // the weights are read once per call: non-temporal loads
   TileWords<T> r;
   if constexpr (T == 8) {
-    const u32x4 a = *(const u32x4*)p, b = *(const u32x4*)(p + 4);
+    const u32x4 a = __builtin_nontemporal_load((const u32x4*)p), b = __builtin_nontemporal_load((const u32x4*)(p + 4));
     r.v[0] = a.x, r.v[1] = a.y, r.v[2] = a.z, r.v[3] = a.w, r.v[4] = b.x, r.v[5] = b.y, r.v[6] = b.z, r.v[7] = b.w;
   } else if constexpr (T == 4) {
-    const u32x4 a = *(const u32x4*)p;
+    const u32x4 a = __builtin_nontemporal_load((const u32x4*)p);
     r.v[0] = a.x, r.v[1] = a.y, r.v[2] = a.z, r.v[3] = a.w;
   } else if constexpr (T == 2) {
-    const uint2 a = *(const uint2*)p;
-    r.v[0] = a.x, r.v[1] = a.y;
+    typedef uint32_t u32x2t __attribute__((ext_vector_type(2)));
+    const u32x2t a = __builtin_nontemporal_load((const u32x2t*)p);
+    r.v[0] = a[0], r.v[1] = a[1];
   } else {
-    r.v[0] = *p;
+    r.v[0] = __builtin_nontemporal_load(p);
   }
   return r;
 }
