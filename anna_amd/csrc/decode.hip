@@ -689,19 +689,21 @@ struct MfmaTileRegs {
   uint32_t kn[8];
 };
 
-// n 32-bit words from p (aligned to min(4 n, 16) bytes) as whole-vector loads.
+// n 32-bit words from p (aligned to min(4 n, 16) bytes) as whole-vector non-temporal loads (the
+// cache's codes are read once per call).
+typedef uint32_t u32x2w __attribute__((ext_vector_type(2)));
 template <int N>
 __device__ __forceinline__ void load_words(uint32_t (&w)[N], const uint8_t* p) {
   if constexpr (N == 1) {
-    w[0] = *(const uint32_t*)p;
+    w[0] = __builtin_nontemporal_load((const uint32_t*)p);
   } else if constexpr (N == 2) {
-    const uint2 v = *(const uint2*)p;
-    w[0] = v.x;
-    w[1] = v.y;
+    const u32x2w v = __builtin_nontemporal_load((const u32x2w*)p);
+    w[0] = v[0];
+    w[1] = v[1];
   } else {
 #pragma unroll
     for (int i = 0; i < N / 4; ++i) {
-      const u32x4 v = *(const u32x4*)(p + 16 * i);
+      const u32x4 v = __builtin_nontemporal_load((const u32x4*)(p + 16 * i));
 #pragma unroll
       for (int e = 0; e < 4; ++e) w[4 * i + e] = v[e];
     }
